@@ -1,0 +1,77 @@
+"""ctypes binding of librew_mi355x.so (declared in include/rew_mi355x.h).
+
+Loading fails loudly when the library is missing: there is no fallback
+execution path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "librew_mi355x.so"
+
+# Every symbol include/rew_mi355x.h declares, with (restype, argtypes).
+_c_buf = C.c_void_p
+_c_ctx = C.c_void_p
+SIGNATURES = {
+    "rew_mi355x_abi_version": (C.c_int, []),
+    "rew_mi355x_last_error": (C.c_char_p, []),
+    "rew_mi355x_device_count": (C.c_int, [C.POINTER(C.c_int)]),
+    "rew_mi355x_init": (C.c_int, [C.c_int, C.POINTER(_c_ctx)]),
+    "rew_mi355x_shutdown": (C.c_int, [_c_ctx]),
+    "rew_mi355x_from_host": (C.c_int, [_c_ctx, C.c_int, C.POINTER(C.c_int64), C.c_int,
+                                       C.c_void_p, C.c_int64, C.POINTER(_c_buf)]),
+    "rew_mi355x_to_host": (C.c_int, [_c_buf, C.c_void_p, C.c_int64]),
+    "rew_mi355x_buf_meta": (C.c_int, [_c_buf, C.POINTER(C.c_int), C.POINTER(C.c_int),
+                                      C.POINTER(C.c_int64)]),
+    "rew_mi355x_retain": (C.c_int, [_c_buf]),
+    "rew_mi355x_release": (None, [_c_buf]),
+    "rew_mi355x_execute": (C.c_int, [_c_ctx, C.c_char_p, C.POINTER(_c_buf), C.c_int,
+                                     C.POINTER(C.c_char_p), C.POINTER(C.c_char_p), C.c_int,
+                                     C.POINTER(_c_buf), C.c_int, C.POINTER(C.c_int)]),
+    "rew_mi355x_flush": (C.c_int, [_c_ctx]),
+    "rew_mi355x_sync": (C.c_int, [_c_ctx]),
+    "rew_mi355x_set_mode": (C.c_int, [_c_ctx, C.c_int]),
+    "rew_mi355x_clear_cache": (C.c_int, [_c_ctx]),
+    "rew_mi355x_get_stats": (C.c_int, [_c_ctx, C.c_void_p]),
+    "rew_mi355x_reset_stats": (C.c_int, [_c_ctx]),
+    "rew_mi355x_profile_begin": (C.c_int, [_c_ctx]),
+    "rew_mi355x_profile_end": (C.c_int, [_c_ctx]),
+    "rew_mi355x_profile_entry": (C.c_int, [_c_ctx, C.c_int, C.c_char_p, C.c_int,
+                                           C.POINTER(C.c_int64), C.POINTER(C.c_double)]),
+    "rew_mi355x_stream": (C.c_int, [_c_ctx, C.POINTER(C.c_void_p)]),
+    "rew_mi355x_rng_split": (None, [C.c_uint32, C.c_uint32, C.c_int, C.POINTER(C.c_uint32)]),
+    "rew_mi355x_rng_fold_in": (None, [C.c_uint32, C.c_uint32, C.c_uint64,
+                                      C.POINTER(C.c_uint32)]),
+    "rew_mi355x_rng_uniform_f32": (None, [C.c_uint32, C.c_uint32, C.c_int64, C.c_float,
+                                          C.c_float, C.c_void_p]),
+    "rew_mi355x_rng_normal_f32": (None, [C.c_uint32, C.c_uint32, C.c_int64, C.c_float,
+                                         C.c_float, C.c_void_p]),
+}
+
+
+class Stats(C.Structure):
+    _fields_ = [(n, C.c_int64) for n in (
+        "ops_recorded", "kernels_launched", "flushes", "fused_groups",
+        "bytes_in_use", "bytes_cached", "plan_cache_hits")]
+
+
+_lib = None
+
+
+def load() -> C.CDLL:
+    """Returns the loaded library, raising if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build it with `python -m rew_amd.build` "
+            "(there is no CPU fallback for the mi355x backend)")
+    lib = C.CDLL(str(LIB_PATH))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib

@@ -1,0 +1,65 @@
+// Host-callable launchers of the HIP kernels (one .hip file each).
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include "common.h"
+#include "vm.h"
+
+namespace rew {
+
+// ---- fused elementwise (k_ew.hip) ------------------------------------------
+// `vec`: the innermost space dim is a multiple of vm::kVec and every
+// LM_CONTIG leaf / output is vector-aligned.
+void launch_ew(const vm::Program& P, const vm::Space& S, bool vec,
+               hipStream_t stream);
+
+// ---- reductions (k_reduce.hip) ---------------------------------------------
+enum RedOp : int {
+  RED_SUM = 0, RED_MAX, RED_MIN, RED_PROD, RED_AND, RED_OR, RED_MAXI, RED_MINI
+};
+struct ReduceArgs {
+  int op;
+  uint32_t n_out;   // product of kept dims
+  uint32_t n_red;   // product of reduced dims
+  void* out;
+  int out_dtype;
+};
+// Space = [kept..., reduced...]; program output 0 names the value register.
+void launch_reduce(const vm::Program& P, const vm::Space& S,
+                   const ReduceArgs& A, bool vec, hipStream_t stream);
+
+// ---- dot_general as a batched GEMM (k_gemm.hip) ------------------------------
+// C[b, m, n] = sum_k A[b, m, k] * B[b, k, n]; all strides in elements.
+// Dense C with row pitch ldc = N unless c_sm says otherwise.
+struct GemmArgs {
+  const void* a;
+  const void* b;
+  void* c;
+  int dtype;       // operand dtype (bf16 / f16 / f32)
+  int c_dtype;     // result dtype
+  int64_t batch, M, N, K;
+  int64_t a_sb, a_sm, a_sk;
+  int64_t b_sb, b_sk, b_sn;
+  int64_t c_sb, c_sm;
+};
+void launch_gemm(const GemmArgs& g, hipStream_t stream);
+// Name of the kernel variant launch_gemm would pick (for profiles/tests).
+const char* gemm_variant(const GemmArgs& g);
+
+// ---- gather (k_gather.hip) ---------------------------------------------------
+// torch_index_select with batch_dims = 0: out[pre, i, post] =
+// operand[pre, index[i], post]; rows of `row_bytes` contiguous bytes.
+struct GatherArgs {
+  const void* src;
+  const void* index;
+  void* out;
+  int index_dtype;
+  int64_t n_pre;        // product of operand dims before `dim`
+  int64_t src_dim;      // operand.shape[dim]
+  int64_t n_idx;        // number of indices
+  int64_t row_bytes;    // product of operand dims after `dim` * elem size
+};
+void launch_gather(const GatherArgs& g, hipStream_t stream);
+
+}  // namespace rew

@@ -1,0 +1,1237 @@
+// Graph lowering: turns the pending op graph of a context into HIP launches.
+//
+// 1. Dead nodes (no owner and no consumer) are dropped.
+// 2. Each pending tensor is classified: anchors (reductions, dot_general,
+//    gathers, ...) always materialize; elementwise results materialize when
+//    the caller still holds them, when a consumer needs them in memory, or
+//    when several consumers would each recompute a non-trivial expression;
+//    view ops (reshape/transpose/broadcast/slice/reverse) never do unless
+//    the caller holds them.
+// 3. Every materialization of an elementwise tensor becomes one vm::Program
+//    whose leaves read materialized tensors through affine index maps built
+//    by composing the view ops between them, so chains like rew's RoPE
+//    (~26 reshape/slice/mul/concat ops) or a bias-add + SiLU + gate product
+//    become a single HBM pass.  Reductions take their input expression as a
+//    prologue.  dot_general folds transposes into GEMM strides.
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <functional>
+
+#include "kernels.h"
+#include "runtime.h"
+
+namespace rew {
+
+using namespace vm;
+
+static_assert(sizeof(Program) + sizeof(Space) + sizeof(ReduceArgs) < 4000,
+              "kernel arguments must stay below 4 KiB");
+
+// ---------------------------------------------------------------------------
+// classification
+// ---------------------------------------------------------------------------
+
+static bool is_view(int k) {
+  return k == K_RESHAPE || k == K_TRANSPOSE || k == K_REVERSE ||
+         k == K_BROADCAST_TO || k == K_BROADCAST || k == K_SLICE;
+}
+static bool is_ew(int k) {
+  return k == K_BINARY || k == K_UNARY || k == K_CONVERT || k == K_ISFINITE ||
+         k == K_COMPARE || k == K_SELECT || k == K_CLAMP || k == K_IOTA ||
+         k == K_CONCAT || k == K_REDUCE_PRECISION;
+}
+// Consumers that read an operand through a fused prologue.
+static bool takes_expression(int k) { return is_ew(k) || is_view(k) || k == K_REDUCE; }
+
+// ---------------------------------------------------------------------------
+// affine index maps: kernel coordinates -> tensor coordinates
+// ---------------------------------------------------------------------------
+
+struct Affine {
+  int R = 0;  // kernel rank
+  int r = 0;  // tensor rank
+  int64_t off[kMaxRank] = {0};
+  int64_t S[kMaxRank][kMaxRank] = {{0}};
+
+  static Affine identity(int rank) {
+    Affine a;
+    a.R = a.r = rank;
+    for (int i = 0; i < rank; ++i) a.S[i][i] = 1;
+    return a;
+  }
+  bool operator==(const Affine& o) const {
+    if (R != o.R || r != o.r) return false;
+    for (int i = 0; i < r; ++i) {
+      if (off[i] != o.off[i]) return false;
+      for (int k = 0; k < R; ++k)
+        if (S[i][k] != o.S[i][k]) return false;
+    }
+    return true;
+  }
+};
+
+static void dense_strides(const Shape& s, int64_t* st) {
+  int64_t acc = 1;
+  for (int i = s.rank - 1; i >= 0; --i) {
+    st[i] = acc;
+    acc *= s.d[i];
+  }
+}
+
+// Map through u = reshape(x): fine when every group of u dims merges into a
+// single x dim (x coordinate = mixed-radix combination of u coordinates).
+static bool compose_reshape(const Shape& U, const Shape& X, const Affine& m,
+                            Affine* out) {
+  out->R = m.R;
+  out->r = X.rank;
+  for (int j = 0; j < X.rank; ++j) {
+    out->off[j] = 0;
+    for (int k = 0; k < m.R; ++k) out->S[j][k] = 0;
+  }
+  // Non-unit dims of each side.
+  std::vector<int> ui, xj;
+  for (int i = 0; i < U.rank; ++i)
+    if (U.d[i] != 1) ui.push_back(i);
+  for (int j = 0; j < X.rank; ++j)
+    if (X.d[j] != 1) xj.push_back(j);
+  size_t a = 0, b = 0;
+  while (a < ui.size() || b < xj.size()) {
+    if (a >= ui.size() || b >= xj.size()) return false;
+    // grow a minimal group with equal products
+    size_t a1 = a + 1, b1 = b + 1;
+    int64_t pu = U.d[ui[a]], px = X.d[xj[b]];
+    while (pu != px) {
+      if (pu < px) {
+        if (a1 >= ui.size()) return false;
+        pu *= U.d[ui[a1++]];
+      } else {
+        if (b1 >= xj.size()) return false;
+        px *= X.d[xj[b1++]];
+      }
+    }
+    if (b1 - b != 1) return false;  // would need a division
+    const int j = xj[b];
+    int64_t w = 1;
+    for (size_t t = a1; t-- > a;) {
+      const int i = ui[t];
+      out->off[j] += m.off[i] * w;
+      for (int k = 0; k < m.R; ++k) out->S[j][k] += m.S[i][k] * w;
+      w *= U.d[i];
+    }
+    a = a1;
+    b = b1;
+  }
+  return true;
+}
+
+// Given m: kernel -> coordinates of u = v(x), produce kernel -> x.
+static bool compose_view(const Node* v, const Affine& m, Affine* out) {
+  const Shape& X = v->in[0]->shape;
+  const Shape& U = v->out[0]->shape;
+  switch (v->kind) {
+    case K_RESHAPE:
+      return compose_reshape(U, X, m, out);
+    case K_TRANSPOSE: {
+      *out = m;
+      for (int i = 0; i < U.rank; ++i) {
+        const int p = (int)v->l0[i];
+        out->off[p] = m.off[i];
+        for (int k = 0; k < m.R; ++k) out->S[p][k] = m.S[i][k];
+      }
+      return true;
+    }
+    case K_BROADCAST_TO: {
+      Affine o;
+      o.R = m.R;
+      o.r = X.rank;
+      for (int j = 0; j < X.rank; ++j) {
+        if (X.d[j] == 1) continue;  // row of zeros
+        const int i = (int)v->l1[j];
+        o.off[j] = m.off[i];
+        for (int k = 0; k < m.R; ++k) o.S[j][k] = m.S[i][k];
+      }
+      *out = o;
+      return true;
+    }
+    case K_BROADCAST: {
+      Affine o;
+      o.R = m.R;
+      o.r = X.rank;
+      const int nb = (int)v->l0.size();
+      for (int j = 0; j < X.rank; ++j) {
+        o.off[j] = m.off[nb + j];
+        for (int k = 0; k < m.R; ++k) o.S[j][k] = m.S[nb + j][k];
+      }
+      *out = o;
+      return true;
+    }
+    case K_SLICE: {
+      *out = m;
+      for (int i = 0; i < X.rank; ++i) {
+        out->off[i] = v->l0[i] + v->l2[i] * m.off[i];
+        for (int k = 0; k < m.R; ++k) out->S[i][k] = v->l2[i] * m.S[i][k];
+      }
+      return true;
+    }
+    case K_REVERSE: {
+      *out = m;
+      for (auto d : v->l0) {
+        out->off[d] = X.d[d] - 1 - m.off[d];
+        for (int k = 0; k < m.R; ++k) out->S[d][k] = -m.S[d][k];
+      }
+      return true;
+    }
+    default:
+      return false;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// lowering state
+// ---------------------------------------------------------------------------
+
+struct Lower {
+  Ctx* c;
+  std::vector<Node*> nodes;  // live pending nodes in creation order
+
+  explicit Lower(Ctx* ctx) : c(ctx) {}
+
+  void ensure_mat(Tensor* t);
+  void emit_ew_root(Tensor* t);
+  void emit_anchor(Node* n);
+  void emit_reduce(Node* n);
+  void emit_dot(Node* n);
+  void emit_gather(Node* n);
+  void emit_argmax(Node* n);
+  void emit_topk(Node* n);
+  // Materialize `t` (any kind) into a fresh dense tensor whose shape is the
+  // permutation `perm` of t's shape.
+  Tensor* emit_permuted_copy(Tensor* t, const std::vector<int>& perm);
+  // Strides (in elements) of every dim of `t` over a materialized base.
+  void operand_strides(Tensor* t, Tensor** base, int64_t* off, int64_t* st);
+};
+
+// ---------------------------------------------------------------------------
+// expression code generation
+// ---------------------------------------------------------------------------
+
+struct GenFail {};
+
+struct Gen {
+  Lower& L;
+  Shape space;             // kernel index space (before collapsing)
+  Program P;
+  std::vector<Tensor*> leaf_t;
+  struct Memo {
+    Tensor* t;
+    Affine m;
+    int clamp;
+    int val;
+  };
+  std::vector<Memo> memo;
+  int clamp_depth = 0;
+  int n_vals = 0;
+
+  Gen(Lower& l, const Shape& s) : L(l), space(s) {
+    std::memset(&P, 0, sizeof(P));
+  }
+
+  int emit(uint8_t op, int a = 0, int b = 0, int cc = 0, uint8_t aux = 0,
+           uint32_t imm = 0) {
+    if (P.n_ins >= kMaxIns) throw GenFail();
+    Ins& I = P.ins[P.n_ins++];
+    I.op = op;
+    I.a = (uint8_t)a;
+    I.b = (uint8_t)b;
+    I.c = (uint8_t)cc;
+    I.aux = aux;
+    I.imm = imm;
+    I.dst = 0;
+    // Until register allocation, operands and dst hold SSA value ids; ids
+    // are instruction indices, kept < 256 by kMaxIns.
+    I.pad = 0;
+    return n_vals++;
+  }
+
+  int add_leaf(Tensor* t, const Affine& m, bool iota) {
+    int64_t ds[kMaxRank];
+    int64_t off = 0, st[kMaxRank] = {0};
+    if (iota) {
+      // value = coordinate m.row(iota_dim); the caller passes a 1-row map.
+      off = m.off[0];
+      for (int k = 0; k < m.R; ++k) st[k] = m.S[0][k];
+    } else {
+      dense_strides(t->shape, ds);
+      for (int i = 0; i < m.r; ++i) {
+        off += m.off[i] * ds[i];
+        for (int k = 0; k < m.R; ++k) st[k] += m.S[i][k] * ds[i];
+      }
+    }
+    for (int i = 0; i < P.n_leaves; ++i) {
+      const Leaf& q = P.leaf[i];
+      if (leaf_t[i] == t && q.ptr == (iota ? nullptr : t->data()) && q.off == off &&
+          (q.clamp_hi >= 0) == (clamp_depth > 0 && !iota)) {
+        bool same = true;
+        for (int k = 0; k < m.R; ++k)
+          if (q.stride[k] != st[k]) same = false;
+        if (same) return i;
+      }
+    }
+    if (P.n_leaves >= kMaxLeaves) throw GenFail();
+    const int li = P.n_leaves++;
+    Leaf& lf = P.leaf[li];
+    std::memset(&lf, 0, sizeof(lf));
+    lf.ptr = iota ? nullptr : t->data();
+    lf.dtype = iota ? (uint8_t)kI32 : (uint8_t)t->dt;
+    lf.mode = LM_STRIDED;
+    lf.off = (int32_t)off;
+    lf.clamp_hi = (!iota && clamp_depth > 0) ? (int32_t)(t->numel() - 1) : -1;
+    for (int k = 0; k < m.R; ++k) lf.stride[k] = (int32_t)st[k];
+    leaf_t.push_back(t);
+    return li;
+  }
+
+  uint32_t const_bits(Tensor* t) {
+    uint32_t u = 0;
+    switch (t->dt) {
+      case kF32: case kI32: case kU32: std::memcpy(&u, t->host, 4); break;
+      case kBF16: { uint16_t h; std::memcpy(&h, t->host, 2); u = (uint32_t)h << 16; break; }
+      case kF16: {
+        uint16_t h; std::memcpy(&h, t->host, 2);
+        // f16 -> f32 (exact)
+        uint32_t sgn = (h & 0x8000u) << 16, e = (h >> 10) & 0x1f, f = h & 0x3ff;
+        if (e == 0) {
+          float v = std::ldexp((float)f, -24);
+          std::memcpy(&u, &v, 4);
+          u |= sgn;
+        } else if (e == 31) {
+          u = sgn | 0x7f800000u | (f << 13);
+        } else {
+          u = sgn | ((e + 112) << 23) | (f << 13);
+        }
+        break;
+      }
+      case kI16: { int16_t v; std::memcpy(&v, t->host, 2); u = (uint32_t)(int32_t)v; break; }
+      case kU16: { uint16_t v; std::memcpy(&v, t->host, 2); u = v; break; }
+      case kI8: { int8_t v; std::memcpy(&v, t->host, 1); u = (uint32_t)(int32_t)v; break; }
+      default: u = t->host[0]; break;  // bool, u8
+    }
+    return u;
+  }
+
+  // Leaf value of a materialized tensor `t` read at map `m`.
+  int load_mat(Tensor* t, const Affine& m) {
+    if (t->has_host && t->numel() == 1) return emit(OP_CONST, 0, 0, 0, 0, const_bits(t));
+    const int li = add_leaf(t, m, false);
+    return emit(OP_LOAD, 0, 0, 0, 0, (uint32_t)li);
+  }
+
+  int gen(Tensor* u, const Affine& m);
+  int gen_node(Node* p, Tensor* u, const Affine& m);
+};
+
+static bool is_float_dt(int dt) { return dt == kF32 || dt == kBF16 || dt == kF16; }
+
+// Re-rounds a float register to the storage precision of `dt`, or narrows
+// an integer register to its width.
+static int fix_width(Gen& g, int v, int dt) {
+  switch (dt) {
+    case kBF16: return g.emit(OP_RBF16, v);
+    case kF16: return g.emit(OP_RF16, v);
+    case kI8: return g.emit(OP_SEXT8, v);
+    case kU8: return g.emit(OP_ZEXT8, v);
+    case kI16: return g.emit(OP_SEXT16, v);
+    case kU16: return g.emit(OP_ZEXT16, v);
+    default: return v;
+  }
+}
+
+int Gen::gen(Tensor* u, const Affine& m) {
+  if (u->st || !u->prod) return load_mat(u, m);
+  Node* p = u->prod;
+  if (u->plan_mat) {
+    L.ensure_mat(u);
+    return load_mat(u, m);
+  }
+  if (is_view(p->kind)) {
+    Affine m2;
+    if (compose_view(p, m, &m2)) return gen(p->in[0], m2);
+    // A reshape that would split a coordinate: read its input as a dense
+    // buffer instead (same linear order as u).
+    Tensor* x = p->in[0];
+    L.ensure_mat(x);
+    if (x->has_host && x->numel() == 1) return load_mat(x, m);
+    int64_t ds[kMaxRank];
+    dense_strides(u->shape, ds);
+    Affine flat;
+    flat.R = m.R;
+    flat.r = 1;
+    for (int i = 0; i < m.r; ++i) {
+      flat.off[0] += m.off[i] * ds[i];
+      for (int k = 0; k < m.R; ++k) flat.S[0][k] += m.S[i][k] * ds[i];
+    }
+    // treat x as a 1-D dense buffer
+    Shape saved = x->shape;
+    x->shape = Shape(std::vector<int64_t>{x->numel()});
+    int v = load_mat(x, flat);
+    x->shape = saved;
+    return v;
+  }
+  if (is_ew(p->kind)) {
+    for (auto& e : memo)
+      if (e.t == u && e.clamp == (clamp_depth > 0) && e.m == m) return e.val;
+    int v = gen_node(p, u, m);
+    memo.push_back({u, m, clamp_depth > 0, v});
+    return v;
+  }
+  L.ensure_mat(u);
+  return load_mat(u, m);
+}
+
+int Gen::gen_node(Node* p, Tensor* u, const Affine& m) {
+  const int odt = u->dt;
+  switch (p->kind) {
+    case K_BINARY: {
+      const int dt = p->in[0]->dt;
+      int a = gen(p->in[0], m);
+      int b = gen(p->in[1], m);
+      uint8_t op = OP_NOP;
+      if (is_float_dt(dt)) {
+        static const uint8_t fop[] = {OP_ADDF, OP_SUBF, OP_MULF, OP_DIVF, OP_MAXF,
+                                      OP_MINF, OP_ATAN2F, OP_POWF, OP_REMF};
+        if (p->sub > 8) throw Error(REW_MI355X_ERR_INVALID, "bad float binary op");
+        op = fop[p->sub];
+        return fix_width(*this, emit(op, a, b), dt);
+      }
+      if (dt == kBool) {
+        switch (p->sub) {
+          case 0: case 4: case 10: op = OP_OR; break;    // add, max, or
+          case 2: case 5: case 9: op = OP_AND; break;    // mul, min, and
+          case 11: op = OP_XOR; break;
+          default:
+            throw Error(REW_MI355X_ERR_UNSUPPORTED,
+                        "eager '" + p->name + "': not supported on bool");
+        }
+        return emit(op, a, b);
+      }
+      const bool un = !dt_is_signed(dt);
+      switch (p->sub) {
+        case 0: op = OP_ADDI; break;
+        case 1: op = OP_SUBI; break;
+        case 2: op = OP_MULI; break;
+        case 3: op = un ? OP_DIVU : OP_DIVI; break;
+        case 4: op = un ? OP_MAXU : OP_MAXI; break;
+        case 5: op = un ? OP_MINU : OP_MINI; break;
+        case 8: op = un ? OP_REMU : OP_REMI; break;
+        case 9: op = OP_AND; break;
+        case 10: op = OP_OR; break;
+        case 11: op = OP_XOR; break;
+        case 12: op = OP_SHL; break;
+        case 13: op = OP_SHRA; break;
+        case 14: op = OP_SHRL; break;
+        default:
+          throw Error(REW_MI355X_ERR_UNSUPPORTED,
+                      "eager '" + p->name + "': not supported on integers");
+      }
+      return fix_width(*this, emit(op, a, b), dt);
+    }
+    case K_UNARY: {
+      const int dt = p->in[0]->dt;
+      int a = gen(p->in[0], m);
+      static const uint8_t fop[] = {
+          OP_NEGF, OP_ABSF, OP_EXPF, OP_LOGF, OP_SQRTF, OP_TANHF, OP_CBRTF,
+          OP_CEILF, OP_EXPM1F, OP_FLOORF, OP_LOG1PF, OP_LOGISTICF, OP_TANF,
+          OP_SIGNF, OP_ROUNDAFZF, OP_ROUNDEVENF, OP_NOP, OP_NOP, OP_NOP, OP_NOP,
+          OP_SINF, OP_COSF, OP_RSQRTF};
+      if (p->sub == 19) return a;  // optimizationBarrier / stopGradient
+      if (is_float_dt(dt)) return fix_width(*this, emit(fop[p->sub], a), dt);
+      uint8_t op;
+      switch (p->sub) {
+        case 0: op = OP_NEGI; break;
+        case 1: op = OP_ABSI; break;
+        case 13: op = OP_SIGNI; break;
+        case 16: op = dt == kBool ? OP_NOTB : OP_NOT; break;
+        case 17:
+          if (dt_size(dt) != 4)
+            throw Error(REW_MI355X_ERR_UNSUPPORTED, "countLeadingZeros: 32-bit only");
+          op = OP_CLZ;
+          break;
+        case 18:
+          if (dt_size(dt) != 4) {
+            a = emit(dt_size(dt) == 1 ? OP_ZEXT8 : OP_ZEXT16, a);
+          }
+          op = OP_POPCNT;
+          break;
+        default:
+          throw Error(REW_MI355X_ERR_UNSUPPORTED, "eager '" + p->name + "' on integers");
+      }
+      int v = emit(op, a);
+      return dt == kBool ? v : fix_width(*this, v, dt);
+    }
+    case K_CONVERT: {
+      const int sdt = p->in[0]->dt, ddt = odt;
+      int a = gen(p->in[0], m);
+      if (sdt == ddt) return a;
+      const bool sf = is_float_dt(sdt), df = is_float_dt(ddt);
+      if (sf && df) return fix_width(*this, a, ddt);
+      if (sf && ddt == kBool) return emit(OP_FTOBOOL, a);
+      if (sf) {
+        int v = emit(dt_is_signed(ddt) ? OP_F2I : OP_F2U, a);
+        return fix_width(*this, v, ddt);
+      }
+      // integer / bool source
+      if (df) {
+        int v = emit((dt_is_signed(sdt)) ? OP_I2F : OP_U2F, a);
+        return fix_width(*this, v, ddt);
+      }
+      if (ddt == kBool) return emit(OP_TOBOOL, a);
+      return fix_width(*this, a, ddt);
+    }
+    case K_ISFINITE:
+      return emit(OP_ISFINITEF, gen(p->in[0], m));
+    case K_REDUCE_PRECISION: {
+      int a = gen(p->in[0], m);
+      if (p->i1 == 7) return emit(OP_RBF16, a);
+      if (p->i1 == 10) return emit(OP_RF16, a);
+      return a;
+    }
+    case K_COMPARE: {
+      const int dt = p->in[0]->dt;
+      int a = gen(p->in[0], m), b = gen(p->in[1], m);
+      uint8_t op = is_float_dt(dt) ? OP_CMPF : (dt_is_signed(dt) ? OP_CMPI : OP_CMPU);
+      return emit(op, a, b, 0, (uint8_t)p->cmp);
+    }
+    case K_SELECT: {
+      int pr = gen(p->in[0], m);
+      int a = gen(p->in[1], m);
+      int b = gen(p->in[2], m);
+      return emit(OP_SELECT, pr, a, b);
+    }
+    case K_CLAMP: {
+      const int dt = p->in[1]->dt;
+      auto bound = [&](Tensor* t) {
+        if (t->shape.rank == 0) {
+          Affine z;
+          z.R = m.R;
+          z.r = 0;
+          return gen(t, z);
+        }
+        return gen(t, m);
+      };
+      int lo = bound(p->in[0]);
+      int x = gen(p->in[1], m);
+      int hi = bound(p->in[2]);
+      uint8_t op = is_float_dt(dt) ? OP_CLAMPF : (dt_is_signed(dt) ? OP_CLAMPI : OP_CLAMPU);
+      return emit(op, lo, x, hi);
+    }
+    case K_IOTA: {
+      Affine row;
+      row.R = m.R;
+      row.r = 1;
+      row.off[0] = m.off[p->i0];
+      for (int k = 0; k < m.R; ++k) row.S[0][k] = m.S[p->i0][k];
+      const int li = add_leaf(u, row, true);
+      int v = emit(OP_IOTA, 0, 0, 0, 0, (uint32_t)li);
+      if (is_float_dt(odt)) return fix_width(*this, emit(OP_I2F, v), odt);
+      return fix_width(*this, v, odt);
+    }
+    case K_CONCAT: {
+      const int dim = (int)p->i0;
+      const int nparts = (int)p->in.size();
+      std::vector<int> vals(nparts);
+      std::vector<int64_t> starts(nparts);
+      int64_t o = 0;
+      for (int j = 0; j < nparts; ++j) {
+        starts[j] = o;
+        Affine mj = m;
+        mj.off[dim] -= o;
+        if (nparts > 1) ++clamp_depth;
+        vals[j] = gen(p->in[j], mj);
+        if (nparts > 1) --clamp_depth;
+        o += p->in[j]->shape.d[dim];
+      }
+      if (nparts == 1) return vals[0];
+      Affine row;
+      row.R = m.R;
+      row.r = 1;
+      row.off[0] = m.off[dim];
+      for (int k = 0; k < m.R; ++k) row.S[0][k] = m.S[dim][k];
+      const int li = add_leaf(u, row, true);
+      int coord = emit(OP_IOTA, 0, 0, 0, 0, (uint32_t)li);
+      int r = vals[nparts - 1];
+      for (int j = nparts - 2; j >= 0; --j) {
+        int lim = emit(OP_CONST, 0, 0, 0, 0, (uint32_t)starts[j + 1]);
+        int cond = emit(OP_CMPI, coord, lim, 0, CMP_LT);
+        r = emit(OP_SELECT, cond, vals[j], r);
+      }
+      return r;
+    }
+    default:
+      throw Error(REW_MI355X_ERR_UNSUPPORTED, "cannot fuse op '" + p->name + "'");
+  }
+}
+
+// ---------------------------------------------------------------------------
+// program finishing: dim collapsing, leaf modes, register allocation
+// ---------------------------------------------------------------------------
+
+static FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f;
+  f.d = d;
+  uint32_t s = 0;
+  while (((uint64_t)1 << s) < d) ++s;
+  f.s = s;
+  f.m = (uint32_t)((((uint64_t)1 << 32) * (((uint64_t)1 << s) - d)) / d + 1);
+  return f;
+}
+
+// Collapses the kernel space: drops unit dims and merges neighbours whose
+// strides agree for every leaf and output.  `groups` marks dims that must
+// not merge across (the kept/reduced boundary of a reduction).
+static Space finish_space(Program& P, const Shape& space, int boundary,
+                          std::vector<int64_t>* out_dims) {
+  const int R = space.rank;
+  std::vector<int> keep;
+  for (int k = 0; k < R; ++k)
+    if (space.d[k] != 1) keep.push_back(k);
+  // merged dims as lists of original dims
+  std::vector<std::vector<int>> groups;
+  std::vector<int64_t> sizes;
+  for (int k : keep) {
+    bool merged = false;
+    if (!groups.empty()) {
+      const int prev = groups.back().back();
+      const bool cross = boundary >= 0 && prev < boundary && k >= boundary;
+      if (!cross) {
+        bool ok = true;
+        for (int l = 0; l < P.n_leaves && ok; ++l)
+          if ((int64_t)P.leaf[l].stride[prev] != (int64_t)P.leaf[l].stride[k] * space.d[k])
+            ok = false;
+        if (ok) {
+          groups.back().push_back(k);
+          sizes.back() *= space.d[k];
+          merged = true;
+        }
+      }
+    }
+    if (!merged) {
+      groups.push_back({k});
+      sizes.push_back(space.d[k]);
+    }
+  }
+  // rewrite leaf strides: stride of a merged group = stride of its last dim
+  for (int l = 0; l < P.n_leaves; ++l) {
+    int32_t ns[kRank] = {0};
+    for (size_t g = 0; g < groups.size(); ++g) ns[g] = P.leaf[l].stride[groups[g].back()];
+    std::memcpy(P.leaf[l].stride, ns, sizeof(ns));
+  }
+  Space S;
+  std::memset(&S, 0, sizeof(S));
+  S.rank = (int)groups.size();
+  S.numel = space.numel();
+  for (size_t g = 0; g < groups.size(); ++g) S.dim[g] = make_fastdiv((uint32_t)sizes[g]);
+  if (S.rank == 0) {  // scalar space
+    S.rank = 1;
+    S.dim[0] = make_fastdiv(1);
+    sizes.push_back(1);
+  }
+  if (out_dims) *out_dims = sizes;
+  // reduction boundary after collapsing is recomputed by the caller
+  return S;
+}
+
+// Refuses to launch a program whose leaves could address outside their
+// tensors anywhere in the kernel space (clamped concat leaves excepted):
+// a planner bug becomes a host error, never a device fault.
+static void check_bounds(const Program& P, const std::vector<Tensor*>& leaf_t,
+                         const std::vector<int64_t>& dims) {
+  for (int l = 0; l < P.n_leaves; ++l) {
+    const Leaf& lf = P.leaf[l];
+    if (!lf.ptr || lf.clamp_hi >= 0) continue;
+    int64_t lo = lf.off, hi = lf.off;
+    for (size_t k = 0; k < dims.size(); ++k) {
+      const int64_t e = (int64_t)lf.stride[k] * (dims[k] - 1);
+      if (e < 0) lo += e; else hi += e;
+    }
+    const int64_t n = leaf_t[l]->numel();
+    if (lo < 0 || hi >= n)
+      throw Error(REW_MI355X_ERR_INVALID,
+                  "internal: fused program would read elements [" + std::to_string(lo) +
+                      ", " + std::to_string(hi) + "] of a tensor with " + std::to_string(n));
+  }
+}
+
+// Leaf addressing modes for a kVec-wide lane when `vec`.
+static void set_leaf_modes(Program& P, const Space& S, bool vec) {
+  const int in = S.rank - 1;
+  for (int l = 0; l < P.n_leaves; ++l) {
+    Leaf& lf = P.leaf[l];
+    lf.mode = LM_STRIDED;
+    if (!vec || !lf.ptr || lf.clamp_hi >= 0) continue;
+    if (lf.stride[in] == 0) {
+      lf.mode = LM_BCAST;
+      continue;
+    }
+    if (lf.stride[in] != 1) continue;
+    bool al = (lf.off % kVec) == 0;
+    for (int k = 0; k < in; ++k)
+      if (lf.stride[k] % kVec != 0) al = false;
+    const int esz = dt_size(lf.dtype);
+    const uintptr_t need = (uintptr_t)(esz * kVec);
+    if (((uintptr_t)lf.ptr % need) != 0) al = false;
+    if (al && (lf.dtype == kF32 || lf.dtype == kI32 || lf.dtype == kU32 ||
+               lf.dtype == kBF16))
+      lf.mode = LM_CONTIG;
+  }
+}
+
+// Linear-scan register allocation over the SSA program.  `live_out` values
+// must survive to the end.
+static void alloc_regs(Program& P, const std::vector<int>& live_out,
+                       std::vector<int>* phys_of_out) {
+  const int n = P.n_ins;
+  std::vector<int> last(n, -1);
+  auto use = [&](int v, int at) { if (v >= 0 && v < n) last[v] = std::max(last[v], at); };
+  for (int i = 0; i < n; ++i) {
+    const Ins& I = P.ins[i];
+    int ar;
+    if (I.op <= OP_IOTA) ar = 0;
+    else if (I.op >= OP_SELECT && I.op <= OP_CLAMPU) ar = 3;
+    else if ((I.op >= OP_ADDF && I.op <= OP_SHRL) || (I.op >= OP_CMPF && I.op <= OP_CMPU)) ar = 2;
+    else ar = 1;
+    if (ar >= 1) use(I.a, i);
+    if (ar >= 2) use(I.b, i);
+    if (ar >= 3) use(I.c, i);
+  }
+  for (int v : live_out) last[v] = n;
+  std::vector<int> phys(n, -1);
+  std::vector<int> free_regs;
+  for (int r = kMaxRegs - 1; r >= 0; --r) free_regs.push_back(r);
+  std::vector<std::vector<int>> expire(n + 1);
+  for (int i = 0; i < n; ++i) {
+    Ins& I = P.ins[i];
+    int ar;
+    if (I.op <= OP_IOTA) ar = 0;
+    else if (I.op >= OP_SELECT && I.op <= OP_CLAMPU) ar = 3;
+    else if ((I.op >= OP_ADDF && I.op <= OP_SHRL) || (I.op >= OP_CMPF && I.op <= OP_CMPU)) ar = 2;
+    else ar = 1;
+    // operands read before the destination is written, so registers of
+    // operands dying here may be reused as the destination
+    int pa = ar >= 1 ? phys[I.a] : 0, pb = ar >= 2 ? phys[I.b] : 0,
+        pc = ar >= 3 ? phys[I.c] : 0;
+    for (int v : expire[i]) free_regs.push_back(phys[v]);
+    if (free_regs.empty()) throw GenFail();
+    const int r = free_regs.back();
+    free_regs.pop_back();
+    phys[i] = r;
+    I.a = (uint8_t)pa;
+    I.b = (uint8_t)pb;
+    I.c = (uint8_t)pc;
+    I.dst = (uint8_t)r;
+    const int end = last[i] < 0 ? i : last[i];
+    if (end >= n) continue;
+    if (end == i) {
+      free_regs.push_back(r);  // dead value
+    } else {
+      expire[end].push_back(i);
+    }
+  }
+  phys_of_out->clear();
+  for (int v : live_out) phys_of_out->push_back(phys[v]);
+}
+
+// ---------------------------------------------------------------------------
+// emission
+// ---------------------------------------------------------------------------
+
+static void note_launch(Ctx* c, bool fused) {
+  c->stats.kernels_launched++;
+  if (fused) c->stats.fused_groups++;
+}
+
+void Lower::ensure_mat(Tensor* t) {
+  if (t->st) return;
+  Node* p = t->prod;
+  if (!p) throw Error(REW_MI355X_ERR_INVALID, "internal: tensor has neither data nor producer");
+  if (is_ew(p->kind) || is_view(p->kind)) {
+    // a reshape of a materialized (or materializable) dense tensor aliases it
+    if (p->kind == K_RESHAPE) {
+      Tensor* x = p->in[0];
+      if (x->st || x->plan_mat || !x->prod) {
+        ensure_mat(x);
+        tensor_alias(t, x);
+        return;
+      }
+    }
+    emit_ew_root(t);
+    return;
+  }
+  emit_anchor(p);
+  if (!t->st) throw Error(REW_MI355X_ERR_INVALID, "internal: anchor did not materialize");
+}
+
+void Lower::emit_ew_root(Tensor* t) {
+  // Kernel space: the deepest reshape source with the same linear order.
+  Tensor* root = t;
+  while (root->prod && root->prod->kind == K_RESHAPE && !root->prod->in[0]->st &&
+         !root->prod->in[0]->plan_mat && root->prod->in[0]->prod &&
+         (is_ew(root->prod->in[0]->prod->kind) || is_view(root->prod->in[0]->prod->kind)))
+    root = root->prod->in[0];
+  for (int attempt = 0; attempt < 64; ++attempt) {
+    Gen g(*this, root->shape);
+    try {
+      Affine id = Affine::identity(root->shape.rank);
+      int v;
+      if (root == t) {
+        // gen(t) would return a load of t once materialized; expand its node
+        Node* p = t->prod;
+        if (is_view(p->kind)) {
+          Affine m2;
+          if (!compose_view(p, id, &m2))
+            throw Error(REW_MI355X_ERR_INVALID, "internal: view root not composable");
+          v = g.gen(p->in[0], m2);
+        } else {
+          v = g.gen_node(p, t, id);
+        }
+      } else {
+        v = g.gen(root, id);
+      }
+      tensor_alloc(t);
+      std::vector<int64_t> dims;
+      Space S = finish_space(g.P, root->shape, -1, &dims);
+      check_bounds(g.P, g.leaf_t, dims);
+      std::vector<int> outs_phys;
+      alloc_regs(g.P, {v}, &outs_phys);
+      g.P.n_outs = 1;
+      g.P.out[0].ptr = t->data();
+      g.P.out[0].dtype = (uint8_t)t->dt;
+      g.P.out[0].reg = (uint8_t)outs_phys[0];
+      g.P.out[0].off = 0;
+      const bool vec = (dims.back() % kVec) == 0 &&
+                       ((uintptr_t)t->data() % (dt_size(t->dt) * kVec)) == 0 &&
+                       (t->dt == kF32 || t->dt == kI32 || t->dt == kU32 || t->dt == kBF16);
+      set_leaf_modes(g.P, S, vec);
+      prof_begin(c, "ew_fused");
+      launch_ew(g.P, S, vec, c->stream);
+      prof_end(c);
+      note_launch(c, g.P.n_ins > 2);
+      return;
+    } catch (GenFail&) {
+      tensor_drop_storage(t);
+      // Too large for one program: materialize the direct inputs of the
+      // root's expression and retry.
+      Node* p = root->prod;
+      bool progressed = false;
+      std::function<void(Node*, int)> mat_inputs = [&](Node* q, int depth) {
+        for (Tensor* x : q->in) {
+          if (x->st) continue;
+          if (x->prod && is_view(x->prod->kind) && depth < 8) {
+            mat_inputs(x->prod, depth + 1);
+            continue;
+          }
+          x->plan_mat = true;
+          progressed = true;
+        }
+      };
+      mat_inputs(p, 0);
+      if (!progressed)
+        throw Error(REW_MI355X_ERR_UNSUPPORTED, "expression too large to lower");
+    }
+  }
+  throw Error(REW_MI355X_ERR_UNSUPPORTED, "expression too large to lower");
+}
+
+void Lower::emit_anchor(Node* n) {
+  switch (n->kind) {
+    case K_REDUCE: emit_reduce(n); break;
+    case K_DOT_GENERAL: emit_dot(n); break;
+    case K_INDEX_SELECT: emit_gather(n); break;
+    case K_ARGMAX: emit_argmax(n); break;
+    case K_TOPK: emit_topk(n); break;
+    case K_BITCAST: {
+      Tensor* x = n->in[0];
+      ensure_mat(x);
+      tensor_alias(n->out[0], x);
+      break;
+    }
+    default:
+      throw Error(REW_MI355X_ERR_UNSUPPORTED, "no lowering for op '" + n->name + "'");
+  }
+}
+
+void Lower::emit_reduce(Node* n) {
+  Tensor* x = n->in[0];
+  Tensor* out = n->out[0];
+  const Shape& X = x->shape;
+  std::vector<bool> red(X.rank, false);
+  for (auto d : n->l0) red[d] = true;
+  std::vector<int> order;
+  for (int i = 0; i < X.rank; ++i)
+    if (!red[i]) order.push_back(i);
+  const int n_kept = (int)order.size();
+  for (int i = 0; i < X.rank; ++i)
+    if (red[i]) order.push_back(i);
+  Shape space;
+  space.rank = X.rank;
+  Affine m;
+  m.R = m.r = X.rank;
+  int64_t n_out = 1, n_red = 1;
+  for (int k = 0; k < X.rank; ++k) {
+    space.d[k] = X.d[order[k]];
+    m.S[order[k]][k] = 1;
+    if (k < n_kept) n_out *= space.d[k]; else n_red *= space.d[k];
+  }
+  for (int attempt = 0; attempt < 2; ++attempt) {
+    Gen g(*this, space);
+    try {
+      int v = g.gen(x, m);
+      std::vector<int64_t> dims;
+      // collapse; keep the kept/reduced boundary
+      Space S = finish_space(g.P, space, n_kept, &dims);
+      check_bounds(g.P, g.leaf_t, dims);
+      std::vector<int> phys;
+      alloc_regs(g.P, {v}, &phys);
+      g.P.n_outs = 1;
+      g.P.out[0].reg = (uint8_t)phys[0];
+      tensor_alloc(out);
+      ReduceArgs A;
+      A.op = n->sub;
+      A.n_out = (uint32_t)n_out;
+      A.n_red = (uint32_t)n_red;
+      A.out = out->data();
+      A.out_dtype = out->dt;
+      const bool vec = n_red > 0 && (dims.back() % kVec) == 0 &&
+                       (n_red % kVec) == 0 && space.d[X.rank - 1] != 1;
+      set_leaf_modes(g.P, S, vec);
+      prof_begin(c, "reduce");
+      launch_reduce(g.P, S, A, vec, c->stream);
+      prof_end(c);
+      note_launch(c, g.P.n_ins > 1);
+      return;
+    } catch (GenFail&) {
+      tensor_drop_storage(out);
+      x->plan_mat = true;
+      ensure_mat(x);
+    }
+  }
+  throw Error(REW_MI355X_ERR_UNSUPPORTED, "reduction prologue too large");
+}
+
+void Lower::operand_strides(Tensor* t, Tensor** base, int64_t* off, int64_t* st) {
+  Affine m = Affine::identity(t->shape.rank);
+  Tensor* u = t;
+  for (;;) {
+    if (u->st || !u->prod) break;
+    Node* p = u->prod;
+    if (u->plan_mat || !is_view(p->kind)) {
+      ensure_mat(u);
+      break;
+    }
+    Affine m2;
+    if (!compose_view(p, m, &m2)) {
+      // reshape that splits a coordinate: read u as dense (its input
+      // materialized in the same linear order)
+      ensure_mat(u);
+      break;
+    }
+    m = m2;
+    u = p->in[0];
+  }
+  int64_t ds[kMaxRank];
+  dense_strides(u->shape, ds);
+  *off = 0;
+  for (int k = 0; k < m.R; ++k) st[k] = 0;
+  for (int i = 0; i < m.r; ++i) {
+    *off += m.off[i] * ds[i];
+    for (int k = 0; k < m.R; ++k) st[k] += m.S[i][k] * ds[i];
+  }
+  *base = u;
+}
+
+Tensor* Lower::emit_permuted_copy(Tensor* t, const std::vector<int>& perm) {
+  Shape s;
+  s.rank = t->shape.rank;
+  for (int i = 0; i < s.rank; ++i) s.d[i] = t->shape.d[perm[i]];
+  Tensor* out = new_tensor(c, t->dt, s);
+  out->plan_dead = true;  // marks a planner-private temporary
+  Affine m;
+  m.R = m.r = s.rank;
+  for (int k = 0; k < s.rank; ++k) m.S[perm[k]][k] = 1;
+  Gen g(*this, s);
+  int v = g.gen(t, m);
+  tensor_alloc(out);
+  std::vector<int64_t> dims;
+  Space S = finish_space(g.P, s, -1, &dims);
+  check_bounds(g.P, g.leaf_t, dims);
+  std::vector<int> phys;
+  alloc_regs(g.P, {v}, &phys);
+  g.P.n_outs = 1;
+  g.P.out[0].ptr = out->data();
+  g.P.out[0].dtype = (uint8_t)out->dt;
+  g.P.out[0].reg = (uint8_t)phys[0];
+  const bool vec = (dims.back() % kVec) == 0 &&
+                   (out->dt == kF32 || out->dt == kI32 || out->dt == kBF16);
+  set_leaf_modes(g.P, S, vec);
+  prof_begin(c, "ew_copy");
+  launch_ew(g.P, S, vec, c->stream);
+  prof_end(c);
+  note_launch(c, false);
+  return out;
+}
+
+// Merges the dims `dims` (in order) of a strided operand into one
+// (size, stride); false when they are not uniformly strided.
+static bool merge_group(const Shape& s, const int64_t* st, const std::vector<int64_t>& dims,
+                        int64_t* size, int64_t* stride) {
+  int64_t sz = 1, str = 0;
+  bool have = false;
+  int64_t prev_st = 0, prev_sz = 0;
+  for (auto d : dims) {
+    if (s.d[d] == 1) continue;
+    if (have && prev_st != st[d] * s.d[d]) return false;
+    prev_st = st[d];
+    prev_sz = s.d[d];
+    sz *= s.d[d];
+    str = st[d];
+    have = true;
+  }
+  (void)prev_sz;
+  for (auto d : dims) if (s.d[d] == 0) sz = 0;
+  *size = sz;
+  *stride = have ? str : 0;
+  return true;
+}
+
+void Lower::emit_dot(Node* n) {
+  Tensor *a = n->in[0], *b = n->in[1], *out = n->out[0];
+  const std::vector<int64_t> &lb = n->l0, &rb = n->l1, &lc = n->l2, &rc = n->l3;
+  std::vector<int64_t> lf, rf;
+  {
+    std::vector<bool> u(a->shape.rank, false);
+    for (auto d : lb) u[d] = true;
+    for (auto d : lc) u[d] = true;
+    for (int i = 0; i < a->shape.rank; ++i) if (!u[i]) lf.push_back(i);
+    std::vector<bool> v(b->shape.rank, false);
+    for (auto d : rb) v[d] = true;
+    for (auto d : rc) v[d] = true;
+    for (int i = 0; i < b->shape.rank; ++i) if (!v[i]) rf.push_back(i);
+  }
+  GemmArgs g;
+  std::memset(&g, 0, sizeof(g));
+  g.dtype = a->dt;
+  g.c_dtype = out->dt;
+
+  auto prep = [&](Tensor* t, const std::vector<int64_t>& g0,
+                  const std::vector<int64_t>& g1, const std::vector<int64_t>& g2,
+                  const void** ptr, int64_t* n0, int64_t* s0, int64_t* n1,
+                  int64_t* s1, int64_t* n2, int64_t* s2) {
+    for (int attempt = 0; attempt < 2; ++attempt) {
+      Tensor* base;
+      int64_t off, st[kMaxRank];
+      operand_strides(t, &base, &off, st);
+      if (merge_group(t->shape, st, g0, n0, s0) && merge_group(t->shape, st, g1, n1, s1) &&
+          merge_group(t->shape, st, g2, n2, s2)) {
+        *ptr = (const char*)base->data() + off * dt_size(base->dt);
+        return base;
+      }
+      // canonical dense copy [g0..., g1..., g2...]
+      std::vector<int> perm;
+      for (auto d : g0) perm.push_back((int)d);
+      for (auto d : g1) perm.push_back((int)d);
+      for (auto d : g2) perm.push_back((int)d);
+      Tensor* cp = emit_permuted_copy(t, perm);
+      int64_t ds[kMaxRank];
+      dense_strides(cp->shape, ds);
+      // rebuild groups on the copy
+      std::vector<int64_t> h0, h1, h2;
+      int k = 0;
+      for (size_t i = 0; i < g0.size(); ++i) h0.push_back(k++);
+      for (size_t i = 0; i < g1.size(); ++i) h1.push_back(k++);
+      for (size_t i = 0; i < g2.size(); ++i) h2.push_back(k++);
+      merge_group(cp->shape, ds, h0, n0, s0);
+      merge_group(cp->shape, ds, h1, n1, s1);
+      merge_group(cp->shape, ds, h2, n2, s2);
+      *ptr = cp->data();
+      return cp;
+    }
+    return (Tensor*)nullptr;
+  };
+  int64_t bA, bB, kA, kB;
+  Tensor* ta = prep(a, lb, lf, lc, &g.a, &bA, &g.a_sb, &g.M, &g.a_sm, &kA, &g.a_sk);
+  Tensor* tb = prep(b, rb, rc, rf, &g.b, &bB, &g.b_sb, &kB, &g.b_sk, &g.N, &g.b_sn);
+  g.batch = bA;
+  g.K = kA;
+  if (g.M == 1) g.a_sm = 0;
+  if (g.N == 1) g.b_sn = 0;
+  if (g.batch == 1) { g.a_sb = 0; g.b_sb = 0; }
+  if (g.K == 1) { g.a_sk = 0; g.b_sk = 0; }
+  // operand extents must stay inside their base tensors
+  auto extent_ok = [&](Tensor* base, const void* p, int64_t n0, int64_t s0, int64_t n1,
+                       int64_t s1, int64_t n2, int64_t s2) {
+    const int64_t off = ((const char*)p - (const char*)base->data()) / dt_size(base->dt);
+    int64_t lo = off, hi = off;
+    for (auto e : {s0 * (n0 - 1), s1 * (n1 - 1), s2 * (n2 - 1)}) {
+      if (e < 0) lo += e; else hi += e;
+    }
+    return lo >= 0 && hi < base->numel();
+  };
+  if (g.batch > 0 && g.M > 0 && g.N > 0 && g.K > 0 &&
+      (!extent_ok(ta, g.a, g.batch, g.a_sb, g.M, g.a_sm, g.K, g.a_sk) ||
+       !extent_ok(tb, g.b, g.batch, g.b_sb, g.K, g.b_sk, g.N, g.b_sn)))
+    throw Error(REW_MI355X_ERR_INVALID, "internal: dot_general operand view out of bounds");
+  tensor_alloc(out);
+  g.c = out->data();
+  g.c_sb = g.M * g.N;
+  g.c_sm = g.N;
+  if (g.K == 0) {
+    // empty contraction: zeros
+    REW_HIP(hipMemsetAsync(out->data(), 0, out->nbytes(), c->stream));
+  } else {
+    prof_begin(c, gemm_variant(g));
+    launch_gemm(g, c->stream);
+    prof_end(c);
+    note_launch(c, false);
+  }
+  // canonical copies made for this GEMM die with it (stream-ordered free)
+  for (Tensor* t : {ta, tb})
+    if (t && t->ctx == c && !t->prod && t->ext == 0 && t->uses == 0 && t != a &&
+        t != b && t->plan_dead)
+      maybe_destroy(t);
+}
+
+void Lower::emit_gather(Node* n) {
+  Tensor *src = n->in[0], *ix = n->in[1], *out = n->out[0];
+  ensure_mat(src);
+  ensure_mat(ix);
+  tensor_alloc(out);
+  GatherArgs g;
+  g.src = src->data();
+  g.index = ix->data();
+  g.out = out->data();
+  g.index_dtype = ix->dt;
+  const int dim = (int)n->i0;
+  g.n_pre = 1;
+  for (int i = 0; i < dim; ++i) g.n_pre *= src->shape.d[i];
+  g.src_dim = src->shape.d[dim];
+  g.n_idx = ix->numel();
+  int64_t post = 1;
+  for (int i = dim + 1; i < src->shape.rank; ++i) post *= src->shape.d[i];
+  g.row_bytes = post * dt_size(src->dt);
+  prof_begin(c, "gather_rows");
+  launch_gather(g, c->stream);
+  prof_end(c);
+  note_launch(c, false);
+}
+
+void Lower::emit_argmax(Node* n) {
+  throw Error(REW_MI355X_ERR_UNSUPPORTED, "argmax lowering not built yet");
+}
+void Lower::emit_topk(Node* n) {
+  throw Error(REW_MI355X_ERR_UNSUPPORTED, "topK lowering not built yet");
+}
+
+// ---------------------------------------------------------------------------
+// flush
+// ---------------------------------------------------------------------------
+
+void flush(Ctx* c) {
+  if (c->pending.empty()) return;
+  std::vector<Node*> all;
+  all.swap(c->pending);
+  c->stats.flushes++;
+
+  // 1. dead-node elimination (reverse creation order)
+  for (size_t i = all.size(); i-- > 0;) {
+    Node* n = all[i];
+    bool dead = true;
+    for (Tensor* t : n->out)
+      if (t->ext > 0 || t->uses > 0) dead = false;
+    if (dead) {
+      n->dead = true;
+      for (Tensor* t : n->in) t->uses--;
+    }
+  }
+  Lower L(c);
+  for (Node* n : all)
+    if (!n->dead) L.nodes.push_back(n);
+
+  // 2. classification
+  std::unordered_map<Tensor*, std::vector<Node*>> consumers;
+  for (Node* n : L.nodes)
+    for (Tensor* t : n->in) consumers[t].push_back(n);
+  // walk consumers through views: (count of expression uses, needs memory)
+  std::function<void(Tensor*, int*, bool*)> uses_of = [&](Tensor* t, int* cnt, bool* mem) {
+    auto it = consumers.find(t);
+    if (it == consumers.end()) return;
+    for (Node* q : it->second) {
+      if (is_view(q->kind) && q->out[0]->ext == 0) {
+        uses_of(q->out[0], cnt, mem);
+      } else {
+        *cnt += 1;
+        if (!takes_expression(q->kind)) *mem = true;
+      }
+    }
+  };
+  std::unordered_map<Tensor*, int> cost;
+  for (Node* n : L.nodes) {
+    for (Tensor* t : n->out) {
+      t->plan_mat = false;
+      if (!is_ew(n->kind) && !is_view(n->kind)) {
+        t->plan_mat = true;
+        continue;
+      }
+      if (t->ext > 0) {
+        t->plan_mat = true;
+        continue;
+      }
+      if (is_view(n->kind)) continue;
+      int cnt = 0;
+      bool mem = false;
+      uses_of(t, &cnt, &mem);
+      int cst = 1;
+      for (Tensor* x : n->in) {
+        Tensor* y = x;
+        while (y->prod && is_view(y->prod->kind) && !y->plan_mat && !y->st) y = y->prod->in[0];
+        if (y->prod && !y->st && !y->plan_mat && is_ew(y->prod->kind)) cst += cost[y];
+      }
+      cost[t] = cst;
+      if (mem || (cnt >= 2 && cst > 2) || cst > 48) t->plan_mat = true;
+      if (t->plan_mat) cost[t] = 0;
+    }
+  }
+
+  // 3. emission in creation order
+  std::exception_ptr err;
+  try {
+    for (Node* n : L.nodes)
+      for (Tensor* t : n->out)
+        if (t->plan_mat && !t->st) L.ensure_mat(t);
+  } catch (...) {
+    err = std::current_exception();
+  }
+
+  // 4. release: graph references drop, temporaries free
+  for (Node* n : all) {
+    if (!n->dead)
+      for (Tensor* t : n->in) t->uses--;
+  }
+  std::vector<Tensor*> touched;
+  for (Node* n : all) {
+    for (Tensor* t : n->in) touched.push_back(t);
+    for (Tensor* t : n->out) {
+      t->prod = nullptr;
+      touched.push_back(t);
+    }
+  }
+  std::sort(touched.begin(), touched.end());
+  touched.erase(std::unique(touched.begin(), touched.end()), touched.end());
+  for (Tensor* t : touched) {
+    t->plan_mat = false;
+    maybe_destroy(t);
+  }
+  for (Node* n : all) delete n;
+  if (err) std::rethrow_exception(err);
+}
+
+}  // namespace rew

@@ -1,0 +1,641 @@
+// Op table, attribute parsing and output shape/dtype derivation of the
+// eager backend.  Mirrors executeEagerOp's front half
+// (src/rew/eager.nim:717-1283, 1717-1735): the op name selects a kind,
+// string attrs are parsed in rew's wire format, outputs get their final
+// shape/dtype at record time, and every error names the op.
+#include <algorithm>
+#include <cctype>
+#include <cstdlib>
+#include <unordered_map>
+
+#include "kernels.h"
+#include "runtime.h"
+
+namespace rew {
+
+// ---- dtype names (src/rew/dtype.nim:58-108) -----------------------------------
+
+static const char* kDtNames[kNumDT] = {
+    "bool", "int8", "int16", "int32", "int64", "uint8", "uint16", "uint32",
+    "uint64", "float16", "bfloat16", "float32", "float64", "complex64",
+    "complex128", "int4", "uint4", "nf4", "float8_e4m3fn", "float8_e5m2"};
+static const char* kDtEnum[kNumDT] = {
+    "dtBool", "dtInt8", "dtInt16", "dtInt32", "dtInt64", "dtUint8", "dtUint16",
+    "dtUint32", "dtUint64", "dtFloat16", "dtBFloat16", "dtFloat32", "dtFloat64",
+    "dtComplex64", "dtComplex128", "dtInt4", "dtUint4", "dtNF4",
+    "dtFloat8E4M3Fn", "dtFloat8E5M2"};
+
+const char* dt_name(int dt) { return (dt >= 0 && dt < kNumDT) ? kDtNames[dt] : "?"; }
+const char* dt_enum_name(int dt) { return (dt >= 0 && dt < kNumDT) ? kDtEnum[dt] : "?"; }
+
+int parse_dtype(const std::string& s) {
+  for (int i = 0; i < kNumDT; ++i)
+    if (s == kDtNames[i] || s == kDtEnum[i]) return i;
+  return -1;
+}
+
+std::string Shape::str() const {
+  std::string r = "[";
+  for (int i = 0; i < rank; ++i) {
+    if (i) r += ",";
+    r += std::to_string(d[i]);
+  }
+  return r + "]";
+}
+
+// ---- op table -------------------------------------------------------------------
+
+enum BinOp { B_ADD, B_SUB, B_MUL, B_DIV, B_MAX, B_MIN, B_ATAN2, B_POW, B_REM,
+             B_AND, B_OR, B_XOR, B_SHL, B_SHRA, B_SHRL };
+enum UnOp { U_NEG, U_ABS, U_EXP, U_LOG, U_SQRT, U_TANH, U_CBRT, U_CEIL, U_EXPM1,
+            U_FLOOR, U_LOG1P, U_LOGISTIC, U_TAN, U_SIGN, U_ROUNDAFZ, U_ROUNDEVEN,
+            U_NOT, U_CLZ, U_POPCNT, U_IDENT, U_SIN, U_COS, U_RSQRT };
+
+struct OpSpec {
+  int kind;
+  int sub;
+};
+
+static const std::unordered_map<std::string, OpSpec>& op_table() {
+  static const std::unordered_map<std::string, OpSpec> t = {
+      {"add", {K_BINARY, B_ADD}}, {"sub", {K_BINARY, B_SUB}},
+      {"mul", {K_BINARY, B_MUL}}, {"divide", {K_BINARY, B_DIV}},
+      {"maximum", {K_BINARY, B_MAX}}, {"minimum", {K_BINARY, B_MIN}},
+      {"atan2", {K_BINARY, B_ATAN2}}, {"power", {K_BINARY, B_POW}},
+      {"remainder", {K_BINARY, B_REM}}, {"bitwiseAnd", {K_BINARY, B_AND}},
+      {"bitwiseOr", {K_BINARY, B_OR}}, {"bitwiseXor", {K_BINARY, B_XOR}},
+      {"shiftLeft", {K_BINARY, B_SHL}},
+      {"shiftRightArithmetic", {K_BINARY, B_SHRA}},
+      {"shiftRightLogical", {K_BINARY, B_SHRL}},
+      {"neg", {K_UNARY, U_NEG}}, {"abs", {K_UNARY, U_ABS}},
+      {"exp", {K_UNARY, U_EXP}}, {"log", {K_UNARY, U_LOG}},
+      {"sqrt", {K_UNARY, U_SQRT}}, {"tanh", {K_UNARY, U_TANH}},
+      {"cbrt", {K_UNARY, U_CBRT}}, {"ceil", {K_UNARY, U_CEIL}},
+      {"expm1", {K_UNARY, U_EXPM1}}, {"floor", {K_UNARY, U_FLOOR}},
+      {"log1p", {K_UNARY, U_LOG1P}}, {"logistic", {K_UNARY, U_LOGISTIC}},
+      {"tan", {K_UNARY, U_TAN}}, {"sign", {K_UNARY, U_SIGN}},
+      {"roundNearestAfz", {K_UNARY, U_ROUNDAFZ}},
+      {"roundNearestEven", {K_UNARY, U_ROUNDEVEN}},
+      {"bitwiseNot", {K_UNARY, U_NOT}}, {"countLeadingZeros", {K_UNARY, U_CLZ}},
+      {"popcnt", {K_UNARY, U_POPCNT}},
+      {"optimizationBarrier", {K_UNARY, U_IDENT}},
+      {"stopGradient", {K_UNARY, U_IDENT}},
+      {"sine", {K_UNARY, U_SIN}}, {"cosine", {K_UNARY, U_COS}},
+      {"rsqrt", {K_UNARY, U_RSQRT}},
+      {"astype", {K_CONVERT, 0}}, {"isFinite", {K_ISFINITE, 0}},
+      {"bitcastConvert", {K_BITCAST, 0}},
+      {"reducePrecision", {K_REDUCE_PRECISION, 0}},
+      {"reshape", {K_RESHAPE, 0}}, {"transpose", {K_TRANSPOSE, 0}},
+      {"reverse", {K_REVERSE, 0}}, {"broadcastTo", {K_BROADCAST_TO, 0}},
+      {"broadcast", {K_BROADCAST, 0}}, {"slice", {K_SLICE, 0}},
+      {"concat", {K_CONCAT, 0}}, {"iota", {K_IOTA, 0}},
+      {"compare", {K_COMPARE, 0}}, {"select", {K_SELECT, 0}},
+      {"clamp", {K_CLAMP, 0}},
+      {"reduceSum", {K_REDUCE, RED_SUM}}, {"reduceMax", {K_REDUCE, RED_MAX}},
+      {"reduceMin", {K_REDUCE, RED_MIN}}, {"reduceProd", {K_REDUCE, RED_PROD}},
+      {"all", {K_REDUCE, RED_AND}}, {"any", {K_REDUCE, RED_OR}},
+      {"dotGeneral", {K_DOT_GENERAL, 0}}, {"dot", {K_DOT, 0}},
+      {"torchIndexSelect", {K_INDEX_SELECT, 0}},
+      // backend extensions (no eager counterpart in the reference)
+      {"argmax", {K_ARGMAX, 0}}, {"topK", {K_TOPK, 0}},
+  };
+  return t;
+}
+
+// Op names rew's table knows (src/rew/eager.nim:775-868) that this backend
+// does not implement natively.
+static bool known_but_unimplemented(const std::string& n) {
+  static const char* names[] = {
+      "complex", "real", "imag", "conv2d", "maxPool2d", "batchNormInference",
+      "batchNormTraining", "batchNormGrad", "cholesky", "getDimensionSize",
+      "pad", "dynamicSlice", "dynamicUpdateSlice", "replicaId", "partitionId",
+      "setDimensionSize", "dynamicReshape", "dynamicPad", "dynamicIota",
+      "realDynamicSlice", "dynamicBroadcastInDim", "fft", "triangularSolve",
+      "einsum", "unaryEinsum"};
+  for (auto* s : names)
+    if (n == s) return true;
+  return false;
+}
+
+// ---- attribute parsing (src/rew/eager.nim:887-983) --------------------------------
+
+using Attrs = std::vector<std::pair<std::string, std::string>>;
+
+static const std::string& find_attr(const Attrs& a, const std::string& key,
+                                    const std::string& op) {
+  for (auto& kv : a)
+    if (kv.first == key) return kv.second;
+  invalid("eager '" + op + "': required attr '" + key + "' missing");
+}
+
+static std::string strip(const std::string& s) {
+  size_t b = 0, e = s.size();
+  while (b < e && std::isspace((unsigned char)s[b])) ++b;
+  while (e > b && std::isspace((unsigned char)s[e - 1])) --e;
+  return s.substr(b, e - b);
+}
+
+static int64_t parse_int(const std::string& s0, const std::string& op) {
+  std::string s = strip(s0);
+  if (s.empty()) invalid("eager '" + op + "': malformed int attr '" + s0 + "'");
+  char* end = nullptr;
+  long long v = std::strtoll(s.c_str(), &end, 10);
+  if (*end != '\0') invalid("eager '" + op + "': malformed int attr '" + s0 + "'");
+  return v;
+}
+
+// Accepts "[1,2]" (joinInts) and "@[1, 2]" (Nim seq repr).
+static std::vector<int64_t> parse_int_list(const std::string& s0,
+                                           const std::string& op) {
+  std::string t = strip(s0);
+  if (!t.empty() && t[0] == '@') t = t.substr(1);
+  if (t.size() < 2 || t.front() != '[' || t.back() != ']')
+    invalid("eager '" + op + "': malformed int-list attr (expected '[a,b,c]', got '" +
+            s0 + "')");
+  std::string body = strip(t.substr(1, t.size() - 2));
+  std::vector<int64_t> r;
+  if (body.empty()) return r;
+  size_t p = 0;
+  while (p <= body.size()) {
+    size_t q = body.find(',', p);
+    if (q == std::string::npos) q = body.size();
+    r.push_back(parse_int(body.substr(p, q - p), op));
+    p = q + 1;
+  }
+  return r;
+}
+
+static int parse_dtype_attr(const std::string& s, const std::string& op) {
+  int dt = parse_dtype(strip(s));
+  if (dt < 0) invalid("eager '" + op + "': unknown dtype attr '" + s + "'");
+  return dt;
+}
+
+static int parse_cmp(const std::string& s, const std::string& op) {
+  static const char* d[] = {"EQ", "NE", "LT", "LE", "GT", "GE"};
+  for (int i = 0; i < 6; ++i)
+    if (s == d[i]) return i;
+  invalid("eager '" + op + "': invalid comparison_direction '" + s + "'");
+}
+
+// ---- helpers ----------------------------------------------------------------------
+
+static void check_axis_list(const std::vector<int64_t>& dims, int rank,
+                            const std::string& op, const char* what) {
+  std::vector<bool> seen(rank, false);
+  for (auto d : dims) {
+    if (d < 0 || d >= rank)
+      invalid("eager '" + op + "': " + what + " index " + std::to_string(d) +
+              " out of range for rank " + std::to_string(rank));
+    if (seen[d])
+      invalid("eager '" + op + "': " + what + " index " + std::to_string(d) +
+              " repeated");
+    seen[d] = true;
+  }
+}
+
+static bool vm_dtype_ok(int dt) {
+  switch (dt) {
+    case kBool: case kI8: case kI16: case kI32: case kU8: case kU16: case kU32:
+    case kF16: case kBF16: case kF32:
+      return true;
+    default:
+      return false;
+  }
+}
+
+static void require_vm_dtype(int dt, const std::string& op) {
+  if (!vm_dtype_ok(dt))
+    fail(REW_MI355X_ERR_UNSUPPORTED, "eager '" + op + "': dtype " +
+                                         dt_enum_name(dt) +
+                                         " not supported by the mi355x backend");
+}
+
+static const int64_t kMaxElems = (int64_t)1 << 31;
+
+// ---- record ------------------------------------------------------------------------
+
+std::vector<Tensor*> record_op(Ctx* c, const std::string& op,
+                               const std::vector<Tensor*>& ins,
+                               const Attrs& attrs) {
+  auto it = op_table().find(op);
+  if (it == op_table().end()) {
+    if (known_but_unimplemented(op))
+      fail(REW_MI355X_ERR_UNSUPPORTED,
+           "eager backend (mi355x): op '" + op + "' is not implemented natively");
+    fail(REW_MI355X_ERR_UNSUPPORTED, "eager backend: unsupported op '" + op + "'");
+  }
+  const OpSpec spec = it->second;
+  for (size_t i = 0; i < ins.size(); ++i) {
+    if (ins[i]->ctx != c)
+      invalid("eager '" + op + "': cross-device operands forbidden");
+  }
+  auto nin = [&](size_t n) {
+    if (ins.size() != n)
+      invalid("eager '" + op + "': expected " + std::to_string(n) +
+              " operand(s), got " + std::to_string(ins.size()));
+  };
+
+  Node* n = new Node();
+  n->kind = spec.kind;
+  n->sub = spec.sub;
+  n->name = op;
+  n->in = ins;
+  std::vector<std::pair<int, Shape>> outs;  // dtype, shape
+
+  try {
+    switch (spec.kind) {
+      case K_BINARY: {
+        nin(2);
+        Tensor *a = ins[0], *b = ins[1];
+        if (a->dt != b->dt)
+          invalid("eager '" + op + "': dtype mismatch (" + dt_enum_name(a->dt) +
+                  " vs " + dt_enum_name(b->dt) + ")");
+        if (a->shape != b->shape) invalid("eager '" + op + "': shape mismatch");
+        require_vm_dtype(a->dt, op);
+        bool fl = dt_is_float(a->dt);
+        int s = spec.sub;
+        if ((s == B_AND || s == B_OR || s == B_XOR || s == B_SHL || s == B_SHRA ||
+             s == B_SHRL) && fl)
+          invalid("eager '" + op + "': expected an integer or bool operand");
+        if ((s == B_ATAN2 || s == B_POW) && !fl)
+          fail(REW_MI355X_ERR_UNSUPPORTED, "eager '" + op + "': integer " + op +
+                                               " not supported");
+        outs.push_back({a->dt, a->shape});
+        break;
+      }
+      case K_UNARY: {
+        nin(1);
+        require_vm_dtype(ins[0]->dt, op);
+        int s = spec.sub;
+        bool fl = dt_is_float(ins[0]->dt);
+        bool float_only = !(s == U_NEG || s == U_ABS || s == U_NOT || s == U_CLZ ||
+                            s == U_POPCNT || s == U_IDENT || s == U_SIGN);
+        if (float_only && !fl)
+          invalid("eager '" + op + "': expected a floating-point operand");
+        if ((s == U_NOT || s == U_CLZ || s == U_POPCNT) && fl)
+          invalid("eager '" + op + "': expected an integer operand");
+        outs.push_back({ins[0]->dt, ins[0]->shape});
+        break;
+      }
+      case K_CONVERT: {
+        nin(1);
+        n->dt_attr = parse_dtype_attr(find_attr(attrs, "dtype", op), op);
+        require_vm_dtype(ins[0]->dt, op);
+        require_vm_dtype(n->dt_attr, op);
+        outs.push_back({n->dt_attr, ins[0]->shape});
+        break;
+      }
+      case K_ISFINITE: {
+        nin(1);
+        if (!dt_is_float(ins[0]->dt)) invalid("eager 'isFinite': expected float operand");
+        require_vm_dtype(ins[0]->dt, op);
+        outs.push_back({kBool, ins[0]->shape});
+        break;
+      }
+      case K_REDUCE_PRECISION: {
+        nin(1);
+        n->i0 = parse_int(find_attr(attrs, "exponent_bits", op), op);
+        n->i1 = parse_int(find_attr(attrs, "mantissa_bits", op), op);
+        if (ins[0]->dt != kF32 ||
+            !((n->i0 == 8 && n->i1 == 7) || (n->i0 == 5 && n->i1 == 10) ||
+              (n->i0 == 8 && n->i1 == 23)))
+          fail(REW_MI355X_ERR_UNSUPPORTED,
+               "eager 'reducePrecision': only float32 to bf16/f16/f32 precision");
+        outs.push_back({ins[0]->dt, ins[0]->shape});
+        break;
+      }
+      case K_BITCAST: {
+        nin(1);
+        n->dt_attr = parse_dtype_attr(find_attr(attrs, "dtype", op), op);
+        Shape s(parse_int_list(find_attr(attrs, "output_shape", op), op));
+        if (dt_size(n->dt_attr) != dt_size(ins[0]->dt) || s.numel() != ins[0]->numel())
+          fail(REW_MI355X_ERR_UNSUPPORTED,
+               "eager 'bitcastConvert': only same-width element types");
+        n->l0 = s.vec();
+        outs.push_back({n->dt_attr, s});
+        break;
+      }
+      case K_RESHAPE: {
+        nin(1);
+        n->l0 = parse_int_list(find_attr(attrs, "shape", op), op);
+        Shape s(n->l0);
+        for (auto d : n->l0)
+          if (d < 0) invalid("eager 'reshape': negative dim");
+        if (s.numel() != ins[0]->numel())
+          invalid("eager 'reshape': element count mismatch");
+        outs.push_back({ins[0]->dt, s});
+        break;
+      }
+      case K_TRANSPOSE: {
+        nin(1);
+        n->l0 = parse_int_list(find_attr(attrs, "permutation", op), op);
+        int r = ins[0]->shape.rank;
+        if ((int)n->l0.size() != r)
+          invalid("eager 'transpose': permutation length does not match rank");
+        check_axis_list(n->l0, r, op, "permutation");
+        Shape s;
+        s.rank = r;
+        for (int i = 0; i < r; ++i) s.d[i] = ins[0]->shape.d[n->l0[i]];
+        outs.push_back({ins[0]->dt, s});
+        break;
+      }
+      case K_REVERSE: {
+        nin(1);
+        n->l0 = parse_int_list(find_attr(attrs, "dimensions", op), op);
+        check_axis_list(n->l0, ins[0]->shape.rank, op, "dimensions");
+        outs.push_back({ins[0]->dt, ins[0]->shape});
+        break;
+      }
+      case K_BROADCAST_TO: {
+        nin(1);
+        n->l0 = parse_int_list(find_attr(attrs, "output_shape", op), op);
+        n->l1 = parse_int_list(find_attr(attrs, "broadcast_dimensions", op), op);
+        Shape s(n->l0);
+        const Shape& is = ins[0]->shape;
+        if ((int)n->l1.size() != is.rank)
+          invalid("eager 'broadcastTo': broadcast_dimensions length " +
+                  std::to_string(n->l1.size()) + " does not match operand rank " +
+                  std::to_string(is.rank));
+        check_axis_list(n->l1, s.rank, op, "broadcast_dimensions");
+        for (int i = 0; i < is.rank; ++i) {
+          int64_t od = s.d[n->l1[i]];
+          if (is.d[i] != 1 && is.d[i] != od)
+            invalid("eager 'broadcastTo': operand dim " + std::to_string(i) +
+                    " (size " + std::to_string(is.d[i]) +
+                    ") is not 1 and does not match output dim " +
+                    std::to_string(n->l1[i]) + " (size " + std::to_string(od) + ")");
+        }
+        outs.push_back({ins[0]->dt, s});
+        break;
+      }
+      case K_BROADCAST: {
+        nin(1);
+        n->l0 = parse_int_list(find_attr(attrs, "broadcast_sizes", op), op);
+        std::vector<int64_t> v = n->l0;
+        for (int i = 0; i < ins[0]->shape.rank; ++i) v.push_back(ins[0]->shape.d[i]);
+        outs.push_back({ins[0]->dt, Shape(v)});
+        break;
+      }
+      case K_SLICE: {
+        nin(1);
+        n->l0 = parse_int_list(find_attr(attrs, "start_indices", op), op);
+        n->l1 = parse_int_list(find_attr(attrs, "limit_indices", op), op);
+        n->l2 = parse_int_list(find_attr(attrs, "strides", op), op);
+        const Shape& is = ins[0]->shape;
+        int r = is.rank;
+        if ((int)n->l0.size() != r || (int)n->l1.size() != r || (int)n->l2.size() != r)
+          invalid("eager slice: index arrays length must match operand rank " +
+                  std::to_string(r));
+        Shape s;
+        s.rank = r;
+        for (int i = 0; i < r; ++i) {
+          if (n->l0[i] < 0 || n->l1[i] > is.d[i] || n->l0[i] > n->l1[i] || n->l2[i] <= 0)
+            invalid("eager slice: invalid bounds at dim " + std::to_string(i));
+          s.d[i] = (n->l1[i] - n->l0[i] + n->l2[i] - 1) / n->l2[i];
+        }
+        outs.push_back({ins[0]->dt, s});
+        break;
+      }
+      case K_CONCAT: {
+        if (ins.empty()) invalid("eager concat: empty input list");
+        n->i0 = parse_int(find_attr(attrs, "dimension", op), op);
+        Shape s = ins[0]->shape;
+        if (n->i0 < 0 || n->i0 >= s.rank)
+          invalid("eager concat: dimension " + std::to_string(n->i0) +
+                  " out of range for rank " + std::to_string(s.rank));
+        for (size_t i = 1; i < ins.size(); ++i) {
+          if (ins[i]->dt != ins[0]->dt)
+            invalid("eager concat: dtype mismatch at operand #" + std::to_string(i));
+          if (ins[i]->shape.rank != s.rank)
+            invalid("eager concat: rank mismatch at operand #" + std::to_string(i));
+          for (int d = 0; d < s.rank; ++d)
+            if (d != n->i0 && ins[i]->shape.d[d] != s.d[d])
+              invalid("eager concat: shape mismatch at operand #" + std::to_string(i));
+          s.d[n->i0] += ins[i]->shape.d[n->i0];
+        }
+        require_vm_dtype(ins[0]->dt, op);
+        outs.push_back({ins[0]->dt, s});
+        break;
+      }
+      case K_IOTA: {
+        nin(0);
+        n->dt_attr = parse_dtype_attr(find_attr(attrs, "dtype", op), op);
+        n->l0 = parse_int_list(find_attr(attrs, "shape", op), op);
+        n->i0 = parse_int(find_attr(attrs, "dimension", op), op);
+        for (auto& kv : attrs)
+          if (kv.first == "device") {
+            std::string d = strip(kv.second);
+            size_t colon = d.find(':');
+            if (colon != std::string::npos && d.substr(0, colon) == "mi355x" &&
+                parse_int(d.substr(colon + 1), op) != c->ordinal)
+              invalid("eager 'iota': device attr '" + d +
+                      "' does not match this context");
+          }
+        Shape s(n->l0);
+        if (n->i0 < 0 || n->i0 >= s.rank)
+          invalid("eager 'iota': dimension out of range");
+        if (n->dt_attr == kBool) invalid("eager 'iota': bool dtype is not supported");
+        require_vm_dtype(n->dt_attr, op);
+        outs.push_back({n->dt_attr, s});
+        break;
+      }
+      case K_COMPARE: {
+        nin(2);
+        n->cmp = parse_cmp(find_attr(attrs, "comparison_direction", op), op);
+        if (ins[0]->dt != ins[1]->dt || ins[0]->shape != ins[1]->shape)
+          invalid("eager 'compare': operands must agree on dtype and shape");
+        require_vm_dtype(ins[0]->dt, op);
+        outs.push_back({kBool, ins[0]->shape});
+        break;
+      }
+      case K_SELECT: {
+        nin(3);
+        if (ins[0]->dt != kBool) invalid("eager 'select': pred must be bool");
+        if (ins[1]->dt != ins[2]->dt || ins[1]->shape != ins[2]->shape)
+          invalid("eager 'select': on_true/on_false must agree on dtype and shape");
+        if (ins[0]->shape != ins[1]->shape)
+          fail(REW_MI355X_ERR_UNSUPPORTED,
+               "eager 'select': pred shape must equal the operand shape");
+        require_vm_dtype(ins[1]->dt, op);
+        outs.push_back({ins[1]->dt, ins[0]->shape});
+        break;
+      }
+      case K_CLAMP: {
+        nin(3);
+        for (int i : {0, 2}) {
+          if (ins[i]->dt != ins[1]->dt) invalid("eager 'clamp': dtype mismatch");
+          if (ins[i]->shape.rank != 0 && ins[i]->shape != ins[1]->shape)
+            invalid("eager 'clamp': bounds must be scalars or match the operand shape");
+        }
+        require_vm_dtype(ins[1]->dt, op);
+        outs.push_back({ins[1]->dt, ins[1]->shape});
+        break;
+      }
+      case K_REDUCE: {
+        nin(1);
+        n->l0 = parse_int_list(find_attr(attrs, "dims", op), op);
+        const Shape& is = ins[0]->shape;
+        check_axis_list(n->l0, is.rank, op, "dims");
+        int s = spec.sub;
+        if (s == RED_AND || s == RED_OR) {
+          if (ins[0]->dt != kBool)
+            invalid("eager '" + op + "': expected bool tensor (got " +
+                    dt_enum_name(ins[0]->dt) + ")");
+        } else if (ins[0]->dt != kF32) {
+          // reductionInit (src/rew/eager.nim:1027-1033)
+          invalid("eager '" + op + "': v1 supports only float32 (got " +
+                  dt_enum_name(ins[0]->dt) + ")");
+        }
+        std::vector<bool> red(is.rank, false);
+        for (auto d : n->l0) red[d] = true;
+        std::vector<int64_t> od;
+        for (int i = 0; i < is.rank; ++i)
+          if (!red[i]) od.push_back(is.d[i]);
+        outs.push_back({ins[0]->dt, Shape(od)});
+        break;
+      }
+      case K_ARGMAX: {
+        nin(1);
+        n->i0 = parse_int(find_attr(attrs, "dimension", op), op);
+        const Shape& is = ins[0]->shape;
+        if (n->i0 < 0) n->i0 += is.rank;
+        if (n->i0 < 0 || n->i0 >= is.rank) invalid("eager 'argmax': dim out of range");
+        if (ins[0]->dt != kF32) invalid("eager 'argmax': float32 operand required");
+        if (is.d[n->i0] == 0) invalid("eager 'argmax': empty dimension");
+        std::vector<int64_t> od;
+        for (int i = 0; i < is.rank; ++i)
+          if (i != n->i0) od.push_back(is.d[i]);
+        outs.push_back({kI32, Shape(od)});
+        break;
+      }
+      case K_TOPK: {
+        nin(1);
+        n->i0 = parse_int(find_attr(attrs, "k", op), op);
+        n->i1 = parse_int(find_attr(attrs, "dimension", op), op);
+        n->i2 = 1;
+        for (auto& kv : attrs)
+          if (kv.first == "largest") n->i2 = (strip(kv.second) == "true" || strip(kv.second) == "1");
+        const Shape& is = ins[0]->shape;
+        if (n->i1 < 0) n->i1 += is.rank;
+        if (is.rank == 0 || n->i1 != is.rank - 1)
+          fail(REW_MI355X_ERR_UNSUPPORTED, "eager 'topK': only the last dimension");
+        if (n->i0 <= 0 || n->i0 > is.d[n->i1])
+          invalid("eager 'topK': k out of range");
+        if (n->i0 > 64) fail(REW_MI355X_ERR_UNSUPPORTED, "eager 'topK': k > 64");
+        if (ins[0]->dt != kF32) invalid("eager 'topK': float32 operand required");
+        Shape s = is;
+        s.d[n->i1] = n->i0;
+        outs.push_back({ins[0]->dt, s});
+        outs.push_back({kI32, s});
+        break;
+      }
+      case K_DOT:
+      case K_DOT_GENERAL: {
+        nin(2);
+        Tensor *a = ins[0], *b = ins[1];
+        if (a->dt != b->dt)
+          invalid("eager '" + op + "': dtype mismatch (" + dt_enum_name(a->dt) +
+                  " vs " + dt_enum_name(b->dt) + ")");
+        if (a->dt != kF32 && a->dt != kBF16 && a->dt != kF16)
+          fail(REW_MI355X_ERR_UNSUPPORTED,
+               "eager '" + op + "': dtype " + dt_enum_name(a->dt) +
+                   " not supported by the mi355x backend");
+        if (spec.kind == K_DOT) {
+          // stablehlo.dot: rank <= 2, contracts lhs last dim with rhs first dim.
+          int ra = a->shape.rank, rb = b->shape.rank;
+          if (ra < 1 || ra > 2 || rb < 1 || rb > 2)
+            invalid("eager dot: operands must be rank 1 or 2");
+          n->kind = K_DOT_GENERAL;
+          n->l0 = {};
+          n->l1 = {};
+          n->l2 = {ra - 1};
+          n->l3 = {0};
+        } else {
+          n->l0 = parse_int_list(find_attr(attrs, "lhs_batching", op), op);
+          n->l1 = parse_int_list(find_attr(attrs, "rhs_batching", op), op);
+          n->l2 = parse_int_list(find_attr(attrs, "lhs_contracting", op), op);
+          n->l3 = parse_int_list(find_attr(attrs, "rhs_contracting", op), op);
+        }
+        const Shape &sa = a->shape, &sb = b->shape;
+        if (n->l0.size() != n->l1.size() || n->l2.size() != n->l3.size())
+          invalid("eager '" + op + "': batching/contracting lists differ in length");
+        std::vector<int64_t> la = n->l0, lb = n->l1;
+        la.insert(la.end(), n->l2.begin(), n->l2.end());
+        lb.insert(lb.end(), n->l3.begin(), n->l3.end());
+        check_axis_list(la, sa.rank, op, "lhs");
+        check_axis_list(lb, sb.rank, op, "rhs");
+        for (size_t i = 0; i < n->l0.size(); ++i)
+          if (sa.d[n->l0[i]] != sb.d[n->l1[i]])
+            invalid("eager '" + op + "': batching dim size mismatch");
+        for (size_t i = 0; i < n->l2.size(); ++i)
+          if (sa.d[n->l2[i]] != sb.d[n->l3[i]])
+            invalid("eager '" + op + "': contracting dim size mismatch");
+        // dotGeneralShape (src/rew/eager.nim:1000-1014)
+        std::vector<bool> ua(sa.rank, false), ub(sb.rank, false);
+        for (auto d : la) ua[d] = true;
+        for (auto d : lb) ub[d] = true;
+        std::vector<int64_t> od;
+        for (auto d : n->l0) od.push_back(sa.d[d]);
+        for (int i = 0; i < sa.rank; ++i)
+          if (!ua[i]) od.push_back(sa.d[i]);
+        for (int i = 0; i < sb.rank; ++i)
+          if (!ub[i]) od.push_back(sb.d[i]);
+        outs.push_back({a->dt, Shape(od)});
+        break;
+      }
+      case K_INDEX_SELECT: {
+        nin(2);
+        n->i0 = parse_int(find_attr(attrs, "dim", op), op);
+        n->i1 = parse_int(find_attr(attrs, "batch_dims", op), op);
+        Tensor *a = ins[0], *ix = ins[1];
+        if (!dt_is_int(ix->dt))
+          invalid("torchIndexSelect: index must be an integer tensor");
+        if (n->i1 != 0)
+          fail(REW_MI355X_ERR_UNSUPPORTED,
+               "eager 'torchIndexSelect': batch_dims > 0 not supported");
+        if (n->i0 < 0 || n->i0 >= a->shape.rank)
+          invalid("eager torchIndexSelect: dim out of range");
+        std::vector<int64_t> od;
+        for (int i = 0; i < n->i0; ++i) od.push_back(a->shape.d[i]);
+        for (int i = 0; i < ix->shape.rank; ++i) od.push_back(ix->shape.d[i]);
+        for (int i = n->i0 + 1; i < a->shape.rank; ++i) od.push_back(a->shape.d[i]);
+        outs.push_back({a->dt, Shape(od)});
+        break;
+      }
+      default:
+        fail(REW_MI355X_ERR_UNSUPPORTED, "eager backend: unsupported op '" + op + "'");
+    }
+  } catch (...) {
+    delete n;
+    throw;
+  }
+
+  for (auto& o : outs)
+    if (o.second.numel() >= kMaxElems) {
+      delete n;
+      fail(REW_MI355X_ERR_UNSUPPORTED, "eager '" + op + "': result of " +
+                                           std::to_string(o.second.numel()) +
+                                           " elements exceeds the 2^31 limit");
+    }
+
+  std::vector<Tensor*> result;
+  for (size_t i = 0; i < outs.size(); ++i) {
+    Tensor* t = new_tensor(c, outs[i].first, outs[i].second);
+    t->prod = n;
+    t->prod_out = (int)i;
+    t->ext = 1;
+    n->out.push_back(t);
+    result.push_back(t);
+  }
+  for (auto* t : ins) t->uses++;
+  n->order = c->order_counter++;
+  c->pending.push_back(n);
+  c->stats.ops_recorded++;
+  if (c->mode == REW_MI355X_MODE_OP_BY_OP ||
+      (int)c->pending.size() >= c->flush_threshold)
+    flush(c);
+  return result;
+}
+
+}  // namespace rew

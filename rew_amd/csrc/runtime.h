@@ -1,0 +1,137 @@
+// Internal runtime structures of librew_mi355x: tensor records, the
+// deferred op graph, the per-device context and its caching allocator.
+#pragma once
+
+#include <map>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <unordered_set>
+#include <vector>
+
+#include "common.h"
+
+namespace rew {
+
+struct Ctx;
+struct Node;
+
+// A device allocation shared by every tensor that aliases it (a reshape of
+// a materialized tensor aliases its source).
+struct Storage {
+  Ctx* ctx = nullptr;
+  void* ptr = nullptr;
+  size_t bytes = 0;   // rounded block size
+  int refs = 0;
+};
+
+// The record behind an opaque rew_mi355x_buf handle.
+struct Tensor {
+  Ctx* ctx = nullptr;
+  int ext = 0;              // owner references held through the ABI
+  int uses = 0;             // references from pending graph nodes
+  int dt = kF32;
+  Shape shape;
+  Storage* st = nullptr;    // dense row-major data once materialized
+  Node* prod = nullptr;     // pending producer, nullptr once materialized
+  int prod_out = 0;         // which output of `prod`
+  bool has_host = false;    // small constant whose bytes are known on host
+  uint8_t host[16] = {0};
+  // planner scratch (valid during one flush)
+  int plan_uses = 0;        // remaining consumer launches in this flush
+  bool plan_mat = false;    // planner decided to materialize
+  bool plan_dead = false;
+
+  int64_t numel() const { return shape.numel(); }
+  int64_t nbytes() const { return numel() * dt_size(dt); }
+  void* data() const { return st ? st->ptr : nullptr; }
+};
+
+// Op kinds (the subset of rew's EagerOpKind this backend implements,
+// src/rew/eager.nim:718-764, plus backend extensions argmax/topK).
+enum Kind : int {
+  K_BINARY, K_UNARY, K_CONVERT, K_ISFINITE, K_BITCAST, K_RESHAPE,
+  K_TRANSPOSE, K_REVERSE, K_BROADCAST_TO, K_BROADCAST, K_SLICE, K_CONCAT,
+  K_IOTA, K_COMPARE, K_SELECT, K_CLAMP, K_REDUCE, K_DOT_GENERAL, K_DOT,
+  K_INDEX_SELECT, K_ARGMAX, K_TOPK, K_REDUCE_PRECISION, K_PAD,
+  // composite kernels created by the planner (never recorded directly)
+  K_COUNT
+};
+
+struct Node {
+  int kind = 0;
+  int sub = 0;              // op-specific selector (binary op, reduce op, ...)
+  std::string name;         // rew op name
+  std::vector<Tensor*> in;
+  std::vector<Tensor*> out;
+  // typed attributes
+  std::vector<int64_t> l0, l1, l2, l3;
+  int64_t i0 = 0, i1 = 0, i2 = 0;
+  int dt_attr = -1;
+  int cmp = 0;
+  // planner scratch
+  bool dead = false;
+  bool done = false;
+  int order = 0;
+};
+
+// Stream-ordered caching allocator.  All work of a context runs on one
+// stream, so a block freed after its last consumer was enqueued can be
+// handed to the next producer without synchronising.
+struct Allocator {
+  std::multimap<size_t, void*> free_blocks;
+  size_t cached = 0;   // bytes in free_blocks
+  size_t in_use = 0;   // bytes handed out
+  int ordinal = 0;
+  void* get(size_t bytes, size_t* rounded);
+  void put(void* p, size_t rounded);
+  void trim();
+  static size_t round(size_t bytes);
+};
+
+struct ProfEntry {
+  std::string name;
+  hipEvent_t start, stop;
+};
+
+struct Ctx {
+  int ordinal = 0;
+  hipStream_t stream = nullptr;
+  std::recursive_mutex mu;
+  Allocator alloc;
+  std::vector<Node*> pending;
+  int mode = REW_MI355X_MODE_DEFERRED;
+  int flush_threshold = 4096;
+  rew_mi355x_stats stats{};
+  // pinned staging ring for small host->device copies
+  uint8_t* ring = nullptr;
+  size_t ring_size = 0, ring_pos = 0;
+  // profiling
+  bool profiling = false;
+  std::vector<ProfEntry> prof;
+  std::vector<std::pair<std::string, std::pair<int64_t, double>>> prof_summary;
+  std::vector<hipEvent_t> event_pool;
+  int order_counter = 0;
+};
+
+// ---- runtime services (runtime.cpp) -----------------------------------------
+Tensor* new_tensor(Ctx* c, int dt, const Shape& s);
+void tensor_alloc(Tensor* t);                 // give t fresh storage
+void tensor_alias(Tensor* t, Tensor* src);    // share src's storage
+void tensor_drop_storage(Tensor* t);
+void maybe_destroy(Tensor* t);                // free when unreferenced
+bool tensor_is_live_handle(const Tensor* t);
+
+// Launch bracketing for profiling: call before/after each kernel launch.
+void prof_begin(Ctx* c, const char* name);
+void prof_end(Ctx* c);
+
+// ---- graph (ops.cpp / lower.cpp) ----------------------------------------------
+// Records op `name` (validating and deriving outputs exactly like
+// executeEagerOp); returns new tensors with one owner reference each.
+std::vector<Tensor*> record_op(Ctx* c, const std::string& name,
+                               const std::vector<Tensor*>& ins,
+                               const std::vector<std::pair<std::string, std::string>>& attrs);
+void flush(Ctx* c);
+
+}  // namespace rew

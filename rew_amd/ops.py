@@ -1,0 +1,322 @@
+"""Mirror of rew's eager ``{.rewOp.}`` procs used on the hot path.
+
+Each function validates like the reference op, then calls ``dispatchEager``
+with the same op name and the same stringly-typed attrs in the same wire
+format, so the native backend sees exactly what rew would send it:
+
+* ``joinInts`` lists "[a,b]" (src/rew/ops/linalg.nim:21-29, reduce.nim:87-92)
+* Nim seq reprs "@[a, b]" for reshape/transpose/slice/iota shapes
+  (src/rew/ops/shape.nim:41, 73; concat.nim:94-96; shape.nim:316-320)
+* dtype names "float32" for astype (unary.nim:125), "dtInt32" for iota
+"""
+from __future__ import annotations
+
+from typing import Sequence
+
+import numpy as np
+
+from .eager import (DType, Device, Tensor, TensorError, defaultDevice, dispatchEager,
+                    fromHost)
+
+
+def _join(xs: Sequence[int]) -> str:
+    return "[" + ",".join(str(int(x)) for x in xs) + "]"
+
+
+def _nimseq(xs: Sequence[int]) -> str:
+    return "@[" + ", ".join(str(int(x)) for x in xs) + "]"
+
+
+def _one(op, operands, attrs=()):
+    outs = dispatchEager(op, operands, attrs)
+    assert len(outs) == 1, f"{op}: eager backend returned wrong arity"
+    return outs[0]
+
+
+def _same(a: Tensor, b: Tensor, op: str):
+    # src/rew/ops/arith.nim:21-28
+    if a.device != b.device:
+        raise TensorError(f"{op}: device mismatch")
+    if a.dtype != b.dtype:
+        raise TensorError(f"{op}: dtype mismatch ({a.dtype.enum_name} vs {b.dtype.enum_name})")
+    if a.shape != b.shape:
+        raise TensorError(f"{op}: shape mismatch")
+
+
+# ---- literals (src/rew/ops/literal.nim:56-194) -------------------------------------
+
+def constant(dtype: DType, shape: Sequence[int], data, device: Device | None = None) -> Tensor:
+    return fromHost(np.asarray(data), dtype=dtype, shape=shape, device=device)
+
+
+def scalarF32(v: float, device: Device | None = None) -> Tensor:
+    return fromHost(np.array(v, dtype=np.float32), DType.FLOAT32, (), device)
+
+
+def scalarI32(v: int, device: Device | None = None) -> Tensor:
+    return fromHost(np.array(v, dtype=np.int32), DType.INT32, (), device)
+
+
+def constantF32(shape: Sequence[int], data, device: Device | None = None) -> Tensor:
+    a = np.asarray(data, dtype=np.float32)
+    n = int(np.prod(shape)) if len(shape) else 1
+    if a.size != n:
+        raise TensorError(f"constantF32: data length {a.size} does not match shape product {n}")
+    return fromHost(a, DType.FLOAT32, shape, device)
+
+
+# ---- elementwise (src/rew/ops/arith.nim, unary.nim) ---------------------------------
+
+def _binary(name):
+    def f(a: Tensor, b: Tensor) -> Tensor:
+        _same(a, b, name)
+        return _one(name, [a, b])
+    f.__name__ = name
+    return f
+
+
+add = _binary("add")
+sub = _binary("sub")
+mul = _binary("mul")
+divide = _binary("divide")
+maximum = _binary("maximum")
+minimum = _binary("minimum")
+power = _binary("power")
+remainder = _binary("remainder")
+atan2 = _binary("atan2")
+bitwiseAnd = _binary("bitwiseAnd")
+bitwiseOr = _binary("bitwiseOr")
+bitwiseXor = _binary("bitwiseXor")
+
+
+def _unary(name):
+    def f(a: Tensor) -> Tensor:
+        return _one(name, [a])
+    f.__name__ = name
+    return f
+
+
+neg = _unary("neg")
+abs_ = _unary("abs")
+exp = _unary("exp")
+log = _unary("log")
+sqrt = _unary("sqrt")
+rsqrt = _unary("rsqrt")
+tanh = _unary("tanh")
+logistic = _unary("logistic")
+sine = _unary("sine")
+cosine = _unary("cosine")
+floor = _unary("floor")
+ceil = _unary("ceil")
+sign = _unary("sign")
+isFinite = _unary("isFinite")
+
+
+def astype(a: Tensor, dtype: DType) -> Tensor:
+    return _one("astype", [a], [("dtype", DType(dtype).rew_name)])
+
+
+def clamp(lo: Tensor, x: Tensor, hi: Tensor) -> Tensor:
+    return _one("clamp", [lo, x, hi])
+
+
+# ---- shape ops (src/rew/ops/shape.nim, concat.nim, linalg.nim) ----------------------
+
+def reshape(a: Tensor, newShape: Sequence[int]) -> Tensor:
+    for d in newShape:
+        if d <= 0:
+            raise TensorError(f"reshape: shape contains non-positive dim {d}")
+    n = 1
+    for d in newShape:
+        n *= d
+    if n != a.numElements:
+        raise TensorError(
+            f"reshape: element count mismatch — operand has {a.numElements} elements, "
+            f"target shape has {n}")
+    return _one("reshape", [a], [("shape", _nimseq(newShape))])
+
+
+def transpose(a: Tensor, permutation: Sequence[int]) -> Tensor:
+    if len(permutation) != len(a.shape):
+        raise TensorError(
+            f"transpose: permutation length {len(permutation)} does not match operand rank "
+            f"{len(a.shape)}")
+    if sorted(permutation) != list(range(len(a.shape))):
+        raise TensorError("transpose: invalid permutation")
+    return _one("transpose", [a], [("permutation", _nimseq(permutation))])
+
+
+def broadcastTo(t: Tensor, outputShape: Sequence[int],
+                broadcastDimensions: Sequence[int]) -> Tensor:
+    if len(broadcastDimensions) != len(t.shape):
+        raise TensorError("broadcastTo: broadcastDimensions length must match operand rank")
+    for i, od in enumerate(broadcastDimensions):
+        if t.shape[i] != 1 and t.shape[i] != outputShape[od]:
+            raise TensorError("broadcastTo: operand dim is not 1 and does not match")
+    return _one("broadcastTo", [t], [("output_shape", _join(outputShape)),
+                                     ("broadcast_dimensions", _join(broadcastDimensions))])
+
+
+def slice_(t: Tensor, startIndices: Sequence[int], limitIndices: Sequence[int],
+           strides: Sequence[int] = ()) -> Tensor:
+    rank = len(t.shape)
+    if len(startIndices) != rank or len(limitIndices) != rank:
+        raise TensorError(f"slice: index arrays must match operand rank {rank}")
+    st = list(strides) if len(strides) else [1] * rank
+    for i in range(rank):
+        if (startIndices[i] < 0 or limitIndices[i] > t.shape[i]
+                or startIndices[i] >= limitIndices[i] or st[i] <= 0):
+            raise TensorError(f"slice: invalid bounds at dim {i}")
+    return _one("slice", [t], [("start_indices", _nimseq(startIndices)),
+                               ("limit_indices", _nimseq(limitIndices)),
+                               ("strides", _nimseq(st))])
+
+
+def concat(tensors: Sequence[Tensor], dimension: int) -> Tensor:
+    if not tensors:
+        raise TensorError("concat: empty input list")
+    return _one("concat", list(tensors), [("dimension", str(dimension))])
+
+
+def iota(dtype: DType, shape: Sequence[int], dimension: int,
+         device: Device | None = None) -> Tensor:
+    if dtype == DType.BOOL:
+        raise TensorError("iota: bool dtype is not supported")
+    if dimension < 0 or dimension >= len(shape):
+        raise TensorError(f"iota: dimension {dimension} out of range for rank {len(shape)}")
+    d = device or defaultDevice()
+    return _one("iota", [], [("dtype", DType(dtype).enum_name), ("shape", _nimseq(shape)),
+                             ("dimension", str(dimension)), ("device", str(d))])
+
+
+def unsqueeze(a: Tensor, dim: int) -> Tensor:
+    s = list(a.shape)
+    s.insert(dim, 1)
+    return reshape(a, s)
+
+
+def compare(lhs: Tensor, rhs: Tensor, direction: str) -> Tensor:
+    if direction not in ("LT", "LE", "GT", "GE", "EQ", "NE"):
+        raise TensorError(f"compare: invalid direction '{direction}'")
+    return _one("compare", [lhs, rhs], [("comparison_direction", direction)])
+
+
+def select(pred: Tensor, onTrue: Tensor, onFalse: Tensor) -> Tensor:
+    if pred.dtype != DType.BOOL:
+        raise TensorError(f"select: pred must be bool, got {pred.dtype.enum_name}")
+    return _one("select", [pred, onTrue, onFalse])
+
+
+# ---- reductions (src/rew/ops/reduce.nim:93-225) --------------------------------------
+
+def _norm_dims(op: str, rank: int, dims: Sequence[int]) -> list[int]:
+    out = []
+    for d in dims:
+        p = d + rank if d < 0 else d
+        if p < 0 or p >= rank:
+            raise TensorError(f"{op}: dim {d} out of range for rank {rank}")
+        if p in out:
+            raise TensorError(f"{op}: dim {d} repeated")
+        out.append(p)
+    return out
+
+
+def _reduction(op: str, t: Tensor, dims: Sequence[int]) -> Tensor:
+    rd = _norm_dims(op, len(t.shape), dims)
+    if t.dtype != DType.FLOAT32:
+        raise TensorError(f"{op}: v1 supports only float32 (got {t.dtype.enum_name})")
+    return _one(op, [t], [("dims", _join(rd))])
+
+
+def reduceSum(t: Tensor, dims: Sequence[int]) -> Tensor:
+    return _reduction("reduceSum", t, dims)
+
+
+def reduceMax(t: Tensor, dims: Sequence[int]) -> Tensor:
+    return _reduction("reduceMax", t, dims)
+
+
+def reduceMin(t: Tensor, dims: Sequence[int]) -> Tensor:
+    return _reduction("reduceMin", t, dims)
+
+
+def reduceProd(t: Tensor, dims: Sequence[int]) -> Tensor:
+    return _reduction("reduceProd", t, dims)
+
+
+def reduceMean(t: Tensor, dims: Sequence[int]) -> Tensor:
+    # src/rew/ops/reduce.nim:132-150: reduceSum then divide by broadcast n.
+    rd = _norm_dims("reduceMean", len(t.shape), dims)
+    summed = reduceSum(t, rd)
+    n = 1
+    for d in rd:
+        n *= t.shape[d]
+    if n <= 0:
+        raise TensorError(f"reduceMean: empty reduction (n = {n})")
+    divisor = scalarF32(float(n), t.device)
+    if len(summed.shape) == 0:
+        return divide(summed, divisor)
+    return divide(summed, broadcastTo(divisor, summed.shape, []))
+
+
+def argmax(t: Tensor, dim: int) -> Tensor:
+    """Index of the maximum along ``dim``; ties go to the smallest index.
+
+    rew's composite (src/rew/ops/reduce.nim:202-225) raises at its int32
+    ``reduceMin`` (fp32-only guard, reduce.nim:66-69); the backend runs the
+    documented semantics as one native op instead, including the
+    composite's NaN behaviour (a row containing NaN yields int32.high).
+    """
+    pos = dim + len(t.shape) if dim < 0 else dim
+    if pos < 0 or pos >= len(t.shape):
+        raise TensorError(f"argmax: dim {dim} out of range for rank {len(t.shape)}")
+    return _one("argmax", [t], [("dimension", str(pos))])
+
+
+def topK(operand: Tensor, k: int, dimension: int = -1, largest: bool = True):
+    """(values, indices) of the k largest along the last dim, largest first,
+    ties to the lower index (src/rew/ops/sort.nim:36-90 semantics; eager here,
+    trace-only in the reference)."""
+    if k <= 0:
+        raise TensorError(f"topK: k must be positive, got {k}")
+    rank = len(operand.shape)
+    d = dimension + rank if dimension < 0 else dimension
+    if k > operand.shape[d]:
+        raise TensorError(f"topK: k {k} > dim size {operand.shape[d]}")
+    outs = dispatchEager("topK", [operand], [("k", str(k)), ("dimension", str(d)),
+                                             ("largest", "true" if largest else "false")])
+    return outs[0], outs[1]
+
+
+# ---- linear algebra (src/rew/ops/linalg.nim:204-256, 432-461) -------------------------
+
+def dotGeneral(a: Tensor, b: Tensor, lhsBatching: Sequence[int], rhsBatching: Sequence[int],
+               lhsContracting: Sequence[int], rhsContracting: Sequence[int]) -> Tensor:
+    if a.dtype != b.dtype:
+        raise TensorError(
+            f"dotGeneral: dtype mismatch ({a.dtype.enum_name} vs {b.dtype.enum_name})")
+    return _one("dotGeneral", [a, b], [("lhs_batching", _join(lhsBatching)),
+                                       ("rhs_batching", _join(rhsBatching)),
+                                       ("lhs_contracting", _join(lhsContracting)),
+                                       ("rhs_contracting", _join(rhsContracting))])
+
+
+def matmul(a: Tensor, b: Tensor) -> Tensor:
+    if len(a.shape) != 2 or len(b.shape) != 2:
+        raise TensorError(
+            f"matmul: expected rank-2 operands, got shapes {list(a.shape)} and {list(b.shape)}")
+    if a.shape[1] != b.shape[0]:
+        raise TensorError(f"matmul: inner dim mismatch — {list(a.shape)} * {list(b.shape)}")
+    return dotGeneral(a, b, [], [], [1], [0])
+
+
+def dot(a: Tensor, b: Tensor) -> Tensor:
+    return _one("dot", [a, b])
+
+
+def torchIndexSelect(operand: Tensor, index: Tensor, dim: int, batchDims: int) -> Tensor:
+    if index.dtype not in (DType.INT8, DType.INT16, DType.INT32, DType.INT64, DType.UINT8,
+                           DType.UINT16, DType.UINT32, DType.UINT64):
+        raise TensorError("torchIndexSelect: index must be an integer tensor")
+    return _one("torchIndexSelect", [operand, index], [("dim", str(dim)),
+                                                        ("batch_dims", str(batchDims))])
