@@ -22,8 +22,12 @@
 #include "rew_oracle.h"
 
 #include <math.h>
+#include <omp.h>
 #include <stdlib.h>
 #include <string.h>
+
+/* Threads the OpenMP loops below use (the cpu_baseline's core count). */
+int orc_num_threads(void) { return omp_get_max_threads(); }
 
 /* ---- rng: src/rew/rng.nim:32-80, src/rew/nn/init.nim:14-51 ------------------ */
 

@@ -17,6 +17,8 @@ void orc_fold_in(uint32_t k0, uint32_t k1, uint64_t data, uint32_t out[2]);
 void orc_uniform_f32(uint32_t k0, uint32_t k1, int64_t n, float lo, float hi, float* out);
 void orc_normal_f32(uint32_t k0, uint32_t k1, int64_t n, float mean, float sd, float* out);
 
+int orc_num_threads(void);
+
 uint16_t orc_bf16(float f);
 float orc_bf16_f32(uint16_t h);
 void orc_f32_to_bf16(const float* x, int64_t n, uint16_t* out);

@@ -1088,7 +1088,13 @@ void Lower::emit_dot(Node* n) {
     // empty contraction: zeros
     REW_HIP(hipMemsetAsync(out->data(), 0, out->nbytes(), c->stream));
   } else {
-    prof_begin(c, gemm_variant(g));
+    if (c->profiling) {
+      // "<variant>[batch,M,N,K]": the shape fixes the algorithmic FLOPs
+      char nm[160];
+      std::snprintf(nm, sizeof nm, "%s[%lld,%lld,%lld,%lld]", gemm_variant(g),
+                    (long long)g.batch, (long long)g.M, (long long)g.N, (long long)g.K);
+      prof_begin(c, nm);
+    }
     launch_gemm(g, c->stream);
     prof_end(c);
     note_launch(c, false);

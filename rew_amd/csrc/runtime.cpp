@@ -164,7 +164,7 @@ static hipEvent_t take_event(Ctx* c) {
   return e;
 }
 
-void prof_begin(Ctx* c, const char* name) {
+void prof_begin(Ctx* c, const std::string& name) {
   if (!c->profiling) return;
   ProfEntry e;
   e.name = name;

@@ -123,7 +123,7 @@ void maybe_destroy(Tensor* t);                // free when unreferenced
 bool tensor_is_live_handle(const Tensor* t);
 
 // Launch bracketing for profiling: call before/after each kernel launch.
-void prof_begin(Ctx* c, const char* name);
+void prof_begin(Ctx* c, const std::string& name);
 void prof_end(Ctx* c);
 
 // ---- graph (ops.cpp / lower.cpp) ----------------------------------------------
