@@ -110,17 +110,32 @@ def profile_step(step):
     return out
 
 
-def gemm_flops(entry_name: str) -> int | None:
-    """2*b*M*N*K from a "<variant>[b,M,N,K]" profile name."""
+def visible_pairs(Sq: int, Sk: int, cmp: int) -> int:
+    """(query, key) pairs a mask predicate cmp(i, j) keeps; -1 = no mask."""
+    if cmp == -1:
+        return Sq * Sk
+    i = np.arange(Sq)[:, None]
+    j = np.arange(Sk)[None, :]
+    pred = {0: i == j, 1: i != j, 2: i < j, 3: i <= j, 4: i > j, 5: i >= j}[cmp]
+    return int(pred.sum())
+
+
+def entry_flops(entry_name: str) -> int | None:
+    """Algorithmic FLOPs of one launch from its profile name:
+    "<gemm variant>[b,M,N,K]" -> 2bMNK; "flash_attn[B,H,Hkv,Sq,Sk,D,cmp,skip]"
+    -> 4*B*H*D*(visible pairs) (QK^T and PV over the pairs the mask keeps)."""
     if "[" not in entry_name:
         return None
     dims = [int(v) for v in entry_name[entry_name.index("[") + 1:-1].split(",")]
+    if entry_name.startswith("flash_attn"):
+        B, H, _, Sq, Sk, D, cmp, _ = dims
+        return 4 * B * H * D * visible_pairs(Sq, Sk, cmp)
     b, m, n, k = dims
     return 2 * b * m * n * k
 
 
 def kernel_symbol(entry_name: str) -> str:
-    return entry_name.split("[")[0]
+    return entry_name.split("[")[0].split("{")[0]
 
 
 # ---- C4: Llama decoder layer prefill -------------------------------------------------------
@@ -231,13 +246,15 @@ def run_llama(args):
     # per-kernel breakdown of one extra step
     prof = profile_step(step)
     E.sync()
+    for name, n, ms in sorted(prof, key=lambda r: -r[2]):
+        print(f"#   {ms * 1e3:9.1f} us  x{n:<3d} {name}", file=sys.stderr)
     by_sym = {}
     for name, n, ms in prof:
         sym = kernel_symbol(name)
         d = by_sym.setdefault(sym, {"launches": 0, "ms": 0.0, "flops": 0, "flops_known": True})
         d["launches"] += n
         d["ms"] += ms
-        f = gemm_flops(name)
+        f = entry_flops(name)
         if f is None:
             d["flops_known"] = False
         else:

@@ -242,9 +242,11 @@ def rope_tables(head_dim: int, max_seq: int, theta: float):
     return np.repeat(c, 2, axis=1), np.repeat(s, 2, axis=1)
 
 
-def sdpa(q, k, v, causal: bool, scale: float | None = None, mixed: bool = False) -> np.ndarray:
+def sdpa(q, k, v, causal, scale: float | None = None, mixed: bool = False) -> np.ndarray:
     """src/rew/nn/attention.nim:36-81 with GQA sharing (groupedqueryattention.nim:126-133).
-    q [B,H,Sq,D], k/v [B,Hkv,Sk,D] as float arrays (bf16-valued when mixed)."""
+    q [B,H,Sq,D], k/v [B,Hkv,Sk,D] as float arrays (bf16-valued when mixed).
+    causal: False/0 unmasked, True/1 rew's makeCausalMask (i <= j visible),
+    2 the mirrored mask (i >= j visible)."""
     q = np.ascontiguousarray(q, np.float32)
     k = np.ascontiguousarray(k, np.float32)
     v = np.ascontiguousarray(v, np.float32)
@@ -253,7 +255,7 @@ def sdpa(q, k, v, causal: bool, scale: float | None = None, mixed: bool = False)
     sc = np.float32(1.0) / np.sqrt(np.float32(D)) if scale is None else np.float32(scale)
     out = np.empty_like(q)
     lib().orc_sdpa(_p(q), _p(k), _p(v), C.c_int64(B), C.c_int64(H), C.c_int64(Hkv),
-                   C.c_int64(Sq), C.c_int64(Sk), C.c_int64(D), C.c_int(1 if causal else 0),
+                   C.c_int64(Sq), C.c_int64(Sk), C.c_int64(D), C.c_int(int(causal)),
                    C.c_float(sc), C.c_int(1 if mixed else 0), _p(out))
     return out
 

@@ -386,8 +386,9 @@ void orc_rope(const float* x, const float* cos_t, const float* sin_t, int64_t ou
 
 /* scaledDotProductAttention with GQA head sharing: src/rew/nn/attention.nim:36-81,
  * groupedqueryattention.nim:126-133 (kv head = h / (H / Hkv)).
- * q [B,H,Sq,D], k/v [B,Hkv,Sk,D]; causal uses makeCausalMask's orientation
- * (attention.nim:18-34): score[i][j] gets -1e9 where i > j.
+ * q [B,H,Sq,D], k/v [B,Hkv,Sk,D]; causal = 1 uses makeCausalMask's orientation
+ * (attention.nim:18-34): score[i][j] gets -1e9 where i > j; causal = 2 is the
+ * mirrored mask (-1e9 where i < j); 0 is unmasked.
  * mixed = 1 emulates the bf16 op sequence: q/k/v are bf16-valued, scores
  * are rounded to bf16 before the fp32 scale/mask/softmax, probabilities are
  * rounded to bf16 before the PV product, the output is rounded to bf16. */
@@ -409,7 +410,8 @@ void orc_sdpa(const float* q, const float* k, const float* v, int64_t B, int64_t
           float sf = (float)s;
           if (mixed) sf = rbf(sf);
           sf = sf * scale;
-          if (causal) sf = sf + ((i <= j) ? 0.0f : -1e9f);
+          if (causal == 1) sf = sf + ((i <= j) ? 0.0f : -1e9f);
+          else if (causal == 2) sf = sf + ((i >= j) ? 0.0f : -1e9f);
           p[j] = sf;
         }
         float m = -INFINITY;

@@ -62,4 +62,29 @@ struct GatherArgs {
 };
 void launch_gather(const GatherArgs& g, hipStream_t stream);
 
+// ---- fused attention (k_attn.hip) ---------------------------------------------
+// out[b,h,i,:] = sum_j softmax_j(bf16(q[b,h,i,:].k[b,hk,j,:]) * scale + mask(i,j))
+//                * v[b,hk,j,:],  hk = h / (H / Hkv); bf16 operands, d contiguous.
+// mask(i, j) = cmp(i, j) ? mask_true : mask_false when `mask` is set.
+struct FlashArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  int B, H, Hkv, Sq, Sk, D;
+  int64_t q_sb, q_sh, q_ss;  // strides in elements (b, head, position)
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t o_sb, o_sh, o_ss;
+  float scale;
+  int round_scores;  // scores are rounded to bf16 before the fp32 scale / mask
+  int mask;          // additive two-valued mask present
+  int cmp;           // vm::Cmp direction of the predicate cmp(i, j)
+  float mask_true, mask_false;
+  int skip;          // key tiles masked everywhere may be skipped (exact)
+  int heavy_last;    // the last query tiles carry the most keys
+};
+bool flash_supported(const FlashArgs& a);
+void launch_flash(const FlashArgs& a, hipStream_t stream);
+
 }  // namespace rew

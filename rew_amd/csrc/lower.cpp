@@ -191,11 +191,28 @@ static bool compose_view(const Node* v, const Affine& m, Affine* out) {
 // lowering state
 // ---------------------------------------------------------------------------
 
+// A recognised SDPA chain (src/rew/nn/attention.nim:36-81): the PV
+// dot_general it ends in is lowered to one flash-attention launch.
+struct FlashPlan {
+  Tensor *q = nullptr, *k = nullptr, *v = nullptr;
+  float scale = 1.0f;
+  bool round_scores = true;
+  bool mask = false;
+  int cmp = 0;
+  float mask_true = 0.0f, mask_false = 0.0f;
+};
+
 struct Lower {
   Ctx* c;
   std::vector<Node*> nodes;  // live pending nodes in creation order
+  std::unordered_map<Node*, FlashPlan> flash;  // keyed by the PV dot_general
 
   explicit Lower(Ctx* ctx) : c(ctx) {}
+
+  bool match_flash(Node* pv);
+  bool emit_flash(Node* pv, const FlashPlan& fp);
+  bool kv_operand(Tensor* t, int H, const void** ptr, int64_t* sb, int64_t* sh,
+                  int64_t* ss, int* hkv);
 
   void ensure_mat(Tensor* t);
   void emit_ew_root(Tensor* t);
@@ -812,7 +829,9 @@ void Lower::emit_ew_root(Tensor* t) {
                        ((uintptr_t)t->data() % (dt_size(t->dt) * kVec)) == 0 &&
                        (t->dt == kF32 || t->dt == kI32 || t->dt == kU32 || t->dt == kBF16);
       set_leaf_modes(g.P, S, vec);
-      prof_begin(c, "ew_fused");
+      if (c->profiling)
+        prof_begin(c, "ew_fused{" + std::to_string(S.numel) + "x" + std::to_string(g.P.n_ins) +
+                          "," + dt_name(t->dt) + "}");
       launch_ew(g.P, S, vec, c->stream);
       prof_end(c);
       note_launch(c, g.P.n_ins > 2);
@@ -904,7 +923,9 @@ void Lower::emit_reduce(Node* n) {
       const bool vec = n_red > 0 && (dims.back() % kVec) == 0 &&
                        (n_red % kVec) == 0 && space.d[X.rank - 1] != 1;
       set_leaf_modes(g.P, S, vec);
-      prof_begin(c, "reduce");
+      if (c->profiling)
+        prof_begin(c, "reduce{" + std::to_string(n_out) + "x" + std::to_string(n_red) + "x" +
+                          std::to_string(g.P.n_ins) + "}");
       launch_reduce(g.P, S, A, vec, c->stream);
       prof_end(c);
       note_launch(c, g.P.n_ins > 1);
@@ -1004,6 +1025,13 @@ static bool merge_group(const Shape& s, const int64_t* st, const std::vector<int
 }
 
 void Lower::emit_dot(Node* n) {
+  auto fit = flash.find(n);
+  if (fit != flash.end()) {
+    FlashPlan fp = fit->second;
+    flash.erase(fit);
+    if (emit_flash(n, fp)) return;
+    // unsupported layout: the chain is rebuilt on demand by the generic path
+  }
   Tensor *a = n->in[0], *b = n->in[1], *out = n->out[0];
   const std::vector<int64_t> &lb = n->l0, &rb = n->l1, &lc = n->l2, &rc = n->l3;
   std::vector<int64_t> lf, rf;
@@ -1106,6 +1134,271 @@ void Lower::emit_dot(Node* n) {
       maybe_destroy(t);
 }
 
+
+// ---------------------------------------------------------------------------
+// fused attention: recognition of rew's SDPA op chain
+// ---------------------------------------------------------------------------
+
+// Pending (not materialized, not held by the caller) output of a node of
+// `kind`, consumed exactly `uses` times inside the graph.
+static Node* chain_node(Tensor* t, int kind, int uses) {
+  if (!t || t->st || !t->prod || t->ext != 0 || t->uses != uses) return nullptr;
+  return t->prod->kind == kind ? t->prod : nullptr;
+}
+
+static bool dims_are(const std::vector<int64_t>& v, std::initializer_list<int64_t> w) {
+  return v.size() == w.size() && std::equal(v.begin(), v.end(), w.begin());
+}
+
+// Value of broadcastTo(scalar f32 constant, shape, []) (src/rew/ops/literal.nim:56-77).
+static bool const_bcast(Tensor* t, float* val) {
+  if (!t || t->st || !t->prod || t->prod->kind != K_BROADCAST_TO) return false;
+  Tensor* s = t->prod->in[0];
+  if (s->shape.rank != 0 || s->dt != kF32 || !s->has_host) return false;
+  std::memcpy(val, s->host, 4);
+  return true;
+}
+
+// makeCausalMask (src/rew/nn/attention.nim:18-34):
+//   select(compare(iota(dim 0), iota(dim 1), dir), bcast(a), bcast(b))
+// broadcast over the two trailing dims of the scores.
+static bool match_mask(Tensor* maskB, int64_t Sq, int64_t Sk, FlashPlan* fp) {
+  if (!maskB || maskB->st || !maskB->prod || maskB->prod->kind != K_BROADCAST_TO) return false;
+  Node* bc = maskB->prod;
+  if (!dims_are(bc->l1, {2, 3})) return false;
+  Tensor* m = bc->in[0];
+  if (m->st || !m->prod || m->prod->kind != K_SELECT || m->dt != kF32) return false;
+  if (m->shape.rank != 2 || m->shape.d[0] != Sq || m->shape.d[1] != Sk) return false;
+  Node* sel = m->prod;
+  float vt, vf;
+  if (!const_bcast(sel->in[1], &vt) || !const_bcast(sel->in[2], &vf)) return false;
+  Tensor* pr = sel->in[0];
+  if (pr->st || !pr->prod || pr->prod->kind != K_COMPARE) return false;
+  Node* cm = pr->prod;
+  Tensor *x = cm->in[0], *y = cm->in[1];
+  auto iota_dim = [](Tensor* t) -> int {
+    if (t->st || !t->prod || t->prod->kind != K_IOTA || t->dt != kI32) return -1;
+    return (int)t->prod->i0;
+  };
+  const int dx = iota_dim(x), dy = iota_dim(y);
+  int dir = cm->cmp;
+  if (dx == 0 && dy == 1) {
+    // cmp(i, j)
+  } else if (dx == 1 && dy == 0) {
+    // cmp(j, i): flip the direction
+    static const int flip[] = {CMP_EQ, CMP_NE, CMP_GT, CMP_GE, CMP_LT, CMP_LE};
+    dir = flip[dir];
+  } else {
+    return false;
+  }
+  fp->mask = true;
+  fp->cmp = dir;
+  fp->mask_true = vt;
+  fp->mask_false = vf;
+  return true;
+}
+
+bool Lower::match_flash(Node* pv) {
+  if (pv->kind != K_DOT_GENERAL || pv->out[0]->dt != kBF16) return false;
+  Tensor *attnB = pv->in[0], *v = pv->in[1];
+  if (attnB->shape.rank != 4 || v->shape.rank != 4 || v->dt != kBF16) return false;
+  if (!dims_are(pv->l0, {0, 1}) || !dims_are(pv->l1, {0, 1}) || !dims_are(pv->l2, {3}) ||
+      !dims_are(pv->l3, {2}))
+    return false;
+  // attnB = astype(attn, bf16); attn = e / bcast(reduceSum(e, [3]))
+  Node* cv = chain_node(attnB, K_CONVERT, 1);
+  if (!cv || cv->in[0]->dt != kF32) return false;
+  Tensor* attn = cv->in[0];
+  Node* dv = chain_node(attn, K_BINARY, 1);
+  if (!dv || dv->sub != 3 /* divide */) return false;
+  Tensor *e = dv->in[0], *sumB = dv->in[1];
+  Node* sb = chain_node(sumB, K_BROADCAST_TO, 1);
+  if (!sb || !dims_are(sb->l1, {0, 1, 2})) return false;
+  Tensor* sumE = sb->in[0];
+  Node* rs = chain_node(sumE, K_REDUCE, 1);
+  if (!rs || rs->sub != RED_SUM || !dims_are(rs->l0, {3}) || rs->in[0] != e) return false;
+  // e = exp(s3 - bcast(reduceMax(s3, [3])))
+  Node* ex = chain_node(e, K_UNARY, 2);
+  if (!ex || ex->sub != 2 /* exp */) return false;
+  Tensor* shifted = ex->in[0];
+  Node* sub = chain_node(shifted, K_BINARY, 1);
+  if (!sub || sub->sub != 1 /* sub */) return false;
+  Tensor *s3 = sub->in[0], *maxB = sub->in[1];
+  Node* mb = chain_node(maxB, K_BROADCAST_TO, 1);
+  if (!mb || !dims_are(mb->l1, {0, 1, 2})) return false;
+  Tensor* maxV = mb->in[0];
+  Node* rm = chain_node(maxV, K_REDUCE, 1);
+  if (!rm || rm->sub != RED_MAX || !dims_are(rm->l0, {3}) || rm->in[0] != s3) return false;
+  if (!s3 || s3->st || !s3->prod || s3->ext != 0 || s3->uses != 2 || s3->dt != kF32)
+    return false;
+  const int64_t Sq = s3->shape.d[2], Sk = s3->shape.d[3];
+  FlashPlan fp;
+  std::vector<Tensor*> inner = {attnB, attn, sumB, sumE, e, shifted, maxB, maxV, s3};
+  // optional mask: s = s2 + maskB
+  Tensor* cur = s3;
+  int cur_uses = 2;
+  if (cur->prod->kind == K_BINARY && cur->prod->sub == 0 /* add */) {
+    Node* ad = cur->prod;
+    if (match_mask(ad->in[1], Sq, Sk, &fp)) cur = ad->in[0];
+    else if (match_mask(ad->in[0], Sq, Sk, &fp)) cur = ad->in[1];
+    else return false;
+    cur_uses = 1;
+    if (cur->st || !cur->prod || cur->ext != 0 || cur->uses != 1) return false;
+    inner.push_back(cur);
+  }
+  // optional scale: s2 = s32 * bcast(scale)
+  if (cur->prod->kind == K_BINARY && cur->prod->sub == 2 /* mul */) {
+    Node* mu = cur->prod;
+    float sc;
+    if (const_bcast(mu->in[1], &sc)) cur = mu->in[0];
+    else if (const_bcast(mu->in[0], &sc)) cur = mu->in[1];
+    else return false;
+    fp.scale = sc;
+    if (cur->st || !cur->prod || cur->ext != 0 || cur->uses != 1) return false;
+    inner.push_back(cur);
+  }
+  (void)cur_uses;
+  // s32 = astype(scores, f32); scores = dot_general(q, k) over d
+  Node* c32 = chain_node(cur, K_CONVERT, 1);
+  if (!c32 || c32->in[0]->dt != kBF16) return false;
+  Tensor* scores = c32->in[0];
+  Node* qk = chain_node(scores, K_DOT_GENERAL, 1);
+  if (!qk || !dims_are(qk->l0, {0, 1}) || !dims_are(qk->l1, {0, 1}) ||
+      !dims_are(qk->l2, {3}) || !dims_are(qk->l3, {3}))
+    return false;
+  Tensor *q = qk->in[0], *k = qk->in[1];
+  if (q->dt != kBF16 || k->dt != kBF16 || q->shape.rank != 4 || k->shape.rank != 4)
+    return false;
+  const int64_t D = q->shape.d[3];
+  if (D != 32 && D != 64 && D != 128) return false;
+  if (v->shape.d[2] != Sk || v->shape.d[3] != D) return false;
+  inner.push_back(scores);
+  fp.q = q;
+  fp.k = k;
+  fp.v = v;
+  for (Tensor* t : inner) t->plan_mat = false;
+  flash[pv] = fp;
+  return true;
+}
+
+// K / V operand of the fused attention: rew's GQA head expansion
+// (src/rew/nn/groupedqueryattention.nim:126-133)
+//   reshape(broadcastTo(reshape(x, [B,Hkv,1,S,D]), [B,Hkv,G,S,D]), [B,H,S,D])
+// is read as x with kv head h / G; any other operand is read through its
+// view strides with Hkv = H.
+bool Lower::kv_operand(Tensor* t, int H, const void** ptr, int64_t* sb, int64_t* sh,
+                       int64_t* ss, int* hkv) {
+  Tensor* x = t;
+  int nkv = H;
+  if (!t->st && t->prod && !t->plan_mat && t->prod->kind == K_RESHAPE) {
+    Tensor* u = t->prod->in[0];
+    if (u->shape.rank == 5 && !u->st && u->prod && !u->plan_mat &&
+        u->prod->kind == K_BROADCAST_TO && dims_are(u->prod->l1, {0, 1, 2, 3, 4})) {
+      Tensor* w = u->prod->in[0];
+      if (w->shape.rank == 5 && w->shape.d[2] == 1 && !w->st && w->prod && !w->plan_mat &&
+          w->prod->kind == K_RESHAPE) {
+        Tensor* y = w->prod->in[0];
+        if (y->shape.rank == 4 && y->shape.d[1] == u->shape.d[1] &&
+            u->shape.d[1] * u->shape.d[2] == H && y->shape.d[2] == t->shape.d[2] &&
+            y->shape.d[3] == t->shape.d[3]) {
+          x = y;
+          nkv = (int)y->shape.d[1];
+        }
+      }
+    }
+  }
+  Tensor* base;
+  int64_t off, st[kMaxRank];
+  operand_strides(x, &base, &off, st);
+  if (st[3] != 1) {
+    // not d-contiguous: dense copy
+    Tensor* cp = emit_permuted_copy(x, {0, 1, 2, 3});
+    base = cp;
+    off = 0;
+    dense_strides(cp->shape, st);
+  }
+  *ptr = (const char*)base->data() + off * dt_size(base->dt);
+  *sb = x->shape.d[0] == 1 ? 0 : st[0];
+  *sh = x->shape.d[1] == 1 ? 0 : st[1];
+  *ss = st[2];
+  *hkv = nkv;
+  return true;
+}
+
+bool Lower::emit_flash(Node* pv, const FlashPlan& fp) {
+  Tensor* out = pv->out[0];
+  FlashArgs a;
+  std::memset(&a, 0, sizeof(a));
+  const Shape& Q = fp.q->shape;
+  a.B = (int)Q.d[0];
+  a.H = (int)Q.d[1];
+  a.Sq = (int)Q.d[2];
+  a.D = (int)Q.d[3];
+  a.Sk = (int)fp.k->shape.d[2];
+  {
+    Tensor* base;
+    int64_t off, st[kMaxRank];
+    Tensor* q = fp.q;
+    operand_strides(q, &base, &off, st);
+    if (st[3] != 1) {
+      base = emit_permuted_copy(q, {0, 1, 2, 3});
+      off = 0;
+      dense_strides(base->shape, st);
+    }
+    a.q = (const char*)base->data() + off * dt_size(base->dt);
+    a.q_sb = Q.d[0] == 1 ? 0 : st[0];
+    a.q_sh = Q.d[1] == 1 ? 0 : st[1];
+    a.q_ss = st[2];
+  }
+  int hk_k, hk_v;
+  kv_operand(fp.k, a.H, &a.k, &a.k_sb, &a.k_sh, &a.k_ss, &hk_k);
+  kv_operand(fp.v, a.H, &a.v, &a.v_sb, &a.v_sh, &a.v_ss, &hk_v);
+  if (hk_k != hk_v) {
+    // mixed head mappings: read the expanded K and V directly
+    kv_operand(fp.k, -1, &a.k, &a.k_sb, &a.k_sh, &a.k_ss, &hk_k);
+    kv_operand(fp.v, -1, &a.v, &a.v_sb, &a.v_sh, &a.v_ss, &hk_v);
+    hk_k = hk_v = a.H;
+  }
+  a.Hkv = hk_k;
+  tensor_alloc(out);
+  a.o = out->data();
+  a.o_sb = (int64_t)a.H * a.Sq * a.D;
+  a.o_sh = (int64_t)a.Sq * a.D;
+  a.o_ss = a.D;
+  a.scale = fp.scale;
+  a.round_scores = fp.round_scores ? 1 : 0;
+  a.mask = fp.mask ? 1 : 0;
+  a.cmp = fp.cmp;
+  a.mask_true = fp.mask_true;
+  a.mask_false = fp.mask_false;
+  // Skipping key tiles that are masked everywhere is exact when the masked
+  // value underflows exp() against every visible score and every query row
+  // keeps at least one visible key.
+  bool rows_ok = false;
+  switch (a.cmp) {
+    case CMP_LE: rows_ok = a.Sq <= a.Sk; break;
+    case CMP_LT: rows_ok = a.Sq <= a.Sk - 1; break;
+    case CMP_GE: rows_ok = true; break;
+    default: rows_ok = false; break;
+  }
+  a.skip = (a.mask && rows_ok && a.mask_false - a.mask_true <= -1e8f) ? 1 : 0;
+  a.heavy_last = (a.mask && (a.cmp == CMP_GE || a.cmp == CMP_GT)) ? 1 : 0;
+  if (!flash_supported(a)) {
+    tensor_drop_storage(out);
+    return false;
+  }
+  if (c->profiling) {
+    char nm[160];
+    std::snprintf(nm, sizeof nm, "flash_attn[%d,%d,%d,%d,%d,%d,%d,%d]", a.B, a.H, a.Hkv, a.Sq,
+                  a.Sk, a.D, a.mask ? a.cmp : -1, a.skip);
+    prof_begin(c, nm);
+  }
+  launch_flash(a, c->stream);
+  prof_end(c);
+  note_launch(c, true);
+  return true;
+}
+
 void Lower::emit_gather(Node* n) {
   Tensor *src = n->in[0], *ix = n->in[1], *out = n->out[0];
   ensure_mat(src);
@@ -1206,6 +1499,12 @@ void flush(Ctx* c) {
       if (t->plan_mat) cost[t] = 0;
     }
   }
+
+  // 2b. fused attention: an SDPA chain is emitted as one launch at its PV
+  // product; its intermediates are never materialized
+  if (c->mode == REW_MI355X_MODE_DEFERRED && !c->no_fusion_patterns)
+    for (Node* n : L.nodes)
+      if (n->kind == K_DOT_GENERAL) L.match_flash(n);
 
   // 3. emission in creation order
   std::exception_ptr err;

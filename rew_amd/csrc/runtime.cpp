@@ -277,6 +277,8 @@ int rew_mi355x_init(int ordinal, rew_mi355x_ctx** out) {
       REW_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
       if (const char* s = std::getenv("REW_MI355X_EAGER_SYNC"))
         if (s[0] == '1') c->mode = REW_MI355X_MODE_OP_BY_OP;
+      if (const char* s = std::getenv("REW_MI355X_NO_PATTERNS"))
+        if (s[0] == '1') c->no_fusion_patterns = true;
       g_ctx[ordinal] = c;
     }
     *out = reinterpret_cast<rew_mi355x_ctx*>(g_ctx[ordinal]);

@@ -102,6 +102,7 @@ struct Ctx {
   std::vector<Node*> pending;
   int mode = REW_MI355X_MODE_DEFERRED;
   int flush_threshold = 4096;
+  bool no_fusion_patterns = false;  // REW_MI355X_NO_PATTERNS=1: per-op kernels only
   rew_mi355x_stats stats{};
   // pinned staging ring for small host->device copies
   uint8_t* ring = nullptr;

@@ -388,3 +388,26 @@ def deviceCount() -> int:
     n = C.c_int()
     _check(_lib.load().rew_mi355x_device_count(C.byref(n)))
     return n.value
+
+
+# ---- kernel timing hooks (rew_mi355x_profile_*) ----------------------------------------
+
+def profileBegin(d: Device | None = None) -> None:
+    """Starts bracketing every kernel launch with HIP events on the backend stream."""
+    _check(_lib.load().rew_mi355x_profile_begin(context(d)))
+
+
+def profileEnd(d: Device | None = None) -> list:
+    """Stops profiling; returns [(kernel name, launches, total device ms)]."""
+    lib = _lib.load()
+    ctx = context(d)
+    _check(lib.rew_mi355x_profile_end(ctx))
+    out = []
+    name = C.create_string_buffer(256)
+    n = C.c_int64()
+    ms = C.c_double()
+    i = 0
+    while lib.rew_mi355x_profile_entry(ctx, i, name, 256, C.byref(n), C.byref(ms)) == 0:
+        out.append((name.value.decode(), int(n.value), float(ms.value)))
+        i += 1
+    return out
