@@ -131,11 +131,12 @@ def entry_flops(entry_name: str) -> int | None:
         B, H, _, Sq, Sk, D, cmp, _ = dims
         return 4 * B * H * D * visible_pairs(Sq, Sk, cmp)
     b, m, n, k = dims
-    return 2 * b * m * n * k
+    # the SwiGLU kernel runs the gate and up projections over the same A
+    return (4 if "swiglu" in entry_name else 2) * b * m * n * k
 
 
 def kernel_symbol(entry_name: str) -> str:
-    return entry_name.split("[")[0].split("{")[0]
+    return entry_name.split("[")[0].split("{")[0].split("+")[0]
 
 
 # ---- C4: Llama decoder layer prefill -------------------------------------------------------

@@ -9,6 +9,8 @@
 //   Double-buffered: the next tile's global loads are in flight while the
 //   current tile feeds the MFMAs.
 // gemm_generic: any dtype / strides, 64x64x16 LDS tiles, fp32 accumulation.
+#include <cstdlib>
+
 #include "kernels.h"
 #include "vm_device.h"
 
@@ -16,6 +18,43 @@ namespace rew {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// ---- fused epilogues (see GemmArgs) -----------------------------------------
+
+__device__ __forceinline__ float epi_rnd(int dt, float v) {
+  return dt == REW_DT_BFLOAT16 ? vm::round_bf16(v) : v;
+}
+__device__ __forceinline__ float epi_ld(const void* p, int dt, int64_t i) {
+  return dt == REW_DT_BFLOAT16 ? vm::as_f((uint32_t)((const uint16_t*)p)[i] << 16)
+                               : ((const float*)p)[i];
+}
+__device__ __forceinline__ void epi_st(void* p, int dt, int64_t i, float v) {
+  if (dt == REW_DT_BFLOAT16) ((uint16_t*)p)[i] = vm::bf16_bits(v);
+  else ((float*)p)[i] = v;
+}
+// Value stored at C[b, m, n] for the single-GEMM epilogues.
+__device__ __forceinline__ float epi_value(const GemmArgs& g, int64_t b, int64_t m, int64_t n,
+                                           float acc) {
+  const int dt = g.c_dtype;
+  const float d = epi_rnd(dt, acc);
+  if (g.epi == EPI_NONE) return d;
+  const float y = epi_rnd(dt, d + epi_ld(g.bias, dt, n));
+  if (g.epi == EPI_BIAS) return y;
+  return epi_rnd(dt, epi_ld(g.res, dt, b * g.res_sb + m * g.res_sm + n) + y);
+}
+// GatedFeedForward's gate (src/rew/nn/gated_ffn.nim:46-67 with
+// activation.nim:28-38), op by op in fp32.
+__device__ __forceinline__ float epi_swiglu(const GemmArgs& g, int64_t n, float acc_g,
+                                            float acc_u) {
+  const int dt = g.c_dtype;
+  const float yg = epi_rnd(dt, epi_rnd(dt, acc_g) + epi_ld(g.bias, dt, n));
+  const float yu = epi_rnd(dt, epi_rnd(dt, acc_u) + epi_ld(g.bias2, dt, n));
+  const float e = expf(-yg);
+  const float den = 1.0f + e;
+  const float sig = 1.0f / den;
+  const float act = yg * sig;
+  return act * yu;
+}
 
 // ---------------------------------------------------------------------------
 // generic
@@ -74,7 +113,7 @@ __global__ void __launch_bounds__(256) gemm_generic_kernel(GemmArgs g) {
         int64_t n = n0 + tx * 4 + j;
         if (n >= g.N) continue;
         vm::store_scalar(g.c, g.c_dtype, b * g.c_sb + m * g.c_sm + n,
-                         vm::as_u(acc[i][j]));
+                         vm::as_u(epi_value(g, b, m, n, acc[i][j])));
       }
     }
   }
@@ -248,12 +287,318 @@ __global__ void __launch_bounds__(256) gemm_bf16_mfma_kernel(GemmArgs g) {
           const int64_t m = m0 + wm * 64 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
           if (m >= g.M) continue;
           const int64_t off = b * g.c_sb + m * g.c_sm + n;
+          const float v = epi_value(g, b, m, n, acc[i][j][e]);
           if (esz == 4)
-            ((float*)C)[off] = acc[i][j][e];
+            ((float*)C)[off] = v;
           else
-            ((uint16_t*)C)[off] = vm::bf16_bits(acc[i][j][e]);
+            ((uint16_t*)C)[off] = vm::bf16_bits(v);
         }
       }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// bf16 MFMA, large tiles: 256x256x64 per workgroup, 4 waves of 128x128
+// ---------------------------------------------------------------------------
+//
+// Each wave owns a 128x128 block of C as 4x4 v_mfma_f32_32x32x16_bf16 tiles
+// (256 fp32 accumulators per lane), so one 16-byte LDS fragment read feeds
+// four MFMAs.  Operands are read with buffer loads (one scalar resource per
+// operand, one VGPR offset per lane; rows past the tile's extent come back
+// as zeros from the hardware range check).  A (K-contiguous rows) is staged
+// as 16-byte chunks; B is staged K-contiguous per output column: when it is
+// N-contiguous in HBM (rew's [in, out] Linear weights) each thread loads an
+// 8(k) x 8(n) block (8 lanes = 8 k-blocks of one n-block: full 128-byte
+// lines) and transposes it in registers; those 8 lanes then write 8
+// different 16-byte chunks of LDS banks, so the 144-byte row pitch keeps both
+// the writes and the fragment reads conflict-free.  A of the next k-tile is
+// in flight during the first half of the MFMAs, B during the second half.
+// Tiles are ordered so each XCD (every 8th workgroup) walks a contiguous,
+// row-grouped range of C, keeping the A rows and B columns its 32 CUs share
+// resident in its L2.
+
+namespace mf2 {
+constexpr int BM = 256, BN = 256, BK = 64, LDK = BK + 8;
+constexpr int GROUP_M = 4;
+}  // namespace mf2
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  // dword3 0x00020000: raw 32-bit buffer on gfx9 (CDNA)
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  auto x = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  uint4 v;
+  __builtin_memcpy(&v, &x, 16);
+  return v;
+}
+
+__device__ __forceinline__ void tile_of(int64_t bid, int64_t tiles_m, int64_t tiles_n,
+                                        int64_t batch, int64_t* b, int64_t* tm, int64_t* tn) {
+  const int64_t per = tiles_m * tiles_n;
+  const int64_t total = per * batch;
+  int64_t t = bid;
+  if (total % 8 == 0) t = (bid % 8) * (total / 8) + bid / 8;  // XCD-contiguous ranges
+  *b = t / per;
+  t -= *b * per;
+  const int64_t group = mf2::GROUP_M * tiles_n;
+  const int64_t first_m = (t / group) * mf2::GROUP_M;
+  const int64_t gsize = min((int64_t)mf2::GROUP_M, tiles_m - first_m);
+  const int64_t r = t % group;
+  *tm = first_m + r % gsize;
+  *tn = r / gsize;
+}
+
+// DUAL (EPI_SWIGLU): the workgroup covers 128 output columns of two GEMMs
+// sharing A; wave column wn holds gate columns n0 + wn*64 + [0, 64) in its
+// accumulator columns j = 0, 1 and the same up-projection columns in
+// j = 2, 3, so the SwiGLU epilogue is lane-local.
+template <bool B_KC, bool DUAL>
+__global__ void __launch_bounds__(256, 1) gemm_bf16_256_kernel(GemmArgs g) {
+  using namespace mf2;
+  // operand double buffers; after the main loop the same memory holds the
+  // rounded C tile for the epilogue pass
+  constexpr int CP = 256 + 8;  // C tile row pitch (elements)
+  static_assert(BM * CP <= 2 * (BM + BN) * LDK, "C tile must fit the operand buffers");
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (BM + BN) * LDK];
+  uint16_t (*As)[BM * LDK] = reinterpret_cast<uint16_t (*)[BM * LDK]>(smem);
+  uint16_t (*Bs)[BN * LDK] = reinterpret_cast<uint16_t (*)[BN * LDK]>(smem + 2 * BM * LDK);
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  constexpr int TN = DUAL ? BN / 2 : BN;  // output columns per workgroup
+  const int64_t tiles_m = (g.M + BM - 1) / BM, tiles_n = (g.N + TN - 1) / TN;
+  int64_t b, tm, tn;
+  tile_of(blockIdx.x, tiles_m, tiles_n, g.batch, &b, &tm, &tn);
+  const int64_t m0 = tm * BM, n0 = tn * TN;
+  const int64_t m_rows = min((int64_t)BM, g.M - m0), n_rows = min((int64_t)BN, g.N - n0);
+  const int K = (int)g.K;
+
+  // A: rows m0 .. m0 + m_rows of the batch, K-contiguous
+  const uint16_t* Ab = (const uint16_t*)g.a + b * g.a_sb + m0 * g.a_sm;
+  const __amdgpu_buffer_rsrc_t ra =
+      make_rsrc(Ab, (uint32_t)(((m_rows - 1) * g.a_sm + K) * 2));
+  const uint32_t a_sm2 = (uint32_t)(g.a_sm * 2);
+  // B: K-contiguous rows n0.. (B_KC) or the whole [K, N] batch matrix
+  const uint16_t* Bb = B_KC ? (const uint16_t*)g.b + b * g.b_sb + n0 * g.b_sn
+                            : (const uint16_t*)g.b + b * g.b_sb;
+  const uint32_t b_bytes = B_KC ? (uint32_t)(((n_rows - 1) * g.b_sn + K) * 2)
+                                : (uint32_t)(((g.K - 1) * g.b_sk + g.N) * 2);
+  // DUAL: odd waves stage the up-projection weights (wave-uniform choice)
+  const uint16_t* Bsrc = (DUAL && (wave & 1)) ? (const uint16_t*)g.b2 + b * g.b_sb : Bb;
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(Bsrc, b_bytes);
+  const uint32_t b_s2 = (uint32_t)((B_KC ? g.b_sn : g.b_sk) * 2);
+
+  // per-lane parts of the staging addresses
+  const int row8 = tid >> 3, kc = tid & 7;             // A / B_KC: 16-byte chunk kc of row
+  const uint32_t a_voff = row8 * a_sm2 + kc * 16;
+  const int nb = tid >> 3, kb = tid & 7;               // !B_KC: 8x8 block (k-block kb, n-block nb)
+  // DUAL: virtual column block nb maps to column n0 + (nb >> 4) * 64 + (nb & 7) * 8
+  const int64_t bcol = DUAL ? n0 + (nb >> 4) * 64 + (nb & 7) * 8 : n0 + nb * 8;
+  const uint32_t bt_voff = B_KC ? row8 * b_s2 + kc * 16
+                                : (kb * 8) * b_s2 + (uint32_t)(bcol * 2);
+
+  uint4 rs[8];
+  // K-tail lanes are zeroed when the chunk is written to LDS, not at load
+  // time, so the loads stay in flight across the MFMAs.
+  bool kok_a = true;
+  auto load_a = [&](int k0) {
+    kok_a = k0 + kc * 8 < K;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      rs[i] = bload16(ra, a_voff, (uint32_t)(i * 32) * a_sm2 + (uint32_t)k0 * 2);
+  };
+  auto store_a = [&](int buf) {
+    uint16_t* as = As[buf] + row8 * LDK + kc * 8;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      *(uint4*)(as + i * 32 * LDK) = kok_a ? rs[i] : make_uint4(0, 0, 0, 0);
+  };
+  bool kok_b = true;
+  auto load_b = [&](int k0) {
+    if (B_KC) {
+      kok_b = k0 + kc * 8 < K;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        rs[i] = bload16(rb, bt_voff, (uint32_t)(i * 32) * b_s2 + (uint32_t)k0 * 2);
+    } else {
+      // rows k >= K fall past the resource's extent and read as zeros
+#pragma unroll
+      for (int r = 0; r < 8; ++r) rs[r] = bload16(rb, bt_voff, (uint32_t)(k0 + r) * b_s2);
+    }
+  };
+  auto store_b = [&](int buf) {
+    if (B_KC) {
+      uint16_t* bs = Bs[buf] + row8 * LDK + kc * 8;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        *(uint4*)(bs + i * 32 * LDK) = kok_b ? rs[i] : make_uint4(0, 0, 0, 0);
+    } else {
+      uint16_t* bs = Bs[buf] + (nb * 8) * LDK + kb * 8;
+#pragma unroll
+      for (int nn = 0; nn < 8; ++nn) {
+        const int w = nn >> 1;
+        uint32_t o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t x = (&rs[2 * j].x)[w], y = (&rs[2 * j + 1].x)[w];
+          o[j] = (nn & 1) ? ((x >> 16) | (y & 0xffff0000u)) : ((x & 0xffffu) | (y << 16));
+        }
+        *(uint4*)(bs + nn * LDK) = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+    }
+  };
+
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  const int frag_a = (wm * 128 + (lane & 31)) * LDK + (lane >> 5) * 8;
+  const int frag_b = (wn * 128 + (lane & 31)) * LDK + (lane >> 5) * 8;
+  // Fragments of substep s + 1 are read while the 16 MFMAs of substep s run.
+  bf16x8_t fa[2][4], fb[2][4];
+  auto read_frags = [&](const uint16_t* as, const uint16_t* bs, int s, int slot) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      fa[slot][i] = *(const bf16x8_t*)(as + frag_a + i * 32 * LDK + s * 16);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      fb[slot][j] = *(const bf16x8_t*)(bs + frag_b + j * 32 * LDK + s * 16);
+  };
+  auto mfmas = [&](int slot) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[slot][i], fb[slot][j],
+                                                            acc[i][j], 0, 0, 0);
+  };
+
+  // One scheduling region per k-substep: the 8 fragment reads of the next
+  // substep are interleaved one-for-one with the first 8 of the 16 MFMAs of
+  // this one, so LDS latency hides under the matrix pipe.
+  auto pin = [&]() {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+  };
+
+  const int nk = (K + BK - 1) / BK;
+  load_a(0);
+  store_a(0);
+  load_b(0);
+  store_b(0);
+  __syncthreads();
+  read_frags(As[0], Bs[0], 0, 0);
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < nk;
+    const uint16_t* as = As[cur];
+    const uint16_t* bs = Bs[cur];
+    if (more) load_a((kt + 1) * BK);
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(as, bs, 1, 1);
+    mfmas(0);
+    pin();
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(as, bs, 2, 0);
+    mfmas(1);
+    pin();
+    __builtin_amdgcn_sched_barrier(0);
+    if (more) {
+      store_a(cur ^ 1);
+      load_b((kt + 1) * BK);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(as, bs, 3, 1);
+    mfmas(0);
+    pin();
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(1);
+    if (more) store_b(cur ^ 1);
+    __syncthreads();
+    if (more) read_frags(As[cur ^ 1], Bs[cur ^ 1], 0, 0);
+  }
+
+  // Epilogue, phase 1: every lane writes bf16(acc) of its fragments into
+  // the C tile in LDS (the operand buffers are free after the last barrier).
+  uint16_t* Cs = smem;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int col = wn * 128 + j * 32 + (lane & 31);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = wm * 128 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+        Cs[row * CP + col] = vm::bf16_bits(acc[i][j][e]);
+      }
+    }
+  __syncthreads();
+  // Phase 2: row-major pass, 8 output columns (16 bytes) per thread and
+  // step, with the bias / residual / up-projection operands read coalesced.
+  const int OC = DUAL ? 128 : 256;           // output columns of the tile
+  const int CH = OC / 8;                     // 16-byte chunks per row
+  uint16_t* C = (uint16_t*)g.c + b * g.c_sb;
+  const uint16_t* bias = (const uint16_t*)g.bias;
+  const uint16_t* bias2 = (const uint16_t*)g.bias2;
+  const uint16_t* res = (const uint16_t*)g.res + b * g.res_sb;
+  for (int t = tid; t < BM * CH; t += 256) {
+    const int row = t / CH, ch = t - row * CH;
+    const int64_t m = m0 + row;
+    const int64_t n = n0 + ch * 8;
+    if (m >= g.M || n >= g.N) continue;
+    // local column of the value (gate column for DUAL)
+    const int lc = DUAL ? (ch >> 3) * 128 + (ch & 7) * 8 : ch * 8;
+    const uint4 dv = *(const uint4*)(Cs + row * CP + lc);
+    const uint16_t* dh = (const uint16_t*)&dv;
+    uint16_t out[8];
+    if (DUAL) {
+      const uint4 uv = *(const uint4*)(Cs + row * CP + lc + 64);
+      const uint4 bg = *(const uint4*)(bias + n);
+      const uint4 bu = *(const uint4*)(bias2 + n);
+      const uint16_t* uh = (const uint16_t*)&uv;
+      const uint16_t* bgh = (const uint16_t*)&bg;
+      const uint16_t* buh = (const uint16_t*)&bu;
+#pragma unroll
+      for (int x = 0; x < 8; ++x) {
+        const float yg = vm::round_bf16(vm::as_f((uint32_t)dh[x] << 16) +
+                                        vm::as_f((uint32_t)bgh[x] << 16));
+        const float yu = vm::round_bf16(vm::as_f((uint32_t)uh[x] << 16) +
+                                        vm::as_f((uint32_t)buh[x] << 16));
+        const float e = expf(-yg);
+        const float den = 1.0f + e;
+        const float sig = 1.0f / den;
+        const float act = yg * sig;
+        out[x] = vm::bf16_bits(act * yu);
+      }
+    } else if (g.epi == EPI_NONE) {
+#pragma unroll
+      for (int x = 0; x < 8; ++x) out[x] = dh[x];
+    } else {
+      const uint4 bv = *(const uint4*)(bias + n);
+      const uint16_t* bh = (const uint16_t*)&bv;
+      uint4 rv = make_uint4(0, 0, 0, 0);
+      if (g.epi == EPI_BIAS_RES) rv = *(const uint4*)(res + m * g.res_sm + n);
+      const uint16_t* rh = (const uint16_t*)&rv;
+#pragma unroll
+      for (int x = 0; x < 8; ++x) {
+        float y = vm::round_bf16(vm::as_f((uint32_t)dh[x] << 16) +
+                                 vm::as_f((uint32_t)bh[x] << 16));
+        if (g.epi == EPI_BIAS_RES) y = vm::round_bf16(vm::as_f((uint32_t)rh[x] << 16) + y);
+        out[x] = vm::bf16_bits(y);
+      }
+    }
+    *(uint4*)(C + m * g.c_sm + n) = *(const uint4*)out;
   }
 }
 
@@ -273,9 +618,56 @@ static bool mfma_ok(const GemmArgs& g, bool* a_kc, bool* b_kc) {
   return true;
 }
 
+// The 256x256 kernel needs K-contiguous A and enough tiles to fill the
+// 256 CUs at least once; smaller problems run the 128x128 kernel.
+// REW_MI355X_GEMM_TILE=256 / 128 forces a kernel (tests use it to cover
+// the large-tile kernel's tails at small sizes); unset picks by size.
+static int forced_tile() {
+  static const int v = [] {
+    const char* s = std::getenv("REW_MI355X_GEMM_TILE");
+    return s ? std::atoi(s) : 0;
+  }();
+  return v;
+}
+
+// The epilogue pass of the 256 kernels writes 16-byte chunks of bf16 rows.
+static bool epi256_ok(const GemmArgs& g) {
+  auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  if (g.c_dtype != REW_DT_BFLOAT16 || g.N % 8 || g.c_sm % 8 || g.c_sb % 8 || !al16(g.c))
+    return false;
+  if (g.epi != EPI_NONE && !al16(g.bias)) return false;
+  if (g.epi == EPI_SWIGLU && !al16(g.bias2)) return false;
+  if (g.epi == EPI_BIAS_RES && (!al16(g.res) || g.res_sm % 8 || g.res_sb % 8)) return false;
+  return true;
+}
+
+static bool use_256(const GemmArgs& g, bool akc) {
+  if (!akc || forced_tile() == 128 || !epi256_ok(g)) return false;
+  const int64_t tiles = ((g.M + 255) / 256) * ((g.N + 255) / 256) * g.batch;
+  if ((tiles < 256 && forced_tile() != 256) || tiles >= (1ll << 31)) return false;
+  // buffer offsets are 32-bit: every operand extent a tile addresses < 2 GiB
+  bool bkc = g.b_sk == 1;
+  const int64_t a_ext = (256 * g.a_sm + g.K) * 2;
+  const int64_t b_ext = bkc ? (256 * g.b_sn + g.K) * 2 : (g.K * g.b_sk + g.N) * 2;
+  return a_ext < (1ll << 31) && b_ext < (1ll << 31);
+}
+
+bool gemm_epilogue_ok(const GemmArgs& g) {
+  if (g.epi == EPI_NONE) return true;
+  if (g.c_dtype != REW_DT_BFLOAT16 && g.c_dtype != REW_DT_FLOAT32) return false;
+  if (g.epi != EPI_SWIGLU) return true;
+  bool akc, bkc;
+  if (!mfma_ok(g, &akc, &bkc) || !akc || bkc || !epi256_ok(g)) return false;
+  const int64_t a_ext = (256 * g.a_sm + g.K) * 2;
+  const int64_t b_ext = (g.K * g.b_sk + g.N) * 2;
+  return a_ext < (1ll << 31) && b_ext < (1ll << 31) && ((uintptr_t)g.b2 & 15) == 0;
+}
+
 const char* gemm_variant(const GemmArgs& g) {
   bool akc, bkc;
+  if (g.epi == EPI_SWIGLU) return "gemm_bf16_256_swiglu";
   if (!mfma_ok(g, &akc, &bkc)) return "gemm_generic";
+  if (use_256(g, akc)) return bkc ? "gemm_bf16_256_tn" : "gemm_bf16_256_nn";
   if (akc && bkc) return "gemm_bf16_mfma_tn";
   if (akc) return "gemm_bf16_mfma_nn";
   if (bkc) return "gemm_bf16_mfma_tt";
@@ -285,7 +677,20 @@ const char* gemm_variant(const GemmArgs& g) {
 void launch_gemm(const GemmArgs& g, hipStream_t stream) {
   if (g.M == 0 || g.N == 0 || g.batch == 0) return;
   bool akc, bkc;
-  if (mfma_ok(g, &akc, &bkc)) {
+  if (g.epi == EPI_SWIGLU) {
+    if (!gemm_epilogue_ok(g)) fail(REW_MI355X_ERR_INVALID, "internal: SwiGLU GEMM not launchable");
+    const int64_t tiles = ((g.M + 255) / 256) * ((g.N + 127) / 128) * g.batch;
+    hipLaunchKernelGGL((gemm_bf16_256_kernel<false, true>), dim3((unsigned)tiles), dim3(256), 0,
+                       stream, g);
+  } else if (mfma_ok(g, &akc, &bkc) && use_256(g, akc)) {
+    const int64_t tiles = ((g.M + 255) / 256) * ((g.N + 255) / 256) * g.batch;
+    if (bkc)
+      hipLaunchKernelGGL((gemm_bf16_256_kernel<true, false>), dim3((unsigned)tiles), dim3(256), 0,
+                         stream, g);
+    else
+      hipLaunchKernelGGL((gemm_bf16_256_kernel<false, false>), dim3((unsigned)tiles), dim3(256),
+                         0, stream, g);
+  } else if (mfma_ok(g, &akc, &bkc)) {
     const int64_t tiles = ((g.M + 127) / 128) * ((g.N + 127) / 128) * g.batch;
     const unsigned grid = (unsigned)(tiles < 1 << 20 ? tiles : 1 << 20);
     if (akc && bkc)

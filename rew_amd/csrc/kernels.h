@@ -42,8 +42,26 @@ struct GemmArgs {
   int64_t a_sb, a_sm, a_sk;
   int64_t b_sb, b_sk, b_sn;
   int64_t c_sb, c_sm;
+  // Fused epilogue (rew's Linear.forward bias add, the decoder's residual
+  // add, GatedFeedForward's SiLU gate), each rounded like the op sequence:
+  //   EPI_BIAS      c = rnd(rnd(acc) + bias[n])
+  //   EPI_BIAS_RES  c = rnd(res[b,m,n] + rnd(rnd(acc) + bias[n]))
+  //   EPI_SWIGLU    dual GEMM with B and b2: g = rnd(rnd(acc) + bias[n]),
+  //                 u = rnd(rnd(acc2) + bias2[n]),
+  //                 c = bf16(g * (1 / (1 + exp(-g))) * u)   (fp32 ops)
+  // rnd() rounds to c_dtype; bias / res / c share c_dtype.
+  int epi;
+  const void* bias;
+  const void* bias2;
+  const void* res;
+  int64_t res_sb, res_sm;
+  const void* b2;
 };
+enum GemmEpi : int { EPI_NONE = 0, EPI_BIAS = 1, EPI_BIAS_RES = 2, EPI_SWIGLU = 3 };
 void launch_gemm(const GemmArgs& g, hipStream_t stream);
+// Whether launch_gemm runs g with its epilogue (EPI_SWIGLU needs the large
+// dual kernel; the others run on every MFMA kernel).
+bool gemm_epilogue_ok(const GemmArgs& g);
 // Name of the kernel variant launch_gemm would pick (for profiles/tests).
 const char* gemm_variant(const GemmArgs& g);
 

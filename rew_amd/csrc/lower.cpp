@@ -202,14 +202,28 @@ struct FlashPlan {
   float mask_true = 0.0f, mask_false = 0.0f;
 };
 
+// A dot_general whose consumers fold into its epilogue (see GemmArgs::epi).
+struct GemmPlan {
+  Node* dot = nullptr;
+  Node* dot2 = nullptr;  // EPI_SWIGLU: the up projection
+  int epi = 0;
+  Tensor* bias = nullptr;
+  Tensor* bias2 = nullptr;
+  Tensor* res = nullptr;
+};
+
 struct Lower {
   Ctx* c;
   std::vector<Node*> nodes;  // live pending nodes in creation order
   std::unordered_map<Node*, FlashPlan> flash;  // keyed by the PV dot_general
+  std::unordered_map<Tensor*, std::vector<Node*>> cons;  // pending consumers
+  std::unordered_map<Tensor*, GemmPlan> gemm_out;  // fused GEMM result -> plan
 
   explicit Lower(Ctx* ctx) : c(ctx) {}
 
   bool match_flash(Node* pv);
+  void match_gemm_epilogues();
+  bool emit_gemm_fused(Tensor* t, const GemmPlan& p);
   bool emit_flash(Node* pv, const FlashPlan& fp);
   bool kv_operand(Tensor* t, int H, const void** ptr, int64_t* sb, int64_t* sh,
                   int64_t* ss, int* hkv);
@@ -219,6 +233,7 @@ struct Lower {
   void emit_anchor(Node* n);
   void emit_reduce(Node* n);
   void emit_dot(Node* n);
+  void dot_args(Node* n, GemmArgs& g, Tensor*& ta, Tensor*& tb);
   void emit_gather(Node* n);
   void emit_argmax(Node* n);
   void emit_topk(Node* n);
@@ -769,6 +784,13 @@ static void note_launch(Ctx* c, bool fused) {
 
 void Lower::ensure_mat(Tensor* t) {
   if (t->st) return;
+  auto git = gemm_out.find(t);
+  if (git != gemm_out.end()) {
+    GemmPlan gp = git->second;
+    gemm_out.erase(git);
+    if (emit_gemm_fused(t, gp)) return;
+    // not launchable fused: the expression is rebuilt around a plain GEMM
+  }
   Node* p = t->prod;
   if (!p) throw Error(REW_MI355X_ERR_INVALID, "internal: tensor has neither data nor producer");
   if (is_ew(p->kind) || is_view(p->kind)) {
@@ -1024,15 +1046,12 @@ static bool merge_group(const Shape& s, const int64_t* st, const std::vector<int
   return true;
 }
 
-void Lower::emit_dot(Node* n) {
-  auto fit = flash.find(n);
-  if (fit != flash.end()) {
-    FlashPlan fp = fit->second;
-    flash.erase(fit);
-    if (emit_flash(n, fp)) return;
-    // unsupported layout: the chain is rebuilt on demand by the generic path
-  }
+// GEMM operands of dot_general node `n`: batch / free / contracting groups
+// merged into strided [batch, M, K] x [batch, K, N] views (dense copies
+// where a group is not uniformly strided); ta / tb are the base tensors.
+void Lower::dot_args(Node* n, GemmArgs& g, Tensor*& ta_out, Tensor*& tb_out) {
   Tensor *a = n->in[0], *b = n->in[1], *out = n->out[0];
+  (void)out;
   const std::vector<int64_t> &lb = n->l0, &rb = n->l1, &lc = n->l2, &rc = n->l3;
   std::vector<int64_t> lf, rf;
   {
@@ -1045,7 +1064,6 @@ void Lower::emit_dot(Node* n) {
     for (auto d : rc) v[d] = true;
     for (int i = 0; i < b->shape.rank; ++i) if (!v[i]) rf.push_back(i);
   }
-  GemmArgs g;
   std::memset(&g, 0, sizeof(g));
   g.dtype = a->dt;
   g.c_dtype = out->dt;
@@ -1108,6 +1126,22 @@ void Lower::emit_dot(Node* n) {
       (!extent_ok(ta, g.a, g.batch, g.a_sb, g.M, g.a_sm, g.K, g.a_sk) ||
        !extent_ok(tb, g.b, g.batch, g.b_sb, g.K, g.b_sk, g.N, g.b_sn)))
     throw Error(REW_MI355X_ERR_INVALID, "internal: dot_general operand view out of bounds");
+  ta_out = ta;
+  tb_out = tb;
+}
+
+void Lower::emit_dot(Node* n) {
+  auto fit = flash.find(n);
+  if (fit != flash.end()) {
+    FlashPlan fp = fit->second;
+    flash.erase(fit);
+    if (emit_flash(n, fp)) return;
+    // unsupported layout: the chain is rebuilt on demand by the generic path
+  }
+  Tensor *a = n->in[0], *b = n->in[1], *out = n->out[0];
+  GemmArgs g;
+  Tensor *ta, *tb;
+  dot_args(n, g, ta, tb);
   tensor_alloc(out);
   g.c = out->data();
   g.c_sb = g.M * g.N;
@@ -1399,6 +1433,216 @@ bool Lower::emit_flash(Node* pv, const FlashPlan& fp) {
   return true;
 }
 
+
+// ---------------------------------------------------------------------------
+// GEMM epilogue fusion: rew's Linear bias add (src/rew/nn/linear.nim:43-49),
+// the decoder's residual adds (src/rew/models/llama.nim:106-117) and
+// GatedFeedForward's SiLU gate (src/rew/nn/gated_ffn.nim:46-67,
+// src/rew/nn/activation.nim:28-38) run inside the GEMM that feeds them.
+// ---------------------------------------------------------------------------
+
+static Node* sole_consumer(Lower& L, Tensor* t) {
+  if (!t || t->st || t->ext != 0 || t->uses != 1) return nullptr;
+  auto it = L.cons.find(t);
+  if (it == L.cons.end() || it->second.size() != 1) return nullptr;
+  return it->second[0];
+}
+
+// broadcastTo(bias[N], [M, N], [1]) of a same-dtype vector
+static bool bias_of(Tensor* t, const Shape& ys, Tensor** bias) {
+  if (!t || t->st || !t->prod || t->prod->kind != K_BROADCAST_TO) return false;
+  Node* bc = t->prod;
+  Tensor* v = bc->in[0];
+  if (t->shape != ys || ys.rank != 2 || !dims_are(bc->l1, {1})) return false;
+  if (v->shape.rank != 1 || v->shape.d[0] != ys.d[1] || v->dt != t->dt) return false;
+  *bias = v;
+  return true;
+}
+
+// y = add(D, bias) / add(bias, D) for the pending matmul output D
+static Node* bias_add(Lower& L, Tensor* D, Tensor** bias) {
+  Node* ad = sole_consumer(L, D);
+  if (!ad || ad->kind != K_BINARY || ad->sub != 0) return nullptr;
+  Tensor* other = ad->in[0] == D ? ad->in[1] : ad->in[0];
+  if (!bias_of(other, D->shape, bias)) return nullptr;
+  return ad;
+}
+
+static bool plain_matmul(Node* n) {
+  return n && n->kind == K_DOT_GENERAL && n->l0.empty() && n->l1.empty() &&
+         n->in[0]->shape.rank == 2 && n->in[1]->shape.rank == 2 && dims_are(n->l2, {1}) &&
+         dims_are(n->l3, {0}) && (n->out[0]->dt == kBF16 || n->out[0]->dt == kF32);
+}
+
+static bool is_one(Tensor* t) {
+  float v;
+  return const_bcast(t, &v) && v == 1.0f;
+}
+
+void Lower::match_gemm_epilogues() {
+  // 1. SwiGLU: hb = astype(mul(silu(astype(yg)), astype(yu)), bf16)
+  for (Node* cv : nodes) {
+    if (cv->kind != K_CONVERT || cv->out[0]->dt != kBF16 || cv->in[0]->dt != kF32) continue;
+    Tensor* hb = cv->out[0];
+    Node* mu = chain_node(cv->in[0], K_BINARY, 1);
+    if (!mu || mu->sub != 2) continue;
+    for (int ord = 0; ord < 2; ++ord) {
+      Tensor* act = mu->in[ord];
+      Tensor* u32 = mu->in[1 - ord];
+      Node* am = chain_node(act, K_BINARY, 1);
+      if (!am || am->sub != 2) continue;
+      Tensor *g32 = nullptr, *sig = nullptr;
+      for (int o2 = 0; o2 < 2 && !g32; ++o2) {
+        Node* dv = chain_node(am->in[1 - o2], K_BINARY, 1);
+        if (dv && dv->sub == 3 && is_one(dv->in[0])) {
+          g32 = am->in[o2];
+          sig = am->in[1 - o2];
+        }
+      }
+      if (!g32) continue;
+      Node* dv = sig->prod;
+      Tensor* den = dv->in[1];
+      Node* da = chain_node(den, K_BINARY, 1);
+      if (!da || da->sub != 0) continue;
+      Tensor* ex = is_one(da->in[0]) ? da->in[1] : (is_one(da->in[1]) ? da->in[0] : nullptr);
+      Node* en = chain_node(ex, K_UNARY, 1);
+      if (!en || en->sub != 2) continue;
+      Node* ng = chain_node(en->in[0], K_UNARY, 1);
+      if (!ng || ng->sub != 0 || ng->in[0] != g32) continue;
+      Node* gc = chain_node(g32, K_CONVERT, 2);
+      Node* uc = chain_node(u32, K_CONVERT, 1);
+      if (!gc || !uc || gc->in[0]->dt != kBF16 || uc->in[0]->dt != kBF16) continue;
+      Tensor *yg = gc->in[0], *yu = uc->in[0];
+      Node* ga = chain_node(yg, K_BINARY, 1);
+      Node* ua = chain_node(yu, K_BINARY, 1);
+      if (!ga || !ua || ga->sub != 0 || ua->sub != 0) continue;
+      auto split = [](Node* ad, Tensor** D, Tensor** bias) {
+        for (int o = 0; o < 2; ++o) {
+          Tensor* d = ad->in[o];
+          if (d->prod && !d->st && d->ext == 0 && d->uses == 1 && plain_matmul(d->prod) &&
+              bias_of(ad->in[1 - o], d->shape, bias)) {
+            *D = d;
+            return true;
+          }
+        }
+        return false;
+      };
+      Tensor *Dg, *Du, *bg, *bu;
+      if (!split(ga, &Dg, &bg) || !split(ua, &Du, &bu)) continue;
+      Node *ng_ = Dg->prod, *nu = Du->prod;
+      if (ng_->in[0] != nu->in[0] || ng_->in[1]->shape != nu->in[1]->shape ||
+          Dg->dt != kBF16 || !Dg->plan_mat || !Du->plan_mat)
+        continue;
+      GemmPlan gp;
+      gp.dot = ng_;
+      gp.dot2 = nu;
+      gp.epi = EPI_SWIGLU;
+      gp.bias = bg;
+      gp.bias2 = bu;
+      for (Tensor* t : {Dg, Du, yg, yu, g32, u32, ng->out[0], ex, den, sig, act, cv->in[0]})
+        t->plan_mat = false;
+      hb->plan_mat = true;
+      gemm_out[hb] = gp;
+      break;
+    }
+  }
+  // 2. bias (+ residual) epilogues of the remaining matmuls
+  for (Node* n : nodes) {
+    if (!plain_matmul(n)) continue;
+    Tensor* D = n->out[0];
+    if (!D->plan_mat || D->ext != 0) continue;  // claimed, or held by the caller
+    Tensor* bias;
+    Node* ad = bias_add(*this, D, &bias);
+    if (!ad) continue;
+    Tensor* y = ad->out[0];
+    GemmPlan gp;
+    gp.dot = n;
+    gp.epi = EPI_BIAS;
+    gp.bias = bias;
+    Tensor* out = y;
+    std::vector<Tensor*> inner = {D};
+    // residual: add(R, y), add(y, R), or through one reshape of y
+    Tensor* r = y;
+    Node* c1 = sole_consumer(*this, y);
+    if (c1 && c1->kind == K_RESHAPE && c1->out[0]->ext == 0) {
+      r = c1->out[0];
+      c1 = sole_consumer(*this, r);
+    }
+    if (c1 && c1->kind == K_BINARY && c1->sub == 0 && c1->in[0] != c1->in[1]) {
+      Tensor* R = c1->in[0] == r ? c1->in[1] : c1->in[0];
+      if (R->dt == D->dt && R->shape == r->shape && R->shape.numel() == D->numel()) {
+        gp.epi = EPI_BIAS_RES;
+        gp.res = R;
+        inner.push_back(y);
+        if (r != y) inner.push_back(r);
+        out = c1->out[0];
+      }
+    }
+    for (Tensor* t : inner) t->plan_mat = false;
+    out->plan_mat = true;
+    gemm_out[out] = gp;
+  }
+}
+
+bool Lower::emit_gemm_fused(Tensor* t, const GemmPlan& p) {
+  GemmArgs g;
+  Tensor *ta, *tb;
+  dot_args(p.dot, g, ta, tb);
+  if (g.batch != 1 || g.K == 0 || t->numel() != g.M * g.N || t->dt != g.c_dtype) return false;
+  auto vec = [&](Tensor* v) -> const void* {
+    ensure_mat(v);
+    return (v->shape.rank == 1 && v->numel() == g.N) ? v->data() : nullptr;
+  };
+  g.epi = p.epi;
+  g.bias = vec(p.bias);
+  if (!g.bias) return false;
+  if (p.epi == EPI_SWIGLU) {
+    GemmArgs g2;
+    Tensor *ta2, *tb2;
+    dot_args(p.dot2, g2, ta2, tb2);
+    if (g2.a != g.a || g2.a_sm != g.a_sm || g2.a_sk != g.a_sk || g2.K != g.K || g2.N != g.N ||
+        g2.b_sk != g.b_sk || g2.b_sn != g.b_sn)
+      return false;
+    g.b2 = g2.b;
+    g.bias2 = vec(p.bias2);
+    if (!g.bias2) return false;
+  }
+  if (p.epi == EPI_BIAS_RES) {
+    Tensor* base;
+    int64_t off, st[kMaxRank], ds[kMaxRank];
+    operand_strides(p.res, &base, &off, st);
+    dense_strides(p.res->shape, ds);
+    bool dense = true;
+    for (int i = 0; i < p.res->shape.rank; ++i)
+      if (p.res->shape.d[i] != 1 && st[i] != ds[i]) dense = false;
+    if (!dense) {
+      std::vector<int> id(p.res->shape.rank);
+      for (int i = 0; i < p.res->shape.rank; ++i) id[i] = i;
+      base = emit_permuted_copy(p.res, id);
+      off = 0;
+    }
+    g.res = (const char*)base->data() + off * dt_size(base->dt);
+    g.res_sm = g.N;
+    g.res_sb = 0;
+  }
+  if (!gemm_epilogue_ok(g)) return false;
+  tensor_alloc(t);
+  g.c = t->data();
+  g.c_sb = g.M * g.N;
+  g.c_sm = g.N;
+  if (c->profiling) {
+    char nm[160];
+    std::snprintf(nm, sizeof nm, "%s%s[%lld,%lld,%lld,%lld]", gemm_variant(g),
+                  p.epi == EPI_BIAS ? "+bias" : (p.epi == EPI_BIAS_RES ? "+bias+res" : ""),
+                  (long long)g.batch, (long long)g.M, (long long)g.N, (long long)g.K);
+    prof_begin(c, nm);
+  }
+  launch_gemm(g, c->stream);
+  prof_end(c);
+  note_launch(c, true);
+  return true;
+}
+
 void Lower::emit_gather(Node* n) {
   Tensor *src = n->in[0], *ix = n->in[1], *out = n->out[0];
   ensure_mat(src);
@@ -1502,9 +1746,12 @@ void flush(Ctx* c) {
 
   // 2b. fused attention: an SDPA chain is emitted as one launch at its PV
   // product; its intermediates are never materialized
-  if (c->mode == REW_MI355X_MODE_DEFERRED && !c->no_fusion_patterns)
+  if (c->mode == REW_MI355X_MODE_DEFERRED && !c->no_fusion_patterns) {
     for (Node* n : L.nodes)
       if (n->kind == K_DOT_GENERAL) L.match_flash(n);
+    L.cons = consumers;
+    L.match_gemm_epilogues();
+  }
 
   // 3. emission in creation order
   std::exception_ptr err;

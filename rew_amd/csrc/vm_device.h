@@ -136,9 +136,13 @@ __device__ __forceinline__ void store_vec(void* p, int dt, int64_t i,
 
 // ---- register file: static indexing only, selected by a uniform switch ----
 
+// Sixteen separately named register vectors: a switch over named members
+// keeps every access static, so the file lives in VGPRs (an indexed array
+// would be lowered to scratch memory).
 template <int V>
 struct Regs {
-  uint32_t r[kMaxRegs][V];
+  uint32_t r0[V], r1[V], r2[V], r3[V], r4[V], r5[V], r6[V], r7[V];
+  uint32_t r8[V], r9[V], r10[V], r11[V], r12[V], r13[V], r14[V], r15[V];
 };
 
 #define REW_VM_CASES(X) \
@@ -147,7 +151,7 @@ struct Regs {
 template <int V>
 __device__ __forceinline__ void rget(const Regs<V>& R, int i, uint32_t (&o)[V]) {
   switch (i) {
-#define REW_G(k) case k: _Pragma("unroll") for (int j = 0; j < V; ++j) o[j] = R.r[k][j]; break;
+#define REW_G(k) case k: _Pragma("unroll") for (int j = 0; j < V; ++j) o[j] = R.r##k[j]; break;
     REW_VM_CASES(REW_G)
 #undef REW_G
     default: break;
@@ -157,7 +161,7 @@ __device__ __forceinline__ void rget(const Regs<V>& R, int i, uint32_t (&o)[V]) 
 template <int V>
 __device__ __forceinline__ void rset(Regs<V>& R, int i, const uint32_t (&v)[V]) {
   switch (i) {
-#define REW_S(k) case k: _Pragma("unroll") for (int j = 0; j < V; ++j) R.r[k][j] = v[j]; break;
+#define REW_S(k) case k: _Pragma("unroll") for (int j = 0; j < V; ++j) R.r##k[j] = v[j]; break;
     REW_VM_CASES(REW_S)
 #undef REW_S
     default: break;

@@ -1,0 +1,128 @@
+"""GPU parity of the GEMM epilogue fusions.
+
+rew's Linear.forward bias add (src/rew/nn/linear.nim:43-49), the decoder's
+residual add (src/rew/models/llama.nim:106-117) and GatedFeedForward's SiLU
+gate (src/rew/nn/gated_ffn.nim:46-67, activation.nim:28-38) are recognised in
+the deferred graph and run inside the GEMM.  The fused epilogue repeats the
+op sequence's roundings, so it is compared BIT-EXACTLY with the unfused GPU
+path (op-by-op mode: the same GEMM kernels, then the elementwise ops), and
+with the oracle within the bf16 tolerance (normwise 2e-2).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+from rew_amd import eager as E
+from rew_amd import nn
+from rew_amd import ops as O
+from rew_amd.eager import DType
+
+
+def bf16_close(got, want, tol=2e-2):
+    err = np.linalg.norm((got - want).ravel()) / max(np.linalg.norm(want.ravel()), 1e-30)
+    assert err <= tol, f"normwise relative error {err:.3e} > {tol}"
+
+
+def _run(fn, op_by_op=False):
+    if op_by_op:
+        E.setMode(E.MODE_OP_BY_OP)
+    try:
+        E.profileBegin()
+        out = E.toHost(fn())
+        names = [n for n, _, _ in E.profileEnd()]
+    finally:
+        E.setMode(E.MODE_DEFERRED)
+    return out, names
+
+
+def _lin(oracle, key, fi, fo, bias_sd=0.5):
+    w = oracle.round_bf16(oracle.normal_f32(oracle.fold_in(key, 0), fi * fo, 0.0, 0.05)
+                          .reshape(fi, fo))
+    b = oracle.round_bf16(oracle.normal_f32(oracle.fold_in(key, 1), fo, 0.0, bias_sd))
+    return w, b
+
+
+def _bits_f32(u16):
+    return E.bf16_bits_to_f32(u16)
+
+
+@pytest.mark.parametrize("T,fi,fo", [(300, 256, 520), (1024, 512, 1024), (64, 128, 72)])
+def test_linear_bias_epilogue(gpu, oracle, T, fi, fo):
+    key = oracle.init_key(100 + T)
+    w, b = _lin(oracle, key, fi, fo)
+    x = oracle.round_bf16(oracle.normal_f32(oracle.fold_in(key, 2), T * fi).reshape(T, fi))
+
+    def fn():
+        lin = nn.Linear(E.fromHost(w, DType.BFLOAT16), E.fromHost(b, DType.BFLOAT16))
+        return lin.forward(E.fromHost(x, DType.BFLOAT16))
+
+    got, names = _run(fn)
+    assert any("+bias" in n for n in names), names
+    ref, names2 = _run(fn, op_by_op=True)
+    assert not any("+bias" in n for n in names2)
+    np.testing.assert_array_equal(got, ref)
+    want = oracle.linear(x, w, b, True)
+    bf16_close(_bits_f32(got), want)
+
+
+@pytest.mark.parametrize("B,S,H", [(2, 160, 256), (1, 512, 512)])
+def test_residual_epilogue(gpu, oracle, B, S, H):
+    key = oracle.init_key(200 + S)
+    w, b = _lin(oracle, key, H, H)
+    x = oracle.round_bf16(oracle.normal_f32(oracle.fold_in(key, 2), B * S * H).reshape(B, S, H))
+    r = oracle.round_bf16(oracle.normal_f32(oracle.fold_in(key, 3), B * S * H).reshape(B, S, H))
+
+    def fn():
+        lin = nn.Linear(E.fromHost(w, DType.BFLOAT16), E.fromHost(b, DType.BFLOAT16))
+        y = lin.forward(O.reshape(E.fromHost(x, DType.BFLOAT16), [B * S, H]))
+        return O.add(E.fromHost(r, DType.BFLOAT16), O.reshape(y, [B, S, H]))
+
+    got, names = _run(fn)
+    assert any("+bias+res" in n for n in names), names
+    ref, _ = _run(fn, op_by_op=True)
+    np.testing.assert_array_equal(got, ref)
+    want = oracle.round_bf16(r + oracle.linear(x.reshape(B * S, H), w, b, True).reshape(B, S, H))
+    bf16_close(_bits_f32(got), want)
+
+
+@pytest.mark.parametrize("T,E_,I", [(256, 256, 512), (300, 128, 264), (1024, 512, 1408)])
+def test_swiglu_dual_gemm(gpu, oracle, T, E_, I):
+    key = oracle.init_key(300 + I)
+    wg, bg = _lin(oracle, oracle.fold_in(key, 0), E_, I, 0.3)
+    wu, bu = _lin(oracle, oracle.fold_in(key, 1), E_, I, 0.3)
+    wd, bd = _lin(oracle, oracle.fold_in(key, 2), I, E_, 0.3)
+    x = oracle.round_bf16(oracle.normal_f32(oracle.fold_in(key, 3), T * E_).reshape(1, T, E_))
+
+    def fn():
+        mk = lambda w, b: nn.Linear(E.fromHost(w, DType.BFLOAT16), E.fromHost(b, DType.BFLOAT16))
+        ffn = nn.GatedFeedForward(mk(wg, bg), mk(wu, bu), mk(wd, bd))
+        return ffn.forward(E.fromHost(x, DType.BFLOAT16))
+
+    got, names = _run(fn)
+    assert any("swiglu" in n for n in names), names
+    ref, names2 = _run(fn, op_by_op=True)
+    assert not any("swiglu" in n for n in names2)
+    np.testing.assert_array_equal(got, ref)
+    want = oracle.gated_ffn(x.reshape(T, E_), wg, bg, wu, bu, wd, bd, True).reshape(1, T, E_)
+    bf16_close(_bits_f32(got), want)
+
+
+def test_held_intermediate_blocks_fusion(gpu, oracle):
+    """A matmul result the caller still holds is materialized as is, and the
+    bias add then runs on it: same values as the fused path."""
+    T, fi, fo = 256, 256, 256
+    key = oracle.init_key(400)
+    w, b = _lin(oracle, key, fi, fo)
+    x = oracle.round_bf16(oracle.normal_f32(oracle.fold_in(key, 2), T * fi).reshape(T, fi))
+    xt, wt, bt = (E.fromHost(x, DType.BFLOAT16), E.fromHost(w, DType.BFLOAT16),
+                  E.fromHost(b, DType.BFLOAT16))
+    E.profileBegin()
+    xw = O.matmul(xt, wt)
+    y = O.add(xw, O.broadcastTo(bt, xw.shape, [1]))
+    got = E.toHost(y)
+    names = [n for n, _, _ in E.profileEnd()]
+    assert not any("+bias" in n for n in names), names
+    fused = E.toHost(nn.Linear(wt, bt).forward(xt))
+    np.testing.assert_array_equal(got, fused)
+    bf16_close(_bits_f32(E.toHost(xw)), oracle.gemm(x, w, True))
