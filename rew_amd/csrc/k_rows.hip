@@ -1,0 +1,133 @@
+// Row-wise composites of rew's nn layers as single HBM passes.
+//
+// rmsnorm_rows: rew's rmsNorm (src/rew/nn/norm.nim:204-224) over the last
+//   axis, op by op in fp32:
+//     s = sum_j x_j * x_j;  r = sqrt(s / n + eps);  y_j = gamma_j * (x_j / r)
+//   One workgroup per row; the row is read once into registers (up to
+//   kRowRegs elements per thread, re-read from L2 beyond that), reduced with
+//   a wave64 butterfly and an LDS step across the 4 waves.  The input may be
+//   bf16 (the astype to fp32 in front of the norm happens on load) and the
+//   output bf16 (the astype behind it happens on store).
+//
+// rope_pairs: rew's applyRotate (src/rew/nn/rope.nim:56-108) on adjacent
+//   pairs (2i, 2i+1) of the last axis:
+//     y_2i   = c_i * x_2i - s_i * x_2i+1
+//     y_2i+1 = s_i * x_2i + c_i * x_2i+1
+//   with c / s read through their broadcast views of the fp32 tables, each
+//   product and sum rounded to fp32 as the separate eager ops are.  Four
+//   pairs (16 bytes of bf16) per thread.
+#include "kernels.h"
+#include "vm_device.h"
+
+namespace rew {
+
+using namespace vm;
+
+__device__ __forceinline__ int dt_bytes(int dt) { return dt == REW_DT_BFLOAT16 ? 2 : 4; }
+
+__device__ __forceinline__ float ld_f(const void* p, int dt, int64_t i) {
+  return dt == REW_DT_BFLOAT16 ? as_f((uint32_t)((const uint16_t*)p)[i] << 16)
+                               : ((const float*)p)[i];
+}
+__device__ __forceinline__ void st_f(void* p, int dt, int64_t i, float v) {
+  if (dt == REW_DT_BFLOAT16) ((uint16_t*)p)[i] = bf16_bits(v);
+  else ((float*)p)[i] = v;
+}
+
+constexpr int kRowRegs = 32;  // elements per thread kept in registers
+
+__global__ void __launch_bounds__(256) rmsnorm_rows_kernel(RowNormArgs a) {
+  __shared__ float part[4];
+  const int tid = threadIdx.x;
+  for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x) {
+    const char* x = (const char*)a.x + row * a.x_rs * dt_bytes(a.x_dt);
+    float v[kRowRegs];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kRowRegs; ++k) {
+      const int64_t j = tid + (int64_t)k * 256;
+      v[k] = j < a.n ? ld_f(x, a.x_dt, j) : 0.0f;
+      const float sq = v[k] * v[k];
+      ss += sq;
+    }
+    for (int64_t j = tid + (int64_t)kRowRegs * 256; j < a.n; j += 256) {
+      const float xv = ld_f(x, a.x_dt, j);
+      const float sq = xv * xv;
+      ss += sq;
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+    if ((tid & 63) == 0) part[tid >> 6] = ss;
+    __syncthreads();
+    const float sum = (part[0] + part[1]) + (part[2] + part[3]);
+    __syncthreads();
+    const float mean = sum / a.divisor;
+    const float r = sqrtf(mean + a.eps);
+    char* y = (char*)a.y + row * a.n * dt_bytes(a.y_dt);
+#pragma unroll
+    for (int k = 0; k < kRowRegs; ++k) {
+      const int64_t j = tid + (int64_t)k * 256;
+      if (j < a.n) {
+        const float nv = v[k] / r;
+        st_f(y, a.y_dt, j, a.gamma[j] * nv);
+      }
+    }
+    for (int64_t j = tid + (int64_t)kRowRegs * 256; j < a.n; j += 256) {
+      const float nv = ld_f(x, a.x_dt, j) / r;
+      st_f(y, a.y_dt, j, a.gamma[j] * nv);
+    }
+  }
+}
+
+void launch_rmsnorm_rows(const RowNormArgs& a, hipStream_t stream) {
+  if (a.rows == 0 || a.n == 0) return;
+  const unsigned grid = (unsigned)(a.rows < 65536 ? a.rows : 65536);
+  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(grid), dim3(256), 0, stream, a);
+  REW_HIP(hipGetLastError());
+}
+
+// ---- RoPE ------------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(256) rope_pairs_kernel(RopeArgs a) {
+  // pairs are processed in groups of 4 consecutive i (half % 4 == 0)
+  const uint32_t g4 = (uint32_t)(a.half / 4);
+  const uint32_t total = (uint32_t)(a.d0 * a.d1 * a.S) * g4;
+  FastDiv fg = a.fd_g4, fs = a.fd_s, f1 = a.fd_d1;
+  for (uint32_t t = blockIdx.x * 256 + threadIdx.x; t < total; t += gridDim.x * 256) {
+    uint32_t q = fdiv(t, fg);
+    const uint32_t i0 = (t - q * g4) * 4;
+    uint32_t q2 = fdiv(q, fs);
+    const uint32_t s = q - q2 * (uint32_t)a.S;
+    const uint32_t i1 = q2 - fdiv(q2, f1) * (uint32_t)a.d1;
+    const uint32_t i0d = fdiv(q2, f1);
+    const int64_t xb = i0d * a.x_s0 + i1 * a.x_s1 + s * a.x_ss;
+    const int64_t cb = i0d * a.c_s0 + i1 * a.c_s1 + s * a.c_ss;
+    const int64_t sb = i0d * a.s_s0 + i1 * a.s_s1 + s * a.s_ss;
+    const int64_t yb = ((int64_t)q2 * a.S + s) * (2 * a.half) + 2 * i0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t i = i0 + u;
+      const float x0 = ld_f(a.x, a.x_dt, xb + (2 * i) * a.x_sd);
+      const float x1 = ld_f(a.x, a.x_dt, xb + (2 * i + 1) * a.x_sd);
+      const float c = a.cos[cb + i * a.c_si];
+      const float sn = a.sin[sb + i * a.s_si];
+      const float t1 = c * x0;
+      const float t2 = sn * x1;
+      const float t3 = sn * x0;
+      const float t4 = c * x1;
+      st_f(a.y, a.y_dt, yb + 2 * u, t1 - t2);
+      st_f(a.y, a.y_dt, yb + 2 * u + 1, t3 + t4);
+    }
+  }
+}
+
+void launch_rope(const RopeArgs& a, hipStream_t stream) {
+  const int64_t total = a.d0 * a.d1 * a.S * (a.half / 4);
+  if (total == 0) return;
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 256 * 32) blocks = 256 * 32;
+  hipLaunchKernelGGL(rope_pairs_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+  REW_HIP(hipGetLastError());
+}
+
+}  // namespace rew

@@ -103,6 +103,38 @@ struct FlashArgs {
   int heavy_last;    // the last query tiles carry the most keys
 };
 bool flash_supported(const FlashArgs& a);
+
+// ---- row composites (k_rows.hip) ----------------------------------------------
+// rmsNorm over rows of n contiguous elements (x row stride x_rs elements):
+// y[r, j] = gamma[j] * (x[r, j] / sqrt(sum_j x^2 / divisor + eps)).
+struct RowNormArgs {
+  const void* x;
+  int x_dt;           // bf16 or f32 (converted to f32 on load)
+  int64_t rows, n, x_rs;
+  const float* gamma;
+  float eps, divisor;
+  void* y;            // dense [rows, n]
+  int y_dt;           // bf16 or f32
+};
+void launch_rmsnorm_rows(const RowNormArgs& a, hipStream_t stream);
+
+// applyRotate on adjacent pairs over a [d0, d1, S, 2*half] index space; x,
+// cos and sin are read through strided views (cos / sin indexed by pair i),
+// y is dense.  half % 4 == 0 and d0*d1*S*half/4 < 2^31.
+struct RopeArgs {
+  const void* x;
+  int x_dt;
+  int64_t d0, d1, S, half;
+  int64_t x_s0, x_s1, x_ss, x_sd;
+  const float* cos;
+  int64_t c_s0, c_s1, c_ss, c_si;
+  const float* sin;
+  int64_t s_s0, s_s1, s_ss, s_si;
+  void* y;
+  int y_dt;
+  vm::FastDiv fd_g4, fd_s, fd_d1;  // divisors half/4, S, d1
+};
+void launch_rope(const RopeArgs& a, hipStream_t stream);
 void launch_flash(const FlashArgs& a, hipStream_t stream);
 
 }  // namespace rew

@@ -212,17 +212,37 @@ struct GemmPlan {
   Tensor* res = nullptr;
 };
 
+// rmsNorm chain (src/rew/nn/norm.nim:204-224) lowered to one row kernel.
+struct NormPlan {
+  Tensor* src = nullptr;  // bf16 source (astype folded) or the f32 input itself
+  Tensor* gamma = nullptr;
+  float eps = 0.0f, divisor = 1.0f;
+};
+
+// applyRotate chain (src/rew/nn/rope.nim:56-108) lowered to one pair kernel.
+struct RopePlan {
+  Tensor* src = nullptr;   // x (bf16 when the astype to f32 is folded)
+  Tensor* cos0 = nullptr;  // [..., S, half] views of the fp32 tables
+  Tensor* sin0 = nullptr;
+};
+
 struct Lower {
   Ctx* c;
   std::vector<Node*> nodes;  // live pending nodes in creation order
   std::unordered_map<Node*, FlashPlan> flash;  // keyed by the PV dot_general
   std::unordered_map<Tensor*, std::vector<Node*>> cons;  // pending consumers
   std::unordered_map<Tensor*, GemmPlan> gemm_out;  // fused GEMM result -> plan
+  std::unordered_map<Tensor*, NormPlan> norm_out;
+  std::unordered_map<Tensor*, RopePlan> rope_out;
 
   explicit Lower(Ctx* ctx) : c(ctx) {}
 
   bool match_flash(Node* pv);
   void match_gemm_epilogues();
+  void match_rows();
+  bool emit_norm(Tensor* t, const NormPlan& p);
+  bool emit_rope(Tensor* t, const RopePlan& p);
+  bool rows_view(Tensor* x, int64_t n, const void** ptr, int64_t* rs);
   bool emit_gemm_fused(Tensor* t, const GemmPlan& p);
   bool emit_flash(Node* pv, const FlashPlan& fp);
   bool kv_operand(Tensor* t, int H, const void** ptr, int64_t* sb, int64_t* sh,
@@ -790,6 +810,18 @@ void Lower::ensure_mat(Tensor* t) {
     gemm_out.erase(git);
     if (emit_gemm_fused(t, gp)) return;
     // not launchable fused: the expression is rebuilt around a plain GEMM
+  }
+  auto nit = norm_out.find(t);
+  if (nit != norm_out.end()) {
+    NormPlan np = nit->second;
+    norm_out.erase(nit);
+    if (emit_norm(t, np)) return;
+  }
+  auto rit = rope_out.find(t);
+  if (rit != rope_out.end()) {
+    RopePlan rp = rit->second;
+    rope_out.erase(rit);
+    if (emit_rope(t, rp)) return;
   }
   Node* p = t->prod;
   if (!p) throw Error(REW_MI355X_ERR_INVALID, "internal: tensor has neither data nor producer");
@@ -1643,6 +1675,250 @@ bool Lower::emit_gemm_fused(Tensor* t, const GemmPlan& p) {
   return true;
 }
 
+
+// ---------------------------------------------------------------------------
+// row composites: rmsNorm and RoPE chains as single kernels
+// ---------------------------------------------------------------------------
+
+static std::vector<int64_t> iota_dims(int n) {
+  std::vector<int64_t> v(n);
+  for (int i = 0; i < n; ++i) v[i] = i;
+  return v;
+}
+
+void Lower::match_rows() {
+  for (Node* mo : nodes) {
+    // ---- rmsNorm: mul(bcast(gamma), divide(x, bcast(sqrt(sum(x*x)/n + eps))))
+    if (mo->kind == K_BINARY && mo->sub == 2 && mo->out[0]->dt == kF32 &&
+        mo->out[0]->shape.rank >= 1 && !mo->out[0]->st) {
+      Tensor* o = mo->out[0];
+      const int r = o->shape.rank;
+      const int64_t n = o->shape.d[r - 1];
+      for (int ord = 0; ord < 2; ++ord) {
+        Tensor *gB = mo->in[ord], *normed = mo->in[1 - ord];
+        if (gB->st || !gB->prod || gB->prod->kind != K_BROADCAST_TO) continue;
+        Tensor* gamma = gB->prod->in[0];
+        if (!dims_are(gB->prod->l1, {r - 1}) || gamma->shape.rank != 1 ||
+            gamma->shape.d[0] != n || gamma->dt != kF32)
+          continue;
+        Node* dvn = chain_node(normed, K_BINARY, 1);
+        if (!dvn || dvn->sub != 3) continue;
+        Tensor *x = dvn->in[0], *rmsB = dvn->in[1];
+        Node* rb = chain_node(rmsB, K_BROADCAST_TO, 1);
+        if (!rb || rb->l1 != iota_dims(r - 1)) continue;
+        Node* sq_ = chain_node(rb->in[0], K_UNARY, 1);
+        if (!sq_ || sq_->sub != 4) continue;  // sqrt
+        Node* ad = chain_node(sq_->in[0], K_BINARY, 1);
+        float eps, dv;
+        if (!ad || ad->sub != 0 || !const_bcast(ad->in[1], &eps)) continue;
+        Node* md = chain_node(ad->in[0], K_BINARY, 1);
+        if (!md || md->sub != 3 || !const_bcast(md->in[1], &dv)) continue;
+        Node* rs = chain_node(md->in[0], K_REDUCE, 1);
+        if (!rs || rs->sub != RED_SUM || !dims_are(rs->l0, {r - 1})) continue;
+        Node* sm = chain_node(rs->in[0], K_BINARY, 1);
+        if (!sm || sm->sub != 2 || sm->in[0] != x || sm->in[1] != x) continue;
+        NormPlan np;
+        np.gamma = gamma;
+        np.eps = eps;
+        np.divisor = dv;
+        std::vector<Tensor*> inner = {normed, rmsB, rb->in[0], sq_->in[0], ad->in[0],
+                                      md->in[0], rs->in[0]};
+        np.src = x;
+        if (!x->st && x->prod && x->prod->kind == K_CONVERT && x->ext == 0 && x->uses == 3 &&
+            x->prod->in[0]->dt == kBF16) {
+          np.src = x->prod->in[0];
+          inner.push_back(x);
+        } else if (x->dt != kF32) {
+          continue;
+        }
+        Tensor* out = o;
+        Node* cv = sole_consumer(*this, o);
+        if (cv && cv->kind == K_CONVERT && cv->out[0]->dt == kBF16) {
+          inner.push_back(o);
+          out = cv->out[0];
+        }
+        for (Tensor* t : inner) t->plan_mat = false;
+        out->plan_mat = true;
+        norm_out[out] = np;
+        break;
+      }
+    }
+    // ---- RoPE: [astype(] reshape(concat([x0', x1'] as [..., half, 1]), shape) [)]
+    if (mo->kind == K_CONCAT && mo->in.size() == 2) {
+      Tensor* cc = mo->out[0];
+      const int rc = cc->shape.rank;
+      if (rc < 3 || mo->i0 != rc - 1 || cc->shape.d[rc - 1] != 2 || cc->ext != 0 ||
+          cc->uses != 1)
+        continue;
+      Node* rsh = sole_consumer(*this, cc);
+      if (!rsh || rsh->kind != K_RESHAPE) continue;
+      Tensor* R = rsh->out[0];
+      const int r = R->shape.rank;
+      if (r != rc - 1 || R->shape.d[r - 1] != 2 * cc->shape.d[rc - 2]) continue;
+      const int64_t half = cc->shape.d[rc - 2];
+      Node* a0 = chain_node(mo->in[0], K_RESHAPE, 1);
+      Node* a1 = chain_node(mo->in[1], K_RESHAPE, 1);
+      if (!a0 || !a1) continue;
+      Node* x0r = chain_node(a0->in[0], K_BINARY, 1);
+      Node* x1r = chain_node(a1->in[0], K_BINARY, 1);
+      if (!x0r || !x1r || x0r->sub != 1 || x1r->sub != 0) continue;
+      Node* m1 = chain_node(x0r->in[0], K_BINARY, 1);
+      Node* m2 = chain_node(x0r->in[1], K_BINARY, 1);
+      Node* m3 = chain_node(x1r->in[0], K_BINARY, 1);
+      Node* m4 = chain_node(x1r->in[1], K_BINARY, 1);
+      if (!m1 || !m2 || !m3 || !m4 || m1->sub != 2 || m2->sub != 2 || m3->sub != 2 ||
+          m4->sub != 2)
+        continue;
+      Tensor *cos0 = m1->in[0], *x0F = m1->in[1], *sin0 = m2->in[0], *x1F = m2->in[1];
+      if (m3->in[0] != sin0 || m3->in[1] != x0F || m4->in[0] != cos0 || m4->in[1] != x1F)
+        continue;
+      if (cos0->dt != kF32 || sin0->dt != kF32 || cos0->shape.rank != r ||
+          sin0->shape.rank != r)
+        continue;
+      // x0F / x1F = reshape(slice(reshape(X, [..., half, 2]), [...,0|1], [...,1|2]))
+      auto pair_slice = [&](Tensor* f, int which, Tensor** pairs) -> bool {
+        Node* fr = chain_node(f, K_RESHAPE, 2);
+        if (!fr) return false;
+        Node* sl = chain_node(fr->in[0], K_SLICE, 1);
+        if (!sl) return false;
+        const Shape& P = sl->in[0]->shape;
+        if (P.rank != rc) return false;
+        for (int i = 0; i < rc; ++i) {
+          const int64_t st = i == rc - 1 ? which : 0;
+          const int64_t lim = i == rc - 1 ? which + 1 : P.d[i];
+          if (sl->l0[i] != st || sl->l1[i] != lim || sl->l2[i] != 1) return false;
+        }
+        *pairs = sl->in[0];
+        return true;
+      };
+      Tensor *p0, *p1;
+      if (!pair_slice(x0F, 0, &p0) || !pair_slice(x1F, 1, &p1) || p0 != p1) continue;
+      Node* pr = chain_node(p0, K_RESHAPE, 2);
+      if (!pr) continue;
+      Tensor* X = pr->in[0];
+      if (X->shape != R->shape || X->shape.rank < 2 || X->shape.rank > 4) continue;
+      std::vector<Tensor*> inner = {cc, mo->in[0], mo->in[1], a0->in[0], a1->in[0],
+                                    x0r->in[0], x0r->in[1], x1r->in[0], x1r->in[1], x0F, x1F,
+                                    x0F->prod->in[0], x1F->prod->in[0], p0};
+      RopePlan rp;
+      rp.cos0 = cos0;
+      rp.sin0 = sin0;
+      rp.src = X;
+      if (!X->st && X->prod && X->prod->kind == K_CONVERT && X->ext == 0 && X->uses == 1 &&
+          X->prod->in[0]->dt == kBF16 && X->dt == kF32) {
+        rp.src = X->prod->in[0];
+        inner.push_back(X);
+      } else if (X->dt != kF32) {
+        continue;
+      }
+      if (half % 4) continue;
+      Tensor* out = R;
+      Node* cv = sole_consumer(*this, R);
+      if (cv && cv->kind == K_CONVERT && cv->out[0]->dt == kBF16 && R->dt == kF32) {
+        inner.push_back(R);
+        out = cv->out[0];
+      }
+      (void)half;
+      for (Tensor* t : inner) t->plan_mat = false;
+      out->plan_mat = true;
+      rope_out[out] = rp;
+    }
+  }
+}
+
+// x viewed as rows of n contiguous elements with a uniform row stride.
+bool Lower::rows_view(Tensor* x, int64_t n, const void** ptr, int64_t* rs) {
+  Tensor* base;
+  int64_t off, st[kMaxRank];
+  operand_strides(x, &base, &off, st);
+  const Shape& S = x->shape;
+  const int r = S.rank;
+  bool ok = r >= 1 && (S.d[r - 1] == 1 || st[r - 1] == 1);
+  int64_t row = r >= 2 ? st[r - 2] : n;
+  for (int i = r - 3; i >= 0 && ok; --i)
+    if (S.d[i] != 1 && st[i] != st[i + 1] * S.d[i + 1]) ok = false;
+  if (r >= 2 && S.d[r - 2] == 1) row = n;
+  if (!ok || row < n) {
+    std::vector<int> id(r);
+    for (int i = 0; i < r; ++i) id[i] = i;
+    base = emit_permuted_copy(x, id);
+    off = 0;
+    row = n;
+  }
+  *ptr = (const char*)base->data() + off * dt_size(base->dt);
+  *rs = row;
+  return true;
+}
+
+bool Lower::emit_norm(Tensor* t, const NormPlan& p) {
+  const int64_t n = t->shape.d[t->shape.rank - 1];
+  RowNormArgs a;
+  std::memset(&a, 0, sizeof(a));
+  rows_view(p.src, n, &a.x, &a.x_rs);
+  a.x_dt = p.src->dt;
+  a.n = n;
+  a.rows = n ? t->numel() / n : 0;
+  ensure_mat(p.gamma);
+  a.gamma = (const float*)p.gamma->data();
+  a.eps = p.eps;
+  a.divisor = p.divisor;
+  tensor_alloc(t);
+  a.y = t->data();
+  a.y_dt = t->dt;
+  if (c->profiling)
+    prof_begin(c, "rmsnorm_rows{" + std::to_string(a.rows) + "x" + std::to_string(n) + "}");
+  launch_rmsnorm_rows(a, c->stream);
+  prof_end(c);
+  note_launch(c, true);
+  return true;
+}
+
+bool Lower::emit_rope(Tensor* t, const RopePlan& p) {
+  const Shape& S = t->shape;
+  const int r = S.rank;
+  RopeArgs a;
+  std::memset(&a, 0, sizeof(a));
+  int64_t d[4] = {1, 1, 1, 1};
+  for (int i = 0; i < r; ++i) d[4 - r + i] = S.d[i];
+  a.d0 = d[0];
+  a.d1 = d[1];
+  a.S = d[2];
+  a.half = d[3] / 2;
+  if (a.d0 * a.d1 * a.S * (a.half / 4) >= (1ll << 31) || a.half % 4) return false;
+  auto view4 = [&](Tensor* v, const void** ptr, int64_t* s) {
+    Tensor* base;
+    int64_t off, st[kMaxRank];
+    operand_strides(v, &base, &off, st);
+    for (int i = 0; i < 4; ++i) s[i] = 0;
+    for (int i = 0; i < r; ++i) s[4 - r + i] = v->shape.d[i] == 1 ? 0 : st[i];
+    *ptr = (const char*)base->data() + off * dt_size(base->dt);
+  };
+  int64_t sx[4], sc[4], ss[4];
+  const void *px, *pc, *ps;
+  view4(p.src, &px, sx);
+  view4(p.cos0, &pc, sc);
+  view4(p.sin0, &ps, ss);
+  a.x = px;
+  a.x_dt = p.src->dt;
+  a.x_s0 = sx[0]; a.x_s1 = sx[1]; a.x_ss = sx[2]; a.x_sd = sx[3];
+  a.cos = (const float*)pc;
+  a.c_s0 = sc[0]; a.c_s1 = sc[1]; a.c_ss = sc[2]; a.c_si = sc[3];
+  a.sin = (const float*)ps;
+  a.s_s0 = ss[0]; a.s_s1 = ss[1]; a.s_ss = ss[2]; a.s_si = ss[3];
+  a.fd_g4 = make_fastdiv((uint32_t)(a.half / 4));
+  a.fd_s = make_fastdiv((uint32_t)a.S);
+  a.fd_d1 = make_fastdiv((uint32_t)a.d1);
+  tensor_alloc(t);
+  a.y = t->data();
+  a.y_dt = t->dt;
+  if (c->profiling)
+    prof_begin(c, "rope_pairs{" + std::to_string(t->numel()) + "}");
+  launch_rope(a, c->stream);
+  prof_end(c);
+  note_launch(c, true);
+  return true;
+}
+
 void Lower::emit_gather(Node* n) {
   Tensor *src = n->in[0], *ix = n->in[1], *out = n->out[0];
   ensure_mat(src);
@@ -1751,6 +2027,7 @@ void flush(Ctx* c) {
       if (n->kind == K_DOT_GENERAL) L.match_flash(n);
     L.cons = consumers;
     L.match_gemm_epilogues();
+    L.match_rows();
   }
 
   // 3. emission in creation order

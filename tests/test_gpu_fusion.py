@@ -126,3 +126,62 @@ def test_held_intermediate_blocks_fusion(gpu, oracle):
     fused = E.toHost(nn.Linear(wt, bt).forward(xt))
     np.testing.assert_array_equal(got, fused)
     bf16_close(_bits_f32(E.toHost(xw)), oracle.gemm(x, w, True))
+
+
+# ---- row composites ---------------------------------------------------------------------
+
+@pytest.mark.parametrize("shape,bf16", [((2, 100, 4096), True), ((37, 1000), False),
+                                        ((3, 9000), True)])
+def test_rmsnorm_row_kernel(gpu, oracle, shape, bf16):
+    """rew's rmsNorm chain (src/rew/nn/norm.nim:204-224) runs as one row kernel."""
+    key = oracle.init_key(500 + shape[-1])
+    n = shape[-1]
+    x = oracle.normal_f32(oracle.fold_in(key, 0), int(np.prod(shape))).reshape(shape)
+    if bf16:
+        x = oracle.round_bf16(x)
+    g = oracle.normal_f32(oracle.fold_in(key, 1), n, 1.0, 0.1)
+
+    def fn():
+        xt = E.fromHost(x, DType.BFLOAT16 if bf16 else DType.FLOAT32)
+        y = nn.rmsNorm(nn._f32(xt), E.fromHost(g), 1e-5)
+        return nn._to(y, DType.BFLOAT16) if bf16 else y
+
+    got, names = _run(fn)
+    assert any(k.startswith("rmsnorm_rows") for k in names), names
+    want = oracle.rmsnorm_rows(x.reshape(-1, n), g, 1e-5).reshape(shape)
+    if bf16:
+        got = _bits_f32(got)
+        # within one bf16 ulp of the fp32 reference
+        assert np.all(np.abs(got - want) <= 2.0 ** -7 * np.abs(want) + 1e-30)
+    else:
+        np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("B,H,S,D,bf16", [(2, 4, 64, 128, True), (1, 3, 50, 64, False),
+                                          (1, 2, 7, 32, True)])
+def test_rope_pair_kernel(gpu, oracle, B, H, S, D, bf16):
+    """rew's applyRotate chain (src/rew/nn/rope.nim:56-179) on a transposed
+    projection view runs as one kernel, bit-exact with the op-by-op path."""
+    key = oracle.init_key(600 + S)
+    x = oracle.normal_f32(oracle.fold_in(key, 0), B * S * H * D).reshape(B, S, H, D)
+    if bf16:
+        x = oracle.round_bf16(x)
+    dt = DType.BFLOAT16 if bf16 else DType.FLOAT32
+
+    def fn():
+        rope = nn.RotaryPositionEncoding.init(D, S + 8, 500000.0)
+        xt = O.transpose(E.fromHost(x, dt), [0, 2, 1, 3])  # [B, H, S, D] view
+        return rope.forward(xt, 3)
+
+    got, names = _run(fn)
+    assert any(k.startswith("rope_pairs") for k in names), names
+    ref, names2 = _run(fn, op_by_op=True)
+    assert not any(k.startswith("rope_pairs") for k in names2)
+    np.testing.assert_array_equal(got, ref)
+    c, s = nn.rope_tables(D, S + 8, 500000.0)
+    want = oracle.rope(np.ascontiguousarray(x.transpose(0, 2, 1, 3)), c, s, 3)
+    gotf = _bits_f32(got) if bf16 else got
+    if bf16:
+        assert np.all(np.abs(gotf - want) <= 2.0 ** -8 * np.abs(want) + 1e-6)
+    else:
+        np.testing.assert_allclose(gotf, want, rtol=1e-6, atol=1e-6)
