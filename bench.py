@@ -9,10 +9,17 @@ A step is: torchIndexSelect(table, ids) -> LlamaDecoderLayer.forward, driven
 through the same eager op sequence rew's nn layers emit (rew_amd.nn), with
 every input already resident in HBM.
 
-Prints ONE JSON line (rank 0, N=1) with the metric, a roofline object for
-the dominant kernel (durations from HIP events recorded on the backend's own
-stream), the whole-layer MFMA fraction, and a cpu_baseline: the CPU
-restatement in oracle/ timed on this host's cores on a bounded sample.
+Other workloads (``--workload``) are the remaining configurations of the
+hot path, each measured the same way: ``chain`` (fp32 elementwise +
+reductions + softmax + RMSNorm, HBM-bound), ``swiglu`` (the gated FFN,
+MFMA-bound), ``mnist`` (MLP inference with argmax, latency-bound), ``moe``
+(DeepSeek-style routed MoE layer) and ``copy`` (a plain streaming kernel of
+known size, the calibration for the HBM byte counters).
+
+Prints ONE JSON line with the metric, a roofline object for the dominant
+kernel (its launches timed by HIP events on the backend's own stream over
+the timed steps), and a cpu_baseline: the CPU restatement in oracle/ timed
+on this host's cores on a bounded sample.
 """
 from __future__ import annotations
 
@@ -37,6 +44,7 @@ from rew_amd.eager import DType  # noqa: E402
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2516.6      # MI355X dense bf16 MFMA, TFLOP/s
 FP32_PEAK_TFLOPS = 157.3       # MI355X fp32 vector, TFLOP/s
+TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
 
 # C4 shape (the reference's LlamaDecoderLayer / GroupedQueryAttention / GatedFeedForward)
 C4 = dict(batch=4, seq_len=2048, hidden=4096, heads=32, kv_heads=8, head_dim=128,
@@ -53,6 +61,8 @@ def llama_layer_flops(B, S, H, nh, nkv, hd, I, causal=True):
     attn = 2 * 2 * B * nh * pairs * hd
     return proj + attn + ffn
 
+
+# ---- timing ---------------------------------------------------------------------------------
 
 class HipEvents:
     """HIP events recorded on the backend's stream (not torch's)."""
@@ -90,25 +100,118 @@ def backend_stream():
     return s.value
 
 
-def profile_step(step):
-    """Per-kernel totals of one step from the backend's launch events."""
-    lib = E._lib.load()
-    ctx = E.context()
-    if lib.rew_mi355x_profile_begin(ctx) != 0:
-        raise RuntimeError(lib.rew_mi355x_last_error().decode())
-    step()
-    if lib.rew_mi355x_profile_end(ctx) != 0:
-        raise RuntimeError(lib.rew_mi355x_last_error().decode())
-    out = []
-    name = C.create_string_buffer(256)
-    n = C.c_int64()
-    ms = C.c_double()
-    i = 0
-    while lib.rew_mi355x_profile_entry(ctx, i, name, 256, C.byref(n), C.byref(ms)) == 0:
-        out.append((name.value.decode(), int(n.value), float(ms.value)))
-        i += 1
+def kernel_symbol(entry_name: str) -> str:
+    return entry_name.split("[")[0].split("{")[0].split("+")[0]
+
+
+def timed_run(step, steps, warmup):
+    """First call, warmup, then `steps` timed steps bracketed by sync on both
+    sides.  Every kernel launch inside the timed region is bracketed by HIP
+    events on the backend stream (rew_mi355x_profile_*), so per-kernel
+    durations come from the timed steps themselves.
+
+    Returns (wall_s, device_ms, first_ms, profile entries)."""
+    t0 = time.perf_counter()
+    y = step()
+    E.sync()
+    first_ms = (time.perf_counter() - t0) * 1e3
+    del y
+    for _ in range(warmup):
+        step()
+    E.sync()
+    ev = HipEvents(backend_stream())
+    e0, e1 = ev.event(), ev.event()
+    outs = []
+    E.sync()
+    E.profileBegin()
+    t0 = time.perf_counter()
+    ev.record(e0)
+    for _ in range(steps):
+        outs.append(step())
+        if len(outs) > 2:
+            outs.pop(0)
+    ev.record(e1)
+    E.sync()
+    wall = time.perf_counter() - t0
+    prof = E.profileEnd()
+    dev_ms = ev.elapsed_ms(e0, e1)
+    outs.clear()
+    for name, n, ms in sorted(prof, key=lambda r: -r[2]):
+        print(f"#   {ms * 1e3 / steps:9.1f} us/step  x{n // steps:<3d} {name}", file=sys.stderr)
+    return wall, dev_ms, first_ms, prof
+
+
+def by_symbol(prof, work_of):
+    """Groups profile entries by kernel symbol: launches, ms and the summed
+    algorithmic work (work_of(entry name) -> units, or None if unknown)."""
+    out = {}
+    for name, n, ms in prof:
+        d = out.setdefault(kernel_symbol(name), {"launches": 0, "ms": 0.0, "work": 0,
+                                                 "known": True})
+        d["launches"] += n
+        d["ms"] += ms
+        w = work_of(name)
+        if w is None:
+            d["known"] = False
+        else:
+            d["work"] += w * n
     return out
 
+
+def traffic_for(workload, kernel):
+    """HBM bytes per launch of `kernel` in `workload` from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE runs (profiles/traffic.json), or None."""
+    try:
+        data = json.loads(TRAFFIC_FILE.read_text())
+    except (OSError, ValueError):
+        return None
+    rec = data.get(f"{workload}:{kernel}")
+    return None if rec is None else int(rec["bytes_per_launch"])
+
+
+def roofline(workload, syms, bound):
+    """Roofline object of the kernel with the largest summed duration."""
+    ksym, d = max(syms.items(), key=lambda kv: kv[1]["ms"])
+    avg_ms = d["ms"] / d["launches"]
+    peak, unit = (BF16_PEAK_TFLOPS, "TFLOP/s") if bound == "mfma" else (HBM_PEAK_GBS, "GB/s")
+    roof = {"bound": bound, "kernel": ksym, "achieved": None, "peak": peak, "unit": unit,
+            "frac": None, "traffic": traffic_for(workload, ksym),
+            "avg_launch_us": round(avg_ms * 1e3, 2), "launches": d["launches"]}
+    if d["known"]:
+        per_launch = d["work"] / d["launches"]
+        scale = 1e12 if bound == "mfma" else 1e9
+        achieved = per_launch / (avg_ms * 1e-3) / scale
+        roof["achieved"] = round(achieved, 1)
+        roof["frac"] = round(achieved / peak, 4)
+        roof["algorithmic_" + ("flops" if bound == "mfma" else "bytes") + "_per_launch"] = \
+            int(per_launch)
+    return roof
+
+
+def breakdown(syms, steps):
+    return sorted(((k, round(v["ms"] / steps, 3), v["launches"] // steps)
+                   for k, v in syms.items()), key=lambda r: -r[1])
+
+
+def emit(args, metric, value, unit, ms_per_step, dtype, config, roof, cpu, extra, hib=True):
+    line = {"metric": metric, "value": round(value, 3 if value < 1000 else 1), "unit": unit,
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(ms_per_step, 4), "higher_is_better": hib, "scaling": "weak",
+            "vs_baseline": None, "dtype": dtype,
+            "data": "synthetic (rew Threefry normalF32/uniformF32 inputs, random-init weights)",
+            "config": config, "roofline": roof, "cpu_baseline": cpu}
+    line.update(extra)
+    print(json.dumps(line), flush=True)
+
+
+def oracle_mod():
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as orc
+    orc.build()
+    return orc
+
+
+# ---- C4: Llama decoder layer prefill -------------------------------------------------------
 
 def visible_pairs(Sq: int, Sk: int, cmp: int) -> int:
     """(query, key) pairs a mask predicate cmp(i, j) keeps; -1 = no mask."""
@@ -126,27 +229,23 @@ def entry_flops(entry_name: str) -> int | None:
     -> 4*B*H*D*(visible pairs) (QK^T and PV over the pairs the mask keeps)."""
     if "[" not in entry_name:
         return None
-    dims = [int(v) for v in entry_name[entry_name.index("[") + 1:-1].split(",")]
+    dims = [int(v) for v in entry_name[entry_name.index("[") + 1:entry_name.index("]")].split(",")]
     if entry_name.startswith("flash_attn"):
         B, H, _, Sq, Sk, D, cmp, _ = dims
         return 4 * B * H * D * visible_pairs(Sq, Sk, cmp)
+    if entry_name.startswith("moe_"):
+        return None
     b, m, n, k = dims
     # the SwiGLU kernel runs the gate and up projections over the same A
     return (4 if "swiglu" in entry_name else 2) * b * m * n * k
 
 
-def kernel_symbol(entry_name: str) -> str:
-    return entry_name.split("[")[0].split("{")[0].split("+")[0]
-
-
-# ---- C4: Llama decoder layer prefill -------------------------------------------------------
-
-def build_llama(cfg, seed=0x5EED0004, small_vocab=None):
+def build_llama(cfg, seed=0x5EED0004):
     """Weights ~N(0, 0.02) bf16, zero biases, gammas ~N(1, 0.1) f32, keyed per
     tensor in declaration order from initKey(seed)."""
     H, nh, nkv, hd, I = (cfg["hidden"], cfg["heads"], cfg["kv_heads"], cfg["head_dim"],
                          cfg["intermediate"])
-    V = small_vocab or cfg["vocab"]
+    V = cfg["vocab"]
     keys = rng.split(rng.initKey(seed), 12)
     host = {}
 
@@ -178,27 +277,26 @@ def build_llama(cfg, seed=0x5EED0004, small_vocab=None):
     return layer, emb, E.fromHost(ids), host, table, ids
 
 
-def cpu_baseline_llama(cfg, host, table, ids, tokens):
-    """The oracle's restatement of the same layer on a bounded sample: one
-    sequence of `tokens` tokens (the first `tokens` ids of sequence 0)."""
-    sys.path.insert(0, str(ROOT / "oracle"))
-    import oracle as orc
-    orc.build()
-    nh, nkv, hd = cfg["heads"], cfg["kv_heads"], cfg["head_dim"]
+def cpu_baseline_llama(cfg, host, table, ids, seqs):
+    """The oracle's restatement of the same layer on a bounded sample: the
+    first `seqs` of the batch's sequences, each a full S-token causal prefill."""
+    orc = oracle_mod()
+    nh, nkv, hd, S = cfg["heads"], cfg["kv_heads"], cfg["head_dim"], cfg["seq_len"]
     p = {}
     for n in "qkvogud":
         p["w" + n] = orc.from_bf16(host["w" + n])
         p["b" + n] = host["b" + n]
     p["g1"], p["g2"] = host["g1"], host["g2"]
-    c, s = nn.rope_tables(hd, tokens, cfg["rope_theta"])
-    x = orc.from_bf16(table[ids[:tokens]]).reshape(1, tokens, cfg["hidden"])
+    c, s = nn.rope_tables(hd, S, cfg["rope_theta"])
+    x = orc.from_bf16(table[ids[:seqs * S]]).reshape(seqs, S, cfg["hidden"])
     t0 = time.perf_counter()
     orc.llama_layer(x, p, nh, nkv, c, s, cfg["eps"], True, True, "rms")
     dt = time.perf_counter() - t0
-    return {"value": tokens / dt, "unit": "tokens/s", "cores": int(orc.lib().orc_num_threads()),
-            "kind": "port",
-            "sample": f"1 x {tokens}-token causal prefill of the same layer (full hidden/FFN/"
-                      f"head dims), oracle/ C restatement with OpenMP, {dt:.2f} s"}
+    return {"value": round(seqs * S / dt, 2), "unit": "tokens/s",
+            "cores": int(orc.lib().orc_num_threads()), "kind": "port",
+            "sample": f"{seqs} of the {cfg['batch']} sequences ({seqs * S} tokens, full "
+                      f"hidden/FFN/head dims, causal), oracle/ C restatement with OpenMP, "
+                      f"{dt:.1f} s"}
 
 
 def run_llama(args):
@@ -215,96 +313,161 @@ def run_llama(args):
         E.flush()
         return y
 
-    t0 = time.perf_counter()
-    y = step()
-    E.sync()
-    first_ms = (time.perf_counter() - t0) * 1e3
-    del y
-    for _ in range(args.warmup):
-        step()
-    E.sync()
-    ev = HipEvents(backend_stream())
-    e0, e1 = ev.event(), ev.event()
-    E.sync()
-    t0 = time.perf_counter()
-    ev.record(e0)
-    outs = []
-    for _ in range(args.steps):
-        outs.append(step())
-        if len(outs) > 2:
-            outs.pop(0)
-    ev.record(e1)
-    E.sync()
-    wall = time.perf_counter() - t0
-    dev_ms = ev.elapsed_ms(e0, e1)
-    outs.clear()
+    wall, dev_ms, first_ms, prof = timed_run(step, args.steps, args.warmup)
     ms_per_step = wall * 1e3 / args.steps
-    tokens = B * S
-    value = tokens * args.steps / wall
     flops = llama_layer_flops(B, S, H, cfg["heads"], cfg["kv_heads"], cfg["head_dim"],
                               cfg["intermediate"])
+    syms = by_symbol(prof, entry_flops)
+    roof = roofline("llama", syms, "mfma")
+    kernel_ms = sum(v["ms"] for v in syms.values()) / args.steps
+    cpu = None if args.no_cpu_baseline else cpu_baseline_llama(cfg, host, table, ids,
+                                                               args.cpu_seqs)
+    config = {"workload": "llama_decoder_layer_prefill_bf16", "batch": B, "seq_len": S,
+              "hidden": H, "heads": cfg["heads"], "kv_heads": cfg["kv_heads"],
+              "head_dim": cfg["head_dim"], "intermediate": cfg["intermediate"],
+              "vocab": cfg["vocab"], "rope_theta": cfg["rope_theta"], "causal": True,
+              "parallelism": "single-gpu"}
+    extra = {"layer": {"algorithmic_tflop": round(flops / 1e12, 4),
+                       "achieved_tflops": round(flops / (ms_per_step * 1e-3) / 1e12, 1),
+                       "mfma_frac": round(flops / (ms_per_step * 1e-3) / 1e12 /
+                                          BF16_PEAK_TFLOPS, 4),
+                       "device_ms_per_step": round(dev_ms / args.steps, 3),
+                       "kernel_ms_per_step": round(kernel_ms, 3),
+                       "first_call_ms": round(first_ms, 1),
+                       "kernels": breakdown(syms, args.steps)[:12]}}
+    emit(args, "llama_layer_prefill_tokens_per_s", B * S * args.steps / wall, "tokens/s",
+         ms_per_step, "bf16", config, roof, cpu, extra)
 
-    # per-kernel breakdown of one extra step
-    prof = profile_step(step)
+
+# ---- C3: SwiGLU gated FFN ------------------------------------------------------------------
+
+def run_swiglu(args):
+    T, H, I = 4096, 4096, 14336
+    keys = rng.split(rng.initKey(0x5EED0003), 4)
+    x = E.f32_to_bf16_bits(rng.normalF32(keys[0], T * H)).reshape(1, T, H)
+    ws = [E.f32_to_bf16_bits(rng.normalF32(keys[1 + i], fi * fo, 0.0, 0.02)).reshape(fi, fo)
+          for i, (fi, fo) in enumerate([(H, I), (H, I), (I, H)])]
+    lins = [nn.Linear(E.fromHost(w, DType.BFLOAT16),
+                      E.fromHost(np.zeros(w.shape[1], np.uint16), DType.BFLOAT16)) for w in ws]
+    ffn = nn.GatedFeedForward(*lins)
+    xt = E.fromHost(x, DType.BFLOAT16)
     E.sync()
-    for name, n, ms in sorted(prof, key=lambda r: -r[2]):
-        print(f"#   {ms * 1e3:9.1f} us  x{n:<3d} {name}", file=sys.stderr)
-    by_sym = {}
-    for name, n, ms in prof:
-        sym = kernel_symbol(name)
-        d = by_sym.setdefault(sym, {"launches": 0, "ms": 0.0, "flops": 0, "flops_known": True})
-        d["launches"] += n
-        d["ms"] += ms
-        f = entry_flops(name)
-        if f is None:
-            d["flops_known"] = False
-        else:
-            d["flops"] += f * n
-    dom = max(by_sym.items(), key=lambda kv: kv[1]["ms"])
-    dsym, d = dom
-    avg_ms = d["ms"] / d["launches"]
-    if d["flops_known"]:
-        per_launch = d["flops"] / d["launches"]
-        achieved = per_launch / (avg_ms * 1e-3) / 1e12
-        roof = {"bound": "mfma", "kernel": dsym, "achieved": round(achieved, 1),
-                "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": None,
-                "avg_launch_us": round(avg_ms * 1e3, 2), "launches_per_step": d["launches"],
-                "algorithmic_flops_per_launch": int(per_launch)}
-    else:
-        roof = {"bound": "hbm", "kernel": dsym, "achieved": None, "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": None, "traffic": None,
-                "avg_launch_us": round(avg_ms * 1e3, 2), "launches_per_step": d["launches"]}
-    total_prof_ms = sum(v["ms"] for v in by_sym.values())
-    breakdown = sorted(((k, round(v["ms"], 3), v["launches"]) for k, v in by_sym.items()),
-                       key=lambda r: -r[1])
 
+    def step():
+        y = ffn.forward(xt)
+        E.flush()
+        return y
+
+    wall, dev_ms, first_ms, prof = timed_run(step, args.steps, args.warmup)
+    ms = wall * 1e3 / args.steps
+    flops = 2 * T * H * I * 3
+    syms = by_symbol(prof, entry_flops)
+    roof = roofline("swiglu", syms, "mfma")
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline_llama(cfg, host, table, ids, args.cpu_tokens)
+        orc = oracle_mod()
+        rows = 256
+        xf = orc.from_bf16(x.reshape(T, H)[:rows])
+        wf = [orc.from_bf16(w) for w in ws]
+        z = np.zeros(I, np.float32)
+        t0 = time.perf_counter()
+        orc.gated_ffn(xf, wf[0], z, wf[1], z, wf[2], np.zeros(H, np.float32), True)
+        dt = time.perf_counter() - t0
+        cpu = {"value": round(2 * rows * H * I * 3 / dt / 1e12, 4), "unit": "TFLOP/s",
+               "cores": int(orc.lib().orc_num_threads()), "kind": "port",
+               "sample": f"{rows} of the {T} token rows through the same FFN, oracle/ C "
+                         f"restatement with OpenMP, {dt:.1f} s"}
+    emit(args, "swiglu_ffn_tflops", flops / (ms * 1e-3) / 1e12, "TFLOP/s", ms, "bf16",
+         {"workload": "swiglu_gated_ffn_bf16", "tokens": T, "hidden": H, "intermediate": I},
+         roof, cpu, {"kernels": breakdown(syms, args.steps), "first_call_ms": round(first_ms, 1),
+                     "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)})
 
-    line = {
-        "metric": "llama_layer_prefill_tokens_per_s",
-        "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 3),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic (rew Threefry/normalF32 inputs, random-init weights)",
-        "config": {"workload": "llama_decoder_layer_prefill_bf16", "batch": B, "seq_len": S,
-                   "hidden": H, "heads": cfg["heads"], "kv_heads": cfg["kv_heads"],
-                   "head_dim": cfg["head_dim"], "intermediate": cfg["intermediate"],
-                   "vocab": cfg["vocab"], "rope_theta": cfg["rope_theta"], "causal": True,
-                   "parallelism": "single-gpu"},
-        "roofline": roof,
-        "layer": {"algorithmic_tflop": round(flops / 1e12, 4),
-                  "achieved_tflops": round(flops / (ms_per_step * 1e-3) / 1e12, 1),
-                  "mfma_frac": round(flops / (ms_per_step * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
-                  "device_ms_per_step": round(dev_ms / args.steps, 3),
-                  "kernel_ms_per_step": round(total_prof_ms, 3),
-                  "first_call_ms": round(first_ms, 1),
-                  "kernels": breakdown[:12]},
-        "cpu_baseline": cpu,
-    }
-    print(json.dumps(line), flush=True)
+
+# ---- C2: elementwise + reduction chain (HBM-bound) ----------------------------------------
+
+def run_chain(args):
+    R, Cn = 8192, 4096
+    keys = rng.split(rng.initKey(0x5EED0002), 2)
+    x = rng.normalF32(keys[0], R * Cn).reshape(R, Cn)
+    g = rng.normalF32(keys[1], Cn, 1.0, 0.1)
+    xt, gt = E.fromHost(x), E.fromHost(g)
+    E.sync()
+    nbytes = R * Cn * 4
+    # algorithmic bytes of each op group of the chain
+    groups = {"relu_chain": 2 * nbytes, "reduceSum": nbytes + R * 4, "reduceMean": nbytes + R * 4,
+              "reduceMax": nbytes + R * 4, "softmax": 2 * nbytes, "rmsNorm": 2 * nbytes + Cn * 4}
+    total = sum(groups.values())
+
+    def step():
+        y = nn.relu(O.add(xt, xt))
+        outs = [y, O.reduceSum(y, [1]), O.reduceMean(y, [1]), O.reduceMax(y, [1]),
+                nn.softmax(xt, 1), nn.rmsNorm(xt, gt, 1e-5)]
+        E.flush()
+        return outs
+
+    wall, dev_ms, first_ms, prof = timed_run(step, args.steps, args.warmup)
+    ms = wall * 1e3 / args.steps
+
+    def bytes_of(name):
+        if name.startswith("rmsnorm_rows"):
+            return groups["rmsNorm"]
+        if name.startswith("softmax_rows"):
+            return groups["softmax"]
+        if name.startswith("ew_"):
+            return groups["relu_chain"]
+        if name.startswith("reduce"):
+            return nbytes + R * 4
+        return None
+
+    syms = by_symbol(prof, bytes_of)
+    roof = roofline("chain", syms, "hbm")
+    cpu = None
+    if not args.no_cpu_baseline:
+        orc = oracle_mod()
+        rows = 2048
+        xs, t0 = x[:rows], time.perf_counter()
+        reps = 0
+        while time.perf_counter() - t0 < 10.0:
+            y = orc.binary(orc.MAX, orc.binary(orc.ADD, xs, xs), np.zeros_like(xs))
+            orc.reduce(orc.RSUM, y, [1])
+            orc.reduce(orc.RSUM, y, [1])
+            orc.reduce(orc.RMAX, y, [1])
+            orc.softmax_rows(xs)
+            orc.rmsnorm_rows(xs, g, 1e-5)
+            reps += 1
+        dt = time.perf_counter() - t0
+        cpu = {"value": round(total * rows / R * reps / dt / 1e9, 2), "unit": "GB/s",
+               "cores": int(orc.lib().orc_num_threads()), "kind": "port",
+               "sample": f"{reps} passes of the chain over {rows} of the {R} rows, oracle/ C "
+                         f"restatement, {dt:.1f} s"}
+    emit(args, "eager_chain_hbm_gbs", total / (ms * 1e-3) / 1e9, "GB/s", ms, "f32",
+         {"workload": "eager_elementwise_reduction_chain_f32", "rows": R, "cols": Cn},
+         roof, cpu, {"kernels": breakdown(syms, args.steps), "algorithmic_bytes_per_step": total,
+                     "hbm_frac": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+
+
+# ---- copy: the streaming kernel the HBM byte counters are calibrated on --------------------
+
+def run_copy(args):
+    n = 256 * 1024 * 1024  # 1 GiB of fp32
+    x = E.fromHost(np.ones(n, np.float32))
+    E.sync()
+
+    def step():
+        y = O.neg(x)
+        E.flush()
+        return y
+
+    wall, dev_ms, first_ms, prof = timed_run(step, args.steps, args.warmup)
+    ms = wall * 1e3 / args.steps
+    syms = by_symbol(prof, lambda name: 2 * n * 4)
+    roof = roofline("copy", syms, "hbm")
+    emit(args, "stream_copy_gbs", 2 * n * 4 / (ms * 1e-3) / 1e9, "GB/s", ms, "f32",
+         {"workload": "stream_neg_f32", "elements": n}, roof, None,
+         {"bytes_per_launch": 2 * n * 4})
+
+
+WORKLOADS = {"llama": run_llama, "swiglu": run_swiglu, "chain": run_chain, "copy": run_copy}
 
 
 def main():
@@ -312,20 +475,20 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="llama", choices=["llama"])
-    ap.add_argument("--cpu-tokens", type=int, default=512,
-                    help="tokens in the cpu_baseline sample")
+    ap.add_argument("--workload", default="llama", choices=sorted(WORKLOADS))
+    ap.add_argument("--cpu-seqs", type=int, default=2,
+                    help="sequences of the llama batch in the cpu_baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build measures one MI355X only (the sharded path is design-only); "
-              "run with --gpus 1", file=sys.stderr)
+        print("bench.py: this build measures one MI355X only; the multi-GPU sharding of the "
+              "path is a design note, not code. Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     if E.deviceCount() < 1:
         print("bench.py: no HIP device visible", file=sys.stderr)
         sys.exit(1)
     E.installEagerBackend(E.mi355x(0))
-    run_llama(args)
+    WORKLOADS[args.workload](args)
 
 
 if __name__ == "__main__":
