@@ -233,8 +233,9 @@ def entry_flops(entry_name: str) -> int | None:
     if entry_name.startswith("flash_attn"):
         B, H, _, Sq, Sk, D, cmp, _ = dims
         return 4 * B * H * D * visible_pairs(Sq, Sk, cmp)
-    if entry_name.startswith("moe_"):
-        return None
+    if entry_name.startswith("moe_gemm"):
+        _, rows, n, k = dims  # [members, routed rows, N, K]
+        return (4 if "swiglu" in entry_name else 2) * rows * n * k
     b, m, n, k = dims
     # the SwiGLU kernel runs the gate and up projections over the same A
     return (4 if "swiglu" in entry_name else 2) * b * m * n * k
@@ -467,7 +468,143 @@ def run_copy(args):
          {"bytes_per_launch": 2 * n * 4})
 
 
-WORKLOADS = {"llama": run_llama, "swiglu": run_swiglu, "chain": run_chain, "copy": run_copy}
+# ---- C5: DeepSeek-style routed MoE layer ---------------------------------------------------
+
+C5 = dict(tokens=8192, hidden=2048, intermediate=1408, routed=64, shared=2, top_k=6)
+
+
+def moe_flops(T, H, I, E_, S, k):
+    """Sparse algorithmic FLOPs: router + the k routed experts of every token
+    + the shared experts (each expert 3 GEMMs of 2*H*I per token)."""
+    return 2 * T * H * E_ + 2 * 3 * T * k * H * I + 2 * 3 * T * S * H * I
+
+
+def build_moe(cfg, seed=0x5EED0005):
+    T, H, I, E_, S = (cfg["tokens"], cfg["hidden"], cfg["intermediate"], cfg["routed"],
+                      cfg["shared"])
+    keys = rng.split(rng.initKey(seed), 2 + S + E_)
+    x = E.f32_to_bf16_bits(rng.normalF32(keys[0], T * H)).reshape(T, H)
+    wr = rng.normalF32(keys[1], H * E_, 0.0, 0.02).reshape(H, E_)
+    host = {"x": x, "wr": wr, "experts": []}
+
+    def expert(key):
+        ks = rng.split(key, 3)
+        ws = [E.f32_to_bf16_bits(rng.normalF32(ks[i], fi * fo, 0.0, 0.02)).reshape(fi, fo)
+              for i, (fi, fo) in enumerate([(H, I), (H, I), (I, H)])]
+        host["experts"].append(ws)
+        return nn.DeepSeekExpert(*[nn.Linear(E.fromHost(w, DType.BFLOAT16),
+                                             E.fromHost(np.zeros(w.shape[1], np.uint16),
+                                                        DType.BFLOAT16)) for w in ws])
+
+    shared = [expert(keys[2 + i]) for i in range(S)]
+    routed = [expert(keys[2 + S + e]) for e in range(E_)]
+    moe = nn.DeepSeekMoE(nn.Linear(E.fromHost(wr), E.fromHost(np.zeros(E_, np.float32))),
+                         shared, routed, cfg["top_k"])
+    return moe, E.fromHost(x, DType.BFLOAT16), host
+
+
+def run_moe(args):
+    cfg = dict(C5)
+    T, H, I, E_, S, k = (cfg["tokens"], cfg["hidden"], cfg["intermediate"], cfg["routed"],
+                         cfg["shared"], cfg["top_k"])
+    t0 = time.perf_counter()
+    moe, xt, host = build_moe(cfg)
+    E.sync()
+    print(f"# inputs ready in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+
+    def step():
+        y = moe.forward(xt)
+        E.flush()
+        return y
+
+    wall, dev_ms, first_ms, prof = timed_run(step, args.steps, args.warmup)
+    ms = wall * 1e3 / args.steps
+    flops = moe_flops(T, H, I, E_, S, k)
+    syms = by_symbol(prof, entry_flops)
+    roof = roofline("moe", syms, "mfma")
+    cpu = None
+    if not args.no_cpu_baseline:
+        orc = oracle_mod()
+        rows = 256
+        xs = orc.from_bf16(host["x"][:rows])
+        z = lambda n: np.zeros(n, np.float32)
+        exps = [(orc.from_bf16(a), z(I), orc.from_bf16(b), z(I), orc.from_bf16(c), z(H))
+                for a, b, c in host["experts"]]
+        t0 = time.perf_counter()
+        orc.deepseek_moe(xs, exps[:S], exps[S:], host["wr"], z(E_), k)
+        dt = time.perf_counter() - t0
+        cpu = {"value": round(rows / dt, 2), "unit": "tokens/s",
+               "cores": int(orc.lib().orc_num_threads()), "kind": "port",
+               "sample": f"{rows} of the {T} tokens through the reference's dense "
+                         f"formulation (every routed expert on every token, "
+                         f"deepseek.nim:122-145), oracle/ C restatement, {dt:.1f} s"}
+    emit(args, "moe_layer_tokens_per_s", T * args.steps / wall, "tokens/s", ms, "bf16",
+         {"workload": "deepseek_moe_layer_bf16", "tokens": T, "hidden": H, "intermediate": I,
+          "routed_experts": E_, "shared_experts": S, "top_k": k},
+         roof, cpu, {"kernels": breakdown(syms, args.steps), "first_call_ms": round(first_ms, 1),
+                     "algorithmic_tflop": round(flops / 1e12, 4),
+                     "achieved_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+                     "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)})
+
+
+# ---- C1: MNIST-shaped MLP inference (latency-bound) ----------------------------------------
+
+def run_mnist(args):
+    B, D, Hd, C = 128, 784, 128, 10
+    keys = rng.split(rng.initKey(0x5EED0001), 3)
+    x = rng.uniformF32(keys[0], B * D, 0.0, 1.0).reshape(B, D)
+    w1 = rng.xavierUniformF32(keys[1], D, Hd).reshape(D, Hd)
+    w2 = rng.xavierUniformF32(keys[2], Hd, C).reshape(Hd, C)
+    l1 = nn.Linear(E.fromHost(w1), E.fromHost(np.zeros(Hd, np.float32)))
+    l2 = nn.Linear(E.fromHost(w2), E.fromHost(np.zeros(C, np.float32)))
+    xt = E.fromHost(x)
+    E.sync()
+
+    def step():
+        ids = O.argmax(nn.softmax(l2.forward(nn.relu(l1.forward(xt))), 1), 1)
+        E.flush()
+        return ids
+
+    wall, dev_ms, first_ms, prof = timed_run(step, args.steps, args.warmup)
+    ms = wall * 1e3 / args.steps
+    flops = 2 * B * D * Hd + 2 * B * Hd * C
+
+    def gemm_flops(name):
+        f = entry_flops(name)
+        return f if f is not None and name.startswith("gemm") else None
+
+    syms = by_symbol(prof, gemm_flops)
+    ksym, d = max(syms.items(), key=lambda kv: kv[1]["ms"])
+    roof = {"bound": "fp32", "kernel": ksym, "achieved": None, "peak": FP32_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": None, "traffic": traffic_for("mnist", ksym),
+            "avg_launch_us": round(d["ms"] / d["launches"] * 1e3, 2), "launches": d["launches"]}
+    if d["known"] and d["work"]:
+        ach = d["work"] / d["launches"] / (d["ms"] / d["launches"] * 1e-3) / 1e12
+        roof["achieved"] = round(ach, 3)
+        roof["frac"] = round(ach / FP32_PEAK_TFLOPS, 5)
+    cpu = None
+    if not args.no_cpu_baseline:
+        orc = oracle_mod()
+        t0, reps = time.perf_counter(), 0
+        z1, z2 = np.zeros(Hd, np.float32), np.zeros(C, np.float32)
+        while time.perf_counter() - t0 < 10.0:
+            h = np.maximum(orc.linear(x, w1, z1, False), 0)
+            orc.argmax_rows(orc.softmax_rows(orc.linear(h, w2, z2, False)))
+            reps += 1
+        dt = time.perf_counter() - t0
+        cpu = {"value": round(B * reps / dt, 1), "unit": "rows/s",
+               "cores": int(orc.lib().orc_num_threads()), "kind": "port",
+               "sample": f"{reps} forwards of the full [128,784] batch, oracle/ C restatement, "
+                         f"{dt:.1f} s"}
+    emit(args, "mnist_mlp_rows_per_s", B * args.steps / wall, "rows/s", ms, "f32",
+         {"workload": "mnist_mlp_inference_f32", "batch": B, "layers": [D, Hd, C]},
+         roof, cpu, {"kernels": breakdown(syms, args.steps), "first_call_ms": round(first_ms, 2),
+                     "us_per_forward": round(ms * 1e3, 1), "algorithmic_flops": flops,
+                     "device_us_per_forward": round(dev_ms * 1e3 / args.steps, 1)})
+
+
+WORKLOADS = {"llama": run_llama, "swiglu": run_swiglu, "chain": run_chain, "copy": run_copy,
+             "moe": run_moe, "mnist": run_mnist}
 
 
 def main():

@@ -345,3 +345,27 @@ def llama_layer(x3d, p, nh, nkv, cos_t, sin_t, eps=1e-5, causal=True, bf16=True,
                     p["bd"], bf16).reshape(B, S, E)
     out = binary(ADD, res, mlp)
     return round_bf16(out) if bf16 else out
+
+
+def deepseek_moe(x2d, shared, routed, wr, br, k):
+    """DeepSeekMoE.forward (src/rew/models/deepseek.nim:114-145) as the
+    mixed-precision op sequence rew_amd.nn emits: bf16 expert FFNs, an fp32
+    router on astype(x), topK, renormalisation, and the dense expert loop
+    out = bf16(out + bf16(f32(E_e(x)) * w_e)) in expert order.
+    shared / routed: lists of (wg, bg, wu, bu, wd, bd) float arrays holding
+    bf16 values.  Returns (out, topk indices, renormalised weights)."""
+    x = np.ascontiguousarray(x2d, np.float32)
+    T, H = x.shape
+    out = gated_ffn(x, *shared[0], True) if shared else np.zeros((T, H), np.float32)
+    for s in shared[1:]:
+        out = round_bf16(binary(ADD, out, gated_ffn(x, *s, True)))
+    probs = softmax_rows(linear(x, wr, br, False))
+    tv, ti = topk_rows(probs, k)
+    denom = reduce(RSUM, tv, [1])
+    tw = binary(DIV, tv, np.ascontiguousarray(np.broadcast_to(denom[:, None], tv.shape)))
+    for e, ex in enumerate(routed):
+        w = reduce(RSUM, binary(MUL, tw, (ti == e).astype(np.float32)), [1])
+        y = gated_ffn(x, *ex, True)
+        contrib = round_bf16(binary(MUL, y, np.ascontiguousarray(np.broadcast_to(w[:, None], y.shape))))
+        out = round_bf16(binary(ADD, out, contrib))
+    return out, ti, tw

@@ -355,8 +355,10 @@ __device__ __forceinline__ void tile_of(int64_t bid, int64_t tiles_m, int64_t ti
 // sharing A; wave column wn holds gate columns n0 + wn*64 + [0, 64) in its
 // accumulator columns j = 0, 1 and the same up-projection columns in
 // j = 2, 3, so the SwiGLU epilogue is lane-local.
-template <bool B_KC, bool DUAL>
-__global__ void __launch_bounds__(256, 1) gemm_bf16_256_kernel(GemmArgs g) {
+// GROUP: grouped mode (see GroupArgs): the tile's group, packed rows and
+// operand pointers come from the group tables instead of the batch index.
+template <bool B_KC, bool DUAL, bool GROUP>
+__global__ void __launch_bounds__(256, 1) gemm_bf16_256_kernel(GemmArgs g, GroupArgs ga) {
   using namespace mf2;
   // operand double buffers; after the main loop the same memory holds the
   // rounded C tile for the epilogue pass
@@ -369,31 +371,72 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_256_kernel(GemmArgs g) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   constexpr int TN = DUAL ? BN / 2 : BN;  // output columns per workgroup
-  const int64_t tiles_m = (g.M + BM - 1) / BM, tiles_n = (g.N + TN - 1) / TN;
-  int64_t b, tm, tn;
-  tile_of(blockIdx.x, tiles_m, tiles_n, g.batch, &b, &tm, &tn);
-  const int64_t m0 = tm * BM, n0 = tn * TN;
-  const int64_t m_rows = min((int64_t)BM, g.M - m0), n_rows = min((int64_t)BN, g.N - n0);
+  const int64_t tiles_n = (g.N + TN - 1) / TN;
+  int64_t b = 0, tm = 0, tn = 0;
+  int64_t m_rows;     // valid rows of the tile
+  int64_t row0;       // C row (dense: of the batch matrix; grouped: packed) of tile row 0
+  int grp = 0;
+  if constexpr (GROUP) {
+    const int64_t total = ga.max_mtiles * tiles_n;
+    int64_t t = blockIdx.x;
+    if (total % 8 == 0) t = (t % 8) * (total / 8) + t / 8;  // XCD-contiguous ranges
+    tm = t / tiles_n;
+    tn = t - tm * tiles_n;
+    if (tm >= ga.mt_start[ga.n_groups]) return;  // past the routed work (uniform)
+    int lo = 0, hi = ga.n_groups - 1;             // last group starting at or before tm
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (ga.mt_start[mid] <= tm) lo = mid;
+      else hi = mid - 1;
+    }
+    grp = lo;
+    row0 = ga.off[grp] + (tm - ga.mt_start[grp]) * BM;
+    m_rows = min((int64_t)BM, (int64_t)ga.off[grp + 1] - row0);
+  } else {
+    const int64_t tiles_m = (g.M + BM - 1) / BM;
+    tile_of(blockIdx.x, tiles_m, tiles_n, g.batch, &b, &tm, &tn);
+    row0 = tm * BM;
+    m_rows = min((int64_t)BM, g.M - row0);
+  }
+  const int64_t n0 = tn * TN;
+  const int64_t n_rows = min((int64_t)BN, g.N - n0);
   const int K = (int)g.K;
+  const bool gather = GROUP && ga.rows != nullptr;
 
-  // A: rows m0 .. m0 + m_rows of the batch, K-contiguous
-  const uint16_t* Ab = (const uint16_t*)g.a + b * g.a_sb + m0 * g.a_sm;
+  // A: rows row0 .. row0 + m_rows (K-contiguous), or the whole token
+  // matrix when the rows are gathered
+  const uint16_t* Ab = gather ? (const uint16_t*)g.a
+                              : (const uint16_t*)g.a + b * g.a_sb + row0 * g.a_sm;
   const __amdgpu_buffer_rsrc_t ra =
-      make_rsrc(Ab, (uint32_t)(((m_rows - 1) * g.a_sm + K) * 2));
+      make_rsrc(Ab, (uint32_t)((((gather ? g.M : m_rows) - 1) * g.a_sm + K) * 2));
   const uint32_t a_sm2 = (uint32_t)(g.a_sm * 2);
   // B: K-contiguous rows n0.. (B_KC) or the whole [K, N] batch matrix
-  const uint16_t* Bb = B_KC ? (const uint16_t*)g.b + b * g.b_sb + n0 * g.b_sn
-                            : (const uint16_t*)g.b + b * g.b_sb;
+  const uint16_t* Bw = GROUP ? (const uint16_t*)ga.b[grp] : (const uint16_t*)g.b + b * g.b_sb;
+  const uint16_t* Bb = B_KC ? Bw + n0 * g.b_sn : Bw;
   const uint32_t b_bytes = B_KC ? (uint32_t)(((n_rows - 1) * g.b_sn + K) * 2)
                                 : (uint32_t)(((g.K - 1) * g.b_sk + g.N) * 2);
   // DUAL: odd waves stage the up-projection weights (wave-uniform choice)
-  const uint16_t* Bsrc = (DUAL && (wave & 1)) ? (const uint16_t*)g.b2 + b * g.b_sb : Bb;
+  const uint16_t* Bw2 = GROUP ? (const uint16_t*)(DUAL ? ga.b2[grp] : nullptr)
+                              : (const uint16_t*)g.b2 + b * g.b_sb;
+  const uint16_t* Bsrc = (DUAL && (wave & 1)) ? Bw2 : Bb;
   const __amdgpu_buffer_rsrc_t rb = make_rsrc(Bsrc, b_bytes);
   const uint32_t b_s2 = (uint32_t)((B_KC ? g.b_sn : g.b_sk) * 2);
 
   // per-lane parts of the staging addresses
   const int row8 = tid >> 3, kc = tid & 7;             // A / B_KC: 16-byte chunk kc of row
   const uint32_t a_voff = row8 * a_sm2 + kc * 16;
+  // gathered A: byte offset of each of the lane's 8 rows (rows past the
+  // tile's extent point past the buffer and read as zeros)
+  uint32_t a_gv[GROUP ? 8 : 1];
+  if constexpr (GROUP) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = row8 + i * 32;
+      a_gv[i] = (gather && r < m_rows)
+                    ? (uint32_t)ga.rows[row0 + r] * a_sm2 + kc * 16
+                    : 0x80000000u;
+    }
+  }
   const int nb = tid >> 3, kb = tid & 7;               // !B_KC: 8x8 block (k-block kb, n-block nb)
   // DUAL: virtual column block nb maps to column n0 + (nb >> 4) * 64 + (nb & 7) * 8
   const int64_t bcol = DUAL ? n0 + (nb >> 4) * 64 + (nb & 7) * 8 : n0 + nb * 8;
@@ -406,9 +449,14 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_256_kernel(GemmArgs g) {
   bool kok_a = true;
   auto load_a = [&](int k0) {
     kok_a = k0 + kc * 8 < K;
+    if (gather) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      rs[i] = bload16(ra, a_voff, (uint32_t)(i * 32) * a_sm2 + (uint32_t)k0 * 2);
+      for (int i = 0; i < 8; ++i) rs[i] = bload16(ra, a_gv[GROUP ? i : 0], (uint32_t)k0 * 2);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        rs[i] = bload16(ra, a_voff, (uint32_t)(i * 32) * a_sm2 + (uint32_t)k0 * 2);
+    }
   };
   auto store_a = [&](int buf) {
     uint16_t* as = As[buf] + row8 * LDK + kc * 8;
@@ -549,14 +597,14 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_256_kernel(GemmArgs g) {
   const int OC = DUAL ? 128 : 256;           // output columns of the tile
   const int CH = OC / 8;                     // 16-byte chunks per row
   uint16_t* C = (uint16_t*)g.c + b * g.c_sb;
-  const uint16_t* bias = (const uint16_t*)g.bias;
-  const uint16_t* bias2 = (const uint16_t*)g.bias2;
+  const uint16_t* bias = (const uint16_t*)(GROUP ? ga.bias[grp] : g.bias);
+  const uint16_t* bias2 = (const uint16_t*)(GROUP ? (DUAL ? ga.bias2[grp] : nullptr) : g.bias2);
   const uint16_t* res = (const uint16_t*)g.res + b * g.res_sb;
   for (int t = tid; t < BM * CH; t += 256) {
     const int row = t / CH, ch = t - row * CH;
-    const int64_t m = m0 + row;
+    const int64_t m = row0 + row;
     const int64_t n = n0 + ch * 8;
-    if (m >= g.M || n >= g.N) continue;
+    if (row >= m_rows || n >= g.N) continue;
     // local column of the value (gate column for DUAL)
     const int lc = DUAL ? (ch >> 3) * 128 + (ch & 7) * 8 : ch * 8;
     const uint4 dv = *(const uint4*)(Cs + row * CP + lc);
@@ -680,16 +728,16 @@ void launch_gemm(const GemmArgs& g, hipStream_t stream) {
   if (g.epi == EPI_SWIGLU) {
     if (!gemm_epilogue_ok(g)) fail(REW_MI355X_ERR_INVALID, "internal: SwiGLU GEMM not launchable");
     const int64_t tiles = ((g.M + 255) / 256) * ((g.N + 127) / 128) * g.batch;
-    hipLaunchKernelGGL((gemm_bf16_256_kernel<false, true>), dim3((unsigned)tiles), dim3(256), 0,
-                       stream, g);
+    hipLaunchKernelGGL((gemm_bf16_256_kernel<false, true, false>), dim3((unsigned)tiles),
+                       dim3(256), 0, stream, g, GroupArgs{});
   } else if (mfma_ok(g, &akc, &bkc) && use_256(g, akc)) {
     const int64_t tiles = ((g.M + 255) / 256) * ((g.N + 255) / 256) * g.batch;
     if (bkc)
-      hipLaunchKernelGGL((gemm_bf16_256_kernel<true, false>), dim3((unsigned)tiles), dim3(256), 0,
-                         stream, g);
+      hipLaunchKernelGGL((gemm_bf16_256_kernel<true, false, false>), dim3((unsigned)tiles),
+                         dim3(256), 0, stream, g, GroupArgs{});
     else
-      hipLaunchKernelGGL((gemm_bf16_256_kernel<false, false>), dim3((unsigned)tiles), dim3(256),
-                         0, stream, g);
+      hipLaunchKernelGGL((gemm_bf16_256_kernel<false, false, false>), dim3((unsigned)tiles),
+                         dim3(256), 0, stream, g, GroupArgs{});
   } else if (mfma_ok(g, &akc, &bkc)) {
     const int64_t tiles = ((g.M + 127) / 128) * ((g.N + 127) / 128) * g.batch;
     const unsigned grid = (unsigned)(tiles < 1 << 20 ? tiles : 1 << 20);
@@ -706,6 +754,31 @@ void launch_gemm(const GemmArgs& g, hipStream_t stream) {
               (unsigned)(g.batch < 65535 ? g.batch : 65535));
     hipLaunchKernelGGL(gemm_generic_kernel, grid, dim3(256), 0, stream, g);
   }
+  REW_HIP(hipGetLastError());
+}
+
+bool gemm_grouped_ok(const GemmArgs& g) {
+  bool akc, bkc;
+  if (!mfma_ok(g, &akc, &bkc) || !akc || bkc || g.batch != 1) return false;
+  if (g.epi != EPI_BIAS && g.epi != EPI_SWIGLU) return false;
+  if (g.c_dtype != REW_DT_BFLOAT16 || g.N % 8 || g.c_sm % 8 || ((uintptr_t)g.c & 15)) return false;
+  const int64_t a_ext = ((g.M - 1) * g.a_sm + g.K) * 2;
+  const int64_t b_ext = ((g.K - 1) * g.b_sk + g.N) * 2;
+  return a_ext < (1ll << 31) && b_ext < (1ll << 31);
+}
+
+void launch_gemm_grouped(const GemmArgs& g, const GroupArgs& ga, hipStream_t stream) {
+  if (ga.n_groups <= 0 || ga.max_mtiles <= 0 || g.N == 0) return;
+  if (!gemm_grouped_ok(g)) fail(REW_MI355X_ERR_INVALID, "internal: grouped GEMM not launchable");
+  const bool dual = g.epi == EPI_SWIGLU;
+  const int64_t tiles = ga.max_mtiles * ((g.N + (dual ? 127 : 255)) / (dual ? 128 : 256));
+  if (tiles >= (1ll << 31)) fail(REW_MI355X_ERR_INVALID, "internal: grouped GEMM grid too large");
+  if (dual)
+    hipLaunchKernelGGL((gemm_bf16_256_kernel<false, true, true>), dim3((unsigned)tiles),
+                       dim3(256), 0, stream, g, ga);
+  else
+    hipLaunchKernelGGL((gemm_bf16_256_kernel<false, false, true>), dim3((unsigned)tiles),
+                       dim3(256), 0, stream, g, ga);
   REW_HIP(hipGetLastError());
 }
 

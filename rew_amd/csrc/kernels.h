@@ -59,6 +59,33 @@ struct GemmArgs {
 };
 enum GemmEpi : int { EPI_NONE = 0, EPI_BIAS = 1, EPI_BIAS_RES = 2, EPI_SWIGLU = 3 };
 void launch_gemm(const GemmArgs& g, hipStream_t stream);
+
+// Grouped GEMM over packed rows (the routed experts of a MoE layer).  Group
+// i owns packed rows [off[i], off[i+1]) and 256-row tiles
+// [mt_start[i], mt_start[i+1]); its B / b2 / bias / bias2 come from the
+// device pointer tables.  Row r of the A operand is A row rows[r] when
+// `rows` is set (a gather from the token matrix), else packed row r.  C is
+// written at its packed row.  The per-element arithmetic is the 256x256
+// kernel's (same MFMA sequence over the same k order), so a group's rows
+// equal the dense GEMM's rows bit for bit.  Fields of GemmArgs keep their
+// meaning except: a = the A matrix (token matrix when gathering) with M its
+// row count; b, b2, bias, bias2 ignored (taken from the tables); c = the
+// packed output with c_sm its row stride.
+struct GroupArgs {
+  const int32_t* off;       // n_groups + 1 (device)
+  const int32_t* mt_start;  // n_groups + 1 (device)
+  const int32_t* rows;      // packed row -> A row, or nullptr
+  int n_groups;
+  int64_t max_mtiles;       // grid bound on mt_start[n_groups]
+  const void* const* b;     // n_groups device pointers each
+  const void* const* b2;
+  const void* const* bias;
+  const void* const* bias2;
+};
+// Whether launch_gemm_grouped can run g (dtype, layout, epilogue, 32-bit
+// buffer extents).
+bool gemm_grouped_ok(const GemmArgs& g);
+void launch_gemm_grouped(const GemmArgs& g, const GroupArgs& ga, hipStream_t stream);
 // Whether launch_gemm runs g with its epilogue (EPI_SWIGLU needs the large
 // dual kernel; the others run on every MFMA kernel).
 bool gemm_epilogue_ok(const GemmArgs& g);
@@ -79,6 +106,65 @@ struct GatherArgs {
   int64_t row_bytes;    // product of operand dims after `dim` * elem size
 };
 void launch_gather(const GatherArgs& g, hipStream_t stream);
+
+// ---- argmax / topK (k_select.hip) ----------------------------------------------
+// argmax over dim n of x viewed as dense [outer, n, inner] f32; out [outer, inner]
+// int32 (lowest index of the maximum; INT32_MAX where the slice holds NaN).
+struct ArgmaxArgs {
+  const float* x;
+  int32_t* out;
+  int64_t outer, n, inner;
+};
+void launch_argmax(const ArgmaxArgs& g, hipStream_t stream);
+
+// topK over the last dim of dense f32 [rows, cols]: vals / idx [rows, k],
+// ranked larger-first (smaller-first when !largest), NaN last, ties to the
+// lower column.  1 <= k <= 64, k <= cols <= kTopkMaxCols.
+constexpr int64_t kTopkMaxCols = 4096;
+struct TopkArgs {
+  const float* x;
+  float* vals;
+  int32_t* idx;
+  int64_t rows, cols;
+  int k;
+  int largest;
+};
+void launch_topk(const TopkArgs& g, hipStream_t stream);
+
+// ---- routed MoE (k_moe.hip) ------------------------------------------------------
+constexpr int kMoeMaxK = 16;  // experts per token the combine handles
+// Token placement for one group of routed experts ("members").
+struct MoeRouteArgs {
+  const int32_t* topi;       // [T, k] expert ids
+  int64_t T;
+  int k;
+  int E;                     // router width: ids are in [0, E)
+  const int32_t* member_of;  // [E] member index or -1 (device)
+  const int32_t* members;    // [n_members] expert id (device)
+  int n_members;
+  int tile_m;                // row tile of the grouped GEMMs
+  int32_t* off;              // [n_members + 1] packed row offsets (out)
+  int32_t* mt_start;         // [n_members + 1] tile starts (out)
+  int32_t* perm;             // [T * k] packed row -> token (out)
+  int32_t* slot_of;          // [T * k] (token, k-slot) -> packed row (out)
+};
+void launch_moe_route(const MoeRouteArgs& a, hipStream_t stream);
+
+// out[t, :] = prev[t, :] then, for token t's routed members in chain order,
+// out = bf16(out + bf16(f32(y[slot, :]) * w)); bf16 rows, H % 8 == 0.
+struct MoeCombineArgs {
+  const uint16_t* prev;
+  int64_t prev_rs;           // row stride of prev (elements)
+  const uint16_t* y;         // [T * k, H] packed expert outputs
+  const float* topw;         // [T, k]
+  const int32_t* topi;       // [T, k]
+  const int32_t* slot_of;    // [T, k]
+  const int32_t* member_of;  // [E]
+  int64_t T, H;
+  int k, E;
+  uint16_t* out;             // dense [T, H]
+};
+void launch_moe_combine(const MoeCombineArgs& a, hipStream_t stream);
 
 // ---- fused attention (k_attn.hip) ---------------------------------------------
 // out[b,h,i,:] = sum_j softmax_j(bf16(q[b,h,i,:].k[b,hk,j,:]) * scale + mask(i,j))

@@ -226,6 +226,27 @@ struct RopePlan {
   Tensor* sin0 = nullptr;
 };
 
+// A run of routed-expert contributions of rew's DeepSeekMoE.forward
+// (src/rew/models/deepseek.nim:122-145) added into one running sum:
+//   out_j = add(out_{j-1}, astype(mul(astype(Y_e, f32),
+//                                     broadcastTo(reshape(w_e, [T, 1]))), bf16))
+// Y_e = downProj(SwiGLU(x)) of routed expert e, w_e = routedWeightForExpert
+// (deepseek.nim:114-120) over the same (topWeights, topIndices).  Lowered to
+// routing + two grouped GEMMs over the routed rows + an ordered combine.
+struct MoeMember {
+  int e = 0;
+  GemmPlan sw;  // SwiGLU dual GEMM of x (gate, up)
+  GemmPlan dn;  // down projection + bias
+};
+struct MoePlan {
+  Tensor* start = nullptr;  // running sum before the first member
+  Tensor* x = nullptr;      // token matrix [T, H] bf16
+  Tensor* topi = nullptr;   // [T, k] int32 (topK indices)
+  Tensor* topw = nullptr;   // [T, k] f32
+  int E = 0;                // router width
+  std::vector<MoeMember> mem;
+};
+
 struct Lower {
   Ctx* c;
   std::vector<Node*> nodes;  // live pending nodes in creation order
@@ -234,8 +255,12 @@ struct Lower {
   std::unordered_map<Tensor*, GemmPlan> gemm_out;  // fused GEMM result -> plan
   std::unordered_map<Tensor*, NormPlan> norm_out;
   std::unordered_map<Tensor*, RopePlan> rope_out;
+  std::unordered_map<Tensor*, MoePlan> moe_out;
 
   explicit Lower(Ctx* ctx) : c(ctx) {}
+
+  void match_moe();
+  bool emit_moe(Tensor* t, const MoePlan& p);
 
   bool match_flash(Node* pv);
   void match_gemm_epilogues();
@@ -822,6 +847,13 @@ void Lower::ensure_mat(Tensor* t) {
     RopePlan rp = rit->second;
     rope_out.erase(rit);
     if (emit_rope(t, rp)) return;
+  }
+  auto mit = moe_out.find(t);
+  if (mit != moe_out.end()) {
+    MoePlan mp = mit->second;
+    moe_out.erase(mit);
+    if (emit_moe(t, mp)) return;
+    throw Error(REW_MI355X_ERR_UNSUPPORTED, "routed MoE chain could not be lowered");
   }
   Node* p = t->prod;
   if (!p) throw Error(REW_MI355X_ERR_INVALID, "internal: tensor has neither data nor producer");
@@ -1677,6 +1709,334 @@ bool Lower::emit_gemm_fused(Tensor* t, const GemmPlan& p) {
 
 
 // ---------------------------------------------------------------------------
+// routed mixture of experts (src/rew/models/deepseek.nim:114-145)
+// ---------------------------------------------------------------------------
+
+// Expert id of broadcastTo(scalarI32(e), shape, []) (ops/literal.nim:191-194).
+static bool const_i32_bcast(Tensor* t, int* val) {
+  if (!t || t->st || !t->prod || t->prod->kind != K_BROADCAST_TO) return false;
+  Tensor* s = t->prod->in[0];
+  if (s->shape.rank != 0 || s->dt != kI32 || !s->has_host) return false;
+  std::memcpy(val, s->host, 4);
+  return true;
+}
+
+// w = reduceSum(mul(TW, astype(compare(TI, broadcastTo(e), EQ), f32)), [1])
+// with TI the index output of a pending topK (distinct ids per row).
+static bool routed_weight(Tensor* w, Tensor** tw, Tensor** ti, int* e,
+                          std::vector<Tensor*>* inner) {
+  Node* rs = chain_node(w, K_REDUCE, 1);
+  if (!rs || rs->sub != RED_SUM || !dims_are(rs->l0, {1}) || w->dt != kF32) return false;
+  Node* mu = chain_node(rs->in[0], K_BINARY, 1);
+  if (!mu || mu->sub != 2) return false;
+  for (int ord = 0; ord < 2; ++ord) {
+    Tensor* TW = mu->in[ord];
+    Node* cv = chain_node(mu->in[1 - ord], K_CONVERT, 1);
+    if (!cv || cv->out[0]->dt != kF32 || cv->in[0]->dt != kBool) continue;
+    Node* cp = chain_node(cv->in[0], K_COMPARE, 1);
+    if (!cp || cp->cmp != 0 /* EQ */) continue;
+    for (int o2 = 0; o2 < 2; ++o2) {
+      Tensor* TI = cp->in[o2];
+      if (!const_i32_bcast(cp->in[1 - o2], e)) continue;
+      if (!TI->prod || TI->prod->kind != K_TOPK || TI->prod->out.size() != 2 ||
+          TI->prod->out[1] != TI || TI->dt != kI32 || TI->shape.rank != 2)
+        continue;
+      if (TW->dt != kF32 || TW->shape != TI->shape) continue;
+      *tw = TW;
+      *ti = TI;
+      for (Tensor* t : {w, rs->in[0], mu->in[1 - ord], cv->in[0], cp->in[1 - o2]})
+        inner->push_back(t);
+      return true;
+    }
+  }
+  return false;
+}
+
+// c = astype(mul(astype(Y, f32), broadcastTo(reshape(w, [T, 1]), [T, H], [0, 1])), bf16)
+// with Y the planned down projection of a planned SwiGLU of x.
+bool match_contribution(Lower& L, Tensor* c, MoeMember* m, Tensor** x, Tensor** ti,
+                        Tensor** tw, std::vector<Tensor*>* inner) {
+  Node* cb = chain_node(c, K_CONVERT, 1);
+  if (!cb || c->dt != kBF16 || cb->in[0]->dt != kF32 || c->shape.rank != 2) return false;
+  Node* mu = chain_node(cb->in[0], K_BINARY, 1);
+  if (!mu || mu->sub != 2) return false;
+  const int64_t T = c->shape.d[0], H = c->shape.d[1];
+  for (int ord = 0; ord < 2; ++ord) {
+    Node* cy = chain_node(mu->in[ord], K_CONVERT, 1);
+    if (!cy || cy->in[0]->dt != kBF16) continue;
+    Tensor* Y = cy->in[0];
+    auto dit = L.gemm_out.find(Y);
+    if (dit == L.gemm_out.end() || dit->second.epi != EPI_BIAS || Y->ext != 0 || Y->uses != 1)
+      continue;
+    Tensor* hb = dit->second.dot->in[0];
+    auto sit = L.gemm_out.find(hb);
+    if (sit == L.gemm_out.end() || sit->second.epi != EPI_SWIGLU || hb->ext != 0 ||
+        hb->uses != 1)
+      continue;
+    Node* bw = chain_node(mu->in[1 - ord], K_BROADCAST_TO, 1);
+    if (!bw || !dims_are(bw->l1, {0, 1})) continue;
+    Node* rw = chain_node(bw->in[0], K_RESHAPE, 1);
+    if (!rw || rw->out[0]->shape.rank != 2 || rw->out[0]->shape.d[0] != T ||
+        rw->out[0]->shape.d[1] != 1)
+      continue;
+    std::vector<Tensor*> in2;
+    int e;
+    if (!routed_weight(rw->in[0], tw, ti, &e, &in2)) continue;
+    Tensor* X = sit->second.dot->in[0];
+    if (X->dt != kBF16 || X->shape.rank != 2 || X->shape.d[0] != T || X->shape.d[1] != H ||
+        (*ti)->shape.d[0] != T || (*ti)->shape.d[1] > kMoeMaxK)
+      continue;
+    m->e = e;
+    m->sw = sit->second;
+    m->dn = dit->second;
+    *x = X;
+    for (Tensor* t : {c, cb->in[0], mu->in[ord], Y, hb, mu->in[1 - ord], bw->in[0]})
+      inner->push_back(t);
+    inner->insert(inner->end(), in2.begin(), in2.end());
+    return true;
+  }
+  return false;
+}
+
+void Lower::match_moe() {
+  // running-sum tensor -> the group whose chain currently ends in it
+  std::unordered_map<Tensor*, MoePlan> open;
+  for (Node* ad : nodes) {
+    if (ad->kind != K_BINARY || ad->sub != 0 || ad->out[0]->dt != kBF16) continue;
+    Tensor* out = ad->out[0];
+    for (int ord = 0; ord < 2; ++ord) {
+      Tensor *prev = ad->in[ord], *c = ad->in[1 - ord];
+      if (prev == c) continue;
+      MoeMember m;
+      Tensor *x, *ti, *tw;
+      std::vector<Tensor*> inner;
+      if (!match_contribution(*this, c, &m, &x, &ti, &tw, &inner)) continue;
+      const Tensor* router = ti->prod->in[0];
+      if (m.e < 0 || m.e >= router->shape.d[router->shape.rank - 1]) continue;
+      MoePlan g;
+      auto it = open.find(prev);
+      bool extend = it != open.end() && prev->ext == 0 && prev->uses == 1 &&
+                    it->second.x == x && it->second.topi == ti && it->second.topw == tw;
+      if (extend)
+        for (const MoeMember& q : it->second.mem)
+          if (q.e == m.e) extend = false;
+      if (extend) {
+        g = std::move(it->second);
+        open.erase(it);
+        prev->plan_mat = false;
+      } else {
+        g.start = prev;
+        g.x = x;
+        g.topi = ti;
+        g.topw = tw;
+        Tensor* src = ti->prod->in[0];
+        g.E = (int)src->shape.d[src->shape.rank - 1];
+      }
+      g.mem.push_back(m);
+      for (Tensor* t : inner) {
+        t->plan_mat = false;
+        gemm_out.erase(t);
+      }
+      out->plan_mat = true;
+      open[out] = std::move(g);
+      break;
+    }
+  }
+  for (auto& kv : open) moe_out[kv.first] = std::move(kv.second);
+}
+
+bool Lower::emit_moe(Tensor* t, const MoePlan& p) {
+  const int n = (int)p.mem.size();
+  ensure_mat(p.start);
+  ensure_mat(p.x);
+  ensure_mat(p.topi);
+  ensure_mat(p.topw);
+  const int64_t T = p.x->shape.d[0], H = p.x->shape.d[1];
+  const int k = (int)p.topi->shape.d[1];
+  const void* xp;
+  int64_t x_rs;
+  rows_view(p.x, H, &xp, &x_rs);
+  const void* sp;
+  int64_t s_rs;
+  rows_view(p.start, H, &sp, &s_rs);
+  if (p.topi->st == nullptr || p.topw->st == nullptr) return false;
+
+  // member weights: gate/up [H, I], down [I, H], dense row-major.  Only the
+  // weights are inspected here: the members' A operands (x and the SwiGLU
+  // outputs) are never materialized densely.
+  auto weight = [&](Tensor* w, int64_t rows, int64_t cols) -> const void* {
+    if (w->dt != kBF16 || w->shape.rank != 2 || w->shape.d[0] != rows || w->shape.d[1] != cols)
+      return nullptr;
+    Tensor* base;
+    int64_t off, st[kMaxRank];
+    operand_strides(w, &base, &off, st);
+    if (st[1] != 1 || st[0] != cols) return nullptr;
+    return (const char*)base->data() + off * 2;
+  };
+  auto vec = [&](Tensor* v, int64_t len) -> const void* {
+    ensure_mat(v);
+    if (v->dt != kBF16 || v->numel() != len || !v->st) return nullptr;
+    return v->data();
+  };
+  const int64_t I = p.mem[0].sw.dot->in[1]->shape.d[1];
+  std::vector<uint64_t> ptrs(6 * (size_t)n);
+  for (int i = 0; i < n; ++i) {
+    const MoeMember& m = p.mem[i];
+    const void* q[6] = {weight(m.sw.dot->in[1], H, I), weight(m.sw.dot2->in[1], H, I),
+                        vec(m.sw.bias, I), vec(m.sw.bias2, I),
+                        weight(m.dn.dot->in[1], I, H), vec(m.dn.bias, H)};
+    for (int j = 0; j < 6; ++j) {
+      if (!q[j] || ((uintptr_t)q[j] & 15)) return false;
+      ptrs[(size_t)j * n + i] = (uint64_t)(uintptr_t)q[j];
+    }
+  }
+  GemmArgs gs{}, gd{};
+  for (GemmArgs* g : {&gs, &gd}) {
+    g->dtype = kBF16;
+    g->c_dtype = kBF16;
+    g->batch = 1;
+    g->a_sk = 1;
+    g->b_sn = 1;
+  }
+  gs.K = H;
+  gs.N = I;
+  gs.b_sk = I;
+  gd.K = I;
+  gd.N = H;
+  gd.b_sk = H;
+  const int64_t R = T * k;  // routed rows (upper bound of the packed rows)
+  const int64_t max_mt = (R + 255) / 256 + n;
+
+  // host tables: member_of[E], members[n] (int32) then the 6 pointer tables
+  std::vector<int32_t> member_of(p.E, -1), members(n);
+  for (int i = 0; i < n; ++i) {
+    members[i] = p.mem[i].e;
+    member_of[p.mem[i].e] = i;
+  }
+  const size_t i32_bytes = ((size_t)(p.E + n) * 4 + 255) & ~(size_t)255;
+  const size_t meta_bytes = i32_bytes + ptrs.size() * 8;
+  std::vector<uint8_t> host(meta_bytes, 0);
+  std::memcpy(host.data(), member_of.data(), (size_t)p.E * 4);
+  std::memcpy(host.data() + (size_t)p.E * 4, members.data(), (size_t)n * 4);
+  std::memcpy(host.data() + i32_bytes, ptrs.data(), ptrs.size() * 8);
+
+  auto temp = [&](int dt, int64_t elems) {
+    Shape s;
+    s.rank = 1;
+    s.d[0] = elems;
+    Tensor* x = new_tensor(c, dt, s);
+    x->plan_dead = true;
+    tensor_alloc(x);
+    return x;
+  };
+  Tensor* meta = temp(kU8, (int64_t)meta_bytes);
+  Tensor* route = temp(kI32, 2 * (n + 1) + 2 * R);
+  Tensor* hbuf = temp(kBF16, R * I);
+  Tensor* ybuf = temp(kBF16, R * H);
+  upload_async(c, meta->data(), host.data(), meta_bytes);
+  const uint8_t* mb = (const uint8_t*)meta->data();
+  int32_t* rb = (int32_t*)route->data();
+
+  MoeRouteArgs ra;
+  ra.topi = (const int32_t*)p.topi->data();
+  ra.T = T;
+  ra.k = k;
+  ra.E = p.E;
+  ra.member_of = (const int32_t*)mb;
+  ra.members = (const int32_t*)mb + p.E;
+  ra.n_members = n;
+  ra.tile_m = 256;
+  ra.off = rb;
+  ra.mt_start = rb + (n + 1);
+  ra.perm = rb + 2 * (n + 1);
+  ra.slot_of = rb + 2 * (n + 1) + R;
+  prof_begin(c, "moe_route{" + std::to_string(T) + "x" + std::to_string(k) + ",E" +
+                    std::to_string(n) + "}");
+  launch_moe_route(ra, c->stream);
+  prof_end(c);
+  note_launch(c, true);
+
+  const void* const* tbl = (const void* const*)(mb + i32_bytes);
+  GroupArgs ga;
+  ga.off = ra.off;
+  ga.mt_start = ra.mt_start;
+  ga.n_groups = n;
+  ga.max_mtiles = max_mt;
+  // gate/up: rows gathered from x through the routing permutation
+  gs.a = xp;
+  gs.M = T;
+  gs.a_sm = x_rs;
+  gs.a_sk = 1;
+  gs.a_sb = 0;
+  gs.epi = EPI_SWIGLU;
+  gs.c = hbuf->data();
+  gs.c_sm = I;
+  gs.c_sb = 0;
+  gs.c_dtype = kBF16;
+  ga.rows = ra.perm;
+  ga.b = tbl;
+  ga.b2 = tbl + n;
+  ga.bias = tbl + 2 * n;
+  ga.bias2 = tbl + 3 * n;
+  gd.a = hbuf->data();
+  gd.M = R;
+  gd.a_sm = I;
+  gd.a_sk = 1;
+  gd.a_sb = 0;
+  gd.epi = EPI_BIAS;
+  gd.c = ybuf->data();
+  gd.c_sm = H;
+  gd.c_sb = 0;
+  gd.c_dtype = kBF16;
+  if (!gemm_grouped_ok(gs) || !gemm_grouped_ok(gd))
+    throw Error(REW_MI355X_ERR_UNSUPPORTED, "routed MoE: expert GEMM layout not supported");
+  if (c->profiling) {
+    char nm[160];
+    std::snprintf(nm, sizeof nm, "moe_gemm_swiglu[%lld,%lld,%lld,%lld]", (long long)n,
+                  (long long)R, (long long)I, (long long)H);
+    prof_begin(c, nm);
+  }
+  launch_gemm_grouped(gs, ga, c->stream);
+  prof_end(c);
+  note_launch(c, true);
+  ga.rows = nullptr;
+  ga.b = tbl + 4 * n;
+  ga.b2 = nullptr;
+  ga.bias = tbl + 5 * n;
+  ga.bias2 = nullptr;
+  if (c->profiling) {
+    char nm[160];
+    std::snprintf(nm, sizeof nm, "moe_gemm_down[%lld,%lld,%lld,%lld]", (long long)n,
+                  (long long)R, (long long)H, (long long)I);
+    prof_begin(c, nm);
+  }
+  launch_gemm_grouped(gd, ga, c->stream);
+  prof_end(c);
+  note_launch(c, true);
+
+  tensor_alloc(t);
+  MoeCombineArgs ca;
+  ca.prev = (const uint16_t*)sp;
+  ca.prev_rs = s_rs;
+  ca.y = (const uint16_t*)ybuf->data();
+  ca.topw = (const float*)p.topw->data();
+  ca.topi = ra.topi;
+  ca.slot_of = ra.slot_of;
+  ca.member_of = ra.member_of;
+  ca.T = T;
+  ca.H = H;
+  ca.k = k;
+  ca.E = p.E;
+  ca.out = (uint16_t*)t->data();
+  prof_begin(c, "moe_combine{" + std::to_string(T) + "x" + std::to_string(H) + "}");
+  launch_moe_combine(ca, c->stream);
+  prof_end(c);
+  note_launch(c, true);
+  for (Tensor* x : {meta, route, hbuf, ybuf}) maybe_destroy(x);
+  return true;
+}
+
+// ---------------------------------------------------------------------------
 // row composites: rmsNorm and RoPE chains as single kernels
 // ---------------------------------------------------------------------------
 
@@ -1943,11 +2303,51 @@ void Lower::emit_gather(Node* n) {
   note_launch(c, false);
 }
 
+// argmax (src/rew/ops/reduce.nim:202-225 semantics) over any dim of a dense
+// f32 operand.
 void Lower::emit_argmax(Node* n) {
-  throw Error(REW_MI355X_ERR_UNSUPPORTED, "argmax lowering not built yet");
+  Tensor *x = n->in[0], *out = n->out[0];
+  ensure_mat(x);
+  tensor_alloc(out);
+  ArgmaxArgs g;
+  g.x = (const float*)x->data();
+  g.out = (int32_t*)out->data();
+  const int dim = (int)n->i0;
+  g.outer = 1;
+  g.inner = 1;
+  for (int i = 0; i < dim; ++i) g.outer *= x->shape.d[i];
+  for (int i = dim + 1; i < x->shape.rank; ++i) g.inner *= x->shape.d[i];
+  g.n = x->shape.d[dim];
+  if (g.n > INT32_MAX) throw Error(REW_MI355X_ERR_UNSUPPORTED, "argmax: dimension above 2^31");
+  prof_begin(c, "argmax{" + std::to_string(g.outer) + "x" + std::to_string(g.n) + "x" +
+                    std::to_string(g.inner) + "}");
+  launch_argmax(g, c->stream);
+  prof_end(c);
+  note_launch(c, false);
 }
+
+// topK over the last dim (src/rew/ops/sort.nim:36-90 semantics).
 void Lower::emit_topk(Node* n) {
-  throw Error(REW_MI355X_ERR_UNSUPPORTED, "topK lowering not built yet");
+  Tensor *x = n->in[0], *vals = n->out[0], *idx = n->out[1];
+  ensure_mat(x);
+  tensor_alloc(vals);
+  tensor_alloc(idx);
+  TopkArgs g;
+  g.x = (const float*)x->data();
+  g.vals = (float*)vals->data();
+  g.idx = (int32_t*)idx->data();
+  g.cols = x->shape.d[x->shape.rank - 1];
+  g.rows = g.cols ? x->numel() / g.cols : 0;
+  g.k = (int)n->i0;
+  g.largest = (int)n->i2;
+  if (g.cols > kTopkMaxCols)
+    throw Error(REW_MI355X_ERR_UNSUPPORTED,
+                "eager 'topK': last dimension above " + std::to_string(kTopkMaxCols));
+  prof_begin(c, "topk{" + std::to_string(g.rows) + "x" + std::to_string(g.cols) + ",k" +
+                    std::to_string(g.k) + "}");
+  launch_topk(g, c->stream);
+  prof_end(c);
+  note_launch(c, false);
 }
 
 // ---------------------------------------------------------------------------
@@ -2027,6 +2427,7 @@ void flush(Ctx* c) {
       if (n->kind == K_DOT_GENERAL) L.match_flash(n);
     L.cons = consumers;
     L.match_gemm_epilogues();
+    L.match_moe();
     L.match_rows();
   }
 

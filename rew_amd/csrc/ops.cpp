@@ -523,6 +523,8 @@ std::vector<Tensor*> record_op(Ctx* c, const std::string& op,
         if (n->i0 <= 0 || n->i0 > is.d[n->i1])
           invalid("eager 'topK': k out of range");
         if (n->i0 > 64) fail(REW_MI355X_ERR_UNSUPPORTED, "eager 'topK': k > 64");
+        if (is.d[n->i1] > kTopkMaxCols)
+          fail(REW_MI355X_ERR_UNSUPPORTED, "eager 'topK': last dimension above 4096");
         if (ins[0]->dt != kF32) invalid("eager 'topK': float32 operand required");
         Shape s = is;
         s.d[n->i1] = n->i0;

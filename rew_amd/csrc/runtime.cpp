@@ -222,6 +222,8 @@ static void h2d(Ctx* c, void* dst, const void* src, size_t bytes) {
   REW_HIP(hipStreamSynchronize(c->stream));
 }
 
+void upload_async(Ctx* c, void* dst, const void* src, size_t bytes) { h2d(c, dst, src, bytes); }
+
 }  // namespace rew
 
 using namespace rew;

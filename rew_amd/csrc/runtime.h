@@ -123,6 +123,10 @@ void tensor_drop_storage(Tensor* t);
 void maybe_destroy(Tensor* t);                // free when unreferenced
 bool tensor_is_live_handle(const Tensor* t);
 
+// Stream-ordered copy of a small host table into device memory (through
+// the pinned staging ring; `src` may be reused as soon as this returns).
+void upload_async(Ctx* c, void* dst, const void* src, size_t bytes);
+
 // Launch bracketing for profiling: call before/after each kernel launch.
 void prof_begin(Ctx* c, const std::string& name);
 void prof_end(Ctx* c);

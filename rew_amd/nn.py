@@ -386,10 +386,14 @@ class DeepSeekMoE:
         topWeights = O.divide(topW, O.broadcastTo(denom, topW.shape, [0]))
         return topWeights, topI
 
-    def forward_dense(self, hiddenFlat: Tensor) -> Tensor:
-        """The reference formulation: every routed expert on every token,
-        weighted by its (mostly zero) routing weight (deepseek.nim:122-145)."""
-        out = self.sharedExperts[0].forward(hiddenFlat) if self.sharedExperts else None
+    def forward(self, hiddenFlat: Tensor) -> Tensor:
+        """DeepSeekMoE.forward (deepseek.nim:122-145): shared experts, then every
+        routed expert on every token weighted by its (mostly zero) routing
+        weight, added in expert order.  The backend recognises the chain and
+        evaluates each expert only on its routed tokens (exactly the same sum:
+        every skipped term is an exact zero)."""
+        out = (self.sharedExperts[0].forward(hiddenFlat) if self.sharedExperts
+               else O.zerosLike(hiddenFlat))
         for e in self.sharedExperts[1:]:
             out = O.add(out, e.forward(hiddenFlat))
         topWeights, topI = self.route(hiddenFlat)
@@ -398,5 +402,7 @@ class DeepSeekMoE:
             wB = O.broadcastTo(O.unsqueeze(w, 1), list(hiddenFlat.shape), [0, 1])
             y = _f32(e.forward(hiddenFlat))
             contrib = _to(O.mul(y, wB), hiddenFlat.dtype)
-            out = contrib if out is None else O.add(out, contrib)
+            out = O.add(out, contrib)
         return out
+
+    forward_dense = forward

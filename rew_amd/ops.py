@@ -65,6 +65,20 @@ def constantF32(shape: Sequence[int], data, device: Device | None = None) -> Ten
     return fromHost(a, DType.FLOAT32, shape, device)
 
 
+def zeros(shape: Sequence[int], dtype: DType = DType.FLOAT32,
+          device: Device | None = None) -> Tensor:
+    """A zero scalar constant broadcast to `shape` (src/rew/ops/factory.nim:17-24)."""
+    scalar = constant(dtype, [], np.zeros(1, np.float32), device)
+    if len(shape) == 0:
+        return scalar
+    return broadcastTo(scalar, list(shape), [])
+
+
+def zerosLike(t: Tensor, dtype: DType | None = None) -> Tensor:
+    """src/rew/ops/factory.nim:26-28."""
+    return zeros(t.shape, t.dtype if dtype is None else dtype, t.device)
+
+
 # ---- elementwise (src/rew/ops/arith.nim, unary.nim) ---------------------------------
 
 def _binary(name):

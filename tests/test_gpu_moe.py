@@ -1,0 +1,113 @@
+"""GPU parity of the routed MoE path (config C5 shape family).
+
+rew's DeepSeekMoE.forward (src/rew/models/deepseek.nim:114-145) is a dense
+formulation: every routed expert runs on every token and is added in expert
+order with a routing weight that is zero off the token's top-k.  The backend
+recognises that op chain and evaluates it sparsely (routing, grouped
+SwiGLU / down GEMMs over the routed rows, ordered combine).  Checks:
+
+* against the oracle's dense restatement: bf16 layer tolerance (normwise
+  relative error <= 2e-2); expert ids bit-exact except where the oracle's
+  router probabilities hold a near-tie at the selection boundary;
+* against the backend's own op-by-op (dense, unfused) execution of the same
+  op sequence: equal values (the skipped terms are exact zeros and the
+  kernels share one MFMA accumulation order);
+* that the sparse kernels really ran (profile names).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+from rew_amd import eager as E
+from rew_amd import nn, rng
+from rew_amd import ops as O
+from rew_amd.eager import DType
+
+
+def build_moe(oracle, T, H, I, E_, k, n_shared, seed):
+    keys = rng.split(rng.initKey(seed), 3 + n_shared + E_)
+    x = oracle.round_bf16(rng.normalF32(keys[0], T * H).reshape(T, H))
+    wr = rng.normalF32(keys[1], H * E_, 0.0, 0.02).reshape(H, E_)
+    br = np.zeros(E_, np.float32)
+
+    def expert(key):
+        ks = rng.split(key, 3)
+        ws = [oracle.round_bf16(rng.normalF32(ks[i], fi * fo, 0.0, 0.02).reshape(fi, fo))
+              for i, (fi, fo) in enumerate([(H, I), (H, I), (I, H)])]
+        zI, zH = np.zeros(I, np.float32), np.zeros(H, np.float32)
+        host = (ws[0], zI, ws[1], zI, ws[2], zH)
+        dev = nn.DeepSeekExpert(*[nn.Linear(E.fromHost(w, DType.BFLOAT16),
+                                            E.fromHost(b, DType.BFLOAT16))
+                                  for w, b in [(ws[0], zI), (ws[1], zI), (ws[2], zH)]])
+        return host, dev
+
+    shared = [expert(keys[3 + i]) for i in range(n_shared)]
+    routed = [expert(keys[3 + n_shared + e]) for e in range(E_)]
+    moe = nn.DeepSeekMoE(nn.Linear(E.fromHost(wr), E.fromHost(br)),
+                         [d for _, d in shared], [d for _, d in routed], k)
+    host = dict(x=x, wr=wr, br=br, shared=[h for h, _ in shared],
+                routed=[h for h, _ in routed])
+    return moe, host
+
+
+def ids_match_off_near_ties(oracle, host, k, got_ids, probs_tol=1e-6):
+    """Expert ids must equal the oracle's except on rows whose router
+    probabilities have a near-tie at or above the k-th place."""
+    x = host["x"]
+    probs = oracle.softmax_rows(oracle.linear(x, host["wr"], host["br"], False))
+    _, want = oracle.topk_rows(probs, k)
+    srt = -np.sort(-probs, axis=1)
+    gaps = srt[:, :k] - srt[:, 1:k + 1]
+    near = np.any(gaps <= probs_tol * srt[:, :1], axis=1)
+    bad = np.any(got_ids != want, axis=1) & ~near
+    assert not bad.any(), f"expert ids differ off near-ties in rows {np.where(bad)[0][:10]}"
+    return int(near.sum())
+
+
+@pytest.mark.parametrize("T,H,I,E_,k,n_shared", [(256, 256, 128, 16, 4, 2),
+                                                  (200, 264, 136, 8, 2, 1),
+                                                  (32, 128, 64, 64, 2, 2)])
+def test_moe_matches_oracle(gpu, oracle, T, H, I, E_, k, n_shared):
+    moe, host = build_moe(oracle, T, H, I, E_, k, n_shared, 0x5EED0005 + T)
+    xt = E.fromHost(host["x"], DType.BFLOAT16)
+    E.profileBegin()
+    out = E.toHostF32(moe.forward(xt))
+    prof = [name for name, _, _ in E.profileEnd()]
+    assert any(n.startswith("moe_gemm_swiglu") for n in prof), prof
+    assert any(n.startswith("moe_combine") for n in prof), prof
+    want, ti, tw = oracle.deepseek_moe(host["x"], host["shared"], host["routed"], host["wr"],
+                                       host["br"], k)
+    err = np.linalg.norm(out - want) / np.linalg.norm(want)
+    assert err <= 2e-2, f"normwise relative error {err:.3e}"
+    _, got_ids = moe.route(xt)
+    ids_match_off_near_ties(oracle, host, k, E.toHost(got_ids))
+
+
+def test_moe_sparse_equals_dense_op_by_op(gpu, oracle):
+    moe, host = build_moe(oracle, 256, 256, 128, 16, 4, 2, 0x5EED0105)
+    xt = E.fromHost(host["x"], DType.BFLOAT16)
+    sparse = E.toHostF32(moe.forward(xt))
+    E.setMode(1)
+    try:
+        dense = E.toHostF32(moe.forward(xt))
+    finally:
+        E.setMode(0)
+    # equal values (an exact zero's sign may differ: dense adds +-0 terms)
+    np.testing.assert_array_equal(sparse, dense)
+
+
+def test_moe_routing_weights(gpu, oracle):
+    """topK + renormalisation of the router (deepseek.nim:132-137): the
+    renormalised weights sum to 1 per token and every id is distinct."""
+    keys = rng.split(rng.initKey(0x5EED0205), 2)
+    T, H, E_ = 512, 128, 64
+    x = oracle.round_bf16(rng.normalF32(keys[0], T * H).reshape(T, H))
+    wr = rng.normalF32(keys[1], H * E_, 0.0, 0.02).reshape(H, E_)
+    router = nn.Linear(E.fromHost(wr), E.fromHost(np.zeros(E_, np.float32)))
+    m = nn.DeepSeekMoE(router, [], [], 6)
+    tw, ti = m.route(E.fromHost(x, DType.BFLOAT16))
+    tw, ti = E.toHost(tw), E.toHost(ti)
+    np.testing.assert_allclose(tw.sum(1), 1.0, rtol=1e-6)
+    assert all(len(set(r)) == 6 for r in ti)
+    assert np.all(np.diff(tw, axis=1) <= 0)
