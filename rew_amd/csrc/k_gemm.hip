@@ -10,6 +10,7 @@
 //   current tile feeds the MFMAs.
 // gemm_generic: any dtype / strides, 64x64x16 LDS tiles, fp32 accumulation.
 #include <cstdlib>
+#include <string>
 
 #include "kernels.h"
 #include "vm_device.h"
@@ -670,12 +671,26 @@ static bool mfma_ok(const GemmArgs& g, bool* a_kc, bool* b_kc) {
 // 256 CUs at least once; smaller problems run the 128x128 kernel.
 // REW_MI355X_GEMM_TILE=256 / 128 forces a kernel (tests use it to cover
 // the large-tile kernel's tails at small sizes); unset picks by size.
+// REW_MI355X_GEMM_TILE: "lds" (the direct-to-LDS kernels), "256" or "128".
 static int forced_tile() {
   static const int v = [] {
     const char* s = std::getenv("REW_MI355X_GEMM_TILE");
+    if (s && std::string(s) == "lds") return 1;
     return s ? std::atoi(s) : 0;
   }();
   return v;
+}
+
+// The direct-to-LDS kernels run every bf16 GEMM they support once it has
+// enough 256x256 tiles to occupy most of the 256 CUs (or when forced).
+static bool use_lds(const GemmArgs& g) {
+  bool bkc;
+  const int f = forced_tile();
+  if (f == 128 || f == 256 || !gemm_lds_ok(g, &bkc)) return false;
+  const bool dual = g.epi == EPI_SWIGLU;
+  const int64_t tiles = ((g.M + 255) / 256) * ((g.N + (dual ? 127 : 255)) / (dual ? 128 : 256)) *
+                        g.batch;
+  return f == 1 || tiles >= 96;
 }
 
 // The epilogue pass of the 256 kernels writes 16-byte chunks of bf16 rows.
@@ -704,6 +719,8 @@ bool gemm_epilogue_ok(const GemmArgs& g) {
   if (g.epi == EPI_NONE) return true;
   if (g.c_dtype != REW_DT_BFLOAT16 && g.c_dtype != REW_DT_FLOAT32) return false;
   if (g.epi != EPI_SWIGLU) return true;
+  bool lkc;
+  if (gemm_lds_ok(g, &lkc)) return true;
   bool akc, bkc;
   if (!mfma_ok(g, &akc, &bkc) || !akc || bkc || !epi256_ok(g)) return false;
   const int64_t a_ext = (256 * g.a_sm + g.K) * 2;
@@ -713,6 +730,10 @@ bool gemm_epilogue_ok(const GemmArgs& g) {
 
 const char* gemm_variant(const GemmArgs& g) {
   bool akc, bkc;
+  if (use_lds(g)) {
+    gemm_lds_ok(g, &bkc);
+    return g.epi == EPI_SWIGLU ? "gemm_lds_swiglu" : (bkc ? "gemm_lds_tn" : "gemm_lds_nn");
+  }
   if (g.epi == EPI_SWIGLU) return "gemm_bf16_256_swiglu";
   if (!mfma_ok(g, &akc, &bkc)) return "gemm_generic";
   if (use_256(g, akc)) return bkc ? "gemm_bf16_256_tn" : "gemm_bf16_256_nn";
@@ -725,6 +746,10 @@ const char* gemm_variant(const GemmArgs& g) {
 void launch_gemm(const GemmArgs& g, hipStream_t stream) {
   if (g.M == 0 || g.N == 0 || g.batch == 0) return;
   bool akc, bkc;
+  if (use_lds(g)) {
+    launch_gemm_lds(g, nullptr, stream);
+    return;
+  }
   if (g.epi == EPI_SWIGLU) {
     if (!gemm_epilogue_ok(g)) fail(REW_MI355X_ERR_INVALID, "internal: SwiGLU GEMM not launchable");
     const int64_t tiles = ((g.M + 255) / 256) * ((g.N + 127) / 128) * g.batch;
@@ -758,6 +783,10 @@ void launch_gemm(const GemmArgs& g, hipStream_t stream) {
 }
 
 bool gemm_grouped_ok(const GemmArgs& g) {
+  bool lkc;
+  if (forced_tile() != 256 && gemm_lds_ok(g, &lkc) && g.batch == 1 &&
+      (g.epi == EPI_BIAS || g.epi == EPI_SWIGLU))
+    return true;
   bool akc, bkc;
   if (!mfma_ok(g, &akc, &bkc) || !akc || bkc || g.batch != 1) return false;
   if (g.epi != EPI_BIAS && g.epi != EPI_SWIGLU) return false;
@@ -770,6 +799,11 @@ bool gemm_grouped_ok(const GemmArgs& g) {
 void launch_gemm_grouped(const GemmArgs& g, const GroupArgs& ga, hipStream_t stream) {
   if (ga.n_groups <= 0 || ga.max_mtiles <= 0 || g.N == 0) return;
   if (!gemm_grouped_ok(g)) fail(REW_MI355X_ERR_INVALID, "internal: grouped GEMM not launchable");
+  bool lkc;
+  if (forced_tile() != 256 && gemm_lds_ok(g, &lkc)) {
+    launch_gemm_lds(g, &ga, stream);
+    return;
+  }
   const bool dual = g.epi == EPI_SWIGLU;
   const int64_t tiles = ga.max_mtiles * ((g.N + (dual ? 127 : 255)) / (dual ? 128 : 256));
   if (tiles >= (1ll << 31)) fail(REW_MI355X_ERR_INVALID, "internal: grouped GEMM grid too large");

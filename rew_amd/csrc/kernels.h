@@ -86,6 +86,12 @@ struct GroupArgs {
 // buffer extents).
 bool gemm_grouped_ok(const GemmArgs& g);
 void launch_gemm_grouped(const GemmArgs& g, const GroupArgs& ga, hipStream_t stream);
+
+// The direct-to-LDS 256x256 kernels (k_gemm_lds.hip): bf16 in / out, any
+// epilogue; *b_kc reports whether B is K-contiguous.  `ga` non-null runs
+// the grouped mode.
+bool gemm_lds_ok(const GemmArgs& g, bool* b_kc);
+void launch_gemm_lds(const GemmArgs& g, const GroupArgs* ga, hipStream_t stream);
 // Whether launch_gemm runs g with its epilogue (EPI_SWIGLU needs the large
 // dual kernel; the others run on every MFMA kernel).
 bool gemm_epilogue_ok(const GemmArgs& g);

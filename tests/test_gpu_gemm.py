@@ -57,10 +57,12 @@ SHAPES = [  # M, K, N, B given transposed
     (1024, 1000, 256, 0),
     (256, 64, 256, 1),
     (40, 136, 1032, 0),
+    (300, 1000, 520, 1),   # K tail (1000 % 64) with B K-contiguous
+    (513, 4104, 1024, 0),  # K tail, M tail, several k-tiles
 ]
 
 
-@pytest.mark.parametrize("tile", ["256", "128"])
+@pytest.mark.parametrize("tile", ["lds", "256", "128"])
 def test_gemm_tiles_match_oracle(gpu, oracle, tile):
     env = dict(os.environ, REW_MI355X_GEMM_TILE=tile)
     r = subprocess.run([sys.executable, "-c", CHILD, str(ROOT),
@@ -69,7 +71,7 @@ def test_gemm_tiles_match_oracle(gpu, oracle, tile):
     assert r.returncode == 0, r.stderr[-3000:]
     res = json.loads(r.stdout.strip().splitlines()[-1])
     for item in res:
-        assert any(k.startswith(f"gemm_bf16_{tile}" if tile == "256" else "gemm_bf16_mfma")
-                   for k in item["kernels"]), item
+        prefix = {"lds": "gemm_lds", "256": "gemm_bf16_256", "128": "gemm_bf16_mfma"}[tile]
+        assert any(k.startswith(prefix) for k in item["kernels"]), item
         assert item["err"] <= 2e-2, item
         assert item["worst"] <= 0.0, item
