@@ -9,29 +9,46 @@
 // (kv head = h / (H / Hkv)), not a copy.
 //
 // Per workgroup: 4 waves, 128 queries of one (b, h); each wave owns 32
-// queries.  Key tiles of 64 are staged in LDS (double-buffered through
-// registers).  The wave computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16,
+// queries.  Key tiles of 64 keys stream HBM/L2 -> LDS by DMA
+// (global_load_lds_dwordx4), two stages, so neither K nor V passes through
+// registers.  The wave computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16,
 // so every lane holds the scores of ONE query column: the row max / sum of
 // the online softmax are lane-local plus one exchange with lane ^ 32.  The
 // output is accumulated transposed, O^T = V^T P^T: the probabilities go
-// straight from the S^T accumulators into the B operand, and V is written
-// into LDS transposed with the key order permuted to match the accumulator
-// row order (bits 2 and 3 of the key index swapped inside each 16-key
-// group), so every operand fragment is one 16-byte LDS read.
+// straight from the S^T accumulators into the B operand.
+//
+// LDS layouts (64 keys x D, 16-byte chunks, XOR-swizzled through the DMA
+// source addresses):
+//   K: chunk c of key row r at physical chunk c ^ (r % (D/8)) -- ds_read_b128
+//      fragments (32 keys x one d-chunk) spread over the bank slots;
+//   V: row-major, chunk c of key row r at c ^ (4 (r % 4)), read with
+//      ds_read_b64_tr_b16: in each 16-lane group source lane s points at key
+//      row kb + s/4, d columns d0 + 4 (s % 4), and output lane i receives 4
+//      consecutive keys of d-column d0 + i.  Two such reads give the 8 keys
+//      of a lane's P fragment, in the order the S^T accumulator holds them
+//      (keys 4g..4g+3 and 8+4g..8+4g+3 of each 16-key step), so V needs no
+//      transpose or permutation in registers.
 //
 // Numerics: fp32 accumulation; scores rounded to bf16 (the dot_general
 // result dtype) before the fp32 scale / mask; probabilities rounded to bf16
 // before the PV product (the astype before the second dot_general); the
 // output rounded to bf16 once.  The softmax normalisation is applied at the
 // end (online softmax), which differs from the two-pass op sequence only in
-// rounding.
+// rounding.  On key tiles where the mask adds exactly 0 everywhere and the
+// scale is positive, exp(x * scale - m) is evaluated as
+// exp2(x * (scale log2 e) - m log2 e) with one FMA.
 #include "kernels.h"
 #include "vm_device.h"
 
 namespace rew {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s lds_v4s;
+typedef __attribute__((address_space(3))) void lds_void;
 
 namespace fa {
 constexpr int BQ = 128;  // queries per workgroup
@@ -50,28 +67,44 @@ __device__ __forceinline__ bool fa_visible(int cmp, int i, int j) {
   }
 }
 
-// Row-order position of key w (0..15) inside a 16-key group of the V^T tile.
-__device__ __forceinline__ int fa_perm16(int w) {
-  return (w & 3) | (((w >> 2) & 1) << 3) | (((w >> 3) & 1) << 2);
+// Every (query, key) pair of queries [q0, q1] x keys [k0, k1] (inclusive)
+// satisfies cmp; only the ordered predicates can be decided from corners.
+__device__ __forceinline__ bool fa_all_visible(int cmp, int q0, int q1, int k0, int k1) {
+  switch (cmp) {
+    case vm::CMP_LE: return q1 <= k0;
+    case vm::CMP_LT: return q1 < k0;
+    case vm::CMP_GE: return q0 >= k1;
+    case vm::CMP_GT: return q0 > k1;
+    default: return false;
+  }
 }
 
-__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  return (uint32_t)vm::bf16_bits(a) | ((uint32_t)vm::bf16_bits(b) << 16);
+// Two fp32 values rounded to bf16 (RNE; v_cvt_pk_bf16_f32), packed.
+__device__ __forceinline__ uint32_t cvt_bf16x2(float a, float b) {
+  const bf16x2_t v = __builtin_convertvector((f32x2_t){a, b}, bf16x2_t);
+  uint32_t u;
+  __builtin_memcpy(&u, &v, 4);
+  return u;
+}
+
+__device__ __forceinline__ void dma16(const void* src, uint16_t* lds) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void*)lds, 16, 0, 0);
 }
 
 template <int D>
 __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(FlashArgs a) {
   using namespace fa;
-  constexpr int KP = D + 8;     // K tile row pitch (elements)
-  constexpr int VP = BKV + 8;   // V^T tile row pitch (elements)
-  constexpr int NT = D / 16;    // MFMA k-steps of Q K^T
-  constexpr int DT = D / 32;    // 32-row d tiles of O^T
-  constexpr int KCH = BKV * D / 8;          // 16-byte chunks of a K tile
-  constexpr int KPT = (KCH + 255) / 256;    // per thread
-  constexpr int VG = (D / 8) * (BKV / 4);   // 4-key x 8-d groups of a V tile
-  constexpr int VPT = (VG + 255) / 256;     // per thread
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BKV * KP];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[2][D * VP];
+  constexpr int CPR = D / 8;                       // 16-byte chunks per key row
+  constexpr int NT = D / 16;                       // MFMA k-steps of Q K^T
+  constexpr int DT = D / 32;                       // 32-row d tiles of O^T
+  constexpr int TILE = BKV * D;                    // elements of a K or V tile
+  constexpr int ROWS_PER_DMA = 64 / CPR;           // key rows per 1 KiB DMA instruction
+  constexpr int DMA_PER_WAVE = (TILE / 512) / 4;   // instructions per wave per tile
+  static_assert(CPR >= 4 && CPR <= 16 && DMA_PER_WAVE >= 1, "head dim 32..128");
+  __shared__ __attribute__((aligned(1024))) uint16_t Ks0[TILE];
+  __shared__ __attribute__((aligned(1024))) uint16_t Ks1[TILE];
+  __shared__ __attribute__((aligned(1024))) uint16_t Vs0[TILE];
+  __shared__ __attribute__((aligned(1024))) uint16_t Vs1[TILE];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = lane & 31, g = lane >> 5;
@@ -85,6 +118,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(FlashArgs a) {
   const int hk = h / (a.H / a.Hkv);
   const int q0 = qt * BQ;
   const int qi = q0 + wave * 32 + c;  // this lane's query
+  const int q_last = min(q0 + BQ, a.Sq) - 1;
 
   const uint16_t* Q = (const uint16_t*)a.q + b * a.q_sb + h * a.q_sh;
   const uint16_t* K = (const uint16_t*)a.k + b * a.k_sb + hk * a.k_sh;
@@ -117,59 +151,44 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(FlashArgs a) {
     }
   }
 
-  uint4 kst[KPT], vst[VPT][4];
-  auto load_tile = [&](int kt) {
+  // DMA of one key tile: instruction q of this wave covers key rows
+  // ROWS_PER_DMA * (wave * DMA_PER_WAVE + q) + lane / CPR
+  const int row_in = lane / CPR, pc = lane % CPR;
+  auto dma_tile = [&](uint16_t* ks, uint16_t* vs, int kt) {
     const int k0 = kt * BKV;
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      const int cid = threadIdx.x + i * 256;
-      const int row = cid / (D / 8), col = cid - row * (D / 8);
-      const int key = k0 + row;
-      if (cid < KCH && key < a.Sk)
-        kst[i] = *(const uint4*)(K + (int64_t)key * a.k_ss + col * 8);
-      else
-        kst[i] = make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      const int gid = threadIdx.x + i * 256;
-      const int dc = gid % (D / 8), kg = gid / (D / 8);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = k0 + kg * 4 + r;
-        if (gid < VG && key < a.Sk)
-          vst[i][r] = *(const uint4*)(V + (int64_t)key * a.v_ss + dc * 8);
-        else
-          vst[i][r] = make_uint4(0, 0, 0, 0);
-      }
+    for (int q = 0; q < DMA_PER_WAVE; ++q) {
+      const int blk = wave * DMA_PER_WAVE + q;
+      const int r = blk * ROWS_PER_DMA + row_in;
+      int key = k0 + r;
+      key = key < a.Sk ? key : a.Sk - 1;  // rows past Sk: an in-range row (masked below)
+      const int ck = pc ^ (r % CPR);
+      const int cv = pc ^ ((4 * (r & 3)) % CPR);
+      dma16(K + (int64_t)key * a.k_ss + ck * 8, ks + blk * 512);
+      dma16(V + (int64_t)key * a.v_ss + cv * 8, vs + blk * 512);
     }
   };
-  auto store_tile = [&](int buf) {
+
+  // K fragment offsets (elements): key row kb*32 + c, d-chunk 2t + g
+  int k_off[2][NT];
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      const int cid = threadIdx.x + i * 256;
-      const int row = cid / (D / 8), col = cid - row * (D / 8);
-      if (cid < KCH) *(uint4*)(&Ks[buf][row * KP + col * 8]) = kst[i];
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int r = kb * 32 + c;
+      k_off[kb][t] = r * D + (((2 * t + g) ^ (r % CPR)) * 8);
     }
+  // V fragment offsets: 16-lane group G, source lane s: key row
+  // 4 (G >> 1) + s / 4 (+ 8 for the second read), d column
+  // dt*32 + 16 (G & 1) + 4 (s % 4)
+  const int G = lane >> 4, s16 = lane & 15;
+  int v_off[DT];
 #pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      const int gid = threadIdx.x + i * 256;
-      if (gid >= VG) continue;
-      const int dc = gid % (D / 8), kg = gid / (D / 8);
-      const int kk = kg * 4;
-      const int pos = (kk & ~15) + fa_perm16(kk & 15);
-#pragma unroll
-      for (int dd = 0; dd < 8; ++dd) {
-        const int w = dd >> 1, sh = (dd & 1) * 16;
-        const uint32_t e0 = ((&vst[i][0].x)[w] >> sh) & 0xffffu;
-        const uint32_t e1 = ((&vst[i][1].x)[w] >> sh) & 0xffffu;
-        const uint32_t e2 = ((&vst[i][2].x)[w] >> sh) & 0xffffu;
-        const uint32_t e3 = ((&vst[i][3].x)[w] >> sh) & 0xffffu;
-        *(uint2*)(&Vt[buf][(dc * 8 + dd) * VP + pos]) =
-            make_uint2(e0 | (e1 << 16), e2 | (e3 << 16));
-      }
-    }
-  };
+  for (int dt = 0; dt < DT; ++dt) {
+    const int r = 4 * (G >> 1) + (s16 >> 2);
+    const int col = dt * 32 + 16 * (G & 1) + 4 * (s16 & 3);
+    v_off[dt] = r * D + (((col >> 3) ^ ((4 * (r & 3)) % CPR)) * 8) + (col & 7);
+  }
 
   f32x16_t o[DT];
 #pragma unroll
@@ -177,69 +196,91 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(FlashArgs a) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[dt][e] = 0.0f;
   float m_run = -INFINITY, l_run = 0.0f;
+  const bool fold = a.scale > 0.0f;
+  const float sl2 = a.scale * kLog2e;
 
-  if (kt0 < kt1) {
-    load_tile(kt0);
-    store_tile(0);
-  }
-  __syncthreads();
-
-  for (int kt = kt0; kt < kt1; ++kt) {
-    const int cur = (kt - kt0) & 1;
+  auto k_tile = [&](const uint16_t* ks, const uint16_t* vs, uint16_t* ks_n, uint16_t* vs_n,
+                    int kt) {
     const bool more = kt + 1 < kt1;
-    if (more) load_tile(kt + 1);
-    const uint16_t* ks = Ks[cur];
-    const uint16_t* vt = Vt[cur];
+    // branch-free: on the last tile a spare reload of tile kt0 into the idle stage
+    dma_tile(ks_n, vs_n, more ? kt + 1 : kt0);
 
     // S^T tile: 64 keys x 32 queries as two 32x32 accumulators
-    f32x16_t s[2];
+    f32x16_t sacc[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) s[kb][e] = 0.0f;
+      for (int e = 0; e < 16; ++e) sacc[kb][e] = 0.0f;
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const bf16x8_t kf = *(const bf16x8_t*)(ks + (kb * 32 + c) * KP + t * 16 + g * 8);
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[t], s[kb], 0, 0, 0);
+        const bf16x8_t kf = *(const bf16x8_t*)(ks + k_off[kb][t]);
+        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[t], sacc[kb], 0, 0, 0);
       }
     }
 
-    // scale, mask, online softmax (all 32 scores of this lane are query qi)
+    // bf16 rounding, scale, mask; tile max
     const int k0 = kt * BKV;
+    const bool plain = fold && k0 + BKV <= a.Sk &&
+                       (!a.mask || (a.mask_true == 0.0f &&
+                                    fa_all_visible(a.cmp, q0, q_last, k0, k0 + BKV - 1)));
     float mt = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int j = k0 + kb * 32 + (e >> 2) * 8 + g * 4 + (e & 3);
-        float x = a.round_scores ? vm::round_bf16(s[kb][e]) : s[kb][e];
-        x = x * a.scale;
-        if (a.mask) x = x + (fa_visible(a.cmp, qi, j) ? a.mask_true : a.mask_false);
-        if (j >= a.Sk) x = -INFINITY;
-        s[kb][e] = x;
-        mt = fmaxf(mt, x);
+      for (int e = 0; e < 16; e += 2) {
+        float x0 = sacc[kb][e], x1 = sacc[kb][e + 1];
+        if (a.round_scores) {
+          const uint32_t pr = cvt_bf16x2(x0, x1);
+          x0 = vm::as_f(pr << 16);
+          x1 = vm::as_f(pr & 0xffff0000u);
+        }
+        if (!plain) {
+          const int j0 = k0 + kb * 32 + (e >> 2) * 8 + g * 4 + (e & 3);
+          x0 = x0 * a.scale;
+          x1 = x1 * a.scale;
+          if (a.mask) {
+            x0 += fa_visible(a.cmp, qi, j0) ? a.mask_true : a.mask_false;
+            x1 += fa_visible(a.cmp, qi, j0 + 1) ? a.mask_true : a.mask_false;
+          }
+          if (j0 >= a.Sk) x0 = -INFINITY;
+          if (j0 + 1 >= a.Sk) x1 = -INFINITY;
+        }
+        sacc[kb][e] = x0;
+        sacc[kb][e + 1] = x1;
+        mt = fmaxf(mt, fmaxf(x0, x1));
       }
+    if (plain) mt = mt * a.scale;  // max of x * scale: rounding is monotone
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
     const float m_new = fmaxf(m_run, mt);
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
     const float alpha = exp2f((m_run - m_use) * kLog2e);
     m_run = m_new;
+    const float ml2 = m_use * kLog2e;
     float psum = 0.0f;
     uint32_t pk[2][8];  // bf16 pairs: [kb][e/2]
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int e = 0; e < 16; e += 2) {
-        const float p0 = exp2f((s[kb][e] - m_use) * kLog2e);
-        const float p1 = exp2f((s[kb][e + 1] - m_use) * kLog2e);
+        float p0, p1;
+        if (plain) {
+          p0 = exp2f(fmaf(sacc[kb][e], sl2, -ml2));
+          p1 = exp2f(fmaf(sacc[kb][e + 1], sl2, -ml2));
+        } else {
+          p0 = exp2f((sacc[kb][e] - m_use) * kLog2e);
+          p1 = exp2f((sacc[kb][e + 1] - m_use) * kLog2e);
+        }
         psum += p0 + p1;
-        pk[kb][e >> 1] = pack_bf16x2(p0, p1);
+        pk[kb][e >> 1] = cvt_bf16x2(p0, p1);
       }
     l_run = l_run * alpha + psum;
+    // rescale the accumulators only when some row's max moved
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+      for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
+        for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
+    }
 
     // O^T += V^T P^T over 4 k-steps of 16 keys
 #pragma unroll
@@ -253,13 +294,28 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(FlashArgs a) {
       for (int i = 0; i < 4; ++i) pf.w[i] = pk[kb][half * 4 + i];
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const bf16x8_t vf = *(const bf16x8_t*)(vt + (dt * 32 + c) * VP + u * 16 + g * 8);
-        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf.v, o[dt], 0, 0, 0);
+        const uint16_t* p = vs + v_off[dt] + u * 16 * D;
+        union {
+          v4s h[2];
+          bf16x8_t v;
+        } vf;
+        vf.h[0] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)p);
+        vf.h[1] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(p + 8 * D));
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf.v, pf.v, o[dt], 0, 0, 0);
       }
     }
-
-    if (more) store_tile(cur ^ 1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+  };
+
+  if (kt0 < kt1) {
+    dma_tile(Ks0, Vs0, kt0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    for (int kt = kt0; kt < kt1; kt += 2) {
+      k_tile(Ks0, Vs0, Ks1, Vs1, kt);
+      if (kt + 1 < kt1) k_tile(Ks1, Vs1, Ks0, Vs0, kt + 1);
+    }
   }
 
   // normalise and store: lane (c, g) holds O[qi][dt*32 + (e>>2)*8 + g*4 + (e&3)]
@@ -272,8 +328,8 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(FlashArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int d0 = dt * 32 + r * 8 + g * 4;
-        *(uint2*)(O + d0) = make_uint2(pack_bf16x2(o[dt][r * 4 + 0] * inv, o[dt][r * 4 + 1] * inv),
-                                       pack_bf16x2(o[dt][r * 4 + 2] * inv, o[dt][r * 4 + 3] * inv));
+        *(uint2*)(O + d0) = make_uint2(cvt_bf16x2(o[dt][r * 4 + 0] * inv, o[dt][r * 4 + 1] * inv),
+                                       cvt_bf16x2(o[dt][r * 4 + 2] * inv, o[dt][r * 4 + 3] * inv));
       }
   }
 }

@@ -79,15 +79,103 @@ __global__ void __launch_bounds__(256) rmsnorm_rows_kernel(RowNormArgs a) {
   }
 }
 
+// Fast path: one wave per row, the row held in registers as 16-byte chunks
+// (8 bf16 or 4 f32 per load), CH chunks per lane; a wave-only reduction; the
+// same op order as rmsnorm_rows_kernel (square, sum, / n, + eps, sqrt,
+// x / r, gamma * .).
+template <int XB, int YB, int CH>  // element bytes of x and y; 16-byte chunks per lane
+__global__ void __launch_bounds__(256) rmsnorm_wave_kernel(RowNormArgs a) {
+  constexpr int EPC_X = 16 / XB;          // elements per x chunk
+  const int lane = threadIdx.x & 63;
+  const int64_t waves = (int64_t)gridDim.x * 4;
+  for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < a.rows; row += waves) {
+    const char* x = (const char*)a.x + row * a.x_rs * XB;
+    uint4 raw[CH];
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      const int64_t j = ((int64_t)k * 64 + lane) * EPC_X;
+      raw[k] = j < a.n ? *(const uint4*)(x + j * XB) : make_uint4(0, 0, 0, 0);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      const uint32_t* w = (const uint32_t*)&raw[k];
+#pragma unroll
+      for (int e = 0; e < EPC_X; ++e) {
+        const float v = XB == 2 ? as_f((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16))
+                                : as_f(w[e]);
+        const float sq = v * v;
+        ss += sq;
+      }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+    const float mean = ss / a.divisor;
+    const float r = sqrtf(mean + a.eps);
+    char* y = (char*)a.y + row * a.n * YB;
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      const int64_t j = ((int64_t)k * 64 + lane) * EPC_X;
+      if (j >= a.n) continue;
+      const uint32_t* w = (const uint32_t*)&raw[k];
+      float out[EPC_X];
+#pragma unroll
+      for (int e = 0; e < EPC_X; ++e) {
+        const float v = XB == 2 ? as_f((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16))
+                                : as_f(w[e]);
+        const float nv = v / r;
+        out[e] = a.gamma[j + e] * nv;
+      }
+      if (YB == 2) {
+        uint32_t o[EPC_X / 2];
+#pragma unroll
+        for (int e = 0; e < EPC_X; e += 2)
+          o[e / 2] = (uint32_t)bf16_bits(out[e]) | ((uint32_t)bf16_bits(out[e + 1]) << 16);
+        if (EPC_X == 8) *(uint4*)(y + j * 2) = *(const uint4*)o;
+        else *(uint2*)(y + j * 2) = *(const uint2*)o;
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPC_X; e += 4)
+          *(float4*)(y + (j + e) * 4) = make_float4(out[e], out[e + 1], out[e + 2], out[e + 3]);
+      }
+    }
+  }
+}
+
 void launch_rmsnorm_rows(const RowNormArgs& a, hipStream_t stream) {
   if (a.rows == 0 || a.n == 0) return;
-  const unsigned grid = (unsigned)(a.rows < 65536 ? a.rows : 65536);
-  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(grid), dim3(256), 0, stream, a);
+  const int xb = a.x_dt == REW_DT_BFLOAT16 ? 2 : 4, yb = a.y_dt == REW_DT_BFLOAT16 ? 2 : 4;
+  const int epc = 16 / xb;
+  const int64_t chunks = (a.n + epc - 1) / epc;  // 16-byte chunks per row
+  const bool vec = a.n % epc == 0 && (a.x_rs * xb) % 16 == 0 && ((uintptr_t)a.x & 15) == 0 &&
+                   ((uintptr_t)a.y & 15) == 0 && (a.n * yb) % 16 == 0 && chunks <= 64 * 16;
+  if (vec) {
+    const int64_t blocks = (a.rows + 3) / 4;
+    const dim3 grid((unsigned)(blocks < 65536 ? blocks : 65536)), block(256);
+    const int ch = (int)((chunks + 63) / 64);
+#define REW_RMS(XB, YB, CH) hipLaunchKernelGGL((rmsnorm_wave_kernel<XB, YB, CH>), grid, block, 0, stream, a)
+#define REW_RMS_CH(XB, YB) \
+    if (ch <= 2) REW_RMS(XB, YB, 2); else if (ch <= 4) REW_RMS(XB, YB, 4); \
+    else if (ch <= 8) REW_RMS(XB, YB, 8); else REW_RMS(XB, YB, 16)
+    if (xb == 2 && yb == 2) { REW_RMS_CH(2, 2); }
+    else if (xb == 2) { REW_RMS_CH(2, 4); }
+    else if (yb == 2) { REW_RMS_CH(4, 2); }
+    else { REW_RMS_CH(4, 4); }
+#undef REW_RMS_CH
+#undef REW_RMS
+  } else {
+    const unsigned grid = (unsigned)(a.rows < 65536 ? a.rows : 65536);
+    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(grid), dim3(256), 0, stream, a);
+  }
   REW_HIP(hipGetLastError());
 }
 
 // ---- RoPE ------------------------------------------------------------------------------
 
+// VEC: bf16 x and y with contiguous pairs, cos / sin read at pair stride 2
+// (rew's duplicated tables): one 16-byte x load, two float4 loads of each
+// table, one 16-byte store per four pairs.
+template <bool VEC>
 __global__ void __launch_bounds__(256) rope_pairs_kernel(RopeArgs a) {
   // pairs are processed in groups of 4 consecutive i (half % 4 == 0)
   const uint32_t g4 = (uint32_t)(a.half / 4);
@@ -104,6 +192,28 @@ __global__ void __launch_bounds__(256) rope_pairs_kernel(RopeArgs a) {
     const int64_t cb = i0d * a.c_s0 + i1 * a.c_s1 + s * a.c_ss;
     const int64_t sb = i0d * a.s_s0 + i1 * a.s_s1 + s * a.s_ss;
     const int64_t yb = ((int64_t)q2 * a.S + s) * (2 * a.half) + 2 * i0;
+    if (VEC) {
+      const uint4 xv = *(const uint4*)((const uint16_t*)a.x + xb + 2 * i0);
+      const float4 c0 = *(const float4*)(a.cos + cb + 2 * i0);
+      const float4 c1 = *(const float4*)(a.cos + cb + 2 * i0 + 4);
+      const float4 s0 = *(const float4*)(a.sin + sb + 2 * i0);
+      const float4 s1 = *(const float4*)(a.sin + sb + 2 * i0 + 4);
+      const float cs[4] = {c0.x, c0.z, c1.x, c1.z};
+      const float sn[4] = {s0.x, s0.z, s1.x, s1.z};
+      const uint32_t* w = (const uint32_t*)&xv;
+      uint32_t o[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float x0 = as_f(w[u] << 16), x1 = as_f(w[u] & 0xffff0000u);
+        const float t1 = cs[u] * x0;
+        const float t2 = sn[u] * x1;
+        const float t3 = sn[u] * x0;
+        const float t4 = cs[u] * x1;
+        o[u] = (uint32_t)bf16_bits(t1 - t2) | ((uint32_t)bf16_bits(t3 + t4) << 16);
+      }
+      *(uint4*)((uint16_t*)a.y + yb) = make_uint4(o[0], o[1], o[2], o[3]);
+      continue;
+    }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int64_t i = i0 + u;
@@ -126,7 +236,16 @@ void launch_rope(const RopeArgs& a, hipStream_t stream) {
   if (total == 0) return;
   int64_t blocks = (total + 255) / 256;
   if (blocks > 256 * 32) blocks = 256 * 32;
-  hipLaunchKernelGGL(rope_pairs_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+  auto al = [](const void* p, int b) { return ((uintptr_t)p % b) == 0; };
+  const bool vec = a.x_dt == REW_DT_BFLOAT16 && a.y_dt == REW_DT_BFLOAT16 && a.x_sd == 1 &&
+                   a.x_s0 % 8 == 0 && a.x_s1 % 8 == 0 && a.x_ss % 8 == 0 && al(a.x, 16) &&
+                   al(a.y, 16) && a.c_si == 2 && a.s_si == 2 && a.c_s0 % 4 == 0 &&
+                   a.c_s1 % 4 == 0 && a.c_ss % 4 == 0 && a.s_s0 % 4 == 0 && a.s_s1 % 4 == 0 &&
+                   a.s_ss % 4 == 0 && al(a.cos, 16) && al(a.sin, 16);
+  if (vec)
+    hipLaunchKernelGGL(rope_pairs_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL(rope_pairs_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
   REW_HIP(hipGetLastError());
 }
 

@@ -200,6 +200,10 @@ struct FlashPlan {
   bool mask = false;
   int cmp = 0;
   float mask_true = 0.0f, mask_false = 0.0f;
+  // When the attention output's only consumer is transpose [0, 2, 1, 3]
+  // (GroupedQueryAttention.forward, groupedqueryattention.nim:136-140),
+  // the kernel writes that transposed tensor directly.
+  Tensor* out_t = nullptr;
 };
 
 // A dot_general whose consumers fold into its epilogue (see GemmArgs::epi).
@@ -256,6 +260,7 @@ struct Lower {
   std::unordered_map<Tensor*, NormPlan> norm_out;
   std::unordered_map<Tensor*, RopePlan> rope_out;
   std::unordered_map<Tensor*, MoePlan> moe_out;
+  std::unordered_map<Tensor*, Node*> flash_out;  // transposed flash output -> PV node
 
   explicit Lower(Ctx* ctx) : c(ctx) {}
 
@@ -270,6 +275,7 @@ struct Lower {
   bool rows_view(Tensor* x, int64_t n, const void** ptr, int64_t* rs);
   bool emit_gemm_fused(Tensor* t, const GemmPlan& p);
   bool emit_flash(Node* pv, const FlashPlan& fp);
+  void match_flash_out();
   bool kv_operand(Tensor* t, int H, const void** ptr, int64_t* sb, int64_t* sh,
                   int64_t* ss, int* hkv);
 
@@ -848,6 +854,22 @@ void Lower::ensure_mat(Tensor* t) {
     rope_out.erase(rit);
     if (emit_rope(t, rp)) return;
   }
+  auto fit = flash_out.find(t);
+  if (fit != flash_out.end()) {
+    Node* pv = fit->second;
+    flash_out.erase(fit);
+    auto pit = flash.find(pv);
+    if (pit != flash.end()) {
+      FlashPlan fp = pit->second;
+      if (emit_flash(pv, fp)) {
+        flash.erase(pit);
+        return;
+      }
+      // not launchable: the attention output is produced by the generic path
+      // and transposed by the elementwise kernel below
+      flash[pv].out_t = nullptr;
+    }
+  }
   auto mit = moe_out.find(t);
   if (mit != moe_out.end()) {
     MoePlan mp = mit->second;
@@ -858,10 +880,13 @@ void Lower::ensure_mat(Tensor* t) {
   Node* p = t->prod;
   if (!p) throw Error(REW_MI355X_ERR_INVALID, "internal: tensor has neither data nor producer");
   if (is_ew(p->kind) || is_view(p->kind)) {
-    // a reshape of a materialized (or materializable) dense tensor aliases it
+    // a reshape (or a chain of reshapes) of a materialized or materializable
+    // dense tensor aliases it
     if (p->kind == K_RESHAPE) {
       Tensor* x = p->in[0];
-      if (x->st || x->plan_mat || !x->prod) {
+      Tensor* y = x;
+      while (!y->st && !y->plan_mat && y->prod && y->prod->kind == K_RESHAPE) y = y->prod->in[0];
+      if (y->st || y->plan_mat || !y->prod) {
         ensure_mat(x);
         tensor_alias(t, x);
         return;
@@ -917,7 +942,7 @@ void Lower::emit_ew_root(Tensor* t) {
       set_leaf_modes(g.P, S, vec);
       if (c->profiling)
         prof_begin(c, "ew_fused{" + std::to_string(S.numel) + "x" + std::to_string(g.P.n_ins) +
-                          "," + dt_name(t->dt) + "}");
+                          "," + dt_name(t->dt) + "," + (t->prod ? t->prod->name : "?") + "}");
       launch_ew(g.P, S, vec, c->stream);
       prof_end(c);
       note_launch(c, g.P.n_ins > 2);
@@ -1423,6 +1448,36 @@ bool Lower::kv_operand(Tensor* t, int H, const void** ptr, int64_t* sb, int64_t*
   return true;
 }
 
+// REW_MI355X_DEBUG_PLAN=1: the pattern matchers report their decisions on
+// stderr (diagnostics only).
+static bool debug_plan() {
+  static const bool on = [] {
+    const char* s = std::getenv("REW_MI355X_DEBUG_PLAN");
+    return s && s[0] == '1';
+  }();
+  return on;
+}
+
+void Lower::match_flash_out() {
+  for (auto& kv : flash) {
+    Node* pv = kv.first;
+    Tensor* o = pv->out[0];
+    auto it = cons.find(o);
+    const size_t nc = it == cons.end() ? 0 : it->second.size();
+    if (debug_plan())
+      std::fprintf(stderr, "[plan] flash out: ext=%d uses=%d consumers=%zu first=%s\n", o->ext,
+                   o->uses, nc, nc ? it->second[0]->name.c_str() : "-");
+    if (o->ext != 0 || o->uses != 1 || nc != 1) continue;
+    Node* tr = it->second[0];
+    if (tr->kind != K_TRANSPOSE || !dims_are(tr->l0, {0, 2, 1, 3})) continue;
+    Tensor* t = tr->out[0];
+    o->plan_mat = false;
+    t->plan_mat = true;
+    kv.second.out_t = t;
+    flash_out[t] = pv;
+  }
+}
+
 bool Lower::emit_flash(Node* pv, const FlashPlan& fp) {
   Tensor* out = pv->out[0];
   FlashArgs a;
@@ -1458,11 +1513,19 @@ bool Lower::emit_flash(Node* pv, const FlashPlan& fp) {
     hk_k = hk_v = a.H;
   }
   a.Hkv = hk_k;
+  if (fp.out_t) {
+    // [B, Sq, H, D] dense: the consumer's transposed layout
+    out = fp.out_t;
+    a.o_sb = (int64_t)a.Sq * a.H * a.D;
+    a.o_sh = a.D;
+    a.o_ss = (int64_t)a.H * a.D;
+  } else {
+    a.o_sb = (int64_t)a.H * a.Sq * a.D;
+    a.o_sh = (int64_t)a.Sq * a.D;
+    a.o_ss = a.D;
+  }
   tensor_alloc(out);
   a.o = out->data();
-  a.o_sb = (int64_t)a.H * a.Sq * a.D;
-  a.o_sh = (int64_t)a.Sq * a.D;
-  a.o_ss = a.D;
   a.scale = fp.scale;
   a.round_scores = fp.round_scores ? 1 : 0;
   a.mask = fp.mask ? 1 : 0;
@@ -2426,6 +2489,7 @@ void flush(Ctx* c) {
     for (Node* n : L.nodes)
       if (n->kind == K_DOT_GENERAL) L.match_flash(n);
     L.cons = consumers;
+    L.match_flash_out();
     L.match_gemm_epilogues();
     L.match_moe();
     L.match_rows();
