@@ -24,8 +24,10 @@
 #ifndef REW_MI355X_H
 #define REW_MI355X_H
 
+#ifndef __HIPCC_RTC__ /* hipRTC (run-time compiled kernels) has these types built in */
 #include <stddef.h>
 #include <stdint.h>
+#endif
 
 #ifdef __cplusplus
 extern "C" {

@@ -54,7 +54,7 @@ def build(verbose: bool = False) -> Path:
         objs = list(ex.map(_compile, srcs))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-o", str(tmp),
-           *map(str, objs), "-lpthread"]
+           *map(str, objs), "-L/opt/rocm/lib", "-lhiprtc", "-ldl", "-lpthread"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")

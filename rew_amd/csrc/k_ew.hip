@@ -32,6 +32,7 @@ __global__ void __launch_bounds__(256) ew_kernel(Program P, Space S) {
 void launch_ew(const vm::Program& P, const vm::Space& S, bool vec,
                hipStream_t stream) {
   if (S.numel == 0) return;
+  if (jit_launch_ew(P, S, vec, stream)) return;
   const int V = vec ? vm::kVec : 1;
   const int64_t nvec = S.numel / V;
   int64_t blocks = (nvec + 255) / 256;

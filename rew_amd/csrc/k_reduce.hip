@@ -99,6 +99,7 @@ __global__ void __launch_bounds__(256) reduce_small_kernel(Program P, Space S,
 void launch_reduce(const vm::Program& P, const vm::Space& S,
                    const ReduceArgs& A, bool vec, hipStream_t stream) {
   if (A.n_out == 0) return;
+  if (jit_launch_reduce(P, S, A, vec, stream)) return;
   if (A.n_red >= 128) {
     int64_t blocks = A.n_out < 65536 ? A.n_out : 65536;
     if (vec)

@@ -14,6 +14,15 @@ namespace rew {
 void launch_ew(const vm::Program& P, const vm::Space& S, bool vec,
                hipStream_t stream);
 
+// ---- run-time compiled programs (jit.cpp) ------------------------------------
+// Launch P as a hipRTC-compiled kernel specialised to its constants; false
+// when compiled kernels are off or the program failed to compile (the
+// caller then runs the interpreter).
+struct ReduceArgs;
+bool jit_launch_ew(const vm::Program& P, const vm::Space& S, bool vec, hipStream_t stream);
+bool jit_launch_reduce(const vm::Program& P, const vm::Space& S, const ReduceArgs& A, bool vec,
+                       hipStream_t stream);
+
 // ---- reductions (k_reduce.hip) ---------------------------------------------
 enum RedOp : int {
   RED_SUM = 0, RED_MAX, RED_MIN, RED_PROD, RED_AND, RED_OR, RED_MAXI, RED_MINI

@@ -11,7 +11,9 @@
 // interpretation cost is spread over 64 x kVec elements.
 #pragma once
 
+#ifndef __HIPCC_RTC__
 #include <stdint.h>
+#endif
 
 namespace rew {
 namespace vm {

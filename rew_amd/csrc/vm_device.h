@@ -1,11 +1,18 @@
 // Device-side interpreter of vm::Program (included by the .hip kernels).
 #pragma once
 
+// Compiled both by hipcc (the interpreter kernels) and by hipRTC (the
+// kernels generated for fused programs at run time), where the HIP runtime
+// headers and the math functions are built in.
+#ifndef __HIPCC_RTC__
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 #include <math.h>
 
 #include "../../include/rew_mi355x.h"
+#else
+#include "rtc_prelude.h"
+#endif
 #include "vm.h"
 
 namespace rew {
