@@ -129,6 +129,18 @@ int rew_mi355x_execute(rew_mi355x_ctx* ctx, const char* op,
                        const char* const* attr_vals, int n_attrs,
                        rew_mi355x_buf** outs, int max_outs, int* n_outs);
 
+/* rew_mi355x_execute that also reports each output's dtype, rank and shape:
+ * out_meta[i * (2 + REW_MI355X_MAX_RANK) + {0, 1, 2..}] = dtype, rank, dims.
+ * No reference counterpart (rew derives output shapes on the Nim side with
+ * deriveOutputShapes, src/rew/eager.nim:1061-1283): a convenience for hosts
+ * that would otherwise ask rew_mi355x_buf_meta once per output. */
+int rew_mi355x_execute_ex(rew_mi355x_ctx* ctx, const char* op,
+                          rew_mi355x_buf* const* operands, int n_operands,
+                          const char* const* attr_keys,
+                          const char* const* attr_vals, int n_attrs,
+                          rew_mi355x_buf** outs, int max_outs, int* n_outs,
+                          int64_t* out_meta);
+
 /* Lower and launch every pending op (asynchronous; returns after enqueue).
  * No reference counterpart: the PJRT path executes every op at dispatch
  * (src/rew/eager.nim:1745-1754); this is the deferred-group boundary. */

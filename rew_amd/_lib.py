@@ -29,6 +29,10 @@ SIGNATURES = {
     "rew_mi355x_execute": (C.c_int, [_c_ctx, C.c_char_p, C.POINTER(_c_buf), C.c_int,
                                      C.POINTER(C.c_char_p), C.POINTER(C.c_char_p), C.c_int,
                                      C.POINTER(_c_buf), C.c_int, C.POINTER(C.c_int)]),
+    "rew_mi355x_execute_ex": (C.c_int, [_c_ctx, C.c_char_p, C.POINTER(_c_buf), C.c_int,
+                                        C.POINTER(C.c_char_p), C.POINTER(C.c_char_p), C.c_int,
+                                        C.POINTER(_c_buf), C.c_int, C.POINTER(C.c_int),
+                                        C.POINTER(C.c_int64)]),
     "rew_mi355x_flush": (C.c_int, [_c_ctx]),
     "rew_mi355x_sync": (C.c_int, [_c_ctx]),
     "rew_mi355x_set_mode": (C.c_int, [_c_ctx, C.c_int]),

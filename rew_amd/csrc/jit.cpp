@@ -73,14 +73,59 @@ std::string src_dir() {
   return dir;
 }
 
-JitFn* get_fn(const std::string& src, const char* entry) {
+// Binary signature of a launch: everything the generated source depends on
+// (the program without its pointers, the space, the kind and its constants).
+std::string signature(const vm::Program& P, const vm::Space& S, int kind, int V,
+                      const ReduceArgs* A) {
+  std::string k;
   int dev = 0;
   REW_HIP(hipGetDevice(&dev));
-  const std::string key = std::to_string(dev) + "\n" + src;
+  auto put = [&](const void* p, size_t n) { k.append((const char*)p, n); };
+  put(&dev, sizeof dev);
+  put(&kind, sizeof kind);
+  put(&V, sizeof V);
+  put(&P.n_ins, sizeof P.n_ins);
+  put(&P.n_leaves, sizeof P.n_leaves);
+  put(&P.n_outs, sizeof P.n_outs);
+  put(P.ins, sizeof(vm::Ins) * P.n_ins);
+  // field by field: struct padding is never part of the key
+  for (int i = 0; i < P.n_leaves; ++i) {
+    const vm::Leaf& L = P.leaf[i];
+    put(&L.dtype, 1);
+    put(&L.mode, 1);
+    put(&L.vrank, 1);
+    put(&L.off, sizeof L.off);
+    put(&L.clamp_hi, sizeof L.clamp_hi);
+    put(L.stride, sizeof L.stride);
+    put(L.vdim, sizeof L.vdim);
+  }
+  for (int q = 0; q < P.n_outs; ++q) {
+    const vm::Out& O = P.out[q];
+    put(&O.dtype, 1);
+    put(&O.reg, 1);
+    put(&O.off, sizeof O.off);
+  }
+  put(&S.rank, sizeof S.rank);
+  put(&S.numel, sizeof S.numel);
+  put(S.dim, sizeof(vm::FastDiv) * S.rank);
+  if (A) {
+    put(&A->op, sizeof A->op);
+    put(&A->n_out, sizeof A->n_out);
+    put(&A->n_red, sizeof A->n_red);
+    put(&A->out_dtype, sizeof A->out_dtype);
+  }
+  return k;
+}
+
+// Kernel of `key`; `make_src` is called (and the source compiled) only on a
+// miss.
+template <typename F>
+JitFn* get_fn(const std::string& key, F make_src, const char* entry) {
   std::lock_guard<std::mutex> g(g_jit_mu);
   auto it = g_jit.find(key);
   if (it != g_jit.end()) return it->second.failed ? nullptr : &it->second;
   JitFn& f = g_jit[key];
+  const std::string src = make_src();
   hiprtcProgram prog;
   if (hiprtcCreateProgram(&prog, src.c_str(), "rew_jit.hip", 0, nullptr, nullptr) !=
       HIPRTC_SUCCESS) {
@@ -325,7 +370,7 @@ bool launch(JitFn* f, const vm::Program& P, void* extra_out, bool outs, int64_t 
 bool jit_launch_ew(const vm::Program& P, const vm::Space& S, bool vec, hipStream_t stream) {
   if (!jit_enabled() || S.numel <= 0) return false;
   const int V = vec ? vm::kVec : 1;
-  JitFn* f = get_fn(gen_ew(P, S, V), "rew_ew");
+  JitFn* f = get_fn(signature(P, S, 0, V, nullptr), [&] { return gen_ew(P, S, V); }, "rew_ew");
   if (!f) return false;
   const int64_t nvec = S.numel / V;
   int64_t blocks = (nvec + 256 * kUnroll - 1) / (256 * kUnroll);
@@ -337,7 +382,8 @@ bool jit_launch_reduce(const vm::Program& P, const vm::Space& S, const ReduceArg
                        hipStream_t stream) {
   if (!jit_enabled() || A.n_out == 0) return false;
   const int V = (A.n_red >= 128 && vec) ? vm::kVec : 1;
-  JitFn* f = get_fn(gen_reduce(P, S, A, V), "rew_reduce");
+  JitFn* f = get_fn(signature(P, S, 1, V, &A), [&] { return gen_reduce(P, S, A, V); },
+                    "rew_reduce");
   if (!f) return false;
   int64_t blocks = A.n_red >= 128 ? (A.n_out + 3) / 4 : (A.n_out + 255) / 256;
   if (blocks > 65536) blocks = 65536;

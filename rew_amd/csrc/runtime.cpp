@@ -385,10 +385,10 @@ void rew_mi355x_release(rew_mi355x_buf* buf) {
   }
 }
 
-int rew_mi355x_execute(rew_mi355x_ctx* ctx, const char* op,
-                       rew_mi355x_buf* const* operands, int n_operands,
-                       const char* const* keys, const char* const* vals, int n_attrs,
-                       rew_mi355x_buf** outs, int max_outs, int* n_outs) {
+static int execute_impl(rew_mi355x_ctx* ctx, const char* op,
+                        rew_mi355x_buf* const* operands, int n_operands,
+                        const char* const* keys, const char* const* vals, int n_attrs,
+                        rew_mi355x_buf** outs, int max_outs, int* n_outs, int64_t* meta) {
   return guarded([&] {
     Ctx* c = as_ctx(ctx);
     if (!op) invalid("execute: null op name");
@@ -397,12 +397,19 @@ int rew_mi355x_execute(rew_mi355x_ctx* ctx, const char* op,
     if (n_attrs < 0 || (n_attrs > 0 && (!keys || !vals)))
       invalid(std::string("eager '") + op + "': bad attr arrays");
     std::vector<Tensor*> ins;
-    for (int i = 0; i < n_operands; ++i)
-      ins.push_back(check_handle(operands[i], (std::string("eager '") + op + "'").c_str()));
+    ins.reserve(n_operands);
+    for (int i = 0; i < n_operands; ++i) {
+      Tensor* t = reinterpret_cast<Tensor*>(operands[i]);
+      if (!t || !tensor_is_live_handle(t) || t->ext <= 0)
+        ins.push_back(check_handle(operands[i], (std::string("eager '") + op + "'").c_str()));
+      else
+        ins.push_back(t);
+    }
     std::vector<std::pair<std::string, std::string>> attrs;
+    attrs.reserve(n_attrs);
     for (int i = 0; i < n_attrs; ++i) {
       if (!keys[i] || !vals[i]) invalid(std::string("eager '") + op + "': null attr");
-      attrs.push_back({keys[i], vals[i]});
+      attrs.emplace_back(keys[i], vals[i]);
     }
     std::lock_guard<std::recursive_mutex> g(c->mu);
     REW_HIP(hipSetDevice(c->ordinal));
@@ -415,9 +422,33 @@ int rew_mi355x_execute(rew_mi355x_ctx* ctx, const char* op,
       invalid(std::string("eager '") + op + "': op produces " + std::to_string(res.size()) +
               " output(s), caller has room for " + std::to_string(max_outs));
     }
-    for (size_t i = 0; i < res.size(); ++i) outs[i] = reinterpret_cast<rew_mi355x_buf*>(res[i]);
+    for (size_t i = 0; i < res.size(); ++i) {
+      outs[i] = reinterpret_cast<rew_mi355x_buf*>(res[i]);
+      if (meta) {
+        int64_t* m = meta + i * (2 + REW_MI355X_MAX_RANK);
+        m[0] = res[i]->dt;
+        m[1] = res[i]->shape.rank;
+        for (int k = 0; k < res[i]->shape.rank; ++k) m[2 + k] = res[i]->shape.d[k];
+      }
+    }
     if (n_outs) *n_outs = (int)res.size();
   });
+}
+
+int rew_mi355x_execute(rew_mi355x_ctx* ctx, const char* op,
+                       rew_mi355x_buf* const* operands, int n_operands,
+                       const char* const* keys, const char* const* vals, int n_attrs,
+                       rew_mi355x_buf** outs, int max_outs, int* n_outs) {
+  return execute_impl(ctx, op, operands, n_operands, keys, vals, n_attrs, outs, max_outs, n_outs,
+                      nullptr);
+}
+
+int rew_mi355x_execute_ex(rew_mi355x_ctx* ctx, const char* op,
+                          rew_mi355x_buf* const* operands, int n_operands,
+                          const char* const* keys, const char* const* vals, int n_attrs,
+                          rew_mi355x_buf** outs, int max_outs, int* n_outs, int64_t* out_meta) {
+  return execute_impl(ctx, op, operands, n_operands, keys, vals, n_attrs, outs, max_outs, n_outs,
+                      out_meta);
 }
 
 int rew_mi355x_flush(rew_mi355x_ctx* ctx) {

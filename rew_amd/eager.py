@@ -206,6 +206,16 @@ class Tensor:
         self.shape = tuple(int(s) for s in shape)
         self.device = device
 
+    @classmethod
+    def _make(cls, handle: int, dtype: DType, shape: tuple, device: Device) -> "Tensor":
+        """Fast constructor for already-normalised fields (the dispatch path)."""
+        t = cls.__new__(cls)
+        t.handle = handle
+        t.dtype = dtype
+        t.shape = shape
+        t.device = device
+        return t
+
     def __del__(self):
         h = getattr(self, "handle", None)
         if h and _lib._lib is not None:
@@ -345,6 +355,35 @@ def dispatchEager(op: str, operands: Sequence[Tensor] = (),
     return be(op, operands, list(attrs))
 
 
+_META = 2 + 8  # per output: dtype, rank, 8 dims (rew_mi355x_execute_ex)
+_DTYPE_OF = {int(d): d for d in DType}
+_enc_cache: dict = {}
+
+
+def _enc(s) -> bytes:
+    b = _enc_cache.get(s)
+    if b is None:
+        b = str(s).encode()
+        if len(_enc_cache) < 65536:
+            _enc_cache[s] = b
+    return b
+
+
+class _Scratch(threading.local):
+    """Per-thread ctypes buffers reused by every dispatch."""
+
+    def __init__(self):
+        self.ops = (C.c_void_p * 16)()
+        self.keys = (C.c_char_p * 16)()
+        self.vals = (C.c_char_p * 16)()
+        self.outs = (C.c_void_p * 4)()
+        self.nout = C.c_int()
+        self.meta = (C.c_int64 * (4 * _META))()
+
+
+_scratch = _Scratch()
+
+
 def executeMi355xOp(op: str, operands: Sequence[Tensor],
                     attrs: Sequence[tuple[str, str]]) -> list:
     """The mi355x EagerBackend (counterpart of executeEagerOp, eager.nim:1717-1767)."""
@@ -357,22 +396,31 @@ def executeMi355xOp(op: str, operands: Sequence[Tensor],
                 tgt, _, o = v.partition(":")
                 d = Device(tgt or "mi355x", int(o or 0))
     for t in operands:
-        if t.device != d:
+        if t.device is not d and t.device != d:
             raise EagerError(f"eager '{op}': cross-device operands forbidden")
         if t.handle is None:
             raise BufferReleasedError(f"eager '{op}': tensor already released")
     lib = _lib.load()
-    n = len(operands)
-    ops = (C.c_void_p * max(1, n))(*[t.handle for t in operands])
-    na = len(attrs)
-    keys = (C.c_char_p * max(1, na))(*[k.encode() for k, _ in attrs])
-    vals = (C.c_char_p * max(1, na))(*[str(v).encode() for _, v in attrs])
-    outs = (C.c_void_p * 4)()
-    nout = C.c_int()
-    rc = lib.rew_mi355x_execute(context(d), op.encode(), ops, n, keys, vals, na, outs, 4,
-                                C.byref(nout))
+    sc = _scratch
+    n, na = len(operands), len(attrs)
+    ops = sc.ops if n <= 16 else (C.c_void_p * n)()
+    for i, t in enumerate(operands):
+        ops[i] = t.handle
+    keys = sc.keys if na <= 16 else (C.c_char_p * na)()
+    vals = sc.vals if na <= 16 else (C.c_char_p * na)()
+    for i, (k, v) in enumerate(attrs):
+        keys[i] = _enc(k)
+        vals[i] = _enc(v)
+    rc = lib.rew_mi355x_execute_ex(context(d), _enc(op), ops, n, keys, vals, na, sc.outs, 4,
+                                   C.byref(sc.nout), sc.meta)
     _check(rc)
-    return [_wrap(outs[i], d) for i in range(nout.value)]
+    res = []
+    meta = sc.meta
+    for i in range(sc.nout.value):
+        m = i * _META
+        res.append(Tensor._make(sc.outs[i], _DTYPE_OF[meta[m]],
+                                tuple(meta[m + 2:m + 2 + meta[m + 1]]), d))
+    return res
 
 
 def installEagerBackend(device: Device | None = None) -> None:
