@@ -1,20 +1,21 @@
 // bf16 GEMM on CDNA4 with direct global->LDS staging ("gemm_lds").
 //
 // Output tile 256 x 256 per workgroup, 4 waves of 128 x 128, each a 4 x 4
-// grid of v_mfma_f32_32x32x16_bf16 tiles (fp32 accumulators), BK = 64.
+// grid of v_mfma_f32_32x32x16_bf16 tiles (fp32 accumulators).
 //
-// Operands travel HBM/L2 -> LDS with global_load_lds_dwordx4: every lane
-// moves 16 bytes and lane l of an instruction lands at LDS base + 16 l, so
-// no VGPRs hold staged data and no VALU work writes LDS.  The LDS layout is
-// chosen through the source address each lane fetches:
-//   * K-contiguous operands (A, and B when it is [N, K]): a 256 x 64 tile,
-//     128-byte rows of eight 16-byte chunks, chunk c of row r stored at
-//     physical chunk c ^ ((r >> 1) & 7).  Two rows share a 256-byte bank
-//     window, so the 16 rows a ds_read_b128 serves per cycle land on 16
-//     distinct 16-byte bank slots (a plain c ^ (r & 7) maps rows r and
-//     r + 8 to the same slot: a 2-way conflict on every fragment read).
+// Operands travel HBM/L2 -> LDS with buffer_load_dwordx4 ... lds (or
+// global_load_lds_dwordx4 on the K-tail path): every lane moves 16 bytes
+// and lane l of an instruction lands at LDS base + 16 l, so no VGPRs hold
+// staged data and no VALU work writes LDS.  The LDS layout is chosen
+// through the source address each lane fetches (k-tiles of BK = 32):
+//   * K-contiguous operands (A, and B when it is [N, K]): a 256 x 32 tile,
+//     64-byte rows of four 16-byte chunks, chunk c of row r stored at
+//     physical chunk c ^ ((r >> 2) & 3).  The 16 lanes a ds_read_b128
+//     serves per cycle read one logical chunk of 16 consecutive rows; rows
+//     r and r + 4 share a 256-byte bank window and the XOR gives them
+//     distinct chunks, so the 16 reads hit 16 distinct 16-byte bank slots.
 //   * N-contiguous B (rew's [in, out] Linear weights, the common case): a
-//     64 x 256 tile, 512-byte k-rows of 32 chunks, chunk c of row k stored
+//     32 x 256 tile, 512-byte k-rows of 32 chunks, chunk c of row k stored
 //     at c ^ (4 (k & 3)).  Fragments are read with ds_read_b64_tr_b16: in
 //     each 16-lane group, source lane s points at k-row kb + s/4, columns
 //     4 (s % 4) .. +3, and output lane i receives B[kb + j][col0 + i] for
@@ -22,19 +23,26 @@
 //     straight out of the untransposed tile.  Two such reads (kb, kb + 4)
 //     give the 8 k-values of one fragment.  The XOR spreads the 8 k-rows x
 //     4 chunks of one read over all bank groups.
-// Two LDS stages: tile k + 1 streams into one while the MFMAs consume the
-// other; one s_waitcnt vmcnt(0) + barrier per k-tile.
+// The k-tiles stream through a ring of NS = 4 LDS stages (4 x 32 KiB): tile
+// t + 4 is requested right after the barrier that frees tile t's stage and
+// is first read three k-steps later.  On the Llama shapes the DMA stream
+// alone (no MFMAs) needs 0.45-0.64 us per 32-deep k-step and the MFMAs
+// alone about as long, so the two overlap rather than one hiding the other;
+// a fifth stage measured no faster.
 //
 // Tails: rows / columns past the matrix are read from a clamped in-range
-// address (their outputs are never stored); k-chunks past K are zeroed in
-// LDS after they land, so they add exact zeros.
+// address (their outputs are never stored); on the K-tail path, k-chunks
+// past K are fetched from an in-range address and zeroed in LDS after they
+// land, so they add exact zeros.
 //
 // Modes (template): B N-contiguous or K-contiguous; DUAL (SwiGLU: the tile's
 // 256 B columns are 128 gate + 128 up columns of two weight matrices, each
 // lane fetching from either); GROUP (routed experts: tile -> group from the
-// device tables, A rows gathered through a row list).  The epilogue stages
-// the bf16 C tile through LDS and writes 16-byte row chunks with the fused
-// bias / residual / SwiGLU arithmetic of GemmArgs.
+// device tables, A rows gathered through a row list).  The MFMAs produce
+// C^T blocks, so each lane holds runs of four consecutive output columns:
+// the epilogue writes them to a C tile in LDS as 8-byte chunks, then stores
+// whole 512-byte row segments with the fused bias / residual / SwiGLU
+// arithmetic of GemmArgs.
 #include "kernels.h"
 #include "vm_device.h"
 
@@ -48,18 +56,39 @@ typedef short v4s __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4s lds_v4s;
 typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int BM = 256, BN = 256, BK = 64;
-constexpr int A_BYTES = BM * BK * 2;  // 32 KiB
-constexpr int B_BYTES = BN * BK * 2;  // 32 KiB
-constexpr int STAGE = A_BYTES + B_BYTES;
-constexpr int CP = BN + 8;            // epilogue C tile pitch (elements)
-// Each stage is its own __shared__ array (so the compiler sees that the
-// DMA into one stage cannot alias fragment reads of the other), sized to
-// also hold half of the epilogue's C tile.
-constexpr int SBYTES = (BM / 2) * CP * 2 > STAGE ? (BM / 2) * CP * 2 : STAGE;
+constexpr int BM = 256, BN = 256, BK = 32;
+constexpr int NS = 4;                     // LDS ring stages
+constexpr int A_BYTES = BM * BK * 2;      // 16 KiB
+constexpr int B_BYTES = BN * BK * 2;      // 16 KiB
+constexpr int STAGE = A_BYTES + B_BYTES;  // 32 KiB
+constexpr int DMA_PER_TILE = 8;           // DMA instructions per wave per k-tile
+static_assert((NS - 1) * DMA_PER_TILE <= 63, "vmcnt range");
+
+// s_waitcnt immediate (vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14])
+constexpr int waitcnt_imm(int vm, int lgkm) {
+  return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | ((lgkm & 15) << 8);
+}
 
 __device__ __forceinline__ void to_lds16(const void* src, uint8_t* lds) {
   __builtin_amdgcn_global_load_lds(src, (lds_void*)lds, 16, 0, 0);
+}
+// buffer_load_dwordx4 ... lds: base and extent in the SGPR descriptor, the
+// lane's fixed byte offset in a VGPR, the k advance in an SGPR, so a k-tile
+// of DMA costs no VALU address arithmetic.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ void buf_to_lds16(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                             uint32_t soff, uint8_t* lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, voff, soff, 0, 0);
+}
+// Workgroup barrier without the memory fence of __syncthreads (which would
+// wait for every DMA in flight); callers wait for what they need first.
+__device__ __forceinline__ void block_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 __device__ __forceinline__ void tile_order(int64_t bid, int64_t tiles_m, int64_t tiles_n,
@@ -84,11 +113,22 @@ __device__ __forceinline__ void tile_order(int64_t bid, int64_t tiles_m, int64_t
 
 }  // namespace
 
-template <bool B_KC, bool DUAL, bool GROUP>
+// BUF: K % BK == 0 and every operand byte offset below 2^31 from its
+// descriptor base (checked at launch); the K-tail path then never runs.
+template <bool B_KC, bool DUAL, bool GROUP, bool BUF>
 __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmArgs g, GroupArgs ga) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem0[SBYTES];
-  __shared__ __attribute__((aligned(1024))) uint8_t smem1[SBYTES];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ __attribute__((aligned(1024))) uint8_t s0[STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t s1[STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t s2[STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t s3[STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t s4[NS > 4 ? STAGE : 16];
+  // Each stage is its own __shared__ array so the compiler sees that a DMA
+  // into one stage cannot alias fragment reads of another.
+  auto S = [&](int i) -> uint8_t* {
+    return i == 0 ? s0 : i == 1 ? s1 : i == 2 ? s2 : i == 3 ? s3 : s4;
+  };
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   constexpr int TN = DUAL ? BN / 2 : BN;  // output columns per workgroup
   const int64_t tiles_n = (g.N + TN - 1) / TN;
@@ -126,20 +166,26 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmArgs g, GroupArgs 
   const uint16_t* B2 = nullptr;
   if constexpr (DUAL)
     B2 = GROUP ? (const uint16_t*)ga.b2[grp] : (const uint16_t*)g.b2 + b * g.b_sb;
+  // BUF descriptors: A from its (batch) base; B from the lower of B1 / B2
+  const uint16_t* Bbase = (DUAL && B2 < B1) ? B2 : B1;
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, 0x7fffffffu);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(Bbase, 0x7fffffffu);
 
-  // ---- per-lane source pointers of this wave's 8 A and 8 B load instructions ------
-  // Instruction q of wave w fills LDS block i = 8 w + q (1 KiB).
-  const uint16_t* pa[8];
-  const uint16_t* pb[8];
-  // K-tail bookkeeping: the k-chunk (0..7) each lane fetches for A (and B
-  // when K-contiguous), or the k-row (0..63) when B is N-contiguous
-  int a_kc[8], b_sel[8];
+  // ---- per-lane sources of this wave's 4 A and 4 B DMA instructions per k-tile ----
+  // Instruction q of wave w fills the stage's 1 KiB block i = 4 w + q of A
+  // (and of B).
+  const uint16_t* pa[4];
+  const uint16_t* pb[4];
+  uint32_t va[4], vb[4];  // BUF: byte offsets from the descriptor bases
+  // K-tail bookkeeping: the k-chunk (0..3) each lane fetches for A (and B
+  // when K-contiguous), or the k-row (0..31) when B is N-contiguous
+  int a_kc[4], b_sel[4];
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const int i = wave * 8 + q;
-    // A block i: rows 8 i .. 8 i + 7, lane -> (row, physical chunk)
-    const int r = 8 * i + (lane >> 3);
-    const int c = (lane & 7) ^ ((r >> 1) & 7);
+  for (int q = 0; q < 4; ++q) {
+    const int i = wave * 4 + q;
+    // A block i: rows 16 i .. 16 i + 15, lane -> (row, physical chunk)
+    const int r = 16 * i + (lane >> 2);
+    const int c = (lane & 3) ^ ((r >> 2) & 3);
     const int rr = r < m_rows ? r : (int)m_rows - 1;
     int64_t arow;
     if constexpr (GROUP)
@@ -148,12 +194,14 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmArgs g, GroupArgs 
       arow = row0 + rr;
     pa[q] = A + arow * g.a_sm + c * 8;
     a_kc[q] = c;
+    va[q] = (uint32_t)((arow * g.a_sm + c * 8) * 2);
     if constexpr (B_KC) {
-      // B [N, K]: block i holds n-rows 8 i .. 8 i + 7 like A
+      // B [N, K]: block i holds n-rows 16 i .. 16 i + 15 like A
       int64_t nr = n0 + r;
       if (nr >= g.N) nr = g.N - 1;
       pb[q] = B1 + nr * g.b_sn + c * 8;
       b_sel[q] = c;
+      vb[q] = (uint32_t)((nr * g.b_sn + c * 8) * 2);
     } else {
       // B [K, N]: block i holds k-rows 2 i, 2 i + 1 (512 bytes each)
       const int kr = 2 * i + (lane >> 5);
@@ -170,57 +218,71 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmArgs g, GroupArgs 
       if (col > g.N - 8) col = g.N - 8;
       pb[q] = src + (int64_t)kr * g.b_sk + col;
       b_sel[q] = kr;
+      vb[q] = (uint32_t)((const uint8_t*)src - (const uint8_t*)Bbase) +
+              (uint32_t)(((int64_t)kr * g.b_sk + col) * 2);
     }
   }
 
-  // One k-tile of DMA loads.  Branch-free (it is interleaved with MFMAs):
-  // on the partial last k-tile the lanes whose chunk lies past K fetch an
-  // in-range chunk of the same row instead (a select, not a branch), and
-  // clear_tail zeroes those slots once they have landed.
+  // One k-tile of DMA loads.  Branch-free (it is interleaved with MFMAs).
+  // K-tail path: lanes whose chunk lies past K fetch an in-range chunk of
+  // the same row instead (a select, not a branch), and clear_tail zeroes
+  // those slots once they have landed.
   auto issue = [&](uint8_t* stage, int k0) {
-    uint8_t* sa = stage + wave * 8 * 1024;
-    uint8_t* sb = stage + A_BYTES + wave * 8 * 1024;
+    uint8_t* sa = stage + wave * 4096;
+    uint8_t* sb = stage + A_BYTES + wave * 4096;
+    if constexpr (BUF) {
+      const uint32_t soa = (uint32_t)k0 * 2;
+      const uint32_t sob = B_KC ? (uint32_t)k0 * 2 : (uint32_t)(k0 * g.b_sk * 2);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int ka = k0 + a_kc[q] * 8 < K ? k0 : K - 8 - a_kc[q] * 8;
-      to_lds16(pa[q] + ka, sa + q * 1024);
-    }
+      for (int q = 0; q < 4; ++q) buf_to_lds16(ra, va[q], soa, sa + q * 1024);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      if (B_KC) {
-        const int kb = k0 + b_sel[q] * 8 < K ? k0 : K - 8 - b_sel[q] * 8;
-        to_lds16(pb[q] + kb, sb + q * 1024);
-      } else {
-        const int kb = k0 + b_sel[q] < K ? k0 : K - 1 - b_sel[q];
-        to_lds16(pb[q] + (int64_t)kb * g.b_sk, sb + q * 1024);
+      for (int q = 0; q < 4; ++q) buf_to_lds16(rb, vb[q], sob, sb + q * 1024);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int ka = k0 + a_kc[q] * 8 < K ? k0 : K - 8 - a_kc[q] * 8;
+        to_lds16(pa[q] + ka, sa + q * 1024);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (B_KC) {
+          const int kb = k0 + b_sel[q] * 8 < K ? k0 : K - 8 - b_sel[q] * 8;
+          to_lds16(pb[q] + kb, sb + q * 1024);
+        } else {
+          const int kb = k0 + b_sel[q] < K ? k0 : K - 1 - b_sel[q];
+          to_lds16(pb[q] + (int64_t)kb * g.b_sk, sb + q * 1024);
+        }
       }
     }
   };
+  // (K-tail path) zero this wave's slots of a partial k-tile and wait for
+  // the writes, before the barrier that publishes the tile
   auto clear_tail = [&](uint8_t* stage, int k0) {
-    uint8_t* sa = stage + wave * 8 * 1024 + lane * 16;
-    uint8_t* sb = stage + A_BYTES + wave * 8 * 1024 + lane * 16;
+    uint8_t* sa = stage + wave * 4096 + lane * 16;
+    uint8_t* sb = stage + A_BYTES + wave * 4096 + lane * 16;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
+    for (int q = 0; q < 4; ++q) {
       if (k0 + a_kc[q] * 8 >= K) *(uint4*)(sa + q * 1024) = make_uint4(0, 0, 0, 0);
       const bool dead = B_KC ? k0 + b_sel[q] * 8 >= K : k0 + b_sel[q] >= K;
       if (dead) *(uint4*)(sb + q * 1024) = make_uint4(0, 0, 0, 0);
     }
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
   };
 
   // ---- per-lane fragment offsets (bytes within a stage) ---------------------------
   // A: rows wm*128 + i*32 + (lane & 31), k-chunk 2 s + (lane >> 5)
   const int a_row = wm * 128 + (lane & 31);
-  int a_off[4];
+  int a_off[2];
 #pragma unroll
-  for (int s = 0; s < 4; ++s)
-    a_off[s] = a_row * 128 + (((2 * s + (lane >> 5)) ^ ((lane >> 1) & 7)) * 16);
-  int b_off[4];  // per fragment column block j (substep s adds s * 8192)
-  int bk_off[4];  // B_KC: per substep
+  for (int s = 0; s < 2; ++s)
+    a_off[s] = a_row * 64 + (((2 * s + (lane >> 5)) ^ ((a_row >> 2) & 3)) * 16);
+  int b_off[4];   // per fragment column block j (substep s adds s * 8192)
+  int bk_off[2];  // B_KC: per substep
   if constexpr (B_KC) {
     const int b_row = wn * 128 + (lane & 31);
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-      bk_off[s] = A_BYTES + b_row * 128 + (((2 * s + (lane >> 5)) ^ ((lane >> 1) & 7)) * 16);
+    for (int s = 0; s < 2; ++s)
+      bk_off[s] = A_BYTES + b_row * 64 + (((2 * s + (lane >> 5)) ^ ((b_row >> 2) & 3)) * 16);
   } else {
     const int grp16 = lane >> 4, s16 = lane & 15;
     const int kr = 8 * (grp16 >> 1) + (s16 >> 2);
@@ -242,11 +304,11 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmArgs g, GroupArgs 
   bf16x8_t fa[2][4], fb[2][4];
   auto read_frags = [&](const uint8_t* base, int s, int slot) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fa[slot][i] = *(const bf16x8_t*)(base + a_off[s] + i * 32 * 128);
+    for (int i = 0; i < 4; ++i) fa[slot][i] = *(const bf16x8_t*)(base + a_off[s] + i * 32 * 64);
     if constexpr (B_KC) {
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        fb[slot][j] = *(const bf16x8_t*)(base + bk_off[s] + j * 32 * 128);
+        fb[slot][j] = *(const bf16x8_t*)(base + bk_off[s] + j * 32 * 64);
     } else {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -258,36 +320,33 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmArgs g, GroupArgs 
       }
     }
   };
+  // The B fragment goes in the MFMA's first operand and the A fragment in
+  // the second, so the instruction computes the 32 x 32 block of C^T: lane
+  // l then holds row l % 32 of the C block, columns 8 (e / 4) + 4 (l / 32)
+  // + e % 4 for accumulator element e -- four consecutive columns per group
+  // of four elements, which the epilogue stores as one 8-byte chunk.  The
+  // products and their k order per element are the same either way.
   auto mfmas = [&](int slot) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[slot][i], fb[slot][j], acc[i][j],
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[slot][j], fa[slot][i], acc[i][j],
                                                             0, 0, 0);
   };
 
   // ---- main loop -------------------------------------------------------------------
-  // k-step over stage `cur` (fragments of substep 0 already in slot 0):
-  //   substeps 0-2: 16 MFMAs each, interleaved one-for-one with the 12
-  //     fragment reads of the next substep; the 16 DMA loads of the next
-  //     k-tile (into `nxt`) ride along with substep 0;
-  //   then: wait for the substep-3 fragments and this wave's DMA, zero the
-  //     K tail, barrier (every wave is done reading `cur`, every DMA into
-  //     `nxt` has landed);
-  //   substep 3: its 16 MFMAs overlap the reads of `nxt`'s first fragments.
-  // On the last k-step the DMA re-reads tile 0 into the unused stage (kept
+  // k-step kt over stage `cur` (its substep-0 fragments already in slot 0;
+  // the DMA of tiles kt + 1 .. kt + NS - 1 in flight):
+  //   substep 0: 16 MFMAs interleaved one-for-one with the 12 fragment
+  //     reads of substep 1;
+  //   wait until this wave's DMA of tile kt + 1 has landed (the NS - 2 later
+  //     tiles stay in flight) and the substep-1 fragments are in, barrier:
+  //     every wave is done reading `cur`, tile kt + 1 is complete in `nxt`;
+  //   substep 1: 16 MFMAs overlap the reads of `nxt`'s first fragments and
+  //     the 8 DMA loads of tile kt + NS into the now free `cur`.
+  // Past the last tile the DMA re-reads tile kt (an L2 hit; kept
   // branch-free so it can interleave); the final wait drains it.
-  // substep 0: 16 MFMAs interleaved with the 12 fragment reads of substep 1
-  // and the 16 DMA loads
-  auto pin_first = [&]() {
-#pragma unroll
-    for (int x = 0; x < 16; ++x) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // MFMA
-      if (x < 12) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);    // VMEM (DMA load)
-    }
-  };
   auto pin_reads = [&]() {
 #pragma unroll
     for (int x = 0; x < 12; ++x) {
@@ -296,67 +355,89 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmArgs g, GroupArgs 
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
   };
+  auto pin_last = [&]() {
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      if (x < 12) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      if (x < 8) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // VMEM (DMA)
+    }
+  };
   auto k_step = [&](uint8_t* cur, uint8_t* nxt, int kt) {
-    const bool more = kt + 1 < nk;
-    const int k_next = more ? (kt + 1) * BK : 0;
-    // substep 0 (+ first half of the DMA), substep 1 (+ second half)
     read_frags(cur, 1, 1);
-    issue(nxt, k_next);
-    mfmas(0);
-    pin_first();
-    __builtin_amdgcn_sched_barrier(0);
-    read_frags(cur, 2, 0);
-    mfmas(1);
-    pin_reads();
-    __builtin_amdgcn_sched_barrier(0);
-    read_frags(cur, 3, 1);
     mfmas(0);
     pin_reads();
     __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-    if (more && (kt + 2) * BK > K) clear_tail(nxt, k_next);
-    __syncthreads();
-    // (after the last k-step these reads of the unused stage are dead;
-    // keeping them unconditional avoids a branch that costs registers)
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm((NS - 2) * DMA_PER_TILE, 0));
+    if (!BUF && kt + 2 == nk && K % BK) clear_tail(nxt, (kt + 1) * BK);
+    block_barrier();
+    // (after the last k-step these reads are dead; keeping them
+    // unconditional avoids a branch that costs registers)
     read_frags(nxt, 0, 0);
+    issue(cur, (kt + NS < nk ? kt + NS : kt) * BK);
     mfmas(1);
-    pin_reads();
+    pin_last();
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  issue(smem0, 0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  if (K < BK) clear_tail(smem0, 0);
-  __syncthreads();
-  read_frags(smem0, 0, 0);
-  for (int kt = 0; kt < nk; kt += 2) {
-    k_step(smem0, smem1, kt);
-    if (kt + 1 < nk) k_step(smem1, smem0, kt + 1);
+#pragma unroll
+  for (int t = 0; t < NS; ++t) issue(S(t), (t < nk ? t : 0) * BK);
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm((NS - 1) * DMA_PER_TILE, 15));
+  if (!BUF && nk == 1 && K % BK) clear_tail(s0, 0);
+  block_barrier();
+  read_frags(s0, 0, 0);
+  // Whole turns of the ring, then the remaining (< NS) steps: no path
+  // re-enters the loop with a DMA into the stage it reads first still in
+  // flight, so the compiler adds no wait for one.
+  int kt = 0;
+  for (; kt + NS <= nk; kt += NS) {
+#pragma unroll
+    for (int j = 0; j < NS; ++j) k_step(S(j), S((j + 1) % NS), kt + j);
   }
-  // a possible last DMA (into the unused stage) must land before the
-  // epilogue reuses the LDS
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int j = 0; j < NS - 1; ++j)
+    if (kt + j < nk) k_step(S(j), S(j + 1), kt + j);
+  // the dummy DMAs (into the stages past the last tile) must land before
+  // the epilogue reuses the LDS
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
   __syncthreads();
 
   // ---- epilogue ----------------------------------------------------------------------
-  // phase 1: bf16(acc) into the C tile in LDS (the stages are free now)
-  // (rows 0..127 in smem0, rows 128..255 in smem1: wave row wm owns one)
+  // phase 1: bf16(acc) into the C tile in LDS (the ring is free now): rows
+  // 64 p .. 64 p + 63 in stage p, 512-byte rows, 16-byte chunk ch of row r
+  // stored at ch ^ (r & 15).  For block (i, j) and column group q = e / 4
+  // a lane holds 4 consecutive columns of one row: one ds_write_b64, and
+  // the 32 rows of a write spread over 16 chunk positions (2-way at most).
+  auto pack4 = [](const float* v) {
+    return make_uint2(vm::bf16x2_bits(v[0], v[1]), vm::bf16x2_bits(v[2], v[3]));
+  };
   {
-    uint16_t* Ch = (uint16_t*)(wm ? smem1 : smem0);
+    uint8_t* cb0 = S(2 * wm);      // rows wm * 128 + [0, 64)
+    uint8_t* cb1 = S(2 * wm + 1);  // rows wm * 128 + [64, 128)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i) {
+      uint8_t* cb = i < 2 ? cb0 : cb1;
+      const int lr = (i & 1) * 32 + (lane & 31);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int col = wn * 128 + j * 32 + (lane & 31);
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int row = i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-          Ch[row * CP + col] = vm::bf16_bits(acc[i][j][e]);
+        for (int q = 0; q < 4; ++q) {
+          const int col = wn * 128 + j * 32 + q * 8 + (lane >> 5) * 4;
+          float v[4];
+#pragma unroll
+          for (int x = 0; x < 4; ++x) v[x] = acc[i][j][q * 4 + x];
+          *(uint2*)(cb + lr * 512 + (((col >> 3) ^ (lr & 15)) * 16) + ((col >> 2) & 1) * 8) =
+              pack4(v);
         }
-      }
+    }
   }
   __syncthreads();
-  // phase 2: 16-byte row chunks with the bias / residual / gate operands
+  // phase 2: 16-byte row chunks (a row's 512 bytes per 32 lanes) with the
+  // bias / residual / gate operands
+  auto c_chunk = [&](int row, int lc) -> uint4 {
+    const int lr = row & 63;
+    return *(const uint4*)(S(row >> 6) + lr * 512 + ((((lc >> 3) ^ (lr & 15))) * 16));
+  };
   constexpr int OC = DUAL ? 128 : 256;
   constexpr int CH = OC / 8;
   uint16_t* C = (uint16_t*)g.c + b * g.c_sb;
@@ -364,18 +445,21 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmArgs g, GroupArgs 
   const uint16_t* bias2 = nullptr;
   if constexpr (DUAL) bias2 = (const uint16_t*)(GROUP ? ga.bias2[grp] : g.bias2);
   const uint16_t* res = (const uint16_t*)g.res + b * g.res_sb;
-  for (int t = tid; t < BM * CH; t += 256) {
+  // (a runtime loop: the epilogue runs once per tile, and unrolled it would
+  // stream tens of KB of straight-line code through the instruction cache)
+#pragma unroll 1
+  for (int it = 0; it < BM * CH / 256; ++it) {
+    const int t = it * 256 + tid;
     const int row = t / CH, ch = t - row * CH;
     const int64_t m = row0 + row;
     const int64_t n = n0 + ch * 8;
     if (row >= m_rows || n >= g.N) continue;
     const int lc = DUAL ? (ch >> 3) * 128 + (ch & 7) * 8 : ch * 8;
-    const uint16_t* Cs = (const uint16_t*)(row >= 128 ? smem1 : smem0) + (row & 127) * CP;
-    const uint4 dv = *(const uint4*)(Cs + lc);
+    const uint4 dv = c_chunk(row, lc);
     const uint16_t* dh = (const uint16_t*)&dv;
     uint16_t out[8];
     if constexpr (DUAL) {
-      const uint4 uv = *(const uint4*)(Cs + lc + 64);
+      const uint4 uv = c_chunk(row, lc + 64);
       const uint4 bg = *(const uint4*)(bias + n);
       const uint4 bu = *(const uint4*)(bias2 + n);
       const uint16_t* uh = (const uint16_t*)&uv;
@@ -436,6 +520,23 @@ bool gemm_lds_ok(const GemmArgs& g, bool* b_kc) {
   return true;
 }
 
+// Whether the buffer-descriptor DMA path can run g: K a multiple of BK and
+// every byte offset the kernel forms (row offset + k advance) below 2^31.
+static bool buf_ok(const GemmArgs& g, const GroupArgs* ga, bool bkc, bool dual) {
+  constexpr int64_t kLim = (int64_t)1 << 31;
+  if (g.K % BK) return false;
+  const int64_t a_span = ((g.M - 1) * g.a_sm + g.K) * 2;
+  int64_t b_span = bkc ? ((g.N - 1) * g.b_sn + g.K) * 2 : ((g.K - 1) * g.b_sk + g.N) * 2;
+  if (dual) {
+    int64_t d = -1;
+    if (ga) d = ga->dual_span;
+    else d = (int64_t)((uintptr_t)g.b2 - (uintptr_t)g.b);
+    if (ga && d < 0) return false;
+    b_span += d < 0 ? -d : d;
+  }
+  return a_span < kLim && b_span < kLim;
+}
+
 void launch_gemm_lds(const GemmArgs& g, const GroupArgs* ga, hipStream_t stream) {
   bool bkc = false;
   if (!gemm_lds_ok(g, &bkc)) fail(REW_MI355X_ERR_INVALID, "internal: gemm_lds not launchable");
@@ -447,8 +548,14 @@ void launch_gemm_lds(const GemmArgs& g, const GroupArgs* ga, hipStream_t stream)
   const GroupArgs none{};
   const GroupArgs& G = ga ? *ga : none;
   const dim3 grid((unsigned)tiles), block(256);
-#define REW_LDS_LAUNCH(BKC, DU, GR) \
-  hipLaunchKernelGGL((gemm_lds_kernel<BKC, DU, GR>), grid, block, 0, stream, g, G)
+  const bool buf = buf_ok(g, ga, bkc, dual);
+#define REW_LDS_LAUNCH(BKC, DU, GR)                                                        \
+  do {                                                                                    \
+    if (buf)                                                                              \
+      hipLaunchKernelGGL((gemm_lds_kernel<BKC, DU, GR, true>), grid, block, 0, stream, g, G); \
+    else                                                                                  \
+      hipLaunchKernelGGL((gemm_lds_kernel<BKC, DU, GR, false>), grid, block, 0, stream, g, G); \
+  } while (0)
   if (ga) {
     if (dual) REW_LDS_LAUNCH(false, true, true);
     else if (bkc) REW_LDS_LAUNCH(true, false, true);

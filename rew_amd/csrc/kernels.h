@@ -90,6 +90,9 @@ struct GroupArgs {
   const void* const* b2;
   const void* const* bias;
   const void* const* bias2;
+  // host side: the largest |b2[i] - b[i]| in bytes (the dual B operands
+  // share one buffer descriptor when it is small), -1 when not known
+  int64_t dual_span = -1;
 };
 // Whether launch_gemm_grouped can run g (dtype, layout, epilogue, 32-bit
 // buffer extents).

@@ -2041,6 +2041,11 @@ bool Lower::emit_moe(Tensor* t, const MoePlan& p) {
   ga.b2 = tbl + n;
   ga.bias = tbl + 2 * n;
   ga.bias2 = tbl + 3 * n;
+  ga.dual_span = 0;
+  for (int i = 0; i < n; ++i) {
+    const int64_t d = (int64_t)((uintptr_t)ptrs[n + i] - (uintptr_t)ptrs[i]);
+    ga.dual_span = std::max(ga.dual_span, d < 0 ? -d : d);
+  }
   gd.a = hbuf->data();
   gd.M = R;
   gd.a_sm = I;

@@ -26,18 +26,26 @@ __device__ __forceinline__ uint32_t fdiv(uint32_t x, const FastDiv& f) {
 __device__ __forceinline__ float as_f(uint32_t u) { return __uint_as_float(u); }
 __device__ __forceinline__ uint32_t as_u(float f) { return __float_as_uint(f); }
 
-__device__ __forceinline__ float round_bf16(float f) {
-  uint32_t u = as_u(f);
-  if ((u & 0x7f800000u) == 0x7f800000u) {
-    return (u & 0x007fffffu) ? as_f((u | 0x00400000u) & 0xffff0000u)
-                             : f;  // inf stays inf
-  }
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return as_f(u & 0xffff0000u);
+// f32 -> bf16 bits, round to nearest even; a NaN stays a NaN with its sign,
+// its top payload bits and the quiet bit set ((u | 0x400000) >> 16), inf
+// stays inf, overflow rounds to inf.  gfx950's v_cvt_pk_bf16_f32 implements
+// exactly this rule (checked against the integer formulation on every
+// class of input: ties, denormals, infinities, NaN payloads), so it replaces
+// the branchy integer code.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t bf16x2_bits(float lo, float hi) {
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
 __device__ __forceinline__ uint16_t bf16_bits(float f) {
-  return (uint16_t)(as_u(round_bf16(f)) >> 16);
+  return (uint16_t)bf16x2_bits(f, 0.0f);
+}
+
+__device__ __forceinline__ float round_bf16(float f) {
+  return as_f((uint32_t)bf16_bits(f) << 16);
 }
 
 __device__ __forceinline__ float round_f16(float f) {
