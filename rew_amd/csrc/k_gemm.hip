@@ -717,6 +717,7 @@ static bool use_256(const GemmArgs& g, bool akc) {
 
 bool gemm_epilogue_ok(const GemmArgs& g) {
   if (g.epi == EPI_NONE) return true;
+  if (g.epi == EPI_BIAS_ROPE) return false;  // launch_gemm_multi only
   if (g.c_dtype != REW_DT_BFLOAT16 && g.c_dtype != REW_DT_FLOAT32) return false;
   if (g.epi != EPI_SWIGLU) return true;
   bool lkc;

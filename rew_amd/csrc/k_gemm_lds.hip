@@ -43,6 +43,8 @@
 // the epilogue writes them to a C tile in LDS as 8-byte chunks, then stores
 // whole 512-byte row segments with the fused bias / residual / SwiGLU
 // arithmetic of GemmArgs.
+#include <cstring>
+
 #include "kernels.h"
 #include "vm_device.h"
 
@@ -116,7 +118,7 @@ __device__ __forceinline__ void tile_order(int64_t bid, int64_t tiles_m, int64_t
 // BUF: K % BK == 0 and every operand byte offset below 2^31 from its
 // descriptor base (checked at launch); the K-tail path then never runs.
 template <bool B_KC, bool DUAL, bool GROUP, bool BUF>
-__global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmArgs g, GroupArgs ga) {
+__global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs ga) {
   __shared__ __attribute__((aligned(1024))) uint8_t s0[STAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t s1[STAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t s2[STAGE];
@@ -131,12 +133,12 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmArgs g, GroupArgs 
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   constexpr int TN = DUAL ? BN / 2 : BN;  // output columns per workgroup
-  const int64_t tiles_n = (g.N + TN - 1) / TN;
 
-  // ---- tile ------------------------------------------------------------------------
+  // ---- tile (and, over several GEMMs of one A, its segment) ---------------------------
   int64_t b = 0, tm = 0, tn = 0, m_rows, row0;
-  int grp = 0;
+  int grp = 0, seg = 0;
   if constexpr (GROUP) {
+    const int64_t tiles_n = (gs.g[0].N + TN - 1) / TN;
     const int64_t total = ga.max_mtiles * tiles_n;
     int64_t t = blockIdx.x;
     if (total % 8 == 0) t = (t % 8) * (total / 8) + t / 8;
@@ -153,10 +155,14 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmArgs g, GroupArgs 
     row0 = ga.off[grp] + (tm - ga.mt_start[grp]) * BM;
     m_rows = min((int64_t)BM, (int64_t)ga.off[grp + 1] - row0);
   } else {
-    tile_order(blockIdx.x, (g.M + BM - 1) / BM, tiles_n, g.batch, &b, &tm, &tn);
+    tile_order(blockIdx.x, (gs.g[0].M + BM - 1) / BM, gs.tn0[gs.n], gs.g[0].batch, &b, &tm,
+               &tn);
+    while (seg + 1 < gs.n && tn >= gs.tn0[seg + 1]) ++seg;
+    tn -= gs.tn0[seg];
     row0 = tm * BM;
-    m_rows = min((int64_t)BM, g.M - row0);
+    m_rows = min((int64_t)BM, gs.g[0].M - row0);
   }
+  const GemmArgs& g = gs.g[seg];
   const int64_t n0 = tn * TN;
   const int K = (int)g.K;
   const int nk = (K + BK - 1) / BK;
@@ -483,6 +489,32 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmArgs g, GroupArgs 
       if (g.epi == EPI_NONE) {
 #pragma unroll
         for (int x = 0; x < 8; ++x) out[x] = dh[x];
+      } else if (g.epi == EPI_BIAS_ROPE) {
+        // Linear's bias add, then applyRotate (rope.nim:56-108) on the four
+        // pairs of this chunk, scattered into the rotated tensor's layout
+        const uint4 bv = *(const uint4*)(bias + n);
+        const uint16_t* bh = (const uint16_t*)&bv;
+        const uint32_t mm = (uint32_t)m, nn = (uint32_t)n;
+        const uint32_t bq = mm / (uint32_t)g.rope_S, sq = mm - bq * (uint32_t)g.rope_S;
+        const uint32_t hq = nn / (uint32_t)g.rope_D, dq = nn - hq * (uint32_t)g.rope_D;
+        const int64_t tb = bq * g.rope_tb + sq * g.rope_ts + hq * g.rope_th + (dq >> 1) * g.rope_ti;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const float x0 = vm::round_bf16(vm::as_f((uint32_t)dh[2 * u] << 16) +
+                                          vm::as_f((uint32_t)bh[2 * u] << 16));
+          const float x1 = vm::round_bf16(vm::as_f((uint32_t)dh[2 * u + 1] << 16) +
+                                          vm::as_f((uint32_t)bh[2 * u + 1] << 16));
+          const float cs = g.rope_cos[tb + u * g.rope_ti];
+          const float sn = g.rope_sin[tb + u * g.rope_ti];
+          const float t1 = cs * x0;
+          const float t2 = sn * x1;
+          const float t3 = sn * x0;
+          const float t4 = cs * x1;
+          out[2 * u] = vm::bf16_bits(t1 - t2);
+          out[2 * u + 1] = vm::bf16_bits(t3 + t4);
+        }
+        *(uint4*)(C + bq * g.out_b + sq * g.out_s + hq * g.out_h + dq) = *(const uint4*)out;
+        continue;
       } else {
         const uint4 bv = *(const uint4*)(bias + n);
         const uint16_t* bh = (const uint16_t*)&bv;
@@ -517,6 +549,11 @@ bool gemm_lds_ok(const GemmArgs& g, bool* b_kc) {
   if (g.epi != EPI_NONE && !al16(g.bias)) return false;
   if (g.epi == EPI_SWIGLU && (*b_kc || !al16(g.bias2) || !al16(g.b2))) return false;
   if (g.epi == EPI_BIAS_RES && (!al16(g.res) || g.res_sm % 8 || g.res_sb % 8)) return false;
+  if (g.epi == EPI_BIAS_ROPE &&
+      (g.batch != 1 || g.rope_S <= 0 || g.rope_D <= 0 || g.rope_D % 8 || g.N % g.rope_D ||
+       g.M % g.rope_S || g.M >= (1ll << 31) || g.N >= (1ll << 31) || !g.rope_cos ||
+       !g.rope_sin || g.out_b % 8 || g.out_s % 8 || g.out_h % 8))
+    return false;
   return true;
 }
 
@@ -537,24 +574,23 @@ static bool buf_ok(const GemmArgs& g, const GroupArgs* ga, bool bkc, bool dual) 
   return a_span < kLim && b_span < kLim;
 }
 
-void launch_gemm_lds(const GemmArgs& g, const GroupArgs* ga, hipStream_t stream) {
-  bool bkc = false;
-  if (!gemm_lds_ok(g, &bkc)) fail(REW_MI355X_ERR_INVALID, "internal: gemm_lds not launchable");
+static void launch_segs(const GemmSegs& gs, const GroupArgs* ga, bool bkc, bool buf,
+                        hipStream_t stream) {
+  const GemmArgs& g = gs.g[0];
   const bool dual = g.epi == EPI_SWIGLU;
-  const int64_t tn = (g.N + (dual ? 127 : 255)) / (dual ? 128 : 256);
-  const int64_t tiles = ga ? ga->max_mtiles * tn : ((g.M + 255) / 256) * tn * g.batch;
+  const int64_t tiles = ga ? ga->max_mtiles * gs.tn0[gs.n]
+                           : ((g.M + 255) / 256) * gs.tn0[gs.n] * g.batch;
   if (tiles <= 0) return;
   if (tiles >= (1ll << 31)) fail(REW_MI355X_ERR_INVALID, "internal: gemm_lds grid too large");
   const GroupArgs none{};
   const GroupArgs& G = ga ? *ga : none;
   const dim3 grid((unsigned)tiles), block(256);
-  const bool buf = buf_ok(g, ga, bkc, dual);
-#define REW_LDS_LAUNCH(BKC, DU, GR)                                                        \
-  do {                                                                                    \
-    if (buf)                                                                              \
-      hipLaunchKernelGGL((gemm_lds_kernel<BKC, DU, GR, true>), grid, block, 0, stream, g, G); \
-    else                                                                                  \
-      hipLaunchKernelGGL((gemm_lds_kernel<BKC, DU, GR, false>), grid, block, 0, stream, g, G); \
+#define REW_LDS_LAUNCH(BKC, DU, GR)                                                           \
+  do {                                                                                       \
+    if (buf)                                                                                 \
+      hipLaunchKernelGGL((gemm_lds_kernel<BKC, DU, GR, true>), grid, block, 0, stream, gs, G); \
+    else                                                                                     \
+      hipLaunchKernelGGL((gemm_lds_kernel<BKC, DU, GR, false>), grid, block, 0, stream, gs, G); \
   } while (0)
   if (ga) {
     if (dual) REW_LDS_LAUNCH(false, true, true);
@@ -567,6 +603,52 @@ void launch_gemm_lds(const GemmArgs& g, const GroupArgs* ga, hipStream_t stream)
   }
 #undef REW_LDS_LAUNCH
   REW_HIP(hipGetLastError());
+}
+
+void launch_gemm_lds(const GemmArgs& g, const GroupArgs* ga, hipStream_t stream) {
+  bool bkc = false;
+  if (!gemm_lds_ok(g, &bkc)) fail(REW_MI355X_ERR_INVALID, "internal: gemm_lds not launchable");
+  const bool dual = g.epi == EPI_SWIGLU;
+  GemmSegs gs;
+  std::memset(&gs, 0, sizeof gs);
+  gs.n = 1;
+  gs.g[0] = g;
+  gs.tn0[1] = (g.N + (dual ? 127 : 255)) / (dual ? 128 : 256);
+  launch_segs(gs, ga, bkc, buf_ok(g, ga, bkc, dual), stream);
+}
+
+bool gemm_multi_ok(const GemmArgs* segs, int n) {
+  if (n < 1 || n > kMaxSegs) return false;
+  bool bkc0 = false;
+  for (int i = 0; i < n; ++i) {
+    const GemmArgs& g = segs[i];
+    bool bkc;
+    if (!gemm_lds_ok(g, &bkc) || g.epi == EPI_SWIGLU) return false;
+    if (i == 0) {
+      bkc0 = bkc;
+      continue;
+    }
+    const GemmArgs& f = segs[0];
+    if (bkc != bkc0 || g.a != f.a || g.M != f.M || g.K != f.K || g.a_sm != f.a_sm ||
+        g.a_sb != f.a_sb || g.batch != f.batch)
+      return false;
+  }
+  return true;
+}
+
+void launch_gemm_multi(const GemmArgs* segs, int n, hipStream_t stream) {
+  if (!gemm_multi_ok(segs, n)) fail(REW_MI355X_ERR_INVALID, "internal: GEMM set not launchable");
+  GemmSegs gs;
+  std::memset(&gs, 0, sizeof gs);
+  gs.n = n;
+  bool bkc = false, buf = true;
+  for (int i = 0; i < n; ++i) {
+    gemm_lds_ok(segs[i], &bkc);
+    buf = buf && buf_ok(segs[i], nullptr, bkc, false);
+    gs.g[i] = segs[i];
+    gs.tn0[i + 1] = gs.tn0[i] + (segs[i].N + 255) / 256;
+  }
+  launch_segs(gs, nullptr, bkc, buf, stream);
 }
 
 }  // namespace rew

@@ -65,8 +65,23 @@ struct GemmArgs {
   const void* res;
   int64_t res_sb, res_sm;
   const void* b2;
+  // EPI_BIAS_ROPE (bf16, batch 1): y = rnd(rnd(acc) + bias[n]) as EPI_BIAS,
+  // then rew's applyRotate on the adjacent pairs (2i, 2i+1) of each head
+  // (src/rew/nn/rope.nim:56-108): with row m = b * rope_S + s and column
+  // n = h * rope_D + d,
+  //   c = rope_cos[t], sn = rope_sin[t], t = b tb + s ts + h th + (d / 2) ti
+  //   out[d] = bf16(c y[d] - sn y[d+1]),  out[d+1] = bf16(sn y[d] + c y[d+1])
+  // (each product and sum rounded to fp32), stored at
+  //   c + b out_b + s out_s + h out_h + d   (c_sm / c_sb unused).
+  const float* rope_cos;
+  const float* rope_sin;
+  int64_t rope_S, rope_D;
+  int64_t rope_tb, rope_ts, rope_th, rope_ti;
+  int64_t out_b, out_s, out_h;
 };
-enum GemmEpi : int { EPI_NONE = 0, EPI_BIAS = 1, EPI_BIAS_RES = 2, EPI_SWIGLU = 3 };
+enum GemmEpi : int {
+  EPI_NONE = 0, EPI_BIAS = 1, EPI_BIAS_RES = 2, EPI_SWIGLU = 3, EPI_BIAS_ROPE = 4
+};
 void launch_gemm(const GemmArgs& g, hipStream_t stream);
 
 // Grouped GEMM over packed rows (the routed experts of a MoE layer).  Group
@@ -104,6 +119,18 @@ void launch_gemm_grouped(const GemmArgs& g, const GroupArgs& ga, hipStream_t str
 // the grouped mode.
 bool gemm_lds_ok(const GemmArgs& g, bool* b_kc);
 void launch_gemm_lds(const GemmArgs& g, const GroupArgs* ga, hipStream_t stream);
+// Up to kMaxSegs GEMMs over one A matrix (same a, M, K, strides) in one
+// launch: segment i owns the output-column tiles [tn0[i], tn0[i + 1]) and
+// keeps its own B, bias, C and epilogue (EPI_NONE / EPI_BIAS /
+// EPI_BIAS_RES / EPI_BIAS_ROPE).  gemm_multi_ok checks that the set can run.
+constexpr int kMaxSegs = 3;
+struct GemmSegs {
+  int n;
+  int64_t tn0[kMaxSegs + 1];
+  GemmArgs g[kMaxSegs];
+};
+bool gemm_multi_ok(const GemmArgs* segs, int n);
+void launch_gemm_multi(const GemmArgs* segs, int n, hipStream_t stream);
 // Whether launch_gemm runs g with its epilogue (EPI_SWIGLU needs the large
 // dual kernel; the others run on every MFMA kernel).
 bool gemm_epilogue_ok(const GemmArgs& g);

@@ -214,6 +214,15 @@ struct GemmPlan {
   Tensor* bias = nullptr;
   Tensor* bias2 = nullptr;
   Tensor* res = nullptr;
+  // EPI_BIAS_ROPE: the rotated tensor is [B, H, S, D] (rope_t, the
+  // projection reshaped to [B, S, H, D] and transposed) or [B, S, H, D]
+  Tensor* rope_cos = nullptr;  // the applyRotate chain's fp32 table views
+  Tensor* rope_sin = nullptr;
+  bool rope_t = false;
+  int64_t rope_B = 0, rope_S = 0, rope_H = 0, rope_D = 0;
+  // projections of one input launched together (GroupedQueryAttention's
+  // q / k / v): index into Lower::gemm_groups, or -1
+  int group = -1;
 };
 
 // rmsNorm chain (src/rew/nn/norm.nim:204-224) lowered to one row kernel.
@@ -261,6 +270,7 @@ struct Lower {
   std::unordered_map<Tensor*, RopePlan> rope_out;
   std::unordered_map<Tensor*, MoePlan> moe_out;
   std::unordered_map<Tensor*, Node*> flash_out;  // transposed flash output -> PV node
+  std::vector<std::vector<Tensor*>> gemm_groups;  // outputs of sibling projections
 
   explicit Lower(Ctx* ctx) : c(ctx) {}
 
@@ -274,6 +284,10 @@ struct Lower {
   bool emit_rope(Tensor* t, const RopePlan& p);
   bool rows_view(Tensor* x, int64_t n, const void** ptr, int64_t* rs);
   bool emit_gemm_fused(Tensor* t, const GemmPlan& p);
+  bool gemm_fused_args(Tensor* t, const GemmPlan& p, GemmArgs& g);
+  bool fuse_rope(const RopePlan& rp, Tensor* out);
+  void match_gemm_groups();
+  void view4(Tensor* v, int r, const void** ptr, int64_t* s);
   bool emit_flash(Node* pv, const FlashPlan& fp);
   void match_flash_out();
   bool kv_operand(Tensor* t, int H, const void** ptr, int64_t* sb, int64_t* sh,
@@ -1711,8 +1725,8 @@ void Lower::match_gemm_epilogues() {
   }
 }
 
-bool Lower::emit_gemm_fused(Tensor* t, const GemmPlan& p) {
-  GemmArgs g;
+// Kernel arguments of a planned GEMM (all but the output pointer).
+bool Lower::gemm_fused_args(Tensor* t, const GemmPlan& p, GemmArgs& g) {
   Tensor *ta, *tb;
   dot_args(p.dot, g, ta, tb);
   if (g.batch != 1 || g.K == 0 || t->numel() != g.M * g.N || t->dt != g.c_dtype) return false;
@@ -1752,24 +1766,142 @@ bool Lower::emit_gemm_fused(Tensor* t, const GemmPlan& p) {
     g.res_sm = g.N;
     g.res_sb = 0;
   }
-  if (!gemm_epilogue_ok(g)) return false;
-  tensor_alloc(t);
-  g.c = t->data();
+  if (p.epi == EPI_BIAS_ROPE) {
+    const int64_t B = p.rope_B, S = p.rope_S, H = p.rope_H, D = p.rope_D;
+    if (g.M != B * S || g.N != H * D) return false;
+    int64_t sc[4], sn[4];
+    const void *pc, *ps;
+    view4(p.rope_cos, 4, &pc, sc);
+    view4(p.rope_sin, 4, &ps, sn);
+    for (int i = 0; i < 4; ++i)
+      if (sc[i] != sn[i]) return false;
+    g.rope_cos = (const float*)pc;
+    g.rope_sin = (const float*)ps;
+    g.rope_S = S;
+    g.rope_D = D;
+    g.rope_tb = sc[0];
+    g.rope_ti = sc[3];
+    if (p.rope_t) {  // [B, H, S, D]
+      g.rope_th = sc[1];
+      g.rope_ts = sc[2];
+      g.out_b = H * S * D;
+      g.out_h = S * D;
+      g.out_s = D;
+    } else {  // [B, S, H, D]
+      g.rope_ts = sc[1];
+      g.rope_th = sc[2];
+      g.out_b = S * H * D;
+      g.out_s = H * D;
+      g.out_h = D;
+    }
+  }
   g.c_sb = g.M * g.N;
   g.c_sm = g.N;
+  return true;
+}
+
+static const char* epi_suffix(int epi) {
+  switch (epi) {
+    case EPI_BIAS: return "+bias";
+    case EPI_BIAS_RES: return "+bias+res";
+    case EPI_BIAS_ROPE: return "+bias+rope";
+    default: return "";
+  }
+}
+
+bool Lower::emit_gemm_fused(Tensor* t, const GemmPlan& p) {
+  if (p.group >= 0) {
+    // the planned siblings (q / k / v of one input) in one launch
+    std::vector<Tensor*> outs = {t};
+    std::vector<GemmPlan> plans = {p};
+    for (Tensor* u : gemm_groups[p.group]) {
+      auto it = gemm_out.find(u);
+      if (u == t || it == gemm_out.end() || u->st) continue;
+      outs.push_back(u);
+      plans.push_back(it->second);
+    }
+    std::vector<GemmArgs> args(outs.size());
+    bool ok = outs.size() >= 2 && outs.size() <= (size_t)kMaxSegs;
+    for (size_t i = 0; ok && i < outs.size(); ++i)
+      ok = gemm_fused_args(outs[i], plans[i], args[i]);
+    if (ok) ok = gemm_multi_ok(args.data(), (int)args.size());
+    if (ok) {
+      int64_t n_all = 0;
+      std::string parts;
+      for (size_t i = 0; i < outs.size(); ++i) {
+        tensor_alloc(outs[i]);
+        args[i].c = outs[i]->data();
+        n_all += args[i].N;
+        parts += std::string(i ? "," : "") + std::to_string(args[i].N) + epi_suffix(args[i].epi);
+        if (i) gemm_out.erase(outs[i]);
+      }
+      if (c->profiling) {
+        char nm[200];
+        std::snprintf(nm, sizeof nm, "gemm_lds_nn{%s}[1,%lld,%lld,%lld]", parts.c_str(),
+                      (long long)args[0].M, (long long)n_all, (long long)args[0].K);
+        prof_begin(c, nm);
+      }
+      launch_gemm_multi(args.data(), (int)args.size(), c->stream);
+      prof_end(c);
+      note_launch(c, true);
+      return true;
+    }
+    // otherwise each member is launched on its own
+  }
+  GemmArgs g;
+  if (!gemm_fused_args(t, p, g)) return false;
+  if (p.epi == EPI_BIAS_ROPE) {
+    if (!gemm_multi_ok(&g, 1)) return false;
+  } else if (!gemm_epilogue_ok(g)) {
+    return false;
+  }
+  tensor_alloc(t);
+  g.c = t->data();
   if (c->profiling) {
     char nm[160];
-    std::snprintf(nm, sizeof nm, "%s%s[%lld,%lld,%lld,%lld]", gemm_variant(g),
-                  p.epi == EPI_BIAS ? "+bias" : (p.epi == EPI_BIAS_RES ? "+bias+res" : ""),
+    std::snprintf(nm, sizeof nm, "%s%s[%lld,%lld,%lld,%lld]",
+                  p.epi == EPI_BIAS_ROPE ? "gemm_lds_nn" : gemm_variant(g), epi_suffix(p.epi),
                   (long long)g.batch, (long long)g.M, (long long)g.N, (long long)g.K);
     prof_begin(c, nm);
   }
-  launch_gemm(g, c->stream);
+  if (p.epi == EPI_BIAS_ROPE) launch_gemm_multi(&g, 1, c->stream);
+  else launch_gemm(g, c->stream);
   prof_end(c);
   note_launch(c, true);
   return true;
 }
 
+// Projections of one input that are all planned as fused GEMMs (the q, k and
+// v projections of GroupedQueryAttention.forward, groupedqueryattention.nim)
+// become one multi-segment launch.
+void Lower::match_gemm_groups() {
+  std::unordered_map<Tensor*, std::vector<Tensor*>> by_a;
+  std::vector<Tensor*> order;
+  for (Node* n : nodes)
+    for (Tensor* t : n->out) {
+      auto it = gemm_out.find(t);
+      if (it == gemm_out.end()) continue;
+      const GemmPlan& gp = it->second;
+      if (gp.epi != EPI_BIAS && gp.epi != EPI_BIAS_ROPE && gp.epi != EPI_BIAS_RES) continue;
+      // key: the input seen through reshapes (q, k and v each reshape the
+      // same normed tensor) plus its shape as a matrix
+      Tensor* a = gp.dot->in[0];
+      while (a->prod && a->prod->kind == K_RESHAPE && !a->st) a = a->prod->in[0];
+      if (gp.dot->in[0]->shape.rank != 2) continue;
+      if (!by_a.count(a)) order.push_back(a);
+      by_a[a].push_back(t);
+    }
+  for (Tensor* a : order) {
+    std::vector<Tensor*>& v = by_a[a];
+    for (size_t i = 0; i + 1 < v.size(); i += kMaxSegs) {
+      const size_t n = std::min(v.size() - i, (size_t)kMaxSegs);
+      if (n < 2) break;
+      const int id = (int)gemm_groups.size();
+      gemm_groups.emplace_back(v.begin() + i, v.begin() + i + n);
+      for (size_t j = i; j < i + n; ++j) gemm_out[v[j]].group = id;
+    }
+  }
+}
 
 // ---------------------------------------------------------------------------
 // routed mixture of experts (src/rew/models/deepseek.nim:114-145)
@@ -2249,7 +2381,7 @@ void Lower::match_rows() {
       (void)half;
       for (Tensor* t : inner) t->plan_mat = false;
       out->plan_mat = true;
-      rope_out[out] = rp;
+      if (!fuse_rope(rp, out)) rope_out[out] = rp;
     }
   }
 }
@@ -2301,6 +2433,64 @@ bool Lower::emit_norm(Tensor* t, const NormPlan& p) {
   return true;
 }
 
+// Strides of v's (rank r <= 4) dims right-aligned into 4 (size-1 dims and
+// the missing leading dims get stride 0) over its materialized base.
+void Lower::view4(Tensor* v, int r, const void** ptr, int64_t* s) {
+  Tensor* base;
+  int64_t off, st[kMaxRank];
+  operand_strides(v, &base, &off, st);
+  for (int i = 0; i < 4; ++i) s[i] = 0;
+  for (int i = 0; i < r; ++i) s[4 - r + i] = v->shape.d[i] == 1 ? 0 : st[i];
+  *ptr = (const char*)base->data() + off * dt_size(base->dt);
+}
+
+// When the rotated tensor is a biased projection seen as heads --
+// transpose(reshape(y, [B, S, H, D]), [0, 2, 1, 3]) or reshape(y, [B, S, H, D])
+// with y = add(matmul(x, W), bias) planned as EPI_BIAS and used nowhere
+// else -- the projection's epilogue rotates and writes `out` directly
+// (GroupedQueryAttention.forward with rope: groupedqueryattention.nim).
+bool Lower::fuse_rope(const RopePlan& rp, Tensor* out) {
+  Tensor* X = rp.src;
+  if (X->dt != kBF16 || out->dt != kBF16 || X->shape.rank != 4 || X->st || X->ext != 0 ||
+      X->uses != 1)
+    return false;
+  bool tr = false;
+  Tensor* r4 = X;
+  if (X->prod && X->prod->kind == K_TRANSPOSE) {
+    if (!dims_are(X->prod->l0, {0, 2, 1, 3})) return false;
+    r4 = X->prod->in[0];
+    tr = true;
+    if (r4->st || r4->ext != 0 || r4->uses != 1) return false;
+  }
+  if (!r4->prod || r4->prod->kind != K_RESHAPE || r4->shape.rank != 4) return false;
+  // through a chain of reshapes (the [B * S, N] -> [B, S, N] -> [B, S, H, D]
+  // of GroupedQueryAttention.forward), each used only by the next
+  Tensor* y = r4->prod->in[0];
+  while (!gemm_out.count(y) && y->prod && y->prod->kind == K_RESHAPE && !y->st &&
+         y->ext == 0 && y->uses == 1)
+    y = y->prod->in[0];
+  auto it = gemm_out.find(y);
+  if (it == gemm_out.end() || it->second.epi != EPI_BIAS || y->st || y->ext != 0 ||
+      y->uses != 1 || y->shape.rank != 2)
+    return false;
+  const int64_t B = r4->shape.d[0], S = r4->shape.d[1], H = r4->shape.d[2], D = r4->shape.d[3];
+  if (y->shape.d[0] != B * S || y->shape.d[1] != H * D || D % 8) return false;
+  GemmPlan gp = it->second;
+  gp.epi = EPI_BIAS_ROPE;
+  gp.rope_cos = rp.cos0;
+  gp.rope_sin = rp.sin0;
+  gp.rope_t = tr;
+  gp.rope_B = B;
+  gp.rope_S = S;
+  gp.rope_H = H;
+  gp.rope_D = D;
+  gemm_out.erase(it);
+  y->plan_mat = false;
+  out->plan_mat = true;
+  gemm_out[out] = gp;
+  return true;
+}
+
 bool Lower::emit_rope(Tensor* t, const RopePlan& p) {
   const Shape& S = t->shape;
   const int r = S.rank;
@@ -2313,19 +2503,11 @@ bool Lower::emit_rope(Tensor* t, const RopePlan& p) {
   a.S = d[2];
   a.half = d[3] / 2;
   if (a.d0 * a.d1 * a.S * (a.half / 4) >= (1ll << 31) || a.half % 4) return false;
-  auto view4 = [&](Tensor* v, const void** ptr, int64_t* s) {
-    Tensor* base;
-    int64_t off, st[kMaxRank];
-    operand_strides(v, &base, &off, st);
-    for (int i = 0; i < 4; ++i) s[i] = 0;
-    for (int i = 0; i < r; ++i) s[4 - r + i] = v->shape.d[i] == 1 ? 0 : st[i];
-    *ptr = (const char*)base->data() + off * dt_size(base->dt);
-  };
   int64_t sx[4], sc[4], ss[4];
   const void *px, *pc, *ps;
-  view4(p.src, &px, sx);
-  view4(p.cos0, &pc, sc);
-  view4(p.sin0, &ps, ss);
+  view4(p.src, r, &px, sx);
+  view4(p.cos0, r, &pc, sc);
+  view4(p.sin0, r, &ps, ss);
   a.x = px;
   a.x_dt = p.src->dt;
   a.x_s0 = sx[0]; a.x_s1 = sx[1]; a.x_ss = sx[2]; a.x_sd = sx[3];
@@ -2498,6 +2680,7 @@ void flush(Ctx* c) {
     L.match_gemm_epilogues();
     L.match_moe();
     L.match_rows();
+    L.match_gemm_groups();
   }
 
   // 3. emission in creation order

@@ -148,6 +148,43 @@ def test_llama_layer_bf16(gpu, oracle, causal):
     bf16_close(got, want)
 
 
+def test_llama_layer_kernel_plan(gpu, oracle):
+    """The decoder layer runs as its fused kernels: one launch for the q / k / v
+    projections with RoPE in the q and k epilogues, flash attention, the
+    O projection with bias + residual, the SwiGLU dual GEMM, the down
+    projection with bias + residual, and the two rmsNorm row kernels."""
+    B, S, E_, nh, nkv, I = 2, 64, 256, 4, 2, 512
+    key = oracle.init_key(0x5EED0005)
+    p, m = _llama_params(oracle, key, E_, nh, nkv, I)
+    hd = E_ // nh
+    rope = nn.RotaryPositionEncoding.init(hd, S, 500000.0)
+    attn = nn.GroupedQueryAttention(m["q"], m["k"], m["v"], m["o"], nh, nkv, hd, rope)
+    ffn = nn.GatedFeedForward(m["g"], m["u"], m["d"])
+    layer = nn.LlamaDecoderLayer(attn, ffn, nn.RMSNorm(dev(p["g1"]), 1e-5),
+                                 nn.RMSNorm(dev(p["g2"]), 1e-5))
+    x = oracle.round_bf16(oracle.normal_f32(oracle.fold_in(key, 99), B * S * E_)
+                          .reshape(B, S, E_))
+    xt = dev(x, DType.BFLOAT16)
+    E.profileBegin()
+    got = host(layer.forward(xt, causal=True))
+    prof = E.profileEnd()  # (kernel name, launches, ms)
+    names = [n for n, _, _ in prof]
+
+    def launches(pred):
+        return sum(cnt for n, cnt, _ in prof if pred(n))
+
+    assert launches(lambda n: n.startswith("gemm_lds_nn{") and n.count("+rope") == 2) == 1, names
+    assert launches(lambda n: n.startswith("rope_pairs")) == 0, names
+    assert launches(lambda n: n.startswith("flash_attn")) == 1, names
+    assert launches(lambda n: "swiglu" in n) == 1, names
+    assert launches(lambda n: "+bias+res" in n) == 2, names
+    assert launches(lambda n: n.startswith("rmsnorm_rows")) == 2, names
+    assert sum(cnt for _, cnt, _ in prof) == 7, names
+    c, s = nn.rope_tables(hd, S, 500000.0)
+    want = oracle.llama_layer(x, p, nh, nkv, c, s, 1e-5, True, True, "rms")
+    bf16_close(got, want)
+
+
 def test_embedding_gather_equals_one_hot(gpu, oracle):
     V, H, T = 512, 64, 40
     w = oracle.round_bf16(oracle.normal_f32(oracle.init_key(8), V * H).reshape(V, H))

@@ -185,3 +185,86 @@ def test_rope_pair_kernel(gpu, oracle, B, H, S, D, bf16):
         assert np.all(np.abs(gotf - want) <= 2.0 ** -8 * np.abs(want) + 1e-6)
     else:
         np.testing.assert_allclose(gotf, want, rtol=1e-6, atol=1e-6)
+
+
+# ---- attention projections: RoPE in the GEMM epilogue, q / k / v in one launch -----------
+
+def _proj_rope(oracle, x, w, b, B, S, H, D, c, s, off, transposed):
+    y = oracle.linear(x, w, b, True).reshape(B, S, H, D)  # bf16-rounded projection
+    if transposed:
+        y = np.ascontiguousarray(y.transpose(0, 2, 1, 3))
+    return oracle.rope(y, c, s, off)
+
+
+@pytest.mark.parametrize("B,S,E_,H,D,transposed", [(2, 96, 256, 4, 64, True),
+                                                   (1, 300, 128, 2, 128, True),
+                                                   (2, 40, 128, 3, 32, False)])
+def test_rope_fused_into_projection(gpu, oracle, B, S, E_, H, D, transposed):
+    """Linear -> reshape [B, S, H, D] (-> transpose [0, 2, 1, 3]) -> applyRotate
+    (GroupedQueryAttention's q / k path) runs as one GEMM whose epilogue
+    rotates the pairs and writes the rotated layout, bit-exact with op by op."""
+    key = oracle.init_key(700 + S)
+    w, b = _lin(oracle, key, E_, H * D)
+    x = oracle.round_bf16(oracle.normal_f32(oracle.fold_in(key, 2), B * S * E_).reshape(B * S, E_))
+    seq = H if not transposed else S  # the axis applyRotate treats as positions
+
+    def fn():
+        rope = nn.RotaryPositionEncoding.init(D, seq + 8, 500000.0)
+        lin = nn.Linear(E.fromHost(w, DType.BFLOAT16), E.fromHost(b, DType.BFLOAT16))
+        y = O.reshape(lin.forward(E.fromHost(x, DType.BFLOAT16)), [B, S, H, D])
+        if transposed:
+            y = O.transpose(y, [0, 2, 1, 3])
+        return rope.forward(y, 3)
+
+    got, names = _run(fn)
+    assert any("+bias+rope" in n for n in names), names
+    assert not any(k.startswith("rope_pairs") for k in names), names
+    ref, names2 = _run(fn, op_by_op=True)
+    assert not any("+rope" in n for n in names2)
+    np.testing.assert_array_equal(got, ref)
+    c, s = nn.rope_tables(D, seq + 8, 500000.0)
+    want = _proj_rope(oracle, x, w, b, B, S, H, D, c, s, 3, transposed)
+    bf16_close(_bits_f32(got), want)
+
+
+@pytest.mark.parametrize("B,S,E_,H,KV,D", [(2, 96, 256, 4, 2, 64), (1, 200, 128, 2, 1, 136)])
+def test_qkv_projections_one_launch(gpu, oracle, B, S, E_, H, KV, D):
+    """The q (rotated), k (rotated) and v projections of one input run as one
+    multi-segment GEMM launch; each output equals the op-by-op path."""
+    key = oracle.init_key(800 + S)
+    wq, bq = _lin(oracle, oracle.fold_in(key, 0), E_, H * D)
+    wk, bk = _lin(oracle, oracle.fold_in(key, 1), E_, KV * D)
+    wv, bv = _lin(oracle, oracle.fold_in(key, 2), E_, KV * D)
+    x = oracle.round_bf16(oracle.normal_f32(oracle.fold_in(key, 3), B * S * E_).reshape(B * S, E_))
+    outs = {}
+
+    def run(op_by_op):
+        if op_by_op:
+            E.setMode(E.MODE_OP_BY_OP)
+        try:
+            E.profileBegin()
+            rope = nn.RotaryPositionEncoding.init(D, S, 10000.0)
+            xt = E.fromHost(x, DType.BFLOAT16)
+            mk = lambda w_, b_: nn.Linear(E.fromHost(w_, DType.BFLOAT16),
+                                          E.fromHost(b_, DType.BFLOAT16))
+            q = O.transpose(O.reshape(mk(wq, bq).forward(xt), [B, S, H, D]), [0, 2, 1, 3])
+            k = O.transpose(O.reshape(mk(wk, bk).forward(xt), [B, S, KV, D]), [0, 2, 1, 3])
+            v = O.transpose(O.reshape(mk(wv, bv).forward(xt), [B, S, KV, D]), [0, 2, 1, 3])
+            q, k = rope.forward(q, 0), rope.forward(k, 0)
+            res = [E.toHost(t) for t in (q, k, v)]
+            names = [n for n, _, _ in E.profileEnd()]
+        finally:
+            E.setMode(E.MODE_DEFERRED)
+        return res, names
+
+    got, names = run(False)
+    assert any(n.startswith("gemm_lds_nn{") and n.count("+rope") == 2 for n in names), names
+    ref, _ = run(True)
+    for g_, r_ in zip(got, ref):
+        np.testing.assert_array_equal(g_, r_)
+    c, s = nn.rope_tables(D, S, 10000.0)
+    bf16_close(_bits_f32(got[0]), _proj_rope(oracle, x, wq, bq, B, S, H, D, c, s, 0, True))
+    bf16_close(_bits_f32(got[1]), _proj_rope(oracle, x, wk, bk, B, S, KV, D, c, s, 0, True))
+    want_v = np.ascontiguousarray(oracle.linear(x, wv, bv, True).reshape(B, S, KV, D)
+                                  .transpose(0, 2, 1, 3))
+    bf16_close(_bits_f32(got[2]), want_v)
