@@ -16,10 +16,11 @@ MFMA-bound), ``mnist`` (MLP inference with argmax, latency-bound), ``moe``
 (DeepSeek-style routed MoE layer) and ``copy`` (a plain streaming kernel of
 known size, the calibration for the HBM byte counters).
 
-Prints ONE JSON line with the metric, a roofline object for the dominant
-kernel (its launches timed by HIP events on the backend's own stream over
-the timed steps), and a cpu_baseline: the CPU restatement in oracle/ timed
-on this host's cores on a bounded sample.
+Prints ONE JSON line with the metric (from a timed pass of K steps), a
+roofline object for the dominant kernel (its launches timed by HIP events on
+the backend's own stream over a second, profiled pass of the same K steps),
+and a cpu_baseline: the CPU restatement in oracle/ timed on this host's
+cores on a bounded sample.
 """
 from __future__ import annotations
 
@@ -105,12 +106,18 @@ def kernel_symbol(entry_name: str) -> str:
 
 
 def timed_run(step, steps, warmup):
-    """First call, warmup, then `steps` timed steps bracketed by sync on both
-    sides.  Every kernel launch inside the timed region is bracketed by HIP
-    events on the backend stream (rew_mi355x_profile_*), so per-kernel
-    durations come from the timed steps themselves.
+    """First call, warmup, then two passes of `steps` steps, each bracketed by
+    sync on both sides:
 
-    Returns (wall_s, device_ms, first_ms, profile entries)."""
+    1. the profiled pass: every kernel launch bracketed by HIP events on the
+       backend stream (rew_mi355x_profile_*), which gives per-kernel
+       durations for the roofline and the breakdown.  The per-launch events
+       add gaps between kernels, so this pass is not the one timed;
+    2. the timed pass: wall clock and HIP events at its two ends only; it
+       gives `value` and ms_per_step.
+
+    Returns (wall_s, device_ms, first_ms, profile entries); wall and device
+    time are the timed pass's."""
     t0 = time.perf_counter()
     y = step()
     E.sync()
@@ -121,23 +128,31 @@ def timed_run(step, steps, warmup):
     E.sync()
     ev = HipEvents(backend_stream())
     e0, e1 = ev.event(), ev.event()
-    outs = []
-    E.sync()
-    E.profileBegin()
-    t0 = time.perf_counter()
-    ev.record(e0)
-    for _ in range(steps):
-        outs.append(step())
-        if len(outs) > 2:
-            outs.pop(0)
-    ev.record(e1)
-    E.sync()
-    wall = time.perf_counter() - t0
-    prof = E.profileEnd()
-    dev_ms = ev.elapsed_ms(e0, e1)
-    outs.clear()
+
+    def run(profiled):
+        outs = []
+        E.sync()
+        if profiled:
+            E.profileBegin()
+        t0 = time.perf_counter()
+        ev.record(e0)
+        for _ in range(steps):
+            outs.append(step())
+            if len(outs) > 2:
+                outs.pop(0)
+        ev.record(e1)
+        E.sync()
+        wall = time.perf_counter() - t0
+        prof = E.profileEnd() if profiled else None
+        outs.clear()
+        return wall, ev.elapsed_ms(e0, e1), prof
+
+    pwall, _, prof = run(True)
+    wall, dev_ms, _ = run(False)
     for name, n, ms in sorted(prof, key=lambda r: -r[2]):
         print(f"#   {ms * 1e3 / steps:9.1f} us/step  x{n // steps:<3d} {name}", file=sys.stderr)
+    print(f"#   timed pass {wall * 1e3 / steps:.3f} ms/step, profiled pass "
+          f"{pwall * 1e3 / steps:.3f} ms/step", file=sys.stderr)
     return wall, dev_ms, first_ms, prof
 
 

@@ -166,7 +166,11 @@ typedef struct rew_mi355x_stats {
   int64_t fused_groups;     /* launches that covered more than one op       */
   int64_t bytes_in_use;     /* device bytes held by live tensors            */
   int64_t bytes_cached;     /* device bytes held by the caching allocator   */
-  int64_t plan_cache_hits;  /* lowerings served from the plan cache         */
+  int64_t plan_cache_hits;  /* launches of a fused program served by its     */
+                            /* already compiled kernel (the program cache,  */
+                            /* keyed by the program's binary signature; the */
+                            /* analogue of rew's executable cache); counted */
+                            /* for all contexts of the process since reset  */
 } rew_mi355x_stats;
 
 int rew_mi355x_get_stats(rew_mi355x_ctx* ctx, rew_mi355x_stats* out);

@@ -22,6 +22,8 @@ struct ReduceArgs;
 bool jit_launch_ew(const vm::Program& P, const vm::Space& S, bool vec, hipStream_t stream);
 bool jit_launch_reduce(const vm::Program& P, const vm::Space& S, const ReduceArgs& A, bool vec,
                        hipStream_t stream);
+// Launches so far (process-wide) that reused an already compiled program.
+int64_t jit_cache_hits();
 
 // ---- reductions (k_reduce.hip) ---------------------------------------------
 enum RedOp : int {

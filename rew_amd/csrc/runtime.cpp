@@ -276,6 +276,7 @@ int rew_mi355x_init(int ordinal, rew_mi355x_ctx** out) {
       Ctx* c = new Ctx();
       c->ordinal = ordinal;
       c->alloc.ordinal = ordinal;
+      c->jit_hits_base = jit_cache_hits();
       REW_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
       if (const char* s = std::getenv("REW_MI355X_EAGER_SYNC"))
         if (s[0] == '1') c->mode = REW_MI355X_MODE_OP_BY_OP;
@@ -498,6 +499,7 @@ int rew_mi355x_get_stats(rew_mi355x_ctx* ctx, rew_mi355x_stats* out) {
     std::lock_guard<std::recursive_mutex> g(c->mu);
     c->stats.bytes_in_use = (int64_t)c->alloc.in_use;
     c->stats.bytes_cached = (int64_t)c->alloc.cached;
+    c->stats.plan_cache_hits = jit_cache_hits() - c->jit_hits_base;
     *out = c->stats;
   });
 }
@@ -507,6 +509,7 @@ int rew_mi355x_reset_stats(rew_mi355x_ctx* ctx) {
     Ctx* c = as_ctx(ctx);
     std::lock_guard<std::recursive_mutex> g(c->mu);
     c->stats = rew_mi355x_stats{};
+    c->jit_hits_base = jit_cache_hits();
   });
 }
 

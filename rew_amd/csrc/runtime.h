@@ -104,6 +104,7 @@ struct Ctx {
   int flush_threshold = 4096;
   bool no_fusion_patterns = false;  // REW_MI355X_NO_PATTERNS=1: per-op kernels only
   rew_mi355x_stats stats{};
+  int64_t jit_hits_base = 0;  // jit_cache_hits() when the stats were last reset
   // pinned staging ring for small host->device copies
   uint8_t* ring = nullptr;
   size_t ring_size = 0, ring_pos = 0;

@@ -104,18 +104,36 @@ __device__ __forceinline__ void store_scalar(void* p, int dt, int64_t i,
   }
 }
 
+// Vector loads / stores of the streaming kernels: nontemporal when
+// REW_VM_NT is 1 (the run-time compiled kernels choose it per program).
+#ifndef REW_VM_NT
+#define REW_VM_NT 0
+#endif
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+template <typename T>
+__device__ __forceinline__ T stream_ld(const T* p) {
+  if constexpr (REW_VM_NT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+template <typename T>
+__device__ __forceinline__ void stream_st(T* p, T v) {
+  if constexpr (REW_VM_NT) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
+
 template <int V>
 __device__ __forceinline__ void load_vec(const void* p, int dt, int64_t i,
                                          uint32_t (&d)[V]) {
   if constexpr (V == 4) {
     switch (dt) {
       case REW_DT_FLOAT32: case REW_DT_INT32: case REW_DT_UINT32: {
-        uint4 x = *(const uint4*)((const uint32_t*)p + i);
+        const u32x4_t x = stream_ld((const u32x4_t*)((const uint32_t*)p + i));
         d[0] = x.x; d[1] = x.y; d[2] = x.z; d[3] = x.w;
         return;
       }
       case REW_DT_BFLOAT16: {
-        uint2 x = *(const uint2*)((const uint16_t*)p + i);
+        const u32x2_t x = stream_ld((const u32x2_t*)((const uint16_t*)p + i));
         d[0] = x.x << 16; d[1] = x.x & 0xffff0000u;
         d[2] = x.y << 16; d[3] = x.y & 0xffff0000u;
         return;
@@ -133,13 +151,13 @@ __device__ __forceinline__ void store_vec(void* p, int dt, int64_t i,
   if constexpr (V == 4) {
     switch (dt) {
       case REW_DT_FLOAT32: case REW_DT_INT32: case REW_DT_UINT32: {
-        *(uint4*)((uint32_t*)p + i) = make_uint4(v[0], v[1], v[2], v[3]);
+        stream_st((u32x4_t*)((uint32_t*)p + i), (u32x4_t){v[0], v[1], v[2], v[3]});
         return;
       }
       case REW_DT_BFLOAT16: {
-        uint32_t lo = bf16_bits(as_f(v[0])) | ((uint32_t)bf16_bits(as_f(v[1])) << 16);
-        uint32_t hi = bf16_bits(as_f(v[2])) | ((uint32_t)bf16_bits(as_f(v[3])) << 16);
-        *(uint2*)((uint16_t*)p + i) = make_uint2(lo, hi);
+        stream_st((u32x2_t*)((uint16_t*)p + i),
+                  (u32x2_t){bf16x2_bits(as_f(v[0]), as_f(v[1])),
+                            bf16x2_bits(as_f(v[2]), as_f(v[3]))});
         return;
       }
       default: break;
