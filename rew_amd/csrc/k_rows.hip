@@ -170,6 +170,102 @@ void launch_rmsnorm_rows(const RowNormArgs& a, hipStream_t stream) {
   REW_HIP(hipGetLastError());
 }
 
+// ---- softmax -------------------------------------------------------------------------------
+
+// rew's softmax (src/rew/nn/activation.nim:64-77) over the last axis in one
+// pass: the row is read once and written once.  The compiled row reduction
+// (one wave per row, V = 4) has lane l add its 16-byte chunks c = 0, 1, ...
+// -- elements 4 (64 c + l) + j, j = 0..3 in order -- then combine lanes by a
+// butterfly over xor 32, 16, ..., 1; the sum here runs in exactly that
+// order, and the max (order-free) and exp / divide are the same fp32 ops.
+template <int CH>  // 16-byte chunks per lane
+__global__ void __launch_bounds__(256) softmax_wave_kernel(SoftmaxArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t waves = (int64_t)gridDim.x * 4;
+  for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < a.rows; row += waves) {
+    const float* x = a.x + row * a.x_rs;
+    float4 v[CH];
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      const int64_t j = ((int64_t)k * 64 + lane) * 4;
+      if (j < a.n) {
+        v[k] = *(const float4*)(x + j);
+        m = fmax_prop(m, v[k].x);
+        m = fmax_prop(m, v[k].y);
+        m = fmax_prop(m, v[k].z);
+        m = fmax_prop(m, v[k].w);
+      }
+    }
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) m = fmax_prop(m, __shfl_xor(m, s, 64));
+    float sum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      const int64_t j = ((int64_t)k * 64 + lane) * 4;
+      if (j < a.n) {
+        v[k].x = expf(v[k].x - m);
+        v[k].y = expf(v[k].y - m);
+        v[k].z = expf(v[k].z - m);
+        v[k].w = expf(v[k].w - m);
+        sum = sum + v[k].x;
+        sum = sum + v[k].y;
+        sum = sum + v[k].z;
+        sum = sum + v[k].w;
+      }
+    }
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) sum = sum + __shfl_xor(sum, s, 64);
+    float* y = a.y + row * a.n;
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      const int64_t j = ((int64_t)k * 64 + lane) * 4;
+      if (j < a.n)
+        *(float4*)(y + j) = make_float4(v[k].x / sum, v[k].y / sum, v[k].z / sum, v[k].w / sum);
+    }
+  }
+}
+
+// Rows shorter than 128: the compiled reduction runs a thread per row over
+// j = 0, 1, ... in order; so does this kernel.
+__global__ void __launch_bounds__(256) softmax_thread_kernel(SoftmaxArgs a) {
+  for (int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x; row < a.rows;
+       row += (int64_t)gridDim.x * 256) {
+    const float* x = a.x + row * a.x_rs;
+    float m = -INFINITY;
+    for (int64_t j = 0; j < a.n; ++j) m = fmax_prop(m, x[j]);
+    float sum = 0.0f;
+    for (int64_t j = 0; j < a.n; ++j) sum = sum + expf(x[j] - m);
+    float* y = a.y + row * a.n;
+    for (int64_t j = 0; j < a.n; ++j) y[j] = expf(x[j] - m) / sum;
+  }
+}
+
+bool softmax_rows_ok(const SoftmaxArgs& a) {
+  if (a.rows <= 0 || a.n <= 0) return false;
+  if (a.n < 128) return true;
+  return a.n % 4 == 0 && a.n <= kSoftmaxMaxCols && a.x_rs % 4 == 0 &&
+         ((uintptr_t)a.x & 15) == 0 && ((uintptr_t)a.y & 15) == 0;
+}
+
+void launch_softmax_rows(const SoftmaxArgs& a, hipStream_t stream) {
+  if (!softmax_rows_ok(a)) fail(REW_MI355X_ERR_INVALID, "internal: softmax rows not launchable");
+  if (a.n < 128) {
+    const int64_t blocks = (a.rows + 255) / 256;
+    hipLaunchKernelGGL(softmax_thread_kernel, dim3((unsigned)(blocks < 65536 ? blocks : 65536)),
+                       dim3(256), 0, stream, a);
+  } else {
+    const int64_t blocks = (a.rows + 3) / 4;
+    const dim3 grid((unsigned)(blocks < 65536 ? blocks : 65536)), block(256);
+    const int64_t ch = (a.n / 4 + 63) / 64;
+    if (ch <= 4) hipLaunchKernelGGL(softmax_wave_kernel<4>, grid, block, 0, stream, a);
+    else if (ch <= 8) hipLaunchKernelGGL(softmax_wave_kernel<8>, grid, block, 0, stream, a);
+    else if (ch <= 16) hipLaunchKernelGGL(softmax_wave_kernel<16>, grid, block, 0, stream, a);
+    else hipLaunchKernelGGL(softmax_wave_kernel<32>, grid, block, 0, stream, a);
+  }
+  REW_HIP(hipGetLastError());
+}
+
 // ---- RoPE ------------------------------------------------------------------------------
 
 // VEC: bf16 x and y with contiguous pairs, cos / sin read at pair stride 2

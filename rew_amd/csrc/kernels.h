@@ -251,6 +251,21 @@ struct RowNormArgs {
 };
 void launch_rmsnorm_rows(const RowNormArgs& a, hipStream_t stream);
 
+// softmax over rows of n contiguous f32 (x row stride x_rs elements):
+// m = max_j x, e_j = exp(x_j - m), s = sum_j e_j, y = e / s (dense f32).
+// The sum runs in the order of the compiled row reduction, so y equals the
+// reduceMax / sub / exp / reduceSum / divide sequence bit for bit.
+struct SoftmaxArgs {
+  const float* x;
+  int64_t rows, n, x_rs;
+  float* y;
+};
+// n < 128 (a thread per row) or n % 4 == 0, n <= kSoftmaxMaxCols, 16-byte
+// aligned rows (a wave per row, the row held in registers)
+constexpr int64_t kSoftmaxMaxCols = 8192;
+bool softmax_rows_ok(const SoftmaxArgs& a);
+void launch_softmax_rows(const SoftmaxArgs& a, hipStream_t stream);
+
 // applyRotate on adjacent pairs over a [d0, d1, S, 2*half] index space; x,
 // cos and sin are read through strided views (cos / sin indexed by pair i),
 // y is dense.  half % 4 == 0 and d0*d1*S*half/4 < 2^31.

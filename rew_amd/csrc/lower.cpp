@@ -17,6 +17,8 @@
 #include <cmath>
 #include <cstdio>
 #include <functional>
+#include <map>
+#include <tuple>
 
 #include "kernels.h"
 #include "runtime.h"
@@ -232,6 +234,12 @@ struct NormPlan {
   float eps = 0.0f, divisor = 1.0f;
 };
 
+// softmax chain (src/rew/nn/activation.nim:64-77) over the last axis, lowered
+// to one row kernel.
+struct SoftmaxPlan {
+  Tensor* x = nullptr;  // f32 input
+};
+
 // applyRotate chain (src/rew/nn/rope.nim:56-108) lowered to one pair kernel.
 struct RopePlan {
   Tensor* src = nullptr;   // x (bf16 when the astype to f32 is folded)
@@ -268,9 +276,14 @@ struct Lower {
   std::unordered_map<Tensor*, GemmPlan> gemm_out;  // fused GEMM result -> plan
   std::unordered_map<Tensor*, NormPlan> norm_out;
   std::unordered_map<Tensor*, RopePlan> rope_out;
+  std::unordered_map<Tensor*, SoftmaxPlan> softmax_out;
   std::unordered_map<Tensor*, MoePlan> moe_out;
   std::unordered_map<Tensor*, Node*> flash_out;  // transposed flash output -> PV node
   std::vector<std::vector<Tensor*>> gemm_groups;  // outputs of sibling projections
+  // reductions emitted in this flush, by (input, op, dims, dtype): a repeat
+  // (reduceMean's reduceSum next to a reduceSum of the same tensor) aliases
+  // the first result
+  std::map<std::tuple<Tensor*, int, std::vector<int64_t>, int>, Tensor*> reduce_done;
 
   explicit Lower(Ctx* ctx) : c(ctx) {}
 
@@ -282,6 +295,7 @@ struct Lower {
   void match_rows();
   bool emit_norm(Tensor* t, const NormPlan& p);
   bool emit_rope(Tensor* t, const RopePlan& p);
+  bool emit_softmax(Tensor* t, const SoftmaxPlan& p);
   bool rows_view(Tensor* x, int64_t n, const void** ptr, int64_t* rs);
   bool emit_gemm_fused(Tensor* t, const GemmPlan& p);
   bool gemm_fused_args(Tensor* t, const GemmPlan& p, GemmArgs& g);
@@ -868,6 +882,12 @@ void Lower::ensure_mat(Tensor* t) {
     rope_out.erase(rit);
     if (emit_rope(t, rp)) return;
   }
+  auto sit = softmax_out.find(t);
+  if (sit != softmax_out.end()) {
+    SoftmaxPlan sp = sit->second;
+    softmax_out.erase(sit);
+    if (emit_softmax(t, sp)) return;
+  }
   auto fit = flash_out.find(t);
   if (fit != flash_out.end()) {
     Node* pv = fit->second;
@@ -1007,6 +1027,12 @@ void Lower::emit_anchor(Node* n) {
 void Lower::emit_reduce(Node* n) {
   Tensor* x = n->in[0];
   Tensor* out = n->out[0];
+  const auto key = std::make_tuple(x, n->sub, n->l0, out->dt);
+  auto done = reduce_done.find(key);
+  if (done != reduce_done.end() && done->second->st && done->second->shape == out->shape) {
+    tensor_alias(out, done->second);
+    return;
+  }
   const Shape& X = x->shape;
   std::vector<bool> red(X.rank, false);
   for (auto d : n->l0) red[d] = true;
@@ -1054,6 +1080,7 @@ void Lower::emit_reduce(Node* n) {
       launch_reduce(g.P, S, A, vec, c->stream);
       prof_end(c);
       note_launch(c, g.P.n_ins > 1);
+      reduce_done[key] = out;
       return;
     } catch (GenFail&) {
       tensor_drop_storage(out);
@@ -2303,6 +2330,38 @@ void Lower::match_rows() {
         break;
       }
     }
+    // ---- softmax: divide(e, bcast(reduceSum(e))), e = exp(sub(x, bcast(reduceMax(x))))
+    // (only where the probabilities are materialized anyway: inside a fused
+    // attention they never are)
+    if (mo->kind == K_BINARY && mo->sub == 3 && mo->out[0]->dt == kF32 && !mo->out[0]->st &&
+        mo->out[0]->plan_mat && mo->out[0]->shape.rank >= 1) {
+      Tensor* y = mo->out[0];
+      const int r = y->shape.rank;
+      Tensor *e = mo->in[0], *sB = mo->in[1];
+      Node* en = (!e->st && e->prod && e->prod->kind == K_UNARY && e->prod->sub == 2 &&
+                  e->ext == 0 && e->uses == 2) ? e->prod : nullptr;
+      Node* sb = chain_node(sB, K_BROADCAST_TO, 1);
+      Node* rs = sb ? chain_node(sb->in[0], K_REDUCE, 1) : nullptr;
+      Node* sh = en ? chain_node(en->in[0], K_BINARY, 1) : nullptr;
+      if (en && rs && sh && sh->sub == 1 && rs->sub == RED_SUM && rs->in[0] == e &&
+          dims_are(rs->l0, {r - 1}) && sb->l1 == iota_dims(r - 1)) {
+        Tensor* x = sh->in[0];
+        Node* mb = chain_node(sh->in[1], K_BROADCAST_TO, 1);
+        Node* rm = mb ? chain_node(mb->in[0], K_REDUCE, 1) : nullptr;
+        if (rm && rm->sub == RED_MAX && rm->in[0] == x && dims_are(rm->l0, {r - 1}) &&
+            mb->l1 == iota_dims(r - 1) && x->dt == kF32 && x->shape == y->shape) {
+          // e, its sum and the broadcasts, x - max and the max live only
+          // inside the row kernel
+          for (Tensor* t : {e, sB, sb->in[0], sh->out[0], sh->in[1], mb->in[0]})
+            t->plan_mat = false;
+          y->plan_mat = true;
+          SoftmaxPlan sp;
+          sp.x = x;
+          softmax_out[y] = sp;
+          continue;
+        }
+      }
+    }
     // ---- RoPE: [astype(] reshape(concat([x0', x1'] as [..., half, 1]), shape) [)]
     if (mo->kind == K_CONCAT && mo->in.size() == 2) {
       Tensor* cc = mo->out[0];
@@ -2488,6 +2547,29 @@ bool Lower::fuse_rope(const RopePlan& rp, Tensor* out) {
   y->plan_mat = false;
   out->plan_mat = true;
   gemm_out[out] = gp;
+  return true;
+}
+
+bool Lower::emit_softmax(Tensor* t, const SoftmaxPlan& p) {
+  const int64_t n = t->shape.d[t->shape.rank - 1];
+  SoftmaxArgs a;
+  std::memset(&a, 0, sizeof(a));
+  const void* xp;
+  rows_view(p.x, n, &xp, &a.x_rs);
+  a.x = (const float*)xp;
+  a.n = n;
+  a.rows = n ? t->numel() / n : 0;
+  tensor_alloc(t);
+  a.y = (float*)t->data();
+  if (!softmax_rows_ok(a)) {
+    tensor_drop_storage(t);
+    return false;
+  }
+  if (c->profiling)
+    prof_begin(c, "softmax_rows{" + std::to_string(a.rows) + "x" + std::to_string(n) + "}");
+  launch_softmax_rows(a, c->stream);
+  prof_end(c);
+  note_launch(c, true);
   return true;
 }
 

@@ -268,3 +268,53 @@ def test_qkv_projections_one_launch(gpu, oracle, B, S, E_, H, KV, D):
     want_v = np.ascontiguousarray(oracle.linear(x, wv, bv, True).reshape(B, S, KV, D)
                                   .transpose(0, 2, 1, 3))
     bf16_close(_bits_f32(got[2]), want_v)
+
+
+@pytest.mark.parametrize("shape", [(64, 4096), (33, 100), (16, 2048), (5, 8192), (7, 132),
+                                   (2, 3, 256), (3, 130)])
+def test_softmax_row_kernel(gpu, oracle, shape):
+    """rew's softmax chain (src/rew/nn/activation.nim:64-77) over the last axis
+    runs as one row kernel whose sum follows the compiled row reduction's
+    order, so it equals the op-by-op path bit for bit; rows of n % 4 != 0 at
+    n >= 128 take the generic path."""
+    n = shape[-1]
+    x = oracle.normal_f32(oracle.init_key(900 + n), int(np.prod(shape))).reshape(shape) * 3
+    x[(0,) * (len(shape) - 1)][min(5, n - 1)] = np.nan  # a NaN row
+    if x.shape[-2] > 1:
+        x[(0,) * (len(shape) - 2) + (1,)][:] = -np.inf   # an all -inf row
+
+    def fn():
+        return nn.softmax(E.fromHost(x), len(shape) - 1)
+
+    got, names = _run(fn)
+    fused = any(k.startswith("softmax_rows") for k in names)
+    assert fused == (n < 128 or n % 4 == 0), names
+    ref, names2 = _run(fn, op_by_op=True)
+    assert not any(k.startswith("softmax_rows") for k in names2)
+    # bit-exact, NaN payloads aside
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
+    num = ~np.isnan(got)
+    np.testing.assert_array_equal(got[num].view(np.uint32), ref[num].view(np.uint32))
+    ok = np.isfinite(x).all(axis=-1)
+    want = oracle.softmax_rows(x.reshape(-1, n)).reshape(shape)
+    np.testing.assert_allclose(got[ok], want[ok], rtol=1e-5, atol=1e-9)
+
+
+def test_repeated_reduction_runs_once(gpu, oracle):
+    """reduceMean(y) is reduceSum(y) / n (src/rew/ops/reduce.nim): next to a
+    reduceSum of the same tensor the sum is computed once and shared."""
+    x = oracle.normal_f32(oracle.init_key(950), 256 * 1024).reshape(256, 1024)
+
+    def fn():
+        y = nn.relu(O.add(E.fromHost(x), E.fromHost(x)))
+        return O.add(O.reduceSum(y, [1]), O.reduceMean(y, [1]))
+
+    E.profileBegin()
+    got = E.toHost(fn())
+    prof = E.profileEnd()
+    assert sum(c for n, c, _ in prof if n.startswith("reduce")) == 1, prof
+    ref, _ = _run(fn, op_by_op=True)
+    np.testing.assert_array_equal(got, ref)
+    y = np.maximum(x + x, 0)
+    s = y.astype(np.float64).sum(1)
+    np.testing.assert_allclose(got, (s + s / 1024).astype(np.float32), rtol=1e-5)
