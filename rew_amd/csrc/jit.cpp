@@ -125,6 +125,8 @@ std::string signature(const vm::Program& P, const vm::Space& S, int kind, int V,
     put(&A->n_out, sizeof A->n_out);
     put(&A->n_red, sizeof A->n_red);
     put(&A->out_dtype, sizeof A->out_dtype);
+    put(&A->n_extra, sizeof A->n_extra);
+    put(A->extra_op, sizeof(int) * A->n_extra);
   }
   return k;
 }
@@ -306,11 +308,28 @@ std::string gen_reduce(const vm::Program& P, const vm::Space& S, const ReduceArg
        "    case 5: return (a != 0u) | (b != 0u);\n"
        "    case 6: return (int32_t)a > (int32_t)b ? a : b;\n"
        "    default: return (int32_t)a < (int32_t)b ? a : b;\n  }\n}\n";
+  const int n_acc = 1 + A.n_extra;
   o << "extern \"C\" __global__ void __launch_bounds__(256) rew_reduce(" << params(P, false)
-    << (P.n_leaves ? ", " : "") << "void* out) {\n";
+    << (P.n_leaves ? ", " : "") << "void* out";
+  for (int x = 0; x < A.n_extra; ++x) o << ", void* out" << x + 1;
+  o << ") {\n";
   put_space(o, S);
   put_leaves(o, P);
   o << "  const int op = " << A.op << ";\n";
+  for (int x = 0; x < A.n_extra; ++x) o << "  const int op" << x + 1 << " = " << A.extra_op[x] << ";\n";
+  // one accumulator per op, each updated in the same element order: `stmt`
+  // with @ -> the accumulator's suffix and % -> its op
+  auto accs = [&](const std::string& stmt) {
+    std::string all;
+    for (int x = 0; x < n_acc; ++x) {
+      std::string t = stmt;
+      const std::string suf = x ? std::to_string(x) : "";
+      for (size_t p; (p = t.find('@')) != std::string::npos;) t.replace(p, 1, suf);
+      for (size_t p; (p = t.find('%')) != std::string::npos;) t.replace(p, 1, "op" + suf);
+      all += t;
+    }
+    return all;
+  };
   o << "  const uint32_t n_out = " << A.n_out << "u, n_red = " << A.n_red << "u;\n";
   std::string outs[vm::kMaxOuts];
   if (A.n_red >= 128) {
@@ -318,7 +337,7 @@ std::string gen_reduce(const vm::Program& P, const vm::Space& S, const ReduceArg
     o << "  const int lane = threadIdx.x & 63;\n";
     o << "  for (uint32_t r_out = blockIdx.x * 4u + (threadIdx.x >> 6); r_out < n_out; r_out += "
          "gridDim.x * 4u) {\n";
-    o << "   uint32_t acc = red_init_j(op);\n";
+    o << accs("   uint32_t acc@ = red_init_j(%);\n");
     o << "   for (uint32_t r0 = lane * " << V << "u; r0 < n_red; r0 += " << 64 * V * kUnroll
       << "u) {\n";
     for (int u = 0; u < kUnroll; ++u) {
@@ -332,38 +351,44 @@ std::string gen_reduce(const vm::Program& P, const vm::Space& S, const ReduceArg
     for (int u = 0; u < kUnroll; ++u) {
       const std::string sfx = "_" + std::to_string(u);
       put_body(o, P, V, sfx.c_str(), outs, ("lin" + sfx).c_str(), ("c" + sfx).c_str());
-      o << "    if (ok" << sfx << ") for (int j = 0; j < " << V
-        << "; ++j) acc = red_op_j(op, acc, " << outs[0] << "[j]);\n";
+      o << "    if (ok" << sfx << ") for (int j = 0; j < " << V << "; ++j) {\n"
+        << accs("     acc@ = red_op_j(%, acc@, " + outs[0] + "[j]);\n") << "    }\n";
     }
     o << "   }\n";
-    o << "   for (int m = 32; m >= 1; m >>= 1) acc = red_op_j(op, acc, __shfl_xor(acc, m, 64));\n";
-    o << "   if (lane == 0) store_scalar(out, " << A.out_dtype << ", r_out, acc);\n";
+    o << "   for (int m = 32; m >= 1; m >>= 1) {\n"
+      << accs("    acc@ = red_op_j(%, acc@, __shfl_xor(acc@, m, 64));\n") << "   }\n";
+    o << "   if (lane == 0) {\n"
+      << accs("    store_scalar(out@, " + std::to_string(A.out_dtype) + ", r_out, acc@);\n")
+      << "   }\n";
     o << "  }\n}\n";
   } else {
     o << "  for (uint32_t r_out = blockIdx.x * 256u + threadIdx.x; r_out < n_out; r_out += "
          "gridDim.x * 256u) {\n";
-    o << "   uint32_t acc = red_init_j(op);\n";
+    o << accs("   uint32_t acc@ = red_init_j(%);\n");
     o << "   for (uint32_t r = 0; r < n_red; ++r) {\n";
     o << "    const uint32_t lin = r_out * n_red + r;\n";
     o << "    int32_t c[kRank]; delinearize(S, lin, c);\n";
     put_body(o, P, 1, "", outs, "lin", "c");
-    o << "    acc = red_op_j(op, acc, " << outs[0] << "[0]);\n";
+    o << accs("    acc@ = red_op_j(%, acc@, " + outs[0] + "[0]);\n");
     o << "   }\n";
-    o << "   store_scalar(out, " << A.out_dtype << ", r_out, acc);\n";
+    o << accs("   store_scalar(out@, " + std::to_string(A.out_dtype) + ", r_out, acc@);\n");
     o << "  }\n}\n";
   }
   return o.str();
 }
 
-bool launch(JitFn* f, const vm::Program& P, void* extra_out, bool outs, int64_t blocks,
+bool launch(JitFn* f, const vm::Program& P, const ReduceArgs* A, bool outs, int64_t blocks,
             hipStream_t stream) {
-  void* args[vm::kMaxLeaves + vm::kMaxOuts + 1];
-  const void* ptrs[vm::kMaxLeaves + vm::kMaxOuts + 1];
+  void* args[vm::kMaxLeaves + vm::kMaxOuts + 4];
+  const void* ptrs[vm::kMaxLeaves + vm::kMaxOuts + 4];
   int n = 0;
   for (int i = 0; i < P.n_leaves; ++i) ptrs[n++] = P.leaf[i].ptr;
   if (outs)
     for (int q = 0; q < P.n_outs; ++q) ptrs[n++] = P.out[q].ptr;
-  if (extra_out) ptrs[n++] = extra_out;
+  if (A) {
+    ptrs[n++] = A->out;
+    for (int x = 0; x < A->n_extra; ++x) ptrs[n++] = A->extra_out[x];
+  }
   for (int i = 0; i < n; ++i) args[i] = (void*)&ptrs[i];
   REW_HIP(hipModuleLaunchKernel(f->fn, (unsigned)blocks, 1, 1, 256, 1, 1, 0, stream, args,
                                 nullptr));
@@ -391,7 +416,7 @@ bool jit_launch_reduce(const vm::Program& P, const vm::Space& S, const ReduceArg
   if (!f) return false;
   int64_t blocks = A.n_red >= 128 ? (A.n_out + 3) / 4 : (A.n_out + 255) / 256;
   if (blocks > 65536) blocks = 65536;
-  return launch(f, P, A.out, false, blocks, stream);
+  return launch(f, P, &A, false, blocks, stream);
 }
 
 int64_t jit_cache_hits() { return g_jit_hits.load(std::memory_order_relaxed); }

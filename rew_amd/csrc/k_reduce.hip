@@ -100,6 +100,19 @@ void launch_reduce(const vm::Program& P, const vm::Space& S,
                    const ReduceArgs& A, bool vec, hipStream_t stream) {
   if (A.n_out == 0) return;
   if (jit_launch_reduce(P, S, A, vec, stream)) return;
+  if (A.n_extra > 0) {
+    // the interpreter reduces one op per pass
+    for (int x = -1; x < A.n_extra; ++x) {
+      ReduceArgs one = A;
+      one.n_extra = 0;
+      if (x >= 0) {
+        one.op = A.extra_op[x];
+        one.out = A.extra_out[x];
+      }
+      launch_reduce(P, S, one, vec, stream);
+    }
+    return;
+  }
   if (A.n_red >= 128) {
     int64_t blocks = A.n_out < 65536 ? A.n_out : 65536;
     if (vec)

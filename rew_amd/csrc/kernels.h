@@ -35,6 +35,12 @@ struct ReduceArgs {
   uint32_t n_red;   // product of reduced dims
   void* out;
   int out_dtype;
+  // further reductions of the same values in the same pass (rew's
+  // reduceSum and reduceMax of one tensor over the same axes), each into its
+  // own output of out_dtype; every op accumulates in the single-op order
+  int n_extra = 0;
+  int extra_op[3] = {0, 0, 0};
+  void* extra_out[3] = {nullptr, nullptr, nullptr};
 };
 // Space = [kept..., reduced...]; program output 0 names the value register.
 void launch_reduce(const vm::Program& P, const vm::Space& S,

@@ -1071,16 +1071,37 @@ void Lower::emit_reduce(Node* n) {
       A.n_red = (uint32_t)n_red;
       A.out = out->data();
       A.out_dtype = out->dt;
+      // sibling reductions of the same tensor over the same axes (other ops)
+      // ride along in the same pass
+      std::vector<Node*> sib;
+      for (Node* m : nodes) {
+        if (m == n || m->kind != K_REDUCE || m->in[0] != x || m->l0 != n->l0 || m->sub == n->sub)
+          continue;
+        Tensor* mo = m->out[0];
+        if (mo->st || !mo->plan_mat || mo->dt != out->dt || sib.size() == 3) continue;
+        bool dup = false;
+        for (Node* q : sib) dup = dup || q->sub == m->sub;
+        if (dup) continue;
+        sib.push_back(m);
+      }
+      for (Node* m : sib) {
+        tensor_alloc(m->out[0]);
+        A.extra_op[A.n_extra] = m->sub;
+        A.extra_out[A.n_extra++] = m->out[0]->data();
+      }
       const bool vec = n_red > 0 && (dims.back() % kVec) == 0 &&
                        (n_red % kVec) == 0 && space.d[X.rank - 1] != 1;
       set_leaf_modes(g.P, S, vec);
       if (c->profiling)
         prof_begin(c, "reduce{" + std::to_string(n_out) + "x" + std::to_string(n_red) + "x" +
-                          std::to_string(g.P.n_ins) + "}");
+                          std::to_string(g.P.n_ins) +
+                          (sib.empty() ? "" : "," + std::to_string(1 + sib.size()) + "ops") +
+                          "}");
       launch_reduce(g.P, S, A, vec, c->stream);
       prof_end(c);
-      note_launch(c, g.P.n_ins > 1);
+      note_launch(c, g.P.n_ins > 1 || !sib.empty());
       reduce_done[key] = out;
+      for (Node* m : sib) reduce_done[std::make_tuple(x, m->sub, m->l0, out->dt)] = m->out[0];
       return;
     } catch (GenFail&) {
       tensor_drop_storage(out);

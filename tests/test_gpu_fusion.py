@@ -318,3 +318,32 @@ def test_repeated_reduction_runs_once(gpu, oracle):
     y = np.maximum(x + x, 0)
     s = y.astype(np.float64).sum(1)
     np.testing.assert_allclose(got, (s + s / 1024).astype(np.float32), rtol=1e-5)
+
+
+@pytest.mark.parametrize("shape,axes", [((128, 1024), [1]), ((64, 100), [1]), ((8, 16, 300), [2])])
+def test_sibling_reductions_one_pass(gpu, oracle, shape, axes):
+    """reduceSum, reduceMax and reduceMin of one tensor over the same axes
+    run as one pass with an accumulator per op, each in the single-op order:
+    equal to the op-by-op path bit for bit."""
+    x = oracle.normal_f32(oracle.init_key(960 + shape[-1]), int(np.prod(shape))).reshape(shape)
+
+    def fn():
+        y = nn.relu(O.add(E.fromHost(x), E.fromHost(x)))
+        return [O.reduceSum(y, axes), O.reduceMax(y, axes), O.reduceMin(y, axes)]
+
+    E.profileBegin()
+    outs = fn()
+    got = [E.toHost(t) for t in outs]
+    prof = E.profileEnd()
+    assert sum(c for n, c, _ in prof if n.startswith("reduce")) == 1, prof
+    E.setMode(E.MODE_OP_BY_OP)
+    try:
+        ref = [E.toHost(t) for t in fn()]
+    finally:
+        E.setMode(E.MODE_DEFERRED)
+    for g_, r_ in zip(got, ref):
+        np.testing.assert_array_equal(g_, r_)
+    y = np.maximum(x + x, 0)
+    np.testing.assert_allclose(got[0], y.astype(np.float64).sum(axis=tuple(axes)), rtol=1e-5)
+    np.testing.assert_array_equal(got[1], y.max(axis=tuple(axes)))
+    np.testing.assert_array_equal(got[2], y.min(axis=tuple(axes)))
