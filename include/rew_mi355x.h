@@ -89,7 +89,10 @@ int rew_mi355x_shutdown(rew_mi355x_ctx* ctx);
 
 /* Copy `nbytes` host bytes into a new device tensor of `dtype`/`shape`.
  * The host buffer may be reused as soon as the call returns
- * (ImmutableUntilTransferDone semantics).
+ * (ImmutableUntilTransferDone semantics).  Tensors are immutable, so a
+ * tensor of at most 256 bytes whose dtype, shape and bytes match an earlier
+ * upload shares that upload's device storage (no copy; the scalars rew's
+ * composites upload on every call); rew_mi355x_clear_cache drops them.
  * Replaces: transferToDevice (src/rew/eager.nim:221-235) and through it
  * fromHost[T] / constant (src/rew/eager.nim:360-377, src/rew/ops/literal.nim:56-77). */
 int rew_mi355x_from_host(rew_mi355x_ctx* ctx, int dtype, const int64_t* shape,
@@ -154,7 +157,8 @@ int rew_mi355x_sync(rew_mi355x_ctx* ctx);
  * flushes first. */
 int rew_mi355x_set_mode(rew_mi355x_ctx* ctx, int mode);
 
-/* Drop the cached kernel plans (the caching allocator is kept).
+/* Drop the cached small device constants (see rew_mi355x_from_host); the
+ * programs compiled at run time and the caching allocator are kept.
  * Replaces: clearEagerCache (src/rew/eager.nim:1713-1715). */
 int rew_mi355x_clear_cache(rew_mi355x_ctx* ctx);
 

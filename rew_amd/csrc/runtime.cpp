@@ -131,6 +131,18 @@ void tensor_alias(Tensor* t, Tensor* src) {
   t->st->refs++;
 }
 
+void storage_release(Storage* s) {
+  if (s && --s->refs == 0) {
+    s->ctx->alloc.put(s->ptr, s->bytes);
+    delete s;
+  }
+}
+
+void const_cache_clear(Ctx* c) {
+  for (auto& kv : c->const_cache) storage_release(kv.second);
+  c->const_cache.clear();
+}
+
 void tensor_drop_storage(Tensor* t) {
   Storage* s = t->st;
   if (!s) return;
@@ -295,6 +307,7 @@ int rew_mi355x_shutdown(rew_mi355x_ctx* ctx) {
     REW_HIP(hipSetDevice(c->ordinal));
     flush(c);
     REW_HIP(hipStreamSynchronize(c->stream));
+    const_cache_clear(c);
     c->alloc.trim();
   });
 }
@@ -319,12 +332,34 @@ int rew_mi355x_from_host(rew_mi355x_ctx* ctx, int dtype, const int64_t* shape,
     std::lock_guard<std::recursive_mutex> g(c->mu);
     REW_HIP(hipSetDevice(c->ordinal));
     Tensor* t = new_tensor(c, dtype, s);
-    try {
-      tensor_alloc(t);
-      h2d(c, t->data(), host, (size_t)want);
-    } catch (...) {
-      maybe_destroy(t);
-      throw;
+    // small constants: one device copy per distinct (dtype, shape, bytes)
+    constexpr int64_t kConstMax = 256;
+    std::string key;
+    if (want > 0 && want <= kConstMax) {
+      key.reserve(16 + 8 * rank + (size_t)want);
+      key.append((const char*)&dtype, sizeof dtype);
+      key.append((const char*)&rank, sizeof rank);
+      key.append((const char*)shape, sizeof(int64_t) * rank);
+      key.append((const char*)host, (size_t)want);
+      auto hit = c->const_cache.find(key);
+      if (hit != c->const_cache.end()) {
+        t->st = hit->second;
+        t->st->refs++;
+      }
+    }
+    if (!t->st) {
+      try {
+        tensor_alloc(t);
+        h2d(c, t->data(), host, (size_t)want);
+      } catch (...) {
+        maybe_destroy(t);
+        throw;
+      }
+      if (!key.empty()) {
+        if (c->const_cache.size() >= 4096) const_cache_clear(c);
+        t->st->refs++;
+        c->const_cache.emplace(key, t->st);
+      }
     }
     if (want <= 16 && want > 0) {
       t->has_host = true;
@@ -487,8 +522,9 @@ int rew_mi355x_clear_cache(rew_mi355x_ctx* ctx) {
   return guarded([&] {
     Ctx* c = as_ctx(ctx);
     std::lock_guard<std::recursive_mutex> g(c->mu);
-    // Plans are rebuilt per flush; nothing is cached beyond the allocator.
-    (void)c;
+    // Plans are rebuilt per flush; the cached small constants are dropped
+    // (their storage returns to the allocator once no tensor uses it).
+    const_cache_clear(c);
   });
 }
 

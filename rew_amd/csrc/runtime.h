@@ -105,6 +105,12 @@ struct Ctx {
   bool no_fusion_patterns = false;  // REW_MI355X_NO_PATTERNS=1: per-op kernels only
   rew_mi355x_stats stats{};
   int64_t jit_hits_base = 0;  // jit_cache_hits() when the stats were last reset
+  // device copies of small host constants (dtype, shape and bytes as the
+  // key): eager tensors are immutable, so a repeated upload of the same
+  // scalar (rew's composites upload eps, 1.0, mask values... every call)
+  // shares one storage instead of another H2D copy.  Each entry holds one
+  // reference on its storage.
+  std::unordered_map<std::string, Storage*> const_cache;
   // pinned staging ring for small host->device copies
   uint8_t* ring = nullptr;
   size_t ring_size = 0, ring_pos = 0;
@@ -119,6 +125,8 @@ struct Ctx {
 // ---- runtime services (runtime.cpp) -----------------------------------------
 Tensor* new_tensor(Ctx* c, int dt, const Shape& s);
 void tensor_alloc(Tensor* t);                 // give t fresh storage
+void storage_release(Storage* s);             // drop one reference
+void const_cache_clear(Ctx* c);               // release every cached constant
 void tensor_alias(Tensor* t, Tensor* src);    // share src's storage
 void tensor_drop_storage(Tensor* t);
 void maybe_destroy(Tensor* t);                // free when unreferenced

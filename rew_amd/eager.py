@@ -330,6 +330,12 @@ def resetStats(d: Device | None = None) -> None:
     _check(_lib.load().rew_mi355x_reset_stats(context(d)))
 
 
+def clearEagerCache(d: Device | None = None) -> None:
+    """src/rew/eager.nim:1713-1715: drops the backend's cached state (here the
+    device copies of small constants)."""
+    _check(_lib.load().rew_mi355x_clear_cache(context(d)))
+
+
 # ---- dispatcher (src/rew/dispatch.nim:47-85) ---------------------------------------
 
 EagerBackend = Callable[[str, Sequence[Tensor], Sequence[tuple]], list]

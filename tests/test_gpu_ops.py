@@ -262,3 +262,20 @@ def test_deferred_equals_op_by_op(gpu):
         outs.append(host(y))
     E.setMode(E.MODE_DEFERRED)
     np.testing.assert_array_equal(outs[0], outs[1])
+
+
+def test_small_constants_share_one_upload(gpu):
+    """Repeated uploads of the same small constant share one device copy
+    (no H2D copy), and every handle still reads back its own value."""
+    E.sync()
+    E.resetStats()
+    vals = [1e-5, 2.5, 1e-5, -1.0, 2.5, 1e-5]
+    ts = [O.scalarF32(v) for v in vals]
+    got = [float(E.toHost(t)) for t in ts]
+    assert got == [float(np.float32(v)) for v in vals]
+    big = np.arange(1000, dtype=np.float32)
+    a, b = E.fromHost(big), E.fromHost(big)  # above the size limit: two uploads
+    np.testing.assert_array_equal(E.toHost(a), E.toHost(b))
+    del ts, a, b
+    E.clearEagerCache()
+    assert float(E.toHost(O.scalarF32(3.0))) == 3.0
