@@ -54,6 +54,7 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4s lds_v4s;
 typedef __attribute__((address_space(3))) void lds_void;
@@ -77,9 +78,14 @@ __device__ __forceinline__ void to_lds16(const void* src, uint8_t* lds) {
 // buffer_load_dwordx4 ... lds: base and extent in the SGPR descriptor, the
 // lane's fixed byte offset in a VGPR, the k advance in an SGPR, so a k-tile
 // of DMA costs no VALU address arithmetic.
+// (the base is wave-uniform; readfirstlane states it, so the descriptor is
+// built in SGPRs whatever the rest of the kernel does to register choices)
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
-                                           0x00020000);
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  void* p = (void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(p, (short)0, (int)bytes, 0x00020000);
 }
 __device__ __forceinline__ void buf_to_lds16(__amdgpu_buffer_rsrc_t r, uint32_t voff,
                                              uint32_t soff, uint8_t* lds) {
@@ -92,6 +98,11 @@ __device__ __forceinline__ void block_barrier() {
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 }
+
+template <int V>
+struct IntK {
+  static constexpr int value = V;
+};
 
 __device__ __forceinline__ void tile_order(int64_t bid, int64_t tiles_m, int64_t tiles_n,
                                            int64_t batch, int64_t* b, int64_t* tm,
@@ -437,100 +448,217 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
         }
     }
   }
+  // Phase 2 gives each thread one fixed 16-byte column chunk of the output
+  // (chunk ch of CH per row) on rows r_in, r_in + RPI, ...; its column
+  // operands (bias, gate bias) are requested before the barrier.  Operand
+  // addresses of rows / columns past the matrix are clamped into it, so
+  // every load is unconditional; only the stores are predicated.
+  constexpr int OC = DUAL ? 128 : 256;  // output columns per tile
+  constexpr int CH = OC / 8;            // 16-byte chunks per output row
+  constexpr int RPI = 256 / CH;         // rows per pass of the workgroup
+  constexpr int PASSES = BM / RPI;
+  const int ch = tid % CH, r_in = tid / CH;
+  const int64_t n = n0 + ch * 8;
+  const bool col_ok = n < g.N;
+  const int64_t nc = col_ok ? n : g.N - 8;                          // clamped column
+  const int lc = DUAL ? (ch >> 3) * 128 + (ch & 7) * 8 : ch * 8;  // column in the C tile
+  const int epi = DUAL ? (int)EPI_SWIGLU : g.epi;
+  uint4 bv = make_uint4(0, 0, 0, 0), bv2 = make_uint4(0, 0, 0, 0);
+  if (epi != EPI_NONE) bv = *(const uint4*)((const uint16_t*)(GROUP ? ga.bias[grp] : g.bias) + nc);
+  if constexpr (DUAL)
+    bv2 = *(const uint4*)((const uint16_t*)(GROUP ? ga.bias2[grp] : g.bias2) + nc);
   __syncthreads();
+
   // phase 2: 16-byte row chunks (a row's 512 bytes per 32 lanes) with the
-  // bias / residual / gate operands
-  auto c_chunk = [&](int row, int lc) -> uint4 {
+  // bias / residual / gate / rotation arithmetic, one loop per epilogue
+  // kind so no per-element test or branch sits inside it.  Row operands
+  // (residual, rotation tables) are fetched U passes at a time, the next
+  // batch requested before this batch's stores: the wait for a batch then
+  // never includes stores (vmcnt counts both, in issue order).
+  auto c_chunk = [&](int row, int col) -> uint4 {
     const int lr = row & 63;
-    return *(const uint4*)(S(row >> 6) + lr * 512 + ((((lc >> 3) ^ (lr & 15))) * 16));
+    return *(const uint4*)(S(row >> 6) + lr * 512 + ((((col >> 3) ^ (lr & 15))) * 16));
   };
-  constexpr int OC = DUAL ? 128 : 256;
-  constexpr int CH = OC / 8;
+  auto bf = [](uint16_t h) { return vm::as_f((uint32_t)h << 16); };
   uint16_t* C = (uint16_t*)g.c + b * g.c_sb;
-  const uint16_t* bias = (const uint16_t*)(GROUP ? ga.bias[grp] : g.bias);
-  const uint16_t* bias2 = nullptr;
-  if constexpr (DUAL) bias2 = (const uint16_t*)(GROUP ? ga.bias2[grp] : g.bias2);
-  const uint16_t* res = (const uint16_t*)g.res + b * g.res_sb;
-  // (a runtime loop: the epilogue runs once per tile, and unrolled it would
-  // stream tens of KB of straight-line code through the instruction cache)
+  const uint16_t* bh = (const uint16_t*)&bv;
+  auto row_of = [&](int p) { return p * RPI + r_in; };
+  auto row_ok = [&](int row) { return row < m_rows && col_ok; };
+  auto crow = [&](int row) { return row0 + (row < m_rows ? row : (int)m_rows - 1); };
+  constexpr int U = 8;
+  static_assert(PASSES % U == 0, "passes per operand batch");
+
+  if (epi == EPI_SWIGLU) {
+    const int64_t c_sm = g.c_sm;
+    const uint16_t* buh = (const uint16_t*)&bv2;
+    // (runtime loops here: the epilogue runs once per tile, and unrolled it
+    // would stream tens of KB of straight-line code through the I-cache)
 #pragma unroll 1
-  for (int it = 0; it < BM * CH / 256; ++it) {
-    const int t = it * 256 + tid;
-    const int row = t / CH, ch = t - row * CH;
-    const int64_t m = row0 + row;
-    const int64_t n = n0 + ch * 8;
-    if (row >= m_rows || n >= g.N) continue;
-    const int lc = DUAL ? (ch >> 3) * 128 + (ch & 7) * 8 : ch * 8;
-    const uint4 dv = c_chunk(row, lc);
-    const uint16_t* dh = (const uint16_t*)&dv;
-    uint16_t out[8];
-    if constexpr (DUAL) {
-      const uint4 uv = c_chunk(row, lc + 64);
-      const uint4 bg = *(const uint4*)(bias + n);
-      const uint4 bu = *(const uint4*)(bias2 + n);
-      const uint16_t* uh = (const uint16_t*)&uv;
-      const uint16_t* bgh = (const uint16_t*)&bg;
-      const uint16_t* buh = (const uint16_t*)&bu;
+    for (int p0 = 0; p0 < PASSES; p0 += U) {
 #pragma unroll
-      for (int x = 0; x < 8; ++x) {
-        // GatedFeedForward's gate, op by op in fp32 (gated_ffn.nim:46-67,
-        // activation.nim:28-38)
-        const float yg = vm::round_bf16(vm::as_f((uint32_t)dh[x] << 16) +
-                                        vm::as_f((uint32_t)bgh[x] << 16));
-        const float yu = vm::round_bf16(vm::as_f((uint32_t)uh[x] << 16) +
-                                        vm::as_f((uint32_t)buh[x] << 16));
-        const float e = expf(-yg);
-        const float den = 1.0f + e;
-        const float sig = 1.0f / den;
-        const float act = yg * sig;
-        out[x] = vm::bf16_bits(act * yu);
-      }
-    } else {
-      if (g.epi == EPI_NONE) {
-#pragma unroll
-        for (int x = 0; x < 8; ++x) out[x] = dh[x];
-      } else if (g.epi == EPI_BIAS_ROPE) {
-        // Linear's bias add, then applyRotate (rope.nim:56-108) on the four
-        // pairs of this chunk, scattered into the rotated tensor's layout
-        const uint4 bv = *(const uint4*)(bias + n);
-        const uint16_t* bh = (const uint16_t*)&bv;
-        const uint32_t mm = (uint32_t)m, nn = (uint32_t)n;
-        const uint32_t bq = mm / (uint32_t)g.rope_S, sq = mm - bq * (uint32_t)g.rope_S;
-        const uint32_t hq = nn / (uint32_t)g.rope_D, dq = nn - hq * (uint32_t)g.rope_D;
-        const int64_t tb = bq * g.rope_tb + sq * g.rope_ts + hq * g.rope_th + (dq >> 1) * g.rope_ti;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const float x0 = vm::round_bf16(vm::as_f((uint32_t)dh[2 * u] << 16) +
-                                          vm::as_f((uint32_t)bh[2 * u] << 16));
-          const float x1 = vm::round_bf16(vm::as_f((uint32_t)dh[2 * u + 1] << 16) +
-                                          vm::as_f((uint32_t)bh[2 * u + 1] << 16));
-          const float cs = g.rope_cos[tb + u * g.rope_ti];
-          const float sn = g.rope_sin[tb + u * g.rope_ti];
-          const float t1 = cs * x0;
-          const float t2 = sn * x1;
-          const float t3 = sn * x0;
-          const float t4 = cs * x1;
-          out[2 * u] = vm::bf16_bits(t1 - t2);
-          out[2 * u + 1] = vm::bf16_bits(t3 + t4);
-        }
-        *(uint4*)(C + bq * g.out_b + sq * g.out_s + hq * g.out_h + dq) = *(const uint4*)out;
-        continue;
-      } else {
-        const uint4 bv = *(const uint4*)(bias + n);
-        const uint16_t* bh = (const uint16_t*)&bv;
-        uint4 rv = make_uint4(0, 0, 0, 0);
-        if (g.epi == EPI_BIAS_RES) rv = *(const uint4*)(res + m * g.res_sm + n);
-        const uint16_t* rh = (const uint16_t*)&rv;
+      for (int u = 0; u < U; ++u) {
+        const int row = row_of(p0 + u);
+        const uint4 dv = c_chunk(row, lc);
+        const uint4 uv = c_chunk(row, lc + 64);
+        const uint16_t* dh = (const uint16_t*)&dv;
+        const uint16_t* uh = (const uint16_t*)&uv;
+        uint16_t out[8];
 #pragma unroll
         for (int x = 0; x < 8; ++x) {
-          float y = vm::round_bf16(vm::as_f((uint32_t)dh[x] << 16) +
-                                   vm::as_f((uint32_t)bh[x] << 16));
-          if (g.epi == EPI_BIAS_RES) y = vm::round_bf16(vm::as_f((uint32_t)rh[x] << 16) + y);
-          out[x] = vm::bf16_bits(y);
+          // GatedFeedForward's gate, op by op in fp32 (gated_ffn.nim:46-67,
+          // activation.nim:28-38)
+          const float yg = vm::round_bf16(bf(dh[x]) + bf(bh[x]));
+          const float yu = vm::round_bf16(bf(uh[x]) + bf(buh[x]));
+          const float e = expf(-yg);
+          const float den = 1.0f + e;
+          const float sig = 1.0f / den;
+          const float act = yg * sig;
+          out[x] = vm::bf16_bits(act * yu);
         }
+        if (row_ok(row)) *(uint4*)(C + (row0 + row) * c_sm + n) = *(const uint4*)out;
       }
     }
-    *(uint4*)(C + m * g.c_sm + n) = *(const uint4*)out;
+  } else if (epi == EPI_NONE || epi == EPI_BIAS) {
+    const bool add = epi == EPI_BIAS;
+    const int64_t c_sm = g.c_sm;
+#pragma unroll 1
+    for (int p0 = 0; p0 < PASSES; p0 += U) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int row = row_of(p0 + u);
+        uint4 dv = c_chunk(row, lc);
+        if (add) {
+          uint16_t* dh = (uint16_t*)&dv;
+#pragma unroll
+          for (int x = 0; x < 8; ++x) dh[x] = vm::bf16_bits(bf(dh[x]) + bf(bh[x]));
+        }
+        if (row_ok(row)) *(uint4*)(C + (row0 + row) * c_sm + n) = dv;
+      }
+    }
+  } else if (epi == EPI_BIAS_RES) {
+    const uint16_t* res = (const uint16_t*)g.res + b * g.res_sb;
+    const int64_t res_sm = g.res_sm, c_sm = g.c_sm;
+    // two operand buffers used in turn (a register copy of a pending load
+    // would have to wait for it)
+    uint4 ra[U], rb[U];
+    auto fetch = [&](int p0, uint4* dst) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) dst[u] = *(const uint4*)(res + crow(row_of(p0 + u)) * res_sm + nc);
+    };
+    auto apply = [&](int p0, const uint4* rv) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int row = row_of(p0 + u);
+        const uint4 dv = c_chunk(row, lc);
+        const uint16_t* dh = (const uint16_t*)&dv;
+        const uint16_t* rh = (const uint16_t*)&rv[u];
+        uint16_t out[8];
+#pragma unroll
+        for (int x = 0; x < 8; ++x) {
+          const float y = vm::round_bf16(bf(dh[x]) + bf(bh[x]));
+          out[x] = vm::bf16_bits(bf(rh[x]) + y);
+        }
+        if (row_ok(row)) *(uint4*)(C + (row0 + row) * c_sm + n) = *(const uint4*)out;
+      }
+    };
+    fetch(0, ra);
+#pragma unroll 1
+    for (int p0 = 0; p0 < PASSES; p0 += 2 * U) {
+      fetch(p0 + U, rb);
+      apply(p0, ra);
+      if (p0 + 2 * U < PASSES) fetch(p0 + 2 * U, ra);
+      apply(p0 + U, rb);
+    }
+  } else {
+    // EPI_BIAS_ROPE: Linear's bias add, then applyRotate (rope.nim:56-108)
+    // on the four pairs of a chunk, scattered into the rotated tensor's
+    // layout
+    constexpr int UR = 4;
+    static_assert(PASSES % (2 * UR) == 0, "rotation operand batches");
+    const uint32_t nn = (uint32_t)nc;
+    const uint32_t hq = nn / (uint32_t)g.rope_D, dq = nn - hq * (uint32_t)g.rope_D;
+    const uint32_t rS = (uint32_t)g.rope_S;
+    const int64_t rtb = g.rope_tb, rts = g.rope_ts, rti = g.rope_ti;
+    const int64_t hoff = hq * g.rope_th + (dq >> 1) * rti;
+    const int64_t ob = g.out_b, os = g.out_s, oh = hq * g.out_h + dq;
+    const float* rcos = g.rope_cos;
+    const float* rsin = g.rope_sin;
+    // The four angles of a chunk sit at tb + x * rti.  Unit or 2-element
+    // pair strides (the latter: rew's [S, D] tables with each angle stored
+    // twice, read through applyRotate's even-element slice) with 16-byte
+    // aligned rows take one or two 16-byte loads per table and row.
+    const bool al = ((rtb | rts | g.rope_th) & 3) == 0 &&
+                    (((uintptr_t)rcos | (uintptr_t)rsin) & 15) == 0;
+    const int vmode = !al ? 0 : rti == 1 ? 1 : rti == 2 ? 2 : 0;
+    struct Rot {
+      float c[UR][4], s[UR][4];
+    };
+    auto rotate = [&](auto VM) {
+      constexpr int kV = decltype(VM)::value;
+      Rot ta, tb2;
+      auto fetch = [&](int p0, Rot& t) {
+#pragma unroll
+        for (int u = 0; u < UR; ++u) {
+          const uint32_t mm = (uint32_t)crow(row_of(p0 + u));
+          const uint32_t bq = mm / rS, sq = mm - bq * rS;
+          const int64_t tb = bq * rtb + sq * rts + hoff;
+          if constexpr (kV == 1) {
+            const float4 cv = *(const float4*)(rcos + tb);
+            const float4 sv = *(const float4*)(rsin + tb);
+            t.c[u][0] = cv.x; t.c[u][1] = cv.y; t.c[u][2] = cv.z; t.c[u][3] = cv.w;
+            t.s[u][0] = sv.x; t.s[u][1] = sv.y; t.s[u][2] = sv.z; t.s[u][3] = sv.w;
+          } else if constexpr (kV == 2) {
+            f32x4_t c0 = *(const f32x4_t*)(rcos + tb), c1 = *(const f32x4_t*)(rcos + tb + 4);
+            f32x4_t s0 = *(const f32x4_t*)(rsin + tb), s1 = *(const f32x4_t*)(rsin + tb + 4);
+            // (whole 16-byte loads: left alone the compiler splits them into
+            // the dwords used, four times the memory instructions)
+            asm volatile("" : "+v"(c0), "+v"(c1), "+v"(s0), "+v"(s1));
+            t.c[u][0] = c0[0]; t.c[u][1] = c0[2]; t.c[u][2] = c1[0]; t.c[u][3] = c1[2];
+            t.s[u][0] = s0[0]; t.s[u][1] = s0[2]; t.s[u][2] = s1[0]; t.s[u][3] = s1[2];
+          } else {
+#pragma unroll
+            for (int x = 0; x < 4; ++x) {
+              t.c[u][x] = rcos[tb + x * rti];
+              t.s[u][x] = rsin[tb + x * rti];
+            }
+          }
+        }
+      };
+      auto apply = [&](int p0, const Rot& t) {
+#pragma unroll
+        for (int u = 0; u < UR; ++u) {
+          const int row = row_of(p0 + u);
+          const uint32_t mm = (uint32_t)(row0 + row);
+          const uint32_t bq = mm / rS, sq = mm - bq * rS;
+          const uint4 dv = c_chunk(row, lc);
+          const uint16_t* dh = (const uint16_t*)&dv;
+          uint16_t out[8];
+#pragma unroll
+          for (int x = 0; x < 4; ++x) {
+            const float x0 = vm::round_bf16(bf(dh[2 * x]) + bf(bh[2 * x]));
+            const float x1 = vm::round_bf16(bf(dh[2 * x + 1]) + bf(bh[2 * x + 1]));
+            const float t1 = t.c[u][x] * x0;
+            const float t2 = t.s[u][x] * x1;
+            const float t3 = t.s[u][x] * x0;
+            const float t4 = t.c[u][x] * x1;
+            out[2 * x] = vm::bf16_bits(t1 - t2);
+            out[2 * x + 1] = vm::bf16_bits(t3 + t4);
+          }
+          if (row_ok(row)) *(uint4*)(C + bq * ob + sq * os + oh) = *(const uint4*)out;
+        }
+      };
+      fetch(0, ta);
+#pragma unroll 1
+      for (int p0 = 0; p0 < PASSES; p0 += 2 * UR) {
+        fetch(p0 + UR, tb2);
+        apply(p0, ta);
+        if (p0 + 2 * UR < PASSES) fetch(p0 + 2 * UR, ta);
+        apply(p0 + UR, tb2);
+      }
+    };
+    if (vmode == 2) rotate(IntK<2>{});
+    else if (vmode == 1) rotate(IntK<1>{});
+    else rotate(IntK<0>{});
   }
 }
 

@@ -227,6 +227,42 @@ def test_rope_fused_into_projection(gpu, oracle, B, S, E_, H, D, transposed):
     bf16_close(_bits_f32(got), want)
 
 
+@pytest.mark.parametrize("tables", ["transposed", "pairs_broadcast"])
+def test_rope_fused_table_layouts(gpu, oracle, tables):
+    """applyRotate called directly with cos / sin tables in other layouts: a
+    [D, S] table read through a transpose (angle stride S: the epilogue's
+    element-wise table loads) and a [S, D / 2] table broadcast over the pair
+    axis (unit angle stride).  Fused or not, the result is bit-exact with op
+    by op and within the bf16 tolerance of the oracle."""
+    B, S, E_, H, D = 2, 48, 128, 2, 64
+    key = oracle.init_key(760)
+    w, b = _lin(oracle, key, E_, H * D)
+    x = oracle.round_bf16(oracle.normal_f32(oracle.fold_in(key, 2), B * S * E_).reshape(B * S, E_))
+    c, s = nn.rope_tables(D, S, 10000.0)
+
+    def table(t):
+        if tables == "transposed":
+            return O.transpose(O.constantF32([D, S], np.ascontiguousarray(t.T)), [1, 0])
+        half = O.constantF32([S, D // 2], np.ascontiguousarray(t[:, 0::2]))
+        return O.reshape(O.broadcastTo(half, [S, D // 2, 2], [0, 1]), [S, D])
+
+    def fn():
+        lin = nn.Linear(E.fromHost(w, DType.BFLOAT16), E.fromHost(b, DType.BFLOAT16))
+        y = O.transpose(O.reshape(lin.forward(E.fromHost(x, DType.BFLOAT16)), [B, S, H, D]),
+                        [0, 2, 1, 3])
+        cb = O.broadcastTo(table(c), [B, H, S, D], [2, 3])
+        sb = O.broadcastTo(table(s), [B, H, S, D], [2, 3])
+        return nn._to(nn.applyRotate(nn._f32(y), cb, sb), DType.BFLOAT16)
+
+    got, names = _run(fn)
+    ref, _ = _run(fn, op_by_op=True)
+    np.testing.assert_array_equal(got, ref)
+    want = _proj_rope(oracle, x, w, b, B, S, H, D, c, s, 0, True)
+    bf16_close(_bits_f32(got), want)
+    if tables == "transposed":
+        assert any("+bias+rope" in n for n in names), names
+
+
 @pytest.mark.parametrize("B,S,E_,H,KV,D", [(2, 96, 256, 4, 2, 64), (1, 200, 128, 2, 1, 136)])
 def test_qkv_projections_one_launch(gpu, oracle, B, S, E_, H, KV, D):
     """The q (rotated), k (rotated) and v projections of one input run as one
