@@ -8,12 +8,18 @@
 // and lane l of an instruction lands at LDS base + 16 l, so no VGPRs hold
 // staged data and no VALU work writes LDS.  The LDS layout is chosen
 // through the source address each lane fetches (k-tiles of BK = 32):
-//   * K-contiguous operands (A, and B when it is [N, K]): a 256 x 32 tile,
-//     64-byte rows of four 16-byte chunks, chunk c of row r stored at
-//     physical chunk c ^ ((r >> 2) & 3).  The 16 lanes a ds_read_b128
-//     serves per cycle read one logical chunk of 16 consecutive rows; rows
-//     r and r + 4 share a 256-byte bank window and the XOR gives them
-//     distinct chunks, so the 16 reads hit 16 distinct 16-byte bank slots.
+//   * A on the buffer path: k-tile PAIRS, a 256 x 64 tile of 128-byte rows
+//     (8 chunks; chunk c of row r at physical chunk c ^ ((r >> 1) & 7)), so
+//     each row of a pair is one whole cache line.  Moving A one 64-byte half
+//     line per k-tile cost the vector memory pipeline twice the requests
+//     (the address unit then stalls on the cache far more than a VGPR-staged
+//     kernel does) and measured 3-8 % slower.
+//   * K-contiguous operands otherwise (A on the K-tail path, B when it is
+//     [N, K]): a 256 x 32 tile, 64-byte rows of four 16-byte chunks, chunk c
+//     of row r stored at physical chunk c ^ ((r >> 2) & 3).  The 16 lanes a
+//     ds_read_b128 serves per cycle read one logical chunk of 16 consecutive
+//     rows; rows r and r + 4 share a 256-byte bank window and the XOR gives
+//     them distinct chunks, so the 16 reads hit 16 distinct 16-byte slots.
 //   * N-contiguous B (rew's [in, out] Linear weights, the common case): a
 //     32 x 256 tile, 512-byte k-rows of 32 chunks, chunk c of row k stored
 //     at c ^ (4 (k & 3)).  Fragments are read with ds_read_b64_tr_b16: in
@@ -23,12 +29,13 @@
 //     straight out of the untransposed tile.  Two such reads (kb, kb + 4)
 //     give the 8 k-values of one fragment.  The XOR spreads the 8 k-rows x
 //     4 chunks of one read over all bank groups.
-// The k-tiles stream through a ring of NS = 4 LDS stages (4 x 32 KiB): tile
-// t + 4 is requested right after the barrier that frees tile t's stage and
-// is first read three k-steps later.  On the Llama shapes the DMA stream
-// alone (no MFMAs) needs 0.45-0.64 us per 32-deep k-step and the MFMAs
-// alone about as long, so the two overlap rather than one hiding the other;
-// a fifth stage measured no faster.
+// The k-tiles stream through a ring: four B stages (16 KiB) and two A pair
+// stages (32 KiB) on the buffer path, four 32 KiB A+B stages on the K-tail
+// path.  B of tile t + 4 is requested right after the barrier that frees
+// tile t's stage and first read three k-steps later; an A pair two k-steps
+// before its first read.  On the Llama shapes a k-step of MFMAs alone takes
+// 1024 cycles and the full loop about 1230: the DMA overlaps the MFMAs
+// rather than hiding behind them; a fifth stage measured no faster.
 //
 // Tails: rows / columns past the matrix are read from a clamped in-range
 // address (their outputs are never stored); on the K-tail path, k-chunks
@@ -130,15 +137,28 @@ __device__ __forceinline__ void tile_order(int64_t bid, int64_t tiles_m, int64_t
 // descriptor base (checked at launch); the K-tail path then never runs.
 template <bool B_KC, bool DUAL, bool GROUP, bool BUF>
 __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs ga) {
-  __shared__ __attribute__((aligned(1024))) uint8_t s0[STAGE];
-  __shared__ __attribute__((aligned(1024))) uint8_t s1[STAGE];
-  __shared__ __attribute__((aligned(1024))) uint8_t s2[STAGE];
-  __shared__ __attribute__((aligned(1024))) uint8_t s3[STAGE];
-  __shared__ __attribute__((aligned(1024))) uint8_t s4[NS > 4 ? STAGE : 16];
-  // Each stage is its own __shared__ array so the compiler sees that a DMA
-  // into one stage cannot alias fragment reads of another.
-  auto S = [&](int i) -> uint8_t* {
-    return i == 0 ? s0 : i == 1 ? s1 : i == 2 ? s2 : i == 3 ? s3 : s4;
+  // LDS, 128 KiB.  K-tail path: four 32 KiB stages, each the A and B halves
+  // of one k-tile.  BUF path: two 32 KiB A stages, each a k-tile pair (256
+  // rows x 128 bytes, so every A row of a pair is one whole cache line), and
+  // four 16 KiB B stages.  Each region is its own __shared__ array so the
+  // compiler sees that a DMA into one cannot alias fragment reads of another.
+  __shared__ __attribute__((aligned(1024))) uint8_t L0[STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t L1[STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t L2[BUF ? B_BYTES : STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t L3[BUF ? B_BYTES : STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t L4[BUF ? B_BYTES : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t L5[BUF ? B_BYTES : 16];
+  auto S = [&](int i) -> uint8_t* {  // K-tail stage i
+    return i == 0 ? L0 : i == 1 ? L1 : i == 2 ? L2 : L3;
+  };
+  auto AS = [&](int p) -> uint8_t* { return p ? L1 : L0; };  // BUF A pair stage
+  auto BS = [&](int i) -> uint8_t* {                          // BUF B stage
+    return i == 0 ? L2 : i == 1 ? L3 : i == 2 ? L4 : L5;
+  };
+  // 16 KiB block blk (rows 32 blk .. 32 blk + 31) of the epilogue's C tile
+  auto CB = [&](int blk) -> uint8_t* {
+    if constexpr (BUF) return blk < 4 ? AS(blk >> 1) + (blk & 1) * B_BYTES : BS(blk - 4);
+    else return S(blk >> 1) + (blk & 1) * B_BYTES;
   };
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -240,6 +260,42 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
     }
   }
 
+  // BUF: A moves a k-tile pair at a time, 8 instructions per wave; lane l of
+  // instruction q of wave w covers row r = 8 (8 w + q) + l / 8, physical
+  // 16-byte chunk l % 8, which holds logical chunk (l % 8) ^ ((r >> 1) & 7)
+  // (chunks 0-3 the first k-tile of the pair, 4-7 the second).  The 16 lanes
+  // a ds_read_b128 serves per cycle read one logical chunk of 16 rows;
+  // rows r and r + 1 fall in different halves of a 256-byte bank window and
+  // the XOR spreads the 8 even (odd) rows over 8 distinct chunks.
+  uint32_t vap[8];
+  if constexpr (BUF) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int r = 8 * (8 * wave + q) + (lane >> 3);
+      const int c = (lane & 7) ^ ((r >> 1) & 7);
+      const int rr = r < m_rows ? r : (int)m_rows - 1;
+      int64_t arow;
+      if constexpr (GROUP)
+        arow = ga.rows ? (int64_t)ga.rows[row0 + rr] : row0 + rr;
+      else
+        arow = row0 + rr;
+      vap[q] = (uint32_t)((arow * g.a_sm + c * 8) * 2);
+    }
+  }
+  // BUF: the B half of k-tile k0 / BK into B stage bst
+  auto issue_b = [&](uint8_t* bst, int k0) {
+    uint8_t* sb = bst + wave * 4096;
+    const uint32_t sob = B_KC ? (uint32_t)k0 * 2 : (uint32_t)(k0 * g.b_sk * 2);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) buf_to_lds16(rb, vb[q], sob, sb + q * 1024);
+  };
+  // BUF: A of the k-tile pair starting at k0 into A stage ast
+  auto issue_a = [&](uint8_t* ast, int k0) {
+    uint8_t* sa = ast + wave * 8192;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) buf_to_lds16(ra, vap[q], (uint32_t)k0 * 2, sa + q * 1024);
+  };
+
   // One k-tile of DMA loads.  Branch-free (it is interleaved with MFMAs).
   // K-tail path: lanes whose chunk lies past K fetch an in-range chunk of
   // the same row instead (a select, not a branch), and clear_tail zeroes
@@ -289,24 +345,29 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
   // ---- per-lane fragment offsets (bytes within a stage) ---------------------------
   // A: rows wm*128 + i*32 + (lane & 31), k-chunk 2 s + (lane >> 5)
   const int a_row = wm * 128 + (lane & 31);
-  int a_off[2];
+  int a_off[2];      // K-tail stages: per substep
+  int ap_off[2][2];  // BUF pair stages: [k-tile of the pair][substep]
 #pragma unroll
-  for (int s = 0; s < 2; ++s)
+  for (int s = 0; s < 2; ++s) {
     a_off[s] = a_row * 64 + (((2 * s + (lane >> 5)) ^ ((a_row >> 2) & 3)) * 16);
-  int b_off[4];   // per fragment column block j (substep s adds s * 8192)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      ap_off[h][s] = a_row * 128 + (((4 * h + 2 * s + (lane >> 5)) ^ ((a_row >> 1) & 7)) * 16);
+  }
+  int b_off[4];   // per fragment column block j (substep s adds s * 8192), from the B half
   int bk_off[2];  // B_KC: per substep
   if constexpr (B_KC) {
     const int b_row = wn * 128 + (lane & 31);
 #pragma unroll
     for (int s = 0; s < 2; ++s)
-      bk_off[s] = A_BYTES + b_row * 64 + (((2 * s + (lane >> 5)) ^ ((b_row >> 2) & 3)) * 16);
+      bk_off[s] = b_row * 64 + (((2 * s + (lane >> 5)) ^ ((b_row >> 2) & 3)) * 16);
   } else {
     const int grp16 = lane >> 4, s16 = lane & 15;
     const int kr = 8 * (grp16 >> 1) + (s16 >> 2);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int col = wn * 128 + j * 32 + 16 * (grp16 & 1) + 4 * (s16 & 3);
-      b_off[j] = A_BYTES + kr * 512 + ((((col >> 3) ^ (4 * (kr & 3)))) * 16) + (col & 7) * 2;
+      b_off[j] = kr * 512 + ((((col >> 3) ^ (4 * (kr & 3)))) * 16) + (col & 7) * 2;
     }
   }
 
@@ -319,17 +380,20 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
   bf16x8_t fa[2][4], fb[2][4];
-  auto read_frags = [&](const uint8_t* base, int s, int slot) {
+  // fragments of one substep: A rows from abase (a row stride of `ast`
+  // bytes per 32-row block), B from bbase (the B half of a stage)
+  constexpr int AST = BUF ? 32 * 128 : 32 * 64;
+  auto read_frags = [&](const uint8_t* abase, int aoff, const uint8_t* bbase, int s, int slot) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fa[slot][i] = *(const bf16x8_t*)(base + a_off[s] + i * 32 * 64);
+    for (int i = 0; i < 4; ++i) fa[slot][i] = *(const bf16x8_t*)(abase + aoff + i * AST);
     if constexpr (B_KC) {
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        fb[slot][j] = *(const bf16x8_t*)(base + bk_off[s] + j * 32 * 64);
+        fb[slot][j] = *(const bf16x8_t*)(bbase + bk_off[s] + j * 32 * 64);
     } else {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint8_t* p = base + b_off[j] + s * 16 * 512;
+        const uint8_t* p = bbase + b_off[j] + s * 16 * 512;
         const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)p);
         const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(p + 4 * 512));
         v4s both[2] = {lo, hi};
@@ -353,17 +417,17 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
   };
 
   // ---- main loop -------------------------------------------------------------------
-  // k-step kt over stage `cur` (its substep-0 fragments already in slot 0;
-  // the DMA of tiles kt + 1 .. kt + NS - 1 in flight):
+  // k-step kt (its substep-0 fragments already in slot 0; the DMA of the
+  // next tiles in flight):
   //   substep 0: 16 MFMAs interleaved one-for-one with the 12 fragment
   //     reads of substep 1;
-  //   wait until this wave's DMA of tile kt + 1 has landed (the NS - 2 later
-  //     tiles stay in flight) and the substep-1 fragments are in, barrier:
-  //     every wave is done reading `cur`, tile kt + 1 is complete in `nxt`;
-  //   substep 1: 16 MFMAs overlap the reads of `nxt`'s first fragments and
-  //     the 8 DMA loads of tile kt + NS into the now free `cur`.
-  // Past the last tile the DMA re-reads tile kt (an L2 hit; kept
-  // branch-free so it can interleave); the final wait drains it.
+  //   wait until this wave's DMA of tile kt + 1 has landed (later tiles
+  //     stay in flight) and the substep-1 fragments are in, barrier: every
+  //     wave is done reading tile kt, tile kt + 1 is complete;
+  //   substep 1: 16 MFMAs overlap the reads of tile kt + 1's first
+  //     fragments and the DMA into the stages tile kt freed.
+  // Past the last tile the DMA re-reads data already resident (an L2 hit;
+  // kept branch-free so it can interleave); the final wait drains it.
   auto pin_reads = [&]() {
 #pragma unroll
     for (int x = 0; x < 12; ++x) {
@@ -372,48 +436,96 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
   };
-  auto pin_last = [&]() {
+  auto pin_last = [&](int nvm) {
 #pragma unroll
     for (int x = 0; x < 16; ++x) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
       if (x < 12) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-      if (x < 8) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // VMEM (DMA)
+      if (x < nvm) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM (DMA)
     }
   };
+  // K-tail path: stage kt % NS holds A and B of tile kt; tile kt + NS goes
+  // into it once it is free (8 DMA instructions per wave and step).
   auto k_step = [&](uint8_t* cur, uint8_t* nxt, int kt) {
-    read_frags(cur, 1, 1);
+    read_frags(cur, a_off[1], cur + A_BYTES, 1, 1);
     mfmas(0);
     pin_reads();
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(waitcnt_imm((NS - 2) * DMA_PER_TILE, 0));
-    if (!BUF && kt + 2 == nk && K % BK) clear_tail(nxt, (kt + 1) * BK);
+    if (kt + 2 == nk && K % BK) clear_tail(nxt, (kt + 1) * BK);
     block_barrier();
     // (after the last k-step these reads are dead; keeping them
     // unconditional avoids a branch that costs registers)
-    read_frags(nxt, 0, 0);
+    read_frags(nxt, a_off[0], nxt + A_BYTES, 0, 0);
     issue(cur, (kt + NS < nk ? kt + NS : kt) * BK);
     mfmas(1);
-    pin_last();
+    pin_last(8);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // BUF path, step kt = 4 t + j: B of tile kt in B stage j, A in pair stage
+  // (j >> 1) & 1 (k-tile j & 1 of the pair).  Every step refills the freed
+  // B stage with tile kt + 4 (4 DMA instructions per wave); odd steps, which
+  // free a pair stage, refill it with the pair (kt + 3, kt + 4) (8 more).
+  // Counting back from the wait of step kt, the instructions issued after
+  // the last load tile kt + 1 needs are: even kt, 16 (B of kt + 2, B of
+  // kt + 3 and the pair (kt + 2, kt + 3)); odd kt, 4 (B of kt + 3).
+  auto k_step2 = [&](int j, int kt) {
+    const int jn = (j + 1) & 3;
+    uint8_t* acur = AS((j >> 1) & 1);
+    uint8_t* anxt = AS((jn >> 1) & 1);
+    read_frags(acur, ap_off[j & 1][1], BS(j), 1, 1);
+    mfmas(0);
+    pin_reads();
+    __builtin_amdgcn_sched_barrier(0);
+    if (j & 1) __builtin_amdgcn_s_waitcnt(waitcnt_imm(4, 0));
+    else __builtin_amdgcn_s_waitcnt(waitcnt_imm(16, 0));
+    block_barrier();
+    read_frags(anxt, ap_off[jn & 1][0], BS(jn), 0, 0);
+    issue_b(BS(j), (kt + NS < nk ? kt + NS : kt) * BK);
+    if (j & 1) issue_a(acur, (kt + 3 < nk ? kt + 3 : kt - 1) * BK);
+    mfmas(1);
+    pin_last(j & 1 ? 12 : 4);
     __builtin_amdgcn_sched_barrier(0);
   };
 
-#pragma unroll
-  for (int t = 0; t < NS; ++t) issue(S(t), (t < nk ? t : 0) * BK);
-  __builtin_amdgcn_s_waitcnt(waitcnt_imm((NS - 1) * DMA_PER_TILE, 15));
-  if (!BUF && nk == 1 && K % BK) clear_tail(s0, 0);
-  block_barrier();
-  read_frags(s0, 0, 0);
-  // Whole turns of the ring, then the remaining (< NS) steps: no path
-  // re-enters the loop with a DMA into the stage it reads first still in
-  // flight, so the compiler adds no wait for one.
   int kt = 0;
-  for (; kt + NS <= nk; kt += NS) {
+  if constexpr (BUF) {
+    // the issue order of the (virtual) steps -4 .. -1
+    issue_b(BS(0), 0);
+    issue_b(BS(1), (1 < nk ? 1 : 0) * BK);
+    issue_a(AS(0), 0);
+    issue_b(BS(2), (2 < nk ? 2 : 0) * BK);
+    issue_b(BS(3), (3 < nk ? 3 : 0) * BK);
+    issue_a(AS(1), (2 < nk ? 2 : 0) * BK);
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(16, 15));
+    block_barrier();
+    read_frags(AS(0), ap_off[0][0], BS(0), 0, 0);
+    // Whole turns of the ring, then the remaining steps (nk is even): no
+    // path re-enters the loop with a DMA into a stage it reads first still
+    // in flight, so the compiler adds no wait for one.
+    for (; kt + NS <= nk; kt += NS) {
 #pragma unroll
-    for (int j = 0; j < NS; ++j) k_step(S(j), S((j + 1) % NS), kt + j);
+      for (int j = 0; j < NS; ++j) k_step2(j, kt + j);
+    }
+    if (kt < nk) {
+      k_step2(0, kt);
+      k_step2(1, kt + 1);
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < NS; ++t) issue(S(t), (t < nk ? t : 0) * BK);
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm((NS - 1) * DMA_PER_TILE, 15));
+    if (nk == 1 && K % BK) clear_tail(L0, 0);
+    block_barrier();
+    read_frags(L0, a_off[0], L0 + A_BYTES, 0, 0);
+    for (; kt + NS <= nk; kt += NS) {
+#pragma unroll
+      for (int j = 0; j < NS; ++j) k_step(S(j), S((j + 1) % NS), kt + j);
+    }
+#pragma unroll
+    for (int j = 0; j < NS - 1; ++j)
+      if (kt + j < nk) k_step(S(j), S(j + 1), kt + j);
   }
-#pragma unroll
-  for (int j = 0; j < NS - 1; ++j)
-    if (kt + j < nk) k_step(S(j), S(j + 1), kt + j);
   // the dummy DMAs (into the stages past the last tile) must land before
   // the epilogue reuses the LDS
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
@@ -421,20 +533,18 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
 
   // ---- epilogue ----------------------------------------------------------------------
   // phase 1: bf16(acc) into the C tile in LDS (the ring is free now): rows
-  // 64 p .. 64 p + 63 in stage p, 512-byte rows, 16-byte chunk ch of row r
-  // stored at ch ^ (r & 15).  For block (i, j) and column group q = e / 4
+  // 32 b .. 32 b + 31 in 16 KiB block b, 512-byte rows, 16-byte chunk ch of
+  // row r stored at ch ^ (r & 15).  For block (i, j) and column group q = e / 4
   // a lane holds 4 consecutive columns of one row: one ds_write_b64, and
   // the 32 rows of a write spread over 16 chunk positions (2-way at most).
   auto pack4 = [](const float* v) {
     return make_uint2(vm::bf16x2_bits(v[0], v[1]), vm::bf16x2_bits(v[2], v[3]));
   };
   {
-    uint8_t* cb0 = S(2 * wm);      // rows wm * 128 + [0, 64)
-    uint8_t* cb1 = S(2 * wm + 1);  // rows wm * 128 + [64, 128)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      uint8_t* cb = i < 2 ? cb0 : cb1;
-      const int lr = (i & 1) * 32 + (lane & 31);
+      uint8_t* cb = CB(wm * 4 + i);  // rows wm * 128 + 32 i + [0, 32)
+      const int lr = lane & 31;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -476,8 +586,8 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
   // batch requested before this batch's stores: the wait for a batch then
   // never includes stores (vmcnt counts both, in issue order).
   auto c_chunk = [&](int row, int col) -> uint4 {
-    const int lr = row & 63;
-    return *(const uint4*)(S(row >> 6) + lr * 512 + ((((col >> 3) ^ (lr & 15))) * 16));
+    const int lr = row & 31;
+    return *(const uint4*)(CB(row >> 5) + lr * 512 + ((((col >> 3) ^ (lr & 15))) * 16));
   };
   auto bf = [](uint16_t h) { return vm::as_f((uint32_t)h << 16); };
   uint16_t* C = (uint16_t*)g.c + b * g.c_sb;
@@ -685,11 +795,12 @@ bool gemm_lds_ok(const GemmArgs& g, bool* b_kc) {
   return true;
 }
 
-// Whether the buffer-descriptor DMA path can run g: K a multiple of BK and
-// every byte offset the kernel forms (row offset + k advance) below 2^31.
+// Whether the buffer-descriptor DMA path can run g: K a multiple of 2 BK
+// (A moves in k-tile pairs) and every byte offset the kernel forms (row
+// offset + k advance) below 2^31.
 static bool buf_ok(const GemmArgs& g, const GroupArgs* ga, bool bkc, bool dual) {
   constexpr int64_t kLim = (int64_t)1 << 31;
-  if (g.K % BK) return false;
+  if (g.K % (2 * BK)) return false;
   const int64_t a_span = ((g.M - 1) * g.a_sm + g.K) * 2;
   int64_t b_span = bkc ? ((g.N - 1) * g.b_sn + g.K) * 2 : ((g.K - 1) * g.b_sk + g.N) * 2;
   if (dual) {
