@@ -289,11 +289,13 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
 #pragma unroll
     for (int q = 0; q < 4; ++q) buf_to_lds16(rb, vb[q], sob, sb + q * 1024);
   };
-  // BUF: A of the k-tile pair starting at k0 into A stage ast
-  auto issue_a = [&](uint8_t* ast, int k0) {
+  // BUF: half `half` (rows 128 half .. + 127) of A of the k-tile pair
+  // starting at k0, into A stage ast
+  auto issue_a = [&](uint8_t* ast, int k0, int half) {
     uint8_t* sa = ast + wave * 8192;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) buf_to_lds16(ra, vap[q], (uint32_t)k0 * 2, sa + q * 1024);
+    for (int q = 4 * half; q < 4 * half + 4; ++q)
+      buf_to_lds16(ra, vap[q], (uint32_t)k0 * 2, sa + q * 1024);
   };
 
   // One k-tile of DMA loads.  Branch-free (it is interleaved with MFMAs).
@@ -436,6 +438,15 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
   };
+  auto pin_reads4 = [&]() {
+#pragma unroll
+    for (int x = 0; x < 12; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      if (x < 4) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+  };
   auto pin_last = [&](int nvm) {
 #pragma unroll
     for (int x = 0; x < 16; ++x) {
@@ -464,40 +475,52 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
   };
   // BUF path, step kt = 4 t + j: B of tile kt in B stage j, A in pair stage
   // (j >> 1) & 1 (k-tile j & 1 of the pair).  Every step refills the freed
-  // B stage with tile kt + 4 (4 DMA instructions per wave); odd steps, which
-  // free a pair stage, refill it with the pair (kt + 3, kt + 4) (8 more).
+  // B stage with tile kt + 4 (4 DMA instructions per wave, substep 1); odd
+  // steps, which free a pair stage, request the first half (rows 0-127) of
+  // the pair (kt + 3, kt + 4) in substep 1, and the next (even) step its
+  // second half in substep 0: 8 DMA instructions every step rather than
+  // bursts of 12 and 4, which the memory pipeline absorbs better.
   // Counting back from the wait of step kt, the instructions issued after
   // the last load tile kt + 1 needs are: even kt, 16 (B of kt + 2, B of
-  // kt + 3 and the pair (kt + 2, kt + 3)); odd kt, 4 (B of kt + 3).
+  // kt + 3, both halves of the pair (kt + 2, kt + 3)); odd kt, 4 (B of
+  // kt + 3).
   auto k_step2 = [&](int j, int kt) {
     const int jn = (j + 1) & 3;
     uint8_t* acur = AS((j >> 1) & 1);
     uint8_t* anxt = AS((jn >> 1) & 1);
     read_frags(acur, ap_off[j & 1][1], BS(j), 1, 1);
+    // even step: second half of the pair requested in the previous step
+    // (the same k as that step chose: its spare reload past the last tile)
+    if (!(j & 1)) {
+      const int kp = kt + 2 < nk ? kt + 2 : (kt >= 2 ? kt - 2 : 0);
+      issue_a(AS(((j + 3) >> 1) & 1), kp * BK, 1);
+    }
     mfmas(0);
-    pin_reads();
+    if (j & 1) pin_reads(); else pin_reads4();
     __builtin_amdgcn_sched_barrier(0);
     if (j & 1) __builtin_amdgcn_s_waitcnt(waitcnt_imm(4, 0));
     else __builtin_amdgcn_s_waitcnt(waitcnt_imm(16, 0));
     block_barrier();
     read_frags(anxt, ap_off[jn & 1][0], BS(jn), 0, 0);
     issue_b(BS(j), (kt + NS < nk ? kt + NS : kt) * BK);
-    if (j & 1) issue_a(acur, (kt + 3 < nk ? kt + 3 : kt - 1) * BK);
+    if (j & 1) issue_a(acur, (kt + 3 < nk ? kt + 3 : kt - 1) * BK, 0);
     mfmas(1);
-    pin_last(j & 1 ? 12 : 4);
+    pin_last(8);
     __builtin_amdgcn_sched_barrier(0);
   };
 
   int kt = 0;
   if constexpr (BUF) {
-    // the issue order of the (virtual) steps -4 .. -1
+    // the issue order of the (virtual) steps -4 .. -1 (step 0 requests the
+    // second half of the pair (2, 3))
     issue_b(BS(0), 0);
     issue_b(BS(1), (1 < nk ? 1 : 0) * BK);
-    issue_a(AS(0), 0);
+    issue_a(AS(0), 0, 0);
+    issue_a(AS(0), 0, 1);
     issue_b(BS(2), (2 < nk ? 2 : 0) * BK);
     issue_b(BS(3), (3 < nk ? 3 : 0) * BK);
-    issue_a(AS(1), (2 < nk ? 2 : 0) * BK);
-    __builtin_amdgcn_s_waitcnt(waitcnt_imm(16, 15));
+    issue_a(AS(1), (2 < nk ? 2 : 0) * BK, 0);
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(12, 15));
     block_barrier();
     read_frags(AS(0), ap_off[0][0], BS(0), 0, 0);
     // Whole turns of the ring, then the remaining steps (nk is even): no
@@ -653,7 +676,8 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
     uint4 ra[U], rb[U];
     auto fetch = [&](int p0, uint4* dst) {
 #pragma unroll
-      for (int u = 0; u < U; ++u) dst[u] = *(const uint4*)(res + crow(row_of(p0 + u)) * res_sm + nc);
+      for (int u = 0; u < U; ++u)
+        dst[u] = *(const uint4*)(res + crow(row_of(p0 + u)) * res_sm + nc);
     };
     auto apply = [&](int p0, const uint4* rv) {
 #pragma unroll
