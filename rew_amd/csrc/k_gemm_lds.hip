@@ -282,10 +282,14 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
       vap[q] = (uint32_t)((arow * g.a_sm + c * 8) * 2);
     }
   }
+  // B's k-row stride in bytes, held in an SGPR for the whole loop (left to
+  // itself the compiler re-read it from the kernel arguments every other
+  // k-step and waited on that scalar load right after the barrier)
+  const uint32_t b_kbytes = __builtin_amdgcn_readfirstlane((uint32_t)(B_KC ? 2 : g.b_sk * 2));
   // BUF: the B half of k-tile k0 / BK into B stage bst
   auto issue_b = [&](uint8_t* bst, int k0) {
     uint8_t* sb = bst + wave * 4096;
-    const uint32_t sob = B_KC ? (uint32_t)k0 * 2 : (uint32_t)(k0 * g.b_sk * 2);
+    const uint32_t sob = (uint32_t)k0 * b_kbytes;
 #pragma unroll
     for (int q = 0; q < 4; ++q) buf_to_lds16(rb, vb[q], sob, sb + q * 1024);
   };
