@@ -59,6 +59,9 @@ SHAPES = [  # M, K, N, B given transposed
     (40, 136, 1032, 0),
     (300, 1000, 520, 1),   # K tail (1000 % 64) with B K-contiguous
     (513, 4104, 1024, 0),  # K tail, M tail, several k-tiles
+    (333, 192, 264, 0),    # K % 64 == 0 with 6 k-tiles: a ring turn plus a two-step remainder
+    (200, 320, 512, 1),    # the same with B K-contiguous, 10 k-tiles
+    (64, 128, 64, 0),      # exactly one ring turn, M and N far below a tile
 ]
 
 
