@@ -31,11 +31,16 @@
 //     4 chunks of one read over all bank groups.
 // The k-tiles stream through a ring: four B stages (16 KiB) and two A pair
 // stages (32 KiB) on the buffer path, four 32 KiB A+B stages on the K-tail
-// path.  B of tile t + 4 is requested right after the barrier that frees
-// tile t's stage and first read three k-steps later; an A pair two k-steps
-// before its first read.  On the Llama shapes a k-step of MFMAs alone takes
-// 1024 cycles and the full loop about 1230: the DMA overlaps the MFMAs
-// rather than hiding behind them; a fifth stage measured no faster.
+// path.  B of tile t + 4 is requested after the barrier that frees tile
+// t's stage (right after it for even t, two k-steps later for odd t); an A
+// pair two k-steps before its first read.  Every 16-MFMA substep issues
+// exactly 4 DMA instructions per wave, one after every fourth MFMA: the
+// issue is in order, so a DMA instruction that finds the address unit's
+// queue full also holds back the MFMAs behind it, and bursts (8 after
+// eight consecutive MFMAs, with none in the other substep) measured 2-4 %
+// slower per GEMM.  On the Llama shapes a k-step of MFMAs alone takes 1024
+// cycles and the full loop about 1230: the DMA overlaps the MFMAs rather
+// than hiding behind them; a fifth stage measured no faster.
 //
 // Tails: rows / columns past the matrix are read from a clamped in-range
 // address (their outputs are never stored); on the K-tail path, k-chunks
@@ -442,21 +447,22 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
   };
+  // substep 0 with 4 DMA instructions, one after every fourth MFMA
   auto pin_reads4 = [&]() {
 #pragma unroll
-    for (int x = 0; x < 12; ++x) {
+    for (int x = 0; x < 16; ++x) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-      if (x < 4) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM
+      if (x < 12) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      if ((x & 3) == 0) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
   };
+  // substep 1 with nvm (4 or 8) DMA instructions, evenly spaced
   auto pin_last = [&](int nvm) {
 #pragma unroll
     for (int x = 0; x < 16; ++x) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
       if (x < 12) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-      if (x < nvm) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM (DMA)
+      if (x % (16 / nvm) == 0) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM (DMA)
     }
   };
   // K-tail path: stage kt % NS holds A and B of tile kt; tile kt + NS goes
@@ -478,51 +484,54 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
     __builtin_amdgcn_sched_barrier(0);
   };
   // BUF path, step kt = 4 t + j: B of tile kt in B stage j, A in pair stage
-  // (j >> 1) & 1 (k-tile j & 1 of the pair).  Every step refills the freed
-  // B stage with tile kt + 4 (4 DMA instructions per wave, substep 1); odd
-  // steps, which free a pair stage, request the first half (rows 0-127) of
-  // the pair (kt + 3, kt + 4) in substep 1, and the next (even) step its
-  // second half in substep 0: 8 DMA instructions every step rather than
-  // bursts of 12 and 4, which the memory pipeline absorbs better.
+  // (j >> 1) & 1 (k-tile j & 1 of the pair).  Four DMA instructions per
+  // substep, each a quarter of a pair (the first half, rows 0-127, or the
+  // second) or one B tile:
+  //   even kt: substep 0, the second half of the pair (kt + 2, kt + 3);
+  //            substep 1, B of kt + 4 into the stage kt freed;
+  //   odd kt:  substep 0, B of kt + 2 into the stage kt - 2 freed;
+  //            substep 1, the first half of the pair (kt + 3, kt + 4) into
+  //            the pair stage kt freed.
   // Counting back from the wait of step kt, the instructions issued after
-  // the last load tile kt + 1 needs are: even kt, 16 (B of kt + 2, B of
-  // kt + 3, both halves of the pair (kt + 2, kt + 3)); odd kt, 4 (B of
-  // kt + 3).
+  // the last load tile kt + 1 needs are 8 either way: even kt, the two
+  // halves of the pair (kt + 2, kt + 3) after B of kt + 1; odd kt, B of
+  // kt + 3 and B of kt + 2 after the second half of the pair (kt + 1,
+  // kt + 2).
   auto k_step2 = [&](int j, int kt) {
     const int jn = (j + 1) & 3;
     uint8_t* acur = AS((j >> 1) & 1);
     uint8_t* anxt = AS((jn >> 1) & 1);
     read_frags(acur, ap_off[j & 1][1], BS(j), 1, 1);
-    // even step: second half of the pair requested in the previous step
-    // (the same k as that step chose: its spare reload past the last tile)
     if (!(j & 1)) {
+      // (past the last pair: the same k as the previous step chose for the
+      // first half, its spare reload)
       const int kp = kt + 2 < nk ? kt + 2 : (kt >= 2 ? kt - 2 : 0);
       issue_a(AS(((j + 3) >> 1) & 1), kp * BK, 1);
+    } else {
+      issue_b(BS((j + 2) & 3), (kt + 2 < nk ? kt + 2 : kt) * BK);
     }
     mfmas(0);
-    if (j & 1) pin_reads(); else pin_reads4();
+    pin_reads4();
     __builtin_amdgcn_sched_barrier(0);
-    if (j & 1) __builtin_amdgcn_s_waitcnt(waitcnt_imm(4, 0));
-    else __builtin_amdgcn_s_waitcnt(waitcnt_imm(16, 0));
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(8, 0));
     block_barrier();
     read_frags(anxt, ap_off[jn & 1][0], BS(jn), 0, 0);
-    issue_b(BS(j), (kt + NS < nk ? kt + NS : kt) * BK);
     if (j & 1) issue_a(acur, (kt + 3 < nk ? kt + 3 : kt - 1) * BK, 0);
+    else issue_b(BS(j), (kt + NS < nk ? kt + NS : kt) * BK);
     mfmas(1);
-    pin_last(8);
+    pin_last(4);
     __builtin_amdgcn_sched_barrier(0);
   };
 
   int kt = 0;
   if constexpr (BUF) {
     // the issue order of the (virtual) steps -4 .. -1 (step 0 requests the
-    // second half of the pair (2, 3))
+    // second half of the pair (2, 3), step 1 B of tile 3)
     issue_b(BS(0), 0);
-    issue_b(BS(1), (1 < nk ? 1 : 0) * BK);
     issue_a(AS(0), 0, 0);
     issue_a(AS(0), 0, 1);
     issue_b(BS(2), (2 < nk ? 2 : 0) * BK);
-    issue_b(BS(3), (3 < nk ? 3 : 0) * BK);
+    issue_b(BS(1), (1 < nk ? 1 : 0) * BK);
     issue_a(AS(1), (2 < nk ? 2 : 0) * BK, 0);
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(12, 15));
     block_barrier();
