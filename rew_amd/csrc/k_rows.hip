@@ -83,6 +83,59 @@ __global__ void __launch_bounds__(256) rmsnorm_rows_kernel(RowNormArgs a) {
 // (8 bf16 or 4 f32 per load), CH chunks per lane; a wave-only reduction; the
 // same op order as rmsnorm_rows_kernel (square, sum, / n, + eps, sqrt,
 // x / r, gamma * .).
+//
+// rms_row: that arithmetic for one row whose chunks are in raw (chunk k of
+// lane l holds elements (64 k + l) EPC_X ..); gam(k, e) is gamma of element
+// e of chunk k.  FULL: every chunk is in range (n == 64 CH EPC_X).
+template <int XB, int YB, int CH, bool FULL, typename Gamma>
+__device__ __forceinline__ void rms_row(const RowNormArgs& a, int64_t row, int lane,
+                                        const uint4 (&raw)[CH], Gamma gam) {
+  constexpr int EPC_X = 16 / XB;
+  float ss = 0.0f;
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const uint32_t* w = (const uint32_t*)&raw[k];
+#pragma unroll
+    for (int e = 0; e < EPC_X; ++e) {
+      const float v = XB == 2 ? as_f((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16))
+                              : as_f(w[e]);
+      const float sq = v * v;
+      ss += sq;
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+  const float mean = ss / a.divisor;
+  const float r = sqrtf(mean + a.eps);
+  char* y = (char*)a.y + row * a.n * YB;
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const int64_t j = ((int64_t)k * 64 + lane) * EPC_X;
+    if (!FULL && j >= a.n) continue;
+    const uint32_t* w = (const uint32_t*)&raw[k];
+    float out[EPC_X];
+#pragma unroll
+    for (int e = 0; e < EPC_X; ++e) {
+      const float v = XB == 2 ? as_f((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16))
+                              : as_f(w[e]);
+      const float nv = v / r;
+      out[e] = gam(k, e) * nv;
+    }
+    if (YB == 2) {
+      uint32_t o[EPC_X / 2];
+#pragma unroll
+      for (int e = 0; e < EPC_X; e += 2)
+        o[e / 2] = (uint32_t)bf16_bits(out[e]) | ((uint32_t)bf16_bits(out[e + 1]) << 16);
+      if (EPC_X == 8) *(uint4*)(y + j * 2) = *(const uint4*)o;
+      else *(uint2*)(y + j * 2) = *(const uint2*)o;
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPC_X; e += 4)
+        *(float4*)(y + (j + e) * 4) = make_float4(out[e], out[e + 1], out[e + 2], out[e + 3]);
+    }
+  }
+}
+
 template <int XB, int YB, int CH>  // element bytes of x and y; 16-byte chunks per lane
 __global__ void __launch_bounds__(256) rmsnorm_wave_kernel(RowNormArgs a) {
   constexpr int EPC_X = 16 / XB;          // elements per x chunk
@@ -96,49 +149,57 @@ __global__ void __launch_bounds__(256) rmsnorm_wave_kernel(RowNormArgs a) {
       const int64_t j = ((int64_t)k * 64 + lane) * EPC_X;
       raw[k] = j < a.n ? *(const uint4*)(x + j * XB) : make_uint4(0, 0, 0, 0);
     }
-    float ss = 0.0f;
+    rms_row<XB, YB, CH, false>(a, row, lane, raw, [&](int k, int e) {
+      return a.gamma[((int64_t)k * 64 + lane) * EPC_X + e];
+    });
+  }
+}
+
+// Rows of exactly 64 CH EPC_X elements (every chunk in range, no guards):
+// each wave walks rows / (4 gridDim) rows, holds gamma in registers for all
+// of them (read once per wave, not once per row), and loads its next row
+// before the arithmetic of the current one, the rows alternating between two
+// register buffers.  The next row's loads are unconditional (past the last
+// row the wave re-reads the row it just read): loads under a branch would
+// make the compiler wait for every load in flight at the merge.
+template <int XB, int YB, int CH>
+__global__ void __launch_bounds__(256) rmsnorm_pipe_kernel(RowNormArgs a) {
+  constexpr int EPC_X = 16 / XB;
+  const int lane = threadIdx.x & 63;
+  const int64_t waves = (int64_t)gridDim.x * 4;
+  int64_t row = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4 + (threadIdx.x >> 6)));
+  if (row >= a.rows) return;
+  float g[CH][EPC_X];
 #pragma unroll
-    for (int k = 0; k < CH; ++k) {
-      const uint32_t* w = (const uint32_t*)&raw[k];
+  for (int k = 0; k < CH; ++k)
 #pragma unroll
-      for (int e = 0; e < EPC_X; ++e) {
-        const float v = XB == 2 ? as_f((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16))
-                                : as_f(w[e]);
-        const float sq = v * v;
-        ss += sq;
-      }
+    for (int e = 0; e < EPC_X; e += 4) {
+      const float4 t = *(const float4*)(a.gamma + ((int64_t)k * 64 + lane) * EPC_X + e);
+      g[k][e] = t.x;
+      g[k][e + 1] = t.y;
+      g[k][e + 2] = t.z;
+      g[k][e + 3] = t.w;
     }
+  auto load = [&](int64_t r, uint4 (&raw)[CH]) {
+    const char* x = (const char*)a.x + r * a.x_rs * XB;
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
-    const float mean = ss / a.divisor;
-    const float r = sqrtf(mean + a.eps);
-    char* y = (char*)a.y + row * a.n * YB;
-#pragma unroll
-    for (int k = 0; k < CH; ++k) {
-      const int64_t j = ((int64_t)k * 64 + lane) * EPC_X;
-      if (j >= a.n) continue;
-      const uint32_t* w = (const uint32_t*)&raw[k];
-      float out[EPC_X];
-#pragma unroll
-      for (int e = 0; e < EPC_X; ++e) {
-        const float v = XB == 2 ? as_f((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16))
-                                : as_f(w[e]);
-        const float nv = v / r;
-        out[e] = a.gamma[j + e] * nv;
-      }
-      if (YB == 2) {
-        uint32_t o[EPC_X / 2];
-#pragma unroll
-        for (int e = 0; e < EPC_X; e += 2)
-          o[e / 2] = (uint32_t)bf16_bits(out[e]) | ((uint32_t)bf16_bits(out[e + 1]) << 16);
-        if (EPC_X == 8) *(uint4*)(y + j * 2) = *(const uint4*)o;
-        else *(uint2*)(y + j * 2) = *(const uint2*)o;
-      } else {
-#pragma unroll
-        for (int e = 0; e < EPC_X; e += 4)
-          *(float4*)(y + (j + e) * 4) = make_float4(out[e], out[e + 1], out[e + 2], out[e + 3]);
-      }
-    }
+    for (int k = 0; k < CH; ++k) raw[k] = *(const uint4*)(x + ((int64_t)k * 64 + lane) * 16);
+  };
+  auto gam = [&](int k, int e) { return g[k][e]; };
+  uint4 ra[CH], rb[CH];
+  load(row, ra);
+  for (;;) {
+    const int64_t r1 = row + waves;
+    load(r1 < a.rows ? r1 : row, rb);
+    __builtin_amdgcn_sched_barrier(0);  // (issued before this row's work)
+    rms_row<XB, YB, CH, true>(a, row, lane, ra, gam);
+    if (r1 >= a.rows) break;
+    const int64_t r2 = r1 + waves;
+    load(r2 < a.rows ? r2 : r1, ra);
+    __builtin_amdgcn_sched_barrier(0);
+    rms_row<XB, YB, CH, true>(a, r1, lane, rb, gam);
+    if (r2 >= a.rows) break;
+    row = r2;
   }
 }
 
@@ -153,6 +214,22 @@ void launch_rmsnorm_rows(const RowNormArgs& a, hipStream_t stream) {
     const int64_t blocks = (a.rows + 3) / 4;
     const dim3 grid((unsigned)(blocks < 65536 ? blocks : 65536)), block(256);
     const int ch = (int)((chunks + 63) / 64);
+    // whole rows of 2, 4 or 8 chunks per lane: the pipelined kernel, at most
+    // 2048 waves (two workgroups per CU)
+    if (chunks == 64 * ch && ch <= 8 && ((uintptr_t)a.gamma & 15) == 0) {
+      const dim3 grid_pipe((unsigned)(blocks < 512 ? blocks : 512));
+#define REW_RMS(XB, YB, CH) hipLaunchKernelGGL((rmsnorm_pipe_kernel<XB, YB, CH>), grid_pipe, block, 0, stream, a)
+#define REW_RMS_CH(XB, YB) \
+      if (ch == 2) REW_RMS(XB, YB, 2); else if (ch == 4) REW_RMS(XB, YB, 4); else REW_RMS(XB, YB, 8)
+      if (xb == 2 && yb == 2) { REW_RMS_CH(2, 2); }
+      else if (xb == 2) { REW_RMS_CH(2, 4); }
+      else if (yb == 2) { REW_RMS_CH(4, 2); }
+      else { REW_RMS_CH(4, 4); }
+#undef REW_RMS_CH
+#undef REW_RMS
+      REW_HIP(hipGetLastError());
+      return;
+    }
 #define REW_RMS(XB, YB, CH) hipLaunchKernelGGL((rmsnorm_wave_kernel<XB, YB, CH>), grid, block, 0, stream, a)
 #define REW_RMS_CH(XB, YB) \
     if (ch <= 2) REW_RMS(XB, YB, 2); else if (ch <= 4) REW_RMS(XB, YB, 4); \
@@ -178,50 +255,103 @@ void launch_rmsnorm_rows(const RowNormArgs& a, hipStream_t stream) {
 // -- elements 4 (64 c + l) + j, j = 0..3 in order -- then combine lanes by a
 // butterfly over xor 32, 16, ..., 1; the sum here runs in exactly that
 // order, and the max (order-free) and exp / divide are the same fp32 ops.
-template <int CH>  // 16-byte chunks per lane
+// One row per wave; PIPE: each wave walks several rows (grid-stride) and
+// loads its next row before computing the current one, the rows alternating
+// between two register buffers (no copies, which would wait for the loads),
+// so the HBM reads of one row overlap the exp / divide work of the last.
+// FULL: n == 256 CH, every chunk in range; the loads then carry no guards
+// (a guarded load is a branch, and the compiler waits for every load in
+// flight at each one, the next row's included).
+// The arithmetic of each row is the same either way.
+template <int CH, bool FULL>
+__device__ __forceinline__ void softmax_load(const SoftmaxArgs& a, int64_t row, int lane,
+                                             float4 (&v)[CH]) {
+  const float* x = a.x + row * a.x_rs;
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const int64_t j = ((int64_t)k * 64 + lane) * 4;
+    if (FULL || j < a.n) v[k] = *(const float4*)(x + j);
+  }
+}
+template <int CH, bool FULL>
+__device__ __forceinline__ void softmax_row(const SoftmaxArgs& a, int64_t row, int lane,
+                                            float4 (&v)[CH]) {
+  // The row max enters only as x - m, so two of reduceMax's rules cannot
+  // change a result: +0 and -0 give the same exp(x - m) bits, and with a
+  // NaN in the row the sum is NaN and every output NaN however m treats
+  // it.  The plain hardware max (one instruction, NaN-dropping, either
+  // zero) therefore gives the op-by-op outputs bit for bit, NaN payloads
+  // aside.
+  float m = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const int64_t j = ((int64_t)k * 64 + lane) * 4;
+    if (FULL || j < a.n) {
+      m = __builtin_fmaxf(m, v[k].x);
+      m = __builtin_fmaxf(m, v[k].y);
+      m = __builtin_fmaxf(m, v[k].z);
+      m = __builtin_fmaxf(m, v[k].w);
+    }
+  }
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, s, 64));
+  float sum = 0.0f;
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const int64_t j = ((int64_t)k * 64 + lane) * 4;
+    if (FULL || j < a.n) {
+      v[k].x = expf(v[k].x - m);
+      v[k].y = expf(v[k].y - m);
+      v[k].z = expf(v[k].z - m);
+      v[k].w = expf(v[k].w - m);
+      sum = sum + v[k].x;
+      sum = sum + v[k].y;
+      sum = sum + v[k].z;
+      sum = sum + v[k].w;
+    }
+  }
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) sum = sum + __shfl_xor(sum, s, 64);
+  float* y = a.y + row * a.n;
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const int64_t j = ((int64_t)k * 64 + lane) * 4;
+    if (FULL || j < a.n)
+      *(float4*)(y + j) = make_float4(v[k].x / sum, v[k].y / sum, v[k].z / sum, v[k].w / sum);
+  }
+}
+template <int CH, bool PIPE, bool FULL>  // CH: 16-byte chunks per lane
 __global__ void __launch_bounds__(256) softmax_wave_kernel(SoftmaxArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t waves = (int64_t)gridDim.x * 4;
-  for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < a.rows; row += waves) {
-    const float* x = a.x + row * a.x_rs;
-    float4 v[CH];
-    float m = -INFINITY;
-#pragma unroll
-    for (int k = 0; k < CH; ++k) {
-      const int64_t j = ((int64_t)k * 64 + lane) * 4;
-      if (j < a.n) {
-        v[k] = *(const float4*)(x + j);
-        m = fmax_prop(m, v[k].x);
-        m = fmax_prop(m, v[k].y);
-        m = fmax_prop(m, v[k].z);
-        m = fmax_prop(m, v[k].w);
-      }
+  int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if constexpr (!PIPE) {
+    for (; row < a.rows; row += waves) {
+      float4 v[CH];
+      softmax_load<CH, FULL>(a, row, lane, v);
+      softmax_row<CH, FULL>(a, row, lane, v);
     }
-#pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) m = fmax_prop(m, __shfl_xor(m, s, 64));
-    float sum = 0.0f;
-#pragma unroll
-    for (int k = 0; k < CH; ++k) {
-      const int64_t j = ((int64_t)k * 64 + lane) * 4;
-      if (j < a.n) {
-        v[k].x = expf(v[k].x - m);
-        v[k].y = expf(v[k].y - m);
-        v[k].z = expf(v[k].z - m);
-        v[k].w = expf(v[k].w - m);
-        sum = sum + v[k].x;
-        sum = sum + v[k].y;
-        sum = sum + v[k].z;
-        sum = sum + v[k].w;
-      }
-    }
-#pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) sum = sum + __shfl_xor(sum, s, 64);
-    float* y = a.y + row * a.n;
-#pragma unroll
-    for (int k = 0; k < CH; ++k) {
-      const int64_t j = ((int64_t)k * 64 + lane) * 4;
-      if (j < a.n)
-        *(float4*)(y + j) = make_float4(v[k].x / sum, v[k].y / sum, v[k].z / sum, v[k].w / sum);
+  } else {
+    // The next row's loads are unconditional (past the last row a wave
+    // re-reads the row it just read): a load under a branch would leave the
+    // compiler, at the merge, waiting for every load in flight before the
+    // current row's arithmetic.
+    row = __builtin_amdgcn_readfirstlane((int)row);
+    if (row >= a.rows) return;
+    float4 va[CH], vb[CH];
+    softmax_load<CH, FULL>(a, row, lane, va);
+    for (;;) {
+      const int64_t r1 = row + waves;
+      softmax_load<CH, FULL>(a, r1 < a.rows ? r1 : row, lane, vb);
+      __builtin_amdgcn_sched_barrier(0);  // (issued before this row's work)
+      softmax_row<CH, FULL>(a, row, lane, va);
+      if (r1 >= a.rows) break;
+      const int64_t r2 = r1 + waves;
+      softmax_load<CH, FULL>(a, r2 < a.rows ? r2 : r1, lane, va);
+      __builtin_amdgcn_sched_barrier(0);
+      softmax_row<CH, FULL>(a, r1, lane, vb);
+      if (r2 >= a.rows) break;
+      row = r2;
     }
   }
 }
@@ -255,13 +385,20 @@ void launch_softmax_rows(const SoftmaxArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(softmax_thread_kernel, dim3((unsigned)(blocks < 65536 ? blocks : 65536)),
                        dim3(256), 0, stream, a);
   } else {
+    // Rows of exactly 1024, 2048 or 4096 use the pipelined unguarded
+    // kernels: at most 2048 waves (two workgroups per CU), each walking
+    // rows / 2048 rows.  Other widths keep one row per wave.
     const int64_t blocks = (a.rows + 3) / 4;
+    const dim3 grid_pipe((unsigned)(blocks < 512 ? blocks : 512));
     const dim3 grid((unsigned)(blocks < 65536 ? blocks : 65536)), block(256);
     const int64_t ch = (a.n / 4 + 63) / 64;
-    if (ch <= 4) hipLaunchKernelGGL(softmax_wave_kernel<4>, grid, block, 0, stream, a);
-    else if (ch <= 8) hipLaunchKernelGGL(softmax_wave_kernel<8>, grid, block, 0, stream, a);
-    else if (ch <= 16) hipLaunchKernelGGL(softmax_wave_kernel<16>, grid, block, 0, stream, a);
-    else hipLaunchKernelGGL(softmax_wave_kernel<32>, grid, block, 0, stream, a);
+    if (a.n == 1024) hipLaunchKernelGGL((softmax_wave_kernel<4, true, true>), grid_pipe, block, 0, stream, a);
+    else if (a.n == 2048) hipLaunchKernelGGL((softmax_wave_kernel<8, true, true>), grid_pipe, block, 0, stream, a);
+    else if (a.n == 4096) hipLaunchKernelGGL((softmax_wave_kernel<16, true, true>), grid_pipe, block, 0, stream, a);
+    else if (ch <= 4) hipLaunchKernelGGL((softmax_wave_kernel<4, false, false>), grid, block, 0, stream, a);
+    else if (ch <= 8) hipLaunchKernelGGL((softmax_wave_kernel<8, false, false>), grid, block, 0, stream, a);
+    else if (ch <= 16) hipLaunchKernelGGL((softmax_wave_kernel<16, false, false>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((softmax_wave_kernel<32, false, false>), grid, block, 0, stream, a);
   }
   REW_HIP(hipGetLastError());
 }

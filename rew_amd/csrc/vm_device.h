@@ -52,16 +52,20 @@ __device__ __forceinline__ float round_f16(float f) {
   return __half2float(__float2half(f));
 }
 
-// IEEE 754-2019 maximum/minimum: NaN-propagating, -0 < +0.
+// IEEE 754-2019 maximum/minimum: NaN-propagating (the canonical quiet NaN),
+// -0 < +0.  Written as selects: equal operands differ only for +-0, where
+// the smaller bit pattern is +0 and the larger -0.  Bitwise | and & keep
+// it branch-free (early returns or short-circuit || compiled to a branch per
+// element, and the compiler then waited for every load in flight at each).
 __device__ __forceinline__ float fmax_prop(float a, float b) {
-  if (a != a || b != b) return __builtin_nanf("");
-  if (a == b) return (as_u(a) & 0x80000000u) ? b : a;
-  return a > b ? a : b;
+  const bool take_a = (a > b) | ((a == b) & (as_u(a) <= as_u(b)));
+  const float r = take_a ? a : b;
+  return ((a != a) | (b != b)) ? __builtin_nanf("") : r;
 }
 __device__ __forceinline__ float fmin_prop(float a, float b) {
-  if (a != a || b != b) return __builtin_nanf("");
-  if (a == b) return (as_u(a) & 0x80000000u) ? a : b;
-  return a < b ? a : b;
+  const bool take_a = (a < b) | ((a == b) & (as_u(a) >= as_u(b)));
+  const float r = take_a ? a : b;
+  return ((a != a) | (b != b)) ? __builtin_nanf("") : r;
 }
 
 // ---- scalar / vector loads and stores in register representation --------

@@ -131,9 +131,12 @@ def test_held_intermediate_blocks_fusion(gpu, oracle):
 # ---- row composites ---------------------------------------------------------------------
 
 @pytest.mark.parametrize("shape,bf16", [((2, 100, 4096), True), ((37, 1000), False),
-                                        ((3, 9000), True)])
+                                        ((3, 9000), True), ((4100, 4096), True),
+                                        ((2500, 1024), False)])
 def test_rmsnorm_row_kernel(gpu, oracle, shape, bf16):
-    """rew's rmsNorm chain (src/rew/nn/norm.nim:204-224) runs as one row kernel."""
+    """rew's rmsNorm chain (src/rew/nn/norm.nim:204-224) runs as one row kernel.
+    Whole rows of 2, 4 or 8 chunks per lane take the pipelined kernel; more
+    rows than its 2048 waves give waves of two and three rows."""
     key = oracle.init_key(500 + shape[-1])
     n = shape[-1]
     x = oracle.normal_f32(oracle.fold_in(key, 0), int(np.prod(shape))).reshape(shape)
@@ -307,12 +310,15 @@ def test_qkv_projections_one_launch(gpu, oracle, B, S, E_, H, KV, D):
 
 
 @pytest.mark.parametrize("shape", [(64, 4096), (33, 100), (16, 2048), (5, 8192), (7, 132),
-                                   (2, 3, 256), (3, 130)])
+                                   (2, 3, 256), (3, 130), (4099, 1024), (2100, 2048),
+                                   (2050, 4096)])
 def test_softmax_row_kernel(gpu, oracle, shape):
     """rew's softmax chain (src/rew/nn/activation.nim:64-77) over the last axis
     runs as one row kernel whose sum follows the compiled row reduction's
     order, so it equals the op-by-op path bit for bit; rows of n % 4 != 0 at
-    n >= 128 take the generic path."""
+    n >= 128 take the generic path.  More rows than the 2048 waves of the
+    pipelined kernels (n = 1024, 2048, 4096) give waves of two and three rows,
+    leaving the row loop at either half."""
     n = shape[-1]
     x = oracle.normal_f32(oracle.init_key(900 + n), int(np.prod(shape))).reshape(shape) * 3
     x[(0,) * (len(shape) - 1)][min(5, n - 1)] = np.nan  # a NaN row
