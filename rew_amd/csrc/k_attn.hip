@@ -127,7 +127,16 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(FlashArgs a) {
   const int nqt = (a.Sq + BQ - 1) / BQ;
   const int nbh = a.B * a.H;
   const int rank = blockIdx.x / nbh;
-  const int bh = blockIdx.x - rank * nbh;
+  int bh = blockIdx.x - rank * nbh;
+  // GQA: the G query heads of one KV head go to one XCD (workgroups whose
+  // indices agree mod 8 share an XCD) at adjacent dispatch slots, so that
+  // XCD's L2 serves the same K/V tiles to all of them.  A bijection on
+  // [0, B H) when B Hkv is a multiple of 8.
+  if (a.H > a.Hkv && (a.B * a.Hkv) % 8 == 0) {
+    const int G = a.H / a.Hkv, x = bh % 8, j = bh / 8;
+    const int gi = (j / G) * 8 + x, m = j % G;
+    bh = (gi / a.Hkv) * a.H + (gi % a.Hkv) * G + m;
+  }
   // the most expensive query tiles are scheduled first
   const int qt = a.heavy_last ? nqt - 1 - rank : rank;
   const int b = bh / a.H, h = bh - b * a.H;

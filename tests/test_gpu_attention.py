@@ -80,6 +80,8 @@ CASES = [  # B, H, Hkv, Sq, Sk, D
     (1, 2, 1, 70, 70, 32),
     (1, 4, 4, 64, 192, 128),
     (1, 3, 1, 1, 33, 64),
+    (2, 16, 4, 96, 96, 64),     # B * Hkv a multiple of 8: the query heads of a KV
+    (1, 16, 8, 130, 130, 128),  # head share an XCD (a permuted workgroup order)
 ]
 
 
