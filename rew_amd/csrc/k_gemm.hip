@@ -651,6 +651,93 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_256_kernel(GemmArgs g, Group
   }
 }
 
+// f32 GEMM with a narrow output (N <= 64, N % 4 == 0; a router's
+// [T, H] x [H, E]): 16-row tiles, so M / 16 workgroups where the generic
+// kernel's 64 x 64 tiles give M / 64 and leave most of the chip idle.  The
+// k-steps are 32 deep, loaded as 16-byte vectors into two register sets in
+// turn, so each load has two k-steps to land.  Every output is a sequential
+// fmaf chain over k = 0, 1, ..., K - 1 from 0, as in gemm_generic_kernel, so
+// the two kernels give the same bits.  Thread t computes row t / 16, columns
+// 4 (t % 16) .. + 3; columns past N read an in-range chunk and are not stored.
+__global__ void __launch_bounds__(256) gemm_f32_narrow_kernel(GemmArgs g) {
+  __shared__ float As[32][17];  // [k][row]
+  __shared__ float Bs[32][64];  // [k][column]
+  const int tid = threadIdx.x;
+  const int r = tid >> 4, c4 = (tid & 15) * 4;
+  const int64_t m0 = (int64_t)blockIdx.x * 16;
+  const float* A = (const float*)g.a;
+  const float* B = (const float*)g.b;
+  // loaders: A, 16 rows x 32 k (threads 0..127, one 16-byte chunk each);
+  // B, 32 k x 64 columns (two chunks per thread, k rows bk and bk + 16)
+  const int ar = (tid >> 3) & 15, ak = (tid & 7) * 4;
+  const float* ap = A + (m0 + ar < g.M ? m0 + ar : g.M - 1) * g.a_sm + ak;
+  const int bk = tid >> 4;
+  const int64_t bcol = c4 < g.N ? c4 : g.N - 4;
+  const float* bp = B + bk * g.b_sk + bcol;
+  const int64_t b16 = 16 * g.b_sk;
+  // two register sets (named, not indexed: an indexed array went to scratch)
+  float4 pa0 = make_float4(0, 0, 0, 0), pa1 = pa0, pb00, pb01, pb10, pb11;
+  auto gload = [&](float4& pa, float4& pb0, float4& pb1, int64_t k0) {
+    if (tid < 128) pa = *(const float4*)(ap + k0);
+    pb0 = *(const float4*)(bp + k0 * g.b_sk);
+    pb1 = *(const float4*)(bp + k0 * g.b_sk + b16);
+  };
+  auto sstore = [&](const float4& pa, const float4& pb0, const float4& pb1) {
+    if (tid < 128) {
+      As[ak][ar] = pa.x;
+      As[ak + 1][ar] = pa.y;
+      As[ak + 2][ar] = pa.z;
+      As[ak + 3][ar] = pa.w;
+    }
+    *(float4*)&Bs[bk][c4] = pb0;
+    *(float4*)&Bs[bk + 16][c4] = pb1;
+  };
+  float acc0 = 0.0f, acc1 = 0.0f, acc2 = 0.0f, acc3 = 0.0f;
+  auto step = [&]() {
+#pragma unroll 8
+    for (int kk = 0; kk < 32; ++kk) {
+      const float a = As[kk][r];
+      const float4 b = *(const float4*)&Bs[kk][c4];
+      acc0 = fmaf(a, b.x, acc0);
+      acc1 = fmaf(a, b.y, acc1);
+      acc2 = fmaf(a, b.z, acc2);
+      acc3 = fmaf(a, b.w, acc3);
+    }
+  };
+  // K % 64 == 0: the k-steps come in pairs, set 0 then set 1
+  gload(pa0, pb00, pb01, 0);
+  gload(pa1, pb10, pb11, 32);
+  for (int64_t k0 = 0; k0 < g.K; k0 += 64) {
+    sstore(pa0, pb00, pb01);
+    __syncthreads();
+    if (k0 + 64 < g.K) gload(pa0, pb00, pb01, k0 + 64);
+    step();
+    __syncthreads();
+    sstore(pa1, pb10, pb11);
+    __syncthreads();
+    if (k0 + 96 < g.K) gload(pa1, pb10, pb11, k0 + 96);
+    step();
+    __syncthreads();
+  }
+  const int64_t m = m0 + r;
+  if (m >= g.M) return;
+  const float accs[4] = {acc0, acc1, acc2, acc3};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t n = c4 + j;
+    if (n < g.N)
+      vm::store_scalar(g.c, g.c_dtype, m * g.c_sm + n, vm::as_u(epi_value(g, 0, m, n, accs[j])));
+  }
+}
+
+static bool f32_narrow_ok(const GemmArgs& g) {
+  return g.dtype == REW_DT_FLOAT32 && g.batch == 1 && g.M >= 1 && g.N >= 4 && g.N <= 64 &&
+         g.N % 4 == 0 && g.K >= 64 && g.K % 64 == 0 && g.a_sk == 1 && g.b_sn == 1 &&
+         g.a_sm % 4 == 0 && g.b_sk % 4 == 0 && ((uintptr_t)g.a & 15) == 0 &&
+         ((uintptr_t)g.b & 15) == 0 && (g.epi == EPI_NONE || g.epi == EPI_BIAS) &&
+         g.M / 16 < (1 << 30);
+}
+
 static bool mfma_ok(const GemmArgs& g, bool* a_kc, bool* b_kc) {
   if (g.dtype != REW_DT_BFLOAT16) return false;
   if (g.c_dtype != REW_DT_BFLOAT16 && g.c_dtype != REW_DT_FLOAT32) return false;
@@ -775,6 +862,9 @@ void launch_gemm(const GemmArgs& g, hipStream_t stream) {
       hipLaunchKernelGGL((gemm_bf16_mfma_kernel<false, true>), dim3(grid), dim3(256), 0, stream, g);
     else
       hipLaunchKernelGGL((gemm_bf16_mfma_kernel<false, false>), dim3(grid), dim3(256), 0, stream, g);
+  } else if (f32_narrow_ok(g)) {
+    hipLaunchKernelGGL(gemm_f32_narrow_kernel, dim3((unsigned)((g.M + 15) / 16)), dim3(256), 0,
+                       stream, g);
   } else {
     dim3 grid((unsigned)((g.N + 63) / 64), (unsigned)((g.M + 63) / 64),
               (unsigned)(g.batch < 65535 ? g.batch : 65535));

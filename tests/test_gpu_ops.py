@@ -203,6 +203,29 @@ def test_matmul_f32(gpu, oracle, M, K, N):
     assert np.all(np.abs(got - want) <= bound + 1e-30)
 
 
+@pytest.mark.parametrize("M,K,N", [(1000, 256, 64), (33, 128, 12), (8192, 2048, 64)])
+def test_matmul_f32_narrow(gpu, oracle, M, K, N):
+    """f32 products of at most 64 output columns (a router's [T, H] x [H, E])
+    take a 16-row-tile kernel that accumulates each output in the generic
+    kernel's order. The same product with the weight stored [N, K]
+    (k-contiguous, which the narrow kernel does not take) runs the generic
+    kernel and must give the same bits, with and without the bias add."""
+    r = rng(M + K + N + 7)
+    a = r.uniform(-1, 1, (M, K)).astype(np.float32)
+    b = r.uniform(-0.1, 0.1, (K, N)).astype(np.float32)
+    bias = r.uniform(-1, 1, (N,)).astype(np.float32)
+    bt = np.ascontiguousarray(b.T)
+    for with_bias in (False, True):
+        def lin(y):
+            return O.add(y, O.broadcastTo(dev(bias), [M, N], [1])) if with_bias else y
+        got = host(lin(O.matmul(dev(a), dev(b))))
+        ref = host(lin(O.dotGeneral(dev(a), dev(bt), [], [], [1], [1])))
+        np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+    want = oracle.gemm(a, b) + bias
+    bound = 1e-5 * (oracle.gemm(np.abs(a), np.abs(b)) + np.abs(bias))
+    assert np.all(np.abs(got - want) <= bound + 1e-30)
+
+
 def _bf16_close(got, want, tol=2e-2):
     err = np.linalg.norm((got - want).ravel()) / max(np.linalg.norm(want.ravel()), 1e-30)
     assert err <= tol, f"normwise relative error {err:.3e} > {tol}"
