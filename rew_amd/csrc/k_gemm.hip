@@ -660,8 +660,10 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_256_kernel(GemmArgs g, Group
 // the two kernels give the same bits.  Thread t computes row t / 16, columns
 // 4 (t % 16) .. + 3; columns past N read an in-range chunk and are not stored.
 __global__ void __launch_bounds__(256) gemm_f32_narrow_kernel(GemmArgs g) {
-  __shared__ float As[32][17];  // [k][row]
-  __shared__ float Bs[32][64];  // [k][column]
+  // Bs is read and written as float4: both arrays are declared 16-byte
+  // aligned rather than relying on where the compiler places them
+  __shared__ __attribute__((aligned(16))) float As[32][17];  // [k][row]
+  __shared__ __attribute__((aligned(16))) float Bs[32][64];  // [k][column]
   const int tid = threadIdx.x;
   const int r = tid >> 4, c4 = (tid & 15) * 4;
   const int64_t m0 = (int64_t)blockIdx.x * 16;
@@ -823,7 +825,7 @@ const char* gemm_variant(const GemmArgs& g) {
     return g.epi == EPI_SWIGLU ? "gemm_lds_swiglu" : (bkc ? "gemm_lds_tn" : "gemm_lds_nn");
   }
   if (g.epi == EPI_SWIGLU) return "gemm_bf16_256_swiglu";
-  if (!mfma_ok(g, &akc, &bkc)) return "gemm_generic";
+  if (!mfma_ok(g, &akc, &bkc)) return f32_narrow_ok(g) ? "gemm_f32_narrow" : "gemm_generic";
   if (use_256(g, akc)) return bkc ? "gemm_bf16_256_tn" : "gemm_bf16_256_nn";
   if (akc && bkc) return "gemm_bf16_mfma_tn";
   if (akc) return "gemm_bf16_mfma_nn";

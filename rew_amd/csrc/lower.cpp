@@ -266,6 +266,10 @@ struct MoePlan {
   Tensor* topw = nullptr;   // [T, k] f32
   int E = 0;                // router width
   std::vector<MoeMember> mem;
+  // matching state, applied only once the whole group is known lowerable:
+  // the members' intermediates (never materialized) and the running sums
+  // between members
+  std::vector<Tensor*> inner, mids;
 };
 
 struct Lower {
@@ -284,11 +288,19 @@ struct Lower {
   // (reduceMean's reduceSum next to a reduceSum of the same tensor) aliases
   // the first result
   std::map<std::tuple<Tensor*, int, std::vector<int64_t>, int>, Tensor*> reduce_done;
+  // dense copies made by emit_permuted_copy and not yet freed: released
+  // (stream-ordered) when their consumer is enqueued or at the end of the flush
+  std::unordered_set<Tensor*> temps;
 
   explicit Lower(Ctx* ctx) : c(ctx) {}
+  void drop_temp(Tensor* t) {
+    if (temps.erase(t)) maybe_destroy(t);
+  }
 
   void match_moe();
+  bool moe_lowerable(const MoePlan& p);
   bool emit_moe(Tensor* t, const MoePlan& p);
+  void dense_rows(Tensor* x, int64_t n, const void** ptr, int64_t* rs);
 
   bool match_flash(Node* pv);
   void match_gemm_epilogues();
@@ -1149,6 +1161,7 @@ Tensor* Lower::emit_permuted_copy(Tensor* t, const std::vector<int>& perm) {
   for (int i = 0; i < s.rank; ++i) s.d[i] = t->shape.d[perm[i]];
   Tensor* out = new_tensor(c, t->dt, s);
   out->plan_dead = true;  // marks a planner-private temporary
+  temps.insert(out);
   Affine m;
   m.R = m.r = s.rank;
   for (int k = 0; k < s.rank; ++k) m.S[perm[k]][k] = 1;
@@ -1314,9 +1327,7 @@ void Lower::emit_dot(Node* n) {
   }
   // canonical copies made for this GEMM die with it (stream-ordered free)
   for (Tensor* t : {ta, tb})
-    if (t && t->ctx == c && !t->prod && t->ext == 0 && t->uses == 0 && t != a &&
-        t != b && t->plan_dead)
-      maybe_destroy(t);
+    if (t && t != a && t != b) drop_temp(t);
 }
 
 
@@ -2066,7 +2077,7 @@ void Lower::match_moe() {
       if (extend) {
         g = std::move(it->second);
         open.erase(it);
-        prev->plan_mat = false;
+        g.mids.push_back(prev);
       } else {
         g.start = prev;
         g.x = x;
@@ -2076,16 +2087,117 @@ void Lower::match_moe() {
         g.E = (int)src->shape.d[src->shape.rank - 1];
       }
       g.mem.push_back(m);
-      for (Tensor* t : inner) {
-        t->plan_mat = false;
-        gemm_out.erase(t);
-      }
-      out->plan_mat = true;
+      g.inner.insert(g.inner.end(), inner.begin(), inner.end());
       open[out] = std::move(g);
       break;
     }
   }
-  for (auto& kv : open) moe_out[kv.first] = std::move(kv.second);
+  // A group is claimed only when emit_moe cannot fail on it; otherwise its
+  // ops keep their ordinary plans (fused SwiGLU / bias GEMMs, elementwise
+  // combine), exactly as in op-by-op mode.
+  for (auto& kv : open) {
+    MoePlan& g = kv.second;
+    if (!moe_lowerable(g)) {
+      if (debug_plan())
+        std::fprintf(stderr, "[plan] moe: group of %zu experts not lowerable, generic path\n",
+                     g.mem.size());
+      continue;
+    }
+    for (Tensor* t : g.inner) {
+      t->plan_mat = false;
+      gemm_out.erase(t);
+    }
+    for (Tensor* t : g.mids) t->plan_mat = false;
+    kv.first->plan_mat = true;
+    moe_out[kv.first] = std::move(g);
+  }
+}
+
+// Arguments of the two grouped expert GEMMs over dense [*, H] token rows
+// and dense [*, I] hidden rows (operand pointers left null).
+static void moe_gemm_args(int64_t T, int64_t H, int64_t I, int64_t R, GemmArgs* gs,
+                          GemmArgs* gd) {
+  *gs = GemmArgs{};
+  *gd = GemmArgs{};
+  for (GemmArgs* g : {gs, gd}) {
+    g->dtype = kBF16;
+    g->c_dtype = kBF16;
+    g->batch = 1;
+    g->a_sk = 1;
+    g->b_sn = 1;
+    g->a_sb = 0;
+    g->c_sb = 0;
+  }
+  gs->M = T;
+  gs->K = H;
+  gs->N = I;
+  gs->b_sk = I;
+  gs->a_sm = H;
+  gs->c_sm = I;
+  gs->epi = EPI_SWIGLU;
+  gd->M = R;
+  gd->K = I;
+  gd->N = H;
+  gd->b_sk = H;
+  gd->a_sm = I;
+  gd->c_sm = H;
+  gd->epi = EPI_BIAS;
+}
+
+// Whether operand_strides(w) reads w as dense row-major storage at offset 0:
+// a materialized tensor, a pending non-view result (materialized densely
+// when read), a view the planner materializes, or a reshape chain of these.
+static bool reads_dense(Tensor* w) {
+  while (!w->st && !w->plan_mat && w->prod && w->prod->kind == K_RESHAPE) w = w->prod->in[0];
+  return w->st || w->plan_mat || !w->prod || !is_view(w->prod->kind);
+}
+
+// Every condition under which emit_moe would refuse the group, checked
+// before the group's ops give up their own plans: expert weights dense
+// row-major bf16 of the member shapes, bf16 bias vectors, and both grouped
+// GEMMs launchable over dense 16-byte-aligned rows (emit_moe copies x and
+// the running sum densely when their views are not).
+bool Lower::moe_lowerable(const MoePlan& p) {
+  if (p.mem.empty() || p.x->shape.rank != 2 || p.topi->shape.rank != 2) return false;
+  const int64_t T = p.x->shape.d[0], H = p.x->shape.d[1];
+  const int64_t k = p.topi->shape.d[1];
+  if (k < 1 || k > kMoeMaxK || H % 8 || p.start->dt != kBF16 || p.start->numel() != T * H)
+    return false;
+  const int64_t I = p.mem[0].sw.dot->in[1]->shape.d[1];
+  auto weight = [&](Tensor* w, int64_t rows, int64_t cols) {
+    return w->dt == kBF16 && w->shape.rank == 2 && w->shape.d[0] == rows &&
+           w->shape.d[1] == cols && reads_dense(w);
+  };
+  auto vec = [&](Tensor* v, int64_t len) { return v && v->dt == kBF16 && v->numel() == len; };
+  for (const MoeMember& m : p.mem) {
+    if (!m.sw.dot || !m.sw.dot2 || !m.dn.dot) return false;
+    if (!weight(m.sw.dot->in[1], H, I) || !weight(m.sw.dot2->in[1], H, I) ||
+        !weight(m.dn.dot->in[1], I, H) || !vec(m.sw.bias, I) || !vec(m.sw.bias2, I) ||
+        !vec(m.dn.bias, H))
+      return false;
+  }
+  GemmArgs gs, gd;
+  moe_gemm_args(T, H, I, T * k, &gs, &gd);
+  // stand-in operand addresses: the real ones are allocator blocks (aligned)
+  void* const al = reinterpret_cast<void*>(uintptr_t(4096));
+  for (GemmArgs* g : {&gs, &gd}) {
+    g->a = g->b = g->b2 = g->bias = g->bias2 = al;
+    g->c = al;
+  }
+  return gemm_grouped_ok(gs) && gemm_grouped_ok(gd);
+}
+
+// rows_view, with a dense copy when the rows are not 16-byte aligned with
+// a row stride of whole 16-byte chunks (the grouped GEMM and the combine
+// read 16-byte vectors).
+void Lower::dense_rows(Tensor* x, int64_t n, const void** ptr, int64_t* rs) {
+  rows_view(x, n, ptr, rs);
+  if (((uintptr_t)*ptr & 15) == 0 && *rs % 8 == 0) return;
+  std::vector<int> id(x->shape.rank);
+  for (int i = 0; i < x->shape.rank; ++i) id[i] = i;
+  Tensor* d = emit_permuted_copy(x, id);
+  *ptr = d->data();
+  *rs = n;
 }
 
 bool Lower::emit_moe(Tensor* t, const MoePlan& p) {
@@ -2098,10 +2210,10 @@ bool Lower::emit_moe(Tensor* t, const MoePlan& p) {
   const int k = (int)p.topi->shape.d[1];
   const void* xp;
   int64_t x_rs;
-  rows_view(p.x, H, &xp, &x_rs);
+  dense_rows(p.x, H, &xp, &x_rs);
   const void* sp;
   int64_t s_rs;
-  rows_view(p.start, H, &sp, &s_rs);
+  dense_rows(p.start, H, &sp, &s_rs);
   if (p.topi->st == nullptr || p.topw->st == nullptr) return false;
 
   // member weights: gate/up [H, I], down [I, H], dense row-major.  Only the
@@ -2133,22 +2245,21 @@ bool Lower::emit_moe(Tensor* t, const MoePlan& p) {
       ptrs[(size_t)j * n + i] = (uint64_t)(uintptr_t)q[j];
     }
   }
-  GemmArgs gs{}, gd{};
-  for (GemmArgs* g : {&gs, &gd}) {
-    g->dtype = kBF16;
-    g->c_dtype = kBF16;
-    g->batch = 1;
-    g->a_sk = 1;
-    g->b_sn = 1;
-  }
-  gs.K = H;
-  gs.N = I;
-  gs.b_sk = I;
-  gd.K = I;
-  gd.N = H;
-  gd.b_sk = H;
   const int64_t R = T * k;  // routed rows (upper bound of the packed rows)
   const int64_t max_mt = (R + 255) / 256 + n;
+  GemmArgs gs, gd;
+  moe_gemm_args(T, H, I, R, &gs, &gd);
+  gs.a_sm = x_rs;
+  if (x_rs != H && !gemm_grouped_ok(gs)) {
+    // moe_lowerable checked the GEMMs on dense rows: a wider row stride of
+    // x is the one thing that can differ here
+    Tensor* d = emit_permuted_copy(p.x, {0, 1});
+    xp = d->data();
+    x_rs = H;
+    gs.a_sm = H;
+  }
+  if (!gemm_grouped_ok(gs) || !gemm_grouped_ok(gd))
+    throw Error(REW_MI355X_ERR_INVALID, "internal: routed MoE expert GEMM not launchable");
 
   // host tables: member_of[E], members[n] (int32) then the 6 pointer tables
   std::vector<int32_t> member_of(p.E, -1), members(n);
@@ -2207,15 +2318,7 @@ bool Lower::emit_moe(Tensor* t, const MoePlan& p) {
   ga.max_mtiles = max_mt;
   // gate/up: rows gathered from x through the routing permutation
   gs.a = xp;
-  gs.M = T;
-  gs.a_sm = x_rs;
-  gs.a_sk = 1;
-  gs.a_sb = 0;
-  gs.epi = EPI_SWIGLU;
   gs.c = hbuf->data();
-  gs.c_sm = I;
-  gs.c_sb = 0;
-  gs.c_dtype = kBF16;
   ga.rows = ra.perm;
   ga.b = tbl;
   ga.b2 = tbl + n;
@@ -2227,17 +2330,7 @@ bool Lower::emit_moe(Tensor* t, const MoePlan& p) {
     ga.dual_span = std::max(ga.dual_span, d < 0 ? -d : d);
   }
   gd.a = hbuf->data();
-  gd.M = R;
-  gd.a_sm = I;
-  gd.a_sk = 1;
-  gd.a_sb = 0;
-  gd.epi = EPI_BIAS;
   gd.c = ybuf->data();
-  gd.c_sm = H;
-  gd.c_sb = 0;
-  gd.c_dtype = kBF16;
-  if (!gemm_grouped_ok(gs) || !gemm_grouped_ok(gd))
-    throw Error(REW_MI355X_ERR_UNSUPPORTED, "routed MoE: expert GEMM layout not supported");
   if (c->profiling) {
     char nm[160];
     std::snprintf(nm, sizeof nm, "moe_gemm_swiglu[%lld,%lld,%lld,%lld]", (long long)n,
@@ -2795,6 +2888,8 @@ void flush(Ctx* c) {
   } catch (...) {
     err = std::current_exception();
   }
+  for (Tensor* t : L.temps) maybe_destroy(t);
+  L.temps.clear();
 
   // 4. release: graph references drop, temporaries free
   for (Node* n : all) {

@@ -82,6 +82,8 @@ CASES = [  # B, H, Hkv, Sq, Sk, D
     (1, 3, 1, 1, 33, 64),
     (2, 16, 4, 96, 96, 64),     # B * Hkv a multiple of 8: the query heads of a KV
     (1, 16, 8, 130, 130, 128),  # head share an XCD (a permuted workgroup order)
+    (1, 32, 8, 512, 512, 128),  # the Llama layer's heads: head_dim 128, group 4
+    (2, 32, 8, 384, 384, 128),
 ]
 
 

@@ -11,7 +11,10 @@ SwiGLU / down GEMMs over the routed rows, ordered combine).  Checks:
   router probabilities hold a near-tie at the selection boundary;
 * against the backend's own op-by-op (dense, unfused) execution of the same
   op sequence: equal values (the skipped terms are exact zeros and the
-  kernels share one MFMA accumulation order);
+  kernels share one MFMA accumulation order).  This holds while every
+  expert's output is finite: the dense chain turns a token's sum into NaN
+  when an expert it is NOT routed to yields inf or NaN (bf16(inf * 0) is
+  NaN), while the routed path never evaluates that expert on that token;
 * that the sparse kernels really ran (profile names).
 """
 import numpy as np
@@ -21,6 +24,7 @@ pytestmark = pytest.mark.gpu
 
 from rew_amd import eager as E
 from rew_amd import nn, rng
+from rew_amd import ops as O
 from rew_amd import ops as O
 from rew_amd.eager import DType
 
@@ -65,6 +69,32 @@ def ids_match_off_near_ties(oracle, host, k, got_ids, probs_tol=1e-6):
     return int(near.sum())
 
 
+def check_expert_ids(oracle, moe, xt, host, k):
+    """The routing contract: expert ids are bit-exact given identical router
+    probabilities.  The backend's top-k ids must equal the oracle's top-k of
+    the backend's own probabilities; those probabilities must match the
+    oracle's fp32 router within fp32 tolerance (normwise 1e-5); and a row
+    whose ids differ from the oracle's top-k of the oracle's probabilities
+    must hold two candidates closer together than the probability error
+    actually observed on that row (a near-tie).  Returns that row count."""
+    probs_dev = E.toHost(nn.softmax(moe.gate.forward(O.astype(xt, DType.FLOAT32)), 1))
+    _, ids = moe.route(xt)
+    ids = E.toHost(ids)
+    _, want_same = oracle.topk_rows(probs_dev, k)
+    np.testing.assert_array_equal(ids, want_same)
+    probs = oracle.softmax_rows(oracle.linear(host["x"], host["wr"], host["br"], False))
+    err = np.linalg.norm(probs_dev - probs) / np.linalg.norm(probs)
+    assert err <= 1e-5, f"router probabilities normwise relative error {err:.3e}"
+    _, want = oracle.topk_rows(probs, k)
+    diff = np.where(np.any(ids != want, axis=1))[0]
+    for r in diff:
+        row_err = np.max(np.abs(probs_dev[r] - probs[r]))
+        srt = np.sort(probs[r])[::-1]
+        gap = np.min(srt[:k] - srt[1:k + 1])
+        assert gap <= 2 * row_err, (r, gap, row_err)
+    return len(diff)
+
+
 @pytest.mark.parametrize("T,H,I,E_,k,n_shared", [(256, 256, 128, 16, 4, 2),
                                                   (200, 264, 136, 8, 2, 1),
                                                   (32, 128, 64, 64, 2, 2)])
@@ -80,8 +110,7 @@ def test_moe_matches_oracle(gpu, oracle, T, H, I, E_, k, n_shared):
                                        host["br"], k)
     err = np.linalg.norm(out - want) / np.linalg.norm(want)
     assert err <= 2e-2, f"normwise relative error {err:.3e}"
-    _, got_ids = moe.route(xt)
-    ids_match_off_near_ties(oracle, host, k, E.toHost(got_ids))
+    check_expert_ids(oracle, moe, xt, host, k)
 
 
 def test_moe_sparse_equals_dense_op_by_op(gpu, oracle):
@@ -111,3 +140,35 @@ def test_moe_routing_weights(gpu, oracle):
     np.testing.assert_allclose(tw.sum(1), 1.0, rtol=1e-6)
     assert all(len(set(r)) == 6 for r in ti)
     assert np.all(np.diff(tw, axis=1) <= 0)
+
+
+@pytest.mark.parametrize("which", ["down", "gate"])
+def test_moe_unlowerable_weight_falls_back(gpu, oracle, which):
+    """Expert weights given as transposed views.  The down weight keeps its
+    bias-GEMM plan, so the chain matches, but the grouped GEMM cannot read
+    the weight in place: the chain must not be claimed by the MoE lowering,
+    and runs through the ordinary fused GEMMs.  A transposed gate weight
+    has no SwiGLU plan at all, so that expert splits the chain into two
+    routed groups.  Either way the flush succeeds with the op-by-op values."""
+    moe, host = build_moe(oracle, 64, 128, 64, 8, 2, 1, 0x5EED0305)
+    ex = moe.routedExperts[3]
+    attr = "downProj" if which == "down" else "gateProj"
+    w = host["routed"][3][4 if which == "down" else 0]
+    setattr(ex, attr, nn.Linear(O.transpose(E.fromHost(np.ascontiguousarray(w.T),
+                                                       DType.BFLOAT16), [1, 0]),
+                                getattr(ex, attr).bias))
+    xt = E.fromHost(host["x"], DType.BFLOAT16)
+    E.profileBegin()
+    got = E.toHostF32(moe.forward(xt))
+    prof = E.profileEnd()
+    groups = sum(c for n, c, _ in prof if n.startswith("moe_gemm_swiglu"))
+    assert groups == (0 if which == "down" else 2), [n for n, _, _ in prof]
+    E.setMode(1)
+    try:
+        dense = E.toHostF32(moe.forward(xt))
+    finally:
+        E.setMode(0)
+    np.testing.assert_array_equal(got, dense)
+    want, _, _ = oracle.deepseek_moe(host["x"], host["shared"], host["routed"], host["wr"],
+                                     host["br"], 2)
+    assert np.linalg.norm(got - want) / np.linalg.norm(want) <= 2e-2

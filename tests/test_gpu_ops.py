@@ -218,8 +218,14 @@ def test_matmul_f32_narrow(gpu, oracle, M, K, N):
     for with_bias in (False, True):
         def lin(y):
             return O.add(y, O.broadcastTo(dev(bias), [M, N], [1])) if with_bias else y
+        E.profileBegin()
         got = host(lin(O.matmul(dev(a), dev(b))))
+        names = [n for n, _, _ in E.profileEnd()]
+        assert any(n.startswith("gemm_f32_narrow") for n in names), names
+        E.profileBegin()
         ref = host(lin(O.dotGeneral(dev(a), dev(bt), [], [], [1], [1])))
+        names = [n for n, _, _ in E.profileEnd()]
+        assert not any(n.startswith("gemm_f32_narrow") for n in names), names
         np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
     want = oracle.gemm(a, b) + bias
     bound = 1e-5 * (oracle.gemm(np.abs(a), np.abs(b)) + np.abs(bias))
