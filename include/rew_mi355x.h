@@ -105,6 +105,23 @@ int rew_mi355x_from_host(rew_mi355x_ctx* ctx, int dtype, const int64_t* shape,
  * (src/rew/eager.nim:237-247, 558-595, 635-669). */
 int rew_mi355x_to_host(rew_mi355x_buf* buf, void* host, int64_t nbytes);
 
+/* A new tensor of `dtype`/`shape` whose contents are undefined until a
+ * caller writes them on the device (through rew_mi355x_buf_device_ptr).
+ * Replaces: the uninitialised-buffer slot of the PJRT C API that rew's
+ * binding carries (fnClientCreateUninitializedBuffer,
+ * src/rew/pjrt/capi.nim:109); the shim's alloc(ctx, bytes, &h). */
+int rew_mi355x_alloc(rew_mi355x_ctx* ctx, int dtype, const int64_t* shape, int rank,
+                     rew_mi355x_buf** out_buf);
+
+/* Device address of a tensor's storage, valid until its last release.
+ * Flushes the tensor's pending producer first.  Only tensors made by
+ * rew_mi355x_alloc may be written through it: tensors are otherwise
+ * immutable, and small uploads and reshapes share storage.
+ * Replaces: PJRT_Buffer_OpaqueDeviceMemoryDataPointer, the slot rew's
+ * binding carries (fnBufferOpaqueDeviceMemoryDataPointer,
+ * src/rew/pjrt/capi.nim:79). */
+int rew_mi355x_buf_device_ptr(rew_mi355x_buf* buf, void** out_ptr);
+
 /* Dtype, rank and shape (up to REW_MI355X_MAX_RANK dims) of a tensor.
  * Replaces: Tensor.dtype / Tensor.shape (src/rew/tensor.nim:42-52). */
 int rew_mi355x_buf_meta(const rew_mi355x_buf* buf, int* dtype, int* rank,
@@ -195,6 +212,51 @@ int rew_mi355x_profile_entry(rew_mi355x_ctx* ctx, int index, char* name,
 /* Native stream of the context (a hipStream_t), for callers that record
  * their own events around the backend's work. */
 int rew_mi355x_stream(rew_mi355x_ctx* ctx, void** out_stream);
+
+/* ---- routed mixture-of-experts FFN over caller-owned device rows ---------
+ * The routed-expert part of DeepSeekMoE.forward
+ * (src/rew/models/deepseek.nim:122-145), given the router's top-k:
+ *   out[t] = start[t], then for each of token t's routed experts e in chain
+ *   order: out[t] = bf16(out[t] + bf16(f32(E_e(x[t])) * w)),
+ *   E_e(x) = down_e(bf16(silu(gate_e(x)) * up_e(x))) with rew's Linear
+ *   bias adds and bf16 roundings (src/rew/nn/gated_ffn.nim:46-67),
+ * w the token's top-k weight for e.  Exactly the values the backend's
+ * deferred graph computes for the dense op chain (its lowering runs these
+ * kernels), evaluated only on each expert's routed rows.  All pointers
+ * except `expert_ids` and the six weight tables (host arrays of n_experts
+ * device pointers) are device addresses; rows are bf16, 16-byte aligned,
+ * with strides in elements that are multiples of 8; hidden and ffn are
+ * multiples of 8; 1 <= k <= 16; expert ids distinct and in
+ * [0, router_width).  Top-k ids outside the chain's experts add nothing.
+ * Inputs must be ready on the context's stream (e.g. after
+ * rew_mi355x_sync); the work is enqueued on that stream. */
+typedef struct rew_mi355x_moe_args {
+  const void* x;              /* [tokens, hidden] bf16 tokens                */
+  int64_t x_row_stride;
+  const void* start;          /* [tokens, hidden] bf16: output before the    */
+  int64_t start_row_stride;   /* routed experts (shared experts' sum)        */
+  const int32_t* top_ids;     /* [tokens, k] dense                           */
+  const float* top_weights;   /* [tokens, k] dense                           */
+  int64_t tokens, hidden, ffn;
+  int k, router_width, n_experts;
+  const int32_t* expert_ids;  /* host [n_experts]: chain order               */
+  const void* const* gate_w;  /* host [n_experts] of [hidden, ffn] bf16      */
+  const void* const* up_w;    /* host [n_experts] of [hidden, ffn] bf16      */
+  const void* const* gate_b;  /* host [n_experts] of [ffn] bf16              */
+  const void* const* up_b;    /* host [n_experts] of [ffn] bf16              */
+  const void* const* down_w;  /* host [n_experts] of [ffn, hidden] bf16      */
+  const void* const* down_b;  /* host [n_experts] of [hidden] bf16           */
+  void* out;                  /* [tokens, hidden] bf16, dense                */
+} rew_mi355x_moe_args;
+
+/* Enqueues the routed-expert FFN; its working memory (routing tables, the
+ * gathered hidden rows and per-slot expert outputs) comes from the
+ * context's caching allocator.
+ * No reference counterpart: rew reaches this computation only through
+ * DeepSeekMoE.forward's op chain (src/rew/models/deepseek.nim:122-145),
+ * which rew_mi355x_execute records and lowers to the same kernels; this is
+ * the direct form for hosts that already hold the router's top-k. */
+int rew_mi355x_moe_routed_ffn(rew_mi355x_ctx* ctx, const rew_mi355x_moe_args* args);
 
 /* ---- rew's input generators (host) --------------------------------------
  * Threefry-2x32 with 4 rounds and the Box-Muller / 24-bit uniform samplers,

@@ -24,6 +24,9 @@ SIGNATURES = {
     "rew_mi355x_to_host": (C.c_int, [_c_buf, C.c_void_p, C.c_int64]),
     "rew_mi355x_buf_meta": (C.c_int, [_c_buf, C.POINTER(C.c_int), C.POINTER(C.c_int),
                                       C.POINTER(C.c_int64)]),
+    "rew_mi355x_alloc": (C.c_int, [_c_ctx, C.c_int, C.POINTER(C.c_int64), C.c_int,
+                                   C.POINTER(_c_buf)]),
+    "rew_mi355x_buf_device_ptr": (C.c_int, [_c_buf, C.POINTER(C.c_void_p)]),
     "rew_mi355x_retain": (C.c_int, [_c_buf]),
     "rew_mi355x_release": (None, [_c_buf]),
     "rew_mi355x_execute": (C.c_int, [_c_ctx, C.c_char_p, C.POINTER(_c_buf), C.c_int,
@@ -44,6 +47,7 @@ SIGNATURES = {
     "rew_mi355x_profile_entry": (C.c_int, [_c_ctx, C.c_int, C.c_char_p, C.c_int,
                                            C.POINTER(C.c_int64), C.POINTER(C.c_double)]),
     "rew_mi355x_stream": (C.c_int, [_c_ctx, C.POINTER(C.c_void_p)]),
+    "rew_mi355x_moe_routed_ffn": (C.c_int, [_c_ctx, C.c_void_p]),
     "rew_mi355x_rng_split": (None, [C.c_uint32, C.c_uint32, C.c_int, C.POINTER(C.c_uint32)]),
     "rew_mi355x_rng_fold_in": (None, [C.c_uint32, C.c_uint32, C.c_uint64,
                                       C.POINTER(C.c_uint32)]),
@@ -52,6 +56,19 @@ SIGNATURES = {
     "rew_mi355x_rng_normal_f32": (None, [C.c_uint32, C.c_uint32, C.c_int64, C.c_float,
                                          C.c_float, C.c_void_p]),
 }
+
+
+class MoeArgs(C.Structure):
+    """rew_mi355x_moe_args (include/rew_mi355x.h)."""
+    _fields_ = [("x", C.c_void_p), ("x_row_stride", C.c_int64),
+                ("start", C.c_void_p), ("start_row_stride", C.c_int64),
+                ("top_ids", C.c_void_p), ("top_weights", C.c_void_p),
+                ("tokens", C.c_int64), ("hidden", C.c_int64), ("ffn", C.c_int64),
+                ("k", C.c_int), ("router_width", C.c_int), ("n_experts", C.c_int),
+                ("expert_ids", C.c_void_p),
+                ("gate_w", C.c_void_p), ("up_w", C.c_void_p), ("gate_b", C.c_void_p),
+                ("up_b", C.c_void_p), ("down_w", C.c_void_p), ("down_b", C.c_void_p),
+                ("out", C.c_void_p)]
 
 
 class Stats(C.Structure):

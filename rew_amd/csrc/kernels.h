@@ -219,6 +219,35 @@ struct MoeCombineArgs {
 };
 void launch_moe_combine(const MoeCombineArgs& a, hipStream_t stream);
 
+// The routed experts of rew's DeepSeekMoE.forward
+// (src/rew/models/deepseek.nim:122-145) over dense bf16 rows:
+//   out[t] = start[t] + sum over token t's routed experts e, in chain order,
+//            of bf16(f32(down_e(SwiGLU_e(x[t]))) * w[t, e]),
+// rounded to bf16 after every add -- the dense op sequence's arithmetic on
+// the only rows where it is non-zero.  Expert `i` of the chain has id
+// expert[i] in [0, E) and weights ptr[j][i] (device pointers, in the order
+// gate W [H, I], up W [H, I], gate bias [I], up bias [I], down W [I, H],
+// down bias [H]; W dense row-major).  `expert` and the six tables are host
+// arrays of n entries.  Scratch: routed_ffn_scratch_bytes() of device
+// memory, 256-byte aligned, that no other work uses meanwhile.
+struct RoutedFfn {
+  const void* x = nullptr;       // [T, H] bf16, rows x_rs apart
+  int64_t x_rs = 0;
+  const void* start = nullptr;   // [T, H] bf16: the sum before the routed experts
+  int64_t start_rs = 0;
+  const int32_t* topi = nullptr;  // [T, k] expert ids
+  const float* topw = nullptr;    // [T, k] routing weights
+  int64_t T = 0, H = 0, I = 0;
+  int k = 0, E = 0, n = 0;
+  const int32_t* expert = nullptr;
+  const void* const* ptr[6] = {};
+  void* out = nullptr;           // [T, H] bf16, dense
+};
+// Throws Error(REW_MI355X_ERR_INVALID) naming the first argument the
+// kernels cannot take.
+void routed_ffn_check(const RoutedFfn& a);
+size_t routed_ffn_scratch_bytes(const RoutedFfn& a);
+
 // ---- fused attention (k_attn.hip) ---------------------------------------------
 // out[b,h,i,:] = sum_j softmax_j(bf16(q[b,h,i,:].k[b,hk,j,:]) * scale + mask(i,j))
 //                * v[b,hk,j,:],  hk = h / (H / Hkv); bf16 operands, d contiguous.

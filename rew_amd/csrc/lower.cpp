@@ -2234,146 +2234,55 @@ bool Lower::emit_moe(Tensor* t, const MoePlan& p) {
     return v->data();
   };
   const int64_t I = p.mem[0].sw.dot->in[1]->shape.d[1];
-  std::vector<uint64_t> ptrs(6 * (size_t)n);
+  std::vector<const void*> ptrs(6 * (size_t)n);
+  std::vector<int32_t> ids(n);
   for (int i = 0; i < n; ++i) {
     const MoeMember& m = p.mem[i];
+    ids[i] = m.e;
     const void* q[6] = {weight(m.sw.dot->in[1], H, I), weight(m.sw.dot2->in[1], H, I),
                         vec(m.sw.bias, I), vec(m.sw.bias2, I),
                         weight(m.dn.dot->in[1], I, H), vec(m.dn.bias, H)};
     for (int j = 0; j < 6; ++j) {
       if (!q[j] || ((uintptr_t)q[j] & 15)) return false;
-      ptrs[(size_t)j * n + i] = (uint64_t)(uintptr_t)q[j];
+      ptrs[(size_t)j * n + i] = q[j];
     }
   }
-  const int64_t R = T * k;  // routed rows (upper bound of the packed rows)
-  const int64_t max_mt = (R + 255) / 256 + n;
-  GemmArgs gs, gd;
-  moe_gemm_args(T, H, I, R, &gs, &gd);
-  gs.a_sm = x_rs;
-  if (x_rs != H && !gemm_grouped_ok(gs)) {
+  RoutedFfn a;
+  a.x = xp;
+  a.x_rs = x_rs;
+  a.start = sp;
+  a.start_rs = s_rs;
+  a.topi = (const int32_t*)p.topi->data();
+  a.topw = (const float*)p.topw->data();
+  a.T = T;
+  a.H = H;
+  a.I = I;
+  a.k = k;
+  a.E = p.E;
+  a.n = n;
+  a.expert = ids.data();
+  for (int j = 0; j < 6; ++j) a.ptr[j] = ptrs.data() + (size_t)j * n;
+  tensor_alloc(t);
+  a.out = t->data();
+  try {
+    routed_ffn_check(a);
+  } catch (const Error&) {
     // moe_lowerable checked the GEMMs on dense rows: a wider row stride of
     // x is the one thing that can differ here
+    if (x_rs == H) throw;
     Tensor* d = emit_permuted_copy(p.x, {0, 1});
-    xp = d->data();
-    x_rs = H;
-    gs.a_sm = H;
+    a.x = d->data();
+    a.x_rs = H;
+    routed_ffn_check(a);
   }
-  if (!gemm_grouped_ok(gs) || !gemm_grouped_ok(gd))
-    throw Error(REW_MI355X_ERR_INVALID, "internal: routed MoE expert GEMM not launchable");
-
-  // host tables: member_of[E], members[n] (int32) then the 6 pointer tables
-  std::vector<int32_t> member_of(p.E, -1), members(n);
-  for (int i = 0; i < n; ++i) {
-    members[i] = p.mem[i].e;
-    member_of[p.mem[i].e] = i;
-  }
-  const size_t i32_bytes = ((size_t)(p.E + n) * 4 + 255) & ~(size_t)255;
-  const size_t meta_bytes = i32_bytes + ptrs.size() * 8;
-  std::vector<uint8_t> host(meta_bytes, 0);
-  std::memcpy(host.data(), member_of.data(), (size_t)p.E * 4);
-  std::memcpy(host.data() + (size_t)p.E * 4, members.data(), (size_t)n * 4);
-  std::memcpy(host.data() + i32_bytes, ptrs.data(), ptrs.size() * 8);
-
-  auto temp = [&](int dt, int64_t elems) {
-    Shape s;
-    s.rank = 1;
-    s.d[0] = elems;
-    Tensor* x = new_tensor(c, dt, s);
-    x->plan_dead = true;
-    tensor_alloc(x);
-    return x;
-  };
-  Tensor* meta = temp(kU8, (int64_t)meta_bytes);
-  Tensor* route = temp(kI32, 2 * (n + 1) + 2 * R);
-  Tensor* hbuf = temp(kBF16, R * I);
-  Tensor* ybuf = temp(kBF16, R * H);
-  upload_async(c, meta->data(), host.data(), meta_bytes);
-  const uint8_t* mb = (const uint8_t*)meta->data();
-  int32_t* rb = (int32_t*)route->data();
-
-  MoeRouteArgs ra;
-  ra.topi = (const int32_t*)p.topi->data();
-  ra.T = T;
-  ra.k = k;
-  ra.E = p.E;
-  ra.member_of = (const int32_t*)mb;
-  ra.members = (const int32_t*)mb + p.E;
-  ra.n_members = n;
-  ra.tile_m = 256;
-  ra.off = rb;
-  ra.mt_start = rb + (n + 1);
-  ra.perm = rb + 2 * (n + 1);
-  ra.slot_of = rb + 2 * (n + 1) + R;
-  prof_begin(c, "moe_route{" + std::to_string(T) + "x" + std::to_string(k) + ",E" +
-                    std::to_string(n) + "}");
-  launch_moe_route(ra, c->stream);
-  prof_end(c);
-  note_launch(c, true);
-
-  const void* const* tbl = (const void* const*)(mb + i32_bytes);
-  GroupArgs ga;
-  ga.off = ra.off;
-  ga.mt_start = ra.mt_start;
-  ga.n_groups = n;
-  ga.max_mtiles = max_mt;
-  // gate/up: rows gathered from x through the routing permutation
-  gs.a = xp;
-  gs.c = hbuf->data();
-  ga.rows = ra.perm;
-  ga.b = tbl;
-  ga.b2 = tbl + n;
-  ga.bias = tbl + 2 * n;
-  ga.bias2 = tbl + 3 * n;
-  ga.dual_span = 0;
-  for (int i = 0; i < n; ++i) {
-    const int64_t d = (int64_t)((uintptr_t)ptrs[n + i] - (uintptr_t)ptrs[i]);
-    ga.dual_span = std::max(ga.dual_span, d < 0 ? -d : d);
-  }
-  gd.a = hbuf->data();
-  gd.c = ybuf->data();
-  if (c->profiling) {
-    char nm[160];
-    std::snprintf(nm, sizeof nm, "moe_gemm_swiglu[%lld,%lld,%lld,%lld]", (long long)n,
-                  (long long)R, (long long)I, (long long)H);
-    prof_begin(c, nm);
-  }
-  launch_gemm_grouped(gs, ga, c->stream);
-  prof_end(c);
-  note_launch(c, true);
-  ga.rows = nullptr;
-  ga.b = tbl + 4 * n;
-  ga.b2 = nullptr;
-  ga.bias = tbl + 5 * n;
-  ga.bias2 = nullptr;
-  if (c->profiling) {
-    char nm[160];
-    std::snprintf(nm, sizeof nm, "moe_gemm_down[%lld,%lld,%lld,%lld]", (long long)n,
-                  (long long)R, (long long)H, (long long)I);
-    prof_begin(c, nm);
-  }
-  launch_gemm_grouped(gd, ga, c->stream);
-  prof_end(c);
-  note_launch(c, true);
-
-  tensor_alloc(t);
-  MoeCombineArgs ca;
-  ca.prev = (const uint16_t*)sp;
-  ca.prev_rs = s_rs;
-  ca.y = (const uint16_t*)ybuf->data();
-  ca.topw = (const float*)p.topw->data();
-  ca.topi = ra.topi;
-  ca.slot_of = ra.slot_of;
-  ca.member_of = ra.member_of;
-  ca.T = T;
-  ca.H = H;
-  ca.k = k;
-  ca.E = p.E;
-  ca.out = (uint16_t*)t->data();
-  prof_begin(c, "moe_combine{" + std::to_string(T) + "x" + std::to_string(H) + "}");
-  launch_moe_combine(ca, c->stream);
-  prof_end(c);
-  note_launch(c, true);
-  for (Tensor* x : {meta, route, hbuf, ybuf}) maybe_destroy(x);
+  Shape ws;
+  ws.rank = 1;
+  ws.d[0] = (int64_t)routed_ffn_scratch_bytes(a);
+  Tensor* work = new_tensor(c, kU8, ws);
+  work->plan_dead = true;
+  tensor_alloc(work);
+  run_routed_ffn(c, a, work->data());
+  maybe_destroy(work);
   return true;
 }
 

@@ -1,0 +1,334 @@
+// The routed-expert FFN of rew's DeepSeekMoE.forward over raw device rows
+// (src/rew/models/deepseek.nim:122-145): the launch sequence the deferred
+// graph's MoE lowering runs, and the C-ABI entry point that runs it
+// directly on caller-owned buffers.
+//
+// Working memory (one block, carved at 256-byte boundaries):
+//   member_of [E] int32    expert id -> chain index, -1 off the chain
+//   members   [n] int32    chain index -> expert id
+//   tables    [6 n] ptr    per-expert weight / bias device pointers
+//   route     [2 (n + 1) + 2 R] int32   offsets, tile starts, packed row ->
+//                                       token, (token, slot) -> packed row
+//   hbuf      [R, I] bf16  SwiGLU outputs of the routed rows
+//   ybuf      [R, H] bf16  down-projection outputs of the routed rows
+// with R = T k routed rows.  Every byte a kernel reads is written earlier
+// in the same sequence, so nothing has to start at zero.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <mutex>
+
+#include "kernels.h"
+#include "runtime.h"
+
+namespace rew {
+
+// Experts whose table entries one metadata launch writes (from its
+// kernel arguments, so no host staging buffer is involved).
+constexpr int kMetaChunk = 32;
+
+struct MoeMetaChunk {
+  int first, count, n;
+  int32_t ids[kMetaChunk];
+  const void* p[6][kMetaChunk];
+};
+
+__global__ void __launch_bounds__(64) moe_meta_kernel(MoeMetaChunk ch, int32_t* members,
+                                                      const void** tables) {
+  const int i = threadIdx.x;
+  if (i >= ch.count) return;
+  members[ch.first + i] = ch.ids[i];
+#pragma unroll
+  for (int j = 0; j < 6; ++j) tables[(size_t)j * ch.n + ch.first + i] = ch.p[j][i];
+}
+
+__global__ void __launch_bounds__(256) moe_member_of_kernel(const int32_t* members, int n,
+                                                            int E, int32_t* member_of) {
+  for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < E; e += gridDim.x * blockDim.x) {
+    int m = -1;
+    for (int i = 0; i < n; ++i)
+      if (members[i] == e) {
+        m = i;
+        break;
+      }
+    member_of[e] = m;
+  }
+}
+
+namespace {
+
+struct Layout {
+  size_t member_of, members, tables, route, hbuf, ybuf, total;
+};
+
+Layout layout_of(const RoutedFfn& a) {
+  auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  const size_t R = (size_t)a.T * (size_t)a.k;
+  Layout L;
+  size_t o = 0;
+  L.member_of = o;
+  o += up((size_t)a.E * 4);
+  L.members = o;
+  o += up((size_t)a.n * 4);
+  L.tables = o;
+  o += up((size_t)a.n * 6 * sizeof(void*));
+  L.route = o;
+  o += up((2 * ((size_t)a.n + 1) + 2 * R) * 4);
+  L.hbuf = o;
+  o += up(R * (size_t)a.I * 2);
+  L.ybuf = o;
+  o += up(R * (size_t)a.H * 2);
+  L.total = o;
+  return L;
+}
+
+// The two grouped GEMMs: SwiGLU over x's routed rows, down projection over
+// the packed hidden rows (operand tables and outputs filled in by the caller).
+void gemm_args(const RoutedFfn& a, GemmArgs* gs, GemmArgs* gd) {
+  *gs = GemmArgs{};
+  *gd = GemmArgs{};
+  for (GemmArgs* g : {gs, gd}) {
+    g->dtype = REW_DT_BFLOAT16;
+    g->c_dtype = REW_DT_BFLOAT16;
+    g->batch = 1;
+    g->a_sk = 1;
+    g->b_sn = 1;
+  }
+  gs->a = a.x;
+  gs->M = a.T;
+  gs->K = a.H;
+  gs->N = a.I;
+  gs->a_sm = a.x_rs;
+  gs->b_sk = a.I;
+  gs->c_sm = a.I;
+  gs->epi = EPI_SWIGLU;
+  gd->M = a.T * a.k;
+  gd->K = a.I;
+  gd->N = a.H;
+  gd->a_sm = a.I;
+  gd->b_sk = a.H;
+  gd->c_sm = a.H;
+  gd->epi = EPI_BIAS;
+}
+
+bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
+size_t routed_ffn_scratch_bytes(const RoutedFfn& a) { return layout_of(a).total; }
+
+void routed_ffn_check(const RoutedFfn& a) {
+  auto bad = [](const std::string& m) { invalid("routed MoE FFN: " + m); };
+  if (a.T < 0 || a.H <= 0 || a.I <= 0) bad("tokens must be >= 0, hidden and ffn > 0");
+  if (a.H % 8 || a.I % 8) bad("hidden and ffn must be multiples of 8");
+  if (a.k < 1 || a.k > kMoeMaxK) bad("k must be in 1.." + std::to_string(kMoeMaxK));
+  if (a.E < 1) bad("router_width must be positive");
+  if (a.n < 1 || a.n > a.E) bad("n_experts must be in 1..router_width");
+  if (a.T * (int64_t)a.k >= ((int64_t)1 << 31)) bad("tokens * k must be below 2^31");
+  if (!a.expert) bad("null expert_ids");
+  for (int i = 0; i < a.n; ++i) {
+    if (a.expert[i] < 0 || a.expert[i] >= a.E)
+      bad("expert id " + std::to_string(a.expert[i]) + " outside [0, router_width)");
+    for (int j = 0; j < i; ++j)
+      if (a.expert[j] == a.expert[i])
+        bad("expert id " + std::to_string(a.expert[i]) + " repeated");
+  }
+  static const char* kTable[6] = {"gate_w", "up_w", "gate_b", "up_b", "down_w", "down_b"};
+  for (int j = 0; j < 6; ++j) {
+    if (!a.ptr[j]) bad(std::string("null ") + kTable[j] + " table");
+    for (int i = 0; i < a.n; ++i)
+      if (!a.ptr[j][i] || !al16(a.ptr[j][i]))
+        bad(std::string(kTable[j]) + "[" + std::to_string(i) +
+            "] is null or not 16-byte aligned");
+  }
+  if (a.T == 0) return;
+  if (!a.x || !a.start || !a.topi || !a.topw || !a.out) bad("null device pointer");
+  if (!al16(a.x) || !al16(a.start) || !al16(a.out)) bad("rows must be 16-byte aligned");
+  if (a.x_rs < a.H || a.x_rs % 8 || a.start_rs < a.H || a.start_rs % 8)
+    bad("row strides must be >= hidden and multiples of 8 elements");
+  GemmArgs gs, gd;
+  gemm_args(a, &gs, &gd);
+  void* const rows = reinterpret_cast<void*>(uintptr_t(4096));  // scratch rows are aligned
+  gs.c = rows;
+  gd.a = rows;
+  gd.c = rows;
+  if (!gemm_grouped_ok(gs) || !gemm_grouped_ok(gd))
+    bad("the expert GEMMs exceed the grouped kernel's 32-bit operand extents");
+}
+
+void run_routed_ffn(Ctx* c, const RoutedFfn& a, void* scratch) {
+  const Layout L = layout_of(a);
+  uint8_t* s = static_cast<uint8_t*>(scratch);
+  int32_t* member_of = reinterpret_cast<int32_t*>(s + L.member_of);
+  int32_t* members = reinterpret_cast<int32_t*>(s + L.members);
+  const void** tables = reinterpret_cast<const void**>(s + L.tables);
+  int32_t* route = reinterpret_cast<int32_t*>(s + L.route);
+  const int n = a.n;
+  const int64_t R = a.T * a.k;
+
+  // (profile names are built only while profiling: the allocation-free
+  // entry point runs this sequence without touching the host heap)
+  if (c->profiling) prof_begin(c, "moe_tables{E" + std::to_string(n) + "}");
+  for (int first = 0; first < n; first += kMetaChunk) {
+    MoeMetaChunk ch;
+    std::memset(&ch, 0, sizeof ch);
+    ch.first = first;
+    ch.count = std::min(kMetaChunk, n - first);
+    ch.n = n;
+    for (int i = 0; i < ch.count; ++i) {
+      ch.ids[i] = a.expert[first + i];
+      for (int j = 0; j < 6; ++j) ch.p[j][i] = a.ptr[j][first + i];
+    }
+    hipLaunchKernelGGL(moe_meta_kernel, dim3(1), dim3(64), 0, c->stream, ch, members, tables);
+    REW_HIP(hipGetLastError());
+  }
+  hipLaunchKernelGGL(moe_member_of_kernel, dim3((unsigned)((a.E + 255) / 256)), dim3(256), 0,
+                     c->stream, (const int32_t*)members, n, a.E, member_of);
+  REW_HIP(hipGetLastError());
+  prof_end(c);
+
+  MoeRouteArgs ra;
+  ra.topi = a.topi;
+  ra.T = a.T;
+  ra.k = a.k;
+  ra.E = a.E;
+  ra.member_of = member_of;
+  ra.members = members;
+  ra.n_members = n;
+  ra.tile_m = 256;
+  ra.off = route;
+  ra.mt_start = route + (n + 1);
+  ra.perm = route + 2 * (n + 1);
+  ra.slot_of = route + 2 * (n + 1) + R;
+  if (c->profiling)
+    prof_begin(c, "moe_route{" + std::to_string(a.T) + "x" + std::to_string(a.k) + ",E" +
+                      std::to_string(n) + "}");
+  launch_moe_route(ra, c->stream);
+  prof_end(c);
+
+  GemmArgs gs, gd;
+  gemm_args(a, &gs, &gd);
+  gs.c = s + L.hbuf;
+  gd.a = s + L.hbuf;
+  gd.c = s + L.ybuf;
+  GroupArgs ga;
+  ga.off = ra.off;
+  ga.mt_start = ra.mt_start;
+  ga.n_groups = n;
+  ga.max_mtiles = (R + 255) / 256 + n;
+  ga.rows = ra.perm;
+  ga.b = tables;
+  ga.b2 = tables + n;
+  ga.bias = tables + 2 * n;
+  ga.bias2 = tables + 3 * n;
+  ga.dual_span = 0;
+  for (int i = 0; i < n; ++i) {
+    const int64_t d = (int64_t)((uintptr_t)a.ptr[1][i] - (uintptr_t)a.ptr[0][i]);
+    ga.dual_span = std::max(ga.dual_span, d < 0 ? -d : d);
+  }
+  if (c->profiling) {
+    char nm[160];
+    std::snprintf(nm, sizeof nm, "moe_gemm_swiglu[%d,%lld,%lld,%lld]", n, (long long)R,
+                  (long long)a.I, (long long)a.H);
+    prof_begin(c, nm);
+  }
+  launch_gemm_grouped(gs, ga, c->stream);
+  prof_end(c);
+  ga.rows = nullptr;
+  ga.b = tables + 4 * n;
+  ga.b2 = nullptr;
+  ga.bias = tables + 5 * n;
+  ga.bias2 = nullptr;
+  if (c->profiling) {
+    char nm[160];
+    std::snprintf(nm, sizeof nm, "moe_gemm_down[%d,%lld,%lld,%lld]", n, (long long)R,
+                  (long long)a.H, (long long)a.I);
+    prof_begin(c, nm);
+  }
+  launch_gemm_grouped(gd, ga, c->stream);
+  prof_end(c);
+
+  MoeCombineArgs ca;
+  ca.prev = (const uint16_t*)a.start;
+  ca.prev_rs = a.start_rs;
+  ca.y = (const uint16_t*)gd.c;
+  ca.topw = a.topw;
+  ca.topi = a.topi;
+  ca.slot_of = ra.slot_of;
+  ca.member_of = member_of;
+  ca.T = a.T;
+  ca.H = a.H;
+  ca.k = a.k;
+  ca.E = a.E;
+  ca.out = (uint16_t*)a.out;
+  if (c->profiling)
+    prof_begin(c, "moe_combine{" + std::to_string(a.T) + "x" + std::to_string(a.H) + "}");
+  launch_moe_combine(ca, c->stream);
+  prof_end(c);
+  c->stats.kernels_launched += 5 + (n + kMetaChunk - 1) / kMetaChunk;
+  c->stats.fused_groups += 4;
+}
+
+}  // namespace rew
+
+using namespace rew;
+
+namespace {
+
+RoutedFfn from_abi(const rew_mi355x_moe_args* p) {
+  if (!p) invalid("routed MoE FFN: null args");
+  RoutedFfn a;
+  a.x = p->x;
+  a.x_rs = p->x_row_stride;
+  a.start = p->start;
+  a.start_rs = p->start_row_stride;
+  a.topi = p->top_ids;
+  a.topw = p->top_weights;
+  a.T = p->tokens;
+  a.H = p->hidden;
+  a.I = p->ffn;
+  a.k = p->k;
+  a.E = p->router_width;
+  a.n = p->n_experts;
+  a.expert = p->expert_ids;
+  a.ptr[0] = p->gate_w;
+  a.ptr[1] = p->up_w;
+  a.ptr[2] = p->gate_b;
+  a.ptr[3] = p->up_b;
+  a.ptr[4] = p->down_w;
+  a.ptr[5] = p->down_b;
+  a.out = p->out;
+  return a;
+}
+
+Ctx* ctx_of(rew_mi355x_ctx* ctx) {
+  if (!ctx) invalid("null context");
+  return reinterpret_cast<Ctx*>(ctx);
+}
+
+}  // namespace
+
+extern "C" int rew_mi355x_moe_routed_ffn(rew_mi355x_ctx* ctx, const rew_mi355x_moe_args* args) {
+  return guarded([&] {
+    Ctx* c = ctx_of(ctx);
+    const RoutedFfn a = from_abi(args);
+    routed_ffn_check(a);
+    std::lock_guard<std::recursive_mutex> g(c->mu);
+    REW_HIP(hipSetDevice(c->ordinal));
+    Shape s;
+    s.rank = 1;
+    s.d[0] = (int64_t)routed_ffn_scratch_bytes(a);
+    Tensor* w = new_tensor(c, kU8, s);
+    w->plan_dead = true;
+    try {
+      tensor_alloc(w);
+      run_routed_ffn(c, a, w->data());
+    } catch (...) {
+      maybe_destroy(w);
+      throw;
+    }
+    // stream-ordered: the block is reused only by work enqueued after this
+    maybe_destroy(w);
+  });
+}

@@ -17,23 +17,7 @@ namespace rew {
 
 static thread_local std::string g_last_error;
 
-template <class F>
-static int guarded(F&& f) {
-  try {
-    f();
-    g_last_error.clear();
-    return REW_MI355X_OK;
-  } catch (const Error& e) {
-    g_last_error = e.what();
-    return e.code;
-  } catch (const std::bad_alloc&) {
-    g_last_error = "host out of memory";
-    return REW_MI355X_ERR_OOM;
-  } catch (const std::exception& e) {
-    g_last_error = e.what();
-    return REW_MI355X_ERR_INVALID;
-  }
-}
+void set_last_error(const std::string& msg) { g_last_error = msg; }
 
 // ---- live handle registry ---------------------------------------------------------
 
@@ -387,6 +371,45 @@ int rew_mi355x_to_host(rew_mi355x_buf* buf, void* host, int64_t nbytes) {
     REW_HIP(hipMemcpyAsync(host, t->data(), (size_t)nbytes, hipMemcpyDeviceToHost,
                            c->stream));
     REW_HIP(hipStreamSynchronize(c->stream));
+  });
+}
+
+int rew_mi355x_alloc(rew_mi355x_ctx* ctx, int dtype, const int64_t* shape, int rank,
+                     rew_mi355x_buf** out) {
+  return guarded([&] {
+    Ctx* c = as_ctx(ctx);
+    if (!out) invalid("alloc: null out_buf");
+    if (dtype < 0 || dtype >= kNumDT) invalid("alloc: unknown dtype code");
+    if (rank < 0 || rank > kMaxRank) invalid("alloc: rank must be in 0..8");
+    if (rank > 0 && !shape) invalid("alloc: null shape");
+    std::vector<int64_t> v(shape, shape + rank);
+    for (auto d : v)
+      if (d < 0) invalid("alloc: negative dimension");
+    Shape s(v);
+    std::lock_guard<std::recursive_mutex> g(c->mu);
+    REW_HIP(hipSetDevice(c->ordinal));
+    Tensor* t = new_tensor(c, dtype, s);
+    try {
+      tensor_alloc(t);
+    } catch (...) {
+      maybe_destroy(t);
+      throw;
+    }
+    t->ext = 1;
+    *out = reinterpret_cast<rew_mi355x_buf*>(t);
+  });
+}
+
+int rew_mi355x_buf_device_ptr(rew_mi355x_buf* buf, void** out_ptr) {
+  return guarded([&] {
+    Tensor* t = check_handle(buf, "buf_device_ptr");
+    if (!out_ptr) invalid("buf_device_ptr: null out_ptr");
+    Ctx* c = t->ctx;
+    std::lock_guard<std::recursive_mutex> g(c->mu);
+    REW_HIP(hipSetDevice(c->ordinal));
+    if (t->prod) flush(c);
+    if (!t->st) invalid("buf_device_ptr: tensor has no data (an earlier flush failed)");
+    *out_ptr = t->data();
   });
 }
 

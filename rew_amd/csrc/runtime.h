@@ -15,6 +15,7 @@ namespace rew {
 
 struct Ctx;
 struct Node;
+struct RoutedFfn;
 
 // A device allocation shared by every tensor that aliases it (a reshape of
 // a materialized tensor aliases its source).
@@ -139,6 +140,33 @@ void upload_async(Ctx* c, void* dst, const void* src, size_t bytes);
 // Launch bracketing for profiling: call before/after each kernel launch.
 void prof_begin(Ctx* c, const std::string& name);
 void prof_end(Ctx* c);
+
+// Enqueues the routed-expert FFN `a` (checked with routed_ffn_check) on the
+// context's stream, with `scratch` as its working memory (moe_ffn.hip).
+void run_routed_ffn(Ctx* c, const RoutedFfn& a, void* scratch);
+
+// ABI-edge error plumbing (runtime.cpp): the thread-local message behind
+// rew_mi355x_last_error().
+void set_last_error(const std::string& msg);
+
+// Runs f, turning exceptions into an ABI status and the last-error message.
+template <class F>
+int guarded(F&& f) {
+  try {
+    f();
+    set_last_error(std::string());
+    return REW_MI355X_OK;
+  } catch (const Error& e) {
+    set_last_error(e.what());
+    return e.code;
+  } catch (const std::bad_alloc&) {
+    set_last_error("host out of memory");
+    return REW_MI355X_ERR_OOM;
+  } catch (const std::exception& e) {
+    set_last_error(e.what());
+    return REW_MI355X_ERR_INVALID;
+  }
+}
 
 // ---- graph (ops.cpp / lower.cpp) ----------------------------------------------
 // Records op `name` (validating and deriving outputs exactly like

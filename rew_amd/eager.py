@@ -295,6 +295,63 @@ def toHost(t: Tensor) -> np.ndarray:
     return out
 
 
+def empty(dtype: DType, shape: Sequence[int], device: Device | None = None) -> Tensor:
+    """A new tensor with undefined contents (rew_mi355x_alloc), to be written
+    on the device by a caller holding its address (``devicePtr``)."""
+    d = device or defaultDevice()
+    shp = tuple(int(s) for s in shape)
+    cshape = (C.c_int64 * max(1, len(shp)))(*shp)
+    h = C.c_void_p()
+    _check(_lib.load().rew_mi355x_alloc(context(d), int(dtype), cshape, len(shp), C.byref(h)))
+    return Tensor(h.value, DType(dtype), shp, d)
+
+
+def devicePtr(t: Tensor) -> int:
+    """Device address of t's storage (rew_mi355x_buf_device_ptr; flushes t's producer)."""
+    if t.handle is None:
+        raise BufferReleasedError("devicePtr: tensor already released")
+    p = C.c_void_p()
+    _check(_lib.load().rew_mi355x_buf_device_ptr(t.handle, C.byref(p)))
+    return int(p.value or 0)
+
+
+def _moe_args(x: Tensor, start: Tensor, topWeights: Tensor, topIndices: Tensor,
+              experts: Sequence, expertIds: Sequence[int], routerWidth: int, out: Tensor):
+    """Fills rew_mi355x_moe_args from backend tensors; returns (args, keepalive)."""
+    T, H = x.shape
+    ffn = experts[0].gateProj.weight.shape[1]
+    n = len(experts)
+    tables = []
+    for attr, part in (("gateProj", "weight"), ("upProj", "weight"), ("gateProj", "bias"),
+                       ("upProj", "bias"), ("downProj", "weight"), ("downProj", "bias")):
+        tables.append((C.c_void_p * n)(*[devicePtr(getattr(getattr(e, attr), part))
+                                        for e in experts]))
+    ids = (C.c_int32 * n)(*[int(i) for i in expertIds])
+    a = _lib.MoeArgs()
+    a.x, a.x_row_stride = devicePtr(x), H
+    a.start, a.start_row_stride = devicePtr(start), H
+    a.top_ids, a.top_weights = devicePtr(topIndices), devicePtr(topWeights)
+    a.tokens, a.hidden, a.ffn = T, H, ffn
+    a.k, a.router_width, a.n_experts = topIndices.shape[1], int(routerWidth), n
+    a.expert_ids = C.cast(ids, C.c_void_p)
+    (a.gate_w, a.up_w, a.gate_b, a.up_b, a.down_w, a.down_b) = [C.cast(t, C.c_void_p)
+                                                                for t in tables]
+    a.out = devicePtr(out)
+    return a, (tables, ids)
+
+
+def moeRoutedFfn(x: Tensor, start: Tensor, topWeights: Tensor, topIndices: Tensor,
+                 experts: Sequence, expertIds: Sequence[int], routerWidth: int) -> Tensor:
+    """The routed experts of DeepSeekMoE.forward on the router's top-k
+    (rew_mi355x_moe_routed_ffn): start + the chain of routed expert FFNs,
+    each on its routed tokens only.  ``experts`` hold gateProj / upProj /
+    downProj Linears over bf16 tensors."""
+    out = empty(DType.BFLOAT16, x.shape, x.device)
+    a, keep = _moe_args(x, start, topWeights, topIndices, experts, expertIds, routerWidth, out)
+    _check(_lib.load().rew_mi355x_moe_routed_ffn(context(x.device), C.byref(a)))
+    return out
+
+
 def toHostF32(t: Tensor) -> np.ndarray:
     a = toHost(t)
     if t.dtype == DType.BFLOAT16:

@@ -65,3 +65,22 @@ def test_error_paths_without_device():
     assert b"released" in lib.rew_mi355x_last_error()
     rc = lib.rew_mi355x_execute(None, b"add", None, 0, None, None, 0, None, 0, None)
     assert rc == 1 and b"null context" in lib.rew_mi355x_last_error()
+    rc = lib.rew_mi355x_alloc(None, 11, None, 0, C.byref(C.c_void_p()))
+    assert rc == 1 and b"null context" in lib.rew_mi355x_last_error()
+    rc = lib.rew_mi355x_buf_device_ptr(C.c_void_p(0x1234), C.byref(C.c_void_p()))
+    assert rc == 5 and b"released" in lib.rew_mi355x_last_error()
+    rc = lib.rew_mi355x_moe_routed_ffn(None, None)
+    assert rc == 1 and b"null context" in lib.rew_mi355x_last_error()
+
+
+@pytest.mark.parametrize("ordinal", [-1, 64, 1 << 30])
+def test_bad_device_ordinal(ordinal):
+    """An ordinal outside the device table is refused before any HIP call,
+    as rew's selectDevice refuses an ordinal past the client's devices
+    (src/rew/eager.nim:160-172)."""
+    from rew_amd import _lib
+    lib = _lib.load()
+    ctx = C.c_void_p()
+    assert lib.rew_mi355x_init(ordinal, C.byref(ctx)) == 1  # REW_MI355X_ERR_INVALID
+    assert b"ordinal" in lib.rew_mi355x_last_error()
+    assert not ctx.value

@@ -142,27 +142,41 @@ def test_moe_routing_weights(gpu, oracle):
     assert np.all(np.diff(tw, axis=1) <= 0)
 
 
-@pytest.mark.parametrize("which", ["down", "gate"])
+class _TransposedLinear(nn.Linear):
+    """Linear.forward over a weight stored [out, in]: the transposed view is
+    made inside forward, so it is a pending view nobody holds."""
+
+    def forward(self, x):
+        xw = O.matmul(x, O.transpose(self.weight, [1, 0]))
+        return O.add(xw, O.broadcastTo(self.bias, xw.shape, [1]))
+
+
+@pytest.mark.parametrize("which", ["down", "gate", "held"])
 def test_moe_unlowerable_weight_falls_back(gpu, oracle, which):
-    """Expert weights given as transposed views.  The down weight keeps its
-    bias-GEMM plan, so the chain matches, but the grouped GEMM cannot read
-    the weight in place: the chain must not be claimed by the MoE lowering,
-    and runs through the ordinary fused GEMMs.  A transposed gate weight
-    has no SwiGLU plan at all, so that expert splits the chain into two
-    routed groups.  Either way the flush succeeds with the op-by-op values."""
+    """Expert 3's gate or down weight seen through a transposed view.
+    * down / gate: the view is made inside forward, pending and unheld.
+      Expert 3 keeps its SwiGLU and bias-GEMM plans, so the chain matches,
+      but the grouped GEMM cannot read the view in place: the chain must not
+      be claimed by the MoE lowering and runs through the ordinary GEMMs.
+    * held: a view the caller holds is materialized densely, so the whole
+      chain stays one routed group.
+    Each way the flush succeeds with the op-by-op values."""
     moe, host = build_moe(oracle, 64, 128, 64, 8, 2, 1, 0x5EED0305)
     ex = moe.routedExperts[3]
-    attr = "downProj" if which == "down" else "gateProj"
-    w = host["routed"][3][4 if which == "down" else 0]
-    setattr(ex, attr, nn.Linear(O.transpose(E.fromHost(np.ascontiguousarray(w.T),
-                                                       DType.BFLOAT16), [1, 0]),
-                                getattr(ex, attr).bias))
+    attr = "gateProj" if which == "gate" else "downProj"
+    w = host["routed"][3][0 if which == "gate" else 4]
+    wt = E.fromHost(np.ascontiguousarray(w.T), DType.BFLOAT16)
+    bias = getattr(ex, attr).bias
+    if which == "held":
+        setattr(ex, attr, nn.Linear(O.transpose(wt, [1, 0]), bias))
+    else:
+        setattr(ex, attr, _TransposedLinear(wt, bias))
     xt = E.fromHost(host["x"], DType.BFLOAT16)
     E.profileBegin()
     got = E.toHostF32(moe.forward(xt))
     prof = E.profileEnd()
     groups = sum(c for n, c, _ in prof if n.startswith("moe_gemm_swiglu"))
-    assert groups == (0 if which == "down" else 2), [n for n, _, _ in prof]
+    assert groups == (1 if which == "held" else 0), [n for n, _, _ in prof]
     E.setMode(1)
     try:
         dense = E.toHostF32(moe.forward(xt))
@@ -172,3 +186,45 @@ def test_moe_unlowerable_weight_falls_back(gpu, oracle, which):
     want, _, _ = oracle.deepseek_moe(host["x"], host["shared"], host["routed"], host["wr"],
                                      host["br"], 2)
     assert np.linalg.norm(got - want) / np.linalg.norm(want) <= 2e-2
+
+
+@pytest.mark.parametrize("T", [256, 37])
+def test_direct_routed_ffn_equals_graph_lowering(gpu, oracle, T):
+    """rew_mi355x_moe_routed_ffn on the router's top-k and the shared
+    experts' sum gives the same bits as the deferred graph's lowering of
+    DeepSeekMoE.forward's dense chain (both run the same kernels)."""
+    moe, host = build_moe(oracle, T, 256, 128, 16, 4, 2, 0x5EED0405 + T)
+    xt = E.fromHost(host["x"], DType.BFLOAT16)
+    graph = E.toHost(moe.forward(xt))
+    start = O.add(moe.sharedExperts[0].forward(xt), moe.sharedExperts[1].forward(xt))
+    topW, topI = moe.route(xt)
+    E.profileBegin()
+    direct = E.toHost(E.moeRoutedFfn(xt, start, topW, topI, moe.routedExperts,
+                                     list(range(16)), 16))
+    names = [n for n, _, _ in E.profileEnd()]
+    assert any(n.startswith("moe_gemm_swiglu") for n in names), names
+    np.testing.assert_array_equal(direct, graph)
+    # a chain of some experts only: the others' routed rows add nothing
+    sub = [3, 7, 11]
+    part = E.toHostF32(E.moeRoutedFfn(xt, start, topW, topI,
+                                      [moe.routedExperts[e] for e in sub], sub, 16))
+    tw, ti = E.toHost(topW), E.toHost(topI)
+    want = E.toHostF32(start)
+    for e in sub:
+        ex = host["routed"][e]
+        w = np.where(ti == e, tw, 0).sum(1, dtype=np.float32)[:, None]
+        y = oracle.gated_ffn(host["x"], *ex, True)
+        want = oracle.round_bf16(want + oracle.round_bf16(y * w))
+    err = np.linalg.norm(part - want) / np.linalg.norm(want)
+    assert err <= 2e-2
+
+
+def test_direct_routed_ffn_rejects_bad_arguments(gpu, oracle):
+    moe, host = build_moe(oracle, 16, 128, 64, 8, 2, 0, 0x5EED0505)
+    xt = E.fromHost(host["x"], DType.BFLOAT16)
+    topW, topI = moe.route(xt)
+    start = O.zerosLike(xt)
+    with pytest.raises(E.EagerError, match="repeated"):
+        E.moeRoutedFfn(xt, start, topW, topI, moe.routedExperts[:2], [1, 1], 8)
+    with pytest.raises(E.EagerError, match="outside"):
+        E.moeRoutedFfn(xt, start, topW, topI, moe.routedExperts[:1], [8], 8)

@@ -308,3 +308,26 @@ def test_small_constants_share_one_upload(gpu):
     del ts, a, b
     E.clearEagerCache()
     assert float(E.toHost(O.scalarF32(3.0))) == 3.0
+
+
+def test_allocation_failure_is_an_error(gpu):
+    """A device allocation the HBM cannot hold fails with ERR_OOM and a
+    message naming the size; the context keeps working afterwards."""
+    with pytest.raises(E.EagerError, match="device allocation of .* bytes failed"):
+        E.empty(DType.FLOAT32, [1 << 40])
+    t = E.empty(DType.FLOAT32, [1024])
+    p = E.devicePtr(t)
+    assert p and p % 256 == 0
+    x = np.arange(8, dtype=np.float32)
+    np.testing.assert_array_equal(host(O.add(dev(x), dev(x))), x + x)
+
+
+def test_ordinal_past_visible_devices(gpu):
+    """mi355x:n with n >= the visible device count is refused like rew's
+    selectDevice (src/rew/eager.nim:160-172): ERR_DEVICE, naming the count."""
+    import ctypes as C
+    from rew_amd import _lib
+    lib = _lib.load()
+    ctx = C.c_void_p()
+    assert lib.rew_mi355x_init(E.deviceCount(), C.byref(ctx)) == 3
+    assert b"not present" in lib.rew_mi355x_last_error()
