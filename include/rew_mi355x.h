@@ -258,6 +258,22 @@ typedef struct rew_mi355x_moe_args {
  * the direct form for hosts that already hold the router's top-k. */
 int rew_mi355x_moe_routed_ffn(rew_mi355x_ctx* ctx, const rew_mi355x_moe_args* args);
 
+/* rew_mi355x_moe_routed_ffn without any allocation: no hipMalloc / hipFree,
+ * no caching-allocator block and no host staging buffer.  Its working memory
+ * is a static device array of 64 MiB per GPU (part of this library's code
+ * object, held until the process ends); a call needing more (about
+ * tokens * k * (hidden + ffn) * 2 bytes) fails with REW_MI355X_ERR_INVALID
+ * before anything is launched.  Same arguments and bit-identical results.
+ * Every call on one GPU shares that GPU's array, which keeps the last
+ * call's contents (no call reads what it has not written first).  Calls
+ * are ordered on the context's single stream; work that overlaps a call on
+ * the same GPU and uses the array from elsewhere (e.g. a captured copy of
+ * these launches replayed on another stream meanwhile) races with it.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory -- code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation. */
+int rew_mi355x_moe_routed_ffn_noalloc(rew_mi355x_ctx* ctx, const rew_mi355x_moe_args* args);
+
 /* ---- rew's input generators (host) --------------------------------------
  * Threefry-2x32 with 4 rounds and the Box-Muller / 24-bit uniform samplers,
  * used to build the synthetic inputs every config is quoted on.

@@ -48,6 +48,7 @@ SIGNATURES = {
                                            C.POINTER(C.c_int64), C.POINTER(C.c_double)]),
     "rew_mi355x_stream": (C.c_int, [_c_ctx, C.POINTER(C.c_void_p)]),
     "rew_mi355x_moe_routed_ffn": (C.c_int, [_c_ctx, C.c_void_p]),
+    "rew_mi355x_moe_routed_ffn_noalloc": (C.c_int, [_c_ctx, C.c_void_p]),
     "rew_mi355x_rng_split": (None, [C.c_uint32, C.c_uint32, C.c_int, C.POINTER(C.c_uint32)]),
     "rew_mi355x_rng_fold_in": (None, [C.c_uint32, C.c_uint32, C.c_uint64,
                                       C.POINTER(C.c_uint32)]),

@@ -270,6 +270,26 @@ void run_routed_ffn(Ctx* c, const RoutedFfn& a, void* scratch) {
   c->stats.fused_groups += 4;
 }
 
+// Working memory of rew_mi355x_moe_routed_ffn_noalloc: one array per GPU,
+// part of this library's code object, held until the process ends.  Host
+// code never passes `scratch` itself (on the host it names a stand-in, not
+// device memory): noalloc_scratch_lookup() resolves its device address once
+// per device at rew_mi355x_init and the context keeps it.
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+void* noalloc_scratch_lookup(std::string* err) {
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p) {
+    (void)hipGetLastError();
+    *err = std::string("allocation-free MoE entry point unavailable: hipGetSymbolAddress "
+                       "failed (") + hipGetErrorString(e) + ")";
+    return nullptr;
+  }
+  return p;
+}
+
 }  // namespace rew
 
 using namespace rew;
@@ -330,5 +350,24 @@ extern "C" int rew_mi355x_moe_routed_ffn(rew_mi355x_ctx* ctx, const rew_mi355x_m
     }
     // stream-ordered: the block is reused only by work enqueued after this
     maybe_destroy(w);
+  });
+}
+
+extern "C" int rew_mi355x_moe_routed_ffn_noalloc(rew_mi355x_ctx* ctx,
+                                                 const rew_mi355x_moe_args* args) {
+  return guarded([&] {
+    Ctx* c = ctx_of(ctx);
+    const RoutedFfn a = from_abi(args);
+    routed_ffn_check(a);
+    const size_t need = routed_ffn_scratch_bytes(a);
+    if (need > kNoAllocScratchBytes)
+      invalid("routed MoE FFN (allocation-free): needs " + std::to_string(need) +
+              " bytes of working memory, the static scratch holds " +
+              std::to_string(kNoAllocScratchBytes) +
+              "; call rew_mi355x_moe_routed_ffn for this size");
+    std::lock_guard<std::recursive_mutex> g(c->mu);
+    REW_HIP(hipSetDevice(c->ordinal));
+    if (!c->noalloc_scratch) fail(REW_MI355X_ERR_DEVICE, c->noalloc_error);
+    run_routed_ffn(c, a, c->noalloc_scratch);
   });
 }

@@ -274,6 +274,8 @@ int rew_mi355x_init(int ordinal, rew_mi355x_ctx** out) {
       c->alloc.ordinal = ordinal;
       c->jit_hits_base = jit_cache_hits();
       REW_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+      // once per device, with the device current
+      c->noalloc_scratch = noalloc_scratch_lookup(&c->noalloc_error);
       if (const char* s = std::getenv("REW_MI355X_EAGER_SYNC"))
         if (s[0] == '1') c->mode = REW_MI355X_MODE_OP_BY_OP;
       if (const char* s = std::getenv("REW_MI355X_NO_PATTERNS"))

@@ -121,6 +121,11 @@ struct Ctx {
   std::vector<std::pair<std::string, std::pair<int64_t, double>>> prof_summary;
   std::vector<hipEvent_t> event_pool;
   int order_counter = 0;
+  // device address of the static scratch array of the allocation-free
+  // entry point on this context's device (null, with the reason, if the
+  // lookup at init failed)
+  void* noalloc_scratch = nullptr;
+  std::string noalloc_error;
 };
 
 // ---- runtime services (runtime.cpp) -----------------------------------------
@@ -144,6 +149,9 @@ void prof_end(Ctx* c);
 // Enqueues the routed-expert FFN `a` (checked with routed_ffn_check) on the
 // context's stream, with `scratch` as its working memory (moe_ffn.hip).
 void run_routed_ffn(Ctx* c, const RoutedFfn& a, void* scratch);
+// With the context's device current: the device address of the static
+// scratch array (moe_ffn.hip), or null with *err set.
+void* noalloc_scratch_lookup(std::string* err);
 
 // ABI-edge error plumbing (runtime.cpp): the thread-local message behind
 // rew_mi355x_last_error().
