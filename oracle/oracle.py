@@ -246,7 +246,8 @@ def sdpa(q, k, v, causal, scale: float | None = None, mixed: bool = False) -> np
     """src/rew/nn/attention.nim:36-81 with GQA sharing (groupedqueryattention.nim:126-133).
     q [B,H,Sq,D], k/v [B,Hkv,Sk,D] as float arrays (bf16-valued when mixed).
     causal: False/0 unmasked, True/1 rew's makeCausalMask (i <= j visible),
-    2 the mirrored mask (i >= j visible)."""
+    2 the mirrored mask (i >= j visible), 3 / 4 the strict forms (i < j /
+    i > j visible); masked scores get -1e9 added."""
     q = np.ascontiguousarray(q, np.float32)
     k = np.ascontiguousarray(k, np.float32)
     v = np.ascontiguousarray(v, np.float32)

@@ -412,6 +412,8 @@ void orc_sdpa(const float* q, const float* k, const float* v, int64_t B, int64_t
           sf = sf * scale;
           if (causal == 1) sf = sf + ((i <= j) ? 0.0f : -1e9f);
           else if (causal == 2) sf = sf + ((i >= j) ? 0.0f : -1e9f);
+          else if (causal == 3) sf = sf + ((i < j) ? 0.0f : -1e9f);
+          else if (causal == 4) sf = sf + ((i > j) ? 0.0f : -1e9f);
           p[j] = sf;
         }
         float m = -INFINITY;

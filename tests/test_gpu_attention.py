@@ -111,9 +111,14 @@ def test_flash_matches_oracle(gpu, oracle, causal, B, H, Hkv, Sq, Sk, D):
     bf16_close(got, ref)
 
 
-@pytest.mark.parametrize("direction,code", [("LE", 1), ("GE", 2)])
-def test_flash_mask_directions(gpu, oracle, direction, code):
-    B, H, Hkv, S, D = 1, 4, 2, 320, 128
+@pytest.mark.parametrize("S", [300, 256])
+@pytest.mark.parametrize("direction,code", [("LE", 1), ("GE", 2), ("LT", 3), ("GT", 4)])
+def test_flash_mask_directions(gpu, oracle, direction, code, S):
+    """Every ordered mask direction: whole key tiles (S = 256) take the
+    diagonal-tile path on the tiles the mask cuts, a ragged last tile
+    (S = 300) the general path; the strict masks leave one row with no
+    visible key, which averages V."""
+    B, H, Hkv, D = 1, 4, 2, 128
     q, k, v = _qkv(oracle, 77, B, H, Hkv, S, S, D)
     g = H // Hkv
 

@@ -202,6 +202,30 @@ def test_sdpa_mixed_brute_force(oracle):
     assert rel(oracle.sdpa(q, k, v, 2), attn_bf(q, k, v, True)) > 0.05
 
 
+@pytest.mark.parametrize("code,visible", [(1, "le"), (2, "ge"), (3, "lt"), (4, "gt")])
+def test_sdpa_mask_directions(oracle, code, visible):
+    """Each ordered mask against brute force; a row with no visible key
+    (the last row under i < j, the first under i > j) softmaxes scores that
+    all round to -1e9, so it averages V."""
+    rng = np.random.default_rng(40 + code)
+    B, H, S, D = 1, 2, 9, 8
+    q, k, v = (rng.normal(0, 1, (B, H, S, D)).astype(np.float32) for _ in range(3))
+    sc = np.float32(1.0) / np.sqrt(np.float32(D))
+    i, j = np.indices((S, S))
+    vis = {"le": i <= j, "ge": i >= j, "lt": i < j, "gt": i > j}[visible]
+    want = np.zeros((B, H, S, D))
+    for h in range(H):
+        s = f32(f32(q[0, h].astype(np.float64) @ k[0, h].T.astype(np.float64)) * np.float64(sc))
+        s = f32(s + np.where(vis, 0.0, -1e9))
+        p = np.exp(s - s.max(1, keepdims=True))
+        want[0, h] = (p / p.sum(1, keepdims=True)) @ v[0, h]
+    got = oracle.sdpa(q, k, v, code)
+    assert rel(got, want) <= 1e-5
+    empty = np.where(~vis.any(1))[0]
+    for r in empty:
+        np.testing.assert_allclose(got[0, :, r], v[0].mean(1), rtol=1e-5, atol=1e-6)
+
+
 def _gqa_params(rng, E, nkv, hd, bias=0.2):
     p = {}
     for n, fo in [("q", E), ("k", nkv * hd), ("v", nkv * hd), ("o", E)]:
