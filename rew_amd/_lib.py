@@ -1,14 +1,51 @@
 """ctypes binding of librew_mi355x.so (declared in include/rew_mi355x.h).
 
-Loading fails loudly when the library is missing: there is no fallback
-execution path.
+The library is found the way rew's resolvePluginPath finds a plugin
+(src/rew/binaries/resolver.nim:22-78) and loading fails loudly when it is
+missing: there is no fallback execution path.  The library is one
+self-contained file (the run-time kernel compiler's headers are built in).
 """
 from __future__ import annotations
 
 import ctypes as C
+import os
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "librew_mi355x.so"
+LIB_NAME = "librew_mi355x.so"
+LIB_PATH = Path(__file__).resolve().parent / LIB_NAME  # the in-tree build
+
+
+class ResolveError(RuntimeError):
+    """No librew_mi355x.so where the resolution order looks."""
+
+
+def resolve_plugin_path() -> Path:
+    """resolvePluginPath for the mi355x target (resolver.nim:22-78):
+
+    1. REW_PJRT_PLUGIN_PATH, a list of directories separated by ':' -- the
+       first one holding librew_mi355x.so wins;
+    2. REW_BUILD=1 / true -- the in-tree build, which must exist;
+    3. the library next to this package (the in-tree build, or an
+       installed copy).
+
+    There is no step 4 (download and extract): the library is built from
+    this repository."""
+    explicit = os.environ.get("REW_PJRT_PLUGIN_PATH", "")
+    for d in explicit.split(os.pathsep):
+        d = d.strip()
+        if d and (Path(d) / LIB_NAME).is_file():
+            return Path(d) / LIB_NAME
+    if os.environ.get("REW_BUILD", "") in ("1", "true"):
+        if LIB_PATH.is_file():
+            return LIB_PATH
+        raise ResolveError(f"REW_BUILD=true but no built library at {LIB_PATH}: "
+                           "build it with `python -m rew_amd.build`")
+    if LIB_PATH.is_file():
+        return LIB_PATH
+    raise ResolveError(
+        f"{LIB_NAME} not found in REW_PJRT_PLUGIN_PATH ({explicit or 'unset'}) nor at "
+        f"{LIB_PATH}: build it with `python -m rew_amd.build` (there is no CPU fallback "
+        "for the mi355x backend)")
 
 # Every symbol include/rew_mi355x.h declares, with (restype, argtypes).
 _c_buf = C.c_void_p
@@ -79,18 +116,17 @@ class Stats(C.Structure):
 
 
 _lib = None
+loaded_path: Path | None = None
 
 
 def load() -> C.CDLL:
     """Returns the loaded library, raising if it has not been built."""
-    global _lib
+    global _lib, loaded_path
     if _lib is not None:
         return _lib
-    if not LIB_PATH.exists():
-        raise RuntimeError(
-            f"{LIB_PATH} is missing: build it with `python -m rew_amd.build` "
-            "(there is no CPU fallback for the mi355x backend)")
-    lib = C.CDLL(str(LIB_PATH))
+    path = resolve_plugin_path()
+    lib = C.CDLL(str(path))
+    loaded_path = path
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.restype = res

@@ -10,4 +10,5 @@ typedef __hip_internal::int32_t int32_t;
 typedef __hip_internal::uint32_t uint32_t;
 typedef __hip_internal::int64_t int64_t;
 typedef __hip_internal::uint64_t uint64_t;
-#include "../../include/rew_mi355x.h"
+// the public header, registered with hipRTC under this plain name
+#include "rew_mi355x.h"

@@ -84,3 +84,36 @@ def test_bad_device_ordinal(ordinal):
     assert lib.rew_mi355x_init(ordinal, C.byref(ctx)) == 1  # REW_MI355X_ERR_INVALID
     assert b"ordinal" in lib.rew_mi355x_last_error()
     assert not ctx.value
+
+
+def test_plugin_path_resolution(tmp_path, monkeypatch):
+    """The library is resolved like rew's resolvePluginPath
+    (src/rew/binaries/resolver.nim:22-78): REW_PJRT_PLUGIN_PATH directories
+    in order, then REW_BUILD, then the in-tree build."""
+    import shutil
+    from rew_amd import _lib
+    a, b = tmp_path / "a", tmp_path / "b"
+    a.mkdir()
+    b.mkdir()
+    shutil.copy(_lib.LIB_PATH, b / _lib.LIB_NAME)
+    monkeypatch.setenv("REW_PJRT_PLUGIN_PATH", f"{a}:{b}")
+    assert _lib.resolve_plugin_path() == b / _lib.LIB_NAME
+    monkeypatch.setenv("REW_PJRT_PLUGIN_PATH", str(a))
+    assert _lib.resolve_plugin_path() == _lib.LIB_PATH
+    monkeypatch.setenv("REW_BUILD", "true")
+    assert _lib.resolve_plugin_path() == _lib.LIB_PATH
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "missing" / _lib.LIB_NAME)
+    with pytest.raises(_lib.ResolveError, match="REW_BUILD=true"):
+        _lib.resolve_plugin_path()
+    monkeypatch.delenv("REW_BUILD")
+    with pytest.raises(_lib.ResolveError, match="not found"):
+        _lib.resolve_plugin_path()
+
+
+def test_library_carries_its_run_time_headers():
+    """The headers the run-time compiled kernels include are in the library
+    itself, so a lone copy of the .so needs no source tree."""
+    data = (ROOT / "rew_amd" / "librew_mi355x.so").read_bytes()
+    for name in ("vm_device.h", "rtc_prelude.h", "vm.h", "rew_mi355x.h"):
+        assert name.encode() in data
+    assert b"namespace vm" in data and b"Fused elementwise programs" in data

@@ -331,3 +331,42 @@ def test_ordinal_past_visible_devices(gpu):
     ctx = C.c_void_p()
     assert lib.rew_mi355x_init(E.deviceCount(), C.byref(ctx)) == 3
     assert b"not present" in lib.rew_mi355x_last_error()
+
+
+CHILD_LONE = r"""
+import sys
+import numpy as np
+sys.path.insert(0, sys.argv[1])
+from rew_amd import _lib, eager as E, ops as O, nn
+E.installEagerBackend(E.mi355x(0))
+x = np.linspace(-3, 3, 4096, dtype=np.float32).reshape(64, 64)
+t = E.fromHost(x)
+y = E.toHost(nn.silu(O.mul(O.add(t, t), t)))   # one fused program, compiled at run time
+s = E.stats()
+print(str(_lib.loaded_path), s["plan_cache_hits"], float(y.sum()))
+"""
+
+
+def test_lone_library_compiles_fused_kernels(gpu, tmp_path):
+    """A copy of librew_mi355x.so alone in a directory, found through
+    REW_PJRT_PLUGIN_PATH from another working directory, compiles fused
+    programs with its built-in headers (a compile failure would raise)."""
+    import os
+    import shutil
+    import subprocess
+    import sys
+    from pathlib import Path
+    from rew_amd import _lib
+    root = Path(__file__).resolve().parents[1]
+    shutil.copy(_lib.LIB_PATH, tmp_path / _lib.LIB_NAME)
+    env = dict(os.environ, REW_PJRT_PLUGIN_PATH=str(tmp_path))
+    env.pop("REW_MI355X_JIT", None)
+    r = subprocess.run([sys.executable, "-c", CHILD_LONE, str(root)], env=env, cwd=tmp_path,
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-3000:]
+    path, _, total = r.stdout.split()
+    assert path == str(tmp_path / _lib.LIB_NAME)
+    x = np.linspace(-3, 3, 4096, dtype=np.float32)
+    z = (x + x) * x
+    want = float((z / (1 + np.exp(-z))).sum())
+    assert abs(float(total) - want) <= 1e-3 * abs(want)
