@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define REW_MI355X_ABI_VERSION 1
+#define REW_MI355X_ABI_VERSION 2
 
 /* Status codes. */
 enum {
@@ -161,6 +161,32 @@ int rew_mi355x_execute_ex(rew_mi355x_ctx* ctx, const char* op,
                           rew_mi355x_buf** outs, int max_outs, int* n_outs,
                           int64_t* out_meta);
 
+/* Run one jit module: the StableHLO text rew's jit/lazy hand to PJRT
+ * (emitText of the traced module with its entry function renamed "main",
+ * src/rew/transform/jit.nim:178-185, src/rew/stablehlo/text.nim:1969-2025).
+ * The text is parsed and translated once into the graph nodes the eager
+ * ops record, cached under ordinal::jit_name::cache_key::hash(text), and
+ * instantiated over `inputs` on every call, so its ops join the deferred
+ * graph and lower through the same fused kernels.  `text_len` < 0 means
+ * NUL-terminated.  Inputs must match the module's argument types;
+ * `donate_idx` entries must index `inputs` (the buffers are not reused).
+ * Writes one new handle per func.return operand (one owner reference
+ * each) and, when `out_meta` is non-null, their dtype/rank/dims as
+ * rew_mi355x_execute_ex does.  Modules using an op outside the translated
+ * subset fail with REW_MI355X_ERR_UNSUPPORTED naming the op and line.
+ * Replaces: executeJit (src/rew/eager.nim:1782-1847): compileWithPersistentCache
+ * plus PjrtLoadedExecutable.execute. */
+int rew_mi355x_execute_jit(rew_mi355x_ctx* ctx, const char* jit_name,
+                           const char* cache_key, const char* module_text,
+                           int64_t text_len, rew_mi355x_buf* const* inputs,
+                           int n_inputs, const int* donate_idx, int n_donate,
+                           rew_mi355x_buf** outs, int max_outs, int* n_outs,
+                           int64_t* out_meta);
+
+/* Drop every cached jit module of the context (and its constants).
+ * Replaces: clearJitCache (src/rew/eager.nim:1778-1780). */
+int rew_mi355x_clear_jit_cache(rew_mi355x_ctx* ctx);
+
 /* Lower and launch every pending op (asynchronous; returns after enqueue).
  * No reference counterpart: the PJRT path executes every op at dispatch
  * (src/rew/eager.nim:1745-1754); this is the deferred-group boundary. */
@@ -192,6 +218,10 @@ typedef struct rew_mi355x_stats {
                             /* keyed by the program's binary signature; the */
                             /* analogue of rew's executable cache); counted */
                             /* for all contexts of the process since reset  */
+  int64_t jit_module_compiles; /* rew_mi355x_execute_jit calls that parsed  */
+                               /* and translated a module                   */
+  int64_t jit_module_hits;     /* rew_mi355x_execute_jit calls served by a  */
+                               /* cached module                             */
 } rew_mi355x_stats;
 
 int rew_mi355x_get_stats(rew_mi355x_ctx* ctx, rew_mi355x_stats* out);

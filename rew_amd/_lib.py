@@ -73,6 +73,11 @@ SIGNATURES = {
                                         C.POINTER(C.c_char_p), C.POINTER(C.c_char_p), C.c_int,
                                         C.POINTER(_c_buf), C.c_int, C.POINTER(C.c_int),
                                         C.POINTER(C.c_int64)]),
+    "rew_mi355x_execute_jit": (C.c_int, [_c_ctx, C.c_char_p, C.c_char_p, C.c_char_p, C.c_int64,
+                                         C.POINTER(_c_buf), C.c_int, C.POINTER(C.c_int),
+                                         C.c_int, C.POINTER(_c_buf), C.c_int,
+                                         C.POINTER(C.c_int), C.POINTER(C.c_int64)]),
+    "rew_mi355x_clear_jit_cache": (C.c_int, [_c_ctx]),
     "rew_mi355x_flush": (C.c_int, [_c_ctx]),
     "rew_mi355x_sync": (C.c_int, [_c_ctx]),
     "rew_mi355x_set_mode": (C.c_int, [_c_ctx, C.c_int]),
@@ -112,7 +117,8 @@ class MoeArgs(C.Structure):
 class Stats(C.Structure):
     _fields_ = [(n, C.c_int64) for n in (
         "ops_recorded", "kernels_launched", "flushes", "fused_groups",
-        "bytes_in_use", "bytes_cached", "plan_cache_hits")]
+        "bytes_in_use", "bytes_cached", "plan_cache_hits", "jit_module_compiles",
+        "jit_module_hits")]
 
 
 _lib = None

@@ -1,4 +1,4 @@
-// Index-producing row selections: argmax and topK.
+// Index-producing row selections: argmax, topK and the row sort.
 //
 // argmax (src/rew/ops/reduce.nim:202-225): the reference composite is
 //   m = reduceMax(x, [d]); mask = compare(x, broadcast(m), EQ);
@@ -145,6 +145,99 @@ __global__ void __launch_bounds__(256) topk_rows_kernel(TopkArgs g) {
       }
     }
   }
+}
+
+// ---- row sort --------------------------------------------------------------
+//
+// One workgroup per row: the row's keys become 64-bit composites
+// (order key << 32 | column) in LDS, a bitonic network sorts them
+// ascending, and the low halves give every output column its source
+// column.  The column in the low half makes equal keys keep their original
+// order (a stable sort); padding slots are all-ones and sort last.
+
+namespace {
+
+// Monotone unsigned image of one key: ascending order of the image is the
+// comparator's order; NaN maps above every number in both directions.
+__device__ __forceinline__ uint32_t order_key(const SortArgs& g, int64_t i) {
+  uint32_t u;
+  bool flt = false;
+  switch (g.key_dt) {
+    case kF32: u = ((const uint32_t*)g.key)[i]; flt = true; break;
+    case kBF16: u = (uint32_t)((const uint16_t*)g.key)[i] << 16; flt = true; break;
+    case kF16: u = __float_as_uint((float)((const _Float16*)g.key)[i]); flt = true; break;
+    case kI32: u = ((const uint32_t*)g.key)[i] ^ 0x80000000u; break;
+    case kI16: u = (uint32_t)(int32_t)((const int16_t*)g.key)[i] ^ 0x80000000u; break;
+    case kI8: u = (uint32_t)(int32_t)((const int8_t*)g.key)[i] ^ 0x80000000u; break;
+    case kU32: u = ((const uint32_t*)g.key)[i]; break;
+    case kU16: u = ((const uint16_t*)g.key)[i]; break;
+    default: u = ((const uint8_t*)g.key)[i]; break;  // kU8, kBool
+  }
+  if (flt) {
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0xffffffffu;  // NaN: last
+    if (u == 0x80000000u) u = 0;                              // -0 == +0
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  }
+  return g.descending ? ~u : u;
+}
+
+__device__ __forceinline__ void copy_elem(const void* src, void* dst, int esize,
+                                          int64_t s, int64_t d) {
+  switch (esize) {
+    case 1: ((uint8_t*)dst)[d] = ((const uint8_t*)src)[s]; break;
+    case 2: ((uint16_t*)dst)[d] = ((const uint16_t*)src)[s]; break;
+    case 4: ((uint32_t*)dst)[d] = ((const uint32_t*)src)[s]; break;
+    default: ((uint64_t*)dst)[d] = ((const uint64_t*)src)[s]; break;
+  }
+}
+
+}  // namespace
+
+template <int NP, int NT>
+__global__ void __launch_bounds__(NT) sort_rows_kernel(SortArgs g) {
+  __shared__ uint64_t s[NP];
+  for (int64_t r = blockIdx.x; r < g.rows; r += gridDim.x) {
+    const int64_t base = r * g.cols;
+    for (int i = threadIdx.x; i < NP; i += NT)
+      s[i] = i < g.cols ? ((uint64_t)order_key(g, base + i) << 32) | (uint32_t)i : ~0ull;
+    __syncthreads();
+    for (int k = 2; k <= NP; k <<= 1) {
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        for (int t = threadIdx.x; t < NP / 2; t += NT) {
+          const int lo = 2 * t - (t & (j - 1));
+          const int hi = lo + j;
+          const uint64_t a = s[lo], b = s[hi];
+          const bool up = (lo & k) == 0;
+          if ((a > b) == up) {
+            s[lo] = b;
+            s[hi] = a;
+          }
+        }
+        __syncthreads();
+      }
+    }
+    for (int j = threadIdx.x; j < g.cols; j += NT) {
+      const int64_t src = base + (int64_t)(uint32_t)s[j];
+      for (int o = 0; o < g.n_ops; ++o) copy_elem(g.in[o], g.out[o], g.esize[o], src, base + j);
+    }
+    __syncthreads();
+  }
+}
+
+void launch_sort(const SortArgs& g, hipStream_t stream) {
+  if (g.rows == 0 || g.cols == 0) return;
+  if (g.cols > kSortMaxCols || g.n_ops < 1 || g.n_ops > kSortMaxOps)
+    fail(REW_MI355X_ERR_INVALID, "internal: sort launch outside its limits");
+  const unsigned blocks = (unsigned)(g.rows < 65536 ? g.rows : 65536);
+#define REW_SORT_LAUNCH(NP, NT)                                                         \
+  hipLaunchKernelGGL((sort_rows_kernel<NP, NT>), dim3(blocks), dim3(NT), 0, stream, g)
+  if (g.cols <= 64) REW_SORT_LAUNCH(64, 64);
+  else if (g.cols <= 256) REW_SORT_LAUNCH(256, 128);
+  else if (g.cols <= 1024) REW_SORT_LAUNCH(1024, 256);
+  else if (g.cols <= 4096) REW_SORT_LAUNCH(4096, 512);
+  else REW_SORT_LAUNCH(8192, 512);
+#undef REW_SORT_LAUNCH
+  REW_HIP(hipGetLastError());
 }
 
 void launch_argmax(const ArgmaxArgs& g, hipStream_t stream) {

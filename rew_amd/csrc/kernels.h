@@ -184,6 +184,25 @@ struct TopkArgs {
 };
 void launch_topk(const TopkArgs& g, hipStream_t stream);
 
+// Row sort over the last dim (stablehlo.sort with a one-compare comparator,
+// src/rew/ops/sort.nim:13-33): every operand is permuted by the order of
+// the key operand; ascending (LT/LE) or descending (GT/GE), ties and NaN
+// keys keep their original order, NaN keys rank after every number, -0 and
+// +0 compare equal.  Keys: bool, 8/16/32-bit integers, f16, bf16, f32.
+constexpr int kSortMaxOps = 4;
+constexpr int64_t kSortMaxCols = 8192;
+struct SortArgs {
+  const void* key;
+  int key_dt;
+  int descending;
+  int n_ops;
+  const void* in[kSortMaxOps];
+  void* out[kSortMaxOps];
+  int esize[kSortMaxOps];   // 1, 2, 4 or 8 bytes
+  int64_t rows, cols;
+};
+void launch_sort(const SortArgs& g, hipStream_t stream);
+
 // ---- routed MoE (k_moe.hip) ------------------------------------------------------
 constexpr int kMoeMaxK = 16;  // experts per token the combine handles
 // Token placement for one group of routed experts ("members").

@@ -328,6 +328,7 @@ struct Lower {
   void emit_gather(Node* n);
   void emit_argmax(Node* n);
   void emit_topk(Node* n);
+  void emit_sort(Node* n);
   // Materialize `t` (any kind) into a fresh dense tensor whose shape is the
   // permutation `perm` of t's shape.
   Tensor* emit_permuted_copy(Tensor* t, const std::vector<int>& perm);
@@ -1025,6 +1026,7 @@ void Lower::emit_anchor(Node* n) {
     case K_INDEX_SELECT: emit_gather(n); break;
     case K_ARGMAX: emit_argmax(n); break;
     case K_TOPK: emit_topk(n); break;
+    case K_SORT: emit_sort(n); break;
     case K_BITCAST: {
       Tensor* x = n->in[0];
       ensure_mat(x);
@@ -2701,6 +2703,31 @@ void Lower::emit_topk(Node* n) {
   prof_begin(c, "topk{" + std::to_string(g.rows) + "x" + std::to_string(g.cols) + ",k" +
                     std::to_string(g.k) + "}");
   launch_topk(g, c->stream);
+  prof_end(c);
+  note_launch(c, false);
+}
+
+// Row sort over the last dim (the stablehlo.sort form the jit path and the
+// sort extension op record).
+void Lower::emit_sort(Node* n) {
+  SortArgs g;
+  std::memset(&g, 0, sizeof g);
+  for (Tensor* t : n->in) ensure_mat(t);
+  for (Tensor* t : n->out) tensor_alloc(t);
+  Tensor* k = n->in[n->i2];
+  g.key = k->data();
+  g.key_dt = k->dt;
+  g.descending = (int)n->i1;
+  g.n_ops = (int)n->in.size();
+  for (int o = 0; o < g.n_ops; ++o) {
+    g.in[o] = n->in[o]->data();
+    g.out[o] = n->out[o]->data();
+    g.esize[o] = dt_size(n->in[o]->dt);
+  }
+  g.cols = k->shape.d[k->shape.rank - 1];
+  g.rows = g.cols ? k->numel() / g.cols : 0;
+  prof_begin(c, "sort{" + std::to_string(g.rows) + "x" + std::to_string(g.cols) + "}");
+  launch_sort(g, c->stream);
   prof_end(c);
   note_launch(c, false);
 }

@@ -97,7 +97,7 @@ static const std::unordered_map<std::string, OpSpec>& op_table() {
       {"dotGeneral", {K_DOT_GENERAL, 0}}, {"dot", {K_DOT, 0}},
       {"torchIndexSelect", {K_INDEX_SELECT, 0}},
       // backend extensions (no eager counterpart in the reference)
-      {"argmax", {K_ARGMAX, 0}}, {"topK", {K_TOPK, 0}},
+      {"argmax", {K_ARGMAX, 0}}, {"topK", {K_TOPK, 0}}, {"sort", {K_SORT, 0}},
   };
   return t;
 }
@@ -215,9 +215,8 @@ static const int64_t kMaxElems = (int64_t)1 << 31;
 
 // ---- record ------------------------------------------------------------------------
 
-std::vector<Tensor*> record_op(Ctx* c, const std::string& op,
-                               const std::vector<Tensor*>& ins,
-                               const Attrs& attrs) {
+Node* prepare_node(Ctx* c, const std::string& op, const std::vector<Tensor*>& ins,
+                   const Attrs& attrs, std::vector<std::pair<int, Shape>>* outs_out) {
   auto it = op_table().find(op);
   if (it == op_table().end()) {
     if (known_but_unimplemented(op))
@@ -532,6 +531,48 @@ std::vector<Tensor*> record_op(Ctx* c, const std::string& op,
         outs.push_back({kI32, s});
         break;
       }
+      case K_SORT: {
+        // stablehlo.sort whose comparator is one compare of the key
+        // operand's pair (src/rew/ops/sort.nim:13-33): attrs dimension,
+        // comparison_direction (LT/LE ascending, GT/GE descending), key.
+        if (ins.empty() || ins.size() > (size_t)kSortMaxOps)
+          invalid("eager 'sort': expected 1 to " + std::to_string(kSortMaxOps) + " operands");
+        const Shape& is = ins[0]->shape;
+        if (is.rank == 0) invalid("eager 'sort': rank-0 operand");
+        n->i0 = parse_int(find_attr(attrs, "dimension", op), op);
+        if (n->i0 < 0) n->i0 += is.rank;
+        if (n->i0 < 0 || n->i0 >= is.rank) invalid("eager 'sort': dimension out of range");
+        if (n->i0 != is.rank - 1)
+          fail(REW_MI355X_ERR_UNSUPPORTED, "eager 'sort': only the last dimension");
+        std::string dir = "LT";
+        n->i2 = 0;
+        for (auto& kv : attrs) {
+          if (kv.first == "comparison_direction") dir = strip(kv.second);
+          if (kv.first == "key") n->i2 = parse_int(kv.second, op);
+        }
+        if (dir == "LT" || dir == "LE") n->i1 = 0;
+        else if (dir == "GT" || dir == "GE") n->i1 = 1;
+        else invalid("eager 'sort': comparison_direction must be LT, LE, GT or GE");
+        if (n->i2 < 0 || n->i2 >= (int64_t)ins.size()) invalid("eager 'sort': key out of range");
+        for (Tensor* t : ins) {
+          if (t->shape != is) invalid("eager 'sort': all operands must have the same shape");
+          const int sz = dt_size(t->dt);
+          if (t->dt == kI4 || t->dt == kU4 || t->dt == kNF4 ||
+              (sz != 1 && sz != 2 && sz != 4 && sz != 8))
+            fail(REW_MI355X_ERR_UNSUPPORTED,
+                 std::string("eager 'sort': operand dtype ") + dt_enum_name(t->dt) + " not supported");
+          outs.push_back({t->dt, t->shape});
+        }
+        const int kd = ins[n->i2]->dt;
+        if (kd != kF32 && kd != kBF16 && kd != kF16 && kd != kI32 && kd != kI16 &&
+            kd != kI8 && kd != kU32 && kd != kU16 && kd != kU8 && kd != kBool)
+          fail(REW_MI355X_ERR_UNSUPPORTED,
+               std::string("eager 'sort': key dtype ") + dt_enum_name(kd) + " not supported");
+        if (is.d[n->i0] > kSortMaxCols)
+          fail(REW_MI355X_ERR_UNSUPPORTED, "eager 'sort': dimension above " +
+                                               std::to_string(kSortMaxCols));
+        break;
+      }
       case K_DOT:
       case K_DOT_GENERAL: {
         nin(2);
@@ -620,7 +661,13 @@ std::vector<Tensor*> record_op(Ctx* c, const std::string& op,
                                            std::to_string(o.second.numel()) +
                                            " elements exceeds the 2^31 limit");
     }
+  *outs_out = std::move(outs);
+  return n;
+}
 
+std::vector<Tensor*> commit_node(Ctx* c, Node* n, const std::vector<Tensor*>& ins,
+                                 const std::vector<std::pair<int, Shape>>& outs) {
+  n->in = ins;
   std::vector<Tensor*> result;
   for (size_t i = 0; i < outs.size(); ++i) {
     Tensor* t = new_tensor(c, outs[i].first, outs[i].second);
@@ -638,6 +685,14 @@ std::vector<Tensor*> record_op(Ctx* c, const std::string& op,
       (int)c->pending.size() >= c->flush_threshold)
     flush(c);
   return result;
+}
+
+std::vector<Tensor*> record_op(Ctx* c, const std::string& op,
+                               const std::vector<Tensor*>& ins,
+                               const Attrs& attrs) {
+  std::vector<std::pair<int, Shape>> outs;
+  Node* n = prepare_node(c, op, ins, attrs, &outs);
+  return commit_node(c, n, ins, outs);
 }
 
 }  // namespace rew

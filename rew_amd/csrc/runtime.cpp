@@ -220,6 +220,51 @@ static void h2d(Ctx* c, void* dst, const void* src, size_t bytes) {
 
 void upload_async(Ctx* c, void* dst, const void* src, size_t bytes) { h2d(c, dst, src, bytes); }
 
+// A new tensor (one owner reference) holding `host`'s bytes; small
+// constants share one device copy per distinct (dtype, shape, bytes).
+// The context's device must be current.
+Tensor* upload_tensor(Ctx* c, int dtype, const Shape& s, const void* host) {
+  Tensor* t = new_tensor(c, dtype, s);
+  const int64_t want = s.numel() * dt_size(dtype);
+  const int rank = s.rank;
+  const int64_t* shape = s.d;
+  // small constants: one device copy per distinct (dtype, shape, bytes)
+  constexpr int64_t kConstMax = 256;
+  std::string key;
+  if (want > 0 && want <= kConstMax) {
+    key.reserve(16 + 8 * rank + (size_t)want);
+    key.append((const char*)&dtype, sizeof dtype);
+    key.append((const char*)&rank, sizeof rank);
+    key.append((const char*)shape, sizeof(int64_t) * rank);
+    key.append((const char*)host, (size_t)want);
+    auto hit = c->const_cache.find(key);
+    if (hit != c->const_cache.end()) {
+      t->st = hit->second;
+      t->st->refs++;
+    }
+  }
+  if (!t->st) {
+    try {
+      tensor_alloc(t);
+      h2d(c, t->data(), host, (size_t)want);
+    } catch (...) {
+      maybe_destroy(t);
+      throw;
+    }
+    if (!key.empty()) {
+      if (c->const_cache.size() >= 4096) const_cache_clear(c);
+      t->st->refs++;
+      c->const_cache.emplace(key, t->st);
+    }
+  }
+  if (want <= 16 && want > 0) {
+    t->has_host = true;
+    std::memcpy(t->host, host, (size_t)want);
+  }
+  t->ext = 1;
+  return t;
+}
+
 }  // namespace rew
 
 using namespace rew;
@@ -293,10 +338,12 @@ int rew_mi355x_shutdown(rew_mi355x_ctx* ctx) {
     REW_HIP(hipSetDevice(c->ordinal));
     flush(c);
     REW_HIP(hipStreamSynchronize(c->stream));
+    jit_module_cache_clear(c);
     const_cache_clear(c);
     c->alloc.trim();
   });
 }
+
 
 int rew_mi355x_from_host(rew_mi355x_ctx* ctx, int dtype, const int64_t* shape,
                          int rank, const void* host, int64_t nbytes,
@@ -317,41 +364,7 @@ int rew_mi355x_from_host(rew_mi355x_ctx* ctx, int dtype, const int64_t* shape,
     if (want > 0 && !host) invalid("from_host: null host pointer");
     std::lock_guard<std::recursive_mutex> g(c->mu);
     REW_HIP(hipSetDevice(c->ordinal));
-    Tensor* t = new_tensor(c, dtype, s);
-    // small constants: one device copy per distinct (dtype, shape, bytes)
-    constexpr int64_t kConstMax = 256;
-    std::string key;
-    if (want > 0 && want <= kConstMax) {
-      key.reserve(16 + 8 * rank + (size_t)want);
-      key.append((const char*)&dtype, sizeof dtype);
-      key.append((const char*)&rank, sizeof rank);
-      key.append((const char*)shape, sizeof(int64_t) * rank);
-      key.append((const char*)host, (size_t)want);
-      auto hit = c->const_cache.find(key);
-      if (hit != c->const_cache.end()) {
-        t->st = hit->second;
-        t->st->refs++;
-      }
-    }
-    if (!t->st) {
-      try {
-        tensor_alloc(t);
-        h2d(c, t->data(), host, (size_t)want);
-      } catch (...) {
-        maybe_destroy(t);
-        throw;
-      }
-      if (!key.empty()) {
-        if (c->const_cache.size() >= 4096) const_cache_clear(c);
-        t->st->refs++;
-        c->const_cache.emplace(key, t->st);
-      }
-    }
-    if (want <= 16 && want > 0) {
-      t->has_host = true;
-      std::memcpy(t->host, host, (size_t)want);
-    }
-    t->ext = 1;
+    Tensor* t = upload_tensor(c, dtype, s, host);
     *out = reinterpret_cast<rew_mi355x_buf*>(t);
   });
 }
@@ -510,6 +523,63 @@ int rew_mi355x_execute_ex(rew_mi355x_ctx* ctx, const char* op,
                           rew_mi355x_buf** outs, int max_outs, int* n_outs, int64_t* out_meta) {
   return execute_impl(ctx, op, operands, n_operands, keys, vals, n_attrs, outs, max_outs, n_outs,
                       out_meta);
+}
+
+int rew_mi355x_execute_jit(rew_mi355x_ctx* ctx, const char* jit_name, const char* cache_key,
+                           const char* module_text, int64_t text_len,
+                           rew_mi355x_buf* const* inputs, int n_inputs, const int* donate_idx,
+                           int n_donate, rew_mi355x_buf** outs, int max_outs, int* n_outs,
+                           int64_t* out_meta) {
+  return guarded([&] {
+    Ctx* c = as_ctx(ctx);
+    const std::string name = jit_name ? jit_name : "";
+    const std::string who = "jit '" + name + "'";
+    if (!module_text) invalid(who + ": null module text");
+    if (n_inputs <= 0 || !inputs) invalid(who + ": zero inputs");
+    if (n_donate < 0 || (n_donate > 0 && !donate_idx)) invalid(who + ": bad donation array");
+    for (int i = 0; i < n_donate; ++i)
+      if (donate_idx[i] < 0 || donate_idx[i] >= n_inputs)
+        invalid(who + ": donation index " + std::to_string(donate_idx[i]) + " out of range");
+    std::vector<Tensor*> ins;
+    ins.reserve(n_inputs);
+    for (int i = 0; i < n_inputs; ++i) {
+      Tensor* t = check_handle(inputs[i], who.c_str());
+      if (t->ctx != c) invalid(who + ": cross-device inputs forbidden");
+      ins.push_back(t);
+    }
+    const size_t len = text_len < 0 ? std::strlen(module_text) : (size_t)text_len;
+    std::lock_guard<std::recursive_mutex> g(c->mu);
+    REW_HIP(hipSetDevice(c->ordinal));
+    std::vector<Tensor*> res =
+        jit_module_run(c, name, cache_key ? cache_key : "", module_text, len, ins);
+    if ((int)res.size() > max_outs || !outs) {
+      for (Tensor* t : res) {
+        t->ext--;
+        maybe_destroy(t);
+      }
+      invalid(who + ": module returns " + std::to_string(res.size()) +
+              " value(s), caller has room for " + std::to_string(max_outs));
+    }
+    for (size_t i = 0; i < res.size(); ++i) {
+      outs[i] = reinterpret_cast<rew_mi355x_buf*>(res[i]);
+      if (out_meta) {
+        int64_t* m = out_meta + i * (2 + REW_MI355X_MAX_RANK);
+        m[0] = res[i]->dt;
+        m[1] = res[i]->shape.rank;
+        for (int k = 0; k < res[i]->shape.rank; ++k) m[2 + k] = res[i]->shape.d[k];
+      }
+    }
+    if (n_outs) *n_outs = (int)res.size();
+  });
+}
+
+int rew_mi355x_clear_jit_cache(rew_mi355x_ctx* ctx) {
+  return guarded([&] {
+    Ctx* c = as_ctx(ctx);
+    std::lock_guard<std::recursive_mutex> g(c->mu);
+    REW_HIP(hipSetDevice(c->ordinal));
+    jit_module_cache_clear(c);
+  });
 }
 
 int rew_mi355x_flush(rew_mi355x_ctx* ctx) {

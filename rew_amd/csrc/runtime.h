@@ -16,6 +16,7 @@ namespace rew {
 struct Ctx;
 struct Node;
 struct RoutedFfn;
+struct JitModule;
 
 // A device allocation shared by every tensor that aliases it (a reshape of
 // a materialized tensor aliases its source).
@@ -49,12 +50,12 @@ struct Tensor {
 };
 
 // Op kinds (the subset of rew's EagerOpKind this backend implements,
-// src/rew/eager.nim:718-764, plus backend extensions argmax/topK).
+// src/rew/eager.nim:718-764, plus backend extensions argmax/topK/sort).
 enum Kind : int {
   K_BINARY, K_UNARY, K_CONVERT, K_ISFINITE, K_BITCAST, K_RESHAPE,
   K_TRANSPOSE, K_REVERSE, K_BROADCAST_TO, K_BROADCAST, K_SLICE, K_CONCAT,
   K_IOTA, K_COMPARE, K_SELECT, K_CLAMP, K_REDUCE, K_DOT_GENERAL, K_DOT,
-  K_INDEX_SELECT, K_ARGMAX, K_TOPK, K_REDUCE_PRECISION, K_PAD,
+  K_INDEX_SELECT, K_ARGMAX, K_TOPK, K_REDUCE_PRECISION, K_PAD, K_SORT,
   // composite kernels created by the planner (never recorded directly)
   K_COUNT
 };
@@ -126,6 +127,9 @@ struct Ctx {
   // lookup at init failed)
   void* noalloc_scratch = nullptr;
   std::string noalloc_error;
+  // translated jit modules (stablehlo.cpp), keyed by
+  // ordinal::name::cacheKey::hash(text)
+  std::unordered_map<std::string, JitModule*> jit_modules;
 };
 
 // ---- runtime services (runtime.cpp) -----------------------------------------
@@ -142,6 +146,10 @@ bool tensor_is_live_handle(const Tensor* t);
 // the pinned staging ring; `src` may be reused as soon as this returns).
 void upload_async(Ctx* c, void* dst, const void* src, size_t bytes);
 
+// A new tensor (one owner reference) holding a copy of `host`; small
+// constants share one device copy per distinct (dtype, shape, bytes).
+Tensor* upload_tensor(Ctx* c, int dtype, const Shape& s, const void* host);
+
 // Launch bracketing for profiling: call before/after each kernel launch.
 void prof_begin(Ctx* c, const std::string& name);
 void prof_end(Ctx* c);
@@ -152,6 +160,14 @@ void run_routed_ffn(Ctx* c, const RoutedFfn& a, void* scratch);
 // With the context's device current: the device address of the static
 // scratch array (moe_ffn.hip), or null with *err set.
 void* noalloc_scratch_lookup(std::string* err);
+
+// Jit modules (stablehlo.cpp): runs the StableHLO module `text` over `ins`
+// (parsing and translating it on first use) and returns its results, one
+// owner reference each; jit_module_cache_clear drops every cached module.
+std::vector<Tensor*> jit_module_run(Ctx* c, const std::string& name,
+                                    const std::string& cache_key, const char* text,
+                                    size_t len, const std::vector<Tensor*>& ins);
+void jit_module_cache_clear(Ctx* c);
 
 // ABI-edge error plumbing (runtime.cpp): the thread-local message behind
 // rew_mi355x_last_error().
@@ -183,5 +199,16 @@ std::vector<Tensor*> record_op(Ctx* c, const std::string& name,
                                const std::vector<Tensor*>& ins,
                                const std::vector<std::pair<std::string, std::string>>& attrs);
 void flush(Ctx* c);
+// record_op in two halves: prepare_node validates the op against its
+// operands' dtypes and shapes and returns the node (typed attributes set,
+// no operands attached) with its outputs' dtype and shape; commit_node
+// attaches operands, creates the outputs (one owner reference each) and
+// queues the node.  The jit path prepares a module's nodes once and
+// commits copies of them per call.
+Node* prepare_node(Ctx* c, const std::string& op, const std::vector<Tensor*>& ins,
+                   const std::vector<std::pair<std::string, std::string>>& attrs,
+                   std::vector<std::pair<int, Shape>>* outs);
+std::vector<Tensor*> commit_node(Ctx* c, Node* n, const std::vector<Tensor*>& ins,
+                                 const std::vector<std::pair<int, Shape>>& outs);
 
 }  // namespace rew

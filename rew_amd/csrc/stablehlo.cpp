@@ -1,0 +1,1365 @@
+// Jit execution of rew's StableHLO modules.
+//
+// rew's jit/lazy trace a function into a StableHLO module and hand its text
+// to PJRT (src/rew/transform/jit.nim:216-229 -> executeJit,
+// src/rew/eager.nim:1782-1847).  This file is the mi355x side of that call:
+//
+//   * a parser for the textual form rew's emitter writes
+//     (src/rew/stablehlo/text.nim: the pretty forms of the elementwise,
+//     reshape/transpose/broadcast_in_dim/slice/concatenate/compare/select/
+//     clamp/dot_general/reduce ops and constants, and the quoted generic form
+//     "stablehlo.x"(...) ({regions}) {attrs} : (types) -> types used for
+//     iota, convert, torch_index_select, sort, ...);
+//   * a translator that turns each op into the graph node the matching eager
+//     op records (prepare_node, the same validation and output derivation),
+//     with stablehlo.reduce mapped onto reduceSum/Max/Min/Prod by its reducer
+//     body, stablehlo.sort onto the row-sort node, and the sort+slice pair
+//     rew's topK traces (src/rew/ops/sort.nim:36-90) onto one topK node;
+//   * a per-context module cache keyed like rew's jitExecCache
+//     (ordinal::name::cacheKey::hash(text)), whose entries hold prepared
+//     node prototypes and the module's constants on the device, so a call
+//     only copies nodes and links them to its inputs.
+//
+// Nodes join the deferred graph like eager ops, so a lazy batch lowers
+// through the same fused kernels (flash attention, GEMM epilogues, routed
+// MoE) as the eager op stream and is launched at the next flush.
+#include <cmath>
+#include <cstring>
+#include <deque>
+#include <memory>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "kernels.h"
+#include "runtime.h"
+
+namespace rew {
+
+namespace {
+
+using Attrs = std::vector<std::pair<std::string, std::string>>;
+
+// ---- parsed form ----------------------------------------------------------------
+
+struct Ty {
+  int dt = -1;  // -1: a type the backend has no dtype for
+  std::vector<int64_t> d;
+  std::string text;
+};
+
+struct Op {
+  std::string name;  // mnemonic without quotes, e.g. "stablehlo.add"
+  int line = 0;
+  std::vector<int> res;  // value slots defined
+  std::vector<int> arg;  // value slots used
+  std::vector<Ty> res_ty;
+  bool bare_sig = false;  // ": T" signature (result type only)
+  // op-specific operands of the pretty forms
+  std::vector<int64_t> l0, l1, l2, l3;
+  std::string word;             // compare direction
+  std::string bytes;            // constant raw bytes
+  bool splat = false;           // constant dense<number>
+  double splat_v = 0.0;
+  Attrs attrs;                  // generic attribute dictionary (raw values)
+  std::vector<std::vector<int>> region_args;
+  std::vector<std::vector<Op>> regions;
+};
+
+struct Func {
+  std::string name;
+  bool is_private = false;
+  std::vector<int> args;
+  std::vector<Ty> arg_ty;
+  std::vector<Op> ops;
+  std::vector<int> ret;
+};
+
+[[noreturn]] void unsupported(const std::string& m) { fail(REW_MI355X_ERR_UNSUPPORTED, m); }
+
+int elem_dtype(const std::string& e) {
+  static const std::unordered_map<std::string, int> m = {
+      {"i1", kBool},   {"i8", kI8},     {"i16", kI16},         {"i32", kI32},
+      {"i64", kI64},   {"ui8", kU8},    {"ui16", kU16},        {"ui32", kU32},
+      {"ui64", kU64},  {"f16", kF16},   {"bf16", kBF16},       {"f32", kF32},
+      {"f64", kF64},   {"i4", kI4},     {"ui4", kU4},          {"f8E4M3FN", kF8E4M3},
+      {"f8E5M2", kF8E5M2}, {"complex<f32>", kC64}, {"complex<f64>", kC128}};
+  auto it = m.find(e);
+  return it == m.end() ? -1 : it->second;
+}
+
+class Parser {
+ public:
+  Parser(const char* s, size_t n, const std::string& who) : s_(s), n_(n), who_(who) {}
+
+  std::vector<Func> module() {
+    std::vector<Func> fs;
+    expect_word("module");
+    ws();
+    if (peek('@')) {
+      ++p_;
+      name_chars();
+    }
+    if (eat_word("attributes")) skip_balanced('{', '}');
+    expect("{");
+    for (;;) {
+      ws();
+      if (eat("}")) break;
+      if (eat_word("func.func")) {
+        fs.push_back(func());
+        continue;
+      }
+      if (p_ >= n_) err("unterminated module");
+      // other top-level ops (sdy.mesh ...): skip the line
+      while (p_ < n_ && s_[p_] != '\n') ++p_;
+    }
+    return fs;
+  }
+
+  int slots() const { return next_slot_; }
+
+ private:
+  const char* s_;
+  size_t n_;
+  size_t p_ = 0;
+  std::string who_;
+  std::unordered_map<std::string, int> names_;
+  int next_slot_ = 0;
+
+  int line_at(size_t p) const {
+    int l = 1;
+    for (size_t i = 0; i < p && i < n_; ++i) l += s_[i] == '\n';
+    return l;
+  }
+  [[noreturn]] void err(const std::string& m) const {
+    invalid(who_ + ": StableHLO text line " + std::to_string(line_at(p_)) + ": " + m);
+  }
+  void ws() {
+    while (p_ < n_) {
+      const char ch = s_[p_];
+      if (ch == ' ' || ch == '\t' || ch == '\n' || ch == '\r') {
+        ++p_;
+      } else if (ch == '/' && p_ + 1 < n_ && s_[p_ + 1] == '/') {
+        while (p_ < n_ && s_[p_] != '\n') ++p_;
+      } else {
+        break;
+      }
+    }
+  }
+  bool peek(char ch) {
+    ws();
+    return p_ < n_ && s_[p_] == ch;
+  }
+  bool eat(const char* lit) {
+    ws();
+    const size_t l = std::strlen(lit);
+    if (p_ + l <= n_ && std::memcmp(s_ + p_, lit, l) == 0) {
+      p_ += l;
+      return true;
+    }
+    return false;
+  }
+  static bool ident_char(char ch) {
+    return std::isalnum((unsigned char)ch) || ch == '_' || ch == '.' || ch == '$';
+  }
+  bool eat_word(const char* w) {
+    ws();
+    const size_t l = std::strlen(w);
+    if (p_ + l <= n_ && std::memcmp(s_ + p_, w, l) == 0 &&
+        (p_ + l == n_ || !ident_char(s_[p_ + l]))) {
+      p_ += l;
+      return true;
+    }
+    return false;
+  }
+  void expect(const char* lit) {
+    if (!eat(lit)) err(std::string("expected '") + lit + "'");
+  }
+  void expect_word(const char* w) {
+    if (!eat_word(w)) err(std::string("expected '") + w + "'");
+  }
+  std::string name_chars() {
+    const size_t b = p_;
+    while (p_ < n_ && (ident_char(s_[p_]) ||
+                       (s_[p_] == '-' && p_ + 1 < n_ && s_[p_ + 1] != '>')))
+      ++p_;
+    return std::string(s_ + b, p_ - b);
+  }
+  std::string word() {
+    ws();
+    std::string w = name_chars();
+    if (w.empty()) err("expected a name");
+    return w;
+  }
+  std::string value_name() {
+    ws();
+    if (!peek('%')) err("expected an SSA value");
+    ++p_;
+    std::string nm = name_chars();
+    if (nm.empty()) err("empty SSA value name");
+    return nm;
+  }
+  int use_value() {
+    std::string nm = value_name();
+    if (p_ < n_ && s_[p_] == '#') {  // %r#1: result 1 of a multi-result op
+      ++p_;
+      nm += "#" + name_chars();
+    }
+    auto it = names_.find(nm);
+    if (it == names_.end()) err("use of undefined value %" + nm);
+    return it->second;
+  }
+  int define(const std::string& nm) {
+    if (names_.count(nm)) err("redefinition of %" + nm);
+    const int s = next_slot_++;
+    names_.emplace(nm, s);
+    return s;
+  }
+  int64_t integer() {
+    ws();
+    const char* b = s_ + p_;
+    char* e = nullptr;
+    const long long v = std::strtoll(b, &e, 10);
+    if (e == b) err("expected an integer");
+    p_ += (size_t)(e - b);
+    return (int64_t)v;
+  }
+  std::vector<int64_t> int_list() {
+    std::vector<int64_t> v;
+    expect("[");
+    if (eat("]")) return v;
+    for (;;) {
+      v.push_back(integer());
+      if (eat("]")) break;
+      expect(",");
+    }
+    return v;
+  }
+  void skip_balanced(char open, char close) {
+    ws();
+    if (p_ >= n_ || s_[p_] != open) err(std::string("expected '") + open + "'");
+    int depth = 0;
+    bool str = false;
+    for (; p_ < n_; ++p_) {
+      const char ch = s_[p_];
+      if (str) {
+        if (ch == '\\') ++p_;
+        else if (ch == '"') str = false;
+        continue;
+      }
+      if (ch == '"') str = true;
+      else if (ch == open) ++depth;
+      else if (ch == close && --depth == 0) {
+        ++p_;
+        return;
+      }
+    }
+    err("unbalanced brackets");
+  }
+
+  Ty type() {
+    ws();
+    Ty t;
+    const size_t b = p_;
+    if (!eat("tensor<")) {
+      if (peek('!') || eat_word("tuple"))
+        unsupported(who_ + ": StableHLO text line " + std::to_string(line_at(p_)) +
+                    ": only tensor types are supported by the mi355x backend");
+      err("expected a tensor type");
+    }
+    for (;;) {
+      ws();
+      if (p_ < n_ && std::isdigit((unsigned char)s_[p_])) {
+        t.d.push_back(integer());
+        if (p_ < n_ && s_[p_] == 'x') {
+          ++p_;
+          continue;
+        }
+        err("expected 'x' after a dimension");
+      }
+      if (p_ < n_ && s_[p_] == '?')
+        unsupported(who_ + ": dynamic dimensions are not supported by the mi355x backend");
+      break;
+    }
+    std::string e;
+    if (eat("complex<")) {
+      e = "complex<" + name_chars() + ">";
+      expect(">");
+    } else {
+      e = name_chars();
+    }
+    t.dt = elem_dtype(e);
+    if (t.dt < 0) err("unknown element type '" + e + "'");
+    if (eat(",")) skip_balanced('{', '}');  // encoding attribute
+    expect(">");
+    ws();
+    t.text.assign(s_ + b, p_ - b);
+    return t;
+  }
+
+  // "(T, T) -> T" or "(T) -> (T, T)" or "T" or "T, T"; returns the
+  // result types (bare lists: the last type)
+  std::vector<Ty> signature(bool* bare) {
+    expect(":");
+    std::vector<Ty> out;
+    if (eat("(")) {
+      if (!eat(")")) {
+        for (;;) {
+          type();
+          if (eat(")")) break;
+          expect(",");
+        }
+      }
+      expect("->");
+      if (eat("(")) {
+        if (!eat(")")) {
+          for (;;) {
+            out.push_back(type());
+            if (eat(")")) break;
+            expect(",");
+          }
+        }
+      } else {
+        out.push_back(type());
+      }
+      *bare = false;
+      return out;
+    }
+    std::vector<Ty> all;
+    all.push_back(type());
+    while (eat(",")) all.push_back(type());
+    out.push_back(all.back());
+    *bare = true;
+    return out;
+  }
+
+  // key = value pairs with raw values (balanced up to the next top-level
+  // ',' or '}')
+  void attr_dict(Attrs* out) {
+    expect("{");
+    if (eat("}")) return;
+    for (;;) {
+      std::string k = word();
+      expect("=");
+      ws();
+      const size_t b = p_;
+      int depth = 0;
+      bool str = false;
+      for (; p_ < n_; ++p_) {
+        const char ch = s_[p_];
+        if (str) {
+          if (ch == '\\') ++p_;
+          else if (ch == '"') str = false;
+          continue;
+        }
+        if (ch == '"') str = true;
+        else if (ch == '<' || ch == '[' || ch == '(' || ch == '{') ++depth;
+        else if (ch == '>' || ch == ']' || ch == ')' || ch == '}') {
+          if (depth == 0) break;
+          if (ch == '>' && p_ > 0 && s_[p_ - 1] == '-') continue;
+          --depth;
+        } else if (ch == ',' && depth == 0) {
+          break;
+        }
+      }
+      std::string v(s_ + b, p_ - b);
+      while (!v.empty() && std::isspace((unsigned char)v.back())) v.pop_back();
+      out->emplace_back(k, v);
+      if (eat("}")) return;
+      expect(",");
+    }
+  }
+
+  // region body: statements up to the closing '}' (consumed)
+  void region_body(std::vector<Op>* ops) {
+    for (;;) {
+      if (eat("}")) return;
+      if (p_ >= n_) err("unterminated region");
+      std::vector<int> unused;
+      bool ended = false;
+      stmt(ops, &unused, &ended);
+    }
+  }
+
+  // '{' opening an attribute dictionary ("{name = ..."), not a body
+  bool attr_dict_ahead() {
+    if (!peek('{')) return false;
+    size_t q = p_ + 1;
+    while (q < n_ && std::isspace((unsigned char)s_[q])) ++q;
+    const size_t b = q;
+    while (q < n_ && (ident_char(s_[q]) || s_[q] == '"')) ++q;
+    if (q == b) return false;
+    while (q < n_ && (s_[q] == ' ' || s_[q] == '\t')) ++q;
+    return q < n_ && s_[q] == '=';
+  }
+
+  Func func() {
+    Func f;
+    if (eat_word("private")) f.is_private = true;
+    else eat_word("public");
+    expect("@");
+    f.name = name_chars();
+    expect("(");
+    if (!eat(")")) {
+      for (;;) {
+        f.args.push_back(define(value_name()));
+        expect(":");
+        f.arg_ty.push_back(type());
+        if (peek('{')) skip_balanced('{', '}');  // argument attributes (sdy.sharding)
+        if (eat(")")) break;
+        expect(",");
+      }
+    }
+    if (eat("->")) {
+      if (eat("(")) {
+        if (!eat(")")) {
+          for (;;) {
+            type();
+            if (peek('{')) skip_balanced('{', '}');
+            if (eat(")")) break;
+            expect(",");
+          }
+        }
+      } else {
+        type();
+        if (attr_dict_ahead()) skip_balanced('{', '}');
+      }
+    }
+    if (eat_word("attributes")) skip_balanced('{', '}');
+    expect("{");
+    bool ended = false;
+    for (;;) {
+      if (eat("}")) break;
+      if (p_ >= n_) err("unterminated function");
+      stmt(&f.ops, &f.ret, &ended);
+    }
+    if (!ended) err("function @" + f.name + " has no func.return");
+    return f;
+  }
+
+  void stmt(std::vector<Op>* ops, std::vector<int>* ret, bool* ended) {
+    ws();
+    const int line = line_at(p_);
+    if (eat_word("func.return") || eat_word("return")) {
+      ret->clear();
+      if (peek('%')) {
+        for (;;) {
+          ret->push_back(use_value());
+          if (!eat(",")) break;
+        }
+        expect(":");
+        type();
+        while (eat(",")) type();
+      }
+      *ended = true;
+      return;
+    }
+    if (eat_word("stablehlo.return") || eat("\"stablehlo.return\"")) {
+      Op op;
+      op.name = "stablehlo.return";
+      op.line = line;
+      const bool generic = eat("(");
+      if (peek('%')) {
+        for (;;) {
+          op.arg.push_back(use_value());
+          if (!eat(",")) break;
+        }
+      }
+      if (generic) expect(")");
+      if (peek(':')) {
+        bool bare = false;
+        if (generic) {
+          expect(":");
+          skip_balanced('(', ')');
+          expect("->");
+          skip_balanced('(', ')');
+        } else {
+          signature(&bare);
+        }
+      }
+      ops->push_back(std::move(op));
+      return;
+    }
+    // results
+    std::vector<std::string> names;
+    for (;;) {
+      std::string nm = value_name();
+      if (eat(":")) {
+        const int64_t k = integer();
+        for (int64_t i = 0; i < k; ++i) names.push_back(nm + "#" + std::to_string(i));
+      } else {
+        names.push_back(nm);
+      }
+      if (!eat(",")) break;
+    }
+    expect("=");
+    Op op;
+    op.line = line;
+    body(&op);
+    if (op.res_ty.size() != names.size())
+      err(op.name + " defines " + std::to_string(names.size()) + " value(s) but its type " +
+          "lists " + std::to_string(op.res_ty.size()));
+    // results are defined after the operands (and region values) were used
+    for (auto& nm : names) op.res.push_back(define(nm));
+    ops->push_back(std::move(op));
+  }
+
+  void regions(Op* op) {
+    for (;;) {
+      expect("{");
+      std::vector<int> args;
+      if (eat("^")) {
+        name_chars();
+        if (eat("(")) {
+          if (!eat(")")) {
+            for (;;) {
+              args.push_back(define(value_name()));
+              expect(":");
+              type();
+              if (eat(")")) break;
+              expect(",");
+            }
+          }
+        }
+        expect(":");
+      }
+      op->region_args.push_back(args);
+      op->regions.emplace_back();
+      region_body(&op->regions.back());
+      if (!eat(",")) break;
+    }
+  }
+
+  void body(Op* op) {
+    ws();
+    if (peek('"')) {  // generic form
+      ++p_;
+      const size_t b = p_;
+      while (p_ < n_ && s_[p_] != '"') ++p_;
+      if (p_ >= n_) err("unterminated op name");
+      op->name.assign(s_ + b, p_ - b);
+      ++p_;
+      expect("(");
+      if (!eat(")")) {
+        for (;;) {
+          op->arg.push_back(use_value());
+          if (eat(")")) break;
+          expect(",");
+        }
+      }
+      if (eat("(")) {
+        regions(op);
+        expect(")");
+      }
+      if (peek('{')) attr_dict(&op->attrs);
+      op->res_ty = signature(&op->bare_sig);
+      return;
+    }
+    op->name = word();
+    if (op->name == "stablehlo.constant") {
+      expect("dense<");
+      ws();
+      if (eat("\"0x")) {
+        auto hex = [&](char ch) -> int {
+          if (ch >= '0' && ch <= '9') return ch - '0';
+          if (ch >= 'a' && ch <= 'f') return ch - 'a' + 10;
+          if (ch >= 'A' && ch <= 'F') return ch - 'A' + 10;
+          err("bad hex digit in a dense constant");
+        };
+        while (p_ + 1 < n_ && s_[p_] != '"') {
+          op->bytes.push_back((char)(hex(s_[p_]) * 16 + hex(s_[p_ + 1])));
+          p_ += 2;
+        }
+        expect("\"");
+      } else if (eat_word("true")) {
+        op->splat = true;
+        op->splat_v = 1.0;
+      } else if (eat_word("false")) {
+        op->splat = true;
+        op->splat_v = 0.0;
+      } else {
+        const char* b = s_ + p_;
+        char* e = nullptr;
+        op->splat_v = std::strtod(b, &e);
+        if (e == b)
+          unsupported(who_ + ": StableHLO text line " + std::to_string(line_at(p_)) +
+                      ": only hex and splat dense constants are supported");
+        p_ += (size_t)(e - b);
+        op->splat = true;
+      }
+      expect(">");
+      op->res_ty = signature(&op->bare_sig);
+      return;
+    }
+    if (op->name == "stablehlo.compare") {
+      op->word = word();
+      expect(",");
+      op->arg.push_back(use_value());
+      expect(",");
+      op->arg.push_back(use_value());
+      if (eat(",")) word();  // comparison type
+      op->res_ty = signature(&op->bare_sig);
+      return;
+    }
+    if (op->name == "stablehlo.reduce") {
+      expect("(");
+      op->arg.push_back(use_value());
+      expect_word("init");
+      expect(":");
+      op->arg.push_back(use_value());
+      expect(")");
+      if (peek(','))
+        unsupported(who_ + ": multi-operand stablehlo.reduce is not supported by the mi355x "
+                           "backend");
+      expect_word("across");
+      expect_word("dimensions");
+      expect("=");
+      op->l0 = int_list();
+      op->res_ty = signature(&op->bare_sig);
+      expect_word("reducer");
+      expect("(");
+      std::vector<int> args;
+      for (;;) {
+        args.push_back(define(value_name()));
+        expect(":");
+        type();
+        if (eat(")")) break;
+        expect(",");
+      }
+      op->region_args.push_back(args);
+      expect("{");
+      op->regions.emplace_back();
+      region_body(&op->regions.back());
+      return;
+    }
+    // pretty op: operands, then keyword attributes, an optional slice
+    // range list, then the signature
+    for (;;) {
+      ws();
+      if (peek('%')) {
+        op->arg.push_back(use_value());
+        if (eat(",")) continue;
+        break;
+      }
+      if (p_ < n_ && std::isalpha((unsigned char)s_[p_])) {
+        std::string k = word();
+        expect("=");
+        if (k == "dims") {
+          op->l0 = int_list();
+        } else if (k == "batching_dims") {
+          op->l0 = int_list();
+          expect_word("x");
+          op->l1 = int_list();
+        } else if (k == "contracting_dims") {
+          op->l2 = int_list();
+          expect_word("x");
+          op->l3 = int_list();
+        } else if (k == "dim") {
+          op->l0 = {integer()};
+        } else {
+          err("unknown keyword attribute '" + k + "' of " + op->name);
+        }
+        if (eat(",")) continue;
+        break;
+      }
+      break;
+    }
+    if (eat("[")) {  // slice: [start:limit(:stride), ...]
+      if (!eat("]")) {
+        for (;;) {
+          op->l0.push_back(integer());
+          expect(":");
+          op->l1.push_back(integer());
+          op->l2.push_back(eat(":") ? integer() : 1);
+          if (eat("]")) break;
+          expect(",");
+        }
+      }
+    }
+    op->res_ty = signature(&op->bare_sig);
+  }
+};
+
+// ---- translated form ----------------------------------------------------------------
+
+struct Step {
+  Node proto;  // prepared node: typed attributes set, no operands
+  std::vector<int> in, out;
+  std::vector<std::pair<int, Shape>> outs;
+};
+
+}  // namespace
+
+struct JitModule {
+  std::string name;
+  int n_slots = 0;
+  std::vector<int> arg_slot;
+  std::vector<std::pair<int, Shape>> arg_ty;
+  std::vector<std::pair<int, Tensor*>> consts;  // slot, tensor (one reference each)
+  std::vector<Step> steps;
+  std::vector<int> ret;
+  int64_t calls = 0;
+};
+
+namespace {
+
+std::string shape_text(const std::vector<int64_t>& d) {
+  std::string s = "[";
+  for (size_t i = 0; i < d.size(); ++i) s += (i ? "," : "") + std::to_string(d[i]);
+  return s + "]";
+}
+
+std::string type_text(int dt, const Shape& s) { return dt_enum_name(dt) + s.str(); }
+
+int64_t attr_int(const Op& op, const char* key, const std::string& who) {
+  for (auto& kv : op.attrs)
+    if (kv.first == key) {
+      const char* b = kv.second.c_str();
+      char* e = nullptr;
+      const long long v = std::strtoll(b, &e, 10);
+      if (e == b) invalid(who + ": attribute " + key + " is not an integer");
+      return (int64_t)v;
+    }
+  invalid(who + ": missing attribute " + key);
+}
+
+const char* binary_name(const std::string& m) {
+  static const std::unordered_map<std::string, const char*> t = {
+      {"stablehlo.add", "add"},         {"stablehlo.subtract", "sub"},
+      {"stablehlo.multiply", "mul"},    {"stablehlo.divide", "divide"},
+      {"stablehlo.maximum", "maximum"}, {"stablehlo.minimum", "minimum"},
+      {"stablehlo.power", "power"},     {"stablehlo.remainder", "remainder"},
+      {"stablehlo.atan2", "atan2"},     {"stablehlo.and", "bitwiseAnd"},
+      {"stablehlo.or", "bitwiseOr"},    {"stablehlo.xor", "bitwiseXor"},
+      {"stablehlo.shift_left", "shiftLeft"},
+      {"stablehlo.shift_right_arithmetic", "shiftRightArithmetic"},
+      {"stablehlo.shift_right_logical", "shiftRightLogical"}};
+  auto it = t.find(m);
+  return it == t.end() ? nullptr : it->second;
+}
+
+const char* unary_name(const std::string& m) {
+  static const std::unordered_map<std::string, const char*> t = {
+      {"stablehlo.negate", "neg"},
+      {"stablehlo.abs", "abs"},
+      {"stablehlo.exponential", "exp"},
+      {"stablehlo.log", "log"},
+      {"stablehlo.sqrt", "sqrt"},
+      {"stablehlo.rsqrt", "rsqrt"},
+      {"stablehlo.tanh", "tanh"},
+      {"stablehlo.logistic", "logistic"},
+      {"stablehlo.sine", "sine"},
+      {"stablehlo.cosine", "cosine"},
+      {"stablehlo.floor", "floor"},
+      {"stablehlo.ceil", "ceil"},
+      {"stablehlo.sign", "sign"},
+      {"stablehlo.cbrt", "cbrt"},
+      {"stablehlo.exponential_minus_one", "expm1"},
+      {"stablehlo.log_plus_one", "log1p"},
+      {"stablehlo.tan", "tan"},
+      {"stablehlo.round_nearest_afz", "roundNearestAfz"},
+      {"stablehlo.round_nearest_even", "roundNearestEven"},
+      {"stablehlo.not", "bitwiseNot"},
+      {"stablehlo.count_leading_zeros", "countLeadingZeros"},
+      {"stablehlo.popcnt", "popcnt"},
+      {"stablehlo.optimization_barrier", "optimizationBarrier"},
+      {"stablehlo.is_finite", "isFinite"}};
+  auto it = t.find(m);
+  return it == t.end() ? nullptr : it->second;
+}
+
+class Translator {
+ public:
+  Translator(Ctx* c, JitModule* m, const std::string& who) : c_(c), m_(m), who_(who) {}
+
+  void run(const Func& f, int n_parsed_slots) {
+    slot_dt_.assign(n_parsed_slots, -1);
+    slot_shape_.assign(n_parsed_slots, Shape());
+    alias_.assign(n_parsed_slots, -1);
+    is_const_.assign(n_parsed_slots, -1);
+    def_op_.assign(n_parsed_slots, -1);
+    for (size_t i = 0; i < f.ops.size(); ++i)
+      for (int r : f.ops[i].res) def_op_[r] = (int)i;
+    uses_.assign(n_parsed_slots, {});
+    for (size_t i = 0; i < f.ops.size(); ++i)
+      for (int a : f.ops[i].arg) uses_[a].push_back((int)i);
+    ret_use_.assign(n_parsed_slots, false);
+    for (int r : f.ret) ret_use_[r] = true;
+    redirect_.assign(f.ops.size(), -1);
+
+    for (size_t i = 0; i < f.args.size(); ++i) {
+      const Ty& t = f.arg_ty[i];
+      if (t.dt < 0) unsupported(who_ + ": argument type " + t.text + " not supported");
+      set_slot(f.args[i], t.dt, Shape(t.d));
+      m_->arg_slot.push_back(f.args[i]);
+      m_->arg_ty.push_back({t.dt, Shape(t.d)});
+    }
+    f_ = &f;
+    for (size_t i = 0; i < f.ops.size(); ++i) op(f.ops[i], (int)i);
+    for (int r : f.ret) m_->ret.push_back(resolve(r));
+    m_->n_slots = (int)slot_dt_.size();
+    prune();
+  }
+
+  ~Translator() {
+    for (Tensor* t : phantoms_) delete t;
+  }
+
+ private:
+  Ctx* c_;
+  JitModule* m_;
+  std::string who_;
+  const Func* f_ = nullptr;
+  std::vector<int> slot_dt_;
+  std::vector<Shape> slot_shape_;
+  std::vector<int> alias_, is_const_, def_op_, redirect_;
+  std::vector<std::vector<int>> uses_;
+  std::vector<bool> ret_use_;
+  std::vector<Tensor*> phantoms_;
+  std::unordered_map<std::string, std::pair<int, int>> topk_;  // (x, k, largest) -> slots
+
+  [[noreturn]] void fail_at(const Op& o, const std::string& m, int code = REW_MI355X_ERR_INVALID) {
+    fail(code, who_ + ": line " + std::to_string(o.line) + ": " + o.name + ": " + m);
+  }
+
+  int resolve(int s) const {
+    while (s < (int)alias_.size() && alias_[s] >= 0) s = alias_[s];
+    return s;
+  }
+  void set_slot(int s, int dt, Shape sh) {  // by value: sh may live in slot_shape_
+    if (s >= (int)slot_dt_.size()) {
+      slot_dt_.resize(s + 1, -1);
+      slot_shape_.resize(s + 1);
+      alias_.resize(s + 1, -1);
+      is_const_.resize(s + 1, -1);
+    }
+    slot_dt_[s] = dt;
+    slot_shape_[s] = sh;
+  }
+  int new_slot(int dt, const Shape& sh) {
+    const int s = (int)slot_dt_.size();
+    set_slot(s, dt, sh);
+    return s;
+  }
+  Tensor* phantom(int s) {
+    s = resolve(s);
+    Tensor* t = new Tensor();
+    t->ctx = c_;
+    t->dt = slot_dt_[s];
+    t->shape = slot_shape_[s];
+    phantoms_.push_back(t);
+    return t;
+  }
+
+  // Prepares eager op `name` over slots `in`; returns its output slots.
+  std::vector<int> step(const Op& o, const std::string& name, const std::vector<int>& in,
+                        const Attrs& attrs) {
+    std::vector<Tensor*> ph;
+    std::vector<int> rin;
+    for (int s : in) {
+      rin.push_back(resolve(s));
+      ph.push_back(phantom(s));
+    }
+    std::vector<std::pair<int, Shape>> outs;
+    Node* n = nullptr;
+    try {
+      n = prepare_node(c_, name, ph, attrs, &outs);
+    } catch (const Error& e) {
+      fail(e.code, who_ + ": line " + std::to_string(o.line) + ": " + o.name + ": " +
+                       e.what());
+    }
+    Step st;
+    st.proto = *n;
+    delete n;
+    st.proto.in.clear();
+    st.proto.out.clear();
+    st.in = rin;
+    for (auto& od : outs) st.out.push_back(new_slot(od.first, od.second));
+    st.outs = outs;
+    std::vector<int> res = st.out;
+    m_->steps.push_back(std::move(st));
+    return res;
+  }
+
+  // Binds the op's result slot r to `s` after checking the text's type.
+  void bind(const Op& o, size_t r, int s) {
+    s = resolve(s);
+    const Ty& t = o.res_ty[r];
+    if (t.dt != slot_dt_[s] || Shape(t.d) != slot_shape_[s])
+      fail_at(o, "result type " + t.text + " but the operands give " +
+                     type_text(slot_dt_[s], slot_shape_[s]));
+    set_slot(o.res[r], slot_dt_[s], slot_shape_[s]);
+    alias_[o.res[r]] = s;
+  }
+
+  int one(const Op& o, const std::string& name, const std::vector<int>& in,
+          const Attrs& attrs) {
+    std::vector<int> r = step(o, name, in, attrs);
+    bind(o, 0, r[0]);
+    return r[0];
+  }
+
+  void need_args(const Op& o, size_t n) {
+    if (o.arg.size() != n)
+      fail_at(o, "expected " + std::to_string(n) + " operand(s), got " +
+                     std::to_string(o.arg.size()));
+    if (o.res_ty.size() != 1) fail_at(o, "expected one result");
+  }
+
+  void constant(const Op& o) {
+    const Ty& t = o.res_ty.at(0);
+    const Shape s(t.d);
+    if (t.dt < 0 || t.dt == kC64 || t.dt == kC128 || t.dt == kI4 || t.dt == kU4 || t.dt == kNF4)
+      fail_at(o, "constant type " + t.text + " not supported", REW_MI355X_ERR_UNSUPPORTED);
+    const int64_t bytes = s.numel() * dt_size(t.dt);
+    std::string host;
+    if (o.splat) {
+      host.resize((size_t)bytes);
+      std::vector<uint8_t> one(dt_size(t.dt));
+      const double v = o.splat_v;
+      switch (t.dt) {
+        case kF32: { float f = (float)v; std::memcpy(one.data(), &f, 4); break; }
+        case kF64: std::memcpy(one.data(), &v, 8); break;
+        case kBF16: {
+          float f = (float)v;
+          uint32_t u;
+          std::memcpy(&u, &f, 4);
+          const uint16_t h = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+          std::memcpy(one.data(), &h, 2);
+          break;
+        }
+        case kF16: { _Float16 h = (_Float16)v; std::memcpy(one.data(), &h, 2); break; }
+        case kBool: one[0] = v != 0.0; break;
+        default: {
+          const int64_t iv = (int64_t)v;
+          std::memcpy(one.data(), &iv, one.size());  // little-endian truncation
+          break;
+        }
+      }
+      for (int64_t i = 0; i < s.numel(); ++i)
+        std::memcpy(&host[(size_t)(i * one.size())], one.data(), one.size());
+    } else {
+      if ((int64_t)o.bytes.size() != bytes)
+        fail_at(o, "dense data has " + std::to_string(o.bytes.size()) + " bytes, " + t.text +
+                       " needs " + std::to_string(bytes));
+      host = o.bytes;
+    }
+    Tensor* k = upload_tensor(c_, t.dt, s, host.data());
+    m_->consts.push_back({o.res[0], k});
+    set_slot(o.res[0], t.dt, s);
+    is_const_[o.res[0]] = (int)m_->consts.size() - 1;
+    const_bytes_.emplace(o.res[0], host);
+  }
+  std::unordered_map<int, std::string> const_bytes_;
+
+  // the reducer / comparator: one op over the region's arguments plus a
+  // stablehlo.return of its result
+  const Op* single_body(const Op& o, size_t region) {
+    const auto& body = o.regions.at(region);
+    if (body.size() != 2 || body[1].name != "stablehlo.return" || body[1].arg.size() != 1 ||
+        body[0].res.size() != 1 || body[1].arg[0] != body[0].res[0])
+      return nullptr;
+    return &body[0];
+  }
+
+  void reduce(const Op& o) {
+    need_args(o, 2);
+    const Op* b = single_body(o, 0);
+    const auto& ra = o.region_args.at(0);
+    static const std::unordered_map<std::string, const char*> red = {
+        {"stablehlo.add", "reduceSum"},     {"stablehlo.maximum", "reduceMax"},
+        {"stablehlo.minimum", "reduceMin"}, {"stablehlo.multiply", "reduceProd"},
+        {"stablehlo.and", "all"},           {"stablehlo.or", "any"}};
+    if (!b || ra.size() != 2 || b->arg.size() != 2 || !red.count(b->name) ||
+        !((b->arg[0] == ra[0] && b->arg[1] == ra[1]) || (b->arg[0] == ra[1] && b->arg[1] == ra[0])))
+      fail_at(o, "only reducers of one add/maximum/minimum/multiply/and/or are supported",
+              REW_MI355X_ERR_UNSUPPORTED);
+    const int x = o.arg[0], init = resolve(o.arg[1]);
+    std::string dims = shape_text(o.l0);
+    std::vector<int> r = step(o, red.at(b->name), {x}, {{"dims", dims}});
+    // init: the op's identity is dropped; anything else is combined after
+    bool identity = false;
+    auto cb = const_bytes_.find(init);
+    const int dt = slot_dt_[init];
+    if (cb != const_bytes_.end() && slot_shape_[init].rank == 0) {
+      const std::string& h = cb->second;
+      if (dt == kF32) {
+        float v;
+        uint32_t u;
+        std::memcpy(&v, h.data(), 4);
+        std::memcpy(&u, h.data(), 4);
+        if (b->name == "stablehlo.add") identity = u == 0u;
+        else if (b->name == "stablehlo.maximum") identity = std::isinf(v) && v < 0;
+        else if (b->name == "stablehlo.minimum") identity = std::isinf(v) && v > 0;
+        else if (b->name == "stablehlo.multiply") identity = v == 1.0f;
+      } else if (dt == kBool) {
+        identity = (b->name == "stablehlo.and") ? h[0] != 0 : h[0] == 0;
+      }
+    }
+    int out = r[0];
+    if (!identity) {
+      const Shape os = slot_shape_[out];
+      std::vector<int64_t> od(os.d, os.d + os.rank);
+      int bi = init;
+      if (os.rank > 0)
+        bi = step(o, "broadcastTo", {init},
+                  {{"output_shape", shape_text(od)}, {"broadcast_dimensions", "[]"}})[0];
+      out = step(o, binary_name(b->name), {out, bi}, {})[0];
+    }
+    bind(o, 0, out);
+  }
+
+  // (key operand, descending) of a one-compare comparator, or false
+  bool comparator(const Op& o, int* key, int* desc) {
+    const Op* b = single_body(o, 0);
+    const auto& ra = o.region_args.at(0);
+    if (!b || b->name != "stablehlo.compare" || b->arg.size() != 2) return false;
+    for (size_t j = 0; 2 * j + 1 < ra.size(); ++j) {
+      bool fwd = b->arg[0] == ra[2 * j] && b->arg[1] == ra[2 * j + 1];
+      bool rev = b->arg[0] == ra[2 * j + 1] && b->arg[1] == ra[2 * j];
+      if (!fwd && !rev) continue;
+      const std::string& d = b->word;
+      int dsc;
+      if (d == "LT" || d == "LE") dsc = 0;
+      else if (d == "GT" || d == "GE") dsc = 1;
+      else return false;
+      *key = (int)j;
+      *desc = rev ? 1 - dsc : dsc;
+      return true;
+    }
+    return false;
+  }
+
+  // k if op `op_index` slices the first k along `dim` (and nothing else)
+  // of a value of shape `s`, else -1.
+  int64_t head_slice(int op_index, int dim, const Shape& s) {
+    const Op& u = f_->ops[op_index];
+    if (u.name != "stablehlo.slice" || u.arg.size() != 1) return -1;
+    if ((int)u.l0.size() != s.rank) return -1;
+    for (int i = 0; i < s.rank; ++i) {
+      if (u.l0[i] != 0 || u.l2[i] != 1) return -1;
+      if (i != dim && u.l1[i] != s.d[i]) return -1;
+    }
+    return u.l1[dim];
+  }
+
+  // rew's traced topK (src/rew/ops/sort.nim:53-85): sort(x) and sort(x, iota)
+  // with a GE/LE comparator on x, each result read only through a slice of
+  // the first k along the sort dim.  Both become one topK node.
+  bool topk_peephole(const Op& o, int op_index, int dim, int key, int desc) {
+    if (key != 0 || o.arg.empty() || o.arg.size() > 2) return false;
+    const int x = resolve(o.arg[0]);
+    const Shape xs = slot_shape_[x];
+    if (slot_dt_[x] != kF32 || dim != xs.rank - 1 || xs.d[dim] > kTopkMaxCols) return false;
+    if (o.arg.size() == 2) {
+      const int io = def_op_.at(o.arg[1]);
+      if (io < 0) return false;
+      const Op& iota = f_->ops[io];
+      if (iota.name != "stablehlo.iota" || iota.res_ty[0].dt != kI32 ||
+          attr_int(iota, "iota_dimension", who_) != dim)
+        return false;
+    }
+    int64_t k = -1;
+    for (size_t r = 0; r < o.res.size(); ++r) {
+      if (ret_use_[o.res[r]]) return false;
+      for (int u : uses_[o.res[r]]) {
+        const int64_t kk = head_slice(u, dim, xs);
+        if (kk <= 0 || (k >= 0 && kk != k)) return false;
+        k = kk;
+      }
+    }
+    if (k <= 0 || k > 64) return false;
+    const std::string tk = std::to_string(x) + ":" + std::to_string(k) + ":" + std::to_string(desc);
+    auto it = topk_.find(tk);
+    std::pair<int, int> vi;
+    if (it != topk_.end()) {
+      vi = it->second;
+    } else {
+      std::vector<int> r = step(o, "topK", {x},
+                                {{"k", std::to_string(k)}, {"dimension", std::to_string(dim)},
+                                 {"largest", desc ? "true" : "false"}});
+      vi = {r[0], r[1]};
+      topk_.emplace(tk, vi);
+    }
+    for (size_t r = 0; r < o.res.size(); ++r)
+      for (int u : uses_[o.res[r]]) redirect_[u] = (r == 0) ? vi.first : vi.second;
+    (void)op_index;
+    return true;
+  }
+
+  void sort(const Op& o, int op_index) {
+    if (o.arg.empty() || o.res.size() != o.arg.size())
+      fail_at(o, "operand/result count mismatch");
+    int key = 0, desc = 0;
+    if (!comparator(o, &key, &desc))
+      fail_at(o, "only comparators of one LT/LE/GT/GE compare of an operand pair are supported",
+              REW_MI355X_ERR_UNSUPPORTED);
+    const Shape s0 = slot_shape_[resolve(o.arg[0])];
+    int64_t dim = attr_int(o, "dimension", who_);
+    if (dim < 0) dim += s0.rank;
+    if (dim < 0 || dim >= s0.rank) fail_at(o, "dimension out of range");
+    if (topk_peephole(o, op_index, (int)dim, key, desc)) return;
+    // sort along the last dim; other dims go through a transpose each way
+    std::vector<int> in(o.arg.begin(), o.arg.end());
+    std::vector<int64_t> perm;
+    const bool moved = dim != s0.rank - 1;
+    if (moved) {
+      for (int i = 0; i < s0.rank; ++i)
+        if (i != dim) perm.push_back(i);
+      perm.push_back(dim);
+      for (int& s : in) s = step(o, "transpose", {s}, {{"permutation", shape_text(perm)}})[0];
+    }
+    Attrs a = {{"dimension", std::to_string(s0.rank - 1)},
+               {"comparison_direction", desc ? "GT" : "LT"},
+               {"key", std::to_string(key)}};
+    std::vector<int> r = step(o, "sort", in, a);
+    if (moved) {
+      std::vector<int64_t> inv(perm.size());
+      for (size_t i = 0; i < perm.size(); ++i) inv[perm[i]] = (int64_t)i;
+      for (int& s : r) s = step(o, "transpose", {s}, {{"permutation", shape_text(inv)}})[0];
+    }
+    for (size_t i = 0; i < r.size(); ++i) bind(o, i, r[i]);
+  }
+
+  void op(const Op& o, int index) {
+    const std::string& n = o.name;
+    if (redirect_[index] >= 0) {  // a slice the topK peephole answers
+      bind(o, 0, redirect_[index]);
+      return;
+    }
+    if (const char* b = binary_name(n)) {
+      need_args(o, 2);
+      one(o, b, o.arg, {});
+      return;
+    }
+    if (const char* u = unary_name(n)) {
+      need_args(o, 1);
+      one(o, u, o.arg, {});
+      return;
+    }
+    const Ty* rt = o.res_ty.empty() ? nullptr : &o.res_ty[0];
+    if (n == "stablehlo.constant") {
+      if (!o.arg.empty() || o.res_ty.size() != 1) fail_at(o, "malformed constant");
+      constant(o);
+    } else if (n == "stablehlo.convert") {
+      need_args(o, 1);
+      if (rt->dt < 0) fail_at(o, "unsupported result type", REW_MI355X_ERR_UNSUPPORTED);
+      one(o, "astype", o.arg, {{"dtype", dt_enum_name(rt->dt)}});
+    } else if (n == "stablehlo.bitcast_convert") {
+      need_args(o, 1);
+      one(o, "bitcastConvert", o.arg,
+          {{"dtype", dt_enum_name(rt->dt)}, {"shape", shape_text(rt->d)}});
+    } else if (n == "stablehlo.reshape") {
+      need_args(o, 1);
+      one(o, "reshape", o.arg, {{"shape", shape_text(rt->d)}});
+    } else if (n == "stablehlo.transpose") {
+      need_args(o, 1);
+      one(o, "transpose", o.arg, {{"permutation", shape_text(o.l0)}});
+    } else if (n == "stablehlo.reverse") {
+      need_args(o, 1);
+      one(o, "reverse", o.arg, {{"dimensions", shape_text(o.l0)}});
+    } else if (n == "stablehlo.broadcast_in_dim") {
+      need_args(o, 1);
+      one(o, "broadcastTo", o.arg,
+          {{"output_shape", shape_text(rt->d)}, {"broadcast_dimensions", shape_text(o.l0)}});
+    } else if (n == "stablehlo.slice") {
+      need_args(o, 1);
+      one(o, "slice", o.arg,
+          {{"start_indices", shape_text(o.l0)}, {"limit_indices", shape_text(o.l1)},
+           {"strides", shape_text(o.l2)}});
+    } else if (n == "stablehlo.concatenate") {
+      if (o.arg.empty() || o.res_ty.size() != 1) fail_at(o, "malformed concatenate");
+      if (o.l0.size() != 1) fail_at(o, "missing dim");
+      one(o, "concat", o.arg, {{"dimension", std::to_string(o.l0[0])}});
+    } else if (n == "stablehlo.iota") {
+      if (!o.arg.empty() || o.res_ty.size() != 1) fail_at(o, "malformed iota");
+      if (rt->dt < 0) fail_at(o, "unsupported result type", REW_MI355X_ERR_UNSUPPORTED);
+      one(o, "iota", {},
+          {{"dtype", dt_enum_name(rt->dt)}, {"shape", shape_text(rt->d)},
+           {"dimension", std::to_string(attr_int(o, "iota_dimension", who_))}});
+    } else if (n == "stablehlo.compare") {
+      need_args(o, 2);
+      one(o, "compare", o.arg, {{"comparison_direction", o.word}});
+    } else if (n == "stablehlo.select") {
+      need_args(o, 3);
+      one(o, "select", o.arg, {});
+    } else if (n == "stablehlo.clamp") {
+      need_args(o, 3);
+      one(o, "clamp", o.arg, {});
+    } else if (n == "stablehlo.dot_general") {
+      need_args(o, 2);
+      one(o, "dotGeneral", o.arg,
+          {{"lhs_batching", shape_text(o.l0)}, {"rhs_batching", shape_text(o.l1)},
+           {"lhs_contracting", shape_text(o.l2)}, {"rhs_contracting", shape_text(o.l3)}});
+    } else if (n == "stablehlo.dot") {
+      need_args(o, 2);
+      one(o, "dot", o.arg, {});
+    } else if (n == "stablehlo.torch_index_select") {
+      need_args(o, 2);
+      one(o, "torchIndexSelect", o.arg,
+          {{"dim", std::to_string(attr_int(o, "dim", who_))},
+           {"batch_dims", std::to_string(attr_int(o, "batch_dims", who_))}});
+    } else if (n == "stablehlo.reduce") {
+      reduce(o);
+    } else if (n == "stablehlo.sort") {
+      sort(o, index);
+    } else {
+      fail_at(o, "op not supported by the mi355x jit path", REW_MI355X_ERR_UNSUPPORTED);
+    }
+  }
+
+  // Drops steps none of whose outputs reach a func.return.
+  void prune() {
+    std::vector<bool> live(m_->n_slots, false);
+    for (int r : m_->ret) live[r] = true;
+    std::vector<Step> kept;
+    for (size_t i = m_->steps.size(); i-- > 0;) {
+      Step& st = m_->steps[i];
+      bool any = false;
+      for (int o : st.out) any = any || live[o];
+      if (!any) continue;
+      for (int s : st.in) live[s] = true;
+      kept.push_back(std::move(st));
+    }
+    m_->steps.assign(std::make_move_iterator(kept.rbegin()),
+                     std::make_move_iterator(kept.rend()));
+    std::vector<std::pair<int, Tensor*>> consts;
+    for (auto& kc : m_->consts) {
+      if (live[kc.first]) {
+        consts.push_back(kc);
+      } else {
+        kc.second->ext--;
+        maybe_destroy(kc.second);
+      }
+    }
+    m_->consts.swap(consts);
+  }
+};
+
+uint64_t text_hash(const char* s, size_t n) {
+  uint64_t h = 0x243f6a8885a308d3ull ^ (uint64_t)n;
+  size_t i = 0;
+  for (; i + 8 <= n; i += 8) {
+    uint64_t w;
+    std::memcpy(&w, s + i, 8);
+    h = (h ^ w) * 0x9e3779b97f4a7c15ull;
+    h ^= h >> 29;
+  }
+  uint64_t w = 0;
+  std::memcpy(&w, s + i, n - i);
+  h = (h ^ w) * 0x9e3779b97f4a7c15ull;
+  h ^= h >> 32;
+  return h;
+}
+
+void destroy_module(JitModule* m) {
+  for (auto& kc : m->consts) {
+    kc.second->ext--;
+    maybe_destroy(kc.second);
+  }
+  delete m;
+}
+
+JitModule* compile_module(Ctx* c, const std::string& who, const char* text, size_t len) {
+  Parser p(text, len, who);
+  std::vector<Func> fs = p.module();
+  const Func* f = nullptr;
+  for (auto& x : fs)
+    if (x.name == "main") f = &x;
+  if (!f) {
+    for (auto& x : fs)
+      if (!x.is_private) {
+        f = &x;
+        break;
+      }
+  }
+  if (!f) invalid(who + ": module has no public function");
+  for (auto& x : fs)
+    if (&x != f)
+      unsupported(who + ": modules with more than one function are not supported");
+  std::unique_ptr<JitModule> m(new JitModule());
+  m->name = who;
+  try {
+    Translator t(c, m.get(), who);
+    t.run(*f, p.slots());
+  } catch (...) {
+    for (auto& kc : m->consts) {
+      kc.second->ext--;
+      maybe_destroy(kc.second);
+    }
+    m->consts.clear();
+    throw;
+  }
+  return m.release();
+}
+
+}  // namespace
+
+std::vector<Tensor*> jit_module_run(Ctx* c, const std::string& name, const std::string& cache_key,
+                             const char* text, size_t len, const std::vector<Tensor*>& ins) {
+  const std::string who = "jit '" + name + "'";
+  std::string key = std::to_string(c->ordinal) + "::" + name + "::" + cache_key + "::";
+  char hx[17];
+  std::snprintf(hx, sizeof hx, "%016llx", (unsigned long long)text_hash(text, len));
+  key += hx;
+  auto it = c->jit_modules.find(key);
+  JitModule* m;
+  if (it != c->jit_modules.end()) {
+    m = it->second;
+    c->stats.jit_module_hits++;
+  } else {
+    m = compile_module(c, who, text, len);
+    c->jit_modules.emplace(key, m);
+    c->stats.jit_module_compiles++;
+  }
+  if (ins.size() != m->arg_slot.size())
+    invalid(who + ": module takes " + std::to_string(m->arg_slot.size()) + " input(s), got " +
+            std::to_string(ins.size()));
+  for (size_t i = 0; i < ins.size(); ++i)
+    if (ins[i]->dt != m->arg_ty[i].first || ins[i]->shape != m->arg_ty[i].second)
+      invalid(who + ": input " + std::to_string(i) + " is " + type_text(ins[i]->dt, ins[i]->shape) +
+              ", the module expects " + type_text(m->arg_ty[i].first, m->arg_ty[i].second));
+  m->calls++;
+  std::vector<Tensor*> v(m->n_slots, nullptr);
+  for (size_t i = 0; i < ins.size(); ++i) v[m->arg_slot[i]] = ins[i];
+  for (auto& kc : m->consts) v[kc.first] = kc.second;
+  std::vector<Tensor*> made;
+  made.reserve(m->steps.size() * 2);
+  std::vector<Tensor*> in;
+  try {
+    for (const Step& st : m->steps) {
+      in.clear();
+      for (int s : st.in) in.push_back(v[s]);
+      Node* n = new Node(st.proto);
+      std::vector<Tensor*> outs = commit_node(c, n, in, st.outs);
+      for (size_t j = 0; j < outs.size(); ++j) {
+        v[st.out[j]] = outs[j];
+        made.push_back(outs[j]);
+      }
+    }
+  } catch (...) {
+    for (Tensor* t : made) {
+      t->ext--;
+      maybe_destroy(t);
+    }
+    throw;
+  }
+  std::vector<Tensor*> res;
+  for (int r : m->ret) {
+    Tensor* t = v[r];
+    t->ext++;
+    res.push_back(t);
+  }
+  for (Tensor* t : made) {
+    t->ext--;
+    maybe_destroy(t);
+  }
+  return res;
+}
+
+void jit_module_cache_clear(Ctx* c) {
+  for (auto& kv : c->jit_modules) destroy_module(kv.second);
+  c->jit_modules.clear();
+}
+
+}  // namespace rew

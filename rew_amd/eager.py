@@ -20,6 +20,7 @@ from __future__ import annotations
 import ctypes as C
 import enum
 import threading
+import weakref
 from typing import Callable, Iterable, Sequence
 
 import numpy as np
@@ -41,6 +42,14 @@ class TensorError(ValueError):
 
 class BufferReleasedError(EagerError):
     """Use of a handle after its last release (src/rew/buffer.nim:166-173)."""
+
+
+class TensorModeError(TensorError):
+    """A trace tensor and an eager tensor met inside an op (src/rew/tensor.nim:37-40)."""
+
+
+class BufferDonatedError(RuntimeError):
+    """Use of an input buffer donated to a jit call (src/rew/buffer.nim:38, 146-164)."""
 
 
 class DType(enum.IntEnum):
@@ -233,6 +242,31 @@ class Tensor:
         return f"Tensor({self.dtype.enum_name}, {list(self.shape)}, {self.device})"
 
 
+# tensors whose buffers went to a jit call as donations, with the consumer
+_donated: "weakref.WeakKeyDictionary[Tensor, str]" = weakref.WeakKeyDictionary()
+
+
+def markDonated(t: Tensor, consumer: str) -> None:
+    """Hands t's buffer to `consumer` (src/rew/buffer.nim:146-156): the
+    native reference is dropped and later use raises BufferDonatedError."""
+    _donated[t] = consumer
+    h, t.handle = t.handle, None
+    if h and _lib._lib is not None:
+        _lib._lib.rew_mi355x_release(h)
+
+
+def _raise_released(t: Tensor, what: str):
+    """src/rew/buffer.nim:158-173 (requireLive); a trace tensor here is the
+    mode error of requireEager (src/rew/tensor.nim:93-100)."""
+    if hasattr(t, "traceId"):
+        raise TensorModeError(f"{what}: expected an eager tensor, got a trace tensor")
+    by = _donated.get(t)
+    if by is not None:
+        raise BufferDonatedError(
+            f"{what}: buffer has been donated and may no longer be used (donated to: {by})")
+    raise BufferReleasedError(f"{what}: tensor already released")
+
+
 def _wrap(handle: int, d: Device) -> Tensor:
     lib = _lib.load()
     dt = C.c_int()
@@ -288,7 +322,7 @@ def toHost(t: Tensor) -> np.ndarray:
     ``bf16_bits_to_f32`` to widen.
     """
     if t.handle is None:
-        raise BufferReleasedError("toHost: tensor already released")
+        _raise_released(t, "toHost")
     out = np.empty(t.shape, dtype=_NP[t.dtype])
     _check(_lib.load().rew_mi355x_to_host(t.handle, out.ctypes.data_as(C.c_void_p),
                                            out.nbytes))
@@ -309,7 +343,7 @@ def empty(dtype: DType, shape: Sequence[int], device: Device | None = None) -> T
 def devicePtr(t: Tensor) -> int:
     """Device address of t's storage (rew_mi355x_buf_device_ptr; flushes t's producer)."""
     if t.handle is None:
-        raise BufferReleasedError("devicePtr: tensor already released")
+        _raise_released(t, "devicePtr")
     p = C.c_void_p()
     _check(_lib.load().rew_mi355x_buf_device_ptr(t.handle, C.byref(p)))
     return int(p.value or 0)
@@ -462,7 +496,7 @@ def executeMi355xOp(op: str, operands: Sequence[Tensor],
         if t.device is not d and t.device != d:
             raise EagerError(f"eager '{op}': cross-device operands forbidden")
         if t.handle is None:
-            raise BufferReleasedError(f"eager '{op}': tensor already released")
+            _raise_released(t, f"eager '{op}'")
     lib = _lib.load()
     sc = _scratch
     n, na = len(operands), len(attrs)

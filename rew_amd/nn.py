@@ -406,3 +406,30 @@ class DeepSeekMoE:
         return out
 
     forward_dense = forward
+
+
+# ---- parameter lists for jit / lazy ----------------------------------------------------
+# rew's jit traces a function of tensors only (an eager tensor closed over by
+# a traced function is a mode error, src/rew/tensor.nim:177-186), so a layer
+# runs under jit/lazy with its parameters passed as arguments and rebuilt
+# from the argument list inside the traced function.
+
+def moeParams(moe: "DeepSeekMoE") -> list:
+    """The router's weight and bias, then every expert's gate/up/down
+    weight and bias (shared experts first)."""
+    out = [moe.gate.weight, moe.gate.bias]
+    for e in list(moe.sharedExperts) + list(moe.routedExperts):
+        for lin in (e.gateProj, e.upProj, e.downProj):
+            out += [lin.weight, lin.bias]
+    return out
+
+
+def moeFromParams(params, numShared: int, numRouted: int, numExpertsPerTok: int) -> "DeepSeekMoE":
+    """Inverse of moeParams."""
+    p = list(params)
+    gate = Linear(p[0], p[1])
+    experts = []
+    for i in range(numShared + numRouted):
+        q = p[2 + 6 * i: 8 + 6 * i]
+        experts.append(DeepSeekExpert(Linear(q[0], q[1]), Linear(q[2], q[3]), Linear(q[4], q[5])))
+    return DeepSeekMoE(gate, experts[:numShared], experts[numShared:], numExpertsPerTok)

@@ -15,6 +15,7 @@ from typing import Sequence
 
 import numpy as np
 
+from . import jit as _jit
 from .eager import (DType, Device, Tensor, TensorError, defaultDevice, dispatchEager,
                     fromHost)
 
@@ -28,6 +29,8 @@ def _nimseq(xs: Sequence[int]) -> str:
 
 
 def _one(op, operands, attrs=()):
+    if _jit._tls.__dict__.get("trace") is not None:   # trace mode: build the op
+        return _jit.traceOp(op, operands, attrs)[0]
     outs = dispatchEager(op, operands, attrs)
     assert len(outs) == 1, f"{op}: eager backend returned wrong arity"
     return outs[0]
@@ -46,14 +49,20 @@ def _same(a: Tensor, b: Tensor, op: str):
 # ---- literals (src/rew/ops/literal.nim:56-194) -------------------------------------
 
 def constant(dtype: DType, shape: Sequence[int], data, device: Device | None = None) -> Tensor:
+    if _jit.currentMode() == "trace":
+        return _jit.traceConstant(dtype, shape, data)
     return fromHost(np.asarray(data), dtype=dtype, shape=shape, device=device)
 
 
 def scalarF32(v: float, device: Device | None = None) -> Tensor:
+    if _jit.currentMode() == "trace":
+        return _jit.traceConstant(DType.FLOAT32, (), np.float32(v))
     return fromHost(np.array(v, dtype=np.float32), DType.FLOAT32, (), device)
 
 
 def scalarI32(v: int, device: Device | None = None) -> Tensor:
+    if _jit.currentMode() == "trace":
+        return _jit.traceConstant(DType.INT32, (), np.int32(v))
     return fromHost(np.array(v, dtype=np.int32), DType.INT32, (), device)
 
 
@@ -62,6 +71,8 @@ def constantF32(shape: Sequence[int], data, device: Device | None = None) -> Ten
     n = int(np.prod(shape)) if len(shape) else 1
     if a.size != n:
         raise TensorError(f"constantF32: data length {a.size} does not match shape product {n}")
+    if _jit.currentMode() == "trace":
+        return _jit.traceConstant(DType.FLOAT32, shape, a)
     return fromHost(a, DType.FLOAT32, shape, device)
 
 
@@ -124,6 +135,13 @@ floor = _unary("floor")
 ceil = _unary("ceil")
 sign = _unary("sign")
 isFinite = _unary("isFinite")
+cbrt = _unary("cbrt")
+expm1 = _unary("expm1")
+log1p = _unary("log1p")
+tan = _unary("tan")
+roundNearestAfz = _unary("roundNearestAfz")
+roundNearestEven = _unary("roundNearestEven")
+bitwiseNot = _unary("bitwiseNot")
 
 
 def astype(a: Tensor, dtype: DType) -> Tensor:
@@ -284,6 +302,14 @@ def argmax(t: Tensor, dim: int) -> Tensor:
     pos = dim + len(t.shape) if dim < 0 else dim
     if pos < 0 or pos >= len(t.shape):
         raise TensorError(f"argmax: dim {dim} out of range for rank {len(t.shape)}")
+    if _jit.currentMode() == "trace":
+        # rew's composite, which stops at the int32 reduceMin as rew's does
+        m = reduceMax(t, [pos])
+        mask = compare(t, broadcastTo(m, t.shape, [i for i in range(len(t.shape)) if i != pos]),
+                       "EQ")
+        ids = iota(DType.INT32, t.shape, pos, t.device)
+        big = broadcastTo(scalarI32(2**31 - 1, t.device), t.shape, [])
+        return reduceMin(select(mask, ids, big), [pos])
     return _one("argmax", [t], [("dimension", str(pos))])
 
 
@@ -297,9 +323,35 @@ def topK(operand: Tensor, k: int, dimension: int = -1, largest: bool = True):
     d = dimension + rank if dimension < 0 else dimension
     if k > operand.shape[d]:
         raise TensorError(f"topK: k {k} > dim size {operand.shape[d]}")
+    if _jit.currentMode() == "trace":
+        return _jit.traceTopK(operand, k, d, largest)
     outs = dispatchEager("topK", [operand], [("k", str(k)), ("dimension", str(d)),
                                              ("largest", "true" if largest else "false")])
     return outs[0], outs[1]
+
+
+def sort(operand: Tensor, dimension: int = -1, isStable: bool = False,
+         comparator: str = "LT", *others: Tensor):
+    """Sorts along ``dimension`` (src/rew/ops/sort.nim:13-33).  rew takes the
+    comparator as a builder callback; here it is the one compare direction
+    such a callback emits on the operand pair ("LT"/"LE" ascending, "GT"/"GE"
+    descending).  ``others`` are permuted along with ``operand`` (the
+    multi-operand form of stablehlo.sort).  Trace-only in the reference; the
+    backend also runs it eagerly (stable, NaN last)."""
+    if comparator not in ("LT", "LE", "GT", "GE"):
+        raise TensorError(f"sort: comparator must be LT, LE, GT or GE, got '{comparator}'")
+    rank = len(operand.shape)
+    d = dimension + rank if dimension < 0 else dimension
+    if d < 0 or d >= rank:
+        raise TensorError(f"sort: dimension {dimension} out of range for rank {rank}")
+    ins = [operand, *others]
+    if _jit.currentMode() == "trace":
+        res = _jit.traceSort(ins, d, isStable, comparator)
+    else:
+        res = dispatchEager("sort", ins, [("dimension", str(d)),
+                                          ("comparison_direction", comparator),
+                                          ("is_stable", "true" if isStable else "false")])
+    return res[0] if not others else res
 
 
 # ---- linear algebra (src/rew/ops/linalg.nim:204-256, 432-461) -------------------------

@@ -24,7 +24,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(lib, n), f"librew_mi355x.so does not export {n}"
     assert set(names) == set(_lib.SIGNATURES), "ctypes table out of sync with the header"
-    assert lib.rew_mi355x_abi_version() == 1
+    assert lib.rew_mi355x_abi_version() == 2
 
 
 def test_rng_matches_oracle(oracle):

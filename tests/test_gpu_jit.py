@@ -1,0 +1,230 @@
+"""GPU checks of jit/lazy execution through rew_mi355x_execute_jit.
+
+The cases follow rew's tests/tjit_execute.nim:78-302 (eager vs jit on the
+same inputs) for the ops this backend implements, plus:
+
+* the row sort (stablehlo.sort; src/rew/ops/sort.nim:13-33) against numpy's
+  stable argsort (NaN last, -0 == +0), along the last dim and along dim 0,
+  ascending and descending, with a carried operand;
+* rew's traced topK (sort + slice, src/rew/ops/sort.nim:53-85) equal to the
+  eager topK bit for bit and served by the one topK kernel;
+* DeepSeekMoE.forward under lazy (its only executable form in rew, since
+  topK is trace-only) equal to the eager forward bit for bit, through the
+  routed kernels;
+* module cache, donation, input checking and unsupported-op errors.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+from rew_amd import eager as E
+from rew_amd import jit as J
+from rew_amd import nn
+from rew_amd import ops as O
+from rew_amd.eager import DType
+
+from test_gpu_moe import build_moe
+
+
+def f32(x):
+    return E.fromHost(np.asarray(x, np.float32))
+
+
+def close(got, want, tol=1e-4):
+    # tjit_execute.nim:72-75
+    got, want = np.asarray(got), np.asarray(want)
+    assert got.shape == want.shape
+    np.testing.assert_allclose(got, want, rtol=0, atol=tol)
+
+
+def test_add_pair_twice_one_module(gpu):
+    # tjit_execute.nim:84-97
+    E.resetStats()
+    j = J.jit(lambda a: [O.add(a[0], a[1])], "addPair")
+    a, b = f32([1, 2, 3, 4]), f32([10, 20, 30, 40])
+    outs = j.call([a, b])
+    assert len(outs) == 1 and outs[0].shape == (4,)
+    assert E.toHost(outs[0]).tolist() == [11, 22, 33, 44]
+    assert E.toHost(j.call([a, b])[0]).tolist() == [11, 22, 33, 44]
+    assert j.cacheSize() == 1
+    s = E.stats()
+    assert s["jit_module_compiles"] == 1 and s["jit_module_hits"] == 1
+
+
+def test_lazy_batch_execute(gpu):
+    # tjit_execute.nim:99-112
+    def f(a):
+        y = O.add(a[0], a[1])
+        return [O.mul(y, y)]
+    lz = J.lazy(f, "lazyBatchExecute")
+    outs = lz.call([f32([1, 2, 3, 4]), f32([10, 20, 30, 40])])
+    close(E.toHost(outs[0]), [121, 484, 1089, 1936])
+    assert lz.cacheSize() == 1
+
+
+def test_unary_eager_vs_jit(gpu):
+    # tjit_execute.nim:114-125
+    def f(a):
+        x = a[0]
+        return [O.cbrt(x), O.ceil(x), O.expm1(x), O.floor(x), O.log1p(x), O.logistic(x),
+                O.tan(x), O.sign(x), O.roundNearestAfz(x), O.roundNearestEven(x)]
+    x = f32([0.25, 0.5, 1.0, 1.5])
+    eager = f([x])
+    got = J.jit(f, "openxlaUnary").call([x])
+    assert len(got) == len(eager)
+    for g, e in zip(got, eager):
+        close(E.toHost(g), E.toHost(e))
+
+
+def test_binary_eager_vs_jit(gpu):
+    # tjit_execute.nim:127-138
+    f = lambda a: [O.atan2(a[0], a[1]), O.power(a[0], a[1]), O.remainder(a[0], a[1])]
+    a, b = f32([1.5, 2.0, 2.5, 3.0]), f32([2.0, 3.0, 2.0, 2.0])
+    for g, e in zip(J.jit(f, "openxlaBinary").call([a, b]), f([a, b])):
+        close(E.toHost(g), E.toHost(e))
+
+
+def test_clamp_scalar_bounds_eager_vs_jit(gpu):
+    # tjit_execute.nim:140-151
+    f = lambda a: [O.clamp(a[1], a[0], a[2])]
+    ins = [f32([1, 2, 3, 4]), O.scalarF32(1.5), O.scalarF32(3.5)]
+    got = J.jit(f, "clampScalarBounds").call(ins)
+    assert got[0].shape == (4,)
+    close(E.toHost(got[0]), E.toHost(f(ins)[0]))
+
+
+def test_dot_eager_vs_jit(gpu):
+    # tjit_execute.nim:277-285 (exact equality)
+    f = lambda a: [O.dot(O.reshape(a[0], [2, 2]), O.reshape(a[1], [2, 2]))]
+    a, b = f32([1, 2, 3, 4]), f32([10, 20, 30, 40])
+    assert E.toHost(J.jit(f, "dot").call([a, b])[0]).tolist() == E.toHost(f([a, b])[0]).tolist()
+
+
+def test_bitwise_eager_vs_jit(gpu):
+    # tjit_execute.nim:287-302
+    f = lambda a: [O.bitwiseAnd(a[0], a[1]), O.bitwiseOr(a[0], a[1]), O.bitwiseXor(a[0], a[1]),
+                   O.bitwiseNot(a[0])]
+    x = E.fromHost(np.array([0x0F, 0xF0, 0xAA, 0x55], np.uint32))
+    y = E.fromHost(np.array([0xFF, 0x0F, 0x0F, 0xF0], np.uint32))
+    for g, e in zip(J.jit(f, "openxlaBitwise").call([x, y]), f([x, y])):
+        assert E.toHost(g).tolist() == E.toHost(e).tolist()
+
+
+def _np_sort(x, axis, descending):
+    """Stable order: NaN last, -0 == +0 (the comparator's equivalence)."""
+    key = np.where(x == 0, 0, x).astype(np.float64) if x.dtype.kind == "f" else x.astype(np.int64)
+    if descending:
+        key = -key
+    return np.argsort(key, axis=axis, kind="stable")
+
+
+@pytest.mark.parametrize("rows,cols,axis", [(5, 7, 1), (3, 64, 1), (2, 300, 1), (4, 4100, 1),
+                                            (37, 6, 0)])
+@pytest.mark.parametrize("direction", ["LT", "GE"])
+def test_sort_against_stable_argsort(gpu, rows, cols, axis, direction):
+    rs = np.random.default_rng(rows * 131 + cols)
+    x = rs.integers(-4, 5, size=(rows, cols)).astype(np.float32)   # many ties
+    x[rs.random(x.shape) < 0.05] = np.nan
+    x[rs.random(x.shape) < 0.05] = -0.0
+    ids = np.broadcast_to(np.arange(x.shape[axis], dtype=np.int32).reshape(
+        (-1, 1) if axis == 0 else (1, -1)), x.shape).copy()
+    f = lambda a: list(O.sort(a[0], axis, True, direction, a[1]))
+    vals, idx = J.jit(f, f"sort{axis}{direction}").call([E.fromHost(x), E.fromHost(ids)])
+    order = _np_sort(x, axis, direction in ("GT", "GE"))
+    np.testing.assert_array_equal(E.toHost(idx), np.take_along_axis(ids, order, axis))
+    np.testing.assert_array_equal(E.toHost(vals).view(np.uint32),
+                                  np.take_along_axis(x, order, axis).view(np.uint32))
+    if axis == x.ndim - 1:   # the eager extension op (last dim) gives the same bits
+        ev, ei = O.sort(E.fromHost(x), axis, True, direction, E.fromHost(ids))
+        np.testing.assert_array_equal(E.toHost(ei), E.toHost(idx))
+
+
+@pytest.mark.parametrize("dt", [DType.BFLOAT16, DType.INT32])
+def test_sort_key_dtypes(gpu, dt):
+    rs = np.random.default_rng(7)
+    x = rs.integers(-1000, 1000, size=(9, 333)).astype(np.float32)
+    t = E.fromHost(x, dt) if dt == DType.BFLOAT16 else E.fromHost(x.astype(np.int32))
+    got = E.toHost(O.sort(t, -1, True, "GT"))
+    ref = x if dt == DType.BFLOAT16 else x.astype(np.int32)
+    want = np.take_along_axis(ref, _np_sort(ref, 1, True), 1)
+    if dt == DType.BFLOAT16:
+        got = E.bf16_bits_to_f32(got)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_traced_topk_equals_eager_topk(gpu):
+    rs = np.random.default_rng(3)
+    p = rs.random((513, 64)).astype(np.float32)
+    p[5, 10] = p[5, 20]   # an exact tie: lower index first
+    xt = E.fromHost(p)
+    j = J.jit(lambda a: list(O.topK(nn.softmax(a[0], 1), 6, 1, True)), "topk")
+    E.profileBegin()
+    tv, ti = j.call([xt])
+    tv, ti = E.toHost(tv), E.toHost(ti)
+    names = [n for n, _, _ in E.profileEnd()]
+    assert any(n.startswith("topk{") for n in names), names
+    assert not any(n.startswith("sort{") for n in names), names
+    ev, ei = O.topK(nn.softmax(xt, 1), 6, 1, True)
+    np.testing.assert_array_equal(ti, E.toHost(ei))
+    np.testing.assert_array_equal(tv.view(np.uint32), E.toHost(ev).view(np.uint32))
+
+
+def test_moe_lazy_equals_eager(gpu, oracle):
+    T, H, I, E_, k, S = 256, 256, 128, 16, 4, 2
+    moe, host = build_moe(oracle, T, H, I, E_, k, S, 0x5EED0505)
+    xt = E.fromHost(host["x"], DType.BFLOAT16)
+    params = nn.moeParams(moe)
+    lz = J.lazy(lambda a: [nn.moeFromParams(a[1:], S, E_, k).forward(a[0])], "deepseekMoE")
+    E.profileBegin()
+    got = E.toHost(lz.call([xt] + params)[0])
+    names = [n for n, _, _ in E.profileEnd()]
+    assert any(n.startswith("moe_gemm_swiglu") for n in names), names
+    assert any(n.startswith("topk{") for n in names), names
+    want = E.toHost(moe.forward(xt))
+    np.testing.assert_array_equal(got, want)
+    again = E.toHost(lz.call([xt] + params)[0])
+    np.testing.assert_array_equal(again, want)
+    assert lz.cacheSize() == 1
+
+
+def test_reduce_with_a_non_identity_init(gpu):
+    text = """module @trace_module {
+  func.func @main(%v1: tensor<4x3xf32>) -> tensor<4xf32> {
+    %v2 = stablehlo.constant dense<"0x00002041"> : tensor<f32>
+    %v6 = stablehlo.reduce(%v1 init: %v2) across dimensions = [1] : (tensor<4x3xf32>, tensor<f32>) -> tensor<4xf32>
+      reducer(%v3: tensor<f32>, %v4: tensor<f32>) {
+        %v5 = stablehlo.add %v3, %v4 : tensor<f32>
+        stablehlo.return %v5 : tensor<f32>
+      }
+    func.return %v6 : tensor<4xf32>
+  }
+}
+"""
+    x = np.arange(12, dtype=np.float32).reshape(4, 3)
+    (r,) = J.executeJit("reduceInit", "k", text, [E.fromHost(x)], [DType.FLOAT32], [[4]])
+    np.testing.assert_array_equal(E.toHost(r), x.sum(1) + 10.0)
+
+
+def test_donated_input_is_rejected_afterwards(gpu):
+    j = J.jit(lambda a: [O.add(a[0], a[0])], "donate", donateArgs=[0])
+    x = f32([1, 2])
+    y = j.call([x])[0]
+    assert E.toHost(y).tolist() == [2, 4]
+    with pytest.raises(E.BufferDonatedError, match="donated to: jit 'donate'"):
+        E.toHost(x)
+
+
+def test_input_mismatch_and_unsupported_op(gpu):
+    text = J.jit(lambda a: [O.neg(a[0])], "neg").executableText([f32([1, 2])])
+    with pytest.raises(E.EagerError, match="input 0 is dtFloat32\\[3\\], the module expects"):
+        J.executeJit("neg", "k", text, [f32([1, 2, 3])], [DType.FLOAT32], [[3]])
+    bad = """module @m {
+  func.func @main(%v1: tensor<2xf32>) -> tensor<2xf32> {
+    %v2 = stablehlo.fft %v1 : tensor<2xf32>
+    func.return %v2 : tensor<2xf32>
+  }
+}
+"""
+    with pytest.raises(E.EagerError, match="line 3: stablehlo.fft: op not supported"):
+        J.executeJit("fft", "k", bad, [f32([1, 2])], [DType.FLOAT32], [[2]])
