@@ -146,7 +146,8 @@ def test_sort_key_dtypes(gpu, dt):
     x = rs.integers(-1000, 1000, size=(9, 333)).astype(np.float32)
     t = E.fromHost(x, dt) if dt == DType.BFLOAT16 else E.fromHost(x.astype(np.int32))
     got = E.toHost(O.sort(t, -1, True, "GT"))
-    ref = x if dt == DType.BFLOAT16 else x.astype(np.int32)
+    ref = (E.bf16_bits_to_f32(E.f32_to_bf16_bits(x)).reshape(x.shape) if dt == DType.BFLOAT16
+           else x.astype(np.int32))
     want = np.take_along_axis(ref, _np_sort(ref, 1, True), 1)
     if dt == DType.BFLOAT16:
         got = E.bf16_bits_to_f32(got)
