@@ -527,10 +527,25 @@ def run_moe(args):
     E.sync()
     print(f"# inputs ready in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
 
-    def step():
-        y = moe.forward(xt)
-        E.flush()
-        return y
+    if args.moe_path == "lazy":
+        # rew runs DeepSeekMoE.forward only under jit/lazy (its topK is
+        # trace-only, src/rew/ops/sort.nim:88-90): the layer is traced once
+        # with its parameters as arguments and every step is one
+        # rew_mi355x_execute_jit call of the cached module
+        from rew_amd import jit as J
+        lz = J.lazy(lambda a: [nn.moeFromParams(a[1:], S, E_, k).forward(a[0])],
+                    "deepseekMoE")
+        call_args = [xt] + nn.moeParams(moe)
+
+        def step():
+            y = lz.call(call_args)[0]
+            E.flush()
+            return y
+    else:
+        def step():
+            y = moe.forward(xt)
+            E.flush()
+            return y
 
     wall, dev_ms, first_ms, prof = timed_run(step, args.steps, args.warmup)
     ms = wall * 1e3 / args.steps
@@ -555,7 +570,7 @@ def run_moe(args):
                          f"deepseek.nim:122-145), oracle/ C restatement, {dt:.1f} s"}
     emit(args, "moe_layer_tokens_per_s", T * args.steps / wall, "tokens/s", ms, "bf16",
          {"workload": "deepseek_moe_layer_bf16", "tokens": T, "hidden": H, "intermediate": I,
-          "routed_experts": E_, "shared_experts": S, "top_k": k},
+          "routed_experts": E_, "shared_experts": S, "top_k": k, "path": args.moe_path},
          roof, cpu, {"kernels": breakdown(syms, args.steps), "first_call_ms": round(first_ms, 1),
                      "algorithmic_tflop": round(flops / 1e12, 4),
                      "achieved_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
@@ -631,6 +646,9 @@ def main():
     ap.add_argument("--cpu-seqs", type=int, default=2,
                     help="sequences of the llama batch in the cpu_baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--moe-path", default="lazy", choices=["lazy", "eager"],
+                    help="moe workload: rew's lazy batch (its executable form) or the "
+                         "eager op stream of the mirror")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one MI355X only; the multi-GPU sharding of the "
