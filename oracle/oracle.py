@@ -184,6 +184,96 @@ def index_select(x: np.ndarray, idx: np.ndarray, dim: int) -> np.ndarray:
     return np.take(x, i, axis=dim)
 
 
+def _index_vector(idx, ivd, batch):
+    """The index vector of start/scatter indices `idx` at batch coordinate
+    `batch` (coordinates of every dim except index_vector_dim, in order);
+    index_vector_dim == rank means a trailing dim of size 1."""
+    idx = np.asarray(idx)
+    if ivd == idx.ndim:
+        return [int(idx[tuple(batch)])]
+    pos = list(batch[:ivd]) + [slice(None)] + list(batch[ivd:])
+    return [int(v) for v in idx[tuple(pos)]]
+
+
+def gather(x, idx, offset_dims, collapsed, start_index_map, ivd, slice_sizes,
+           operand_batching=(), start_batching=()):
+    """stablehlo.gather (rew builds it at src/rew/stablehlo/ops.nim:1387-1408;
+    semantics: the StableHLO spec's gather): for every result index, the
+    batch coordinates pick an index vector, whose entries set the starts of
+    the operand dims named by start_index_map (operand batching dims start at
+    the matching batch coordinate); every start is clamped into
+    [0, dim - slice]; offset dims walk the operand's window dims in order.
+    Explicit loops: small sizes only."""
+    x, idx = np.asarray(x), np.asarray(idx)
+    rank_i = idx.ndim
+    bdims = [d for d in range(rank_i) if d != ivd]
+    win = [d for d in range(x.ndim) if d not in collapsed and d not in operand_batching]
+    out_rank = len(offset_dims) + len(bdims)
+    shape, bi = [], 0
+    for d in range(out_rank):
+        if d in offset_dims:
+            shape.append(slice_sizes[win[list(offset_dims).index(d)]])
+        else:
+            shape.append(idx.shape[bdims[bi]])
+            bi += 1
+    out = np.empty(shape, x.dtype)
+    batch_out = [d for d in range(out_rank) if d not in offset_dims]
+    for o in np.ndindex(*shape):
+        batch = [o[d] for d in batch_out]
+        start = [0] * x.ndim
+        for j, v in enumerate(_index_vector(idx, ivd, batch)):
+            start[start_index_map[j]] = v
+        for xd, sd in zip(operand_batching, start_batching):
+            start[xd] = batch[bdims.index(sd)]
+        full = [min(max(start[d], 0), x.shape[d] - slice_sizes[d]) for d in range(x.ndim)]
+        for j, d in enumerate(offset_dims):
+            full[win[j]] += o[d]
+        out[o] = x[tuple(full)]
+    return out
+
+
+def scatter(x, idx, upd, update_window_dims, inserted, scatter_dims_to_operand, ivd, op,
+            input_batching=(), index_batching=()):
+    """stablehlo.scatter with one input (rew builds it at
+    src/rew/stablehlo/ops.nim:1531-1569; semantics: the StableHLO spec's
+    scatter): every update element lands at start + window offset and is
+    combined with `op` ("add", "maximum", "minimum", "multiply" or
+    "replace"); an update whose index falls outside the input is skipped.
+    Updates are applied in row-major order of the updates.  Explicit loops:
+    small sizes only."""
+    x, idx, upd = np.asarray(x), np.asarray(idx), np.asarray(upd)
+    out = x.copy()
+    rank_i = idx.ndim
+    bdims = [d for d in range(rank_i) if d != ivd]
+    win = [d for d in range(x.ndim) if d not in inserted and d not in input_batching]
+    scat = [d for d in range(upd.ndim) if d not in update_window_dims]
+    fn = {"add": lambda a, b: a + b, "maximum": lambda a, b: np.maximum(a, b),
+          "minimum": lambda a, b: np.minimum(a, b), "multiply": lambda a, b: a * b,
+          "replace": lambda a, b: b}[op]
+    for u in np.ndindex(*upd.shape):
+        batch = [u[d] for d in scat]
+        start = [0] * x.ndim
+        for j, v in enumerate(_index_vector(idx, ivd, batch)):
+            start[scatter_dims_to_operand[j]] = v
+        for xd, sd in zip(input_batching, index_batching):
+            start[xd] = batch[bdims.index(sd)]
+        full = list(start)
+        for j, d in enumerate(update_window_dims):
+            full[win[j]] += u[d]
+        if all(0 <= full[d] < x.shape[d] for d in range(x.ndim)):
+            out[tuple(full)] = fn(out[tuple(full)], upd[u])
+    return out
+
+
+def sort_order(x, axis: int, descending: bool):
+    """The permutation stablehlo.sort applies with a one-compare comparator
+    (src/rew/ops/sort.nim:13-33): stable, -0 == +0, NaN after every number
+    (numpy's stable argsort keeps NaN last and ties in order)."""
+    x = np.asarray(x)
+    key = np.where(x == 0, 0, x).astype(np.float64) if x.dtype.kind == "f" else x.astype(np.int64)
+    return np.argsort(-key if descending else key, axis=axis, kind="stable")
+
+
 # ---- composites ------------------------------------------------------------------------
 
 def softmax_rows(x: np.ndarray) -> np.ndarray:

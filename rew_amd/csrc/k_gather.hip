@@ -1,4 +1,5 @@
-// torch_index_select (batch_dims = 0): row gather.
+// torch_index_select (batch_dims = 0): row gather; and the general
+// stablehlo.gather / stablehlo.scatter (thread per element, atomic updates).
 //
 // One workgroup per output row; rows are copied with 16-byte loads/stores
 // when the row size and both base addresses allow it (the embedding case:
@@ -51,6 +52,183 @@ void launch_gather(const GatherArgs& g, hipStream_t stream) {
     hipLaunchKernelGGL(gather_kernel<16>, dim3(grid), dim3(256), 0, stream, g);
   else
     hipLaunchKernelGGL(gather_kernel<1>, dim3(grid), dim3(256), 0, stream, g);
+  REW_HIP(hipGetLastError());
+}
+
+}  // namespace rew
+
+// ---- general gather / scatter ----------------------------------------------------
+
+namespace rew {
+
+namespace {
+
+// Linear x offset of iteration element t (false: out of bounds, scatter only).
+__device__ __forceinline__ bool map_element(const IndexMapArgs& g, int64_t t, int64_t* x_lin) {
+  int64_t c[8];
+  int64_t rem = t;
+  for (int d = g.rank_it - 1; d >= 0; --d) {
+    c[d] = rem % g.dims_it[d];
+    rem /= g.dims_it[d];
+  }
+  int64_t win[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int64_t st[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int64_t ib = 0;
+  for (int d = 0; d < g.rank_it; ++d) {
+    if (g.role[d] >= 0) win[g.role[d]] = c[d];
+    else ib += c[d] * g.stride_idx_batch[-1 - g.role[d]];
+  }
+  for (int j = 0; j < g.n_map; ++j)
+    st[g.map_x[j]] = load_index(g.index, g.index_dtype, ib + j * g.stride_idx_vec);
+  for (int i = 0; i < g.n_bat; ++i) st[g.bat_x[i]] = c[g.bat_it[i]];
+  int64_t lin = 0;
+  for (int d = 0; d < g.rank_x; ++d) {
+    int64_t s = st[d];
+    if (g.clamp) {
+      const int64_t hi = g.dims_x[d] - g.slice[d];
+      s = s < 0 ? 0 : (s > hi ? hi : s);
+    }
+    const int64_t v = s + win[d];
+    if (!g.clamp && (v < 0 || v >= g.dims_x[d])) return false;
+    lin += v * g.stride_x[d];
+  }
+  *x_lin = lin;
+  return true;
+}
+
+__device__ __forceinline__ void copy_bytes(const void* src, int64_t s, void* dst, int64_t d,
+                                           int esize) {
+  switch (esize) {
+    case 1: ((uint8_t*)dst)[d] = ((const uint8_t*)src)[s]; break;
+    case 2: ((uint16_t*)dst)[d] = ((const uint16_t*)src)[s]; break;
+    case 4: ((uint32_t*)dst)[d] = ((const uint32_t*)src)[s]; break;
+    default: ((uint64_t*)dst)[d] = ((const uint64_t*)src)[s]; break;
+  }
+}
+
+__device__ __forceinline__ float combine_f(int op, float a, float b) {
+  switch (op) {
+    case kScatterAdd: return a + b;
+    case kScatterMax: return (a != a || b != b) ? __builtin_nanf("") : (a > b ? a : b);
+    case kScatterMin: return (a != a || b != b) ? __builtin_nanf("") : (a < b ? a : b);
+    case kScatterMul: return a * b;
+    default: return b;
+  }
+}
+
+__device__ __forceinline__ uint32_t combine_i(int op, bool sgn, uint32_t a, uint32_t b) {
+  switch (op) {
+    case kScatterAdd: return a + b;
+    case kScatterMax: return sgn ? ((int32_t)a > (int32_t)b ? a : b) : (a > b ? a : b);
+    case kScatterMin: return sgn ? ((int32_t)a < (int32_t)b ? a : b) : (a < b ? a : b);
+    case kScatterMul: return a * b;
+    default: return b;
+  }
+}
+
+__device__ __forceinline__ float half_to_f(uint32_t h, bool bf) {
+  if (bf) return __uint_as_float(h << 16);
+  _Float16 x;
+  const uint16_t u = (uint16_t)h;
+  __builtin_memcpy(&x, &u, 2);
+  return (float)x;
+}
+
+__device__ __forceinline__ uint32_t f_to_half(float f, bool bf) {
+  if (bf) {
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;  // quiet NaN
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;                   // round to nearest even
+  }
+  const _Float16 x = (_Float16)f;
+  uint16_t u;
+  __builtin_memcpy(&u, &x, 2);
+  return u;
+}
+
+// out[d] = op(out[d], src[s]) as one atomic read-modify-write.
+__device__ void update(const IndexMapArgs& g, int64_t s, int64_t d) {
+  if (g.op == kScatterReplace) {
+    copy_bytes(g.src, s, g.out, d, g.esize);
+    return;
+  }
+  if (g.dtype == kF32) {
+    float* p = (float*)g.out + d;
+    const float v = ((const float*)g.src)[s];
+    if (g.op == kScatterAdd) {
+      atomicAdd(p, v);
+      return;
+    }
+    unsigned int* q = (unsigned int*)p;
+    unsigned int old = *q, seen;
+    do {
+      seen = old;
+      old = atomicCAS(q, seen, __float_as_uint(combine_f(g.op, __uint_as_float(seen), v)));
+    } while (old != seen);
+    return;
+  }
+  if (g.dtype == kI32 || g.dtype == kU32) {
+    unsigned int* q = (unsigned int*)g.out + d;
+    const uint32_t v = ((const uint32_t*)g.src)[s];
+    if (g.op == kScatterAdd) {
+      atomicAdd(q, v);
+      return;
+    }
+    unsigned int old = *q, seen;
+    do {
+      seen = old;
+      old = atomicCAS(q, seen, combine_i(g.op, g.dtype == kI32, seen, v));
+    } while (old != seen);
+    return;
+  }
+  // bf16 / f16: compare-and-swap on the aligned 32-bit word holding the element
+  const bool bf = g.dtype == kBF16;
+  const uintptr_t a = (uintptr_t)((uint16_t*)g.out + d);
+  unsigned int* q = (unsigned int*)(a & ~(uintptr_t)3);
+  const int sh = (int)(a & 2) * 8;
+  const float v = half_to_f(((const uint16_t*)g.src)[s], bf);
+  unsigned int old = *q, seen;
+  do {
+    seen = old;
+    const float cur = half_to_f((seen >> sh) & 0xffffu, bf);
+    const uint32_t nh = f_to_half(combine_f(g.op, cur, v), bf);
+    old = atomicCAS(q, seen, (seen & ~(0xffffu << sh)) | (nh << sh));
+  } while (old != seen);
+}
+
+}  // namespace
+
+__global__ void __launch_bounds__(256) gather_nd_kernel(IndexMapArgs g) {
+  const int64_t step = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < g.total; t += step) {
+    int64_t x = 0;
+    map_element(g, t, &x);
+    copy_bytes(g.src, x, g.out, t, g.esize);
+  }
+}
+
+__global__ void __launch_bounds__(256) scatter_kernel(IndexMapArgs g) {
+  const int64_t step = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < g.total; t += step) {
+    int64_t x = 0;
+    if (map_element(g, t, &x)) update(g, t, x);
+  }
+}
+
+static unsigned index_map_grid(int64_t total) {
+  const int64_t b = (total + 255) / 256;
+  return (unsigned)(b < 65536 ? b : 65536);
+}
+
+void launch_gather_nd(const IndexMapArgs& g, hipStream_t stream) {
+  if (g.total == 0) return;
+  hipLaunchKernelGGL(gather_nd_kernel, dim3(index_map_grid(g.total)), dim3(256), 0, stream, g);
+  REW_HIP(hipGetLastError());
+}
+
+void launch_scatter(const IndexMapArgs& g, hipStream_t stream) {
+  if (g.total == 0) return;
+  hipLaunchKernelGGL(scatter_kernel, dim3(index_map_grid(g.total)), dim3(256), 0, stream, g);
   REW_HIP(hipGetLastError());
 }
 

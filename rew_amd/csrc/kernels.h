@@ -160,6 +160,43 @@ struct GatherArgs {
 };
 void launch_gather(const GatherArgs& g, hipStream_t stream);
 
+// stablehlo.gather / stablehlo.scatter over dense row-major tensors of rank
+// <= 8 (src/rew/ops/gather.nim:10-28, scatter.nim:10-39; the StableHLO
+// dimension-number semantics).  One thread per element of the iteration
+// space (gather: the result; scatter: the updates).  The host resolves the
+// dimension numbers into roles:
+//   role[d] >= 0   iteration dim d is a window dim: it offsets x dim role[d]
+//   role[d] = -1-k iteration dim d is batch dim k of the index tensor
+// The index vector of an element is index[sum_k c_k * stride_idx_batch[k] +
+// j * stride_idx_vec], j < n_map, and sets the start of x dim map_x[j];
+// x dim bat_x[i] starts at the iteration coordinate of dim bat_it[i]
+// (operand / input batching dims).  Gather clamps every start into
+// [0, dims_x - slice]; scatter skips an update whose index falls outside x.
+constexpr int kScatterReplace = 0, kScatterAdd = 1, kScatterMax = 2, kScatterMin = 3,
+              kScatterMul = 4;
+struct IndexMapArgs {
+  const void* src;    // gather: operand; scatter: updates
+  const void* index;
+  void* out;          // gather: result; scatter: result, pre-filled with the input
+  int esize, dtype, index_dtype;
+  int op;             // scatter update computation (kScatter*)
+  int clamp;          // 1: gather, 0: scatter
+  int rank_it, rank_x;
+  int64_t dims_it[8];
+  int64_t dims_x[8], stride_x[8];
+  int role[8];
+  int64_t stride_idx_batch[8];
+  int64_t stride_idx_vec;
+  int n_map;
+  int map_x[8];
+  int n_bat;
+  int bat_x[8], bat_it[8];
+  int64_t slice[8];
+  int64_t total;      // elements of the iteration space
+};
+void launch_gather_nd(const IndexMapArgs& g, hipStream_t stream);
+void launch_scatter(const IndexMapArgs& g, hipStream_t stream);
+
 // ---- argmax / topK (k_select.hip) ----------------------------------------------
 // argmax over dim n of x viewed as dense [outer, n, inner] f32; out [outer, inner]
 // int32 (lowest index of the maximum; INT32_MAX where the slice holds NaN).

@@ -329,6 +329,7 @@ struct Lower {
   void emit_argmax(Node* n);
   void emit_topk(Node* n);
   void emit_sort(Node* n);
+  void emit_index_map(Node* n);
   // Materialize `t` (any kind) into a fresh dense tensor whose shape is the
   // permutation `perm` of t's shape.
   Tensor* emit_permuted_copy(Tensor* t, const std::vector<int>& perm);
@@ -1027,6 +1028,8 @@ void Lower::emit_anchor(Node* n) {
     case K_ARGMAX: emit_argmax(n); break;
     case K_TOPK: emit_topk(n); break;
     case K_SORT: emit_sort(n); break;
+    case K_GATHER:
+    case K_SCATTER: emit_index_map(n); break;
     case K_BITCAST: {
       Tensor* x = n->in[0];
       ensure_mat(x);
@@ -2728,6 +2731,93 @@ void Lower::emit_sort(Node* n) {
   g.rows = g.cols ? k->numel() / g.cols : 0;
   prof_begin(c, "sort{" + std::to_string(g.rows) + "x" + std::to_string(g.cols) + "}");
   launch_sort(g, c->stream);
+  prof_end(c);
+  note_launch(c, false);
+}
+
+// stablehlo.gather / stablehlo.scatter: the dimension numbers resolved into
+// the per-dimension roles of IndexMapArgs (dense row-major operands).
+void Lower::emit_index_map(Node* n) {
+  const bool gather = n->kind == K_GATHER;
+  Tensor* x = n->in[0];
+  Tensor* ix = n->in[1];
+  Tensor* src = gather ? x : n->in[2];
+  Tensor* out = n->out[0];
+  for (Tensor* t : n->in) ensure_mat(t);
+  tensor_alloc(out);
+  IndexMapArgs g;
+  std::memset(&g, 0, sizeof g);
+  g.src = src->data();
+  g.index = ix->data();
+  g.out = out->data();
+  g.esize = dt_size(x->dt);
+  g.dtype = x->dt;
+  g.index_dtype = ix->dt;
+  g.op = gather ? 0 : n->sub;
+  g.clamp = gather ? 1 : 0;
+  const Shape& it = gather ? out->shape : src->shape;  // iteration space
+  const Shape& xs = x->shape;
+  const Shape& is = ix->shape;
+  g.rank_it = it.rank;
+  g.rank_x = xs.rank;
+  g.total = it.numel();
+  int64_t st = 1;
+  for (int d = xs.rank - 1; d >= 0; --d) {
+    g.dims_x[d] = xs.d[d];
+    g.stride_x[d] = st;
+    st *= xs.d[d];
+  }
+  int64_t istride[kMaxRank];
+  st = 1;
+  for (int d = is.rank - 1; d >= 0; --d) {
+    istride[d] = st;
+    st *= is.d[d];
+  }
+  const int ivd = (int)n->i0;
+  g.stride_idx_vec = ivd < is.rank ? istride[ivd] : 0;
+  std::vector<int> batch_idx_dims;  // index dims other than the index vector dim
+  for (int d = 0; d < is.rank; ++d)
+    if (d != ivd) batch_idx_dims.push_back(d);
+  // window dims of x: not collapsed / inserted (l1) and not batching (l2)
+  std::vector<bool> drop(xs.rank, false);
+  for (auto d : n->l1) drop[d] = true;
+  for (auto d : n->l2) drop[d] = true;
+  std::vector<int> win;
+  for (int d = 0; d < xs.rank; ++d)
+    if (!drop[d]) win.push_back(d);
+  std::vector<int> it_of_batch;  // iteration dim of each index batch dim
+  size_t wj = 0;
+  for (int d = 0; d < it.rank; ++d) {
+    g.dims_it[d] = it.d[d];
+    if (wj < n->l0.size() && n->l0[wj] == d) {
+      g.role[d] = win[wj++];
+    } else {
+      const int k = (int)it_of_batch.size();
+      g.role[d] = -1 - k;
+      g.stride_idx_batch[k] = istride[batch_idx_dims[k]];
+      it_of_batch.push_back(d);
+    }
+  }
+  g.n_map = (int)n->l4.size();
+  for (int j = 0; j < g.n_map; ++j) g.map_x[j] = (int)n->l4[j];
+  g.n_bat = (int)n->l2.size();
+  for (int i = 0; i < g.n_bat; ++i) {
+    g.bat_x[i] = (int)n->l2[i];
+    int k = 0;
+    while (batch_idx_dims[k] != (int)n->l3[i]) ++k;
+    g.bat_it[i] = it_of_batch[k];
+  }
+  for (int d = 0; d < xs.rank; ++d) g.slice[d] = gather ? n->l5[d] : 0;
+  if (gather) {
+    prof_begin(c, "gather_nd{" + std::to_string(g.total) + "}");
+    launch_gather_nd(g, c->stream);
+  } else {
+    if (out->nbytes())
+      REW_HIP(hipMemcpyAsync(out->data(), x->data(), (size_t)out->nbytes(),
+                             hipMemcpyDeviceToDevice, c->stream));
+    prof_begin(c, "scatter{" + std::to_string(g.total) + "}");
+    launch_scatter(g, c->stream);
+  }
   prof_end(c);
   note_launch(c, false);
 }

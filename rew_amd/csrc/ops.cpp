@@ -98,6 +98,7 @@ static const std::unordered_map<std::string, OpSpec>& op_table() {
       {"torchIndexSelect", {K_INDEX_SELECT, 0}},
       // backend extensions (no eager counterpart in the reference)
       {"argmax", {K_ARGMAX, 0}}, {"topK", {K_TOPK, 0}}, {"sort", {K_SORT, 0}},
+      {"gather", {K_GATHER, 0}}, {"scatter", {K_SCATTER, 0}},
   };
   return t;
 }
@@ -192,6 +193,42 @@ static void check_axis_list(const std::vector<int64_t>& dims, int rank,
               " repeated");
     seen[d] = true;
   }
+}
+
+// An int-list attr that may be absent (empty).
+static std::vector<int64_t> opt_int_list(const Attrs& a, const std::string& key,
+                                         const std::string& op) {
+  for (auto& kv : a)
+    if (kv.first == key) return parse_int_list(kv.second, op);
+  return {};
+}
+
+// Shared checks of stablehlo.gather / scatter dimension numbers: returns the
+// operand's window dims (those not in `drop1` or `drop2`, in order).
+static std::vector<int> window_dims(int rank, const std::vector<int64_t>& drop1,
+                                    const std::vector<int64_t>& drop2, const std::string& op,
+                                    const char* w1, const char* w2) {
+  check_axis_list(drop1, rank, op, w1);
+  check_axis_list(drop2, rank, op, w2);
+  std::vector<bool> dropped(rank, false);
+  for (auto d : drop1) dropped[d] = true;
+  for (auto d : drop2) {
+    if (dropped[d])
+      invalid("eager '" + op + "': dim " + std::to_string(d) + " is both " + w1 + " and " + w2);
+    dropped[d] = true;
+  }
+  std::vector<int> w;
+  for (int d = 0; d < rank; ++d)
+    if (!dropped[d]) w.push_back(d);
+  return w;
+}
+
+static void check_sorted_axes(const std::vector<int64_t>& dims, int rank, const std::string& op,
+                              const char* what) {
+  check_axis_list(dims, rank, op, what);
+  for (size_t i = 1; i < dims.size(); ++i)
+    if (dims[i] <= dims[i - 1])
+      invalid("eager '" + op + "': " + what + " must be sorted ascending");
 }
 
 static bool vm_dtype_ok(int dt) {
@@ -571,6 +608,137 @@ Node* prepare_node(Ctx* c, const std::string& op, const std::vector<Tensor*>& in
         if (is.d[n->i0] > kSortMaxCols)
           fail(REW_MI355X_ERR_UNSUPPORTED, "eager 'sort': dimension above " +
                                                std::to_string(kSortMaxCols));
+        break;
+      }
+      case K_GATHER: {
+        // stablehlo.gather (src/rew/ops/gather.nim:10-28): operand, start
+        // indices; attrs offset_dims, collapsed_slice_dims,
+        // operand_batching_dims, start_indices_batching_dims,
+        // start_index_map, index_vector_dim, slice_sizes
+        nin(2);
+        Tensor *x = ins[0], *ix = ins[1];
+        if (!dt_is_int(ix->dt)) invalid("eager 'gather': start indices must be an integer tensor");
+        const int sz = dt_size(x->dt);
+        if (x->dt == kI4 || x->dt == kU4 || x->dt == kNF4 || (sz != 1 && sz != 2 && sz != 4 && sz != 8))
+          fail(REW_MI355X_ERR_UNSUPPORTED,
+               std::string("eager 'gather': operand dtype ") + dt_enum_name(x->dt) + " not supported");
+        n->l0 = parse_int_list(find_attr(attrs, "offset_dims", op), op);
+        n->l1 = parse_int_list(find_attr(attrs, "collapsed_slice_dims", op), op);
+        n->l2 = opt_int_list(attrs, "operand_batching_dims", op);
+        n->l3 = opt_int_list(attrs, "start_indices_batching_dims", op);
+        n->l4 = parse_int_list(find_attr(attrs, "start_index_map", op), op);
+        n->l5 = parse_int_list(find_attr(attrs, "slice_sizes", op), op);
+        n->i0 = parse_int(find_attr(attrs, "index_vector_dim", op), op);
+        const Shape& xs = x->shape;
+        const Shape& is = ix->shape;
+        if ((int)n->l5.size() != xs.rank) invalid("eager 'gather': slice_sizes must match the operand rank");
+        for (int d = 0; d < xs.rank; ++d)
+          if (n->l5[d] < 0 || n->l5[d] > xs.d[d])
+            invalid("eager 'gather': slice size " + std::to_string(n->l5[d]) +
+                    " out of range for operand dim " + std::to_string(d));
+        if (n->i0 < 0 || n->i0 > is.rank) invalid("eager 'gather': index_vector_dim out of range");
+        const int64_t nvec = n->i0 < is.rank ? is.d[n->i0] : 1;
+        if ((int64_t)n->l4.size() != nvec)
+          invalid("eager 'gather': start_index_map must have one entry per index vector element");
+        check_axis_list(n->l4, xs.rank, op, "start_index_map");
+        std::vector<int> win = window_dims(xs.rank, n->l1, n->l2, op, "collapsed_slice_dims",
+                                           "operand_batching_dims");
+        for (auto d : n->l1)
+          if (n->l5[d] > 1) invalid("eager 'gather': a collapsed dim needs slice size 1");
+        for (auto d : n->l2)
+          if (n->l5[d] > 1) invalid("eager 'gather': a batching dim needs slice size 1");
+        if (n->l3.size() != n->l2.size())
+          invalid("eager 'gather': operand and start-index batching dims differ in count");
+        for (auto d : n->l3)
+          if (d < 0 || d >= is.rank || d == n->i0)
+            invalid("eager 'gather': start_indices_batching_dims out of range");
+        if (win.size() != n->l0.size())
+          invalid("eager 'gather': offset_dims must name one result dim per window dim");
+        const int out_rank = (int)n->l0.size() + is.rank - (n->i0 < is.rank ? 1 : 0);
+        if (out_rank > kMaxRank) fail(REW_MI355X_ERR_UNSUPPORTED, "eager 'gather': result rank above 8");
+        check_sorted_axes(n->l0, out_rank, op, "offset_dims");
+        std::vector<int64_t> od(out_rank, 0);
+        std::vector<bool> is_off(out_rank, false);
+        for (size_t j = 0; j < n->l0.size(); ++j) {
+          is_off[n->l0[j]] = true;
+          od[n->l0[j]] = n->l5[win[j]];
+        }
+        int bi = 0;
+        for (int d = 0; d < out_rank; ++d) {
+          if (is_off[d]) continue;
+          if (bi == n->i0) ++bi;
+          od[d] = is.d[bi++];
+        }
+        outs.push_back({x->dt, Shape(od)});
+        break;
+      }
+      case K_SCATTER: {
+        // stablehlo.scatter (src/rew/ops/scatter.nim:10-39) with one input:
+        // input, scatter indices, updates; attrs update_window_dims,
+        // inserted_window_dims, input_batching_dims,
+        // scatter_indices_batching_dims, scatter_dims_to_operand_dims,
+        // index_vector_dim, update_computation (replace / add / maximum /
+        // minimum / multiply)
+        nin(3);
+        Tensor *x = ins[0], *ix = ins[1], *up = ins[2];
+        if (!dt_is_int(ix->dt)) invalid("eager 'scatter': scatter indices must be an integer tensor");
+        if (up->dt != x->dt) invalid("eager 'scatter': updates dtype differs from the input dtype");
+        const std::string uc = strip(find_attr(attrs, "update_computation", op));
+        if (uc == "replace") n->sub = kScatterReplace;
+        else if (uc == "add") n->sub = kScatterAdd;
+        else if (uc == "maximum") n->sub = kScatterMax;
+        else if (uc == "minimum") n->sub = kScatterMin;
+        else if (uc == "multiply") n->sub = kScatterMul;
+        else invalid("eager 'scatter': update_computation must be replace, add, maximum, minimum or multiply");
+        const int sz = dt_size(x->dt);
+        if (x->dt == kI4 || x->dt == kU4 || x->dt == kNF4 || (sz != 1 && sz != 2 && sz != 4 && sz != 8))
+          fail(REW_MI355X_ERR_UNSUPPORTED,
+               std::string("eager 'scatter': dtype ") + dt_enum_name(x->dt) + " not supported");
+        if (n->sub != kScatterReplace && x->dt != kF32 && x->dt != kI32 && x->dt != kU32 &&
+            x->dt != kBF16 && x->dt != kF16)
+          fail(REW_MI355X_ERR_UNSUPPORTED, "eager 'scatter': " + uc + " updates of " +
+                                               dt_enum_name(x->dt) + " not supported");
+        n->l0 = parse_int_list(find_attr(attrs, "update_window_dims", op), op);
+        n->l1 = parse_int_list(find_attr(attrs, "inserted_window_dims", op), op);
+        n->l2 = opt_int_list(attrs, "input_batching_dims", op);
+        n->l3 = opt_int_list(attrs, "scatter_indices_batching_dims", op);
+        n->l4 = parse_int_list(find_attr(attrs, "scatter_dims_to_operand_dims", op), op);
+        n->i0 = parse_int(find_attr(attrs, "index_vector_dim", op), op);
+        const Shape& xs = x->shape;
+        const Shape& is = ix->shape;
+        const Shape& us = up->shape;
+        if (n->i0 < 0 || n->i0 > is.rank) invalid("eager 'scatter': index_vector_dim out of range");
+        const int64_t nvec = n->i0 < is.rank ? is.d[n->i0] : 1;
+        if ((int64_t)n->l4.size() != nvec)
+          invalid("eager 'scatter': scatter_dims_to_operand_dims must have one entry per index "
+                  "vector element");
+        check_axis_list(n->l4, xs.rank, op, "scatter_dims_to_operand_dims");
+        std::vector<int> win = window_dims(xs.rank, n->l1, n->l2, op, "inserted_window_dims",
+                                           "input_batching_dims");
+        if (n->l3.size() != n->l2.size())
+          invalid("eager 'scatter': input and index batching dims differ in count");
+        for (auto d : n->l3)
+          if (d < 0 || d >= is.rank || d == n->i0)
+            invalid("eager 'scatter': scatter_indices_batching_dims out of range");
+        if (win.size() != n->l0.size())
+          invalid("eager 'scatter': update_window_dims must name one updates dim per window dim");
+        if (us.rank != (int)n->l0.size() + is.rank - (n->i0 < is.rank ? 1 : 0))
+          invalid("eager 'scatter': updates rank does not match the dimension numbers");
+        check_sorted_axes(n->l0, us.rank, op, "update_window_dims");
+        std::vector<bool> is_win(us.rank, false);
+        for (size_t j = 0; j < n->l0.size(); ++j) {
+          is_win[n->l0[j]] = true;
+          if (us.d[n->l0[j]] > xs.d[win[j]])
+            invalid("eager 'scatter': an update window is larger than the input");
+        }
+        int bi = 0;
+        for (int d = 0; d < us.rank; ++d) {
+          if (is_win[d]) continue;
+          if (bi == n->i0) ++bi;
+          if (us.d[d] != is.d[bi++])
+            invalid("eager 'scatter': updates scatter dims do not match the index batch dims");
+        }
+        outs.push_back({x->dt, xs});
         break;
       }
       case K_DOT:

@@ -50,12 +50,12 @@ struct Tensor {
 };
 
 // Op kinds (the subset of rew's EagerOpKind this backend implements,
-// src/rew/eager.nim:718-764, plus backend extensions argmax/topK/sort).
+// src/rew/eager.nim:718-764, plus backend extensions argmax/topK/sort/gather/scatter).
 enum Kind : int {
   K_BINARY, K_UNARY, K_CONVERT, K_ISFINITE, K_BITCAST, K_RESHAPE,
   K_TRANSPOSE, K_REVERSE, K_BROADCAST_TO, K_BROADCAST, K_SLICE, K_CONCAT,
   K_IOTA, K_COMPARE, K_SELECT, K_CLAMP, K_REDUCE, K_DOT_GENERAL, K_DOT,
-  K_INDEX_SELECT, K_ARGMAX, K_TOPK, K_REDUCE_PRECISION, K_PAD, K_SORT,
+  K_INDEX_SELECT, K_ARGMAX, K_TOPK, K_REDUCE_PRECISION, K_PAD, K_SORT, K_GATHER, K_SCATTER,
   // composite kernels created by the planner (never recorded directly)
   K_COUNT
 };
@@ -67,7 +67,7 @@ struct Node {
   std::vector<Tensor*> in;
   std::vector<Tensor*> out;
   // typed attributes
-  std::vector<int64_t> l0, l1, l2, l3;
+  std::vector<int64_t> l0, l1, l2, l3, l4, l5;
   int64_t i0 = 0, i1 = 0, i2 = 0;
   int dt_attr = -1;
   int cmp = 0;

@@ -9,11 +9,12 @@
 //     reshape/transpose/broadcast_in_dim/slice/concatenate/compare/select/
 //     clamp/dot_general/reduce ops and constants, and the quoted generic form
 //     "stablehlo.x"(...) ({regions}) {attrs} : (types) -> types used for
-//     iota, convert, torch_index_select, sort, ...);
+//     iota, convert, torch_index_select, sort, gather, scatter, ...);
 //   * a translator that turns each op into the graph node the matching eager
 //     op records (prepare_node, the same validation and output derivation),
 //     with stablehlo.reduce mapped onto reduceSum/Max/Min/Prod by its reducer
-//     body, stablehlo.sort onto the row-sort node, and the sort+slice pair
+//     body, stablehlo.sort onto the row-sort node, stablehlo.gather /
+//     scatter onto the general index-map nodes, and the sort+slice pair
 //     rew's topK traces (src/rew/ops/sort.nim:36-90) onto one topK node;
 //   * a per-context module cache keyed like rew's jitExecCache
 //     (ordinal::name::cacheKey::hash(text)), whose entries hold prepared
@@ -711,6 +712,74 @@ std::string shape_text(const std::vector<int64_t>& d) {
 
 std::string type_text(int dt, const Shape& s) { return dt_enum_name(dt) + s.str(); }
 
+const std::string* attr_raw(const Op& op, const char* key) {
+  for (auto& kv : op.attrs)
+    if (kv.first == key) return &kv.second;
+  return nullptr;
+}
+
+// "#stablehlo.gather<offset_dims = [1], ..., index_vector_dim = 1>" (and
+// the scatter form) -> "name" -> list; a scalar entry becomes a one-element
+// list (src/rew/stablehlo/ops.nim:170-188 renders them).
+std::unordered_map<std::string, std::vector<int64_t>> dim_numbers(const std::string& raw,
+                                                                  const std::string& who) {
+  std::unordered_map<std::string, std::vector<int64_t>> m;
+  const size_t lt = raw.find('<'), gt = raw.rfind('>');
+  if (lt == std::string::npos || gt == std::string::npos || gt < lt)
+    invalid(who + ": malformed dimension numbers '" + raw + "'");
+  size_t p = lt + 1;
+  while (p < gt) {
+    while (p < gt && (raw[p] == ' ' || raw[p] == ',')) ++p;
+    const size_t eq = raw.find('=', p);
+    if (eq == std::string::npos || eq > gt) break;
+    std::string k = raw.substr(p, eq - p);
+    while (!k.empty() && k.back() == ' ') k.pop_back();
+    p = eq + 1;
+    while (p < gt && raw[p] == ' ') ++p;
+    std::vector<int64_t> v;
+    if (raw[p] == '[') {
+      const size_t e = raw.find(']', p);
+      if (e == std::string::npos) invalid(who + ": malformed dimension numbers '" + raw + "'");
+      std::string body = raw.substr(p + 1, e - p - 1);
+      size_t q = 0;
+      while (q < body.size()) {
+        while (q < body.size() && (body[q] == ' ' || body[q] == ',')) ++q;
+        if (q >= body.size()) break;
+        char* end = nullptr;
+        v.push_back(std::strtoll(body.c_str() + q, &end, 10));
+        q = (size_t)(end - body.c_str());
+        if (end == body.c_str()) break;
+      }
+      p = e + 1;
+    } else {
+      char* end = nullptr;
+      v.push_back(std::strtoll(raw.c_str() + p, &end, 10));
+      p = (size_t)(end - raw.c_str());
+    }
+    m[k] = v;
+  }
+  return m;
+}
+
+// "array<i64: 1, 3>" -> {1, 3}
+std::vector<int64_t> i64_array(const std::string& raw, const std::string& who) {
+  const size_t c = raw.find(':'), e = raw.rfind('>');
+  if (raw.compare(0, 6, "array<") != 0 || c == std::string::npos || e == std::string::npos)
+    invalid(who + ": malformed i64 array '" + raw + "'");
+  std::vector<int64_t> v;
+  std::string body = raw.substr(c + 1, e - c - 1);
+  size_t q = 0;
+  while (q < body.size()) {
+    while (q < body.size() && (body[q] == ' ' || body[q] == ',')) ++q;
+    if (q >= body.size()) break;
+    char* end = nullptr;
+    v.push_back(std::strtoll(body.c_str() + q, &end, 10));
+    if (end == body.c_str() + q) break;
+    q = (size_t)(end - body.c_str());
+  }
+  return v;
+}
+
 int64_t attr_int(const Op& op, const char* key, const std::string& who) {
   for (auto& kv : op.attrs)
     if (kv.first == key) {
@@ -1121,6 +1190,66 @@ class Translator {
     for (size_t i = 0; i < r.size(); ++i) bind(o, i, r[i]);
   }
 
+  static std::string ints(const std::vector<int64_t>& v) { return shape_text(v); }
+
+  void gather(const Op& o) {
+    need_args(o, 2);
+    const std::string* dn = attr_raw(o, "dimension_numbers");
+    const std::string* ss = attr_raw(o, "slice_sizes");
+    if (!dn || !ss) fail_at(o, "missing dimension_numbers or slice_sizes");
+    auto d = dim_numbers(*dn, who_);
+    one(o, "gather", o.arg,
+        {{"offset_dims", ints(d["offset_dims"])},
+         {"collapsed_slice_dims", ints(d["collapsed_slice_dims"])},
+         {"operand_batching_dims", ints(d["operand_batching_dims"])},
+         {"start_indices_batching_dims", ints(d["start_indices_batching_dims"])},
+         {"start_index_map", ints(d["start_index_map"])},
+         {"index_vector_dim", std::to_string(d["index_vector_dim"].empty()
+                                                 ? 0 : d["index_vector_dim"][0])},
+         {"slice_sizes", ints(i64_array(*ss, who_))}});
+  }
+
+  // update computation of a one-input scatter: one op over (current,
+  // update), or the update itself (replace)
+  std::string scatter_update(const Op& o) {
+    const auto& ra = o.region_args.at(0);
+    const auto& body = o.regions.at(0);
+    if (ra.size() != 2) return "";
+    if (body.size() == 1 && body[0].name == "stablehlo.return" && body[0].arg.size() == 1 &&
+        body[0].arg[0] == ra[1])
+      return "replace";
+    const Op* b = single_body(o, 0);
+    if (!b || b->arg.size() != 2) return "";
+    if (!((b->arg[0] == ra[0] && b->arg[1] == ra[1]) || (b->arg[0] == ra[1] && b->arg[1] == ra[0])))
+      return "";
+    if (b->name == "stablehlo.add") return "add";
+    if (b->name == "stablehlo.maximum") return "maximum";
+    if (b->name == "stablehlo.minimum") return "minimum";
+    if (b->name == "stablehlo.multiply") return "multiply";
+    return "";
+  }
+
+  void scatter(const Op& o) {
+    if (o.arg.size() != 3 || o.res_ty.size() != 1)
+      fail_at(o, "only one-input scatters are supported", REW_MI355X_ERR_UNSUPPORTED);
+    const std::string* dn = attr_raw(o, "scatter_dimension_numbers");
+    if (!dn) fail_at(o, "missing scatter_dimension_numbers");
+    const std::string uc = scatter_update(o);
+    if (uc.empty())
+      fail_at(o, "only update computations of one add/maximum/minimum/multiply or a plain "
+                 "replacement are supported", REW_MI355X_ERR_UNSUPPORTED);
+    auto d = dim_numbers(*dn, who_);
+    one(o, "scatter", o.arg,
+        {{"update_window_dims", ints(d["update_window_dims"])},
+         {"inserted_window_dims", ints(d["inserted_window_dims"])},
+         {"input_batching_dims", ints(d["input_batching_dims"])},
+         {"scatter_indices_batching_dims", ints(d["scatter_indices_batching_dims"])},
+         {"scatter_dims_to_operand_dims", ints(d["scatter_dims_to_operand_dims"])},
+         {"index_vector_dim", std::to_string(d["index_vector_dim"].empty()
+                                                 ? 0 : d["index_vector_dim"][0])},
+         {"update_computation", uc}});
+  }
+
   void op(const Op& o, int index) {
     const std::string& n = o.name;
     if (redirect_[index] >= 0) {  // a slice the topK peephole answers
@@ -1203,6 +1332,10 @@ class Translator {
       reduce(o);
     } else if (n == "stablehlo.sort") {
       sort(o, index);
+    } else if (n == "stablehlo.gather") {
+      gather(o);
+    } else if (n == "stablehlo.scatter") {
+      scatter(o);
     } else {
       fail_at(o, "op not supported by the mi355x jit path", REW_MI355X_ERR_UNSUPPORTED);
     }

@@ -406,6 +406,66 @@ def traceSort(inputs: Sequence[Tensor], dim: int, stable: bool, direction: str) 
     return _sort(ctx, list(inputs), dim, stable, direction)
 
 
+def _region_body(ctx, dtype, op):
+    """A two-argument scalar region returning op(a, b), or b for "replace"."""
+    a, b = ctx.fresh(), ctx.fresh()
+    s = _ty(dtype, [])
+    head = f"      ^bb0(%v{a}: {s}, %v{b}: {s}):"
+    if op == "replace":
+        return [head, f"        stablehlo.return %v{b} : {s}"]
+    c = ctx.fresh()
+    return [head, f"        %v{c} = stablehlo.{op} %v{a}, %v{b} : {s}",
+            f"        stablehlo.return %v{c} : {s}"]
+
+
+def traceGather(operand, startIndices, dims, sliceSizes, resultShape, indicesAreSorted):
+    """gather's trace branch (src/rew/ops/gather.nim:18-25; builder
+    ops.nim:1387-1408, dims rendered as ops.nim:170-177)."""
+    ctx = currentTrace()
+    _require_trace(ctx, operand, "gather")
+    _require_trace(ctx, startIndices, "gather")
+    r = ctx.value(operand.dtype, resultShape)
+    dn = (f"#stablehlo.gather<offset_dims = {_list(dims.offsetDims)}, collapsed_slice_dims = "
+          f"{_list(dims.collapsedSliceDims)}, operand_batching_dims = "
+          f"{_list(dims.operandBatchingDims)}, start_indices_batching_dims = "
+          f"{_list(dims.startIndicesBatchingDims)}, start_index_map = "
+          f"{_list(dims.startIndexMap)}, index_vector_dim = {int(dims.indexVectorDim)}>")
+    ss = "array<i64: " + ", ".join(str(int(x)) for x in sliceSizes) + ">"
+    ctx.lines.append(
+        f"    %v{r.traceId} = \"stablehlo.gather\"(%v{operand.traceId}, %v{startIndices.traceId}) "
+        f"{{dimension_numbers = {dn}, slice_sizes = {ss}, indices_are_sorted = "
+        f"{'true' if indicesAreSorted else 'false'}}} : "
+        f"{_sig([operand, startIndices], _ty(operand.dtype, resultShape))}")
+    return r
+
+
+def traceScatter(inputs, scatterIndices, updates, dims, op, indicesAreSorted, uniqueIndices):
+    """scatter's trace branch (src/rew/ops/scatter.nim:20-37; builder
+    ops.nim:1531-1569, dims rendered as ops.nim:179-188)."""
+    ctx = currentTrace()
+    for t in [*inputs, scatterIndices, *updates]:
+        _require_trace(ctx, t, "scatter")
+    if len(inputs) != 1:
+        raise TensorError("scatter: the mirror traces one-input scatters only")
+    body = _region_body(ctx, inputs[0].dtype, op)
+    x = inputs[0]
+    r = ctx.value(x.dtype, x.shape)
+    dn = (f"#stablehlo.scatter<update_window_dims = {_list(dims.updateWindowDims)}, "
+          f"inserted_window_dims = {_list(dims.insertedWindowDims)}, input_batching_dims = "
+          f"{_list(dims.inputBatchingDims)}, scatter_indices_batching_dims = "
+          f"{_list(dims.scatterIndicesBatchingDims)}, scatter_dims_to_operand_dims = "
+          f"{_list(dims.scatterDimsToOperandDims)}, index_vector_dim = "
+          f"{int(dims.indexVectorDim)}>")
+    ops_ = [x, scatterIndices, updates[0]]
+    ctx.lines += ([f"    %v{r.traceId} = \"stablehlo.scatter\"("
+                   + ", ".join(f"%v{t.traceId}" for t in ops_) + ") ({"] + body
+                  + ["    }) {scatter_dimension_numbers = " + dn + ", indices_are_sorted = "
+                     + ("true" if indicesAreSorted else "false") + ", unique_indices = "
+                     + ("true" if uniqueIndices else "false") + "} : "
+                     + _sig(ops_, _ty(x.dtype, x.shape))])
+    return [r]
+
+
 def traceTopK(operand: Tensor, k: int, dim: int, largest: bool):
     """topK's trace branch (src/rew/ops/sort.nim:53-85)."""
     ctx = currentTrace()

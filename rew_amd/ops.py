@@ -11,6 +11,7 @@ format, so the native backend sees exactly what rew would send it:
 """
 from __future__ import annotations
 
+from dataclasses import dataclass
 from typing import Sequence
 
 import numpy as np
@@ -352,6 +353,91 @@ def sort(operand: Tensor, dimension: int = -1, isStable: bool = False,
                                           ("comparison_direction", comparator),
                                           ("is_stable", "true" if isStable else "false")])
     return res[0] if not others else res
+
+
+@dataclass
+class GatherDimensionNumbers:
+    """src/rew/stablehlo/ops.nim:60-68."""
+    offsetDims: Sequence[int]
+    collapsedSliceDims: Sequence[int]
+    startIndexMap: Sequence[int]
+    indexVectorDim: int
+    operandBatchingDims: Sequence[int] = ()
+    startIndicesBatchingDims: Sequence[int] = ()
+
+
+@dataclass
+class ScatterDimensionNumbers:
+    """src/rew/stablehlo/ops.nim:70-77."""
+    updateWindowDims: Sequence[int]
+    insertedWindowDims: Sequence[int]
+    scatterDimsToOperandDims: Sequence[int]
+    indexVectorDim: int
+    inputBatchingDims: Sequence[int] = ()
+    scatterIndicesBatchingDims: Sequence[int] = ()
+
+
+def gather(operand: Tensor, startIndices: Tensor, dims: GatherDimensionNumbers,
+           sliceSizes: Sequence[int], resultShape: Sequence[int],
+           indicesAreSorted: bool = False) -> Tensor:
+    """stablehlo.gather (src/rew/ops/gather.nim:10-28).  Trace-only in the
+    reference; the backend also runs it eagerly (start indices clamped)."""
+    if _jit.currentMode() == "trace":
+        return _jit.traceGather(operand, startIndices, dims, sliceSizes, resultShape,
+                                indicesAreSorted)
+    out = _one("gather", [operand, startIndices], [
+        ("offset_dims", _join(dims.offsetDims)),
+        ("collapsed_slice_dims", _join(dims.collapsedSliceDims)),
+        ("operand_batching_dims", _join(dims.operandBatchingDims)),
+        ("start_indices_batching_dims", _join(dims.startIndicesBatchingDims)),
+        ("start_index_map", _join(dims.startIndexMap)),
+        ("index_vector_dim", str(dims.indexVectorDim)),
+        ("slice_sizes", _join(sliceSizes))])
+    if list(out.shape) != list(resultShape):
+        raise TensorError(f"gather: resultShape {list(resultShape)} does not match the "
+                          f"dimension numbers ({list(out.shape)})")
+    return out
+
+
+_UPDATES = ("replace", "add", "maximum", "minimum", "multiply")
+
+
+def scatter(inputs: Sequence[Tensor], scatterIndices: Tensor, updates: Sequence[Tensor],
+            dims: ScatterDimensionNumbers, updateComputation: str = "add",
+            indicesAreSorted: bool = False, uniqueIndices: bool = False) -> list:
+    """stablehlo.scatter (src/rew/ops/scatter.nim:10-39).  rew takes the update
+    computation as a builder callback; here it names the one op such a
+    callback emits on (current, update): "add", "maximum", "minimum",
+    "multiply", or "replace" (the callback returns the update).  Updates of
+    one element in several places combine in an unspecified order (atomics).
+    Trace-only in the reference; the backend also runs one-input scatters
+    eagerly."""
+    if not inputs or len(inputs) != len(updates):
+        raise TensorError("scatter: inputs and updates must have the same non-zero length")
+    if updateComputation not in _UPDATES:
+        raise TensorError(f"scatter: update computation must be one of {_UPDATES}")
+    if _jit.currentMode() == "trace":
+        return _jit.traceScatter(list(inputs), scatterIndices, list(updates), dims,
+                                 updateComputation, indicesAreSorted, uniqueIndices)
+    if len(inputs) != 1:
+        raise TensorError("scatter: the backend runs one-input scatters only")
+    return [_one("scatter", [inputs[0], scatterIndices, updates[0]], [
+        ("update_window_dims", _join(dims.updateWindowDims)),
+        ("inserted_window_dims", _join(dims.insertedWindowDims)),
+        ("input_batching_dims", _join(dims.inputBatchingDims)),
+        ("scatter_indices_batching_dims", _join(dims.scatterIndicesBatchingDims)),
+        ("scatter_dims_to_operand_dims", _join(dims.scatterDimsToOperandDims)),
+        ("index_vector_dim", str(dims.indexVectorDim)),
+        ("update_computation", updateComputation)])]
+
+
+def indexSelect(operand: Tensor, index: Tensor, dim: int = 0, batchDims: int = 0) -> Tensor:
+    """src/rew/ops/gather.nim:55-81: torch_index_select in trace mode; the
+    backend also runs it eagerly (as torchIndexSelect)."""
+    if dim < 0 or dim >= len(operand.shape):
+        raise TensorError(f"indexSelect: dim {dim} out of range for operand rank "
+                          f"{len(operand.shape)}")
+    return torchIndexSelect(operand, index, dim, batchDims)
 
 
 # ---- linear algebra (src/rew/ops/linalg.nim:204-256, 432-461) -------------------------

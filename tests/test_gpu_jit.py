@@ -229,3 +229,62 @@ def test_input_mismatch_and_unsupported_op(gpu):
 """
     with pytest.raises(E.EagerError, match="line 3: stablehlo.fft: op not supported"):
         J.executeJit("fft", "k", bad, [f32([1, 2])], [DType.FLOAT32], [[2]])
+
+
+GATHER_CASES = [
+    # (x shape, idx, dims kwargs for the oracle) -- index_select rows, points,
+    # clamped windows, batching dims
+    ((6, 5), np.array([[3], [0], [5], [5], [1], [-2], [9]], np.int32),
+     dict(offset_dims=[1], collapsed=[0], start_index_map=[0], ivd=1, slice_sizes=[1, 5])),
+    ((5, 7), np.array([[0, 0], [4, 6], [2, 3], [1, 5]], np.int32),
+     dict(offset_dims=[], collapsed=[0, 1], start_index_map=[0, 1], ivd=1, slice_sizes=[1, 1])),
+    ((5, 7), np.array([[0, 0], [4, 6], [2, 3], [1, 5]], np.int64),
+     dict(offset_dims=[1, 2], collapsed=[], start_index_map=[0, 1], ivd=1, slice_sizes=[2, 3])),
+    ((3, 6, 4), np.random.default_rng(3).integers(0, 6, size=(3, 5)).astype(np.int32),
+     dict(offset_dims=[2], collapsed=[1], start_index_map=[1], ivd=2, slice_sizes=[1, 1, 4],
+          operand_batching=[0], start_batching=[0])),
+]
+
+
+def _gdims(kw):
+    return O.GatherDimensionNumbers(kw["offset_dims"], kw["collapsed"], kw["start_index_map"],
+                                    kw["ivd"], kw.get("operand_batching", ()),
+                                    kw.get("start_batching", ()))
+
+
+@pytest.mark.parametrize("case", range(len(GATHER_CASES)))
+def test_gather_eager_and_jit_against_oracle(gpu, oracle, case):
+    shape, idx, kw = GATHER_CASES[case]
+    x = np.random.default_rng(case).standard_normal(shape).astype(np.float32)
+    want = oracle.gather(x, idx, **kw)
+    dims, ss = _gdims(kw), kw["slice_sizes"]
+    xt, it = E.fromHost(x), E.fromHost(idx)
+    eager = O.gather(xt, it, dims, ss, want.shape)
+    np.testing.assert_array_equal(E.toHost(eager), want)
+    (jitted,) = J.jit(lambda a: [O.gather(a[0], a[1], dims, ss, want.shape)],
+                      f"gather{case}").call([xt, it])
+    np.testing.assert_array_equal(E.toHost(jitted), want)
+
+
+@pytest.mark.parametrize("op", ["add", "maximum", "minimum", "multiply", "replace"])
+@pytest.mark.parametrize("dt", [DType.FLOAT32, DType.INT32, DType.BFLOAT16])
+def test_scatter_eager_and_jit_against_oracle(gpu, oracle, op, dt):
+    rs = np.random.default_rng(11)
+    x = rs.integers(-4, 5, size=(6, 3)).astype(np.float32)
+    upd = rs.integers(-4, 5, size=(7, 3)).astype(np.float32)
+    if op == "replace":   # unique in-range indices: the result is order-free
+        idx = np.array([[1], [4], [0], [9], [-1], [5], [2]], np.int32)
+    else:                 # duplicates and two out-of-range rows (skipped)
+        idx = np.array([[1], [4], [1], [9], [4], [-1], [4]], np.int32)
+    dims = O.ScatterDimensionNumbers([1], [0], [0], 1)
+    want = oracle.scatter(x, idx, upd, update_window_dims=[1], inserted=[0],
+                          scatter_dims_to_operand=[0], ivd=1, op=op)
+    np_dt = {DType.FLOAT32: np.float32, DType.INT32: np.int32}.get(dt)
+    mk = (lambda a: E.fromHost(a.astype(np_dt))) if np_dt else (lambda a: E.fromHost(a, dt))
+    rd = (lambda t: E.toHost(t).astype(np.float32)) if np_dt else (lambda t: E.toHostF32(t))
+    xt, it, ut = mk(x), E.fromHost(idx), mk(upd)
+    (eager,) = O.scatter([xt], it, [ut], dims, op)
+    np.testing.assert_array_equal(rd(eager), want)   # small integers: every order is exact
+    (jitted,) = J.jit(lambda a: O.scatter([a[0]], a[1], [a[2]], dims, op),
+                      f"scatter_{op}_{int(dt)}").call([xt, it, ut])
+    np.testing.assert_array_equal(rd(jitted), want)
