@@ -222,6 +222,9 @@ typedef struct rew_mi355x_stats {
                                /* and translated a module                   */
   int64_t jit_module_hits;     /* rew_mi355x_execute_jit calls served by a  */
                                /* cached module                             */
+  int64_t programs_compiled;   /* fused programs compiled at run time, and  */
+  int64_t programs_loaded;     /* those loaded from the persistent cache    */
+                               /* (REW_CACHE_DIR; process-wide since reset) */
 } rew_mi355x_stats;
 
 int rew_mi355x_get_stats(rew_mi355x_ctx* ctx, rew_mi355x_stats* out);

@@ -118,7 +118,7 @@ class Stats(C.Structure):
     _fields_ = [(n, C.c_int64) for n in (
         "ops_recorded", "kernels_launched", "flushes", "fused_groups",
         "bytes_in_use", "bytes_cached", "plan_cache_hits", "jit_module_compiles",
-        "jit_module_hits")]
+        "jit_module_hits", "programs_compiled", "programs_loaded")]
 
 
 _lib = None

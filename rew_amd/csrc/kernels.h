@@ -22,8 +22,11 @@ struct ReduceArgs;
 bool jit_launch_ew(const vm::Program& P, const vm::Space& S, bool vec, hipStream_t stream);
 bool jit_launch_reduce(const vm::Program& P, const vm::Space& S, const ReduceArgs& A, bool vec,
                        hipStream_t stream);
-// Launches so far (process-wide) that reused an already compiled program.
+// Launches so far (process-wide) that reused an already compiled program;
+// programs compiled by hipRTC and programs loaded from the persistent cache.
 int64_t jit_cache_hits();
+int64_t jit_programs_compiled();
+int64_t jit_programs_loaded();
 
 // ---- reductions (k_reduce.hip) ---------------------------------------------
 enum RedOp : int {

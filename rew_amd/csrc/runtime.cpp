@@ -318,6 +318,8 @@ int rew_mi355x_init(int ordinal, rew_mi355x_ctx** out) {
       c->ordinal = ordinal;
       c->alloc.ordinal = ordinal;
       c->jit_hits_base = jit_cache_hits();
+      c->compiled_base = jit_programs_compiled();
+      c->loaded_base = jit_programs_loaded();
       REW_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
       // once per device, with the device current
       c->noalloc_scratch = noalloc_scratch_lookup(&c->noalloc_error);
@@ -631,6 +633,8 @@ int rew_mi355x_get_stats(rew_mi355x_ctx* ctx, rew_mi355x_stats* out) {
     c->stats.bytes_in_use = (int64_t)c->alloc.in_use;
     c->stats.bytes_cached = (int64_t)c->alloc.cached;
     c->stats.plan_cache_hits = jit_cache_hits() - c->jit_hits_base;
+    c->stats.programs_compiled = jit_programs_compiled() - c->compiled_base;
+    c->stats.programs_loaded = jit_programs_loaded() - c->loaded_base;
     *out = c->stats;
   });
 }
@@ -641,6 +645,8 @@ int rew_mi355x_reset_stats(rew_mi355x_ctx* ctx) {
     std::lock_guard<std::recursive_mutex> g(c->mu);
     c->stats = rew_mi355x_stats{};
     c->jit_hits_base = jit_cache_hits();
+    c->compiled_base = jit_programs_compiled();
+    c->loaded_base = jit_programs_loaded();
   });
 }
 

@@ -107,6 +107,7 @@ struct Ctx {
   bool no_fusion_patterns = false;  // REW_MI355X_NO_PATTERNS=1: per-op kernels only
   rew_mi355x_stats stats{};
   int64_t jit_hits_base = 0;  // jit_cache_hits() when the stats were last reset
+  int64_t compiled_base = 0, loaded_base = 0;  // program counters at the last reset
   // device copies of small host constants (dtype, shape and bytes as the
   // key): eager tensors are immutable, so a repeated upload of the same
   // scalar (rew's composites upload eps, 1.0, mask values... every call)
