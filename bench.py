@@ -590,10 +590,25 @@ def run_mnist(args):
     xt = E.fromHost(x)
     E.sync()
 
-    def step():
-        ids = O.argmax(nn.softmax(l2.forward(nn.relu(l1.forward(xt))), 1), 1)
-        E.flush()
-        return ids
+    if args.mnist_path == "lazy":
+        # Linear -> relu -> Linear -> softmax as one lazy batch (the traced
+        # module, parameters as arguments), then the argmax: rew's argmax
+        # raises in both modes (its int32 reduceMin), so it runs as the
+        # backend's native op on the batch's output
+        from rew_amd import jit as J
+        mlp = J.lazy(lambda a: [nn.softmax(nn.Linear(a[3], a[4]).forward(
+            nn.relu(nn.Linear(a[1], a[2]).forward(a[0]))), 1)], "mnistMlp")
+        call_args = [xt, l1.weight, l1.bias, l2.weight, l2.bias]
+
+        def step():
+            ids = O.argmax(mlp.call(call_args)[0], 1)
+            E.flush()
+            return ids
+    else:
+        def step():
+            ids = O.argmax(nn.softmax(l2.forward(nn.relu(l1.forward(xt))), 1), 1)
+            E.flush()
+            return ids
 
     wall, dev_ms, first_ms, prof = timed_run(step, args.steps, args.warmup)
     ms = wall * 1e3 / args.steps
@@ -627,7 +642,8 @@ def run_mnist(args):
                "sample": f"{reps} forwards of the full [128,784] batch, oracle/ C restatement, "
                          f"{dt:.1f} s"}
     emit(args, "mnist_mlp_rows_per_s", B * args.steps / wall, "rows/s", ms, "f32",
-         {"workload": "mnist_mlp_inference_f32", "batch": B, "layers": [D, Hd, C]},
+         {"workload": "mnist_mlp_inference_f32", "batch": B, "layers": [D, Hd, C],
+          "path": args.mnist_path},
          roof, cpu, {"kernels": breakdown(syms, args.steps), "first_call_ms": round(first_ms, 2),
                      "us_per_forward": round(ms * 1e3, 1), "algorithmic_flops": flops,
                      "device_us_per_forward": round(dev_ms * 1e3 / args.steps, 1)})
@@ -646,6 +662,9 @@ def main():
     ap.add_argument("--cpu-seqs", type=int, default=2,
                     help="sequences of the llama batch in the cpu_baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--mnist-path", default="lazy", choices=["lazy", "eager"],
+                    help="mnist workload: the MLP as a lazy batch then the native argmax, or "
+                         "every op dispatched eagerly")
     ap.add_argument("--moe-path", default="lazy", choices=["lazy", "eager"],
                     help="moe workload: rew's lazy batch (its executable form) or the "
                          "eager op stream of the mirror")

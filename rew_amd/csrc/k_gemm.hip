@@ -41,6 +41,8 @@ __device__ __forceinline__ float epi_value(const GemmArgs& g, int64_t b, int64_t
   if (g.epi == EPI_NONE) return d;
   const float y = epi_rnd(dt, d + epi_ld(g.bias, dt, n));
   if (g.epi == EPI_BIAS) return y;
+  if (g.epi == EPI_BIAS_RELU)
+    return g.relu_first ? vm::fmax_prop(y, g.relu_c) : vm::fmax_prop(g.relu_c, y);
   return epi_rnd(dt, epi_ld(g.res, dt, b * g.res_sb + m * g.res_sm + n) + y);
 }
 // GatedFeedForward's gate (src/rew/nn/gated_ffn.nim:46-67 with
@@ -118,6 +120,149 @@ __global__ void __launch_bounds__(256) gemm_generic_kernel(GemmArgs g) {
       }
     }
   }
+}
+
+// Small problems (too few 64x64 tiles to occupy the GPU, e.g. the MNIST
+// MLP's 128 x 784 x 128): the time is one output's k-chain plus the memory
+// latency in front of it, so every thread owns one output of a 16 x 16 tile
+// (sixteen times the generic kernel's workgroups).  WHOLE: the tile's whole
+// A (16 x K) and B (K x 16) slabs are loaded into LDS at once, one round of
+// loads in flight together, then the chains run; otherwise 64-deep chunks,
+// the next one loaded into registers while the current one is multiplied.
+// Each output is the same sequential fmaf chain over k = 0, 1, ... with zero
+// terms past K (to a multiple of 16) as gemm_generic_kernel's, so the
+// kernels give the same bits.
+constexpr int kSmallWholeK = 1024;  // WHOLE mode: 16-padded K up to this (136 KiB of LDS)
+
+template <bool WHOLE>
+__global__ void __launch_bounds__(256) gemm_f32_small_kernel(GemmArgs g) {
+  extern __shared__ float sm[];  // As [KC][17] then Bs [KC][17], KC = 64 or padded K
+  const int tid = threadIdx.x;
+  const int r = tid >> 4, cc = tid & 15;
+  const int64_t m0 = (int64_t)blockIdx.y * 16, n0 = (int64_t)blockIdx.x * 16;
+  const int K16 = (int)((g.K + 15) & ~15);
+  const int KC = WHOLE ? K16 : 64;
+  float* As = sm;
+  float* Bs = sm + KC * 17;
+  for (int64_t b = blockIdx.z; b < g.batch; b += gridDim.z) {
+    if constexpr (WHOLE) {
+      // A slab 16 x K16: 16 threads per row; B slab K16 x 16: 4 threads per
+      // k row.  f32 rows contiguous and 16-byte aligned (the usual
+      // [M, K] x [K, N] layout): 16-byte loads; otherwise element loads.
+      const int ra = tid >> 4, la = tid & 15, kq = tid >> 2, nq = (tid & 3) * 4;
+      const int64_t ma = m0 + ra;
+      const bool vec = g.dtype == REW_DT_FLOAT32 && g.a_sk == 1 && g.b_sn == 1 &&
+                       g.K % 4 == 0 && g.N % 4 == 0 && g.a_sm % 4 == 0 && g.b_sk % 4 == 0 &&
+                       g.a_sb % 4 == 0 && g.b_sb % 4 == 0 && ((uintptr_t)g.a & 15) == 0 &&
+                       ((uintptr_t)g.b & 15) == 0;
+      if (vec) {
+        const float* ap = (const float*)g.a + b * g.a_sb + (ma < g.M ? ma : 0) * g.a_sm;
+        for (int k = la * 4; k < K16; k += 64) {
+          float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          if (ma < g.M && k < g.K) v = *(const float4*)(ap + k);
+          As[k * 17 + ra] = v.x;
+          As[(k + 1) * 17 + ra] = v.y;
+          As[(k + 2) * 17 + ra] = v.z;
+          As[(k + 3) * 17 + ra] = v.w;
+        }
+        const int64_t nb = n0 + nq;
+        const float* bp = (const float*)g.b + b * g.b_sb + (nb < g.N ? nb : 0);
+        for (int k = kq; k < K16; k += 64) {
+          float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          if (k < g.K && nb < g.N) v = *(const float4*)(bp + (int64_t)k * g.b_sk);
+          Bs[k * 17 + nq] = v.x;
+          Bs[k * 17 + nq + 1] = v.y;
+          Bs[k * 17 + nq + 2] = v.z;
+          Bs[k * 17 + nq + 3] = v.w;
+        }
+      } else {
+        for (int k = la; k < K16; k += 16)
+          As[k * 17 + ra] = (ma < g.M && k < g.K)
+                                ? load_as_float(g.a, g.dtype, b * g.a_sb + ma * g.a_sm + k * g.a_sk)
+                                : 0.0f;
+        const int nc = tid & 15;
+        const int64_t n = n0 + nc;
+        for (int k = tid >> 4; k < K16; k += 16)
+          Bs[k * 17 + nc] = (k < g.K && n < g.N)
+                                ? load_as_float(g.b, g.dtype, b * g.b_sb + k * g.b_sk + n * g.b_sn)
+                                : 0.0f;
+      }
+      __syncthreads();
+      float acc = 0.0f;
+      for (int k = 0; k < K16; k += 16) {
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk)
+          acc = fmaf(As[(k + kk) * 17 + r], Bs[(k + kk) * 17 + cc], acc);
+      }
+      __syncthreads();
+      const int64_t m = m0 + r, n = n0 + cc;
+      if (m < g.M && n < g.N)
+        vm::store_scalar(g.c, g.c_dtype, b * g.c_sb + m * g.c_sm + n,
+                         vm::as_u(epi_value(g, b, m, n, acc)));
+      continue;
+    }
+    // chunked: element e = tid + 256 i of the 16 x 64 A chunk (row e / 64,
+    // k e % 64) and of the 64 x 16 B chunk (k e / 16, column e % 16)
+    float pa[4], pb[4];
+    auto gload = [&](int64_t k0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = tid + 256 * i;
+        const int64_t m = m0 + (e >> 6), ka = k0 + (e & 63);
+        pa[i] = (m < g.M && ka < g.K)
+                    ? load_as_float(g.a, g.dtype, b * g.a_sb + m * g.a_sm + ka * g.a_sk)
+                    : 0.0f;
+        const int64_t kb = k0 + (e >> 4), n = n0 + (e & 15);
+        pb[i] = (kb < g.K && n < g.N)
+                    ? load_as_float(g.b, g.dtype, b * g.b_sb + kb * g.b_sk + n * g.b_sn)
+                    : 0.0f;
+      }
+    };
+    float acc = 0.0f;
+    gload(0);
+    for (int64_t k0 = 0; k0 < g.K; k0 += 64) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = tid + 256 * i;
+        As[(e & 63) * 17 + (e >> 6)] = pa[i];
+        Bs[(e >> 4) * 17 + (e & 15)] = pb[i];
+      }
+      __syncthreads();
+      if (k0 + 64 < g.K) gload(k0 + 64);
+      // the generic kernel's chain ends at the first multiple of 16 >= K
+      const int kn = (g.K - k0 >= 64) ? 64 : (int)(((g.K - k0) + 15) & ~15);
+      if (kn == 64) {
+#pragma unroll
+        for (int kk = 0; kk < 64; ++kk) acc = fmaf(As[kk * 17 + r], Bs[kk * 17 + cc], acc);
+      } else {
+        for (int kk = 0; kk < kn; ++kk) acc = fmaf(As[kk * 17 + r], Bs[kk * 17 + cc], acc);
+      }
+      __syncthreads();
+    }
+    const int64_t m = m0 + r, n = n0 + cc;
+    if (m < g.M && n < g.N)
+      vm::store_scalar(g.c, g.c_dtype, b * g.c_sb + m * g.c_sm + n,
+                       vm::as_u(epi_value(g, b, m, n, acc)));
+  }
+}
+
+static void launch_gemm_small(const GemmArgs& g, hipStream_t stream) {
+  dim3 grid((unsigned)((g.N + 15) / 16), (unsigned)((g.M + 15) / 16),
+            (unsigned)(g.batch < 65535 ? g.batch : 65535));
+  const int64_t k16 = (g.K + 15) & ~(int64_t)15;
+  if (k16 <= kSmallWholeK) {
+    const size_t lds = (size_t)k16 * 17 * 4 * 2;
+    static bool attr = [] {
+      return hipFuncSetAttribute((const void*)gemm_f32_small_kernel<true>,
+                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 kSmallWholeK * 17 * 4 * 2) == hipSuccess;
+    }();
+    if (attr || lds <= 65536) {
+      hipLaunchKernelGGL(gemm_f32_small_kernel<true>, grid, dim3(256), lds, stream, g);
+      return;
+    }
+  }
+  hipLaunchKernelGGL(gemm_f32_small_kernel<false>, grid, dim3(256), 64 * 17 * 4 * 2, stream, g);
 }
 
 // ---------------------------------------------------------------------------
@@ -740,6 +885,12 @@ static bool f32_narrow_ok(const GemmArgs& g) {
          g.M / 16 < (1 << 30);
 }
 
+// Problems whose 64x64 tiles would leave most CUs idle run 16x16 tiles.
+static bool small_ok(const GemmArgs& g) {
+  const int64_t tiles64 = ((g.M + 63) / 64) * ((g.N + 63) / 64) * g.batch;
+  return tiles64 < 128 && g.epi != EPI_SWIGLU && g.epi != EPI_BIAS_ROPE;
+}
+
 static bool mfma_ok(const GemmArgs& g, bool* a_kc, bool* b_kc) {
   if (g.dtype != REW_DT_BFLOAT16) return false;
   if (g.c_dtype != REW_DT_BFLOAT16 && g.c_dtype != REW_DT_FLOAT32) return false;
@@ -807,6 +958,9 @@ static bool use_256(const GemmArgs& g, bool akc) {
 bool gemm_epilogue_ok(const GemmArgs& g) {
   if (g.epi == EPI_NONE) return true;
   if (g.epi == EPI_BIAS_ROPE) return false;  // launch_gemm_multi only
+  bool akc0, bkc0;
+  if (g.epi == EPI_BIAS_RELU)  // the f32 kernels only (generic / small)
+    return g.c_dtype == REW_DT_FLOAT32 && !mfma_ok(g, &akc0, &bkc0) && !use_lds(g);
   if (g.c_dtype != REW_DT_BFLOAT16 && g.c_dtype != REW_DT_FLOAT32) return false;
   if (g.epi != EPI_SWIGLU) return true;
   bool lkc;
@@ -825,7 +979,8 @@ const char* gemm_variant(const GemmArgs& g) {
     return g.epi == EPI_SWIGLU ? "gemm_lds_swiglu" : (bkc ? "gemm_lds_tn" : "gemm_lds_nn");
   }
   if (g.epi == EPI_SWIGLU) return "gemm_bf16_256_swiglu";
-  if (!mfma_ok(g, &akc, &bkc)) return f32_narrow_ok(g) ? "gemm_f32_narrow" : "gemm_generic";
+  if (!mfma_ok(g, &akc, &bkc))
+    return f32_narrow_ok(g) ? "gemm_f32_narrow" : (small_ok(g) ? "gemm_f32_small" : "gemm_generic");
   if (use_256(g, akc)) return bkc ? "gemm_bf16_256_tn" : "gemm_bf16_256_nn";
   if (akc && bkc) return "gemm_bf16_mfma_tn";
   if (akc) return "gemm_bf16_mfma_nn";
@@ -867,6 +1022,8 @@ void launch_gemm(const GemmArgs& g, hipStream_t stream) {
   } else if (f32_narrow_ok(g)) {
     hipLaunchKernelGGL(gemm_f32_narrow_kernel, dim3((unsigned)((g.M + 15) / 16)), dim3(256), 0,
                        stream, g);
+  } else if (small_ok(g)) {
+    launch_gemm_small(g, stream);
   } else {
     dim3 grid((unsigned)((g.N + 63) / 64), (unsigned)((g.M + 63) / 64),
               (unsigned)(g.batch < 65535 ? g.batch : 65535));

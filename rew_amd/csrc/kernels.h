@@ -89,9 +89,15 @@ struct GemmArgs {
   int64_t rope_S, rope_D;
   int64_t rope_tb, rope_ts, rope_th, rope_ti;
   int64_t out_b, out_s, out_h;
+  // EPI_BIAS_RELU (the f32 kernels that store through epi_value): rew's relu
+  // after the bias add, c = maximum(y, relu_c) (relu_first) or
+  // maximum(relu_c, y), NaN-propagating with the VM's zero-sign rule
+  float relu_c;
+  int relu_first;
 };
 enum GemmEpi : int {
-  EPI_NONE = 0, EPI_BIAS = 1, EPI_BIAS_RES = 2, EPI_SWIGLU = 3, EPI_BIAS_ROPE = 4
+  EPI_NONE = 0, EPI_BIAS = 1, EPI_BIAS_RES = 2, EPI_SWIGLU = 3, EPI_BIAS_ROPE = 4,
+  EPI_BIAS_RELU = 5
 };
 void launch_gemm(const GemmArgs& g, hipStream_t stream);
 

@@ -222,6 +222,9 @@ struct GemmPlan {
   Tensor* rope_sin = nullptr;
   bool rope_t = false;
   int64_t rope_B = 0, rope_S = 0, rope_H = 0, rope_D = 0;
+  // EPI_BIAS_RELU: maximum(y, relu_c) or maximum(relu_c, y)
+  float relu_c = 0.0f;
+  bool relu_first = true;
   // projections of one input launched together (GroupedQueryAttention's
   // q / k / v): index into Lower::gemm_groups, or -1
   int group = -1;
@@ -1783,6 +1786,22 @@ void Lower::match_gemm_epilogues() {
         out = c1->out[0];
       }
     }
+    // rew's relu (maximum with a broadcast zero constant) after an f32 bias add
+    if (gp.epi == EPI_BIAS && D->dt == kF32) {
+      Node* c2 = sole_consumer(*this, y);
+      float v;
+      if (c2 && c2->kind == K_BINARY && c2->sub == 4 && c2->in[0] != c2->in[1] &&
+          c2->out[0]->shape == y->shape) {
+        const int yi = c2->in[0] == y ? 0 : 1;
+        if (const_bcast(c2->in[1 - yi], &v)) {
+          gp.epi = EPI_BIAS_RELU;
+          gp.relu_c = v;
+          gp.relu_first = yi == 0;
+          inner.push_back(y);
+          out = c2->out[0];
+        }
+      }
+    }
     for (Tensor* t : inner) t->plan_mat = false;
     out->plan_mat = true;
     gemm_out[out] = gp;
@@ -1801,6 +1820,8 @@ bool Lower::gemm_fused_args(Tensor* t, const GemmPlan& p, GemmArgs& g) {
   g.epi = p.epi;
   g.bias = vec(p.bias);
   if (!g.bias) return false;
+  g.relu_c = p.relu_c;
+  g.relu_first = p.relu_first ? 1 : 0;
   if (p.epi == EPI_SWIGLU) {
     GemmArgs g2;
     Tensor *ta2, *tb2;
@@ -1869,6 +1890,7 @@ static const char* epi_suffix(int epi) {
     case EPI_BIAS: return "+bias";
     case EPI_BIAS_RES: return "+bias+res";
     case EPI_BIAS_ROPE: return "+bias+rope";
+    case EPI_BIAS_RELU: return "+bias+relu";
     default: return "";
   }
 }

@@ -13,6 +13,7 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 from rew_amd import eager as E
+from rew_amd import nn
 from rew_amd import ops as O
 from rew_amd.eager import DType
 
@@ -230,6 +231,63 @@ def test_matmul_f32_narrow(gpu, oracle, M, K, N):
     want = oracle.gemm(a, b) + bias
     bound = 1e-5 * (oracle.gemm(np.abs(a), np.abs(b)) + np.abs(bias))
     assert np.all(np.abs(got - want) <= bound + 1e-30)
+
+
+@pytest.mark.parametrize("M,K,N", [(128, 784, 128), (128, 128, 10), (37, 100, 70)])
+def test_matmul_f32_small_equals_generic(gpu, oracle, M, K, N):
+    """Products with too few 64x64 tiles to fill the GPU (the MNIST MLP's)
+    take 16x16 tiles with the next k-chunk prefetched; each output keeps the
+    generic kernel's fmaf chain, so a batch of 128 of the same product (enough
+    tiles for the generic kernel) gives the same bits in every slice."""
+    r = rng(M * 3 + K + N)
+    a = r.uniform(-1, 1, (M, K)).astype(np.float32)
+    b = r.uniform(-0.1, 0.1, (K, N)).astype(np.float32)
+    E.profileBegin()
+    got = host(O.matmul(dev(a), dev(b)))
+    names = [n for n, _, _ in E.profileEnd()]
+    assert any(n.startswith("gemm_f32_small") for n in names), names
+    ab = np.broadcast_to(a, (128, M, K)).copy()
+    bb = np.broadcast_to(b, (128, K, N)).copy()
+    E.profileBegin()
+    ref = host(O.dotGeneral(dev(ab), dev(bb), [0], [0], [2], [1]))
+    names = [n for n, _, _ in E.profileEnd()]
+    assert any(n.startswith("gemm_generic") for n in names), names
+    for i in range(128):
+        np.testing.assert_array_equal(ref[i].view(np.uint32), got.view(np.uint32))
+    bound = 1e-5 * oracle.gemm(np.abs(a), np.abs(b))
+    assert np.all(np.abs(got - oracle.gemm(a, b)) <= bound + 1e-30)
+
+
+@pytest.mark.parametrize("first", [True, False])
+def test_f32_linear_relu_epilogue(gpu, oracle, first):
+    """rew's relu (maximum with a broadcast zero, nn/activation.nim:21-26)
+    after an f32 Linear folds into the GEMM epilogue; values equal the
+    op-by-op path bit for bit, including zero signs and both operand orders."""
+    r = rng(91 + first)
+    M, K, N = 128, 784, 128
+    a = r.uniform(0, 1, (M, K)).astype(np.float32)
+    b = r.uniform(-0.05, 0.05, (K, N)).astype(np.float32)
+    bias = r.uniform(-0.05, 0.05, (N,)).astype(np.float32)
+    bias[:8] = 0.0
+
+    def fwd():
+        y = nn.Linear(dev(b), dev(bias)).forward(dev(a))
+        zero = O.broadcastTo(O.scalarF32(0.0), [M, N], [])
+        return O.maximum(y, zero) if first else O.maximum(zero, y)
+
+    E.profileBegin()
+    got = host(fwd())
+    names = [n for n, _, _ in E.profileEnd()]
+    assert any(n.startswith("gemm_f32_small") and "+bias+relu" in n for n in names), names
+    assert len(names) == 1, names
+    E.setMode(E.MODE_OP_BY_OP)
+    try:
+        ref = host(fwd())
+    finally:
+        E.setMode(E.MODE_DEFERRED)
+    np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+    want = np.maximum(oracle.gemm(a, b) + bias, 0)
+    assert np.all(np.abs(got - want) <= 1e-5 * (oracle.gemm(np.abs(a), np.abs(b)) + 1) + 1e-30)
 
 
 def _bf16_close(got, want, tol=2e-2):
