@@ -358,16 +358,53 @@ __global__ void __launch_bounds__(256) softmax_wave_kernel(SoftmaxArgs a) {
 
 // Rows shorter than 128: the compiled reduction runs a thread per row over
 // j = 0, 1, ... in order; so does this kernel.
-__global__ void __launch_bounds__(256) softmax_thread_kernel(SoftmaxArgs a) {
-  for (int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x; row < a.rows;
-       row += (int64_t)gridDim.x * 256) {
-    const float* x = a.x + row * a.x_rs;
-    float m = -INFINITY;
-    for (int64_t j = 0; j < a.n; ++j) m = fmax_prop(m, x[j]);
-    float sum = 0.0f;
-    for (int64_t j = 0; j < a.n; ++j) sum = sum + expf(x[j] - m);
-    float* y = a.y + row * a.n;
-    for (int64_t j = 0; j < a.n; ++j) y[j] = expf(x[j] - m) / sum;
+// Rows shorter than 128: a workgroup stages R rows in LDS with coalesced
+// loads (row pitch n + 1 against bank conflicts), one thread runs each row's
+// three sequential passes -- max, sum of expf(x - m), expf(x - m) / sum --
+// in the order of the compiled reductions over short rows, so the result
+// equals rew's five-op sequence bit for bit, and the results leave through
+// LDS as coalesced stores.  R = 256 rows for n <= 62 (64 KiB), else 128.
+template <int R>
+__global__ void __launch_bounds__(256) softmax_tile_kernel(SoftmaxArgs a) {
+  extern __shared__ float tile[];
+  const int n = (int)a.n, pitch = n + 1;
+  const int q = 256 / n, rem = 256 % n;
+  for (int64_t r0 = (int64_t)blockIdx.x * R; r0 < a.rows; r0 += (int64_t)gridDim.x * R) {
+    const int nr = (int)(a.rows - r0 < R ? a.rows - r0 : R);
+    // element i = row * n + col of the tile, walked in steps of 256
+    int row = threadIdx.x / n, col = threadIdx.x - row * n;
+    for (int i = threadIdx.x; i < nr * n; i += 256) {
+      tile[row * pitch + col] = a.x[(r0 + row) * a.x_rs + col];
+      col += rem;
+      row += q;
+      if (col >= n) {
+        col -= n;
+        ++row;
+      }
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < nr) {
+      float* t = tile + threadIdx.x * pitch;
+      float m = -INFINITY;
+      for (int j = 0; j < n; ++j) m = fmax_prop(m, t[j]);
+      float sum = 0.0f;
+      for (int j = 0; j < n; ++j) sum = sum + expf(t[j] - m);
+      for (int j = 0; j < n; ++j) t[j] = expf(t[j] - m) / sum;
+    }
+    __syncthreads();
+    row = threadIdx.x / n;
+    col = threadIdx.x - row * n;
+    float* y = a.y + r0 * n;
+    for (int i = threadIdx.x; i < nr * n; i += 256) {
+      y[i] = tile[row * pitch + col];
+      col += rem;
+      row += q;
+      if (col >= n) {
+        col -= n;
+        ++row;
+      }
+    }
+    __syncthreads();
   }
 }
 
@@ -381,9 +418,17 @@ bool softmax_rows_ok(const SoftmaxArgs& a) {
 void launch_softmax_rows(const SoftmaxArgs& a, hipStream_t stream) {
   if (!softmax_rows_ok(a)) fail(REW_MI355X_ERR_INVALID, "internal: softmax rows not launchable");
   if (a.n < 128) {
-    const int64_t blocks = (a.rows + 255) / 256;
-    hipLaunchKernelGGL(softmax_thread_kernel, dim3((unsigned)(blocks < 65536 ? blocks : 65536)),
-                       dim3(256), 0, stream, a);
+    if (a.n <= 62) {
+      const int64_t blocks = (a.rows + 255) / 256;
+      hipLaunchKernelGGL(softmax_tile_kernel<256>,
+                         dim3((unsigned)(blocks < 65536 ? blocks : 65536)), dim3(256),
+                         (size_t)256 * (a.n + 1) * 4, stream, a);
+    } else {
+      const int64_t blocks = (a.rows + 127) / 128;
+      hipLaunchKernelGGL(softmax_tile_kernel<128>,
+                         dim3((unsigned)(blocks < 65536 ? blocks : 65536)), dim3(256),
+                         (size_t)128 * (a.n + 1) * 4, stream, a);
+    }
   } else {
     // Rows of exactly 1024, 2048 or 4096 use the pipelined unguarded
     // kernels: at most 2048 waves (two workgroups per CU), each walking

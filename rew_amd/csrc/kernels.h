@@ -265,7 +265,9 @@ struct MoeRouteArgs {
   int32_t* mt_start;         // [n_members + 1] tile starts (out)
   int32_t* perm;             // [T * k] packed row -> token (out)
   int32_t* slot_of;          // [T * k] (token, k-slot) -> packed row (out)
+  int32_t* blk_cnt;          // [ceil(T / kMoeRouteBlock) * n_members] working counts
 };
+constexpr int kMoeRouteBlock = 256;  // tokens per routing workgroup
 void launch_moe_route(const MoeRouteArgs& a, hipStream_t stream);
 
 // out[t, :] = prev[t, :] then, for token t's routed members in chain order,

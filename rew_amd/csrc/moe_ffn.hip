@@ -7,8 +7,10 @@
 //   member_of [E] int32    expert id -> chain index, -1 off the chain
 //   members   [n] int32    chain index -> expert id
 //   tables    [6 n] ptr    per-expert weight / bias device pointers
-//   route     [2 (n + 1) + 2 R] int32   offsets, tile starts, packed row ->
-//                                       token, (token, slot) -> packed row
+//   route     [2 (n + 1) + 2 R + nb n] int32   offsets, tile starts,
+//                                       packed row -> token, (token, slot) ->
+//                                       packed row, per-block counts (nb =
+//                                       ceil(T / 256) token blocks)
 //   hbuf      [R, I] bf16  SwiGLU outputs of the routed rows
 //   ybuf      [R, H] bf16  down-projection outputs of the routed rows
 // with R = T k routed rows.  Every byte a kernel reads is written earlier
@@ -74,7 +76,8 @@ Layout layout_of(const RoutedFfn& a) {
   L.tables = o;
   o += up((size_t)a.n * 6 * sizeof(void*));
   L.route = o;
-  o += up((2 * ((size_t)a.n + 1) + 2 * R) * 4);
+  const size_t nb = ((size_t)a.T + kMoeRouteBlock - 1) / kMoeRouteBlock;
+  o += up((2 * ((size_t)a.n + 1) + 2 * R + nb * (size_t)a.n) * 4);
   L.hbuf = o;
   o += up(R * (size_t)a.I * 2);
   L.ybuf = o;
@@ -125,6 +128,7 @@ void routed_ffn_check(const RoutedFfn& a) {
   if (a.k < 1 || a.k > kMoeMaxK) bad("k must be in 1.." + std::to_string(kMoeMaxK));
   if (a.E < 1) bad("router_width must be positive");
   if (a.n < 1 || a.n > a.E) bad("n_experts must be in 1..router_width");
+  if (a.n > 3200) bad("at most 3200 experts per call");
   if (a.T * (int64_t)a.k >= ((int64_t)1 << 31)) bad("tokens * k must be below 2^31");
   if (!a.expert) bad("null expert_ids");
   for (int i = 0; i < a.n; ++i) {
@@ -201,6 +205,7 @@ void run_routed_ffn(Ctx* c, const RoutedFfn& a, void* scratch) {
   ra.mt_start = route + (n + 1);
   ra.perm = route + 2 * (n + 1);
   ra.slot_of = route + 2 * (n + 1) + R;
+  ra.blk_cnt = route + 2 * (n + 1) + 2 * R;
   if (c->profiling)
     prof_begin(c, "moe_route{" + std::to_string(a.T) + "x" + std::to_string(a.k) + ",E" +
                       std::to_string(n) + "}");
