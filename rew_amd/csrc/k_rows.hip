@@ -87,10 +87,31 @@ __global__ void __launch_bounds__(256) rmsnorm_rows_kernel(RowNormArgs a) {
 // rms_row: that arithmetic for one row whose chunks are in raw (chunk k of
 // lane l holds elements (64 k + l) EPC_X ..); gam(k, e) is gamma of element
 // e of chunk k.  FULL: every chunk is in range (n == 64 CH EPC_X).
+// row of x that feeds output row r (the gather form reads it from ids)
+__device__ __forceinline__ int64_t src_row(const RowNormArgs& a, int64_t r) {
+  if (!a.ids) return r;
+  int64_t i;
+  switch (a.ids_dt) {
+    case REW_DT_INT32: i = ((const int32_t*)a.ids)[r]; break;
+    case REW_DT_UINT32: i = ((const uint32_t*)a.ids)[r]; break;
+    case REW_DT_INT64: i = ((const int64_t*)a.ids)[r]; break;
+    default: i = (int64_t)((const uint64_t*)a.ids)[r]; break;
+  }
+  return i < 0 ? 0 : (i >= a.x_rows ? a.x_rows - 1 : i);
+}
+
 template <int XB, int YB, int CH, bool FULL, typename Gamma>
 __device__ __forceinline__ void rms_row(const RowNormArgs& a, int64_t row, int lane,
                                         const uint4 (&raw)[CH], Gamma gam) {
   constexpr int EPC_X = 16 / XB;
+  if (a.xout) {  // gather form: the gathered row itself
+    char* xo = (char*)a.xout + row * a.n * XB;
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      const int64_t j = ((int64_t)k * 64 + lane) * EPC_X;
+      if (FULL || j < a.n) *(uint4*)(xo + j * XB) = raw[k];
+    }
+  }
   float ss = 0.0f;
 #pragma unroll
   for (int k = 0; k < CH; ++k) {
@@ -142,7 +163,7 @@ __global__ void __launch_bounds__(256) rmsnorm_wave_kernel(RowNormArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t waves = (int64_t)gridDim.x * 4;
   for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < a.rows; row += waves) {
-    const char* x = (const char*)a.x + row * a.x_rs * XB;
+    const char* x = (const char*)a.x + src_row(a, row) * a.x_rs * XB;
     uint4 raw[CH];
 #pragma unroll
     for (int k = 0; k < CH; ++k) {
@@ -181,7 +202,7 @@ __global__ void __launch_bounds__(256) rmsnorm_pipe_kernel(RowNormArgs a) {
       g[k][e + 3] = t.w;
     }
   auto load = [&](int64_t r, uint4 (&raw)[CH]) {
-    const char* x = (const char*)a.x + r * a.x_rs * XB;
+    const char* x = (const char*)a.x + src_row(a, r) * a.x_rs * XB;
 #pragma unroll
     for (int k = 0; k < CH; ++k) raw[k] = *(const uint4*)(x + ((int64_t)k * 64 + lane) * 16);
   };
@@ -203,8 +224,21 @@ __global__ void __launch_bounds__(256) rmsnorm_pipe_kernel(RowNormArgs a) {
   }
 }
 
+bool rmsnorm_gather_ok(const RowNormArgs& a) {
+  const int xb = a.x_dt == REW_DT_BFLOAT16 ? 2 : 4, yb = a.y_dt == REW_DT_BFLOAT16 ? 2 : 4;
+  const int epc = 16 / xb;
+  const int64_t chunks = (a.n + epc - 1) / epc;
+  const bool id_ok = a.ids_dt == REW_DT_INT32 || a.ids_dt == REW_DT_UINT32 ||
+                     a.ids_dt == REW_DT_INT64 || a.ids_dt == REW_DT_UINT64;
+  return id_ok && a.x_rows > 0 && a.n % epc == 0 && (a.x_rs * xb) % 16 == 0 &&
+         ((uintptr_t)a.x & 15) == 0 && ((uintptr_t)a.y & 15) == 0 &&
+         ((uintptr_t)a.xout & 15) == 0 && (a.n * yb) % 16 == 0 && chunks <= 64 * 16;
+}
+
 void launch_rmsnorm_rows(const RowNormArgs& a, hipStream_t stream) {
   if (a.rows == 0 || a.n == 0) return;
+  if (a.ids && !rmsnorm_gather_ok(a))
+    fail(REW_MI355X_ERR_INVALID, "internal: gather rmsNorm launch outside its limits");
   const int xb = a.x_dt == REW_DT_BFLOAT16 ? 2 : 4, yb = a.y_dt == REW_DT_BFLOAT16 ? 2 : 4;
   const int epc = 16 / xb;
   const int64_t chunks = (a.n + epc - 1) / epc;  // 16-byte chunks per row

@@ -350,8 +350,18 @@ struct RowNormArgs {
   float eps, divisor;
   void* y;            // dense [rows, n]
   int y_dt;           // bf16 or f32
+  // gather form (an embedding lookup feeding the norm): source row r is row
+  // ids[r] of x, clamped into [0, x_rows) like torchIndexSelect's gather,
+  // and every gathered row is also stored to xout (dense [rows, n], x's
+  // dtype); ids == nullptr: row r of x
+  const void* ids;
+  int ids_dt;
+  int64_t x_rows;
+  void* xout;
 };
 void launch_rmsnorm_rows(const RowNormArgs& a, hipStream_t stream);
+// Whether launch_rmsnorm_rows runs the gather form of `a` (16-byte rows).
+bool rmsnorm_gather_ok(const RowNormArgs& a);
 
 // softmax over rows of n contiguous f32 (x row stride x_rs elements):
 // m = max_j x, e_j = exp(x_j - m), s = sum_j e_j, y = e / s (dense f32).

@@ -282,6 +282,10 @@ struct Lower {
   std::unordered_map<Tensor*, std::vector<Node*>> cons;  // pending consumers
   std::unordered_map<Tensor*, GemmPlan> gemm_out;  // fused GEMM result -> plan
   std::unordered_map<Tensor*, NormPlan> norm_out;
+  // an embedding lookup (torchIndexSelect output, pending) read only
+  // through reshapes by a planned rmsNorm -> that norm's output: both are
+  // written by one launch at the lookup
+  std::unordered_map<Tensor*, Tensor*> gather_norm;
   std::unordered_map<Tensor*, RopePlan> rope_out;
   std::unordered_map<Tensor*, SoftmaxPlan> softmax_out;
   std::unordered_map<Tensor*, MoePlan> moe_out;
@@ -332,6 +336,7 @@ struct Lower {
   void emit_argmax(Node* n);
   void emit_topk(Node* n);
   void emit_sort(Node* n);
+  bool emit_gather_norm(Node* n, Tensor* t, const NormPlan& p);
   void emit_index_map(Node* n);
   // Materialize `t` (any kind) into a fresh dense tensor whose shape is the
   // permutation `perm` of t's shape.
@@ -2377,6 +2382,12 @@ void Lower::match_rows() {
         for (Tensor* t : inner) t->plan_mat = false;
         out->plan_mat = true;
         norm_out[out] = np;
+        {
+          Tensor* s = np.src;
+          while (s && !s->st && s->prod && s->prod->kind == K_RESHAPE) s = s->prod->in[0];
+          if (s && s != np.src && !s->st && s->prod && s->prod->kind == K_INDEX_SELECT)
+            gather_norm[s] = out;
+        }
         break;
       }
     }
@@ -2661,7 +2672,60 @@ bool Lower::emit_rope(Tensor* t, const RopePlan& p) {
   return true;
 }
 
+// The embedding lookup and the rmsNorm that reads it (LlamaDecoderLayer's
+// first norm over Embedding.forward's rows) in one pass: table rows by id
+// in, the rows and their norm out.
+bool Lower::emit_gather_norm(Node* n, Tensor* t, const NormPlan& p) {
+  Tensor *tab = n->in[0], *ix = n->in[1], *G = n->out[0];
+  if (t->st || n->i0 != 0 || n->i1 != 0 || tab->shape.rank != 2 || tab->dt != G->dt ||
+      G->dt != p.src->dt)
+    return false;
+  const int64_t nn = t->shape.d[t->shape.rank - 1];
+  if (tab->shape.d[1] != nn || G->numel() != ix->numel() * nn || t->numel() != G->numel())
+    return false;
+  RowNormArgs a;
+  std::memset(&a, 0, sizeof(a));
+  ensure_mat(tab);
+  ensure_mat(ix);
+  rows_view(tab, nn, &a.x, &a.x_rs);
+  a.x_dt = tab->dt;
+  a.n = nn;
+  a.rows = ix->numel();
+  a.ids = ix->data();
+  a.ids_dt = ix->dt;
+  a.x_rows = tab->shape.d[0];
+  ensure_mat(p.gamma);
+  a.gamma = (const float*)p.gamma->data();
+  a.eps = p.eps;
+  a.divisor = p.divisor;
+  a.y_dt = t->dt;
+  a.xout = a.y = reinterpret_cast<void*>(uintptr_t(256));  // allocator blocks are aligned
+  if (!rmsnorm_gather_ok(a)) return false;
+  tensor_alloc(G);
+  tensor_alloc(t);
+  a.xout = G->data();
+  a.y = t->data();
+  if (c->profiling)
+    prof_begin(c, "gather_rmsnorm{" + std::to_string(a.rows) + "x" + std::to_string(nn) + "}");
+  launch_rmsnorm_rows(a, c->stream);
+  prof_end(c);
+  note_launch(c, true);
+  return true;
+}
+
 void Lower::emit_gather(Node* n) {
+  {
+    auto gn = gather_norm.find(n->out[0]);
+    if (gn != gather_norm.end()) {
+      Tensor* t = gn->second;
+      gather_norm.erase(gn);
+      auto nit = norm_out.find(t);
+      if (nit != norm_out.end() && emit_gather_norm(n, t, nit->second)) {
+        norm_out.erase(nit);
+        return;
+      }
+    }
+  }
   Tensor *src = n->in[0], *ix = n->in[1], *out = n->out[0];
   ensure_mat(src);
   ensure_mat(ix);

@@ -389,3 +389,39 @@ def test_sibling_reductions_one_pass(gpu, oracle, shape, axes):
     np.testing.assert_allclose(got[0], y.astype(np.float64).sum(axis=tuple(axes)), rtol=1e-5)
     np.testing.assert_array_equal(got[1], y.max(axis=tuple(axes)))
     np.testing.assert_array_equal(got[2], y.min(axis=tuple(axes)))
+
+
+@pytest.mark.parametrize("ids_dt", [np.int32, np.int64])
+def test_embedding_lookup_rmsnorm_one_pass(gpu, oracle, ids_dt):
+    """LlamaDecoderLayer's first norm over Embedding.lookup's rows
+    (embedding.nim, norm.nim:204-224): the lookup and the norm run as one
+    launch that writes both the gathered rows (the layer's residual) and
+    their norm; ids out of range clamp like torchIndexSelect.  The rows equal
+    the op-by-op gather bit for bit, and the norm equals the row-norm
+    kernel's on the same rows already in memory bit for bit."""
+    V, H, T = 1000, 4096, 300
+    key = oracle.init_key(4242)
+    w = oracle.round_bf16(oracle.normal_f32(key, V * H).reshape(V, H))
+    g = oracle.normal_f32(oracle.fold_in(key, 1), H, 1.0, 0.1)
+    ids = (np.arange(T) * 7919 % V).astype(ids_dt)
+    ids[3], ids[7] = -5, V + 11
+    table, gamma = E.fromHost(w, DType.BFLOAT16), E.fromHost(g)
+
+    def fwd():
+        x = O.reshape(nn.Embedding(table).lookup(E.fromHost(ids)), [1, T, H])
+        normed = nn._to(nn.RMSNorm(gamma).forward(nn._f32(x)), DType.BFLOAT16)
+        return O.concat([normed, x], 0)   # x is needed again (the residual)
+
+    got, names = _run(fwd)
+    assert any(n.startswith("gather_rmsnorm") for n in names), names
+    assert not any(n.startswith("gather_rows") or n.startswith("rmsnorm_rows") for n in names), names
+    ref, _ = _run(fwd, op_by_op=True)
+    np.testing.assert_array_equal(got[1], ref[1])
+    rows = w[np.clip(ids.astype(np.int64), 0, V - 1)]
+    xt = E.fromHost(rows.reshape(1, T, H), DType.BFLOAT16)
+    plain, pn = _run(lambda: nn._to(nn.RMSNorm(gamma).forward(nn._f32(xt)), DType.BFLOAT16))
+    assert any(n.startswith("rmsnorm_rows") for n in pn), pn
+    np.testing.assert_array_equal(got[0], plain[0])
+    np.testing.assert_array_equal(E.bf16_bits_to_f32(got[1]).reshape(T, H), rows)
+    want = oracle.rmsnorm_rows(rows, g, 1e-5)
+    bf16_close(E.bf16_bits_to_f32(got[0]).reshape(T, H), want, 1e-2)
