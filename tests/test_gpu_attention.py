@@ -84,6 +84,9 @@ CASES = [  # B, H, Hkv, Sq, Sk, D
     (1, 16, 8, 130, 130, 128),  # head share an XCD (a permuted workgroup order)
     (1, 32, 8, 512, 512, 128),  # the Llama layer's heads: head_dim 128, group 4
     (2, 32, 8, 384, 384, 128),
+    (1, 2, 2, 512, 512, 64),    # MHA: the two groups take adjacent query tiles
+    (1, 6, 2, 384, 384, 128),   # odd group size, odd tile count: one idle group
+    (2, 4, 4, 256, 448, 64),
 ]
 
 
@@ -168,3 +171,60 @@ def test_flash_gqa_equals_mha_with_repeated_kv(gpu, oracle):
     o2 = nn.scaledDotProductAttention(qt, E.fromHost(kr, DType.BFLOAT16),
                                       E.fromHost(vr, DType.BFLOAT16), causal=True)
     np.testing.assert_array_equal(E.toHost(o1), E.toHost(o2))
+
+
+PP_CHILD = r"""
+import sys
+import numpy as np
+sys.path.insert(0, sys.argv[1])
+from rew_amd import eager as E, nn, ops as O
+from rew_amd.eager import DType
+E.installEagerBackend(E.mi355x(0))
+rs = np.random.default_rng(11)
+out = []
+for B, H, Hkv, S, D, causal in [(1, 8, 2, 384, 128, True), (1, 8, 2, 256, 64, False),
+                                (1, 3, 3, 320, 128, True), (2, 6, 2, 192, 64, True)]:
+    def mk(h):
+        x = rs.standard_normal((B, h, S, D)).astype(np.float32)
+        return E.fromHost(E.f32_to_bf16_bits(x), DType.BFLOAT16)
+    q, k, v = mk(H), mk(Hkv), mk(Hkv)
+    g = H // Hkv
+    ex = lambda t: O.reshape(O.broadcastTo(O.reshape(t, [B, Hkv, 1, S, D]), [B, Hkv, g, S, D],
+                                           [0, 1, 2, 3, 4]), [B, H, S, D])
+    E.profileBegin()
+    o = nn.scaledDotProductAttention(q, ex(k), ex(v), causal=causal)
+    bits = E.toHost(o)
+    names = [n for n, _, _ in E.profileEnd() if n.startswith("flash_attn")]
+    out.append((names, bits.tobytes().hex()))
+import json
+print(json.dumps(out))
+"""
+
+
+def test_pingpong_equals_single_group_kernel(gpu):
+    """The two-group ping-pong kernel and the single-group kernel run the
+    same per-tile arithmetic in the same key order (extra tiles the union
+    range adds are masked everywhere and add exact zeros), so their outputs
+    agree bit for bit: GQA head pairs, MHA query-tile pairs, an odd head
+    group, causal and unmasked."""
+    import json
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = str(Path(__file__).resolve().parents[1])
+
+    def run(env):
+        r = subprocess.run([sys.executable, "-c", PP_CHILD, root], env=env, capture_output=True,
+                           text=True, timeout=300)
+        assert r.returncode == 0, r.stderr[-3000:]
+        return json.loads(r.stdout.strip().splitlines()[-1])
+
+    base = dict(os.environ)
+    base.pop("REW_MI355X_FLASH", None)
+    pp = run(base)
+    single = run(dict(base, REW_MI355X_FLASH="single"))
+    for (n_pp, b_pp), (n_1, b_1) in zip(pp, single):
+        assert n_pp and all(n.startswith("flash_attn_pp[") for n in n_pp), n_pp
+        assert n_1 and not any(n.startswith("flash_attn_pp") for n in n_1), n_1
+        assert b_pp == b_1

@@ -158,7 +158,7 @@ def test_llama_layer_full_dims(gpu, oracle):
     assert any(n.startswith("gemm_lds_swiglu") for n in names), names
     assert sum(n.startswith("gemm_lds_nn+bias+res") for n in names) == 2, names
     assert any(n.startswith("gemm_lds_nn{") and n.count("+rope") == 2 for n in names), names
-    assert any(n.startswith("flash_attn[1,32,8,2048,2048,128") for n in names), names
+    assert any(n.startswith("flash_attn_pp[1,32,8,2048,2048,128") for n in names), names
     c, s = nn.rope_tables(hd, S, 500000.0)
     want = oracle.llama_layer(x, p, nh, nkv, c, s, 1e-5, True, True, "rms")
     err = bf16_err(got, want)
