@@ -210,11 +210,11 @@ __device__ __forceinline__ float fa_round_max(f32x16_t (&sacc)[2]) {
 enum { FA_PLAIN = 0, FA_DIAG_UP = 1, FA_GENERAL = 2, FA_DIAG_DOWN = 3 };
 template <int DT, int KIND>
 __device__ __forceinline__ void fa_softmax_tile(const FlashArgs& a, int k0, int qi, int g,
-                                                float sl2, const f32x16_t (&sacc_in)[2],
-                                                float mr, uint32_t (&pk)[2][8],
-                                                f32x16_t (&o)[DT], float& m_run, float& l_run) {
+                                                float sl2, f32x16_t (&sacc_in)[2],
+                                                float mr, uint32_t (&pk)[2][8], float& m_run,
+                                                float& l_run, float& alpha_out) {
   using namespace fa;
-  f32x16_t t[2];  // non-plain kinds: the scores in log2 units
+  f32x16_t(&t)[2] = sacc_in;  // non-plain kinds: the scores in log2 units, in place
   float mt;
   if constexpr (KIND == FA_PLAIN) {
     mt = mr * sl2;
@@ -291,7 +291,14 @@ __device__ __forceinline__ void fa_softmax_tile(const FlashArgs& a, int k0, int 
         pk[kb][e >> 1] = cvt_bf16x2(fa_exp2(t[kb][e] - m_use), fa_exp2(t[kb][e + 1] - m_use));
     }
   l_run = __fmul_rn(l_run, alpha);  // the caller adds this tile's fa_row_sum
-  if (rescale) {
+  alpha_out = alpha;                // and rescales O when it is not 1
+}
+
+// O *= alpha when the softmax step moved the running max (alpha is 1 on
+// every other tile, the same for the whole wave).
+template <int DT>
+__device__ __forceinline__ void fa_rescale(f32x16_t (&o)[DT], float alpha) {
+  if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -316,20 +323,22 @@ __device__ __forceinline__ float fa_row_sum(const uint32_t (&pk)[2][8]) {
   return __fadd_rn(__fadd_rn(ps[0], ps[1]), __fadd_rn(ps[2], ps[3]));
 }
 
-// The softmax step of the tile's kind (fa_kind).
+// The softmax step of the tile's kind (fa_kind), then the rescale of O.
 template <int DT>
 __device__ __forceinline__ void fa_softmax_any(int kind, const FlashArgs& a, int k0, int qi,
-                                               int g, float sl2, const f32x16_t (&sacc)[2],
+                                               int g, float sl2, f32x16_t (&sacc)[2],
                                                float mr, uint32_t (&pk)[2][8], f32x16_t (&o)[DT],
                                                float& m_run, float& l_run) {
+  float alpha;
   if (kind == FA_PLAIN)
-    fa_softmax_tile<DT, FA_PLAIN>(a, k0, qi, g, sl2, sacc, mr, pk, o, m_run, l_run);
+    fa_softmax_tile<DT, FA_PLAIN>(a, k0, qi, g, sl2, sacc, mr, pk, m_run, l_run, alpha);
   else if (kind == FA_DIAG_UP)
-    fa_softmax_tile<DT, FA_DIAG_UP>(a, k0, qi, g, sl2, sacc, mr, pk, o, m_run, l_run);
+    fa_softmax_tile<DT, FA_DIAG_UP>(a, k0, qi, g, sl2, sacc, mr, pk, m_run, l_run, alpha);
   else if (kind == FA_DIAG_DOWN)
-    fa_softmax_tile<DT, FA_DIAG_DOWN>(a, k0, qi, g, sl2, sacc, mr, pk, o, m_run, l_run);
+    fa_softmax_tile<DT, FA_DIAG_DOWN>(a, k0, qi, g, sl2, sacc, mr, pk, m_run, l_run, alpha);
   else
-    fa_softmax_tile<DT, FA_GENERAL>(a, k0, qi, g, sl2, sacc, mr, pk, o, m_run, l_run);
+    fa_softmax_tile<DT, FA_GENERAL>(a, k0, qi, g, sl2, sacc, mr, pk, m_run, l_run, alpha);
+  fa_rescale<DT>(o, alpha);
 }
 
 // Workgroup barrier without the memory fence of __syncthreads (which would
@@ -921,6 +930,7 @@ __global__ void __launch_bounds__(512, 1) flash_pp_kernel(FlashArgs a) {
   }
 }
 
+
 bool flash_supported(const FlashArgs& a) {
   if (a.D != 32 && a.D != 64 && a.D != 128) return false;
   if (a.B <= 0 || a.H <= 0 || a.Hkv <= 0 || a.H % a.Hkv) return false;
@@ -947,14 +957,17 @@ static void launch_flash_d(const FlashArgs& a, bool buf, unsigned grid, hipStrea
   else launch_flash_db<D, false>(a, grid, stream);
 }
 
-// The ping-pong kernel runs head dims 64 and 128 when every key tile is
-// whole and every K / V byte offset fits the buffer descriptors' 31 bits;
-// REW_MI355X_FLASH=single forces the single-group kernel (tests compare the
-// two).
-static bool flash_single_forced() {
-  static const bool v = [] {
+// Kernel choice for head dims 64 and 128 when every key tile is whole and
+// every K / V byte offset fits the buffer descriptors' 31 bits; other
+// shapes run the single-group kernel.  REW_MI355X_FLASH = single or pp
+// forces one (tests compare them).
+enum { FA_K_SINGLE = 0, FA_K_PP = 1 };
+static int flash_forced() {
+  static const int v = [] {
     const char* s = std::getenv("REW_MI355X_FLASH");
-    return s && std::string(s) == "single";
+    if (!s) return -1;
+    const std::string t(s);
+    return t == "single" ? FA_K_SINGLE : t == "pp" ? FA_K_PP : -1;
   }();
   return v;
 }
@@ -964,13 +977,23 @@ static bool flash_buf_ok(const FlashArgs& a) {
          ((int64_t)a.Sk * a.v_ss + a.D) * 2 < (1ll << 31);
 }
 
-bool flash_pingpong(const FlashArgs& a) {
-  return (a.D == 64 || a.D == 128) && flash_buf_ok(a) && !flash_single_forced();
+static int flash_kernel_kind(const FlashArgs& a) {
+  if (!((a.D == 64 || a.D == 128) && flash_buf_ok(a))) return FA_K_SINGLE;
+  const int f = flash_forced();
+  return f >= 0 ? f : FA_K_PP;
+}
+
+const char* flash_variant(const FlashArgs& a) {
+  switch (flash_kernel_kind(a)) {
+    case FA_K_PP: return "flash_attn_pp";
+    default: return "flash_attn";
+  }
 }
 
 void launch_flash(const FlashArgs& a, hipStream_t stream) {
   const int nqt = (a.Sq + fa::BQ - 1) / fa::BQ;
-  if (flash_pingpong(a)) {
+  const int kind = flash_kernel_kind(a);
+  if (kind == FA_K_PP) {
     const bool pair = ((a.H / a.Hkv) & 1) == 0;
     const unsigned grid =
         pair ? (unsigned)(nqt * a.B * (a.H / 2)) : (unsigned)(((nqt + 1) / 2) * a.B * a.H);

@@ -338,8 +338,8 @@ struct FlashArgs {
   int heavy_last;    // the last query tiles carry the most keys
 };
 bool flash_supported(const FlashArgs& a);
-// Whether launch_flash runs the two-group ping-pong kernel for `a`.
-bool flash_pingpong(const FlashArgs& a);
+// Profile name of the kernel launch_flash runs for `a`.
+const char* flash_variant(const FlashArgs& a);
 
 // ---- row composites (k_rows.hip) ----------------------------------------------
 // rmsNorm over rows of n contiguous elements (x row stride x_rs elements):

@@ -1637,7 +1637,7 @@ bool Lower::emit_flash(Node* pv, const FlashPlan& fp) {
   if (c->profiling) {
     char nm[160];
     std::snprintf(nm, sizeof nm, "%s[%d,%d,%d,%d,%d,%d,%d,%d]",
-                  flash_pingpong(a) ? "flash_attn_pp" : "flash_attn", a.B, a.H, a.Hkv, a.Sq,
+                  flash_variant(a), a.B, a.H, a.Hkv, a.Sq,
                   a.Sk, a.D, a.mask ? a.cmp : -1, a.skip);
     prof_begin(c, nm);
   }
