@@ -111,6 +111,24 @@ __device__ __forceinline__ void block_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// x * logistic(x) for every bf16 x, as rew's SiLU op sequence computes it
+// in fp32 (silu = mul(x, divide(1, add(1, exp(neg(x))))),
+// src/rew/nn/activation.nim:28-38): the SwiGLU epilogue's gate takes a
+// bf16-rounded input, so it looks the product up instead of running the
+// library expf and an IEEE division per output (about 30 VALU
+// instructions).  Filled on each device by init_silu_table with the same
+// device code as the op-by-op path, so the bits are identical.
+__device__ float g_silu_bf16[65536];
+
+__global__ void __launch_bounds__(256) silu_table_kernel() {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  const float x = vm::as_f(i << 16);
+  const float e = expf(-x);
+  const float den = 1.0f + e;
+  const float sig = 1.0f / den;
+  g_silu_bf16[i] = x * sig;
+}
+
 template <int V>
 struct IntK {
   static constexpr int value = V;
@@ -641,6 +659,11 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
     // would stream tens of KB of straight-line code through the I-cache)
 #pragma unroll 1
     for (int p0 = 0; p0 < PASSES; p0 += U) {
+      // all U rows' table lookups are requested before any store (a store
+      // under the row predicate is a branch, and the compiler waits for
+      // every load in flight at it)
+      float act[U][8];
+      uint32_t up[U][4];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int row = row_of(p0 + u);
@@ -648,19 +671,25 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
         const uint4 uv = c_chunk(row, lc + 64);
         const uint16_t* dh = (const uint16_t*)&dv;
         const uint16_t* uh = (const uint16_t*)&uv;
-        uint16_t out[8];
 #pragma unroll
-        for (int x = 0; x < 8; ++x) {
+        for (int x = 0; x < 8; x += 2) {
           // GatedFeedForward's gate, op by op in fp32 (gated_ffn.nim:46-67,
-          // activation.nim:28-38)
-          const float yg = vm::round_bf16(bf(dh[x]) + bf(bh[x]));
-          const float yu = vm::round_bf16(bf(uh[x]) + bf(buh[x]));
-          const float e = expf(-yg);
-          const float den = 1.0f + e;
-          const float sig = 1.0f / den;
-          const float act = yg * sig;
-          out[x] = vm::bf16_bits(act * yu);
+          // activation.nim:28-38): g and u rounded to bf16 two at a time,
+          // g * logistic(g) from the table by g's bits
+          const uint32_t pg = vm::bf16x2_bits(bf(dh[x]) + bf(bh[x]), bf(dh[x + 1]) + bf(bh[x + 1]));
+          up[u][x >> 1] = vm::bf16x2_bits(bf(uh[x]) + bf(buh[x]), bf(uh[x + 1]) + bf(buh[x + 1]));
+          act[u][x] = g_silu_bf16[pg & 0xffffu];
+          act[u][x + 1] = g_silu_bf16[pg >> 16];
         }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int row = row_of(p0 + u);
+        uint32_t out[4];
+#pragma unroll
+        for (int x = 0; x < 8; x += 2)
+          out[x >> 1] = vm::bf16x2_bits(act[u][x] * vm::as_f(up[u][x >> 1] << 16),
+                                        act[u][x + 1] * vm::as_f(up[u][x >> 1] & 0xffff0000u));
         if (row_ok(row)) *(uint4*)(C + (row0 + row) * c_sm + n) = *(const uint4*)out;
       }
     }
@@ -878,6 +907,11 @@ static void launch_segs(const GemmSegs& gs, const GroupArgs* ga, bool bkc, bool 
     else REW_LDS_LAUNCH(false, false, false);
   }
 #undef REW_LDS_LAUNCH
+  REW_HIP(hipGetLastError());
+}
+
+void init_silu_table(hipStream_t stream) {
+  hipLaunchKernelGGL(silu_table_kernel, dim3(256), dim3(256), 0, stream);
   REW_HIP(hipGetLastError());
 }
 

@@ -338,6 +338,9 @@ struct FlashArgs {
   int heavy_last;    // the last query tiles carry the most keys
 };
 bool flash_supported(const FlashArgs& a);
+// Fills the SwiGLU epilogue's table of x * logistic(x) over all bf16 x on
+// the current device (once per context, before any GEMM).
+void init_silu_table(hipStream_t stream);
 // Profile name of the kernel launch_flash runs for `a`.
 const char* flash_variant(const FlashArgs& a);
 

@@ -321,6 +321,8 @@ int rew_mi355x_init(int ordinal, rew_mi355x_ctx** out) {
       c->compiled_base = jit_programs_compiled();
       c->loaded_base = jit_programs_loaded();
       REW_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+      init_silu_table(c->stream);
+      REW_HIP(hipStreamSynchronize(c->stream));
       // once per device, with the device current
       c->noalloc_scratch = noalloc_scratch_lookup(&c->noalloc_error);
       if (const char* s = std::getenv("REW_MI355X_EAGER_SYNC"))
