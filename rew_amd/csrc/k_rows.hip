@@ -128,6 +128,9 @@ __device__ __forceinline__ void rms_row(const RowNormArgs& a, int64_t row, int l
   for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
   const float mean = ss / a.divisor;
   const float r = sqrtf(mean + a.eps);
+  // x / r as x * (1 / r) (within an ulp of the quotient; the row's sum of
+  // squares already runs in another order than the op sequence's reduction)
+  const float rinv = 1.0f / r;
   char* y = (char*)a.y + row * a.n * YB;
 #pragma unroll
   for (int k = 0; k < CH; ++k) {
@@ -139,14 +142,13 @@ __device__ __forceinline__ void rms_row(const RowNormArgs& a, int64_t row, int l
     for (int e = 0; e < EPC_X; ++e) {
       const float v = XB == 2 ? as_f((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16))
                               : as_f(w[e]);
-      const float nv = v / r;
+      const float nv = v * rinv;
       out[e] = gam(k, e) * nv;
     }
     if (YB == 2) {
       uint32_t o[EPC_X / 2];
 #pragma unroll
-      for (int e = 0; e < EPC_X; e += 2)
-        o[e / 2] = (uint32_t)bf16_bits(out[e]) | ((uint32_t)bf16_bits(out[e + 1]) << 16);
+      for (int e = 0; e < EPC_X; e += 2) o[e / 2] = bf16x2_bits(out[e], out[e + 1]);
       if (EPC_X == 8) *(uint4*)(y + j * 2) = *(const uint4*)o;
       else *(uint2*)(y + j * 2) = *(const uint2*)o;
     } else {

@@ -342,6 +342,24 @@ def test_softmax_row_kernel(gpu, oracle, shape):
     np.testing.assert_allclose(got[ok], want[ok], rtol=1e-5, atol=1e-9)
 
 
+@pytest.mark.parametrize("n", [1024, 4096])
+def test_softmax_wide_range_rows(gpu, oracle, n):
+    """Rows scaled from 1 to 40 (spreads max - min from about 8 to 300, so
+    probabilities from 1 down to the subnormal range): the row kernel's
+    quotients equal the op-by-op ones bit for bit over 4-16 M values."""
+    rows = 4096
+    x = oracle.normal_f32(oracle.init_key(950 + n), rows * n).reshape(rows, n)
+    x *= np.linspace(1.0, 40.0, rows, dtype=np.float32)[:, None]
+
+    def fn():
+        return nn.softmax(E.fromHost(x), 1)
+
+    got, names = _run(fn)
+    assert any(k.startswith("softmax_rows") for k in names), names
+    ref, _ = _run(fn, op_by_op=True)
+    np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
 def test_repeated_reduction_runs_once(gpu, oracle):
     """reduceMean(y) is reduceSum(y) / n (src/rew/ops/reduce.nim): next to a
     reduceSum of the same tensor the sum is computed once and shared."""
