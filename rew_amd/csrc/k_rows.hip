@@ -392,14 +392,13 @@ __global__ void __launch_bounds__(256) softmax_wave_kernel(SoftmaxArgs a) {
   }
 }
 
-// Rows shorter than 128: the compiled reduction runs a thread per row over
-// j = 0, 1, ... in order; so does this kernel.
 // Rows shorter than 128: a workgroup stages R rows in LDS with coalesced
 // loads (row pitch n + 1 against bank conflicts), one thread runs each row's
 // three sequential passes -- max, sum of expf(x - m), expf(x - m) / sum --
 // in the order of the compiled reductions over short rows, so the result
 // equals rew's five-op sequence bit for bit, and the results leave through
-// LDS as coalesced stores.  R = 256 rows for n <= 62 (64 KiB), else 128.
+// LDS as coalesced stores.  Each exp(x - m) is computed once and kept in
+// LDS for the division.
 template <int R>
 __global__ void __launch_bounds__(256) softmax_tile_kernel(SoftmaxArgs a) {
   extern __shared__ float tile[];
@@ -424,8 +423,12 @@ __global__ void __launch_bounds__(256) softmax_tile_kernel(SoftmaxArgs a) {
       float m = -INFINITY;
       for (int j = 0; j < n; ++j) m = fmax_prop(m, t[j]);
       float sum = 0.0f;
-      for (int j = 0; j < n; ++j) sum = sum + expf(t[j] - m);
-      for (int j = 0; j < n; ++j) t[j] = expf(t[j] - m) / sum;
+      for (int j = 0; j < n; ++j) {
+        const float e = expf(t[j] - m);
+        t[j] = e;
+        sum = sum + e;
+      }
+      for (int j = 0; j < n; ++j) t[j] = t[j] / sum;
     }
     __syncthreads();
     row = threadIdx.x / n;
@@ -454,17 +457,11 @@ bool softmax_rows_ok(const SoftmaxArgs& a) {
 void launch_softmax_rows(const SoftmaxArgs& a, hipStream_t stream) {
   if (!softmax_rows_ok(a)) fail(REW_MI355X_ERR_INVALID, "internal: softmax rows not launchable");
   if (a.n < 128) {
-    if (a.n <= 62) {
-      const int64_t blocks = (a.rows + 255) / 256;
-      hipLaunchKernelGGL(softmax_tile_kernel<256>,
-                         dim3((unsigned)(blocks < 65536 ? blocks : 65536)), dim3(256),
-                         (size_t)256 * (a.n + 1) * 4, stream, a);
-    } else {
-      const int64_t blocks = (a.rows + 127) / 128;
-      hipLaunchKernelGGL(softmax_tile_kernel<128>,
-                         dim3((unsigned)(blocks < 65536 ? blocks : 65536)), dim3(256),
-                         (size_t)128 * (a.n + 1) * 4, stream, a);
-    }
+    // 32 rows per workgroup: a thread runs each row's passes serially, so
+    // the rows spread over as many CUs as there are workgroups
+    const int64_t blocks = (a.rows + 31) / 32;
+    hipLaunchKernelGGL(softmax_tile_kernel<32>, dim3((unsigned)(blocks < 65536 ? blocks : 65536)),
+                       dim3(256), (size_t)32 * (a.n + 1) * 4, stream, a);
   } else {
     // Rows of exactly 1024, 2048 or 4096 use the pipelined unguarded
     // kernels: at most 2048 waves (two workgroups per CU), each walking
