@@ -116,8 +116,10 @@ def timed_run(step, steps, warmup):
     2. the timed pass: wall clock and HIP events at its two ends only; it
        gives `value` and ms_per_step.
 
-    Returns (wall_s, device_ms, first_ms, profile entries); wall and device
-    time are the timed pass's."""
+    Returns (wall_s, device_ms, first_ms, profile entries, host counters);
+    wall and device time are the timed pass's.  The host counters are the
+    timed pass's flush host time per step (lowering or replay of a recorded
+    plan, plus enqueueing) and how many of its flushes replayed a plan."""
     t0 = time.perf_counter()
     y = step()
     E.sync()
@@ -148,12 +150,20 @@ def timed_run(step, steps, warmup):
         return wall, ev.elapsed_ms(e0, e1), prof
 
     pwall, _, prof = run(True)
+    s0 = E.stats()
     wall, dev_ms, _ = run(False)
+    s1 = E.stats()
+    hostc = {"flush_host_us_per_step": round((s1["flush_host_ns"] - s0["flush_host_ns"]) / 1e3 /
+                                             steps, 1),
+             "flushes": s1["flushes"] - s0["flushes"],
+             "flush_plan_hits": s1["flush_plan_hits"] - s0["flush_plan_hits"]}
     for name, n, ms in sorted(prof, key=lambda r: -r[2]):
         print(f"#   {ms * 1e3 / steps:9.1f} us/step  x{n // steps:<3d} {name}", file=sys.stderr)
     print(f"#   timed pass {wall * 1e3 / steps:.3f} ms/step, profiled pass "
-          f"{pwall * 1e3 / steps:.3f} ms/step", file=sys.stderr)
-    return wall, dev_ms, first_ms, prof
+          f"{pwall * 1e3 / steps:.3f} ms/step; flush host time "
+          f"{hostc['flush_host_us_per_step']} us/step, {hostc['flush_plan_hits']} of "
+          f"{hostc['flushes']} flushes replayed a recorded plan", file=sys.stderr)
+    return wall, dev_ms, first_ms, prof, hostc
 
 
 def by_symbol(prof, work_of):
@@ -329,7 +339,7 @@ def run_llama(args):
         E.flush()
         return y
 
-    wall, dev_ms, first_ms, prof = timed_run(step, args.steps, args.warmup)
+    wall, dev_ms, first_ms, prof, hostc = timed_run(step, args.steps, args.warmup)
     ms_per_step = wall * 1e3 / args.steps
     flops = llama_layer_flops(B, S, H, cfg["heads"], cfg["kv_heads"], cfg["head_dim"],
                               cfg["intermediate"])
@@ -350,6 +360,7 @@ def run_llama(args):
                        "device_ms_per_step": round(dev_ms / args.steps, 3),
                        "kernel_ms_per_step": round(kernel_ms, 3),
                        "first_call_ms": round(first_ms, 1),
+                       "host": hostc,
                        "kernels": breakdown(syms, args.steps)[:12]}}
     emit(args, "llama_layer_prefill_tokens_per_s", B * S * args.steps / wall, "tokens/s",
          ms_per_step, "bf16", config, roof, cpu, extra)
@@ -374,7 +385,7 @@ def run_swiglu(args):
         E.flush()
         return y
 
-    wall, dev_ms, first_ms, prof = timed_run(step, args.steps, args.warmup)
+    wall, dev_ms, first_ms, prof, hostc = timed_run(step, args.steps, args.warmup)
     ms = wall * 1e3 / args.steps
     flops = 2 * T * H * I * 3
     syms = by_symbol(prof, entry_flops)
@@ -421,7 +432,7 @@ def run_chain(args):
         E.flush()
         return outs
 
-    wall, dev_ms, first_ms, prof = timed_run(step, args.steps, args.warmup)
+    wall, dev_ms, first_ms, prof, hostc = timed_run(step, args.steps, args.warmup)
     ms = wall * 1e3 / args.steps
 
     def bytes_of(name):
@@ -474,7 +485,7 @@ def run_copy(args):
         E.flush()
         return y
 
-    wall, dev_ms, first_ms, prof = timed_run(step, args.steps, args.warmup)
+    wall, dev_ms, first_ms, prof, hostc = timed_run(step, args.steps, args.warmup)
     ms = wall * 1e3 / args.steps
     syms = by_symbol(prof, lambda name: 2 * n * 4)
     roof = roofline("copy", syms, "hbm")
@@ -547,7 +558,7 @@ def run_moe(args):
             E.flush()
             return y
 
-    wall, dev_ms, first_ms, prof = timed_run(step, args.steps, args.warmup)
+    wall, dev_ms, first_ms, prof, hostc = timed_run(step, args.steps, args.warmup)
     ms = wall * 1e3 / args.steps
     flops = moe_flops(T, H, I, E_, S, k)
     syms = by_symbol(prof, entry_flops)
@@ -572,6 +583,7 @@ def run_moe(args):
          {"workload": "deepseek_moe_layer_bf16", "tokens": T, "hidden": H, "intermediate": I,
           "routed_experts": E_, "shared_experts": S, "top_k": k, "path": args.moe_path},
          roof, cpu, {"kernels": breakdown(syms, args.steps), "first_call_ms": round(first_ms, 1),
+                     "host": hostc,
                      "algorithmic_tflop": round(flops / 1e12, 4),
                      "achieved_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
                      "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)})
@@ -610,7 +622,7 @@ def run_mnist(args):
             E.flush()
             return ids
 
-    wall, dev_ms, first_ms, prof = timed_run(step, args.steps, args.warmup)
+    wall, dev_ms, first_ms, prof, hostc = timed_run(step, args.steps, args.warmup)
     ms = wall * 1e3 / args.steps
     flops = 2 * B * D * Hd + 2 * B * Hd * C
 
@@ -645,6 +657,7 @@ def run_mnist(args):
          {"workload": "mnist_mlp_inference_f32", "batch": B, "layers": [D, Hd, C],
           "path": args.mnist_path},
          roof, cpu, {"kernels": breakdown(syms, args.steps), "first_call_ms": round(first_ms, 2),
+                     "host": hostc,
                      "us_per_forward": round(ms * 1e3, 1), "algorithmic_flops": flops,
                      "device_us_per_forward": round(dev_ms * 1e3 / args.steps, 1)})
 

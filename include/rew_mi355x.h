@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define REW_MI355X_ABI_VERSION 2
+#define REW_MI355X_ABI_VERSION 3
 
 /* Status codes. */
 enum {
@@ -200,8 +200,10 @@ int rew_mi355x_sync(rew_mi355x_ctx* ctx);
  * flushes first. */
 int rew_mi355x_set_mode(rew_mi355x_ctx* ctx, int mode);
 
-/* Drop the cached small device constants (see rew_mi355x_from_host); the
- * programs compiled at run time and the caching allocator are kept.
+/* Drop the cached small device constants (see rew_mi355x_from_host) and the
+ * recorded flush plans (a flushed graph's launches, replayed when the same
+ * graph is flushed again); the programs compiled at run time and the
+ * caching allocator are kept.
  * Replaces: clearEagerCache (src/rew/eager.nim:1713-1715). */
 int rew_mi355x_clear_cache(rew_mi355x_ctx* ctx);
 
@@ -225,6 +227,11 @@ typedef struct rew_mi355x_stats {
   int64_t programs_compiled;   /* fused programs compiled at run time, and  */
   int64_t programs_loaded;     /* those loaded from the persistent cache    */
                                /* (REW_CACHE_DIR; process-wide since reset) */
+  int64_t flush_plan_hits;     /* flushes whose graph matched a recorded    */
+                               /* lowering and replayed it (no pattern      */
+                               /* matching or program building)             */
+  int64_t flush_host_ns;       /* host time spent inside flushes: lowering  */
+                               /* or replay, plus enqueueing the launches   */
 } rew_mi355x_stats;
 
 int rew_mi355x_get_stats(rew_mi355x_ctx* ctx, rew_mi355x_stats* out);

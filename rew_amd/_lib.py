@@ -118,7 +118,8 @@ class Stats(C.Structure):
     _fields_ = [(n, C.c_int64) for n in (
         "ops_recorded", "kernels_launched", "flushes", "fused_groups",
         "bytes_in_use", "bytes_cached", "plan_cache_hits", "jit_module_compiles",
-        "jit_module_hits", "programs_compiled", "programs_loaded")]
+        "jit_module_hits", "programs_compiled", "programs_loaded", "flush_plan_hits",
+        "flush_host_ns")]
 
 
 _lib = None

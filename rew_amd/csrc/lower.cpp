@@ -13,7 +13,10 @@
 //    (~26 reshape/slice/mul/concat ops) or a bias-add + SiLU + gate product
 //    become a single HBM pass.  Reductions take their input expression as a
 //    prologue.  dot_general folds transposes into GEMM strides.
+// A graph whose signature was flushed before skips 2 and 3: the launches
+// recorded then are replayed over this flush's buffers (plan.cpp).
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <functional>
@@ -21,6 +24,7 @@
 #include <tuple>
 
 #include "kernels.h"
+#include "plan.h"
 #include "runtime.h"
 
 namespace rew {
@@ -878,11 +882,6 @@ static void alloc_regs(Program& P, const std::vector<int>& live_out,
 // emission
 // ---------------------------------------------------------------------------
 
-static void note_launch(Ctx* c, bool fused) {
-  c->stats.kernels_launched++;
-  if (fused) c->stats.fused_groups++;
-}
-
 void Lower::ensure_mat(Tensor* t) {
   if (t->st) return;
   auto git = gemm_out.find(t);
@@ -996,12 +995,12 @@ void Lower::emit_ew_root(Tensor* t) {
                        ((uintptr_t)t->data() % (dt_size(t->dt) * kVec)) == 0 &&
                        (t->dt == kF32 || t->dt == kI32 || t->dt == kU32 || t->dt == kBF16);
       set_leaf_modes(g.P, S, vec);
+      Launch L{EwL{g.P, S, vec}};
       if (c->profiling)
-        prof_begin(c, "ew_fused{" + std::to_string(S.numel) + "x" + std::to_string(g.P.n_ins) +
-                          "," + dt_name(t->dt) + "," + (t->prod ? t->prod->name : "?") + "}");
-      launch_ew(g.P, S, vec, c->stream);
-      prof_end(c);
-      note_launch(c, g.P.n_ins > 2);
+        L.name = "ew_fused{" + std::to_string(S.numel) + "x" + std::to_string(g.P.n_ins) +
+                 "," + dt_name(t->dt) + "," + (t->prod ? t->prod->name : "?") + "}";
+      L.fused = g.P.n_ins > 2;
+      run_launch(c, std::move(L));
       return;
     } catch (GenFail&) {
       tensor_drop_storage(t);
@@ -1117,14 +1116,13 @@ void Lower::emit_reduce(Node* n) {
       const bool vec = n_red > 0 && (dims.back() % kVec) == 0 &&
                        (n_red % kVec) == 0 && space.d[X.rank - 1] != 1;
       set_leaf_modes(g.P, S, vec);
+      Launch L{ReduceL{g.P, S, A, vec}};
       if (c->profiling)
-        prof_begin(c, "reduce{" + std::to_string(n_out) + "x" + std::to_string(n_red) + "x" +
-                          std::to_string(g.P.n_ins) +
-                          (sib.empty() ? "" : "," + std::to_string(1 + sib.size()) + "ops") +
-                          "}");
-      launch_reduce(g.P, S, A, vec, c->stream);
-      prof_end(c);
-      note_launch(c, g.P.n_ins > 1 || !sib.empty());
+        L.name = "reduce{" + std::to_string(n_out) + "x" + std::to_string(n_red) + "x" +
+                 std::to_string(g.P.n_ins) +
+                 (sib.empty() ? "" : "," + std::to_string(1 + sib.size()) + "ops") + "}";
+      L.fused = g.P.n_ins > 1 || !sib.empty();
+      run_launch(c, std::move(L));
       reduce_done[key] = out;
       for (Node* m : sib) reduce_done[std::make_tuple(x, m->sub, m->l0, out->dt)] = m->out[0];
       return;
@@ -1193,10 +1191,9 @@ Tensor* Lower::emit_permuted_copy(Tensor* t, const std::vector<int>& perm) {
   const bool vec = (dims.back() % kVec) == 0 &&
                    (out->dt == kF32 || out->dt == kI32 || out->dt == kBF16);
   set_leaf_modes(g.P, S, vec);
-  prof_begin(c, "ew_copy");
-  launch_ew(g.P, S, vec, c->stream);
-  prof_end(c);
-  note_launch(c, false);
+  Launch L{EwL{g.P, S, vec}};
+  if (c->profiling) L.name = "ew_copy";
+  run_launch(c, std::move(L));
   return out;
 }
 
@@ -1325,18 +1322,17 @@ void Lower::emit_dot(Node* n) {
   g.c_sm = g.N;
   if (g.K == 0) {
     // empty contraction: zeros
-    REW_HIP(hipMemsetAsync(out->data(), 0, out->nbytes(), c->stream));
+    run_launch(c, Launch{FillL{out->data(), nullptr, (size_t)out->nbytes()}});
   } else {
+    Launch L{GemmL{{g}, false}};
     if (c->profiling) {
       // "<variant>[batch,M,N,K]": the shape fixes the algorithmic FLOPs
       char nm[160];
       std::snprintf(nm, sizeof nm, "%s[%lld,%lld,%lld,%lld]", gemm_variant(g),
                     (long long)g.batch, (long long)g.M, (long long)g.N, (long long)g.K);
-      prof_begin(c, nm);
+      L.name = nm;
     }
-    launch_gemm(g, c->stream);
-    prof_end(c);
-    note_launch(c, false);
+    run_launch(c, std::move(L));
   }
   // canonical copies made for this GEMM die with it (stream-ordered free)
   for (Tensor* t : {ta, tb})
@@ -1634,16 +1630,16 @@ bool Lower::emit_flash(Node* pv, const FlashPlan& fp) {
     tensor_drop_storage(out);
     return false;
   }
+  Launch L{a};
   if (c->profiling) {
     char nm[160];
     std::snprintf(nm, sizeof nm, "%s[%d,%d,%d,%d,%d,%d,%d,%d]",
                   flash_variant(a), a.B, a.H, a.Hkv, a.Sq,
                   a.Sk, a.D, a.mask ? a.cmp : -1, a.skip);
-    prof_begin(c, nm);
+    L.name = nm;
   }
-  launch_flash(a, c->stream);
-  prof_end(c);
-  note_launch(c, true);
+  L.fused = true;
+  run_launch(c, std::move(L));
   return true;
 }
 
@@ -1927,15 +1923,15 @@ bool Lower::emit_gemm_fused(Tensor* t, const GemmPlan& p) {
         parts += std::string(i ? "," : "") + std::to_string(args[i].N) + epi_suffix(args[i].epi);
         if (i) gemm_out.erase(outs[i]);
       }
+      Launch L{GemmL{args, true}};
       if (c->profiling) {
         char nm[200];
         std::snprintf(nm, sizeof nm, "gemm_lds_nn{%s}[1,%lld,%lld,%lld]", parts.c_str(),
                       (long long)args[0].M, (long long)n_all, (long long)args[0].K);
-        prof_begin(c, nm);
+        L.name = nm;
       }
-      launch_gemm_multi(args.data(), (int)args.size(), c->stream);
-      prof_end(c);
-      note_launch(c, true);
+      L.fused = true;
+      run_launch(c, std::move(L));
       return true;
     }
     // otherwise each member is launched on its own
@@ -1949,17 +1945,16 @@ bool Lower::emit_gemm_fused(Tensor* t, const GemmPlan& p) {
   }
   tensor_alloc(t);
   g.c = t->data();
+  Launch L{GemmL{{g}, p.epi == EPI_BIAS_ROPE}};
   if (c->profiling) {
     char nm[160];
     std::snprintf(nm, sizeof nm, "%s%s[%lld,%lld,%lld,%lld]",
                   p.epi == EPI_BIAS_ROPE ? "gemm_lds_nn" : gemm_variant(g), epi_suffix(p.epi),
                   (long long)g.batch, (long long)g.M, (long long)g.N, (long long)g.K);
-    prof_begin(c, nm);
+    L.name = nm;
   }
-  if (p.epi == EPI_BIAS_ROPE) launch_gemm_multi(&g, 1, c->stream);
-  else launch_gemm(g, c->stream);
-  prof_end(c);
-  note_launch(c, true);
+  L.fused = true;
+  run_launch(c, std::move(L));
   return true;
 }
 
@@ -2314,7 +2309,8 @@ bool Lower::emit_moe(Tensor* t, const MoePlan& p) {
   Tensor* work = new_tensor(c, kU8, ws);
   work->plan_dead = true;
   tensor_alloc(work);
-  run_routed_ffn(c, a, work->data());
+  MoeL m{a, ids, ptrs, work->data()};
+  run_launch(c, Launch{std::move(m)});
   maybe_destroy(work);
   return true;
 }
@@ -2546,11 +2542,10 @@ bool Lower::emit_norm(Tensor* t, const NormPlan& p) {
   tensor_alloc(t);
   a.y = t->data();
   a.y_dt = t->dt;
-  if (c->profiling)
-    prof_begin(c, "rmsnorm_rows{" + std::to_string(a.rows) + "x" + std::to_string(n) + "}");
-  launch_rmsnorm_rows(a, c->stream);
-  prof_end(c);
-  note_launch(c, true);
+  Launch L{a};
+  if (c->profiling) L.name = "rmsnorm_rows{" + std::to_string(a.rows) + "x" + std::to_string(n) + "}";
+  L.fused = true;
+  run_launch(c, std::move(L));
   return true;
 }
 
@@ -2627,11 +2622,10 @@ bool Lower::emit_softmax(Tensor* t, const SoftmaxPlan& p) {
     tensor_drop_storage(t);
     return false;
   }
-  if (c->profiling)
-    prof_begin(c, "softmax_rows{" + std::to_string(a.rows) + "x" + std::to_string(n) + "}");
-  launch_softmax_rows(a, c->stream);
-  prof_end(c);
-  note_launch(c, true);
+  Launch L{a};
+  if (c->profiling) L.name = "softmax_rows{" + std::to_string(a.rows) + "x" + std::to_string(n) + "}";
+  L.fused = true;
+  run_launch(c, std::move(L));
   return true;
 }
 
@@ -2665,11 +2659,10 @@ bool Lower::emit_rope(Tensor* t, const RopePlan& p) {
   tensor_alloc(t);
   a.y = t->data();
   a.y_dt = t->dt;
-  if (c->profiling)
-    prof_begin(c, "rope_pairs{" + std::to_string(t->numel()) + "}");
-  launch_rope(a, c->stream);
-  prof_end(c);
-  note_launch(c, true);
+  Launch L{a};
+  if (c->profiling) L.name = "rope_pairs{" + std::to_string(t->numel()) + "}";
+  L.fused = true;
+  run_launch(c, std::move(L));
   return true;
 }
 
@@ -2706,11 +2699,11 @@ bool Lower::emit_gather_norm(Node* n, Tensor* t, const NormPlan& p) {
   tensor_alloc(t);
   a.xout = G->data();
   a.y = t->data();
+  Launch L{a};
   if (c->profiling)
-    prof_begin(c, "gather_rmsnorm{" + std::to_string(a.rows) + "x" + std::to_string(nn) + "}");
-  launch_rmsnorm_rows(a, c->stream);
-  prof_end(c);
-  note_launch(c, true);
+    L.name = "gather_rmsnorm{" + std::to_string(a.rows) + "x" + std::to_string(nn) + "}";
+  L.fused = true;
+  run_launch(c, std::move(L));
   return true;
 }
 
@@ -2744,10 +2737,9 @@ void Lower::emit_gather(Node* n) {
   int64_t post = 1;
   for (int i = dim + 1; i < src->shape.rank; ++i) post *= src->shape.d[i];
   g.row_bytes = post * dt_size(src->dt);
-  prof_begin(c, "gather_rows");
-  launch_gather(g, c->stream);
-  prof_end(c);
-  note_launch(c, false);
+  Launch L{g};
+  if (c->profiling) L.name = "gather_rows";
+  run_launch(c, std::move(L));
 }
 
 // argmax (src/rew/ops/reduce.nim:202-225 semantics) over any dim of a dense
@@ -2766,11 +2758,11 @@ void Lower::emit_argmax(Node* n) {
   for (int i = dim + 1; i < x->shape.rank; ++i) g.inner *= x->shape.d[i];
   g.n = x->shape.d[dim];
   if (g.n > INT32_MAX) throw Error(REW_MI355X_ERR_UNSUPPORTED, "argmax: dimension above 2^31");
-  prof_begin(c, "argmax{" + std::to_string(g.outer) + "x" + std::to_string(g.n) + "x" +
-                    std::to_string(g.inner) + "}");
-  launch_argmax(g, c->stream);
-  prof_end(c);
-  note_launch(c, false);
+  Launch L{g};
+  if (c->profiling)
+    L.name = "argmax{" + std::to_string(g.outer) + "x" + std::to_string(g.n) + "x" +
+             std::to_string(g.inner) + "}";
+  run_launch(c, std::move(L));
 }
 
 // topK over the last dim (src/rew/ops/sort.nim:36-90 semantics).
@@ -2790,11 +2782,11 @@ void Lower::emit_topk(Node* n) {
   if (g.cols > kTopkMaxCols)
     throw Error(REW_MI355X_ERR_UNSUPPORTED,
                 "eager 'topK': last dimension above " + std::to_string(kTopkMaxCols));
-  prof_begin(c, "topk{" + std::to_string(g.rows) + "x" + std::to_string(g.cols) + ",k" +
-                    std::to_string(g.k) + "}");
-  launch_topk(g, c->stream);
-  prof_end(c);
-  note_launch(c, false);
+  Launch L{g};
+  if (c->profiling)
+    L.name = "topk{" + std::to_string(g.rows) + "x" + std::to_string(g.cols) + ",k" +
+             std::to_string(g.k) + "}";
+  run_launch(c, std::move(L));
 }
 
 // Row sort over the last dim (the stablehlo.sort form the jit path and the
@@ -2816,10 +2808,9 @@ void Lower::emit_sort(Node* n) {
   }
   g.cols = k->shape.d[k->shape.rank - 1];
   g.rows = g.cols ? k->numel() / g.cols : 0;
-  prof_begin(c, "sort{" + std::to_string(g.rows) + "x" + std::to_string(g.cols) + "}");
-  launch_sort(g, c->stream);
-  prof_end(c);
-  note_launch(c, false);
+  Launch L{g};
+  if (c->profiling) L.name = "sort{" + std::to_string(g.rows) + "x" + std::to_string(g.cols) + "}";
+  run_launch(c, std::move(L));
 }
 
 // stablehlo.gather / stablehlo.scatter: the dimension numbers resolved into
@@ -2895,45 +2886,22 @@ void Lower::emit_index_map(Node* n) {
     g.bat_it[i] = it_of_batch[k];
   }
   for (int d = 0; d < xs.rank; ++d) g.slice[d] = gather ? n->l5[d] : 0;
-  if (gather) {
-    prof_begin(c, "gather_nd{" + std::to_string(g.total) + "}");
-    launch_gather_nd(g, c->stream);
-  } else {
-    if (out->nbytes())
-      REW_HIP(hipMemcpyAsync(out->data(), x->data(), (size_t)out->nbytes(),
-                             hipMemcpyDeviceToDevice, c->stream));
-    prof_begin(c, "scatter{" + std::to_string(g.total) + "}");
-    launch_scatter(g, c->stream);
-  }
-  prof_end(c);
-  note_launch(c, false);
+  if (!gather)  // the result starts as a copy of the input
+    run_launch(c, Launch{FillL{out->data(), x->data(), (size_t)out->nbytes()}});
+  Launch L{IndexMapL{g, !gather}};
+  if (c->profiling)
+    L.name = (gather ? "gather_nd{" : "scatter{") + std::to_string(g.total) + "}";
+  run_launch(c, std::move(L));
 }
 
 // ---------------------------------------------------------------------------
 // flush
 // ---------------------------------------------------------------------------
 
-void flush(Ctx* c) {
-  if (c->pending.empty()) return;
-  std::vector<Node*> all;
-  all.swap(c->pending);
-  c->stats.flushes++;
-
-  // 1. dead-node elimination (reverse creation order)
-  for (size_t i = all.size(); i-- > 0;) {
-    Node* n = all[i];
-    bool dead = true;
-    for (Tensor* t : n->out)
-      if (t->ext > 0 || t->uses > 0) dead = false;
-    if (dead) {
-      n->dead = true;
-      for (Tensor* t : n->in) t->uses--;
-    }
-  }
-  Lower L(c);
-  for (Node* n : all)
-    if (!n->dead) L.nodes.push_back(n);
-
+// Steps 2 and 3 of a flush: classification, pattern matching and emission.
+static void lower_graph(Ctx* c, Lower& L, const std::string* sig,
+                        const std::vector<Tensor*>& leaves, const std::vector<int32_t>& leaf_slot,
+                        std::exception_ptr* err) {
   // 2. classification
   std::unordered_map<Tensor*, std::vector<Node*>> consumers;
   for (Node* n : L.nodes)
@@ -2992,17 +2960,77 @@ void flush(Ctx* c) {
     L.match_gemm_groups();
   }
 
-  // 3. emission in creation order
-  std::exception_ptr err;
+  // 3. emission in creation order (recorded as the graph's plan when
+  // `sig` is set)
+  if (sig) plan_record_begin(c, L.nodes, leaves, leaf_slot);
   try {
     for (Node* n : L.nodes)
       for (Tensor* t : n->out)
         if (t->plan_mat && !t->st) L.ensure_mat(t);
   } catch (...) {
-    err = std::current_exception();
+    *err = std::current_exception();
   }
   for (Tensor* t : L.temps) maybe_destroy(t);
   L.temps.clear();
+  if (sig) plan_record_end(c, *sig, !*err);
+}
+
+static void flush_graph(Ctx* c, std::vector<Node*>& all);
+
+void flush(Ctx* c) {
+  if (c->pending.empty()) return;
+  const auto t0 = std::chrono::steady_clock::now();
+  std::vector<Node*> all;
+  all.swap(c->pending);
+  c->stats.flushes++;
+  struct Clock {
+    Ctx* c;
+    std::chrono::steady_clock::time_point t0;
+    ~Clock() {
+      c->stats.flush_host_ns +=
+          std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now() - t0)
+              .count();
+    }
+  } clock{c, t0};
+  flush_graph(c, all);
+}
+
+static void flush_graph(Ctx* c, std::vector<Node*>& all) {
+  // 1. dead-node elimination (reverse creation order)
+  for (size_t i = all.size(); i-- > 0;) {
+    Node* n = all[i];
+    bool dead = true;
+    for (Tensor* t : n->out)
+      if (t->ext > 0 || t->uses > 0) dead = false;
+    if (dead) {
+      n->dead = true;
+      for (Tensor* t : n->in) t->uses--;
+    }
+  }
+  Lower L(c);
+  for (Node* n : all)
+    if (!n->dead) L.nodes.push_back(n);
+
+  // 1b. a graph flushed before replays the launches recorded then
+  std::string sig;
+  std::vector<Tensor*> leaves;
+  std::vector<int32_t> leaf_slot;
+  FlushPlan* plan = nullptr;
+  if (c->plan_cache && !L.nodes.empty()) {
+    sig = flush_signature(c, L.nodes, &leaves, &leaf_slot);
+    plan = plan_find(c, sig);
+  }
+  std::exception_ptr err;
+  if (plan && plan->ok) {
+    c->stats.flush_plan_hits++;
+    try {
+      plan_replay(c, *plan, L.nodes, leaves);
+    } catch (...) {
+      err = std::current_exception();
+    }
+  } else {
+    lower_graph(c, L, !sig.empty() && !plan ? &sig : nullptr, leaves, leaf_slot, &err);
+  }
 
   // 4. release: graph references drop, temporaries free
   for (Node* n : all) {

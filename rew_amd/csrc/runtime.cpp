@@ -9,6 +9,7 @@
 #include <unordered_set>
 
 #include "kernels.h"
+#include "plan.h"
 #include "runtime.h"
 
 namespace rew {
@@ -107,16 +108,19 @@ void tensor_alloc(Tensor* t) {
   s->ptr = t->ctx->alloc.get(bytes, &s->bytes);
   s->refs = 1;
   t->st = s;
+  if (t->ctx->rec) plan_note_alloc(t);
 }
 
 void tensor_alias(Tensor* t, Tensor* src) {
   if (t->st) return;
   t->st = src->st;
   t->st->refs++;
+  if (t->ctx->rec) plan_note_alias(t, src);
 }
 
 void storage_release(Storage* s) {
   if (s && --s->refs == 0) {
+    if (s->ctx->rec) plan_note_free(s);
     s->ctx->alloc.put(s->ptr, s->bytes);
     delete s;
   }
@@ -130,8 +134,10 @@ void const_cache_clear(Ctx* c) {
 void tensor_drop_storage(Tensor* t) {
   Storage* s = t->st;
   if (!s) return;
+  if (t->ctx->rec) plan_note_drop(t);
   t->st = nullptr;
   if (--s->refs == 0) {
+    if (s->ctx->rec) plan_note_free(s);
     s->ctx->alloc.put(s->ptr, s->bytes);
     delete s;
   }
@@ -140,6 +146,7 @@ void tensor_drop_storage(Tensor* t) {
 void maybe_destroy(Tensor* t) {
   if (t->ext > 0 || t->uses > 0 || t->prod) return;
   tensor_drop_storage(t);
+  if (t->ctx->rec) plan_note_destroy(t);
   {
     std::lock_guard<std::mutex> g(g_reg_mu);
     g_live.erase(t);
@@ -329,6 +336,8 @@ int rew_mi355x_init(int ordinal, rew_mi355x_ctx** out) {
         if (s[0] == '1') c->mode = REW_MI355X_MODE_OP_BY_OP;
       if (const char* s = std::getenv("REW_MI355X_NO_PATTERNS"))
         if (s[0] == '1') c->no_fusion_patterns = true;
+      if (const char* s = std::getenv("REW_MI355X_PLAN_CACHE"))
+        if (s[0] == '0') c->plan_cache = false;
       g_ctx[ordinal] = c;
     }
     *out = reinterpret_cast<rew_mi355x_ctx*>(g_ctx[ordinal]);
@@ -343,6 +352,7 @@ int rew_mi355x_shutdown(rew_mi355x_ctx* ctx) {
     flush(c);
     REW_HIP(hipStreamSynchronize(c->stream));
     jit_module_cache_clear(c);
+    plan_cache_clear(c);
     const_cache_clear(c);
     c->alloc.trim();
   });
@@ -621,9 +631,10 @@ int rew_mi355x_clear_cache(rew_mi355x_ctx* ctx) {
   return guarded([&] {
     Ctx* c = as_ctx(ctx);
     std::lock_guard<std::recursive_mutex> g(c->mu);
-    // Plans are rebuilt per flush; the cached small constants are dropped
-    // (their storage returns to the allocator once no tensor uses it).
+    // The cached small constants are dropped (their storage returns to the
+    // allocator once no tensor uses it), and so are the recorded flush plans.
     const_cache_clear(c);
+    plan_cache_clear(c);
   });
 }
 

@@ -2,6 +2,7 @@
 // deferred op graph, the per-device context and its caching allocator.
 #pragma once
 
+#include <deque>
 #include <map>
 #include <mutex>
 #include <string>
@@ -17,6 +18,8 @@ struct Ctx;
 struct Node;
 struct RoutedFfn;
 struct JitModule;
+struct FlushPlan;
+struct PlanRecorder;
 
 // A device allocation shared by every tensor that aliases it (a reshape of
 // a materialized tensor aliases its source).
@@ -131,6 +134,12 @@ struct Ctx {
   // translated jit modules (stablehlo.cpp), keyed by
   // ordinal::name::cacheKey::hash(text)
   std::unordered_map<std::string, JitModule*> jit_modules;
+  // recorded lowerings by graph signature (plan.cpp), oldest first in
+  // plan_order; `rec` is set while a flush is being recorded
+  bool plan_cache = true;  // REW_MI355X_PLAN_CACHE=0 turns replay off
+  std::unordered_map<std::string, FlushPlan*> flush_plans;
+  std::deque<std::string> plan_order;
+  PlanRecorder* rec = nullptr;
 };
 
 // ---- runtime services (runtime.cpp) -----------------------------------------
@@ -142,6 +151,14 @@ void tensor_alias(Tensor* t, Tensor* src);    // share src's storage
 void tensor_drop_storage(Tensor* t);
 void maybe_destroy(Tensor* t);                // free when unreferenced
 bool tensor_is_live_handle(const Tensor* t);
+
+// Hooks of the flush-plan recorder (plan.cpp): the tensor services above
+// report what they do while a lowering is being recorded (ctx->rec set).
+void plan_note_alloc(Tensor* t);               // t just received fresh storage
+void plan_note_alias(Tensor* t, Tensor* src);  // t now shares src's storage
+void plan_note_drop(Tensor* t);                // t is about to drop its storage
+void plan_note_destroy(Tensor* t);             // t is about to be deleted
+void plan_note_free(Storage* s);               // s is about to return to the allocator
 
 // Stream-ordered copy of a small host table into device memory (through
 // the pinned staging ring; `src` may be reused as soon as this returns).

@@ -24,7 +24,15 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(lib, n), f"librew_mi355x.so does not export {n}"
     assert set(names) == set(_lib.SIGNATURES), "ctypes table out of sync with the header"
-    assert lib.rew_mi355x_abi_version() == 2
+    assert lib.rew_mi355x_abi_version() == 3
+
+
+def test_stats_struct_matches_header():
+    from rew_amd import _lib
+    text = (ROOT / "include" / "rew_mi355x.h").read_text()
+    body = re.search(r"typedef struct rew_mi355x_stats \{(.*?)\} rew_mi355x_stats;", text, re.S)
+    fields = re.findall(r"int64_t\s+([a-z_0-9]+);", body.group(1))
+    assert [n for n, _ in _lib.Stats._fields_] == fields
 
 
 def test_rng_matches_oracle(oracle):
