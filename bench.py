@@ -166,13 +166,16 @@ def timed_run(step, steps, warmup):
     return wall, dev_ms, first_ms, prof, hostc
 
 
-def by_symbol(prof, work_of):
+def by_symbol(prof, work_of, by_shape=False):
     """Groups profile entries by kernel symbol: launches, ms and the summed
-    algorithmic work (work_of(entry name) -> units, or None if unknown)."""
+    algorithmic work (work_of(entry name) -> units, or None if unknown).
+    by_shape: one group per entry name (symbol and launch shape), so that
+    launches of one symbol over different sizes are not averaged together."""
     out = {}
     for name, n, ms in prof:
-        d = out.setdefault(kernel_symbol(name), {"launches": 0, "ms": 0.0, "work": 0,
-                                                 "known": True})
+        d = out.setdefault(name if by_shape else kernel_symbol(name),
+                           {"launches": 0, "ms": 0.0, "work": 0, "known": True,
+                            "symbol": kernel_symbol(name)})
         d["launches"] += n
         d["ms"] += ms
         w = work_of(name)
@@ -196,7 +199,8 @@ def traffic_for(workload, kernel):
 
 def roofline(workload, syms, bound):
     """Roofline object of the kernel with the largest summed duration."""
-    ksym, d = max(syms.items(), key=lambda kv: kv[1]["ms"])
+    _, d = max(syms.items(), key=lambda kv: kv[1]["ms"])
+    ksym = d["symbol"]
     avg_ms = d["ms"] / d["launches"]
     peak, unit = (BF16_PEAK_TFLOPS, "TFLOP/s") if bound == "mfma" else (HBM_PEAK_GBS, "GB/s")
     roof = {"bound": bound, "kernel": ksym, "achieved": None, "peak": peak, "unit": unit,
@@ -440,14 +444,14 @@ def run_chain(args):
             return groups["rmsNorm"]
         if name.startswith("softmax_rows"):
             return groups["softmax"]
-        if name.startswith("ew_"):
-            return groups["relu_chain"]
+        if name.startswith("ew_"):  # the relu chain, or the [8192] divide of reduceMean
+            return groups["relu_chain"] if name.startswith(f"ew_fused{{{R * Cn}x") else 3 * R * 4
         if name.startswith("reduce"):
             return nbytes + R * 4
         return None
 
     syms = by_symbol(prof, bytes_of)
-    roof = roofline("chain", syms, "hbm")
+    roof = roofline("chain", by_symbol(prof, bytes_of, by_shape=True), "hbm")
     cpu = None
     if not args.no_cpu_baseline:
         orc = oracle_mod()

@@ -226,6 +226,86 @@ __global__ void __launch_bounds__(256) rmsnorm_pipe_kernel(RowNormArgs a) {
   }
 }
 
+// ---- workgroup per row ----------------------------------------------------------------------
+//
+// Rows of exactly 256 CPL 16-byte chunks: the four waves of a workgroup
+// split one row, thread t holding chunks k 256 + t (k < CPL), so each row's
+// arithmetic is a quarter of a wave-per-row kernel's and up to eight
+// workgroups per CU keep loads in flight while others compute (no software
+// pipeline, no persistent loop).  The row total is the wave butterfly of
+// each wave's partials, then the four wave sums as (w0 + w1) + (w2 + w3).
+template <int SLOT>
+__device__ __forceinline__ float wg_row_sum(float v, float (&part)[2][4]) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  if ((threadIdx.x & 63) == 0) part[SLOT][threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (part[SLOT][0] + part[SLOT][1]) + (part[SLOT][2] + part[SLOT][3]);
+}
+
+template <int XB, int YB, int CPL>
+__global__ void __launch_bounds__(256) rmsnorm_wg_kernel(RowNormArgs a) {
+  constexpr int EPC = 16 / XB;
+  __shared__ float part[2][4];
+  const int64_t row = blockIdx.x;
+  const int t = threadIdx.x;
+  const char* x = (const char*)a.x + row * a.x_rs * XB;
+  uint4 raw[CPL];
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) raw[k] = *(const uint4*)(x + ((int64_t)k * 256 + t) * 16);
+  auto elem = [&](int k, int e) {
+    const uint32_t* w = (const uint32_t*)&raw[k];
+    return XB == 2 ? as_f((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16)) : as_f(w[e]);
+  };
+  float ss = 0.0f;
+#pragma unroll
+  for (int k = 0; k < CPL; ++k)
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      const float v = elem(k, e);
+      const float sq = v * v;
+      ss += sq;
+    }
+  ss = wg_row_sum<0>(ss, part);
+  const float mean = ss / a.divisor;
+  const float r = sqrtf(mean + a.eps);
+  const float rinv = 1.0f / r;  // x / r as x * (1 / r), as in rms_row
+  char* y = (char*)a.y + row * a.n * YB;
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) {
+    const int64_t j = ((int64_t)k * 256 + t) * EPC;
+    float out[EPC];
+#pragma unroll
+    for (int e = 0; e < EPC; e += 4) {
+      const float4 g = *(const float4*)(a.gamma + j + e);
+      out[e] = g.x * (elem(k, e) * rinv);
+      out[e + 1] = g.y * (elem(k, e + 1) * rinv);
+      out[e + 2] = g.z * (elem(k, e + 2) * rinv);
+      out[e + 3] = g.w * (elem(k, e + 3) * rinv);
+    }
+    if (YB == 2) {
+      uint32_t o[EPC / 2];
+#pragma unroll
+      for (int e = 0; e < EPC; e += 2) o[e / 2] = bf16x2_bits(out[e], out[e + 1]);
+      if (EPC == 8) *(uint4*)(y + j * 2) = *(const uint4*)o;
+      else *(uint2*)(y + j * 2) = *(const uint2*)o;
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPC; e += 4)
+        *(float4*)(y + (j + e) * 4) = make_float4(out[e], out[e + 1], out[e + 2], out[e + 3]);
+    }
+  }
+}
+
+// REW_MI355X_ROWS=wave keeps the wave-per-row kernels for whole rows.
+static bool rows_wg() {
+  static const bool on = [] {
+    const char* s = std::getenv("REW_MI355X_ROWS");
+    return !(s && std::string(s) == "wave");
+  }();
+  return on;
+}
+
 bool rmsnorm_gather_ok(const RowNormArgs& a) {
   const int xb = a.x_dt == REW_DT_BFLOAT16 ? 2 : 4, yb = a.y_dt == REW_DT_BFLOAT16 ? 2 : 4;
   const int epc = 16 / xb;
@@ -246,6 +326,22 @@ void launch_rmsnorm_rows(const RowNormArgs& a, hipStream_t stream) {
   const int64_t chunks = (a.n + epc - 1) / epc;  // 16-byte chunks per row
   const bool vec = a.n % epc == 0 && (a.x_rs * xb) % 16 == 0 && ((uintptr_t)a.x & 15) == 0 &&
                    ((uintptr_t)a.y & 15) == 0 && (a.n * yb) % 16 == 0 && chunks <= 64 * 16;
+  // fp32 rows of 1024, 2048 or 4096: a workgroup per row (43 us against 59 us
+  // for the wave kernel on [8192, 4096]); bf16 rows keep the pipelined waves
+  // (the same time on [8192, 4096])
+  if (vec && !a.ids && xb == 4 && rows_wg() && ((uintptr_t)a.gamma & 15) == 0 &&
+      a.rows < (1 << 30) && (chunks == 256 || chunks == 512 || chunks == 1024)) {
+    const dim3 grid((unsigned)a.rows), block(256);
+#define REW_RMS(XB, YB, CPL) hipLaunchKernelGGL((rmsnorm_wg_kernel<XB, YB, CPL>), grid, block, 0, stream, a)
+#define REW_RMS_CPL(XB, YB) \
+    if (chunks == 256) REW_RMS(XB, YB, 1); else if (chunks == 512) REW_RMS(XB, YB, 2); else REW_RMS(XB, YB, 4)
+    if (yb == 2) { REW_RMS_CPL(4, 2); }
+    else { REW_RMS_CPL(4, 4); }
+#undef REW_RMS_CPL
+#undef REW_RMS
+    REW_HIP(hipGetLastError());
+    return;
+  }
   if (vec) {
     const int64_t blocks = (a.rows + 3) / 4;
     const dim3 grid((unsigned)(blocks < 65536 ? blocks : 65536)), block(256);
@@ -447,6 +543,51 @@ __global__ void __launch_bounds__(256) softmax_tile_kernel(SoftmaxArgs a) {
   }
 }
 
+// Rows of exactly 1024 CPL fp32 (256 CPL 16-byte chunks): a workgroup per
+// row, thread t holding chunks k 256 + t; the max, then the sum of the
+// exps, each over the workgroup (wg_row_sum's order), then the quotients.
+// The same fp32 ops per element as softmax_row; the sum runs in another
+// order than the compiled row reduction's.
+template <int CPL>
+__global__ void __launch_bounds__(256) softmax_wg_kernel(SoftmaxArgs a) {
+  __shared__ float part[2][4];
+  const int64_t row = blockIdx.x;
+  const int t = threadIdx.x;
+  const float* x = a.x + row * a.x_rs;
+  float4 v[CPL];
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) v[k] = *(const float4*)(x + ((int64_t)k * 256 + t) * 4);
+  float m = -INFINITY;  // the hardware max, as in softmax_row
+#pragma unroll
+  for (int k = 0; k < CPL; ++k)
+    m = __builtin_fmaxf(__builtin_fmaxf(m, __builtin_fmaxf(v[k].x, v[k].y)),
+                        __builtin_fmaxf(v[k].z, v[k].w));
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, s, 64));
+  if ((t & 63) == 0) part[1][t >> 6] = m;
+  __syncthreads();
+  m = __builtin_fmaxf(__builtin_fmaxf(part[1][0], part[1][1]),
+                      __builtin_fmaxf(part[1][2], part[1][3]));
+  float sum = 0.0f;
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) {
+    v[k].x = expf(v[k].x - m);
+    v[k].y = expf(v[k].y - m);
+    v[k].z = expf(v[k].z - m);
+    v[k].w = expf(v[k].w - m);
+    sum = sum + v[k].x;
+    sum = sum + v[k].y;
+    sum = sum + v[k].z;
+    sum = sum + v[k].w;
+  }
+  sum = wg_row_sum<0>(sum, part);
+  float* y = a.y + row * a.n;
+#pragma unroll
+  for (int k = 0; k < CPL; ++k)
+    *(float4*)(y + ((int64_t)k * 256 + t) * 4) =
+        make_float4(v[k].x / sum, v[k].y / sum, v[k].z / sum, v[k].w / sum);
+}
+
 bool softmax_rows_ok(const SoftmaxArgs& a) {
   if (a.rows <= 0 || a.n <= 0) return false;
   if (a.n < 128) return true;
@@ -470,7 +611,12 @@ void launch_softmax_rows(const SoftmaxArgs& a, hipStream_t stream) {
     const dim3 grid_pipe((unsigned)(blocks < 512 ? blocks : 512));
     const dim3 grid((unsigned)(blocks < 65536 ? blocks : 65536)), block(256);
     const int64_t ch = (a.n / 4 + 63) / 64;
-    if (a.n == 1024) hipLaunchKernelGGL((softmax_wave_kernel<4, true, true>), grid_pipe, block, 0, stream, a);
+    const dim3 grid_wg((unsigned)(a.rows < (1 << 30) ? a.rows : 1));
+    if (rows_wg() && a.rows < (1 << 30) && (a.n == 1024 || a.n == 2048 || a.n == 4096)) {
+      if (a.n == 1024) hipLaunchKernelGGL((softmax_wg_kernel<1>), grid_wg, block, 0, stream, a);
+      else if (a.n == 2048) hipLaunchKernelGGL((softmax_wg_kernel<2>), grid_wg, block, 0, stream, a);
+      else hipLaunchKernelGGL((softmax_wg_kernel<4>), grid_wg, block, 0, stream, a);
+    } else if (a.n == 1024) hipLaunchKernelGGL((softmax_wave_kernel<4, true, true>), grid_pipe, block, 0, stream, a);
     else if (a.n == 2048) hipLaunchKernelGGL((softmax_wave_kernel<8, true, true>), grid_pipe, block, 0, stream, a);
     else if (a.n == 4096) hipLaunchKernelGGL((softmax_wave_kernel<16, true, true>), grid_pipe, block, 0, stream, a);
     else if (ch <= 4) hipLaunchKernelGGL((softmax_wave_kernel<4, false, false>), grid, block, 0, stream, a);
