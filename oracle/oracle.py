@@ -274,6 +274,60 @@ def sort_order(x, axis: int, descending: bool):
     return np.argsort(-key if descending else key, axis=axis, kind="stable")
 
 
+def pad(x: np.ndarray, value, lo, hi, interior) -> np.ndarray:
+    """stablehlo.pad as rew emits it (src/rew/ops/shape.nim:139-172; result
+    shape src/rew/stablehlo/ops.nim:807-824): the operand's elements spread
+    `interior` apart, `lo` / `hi` elements of padding at the edges (negative
+    edges crop).  Built element by element from the output side."""
+    x = np.asarray(x)
+    shape = [d + l + h + max(d - 1, 0) * i for d, l, h, i in zip(x.shape, lo, hi, interior)]
+    out = np.full(shape, value, dtype=x.dtype)
+    # every operand element lands at lo + i * (interior + 1), if in range
+    for src in np.ndindex(*x.shape):
+        dst = tuple(l + s * (i + 1) for l, s, i in zip(lo, src, interior))
+        if all(0 <= d < n for d, n in zip(dst, shape)):
+            out[dst] = x[src]
+    return out
+
+
+def _clamped_starts(starts, room):
+    # stablehlo.dynamic_slice / dynamic_update_slice clamp each start into
+    # [0, operand dim - window dim]
+    return [min(max(int(s), 0), r) for s, r in zip(starts, room)]
+
+
+def dynamic_slice(x: np.ndarray, starts, sizes) -> np.ndarray:
+    """stablehlo.dynamic_slice (src/rew/ops/shape.nim:213-250)."""
+    st = _clamped_starts(starts, [d - s for d, s in zip(x.shape, sizes)])
+    return x[tuple(slice(a, a + s) for a, s in zip(st, sizes))].copy()
+
+
+def dynamic_update_slice(x: np.ndarray, upd: np.ndarray, starts) -> np.ndarray:
+    """stablehlo.dynamic_update_slice (src/rew/ops/shape.nim:251-290)."""
+    st = _clamped_starts(starts, [d - u for d, u in zip(x.shape, upd.shape)])
+    out = x.copy()
+    out[tuple(slice(a, a + u) for a, u in zip(st, upd.shape))] = upd
+    return out
+
+
+def cholesky(a: np.ndarray, lower: bool = True) -> np.ndarray:
+    """stablehlo.cholesky (src/rew/ops/linalg.nim:177-202) over the last two
+    dims, in float64 by the Cholesky-Crout recurrence, from the referenced
+    triangle only; the other triangle is zero."""
+    a = np.asarray(a, np.float64)
+    out = np.zeros_like(a)
+    n = a.shape[-1]
+    for b in np.ndindex(*a.shape[:-2]):
+        m = a[b] if lower else a[b].T
+        L = np.zeros((n, n))
+        for j in range(n):
+            L[j, j] = np.sqrt(m[j, j] - sum(L[j, k] * L[j, k] for k in range(j)))
+            for i in range(j + 1, n):
+                L[i, j] = (m[i, j] - sum(L[i, k] * L[j, k] for k in range(j))) / L[j, j]
+        out[b] = L if lower else L.T
+    return out
+
+
 # ---- composites ------------------------------------------------------------------------
 
 def softmax_rows(x: np.ndarray) -> np.ndarray:

@@ -232,4 +232,118 @@ void launch_scatter(const IndexMapArgs& g, hipStream_t stream) {
   REW_HIP(hipGetLastError());
 }
 
+
+// ---- pad / dynamicSlice / dynamicUpdateSlice -----------------------------------------
+
+namespace {
+
+// Start scalar d of a dynamic slice / update, clamped into [0, room]
+// (stablehlo.dynamic_slice / dynamic_update_slice); a uint64 start above
+// INT64_MAX is past every extent, so it clamps to room.
+__device__ __forceinline__ int64_t window_start(const WindowArgs& a, int d, int64_t room) {
+  int64_t s = load_index(a.start[d], a.start_dt[d], 0);
+  if (a.start_dt[d] == REW_DT_UINT64 && s < 0) s = room;
+  return s < 0 ? 0 : (s > room ? room : s);
+}
+
+__global__ void __launch_bounds__(256) window_kernel(WindowArgs a) {
+  int64_t st[8];
+  for (int d = 0; d < a.rank; ++d)
+    st[d] = a.mode == kWinSlice    ? window_start(a, d, a.x_dims[d] - a.out_dims[d])
+            : a.mode == kWinUpdate ? window_start(a, d, a.x_dims[d] - a.y_dims[d])
+                                   : 0;
+  const int64_t step = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < a.total; t += step) {
+    // coordinates of result element t, innermost dim first
+    int64_t rem = t, xl = 0, yl = 0, xs = 1, ys = 1;
+    bool in_x = true, in_y = true;
+    for (int d = a.rank - 1; d >= 0; --d) {
+      const int64_t o = rem % a.out_dims[d];
+      rem /= a.out_dims[d];
+      if (a.mode == kWinPad) {
+        const int64_t p = o - a.lo[d];
+        const int64_t i = p / a.step[d];
+        in_x = in_x && p >= 0 && p == i * a.step[d] && i < a.x_dims[d];
+        xl += i * xs;
+      } else if (a.mode == kWinSlice) {
+        xl += (o + st[d]) * xs;
+      } else {
+        const int64_t u = o - st[d];
+        in_y = in_y && u >= 0 && u < a.y_dims[d];
+        yl += u * ys;
+        xl += o * xs;
+      }
+      xs *= a.x_dims[d];
+      ys *= a.y_dims[d];
+    }
+    if (a.mode == kWinPad) {
+      if (in_x) copy_bytes(a.x, xl, a.out, t, a.esize);
+      else copy_bytes(a.y, 0, a.out, t, a.esize);
+    } else if (a.mode == kWinUpdate && in_y) {
+      copy_bytes(a.y, yl, a.out, t, a.esize);
+    } else {
+      copy_bytes(a.x, xl, a.out, t, a.esize);
+    }
+  }
+}
+
+// One matrix per workgroup, in LDS.  Column j: the pivot
+// d = sqrt(a_jj - sum_{k<j} l_jk^2), then every row i > j in parallel
+// l_ij = (a_ij - sum_{k<j} l_ik l_jk) / d, the sums in k order.  The upper
+// form factors the transpose of the upper triangle the same way.
+template <typename T>
+__global__ void __launch_bounds__(256) cholesky_kernel(CholeskyArgs a) {
+  __shared__ T L[kCholMaxN][kCholMaxN + 1];
+  const int n = (int)a.n;
+  const T* x = (const T*)a.x + blockIdx.x * a.n * a.n;
+  T* out = (T*)a.out + blockIdx.x * a.n * a.n;
+  for (int e = threadIdx.x; e < n * n; e += blockDim.x) {
+    const int i = e / n, j = e % n;
+    // L[i][j] (i >= j) from the referenced triangle
+    if (i >= j) L[i][j] = a.lower ? x[(int64_t)i * n + j] : x[(int64_t)j * n + i];
+  }
+  __syncthreads();
+  for (int j = 0; j < n; ++j) {
+    if (threadIdx.x == 0) {
+      T s = L[j][j];
+      for (int k = 0; k < j; ++k) s -= L[j][k] * L[j][k];
+      L[j][j] = sqrt(s);
+    }
+    __syncthreads();
+    const T d = L[j][j];
+    for (int i = j + 1 + threadIdx.x; i < n; i += blockDim.x) {
+      T s = L[i][j];
+      for (int k = 0; k < j; ++k) s -= L[i][k] * L[j][k];
+      L[i][j] = s / d;
+    }
+    __syncthreads();
+  }
+  for (int e = threadIdx.x; e < n * n; e += blockDim.x) {
+    const int i = e / n, j = e % n;
+    T v = 0;
+    if (a.lower && i >= j) v = L[i][j];
+    if (!a.lower && j >= i) v = L[j][i];
+    out[e] = v;
+  }
+}
+
+}  // namespace
+
+void launch_window(const WindowArgs& a, hipStream_t stream) {
+  if (a.total == 0) return;
+  if (a.rank < 0 || a.rank > 8 || (a.esize != 1 && a.esize != 2 && a.esize != 4 && a.esize != 8))
+    fail(REW_MI355X_ERR_INVALID, "internal: window launch outside its limits");
+  hipLaunchKernelGGL(window_kernel, dim3(index_map_grid(a.total)), dim3(256), 0, stream, a);
+  REW_HIP(hipGetLastError());
+}
+
+void launch_cholesky(const CholeskyArgs& a, hipStream_t stream) {
+  if (a.batch == 0 || a.n == 0) return;
+  if (a.n > kCholMaxN || a.batch > 0x7fffffff)
+    fail(REW_MI355X_ERR_INVALID, "internal: cholesky launch outside its limits");
+  if (a.f64) hipLaunchKernelGGL(cholesky_kernel<double>, dim3((unsigned)a.batch), dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL(cholesky_kernel<float>, dim3((unsigned)a.batch), dim3(256), 0, stream, a);
+  REW_HIP(hipGetLastError());
+}
+
 }  // namespace rew

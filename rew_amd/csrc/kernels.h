@@ -204,6 +204,45 @@ struct IndexMapArgs {
   int64_t total;      // elements of the iteration space
 };
 void launch_gather_nd(const IndexMapArgs& g, hipStream_t stream);
+
+// ---- pad / dynamicSlice / dynamicUpdateSlice (k_gather.hip) ---------------------
+// One thread per result element over dense row-major tensors of rank <= 8.
+//   pad:    out[o] = x[(o - lo) / step] where every dim's o - lo is a
+//           non-negative multiple of step (= interior + 1) inside x, else
+//           the padding value *y (negative lo / high crop);
+//   slice:  out[o] = x[o + s], s the start scalars clamped to [0, x - out];
+//   update: out[o] = y[o - s] inside the update window, else x[o], s clamped
+//           to [0, x - y].
+// Start scalars are read on the device (any integer dtype), so no value
+// leaves the GPU.
+enum { kWinPad = 0, kWinSlice = 1, kWinUpdate = 2 };
+struct WindowArgs {
+  int mode, esize, rank;
+  const void* x;
+  const void* y;  // pad: the padding value; update: the update tensor
+  void* out;
+  int64_t out_dims[8], x_dims[8], y_dims[8];
+  int64_t lo[8], step[8];
+  const void* start[8];
+  int start_dt[8];
+  int64_t total;
+};
+void launch_window(const WindowArgs& a, hipStream_t stream);
+
+// ---- cholesky (k_gather.hip) --------------------------------------------------------
+// Batched Cholesky factorisation of dense [batch, n, n] f32 / f64 matrices,
+// one workgroup per matrix held in LDS (n <= kCholMaxN): A = L L^T from the
+// lower triangle (lower) or A = U^T U from the upper one; the other
+// triangle of the result is zero.  A matrix that is not positive definite
+// gives NaN from the first failing pivot on.
+constexpr int64_t kCholMaxN = 64;
+struct CholeskyArgs {
+  const void* x;
+  void* out;
+  int64_t batch, n;
+  int f64, lower;
+};
+void launch_cholesky(const CholeskyArgs& a, hipStream_t stream);
 void launch_scatter(const IndexMapArgs& g, hipStream_t stream);
 
 // ---- argmax / topK (k_select.hip) ----------------------------------------------

@@ -45,7 +45,7 @@ static bool is_view(int k) {
 static bool is_ew(int k) {
   return k == K_BINARY || k == K_UNARY || k == K_CONVERT || k == K_ISFINITE ||
          k == K_COMPARE || k == K_SELECT || k == K_CLAMP || k == K_IOTA ||
-         k == K_CONCAT || k == K_REDUCE_PRECISION;
+         k == K_CONCAT || k == K_REDUCE_PRECISION || k == K_CONST;
 }
 // Consumers that read an operand through a fused prologue.
 static bool takes_expression(int k) { return is_ew(k) || is_view(k) || k == K_REDUCE; }
@@ -342,6 +342,8 @@ struct Lower {
   void emit_sort(Node* n);
   bool emit_gather_norm(Node* n, Tensor* t, const NormPlan& p);
   void emit_index_map(Node* n);
+  void emit_window(Node* n);
+  void emit_cholesky(Node* n);
   // Materialize `t` (any kind) into a fresh dense tensor whose shape is the
   // permutation `perm` of t's shape.
   Tensor* emit_permuted_copy(Tensor* t, const std::vector<int>& perm);
@@ -662,6 +664,8 @@ int Gen::gen_node(Node* p, Tensor* u, const Affine& m) {
       uint8_t op = is_float_dt(dt) ? OP_CLAMPF : (dt_is_signed(dt) ? OP_CLAMPI : OP_CLAMPU);
       return emit(op, lo, x, hi);
     }
+    case K_CONST:  // a 32-bit integer scalar fixed by the op
+      return emit(OP_CONST, 0, 0, 0, 0, (uint32_t)p->i0);
     case K_IOTA: {
       Affine row;
       row.R = m.R;
@@ -1037,6 +1041,8 @@ void Lower::emit_anchor(Node* n) {
     case K_SORT: emit_sort(n); break;
     case K_GATHER:
     case K_SCATTER: emit_index_map(n); break;
+    case K_WINDOW: emit_window(n); break;
+    case K_CHOLESKY: emit_cholesky(n); break;
     case K_BITCAST: {
       Tensor* x = n->in[0];
       ensure_mat(x);
@@ -2810,6 +2816,59 @@ void Lower::emit_sort(Node* n) {
   g.rows = g.cols ? k->numel() / g.cols : 0;
   Launch L{g};
   if (c->profiling) L.name = "sort{" + std::to_string(g.rows) + "x" + std::to_string(g.cols) + "}";
+  run_launch(c, std::move(L));
+}
+
+// pad / dynamicSlice / dynamicUpdateSlice over dense operands: in[0] the
+// operand, then the padding value (pad), or the update (dynamicUpdateSlice),
+// then the start scalars.
+void Lower::emit_window(Node* n) {
+  for (Tensor* t : n->in) ensure_mat(t);
+  Tensor* out = n->out[0];
+  tensor_alloc(out);
+  WindowArgs a;
+  std::memset(&a, 0, sizeof a);
+  Tensor* x = n->in[0];
+  a.mode = n->sub;
+  a.esize = dt_size(x->dt);
+  a.rank = x->shape.rank;
+  a.x = x->data();
+  a.out = out->data();
+  a.total = out->numel();
+  const int first_start = n->sub == kWinSlice ? 1 : 2;
+  if (n->sub != kWinSlice) a.y = n->in[1]->data();
+  for (int d = 0; d < a.rank; ++d) {
+    a.out_dims[d] = out->shape.d[d];
+    a.x_dims[d] = x->shape.d[d];
+    a.y_dims[d] = n->sub == kWinUpdate ? n->in[1]->shape.d[d] : 1;
+    if (n->sub == kWinPad) {
+      a.lo[d] = n->l0[d];
+      a.step[d] = n->l2[d] + 1;
+    } else {
+      a.start[d] = n->in[first_start + d]->data();
+      a.start_dt[d] = n->in[first_start + d]->dt;
+    }
+  }
+  Launch L{a};
+  if (c->profiling) L.name = n->name + "{" + std::to_string(a.total) + "}";
+  run_launch(c, std::move(L));
+}
+
+void Lower::emit_cholesky(Node* n) {
+  Tensor* x = n->in[0];
+  ensure_mat(x);
+  tensor_alloc(n->out[0]);
+  CholeskyArgs a;
+  std::memset(&a, 0, sizeof a);
+  a.x = x->data();
+  a.out = n->out[0]->data();
+  a.n = x->shape.d[x->shape.rank - 1];
+  a.batch = a.n ? x->numel() / (a.n * a.n) : 0;
+  a.f64 = x->dt == kF64;
+  a.lower = (int)n->i0;
+  Launch L{a};
+  if (c->profiling)
+    L.name = "cholesky{" + std::to_string(a.batch) + "x" + std::to_string(a.n) + "}";
   run_launch(c, std::move(L));
 }
 

@@ -99,6 +99,12 @@ static const std::unordered_map<std::string, OpSpec>& op_table() {
       // backend extensions (no eager counterpart in the reference)
       {"argmax", {K_ARGMAX, 0}}, {"topK", {K_TOPK, 0}}, {"sort", {K_SORT, 0}},
       {"gather", {K_GATHER, 0}}, {"scatter", {K_SCATTER, 0}},
+      // eager ops of rew's table outside the configs (src/rew/eager.nim:838-850)
+      {"pad", {K_WINDOW, kWinPad}}, {"dynamicSlice", {K_WINDOW, kWinSlice}},
+      {"dynamicUpdateSlice", {K_WINDOW, kWinUpdate}}, {"cholesky", {K_CHOLESKY, 0}},
+      {"getDimensionSize", {K_CONST, 0}}, {"replicaId", {K_CONST, 1}},
+      {"partitionId", {K_CONST, 1}}, {"setDimensionSize", {K_RESHAPE, 1}},
+      {"dynamicReshape", {K_RESHAPE, 2}}, {"dynamicIota", {K_IOTA, 1}},
   };
   return t;
 }
@@ -108,9 +114,7 @@ static const std::unordered_map<std::string, OpSpec>& op_table() {
 static bool known_but_unimplemented(const std::string& n) {
   static const char* names[] = {
       "complex", "real", "imag", "conv2d", "maxPool2d", "batchNormInference",
-      "batchNormTraining", "batchNormGrad", "cholesky", "getDimensionSize",
-      "pad", "dynamicSlice", "dynamicUpdateSlice", "replicaId", "partitionId",
-      "setDimensionSize", "dynamicReshape", "dynamicPad", "dynamicIota",
+      "batchNormTraining", "batchNormGrad", "dynamicPad",
       "realDynamicSlice", "dynamicBroadcastInDim", "fft", "triangularSolve",
       "einsum", "unaryEinsum"};
   for (auto* s : names)
@@ -353,8 +357,37 @@ Node* prepare_node(Ctx* c, const std::string& op, const std::vector<Tensor*>& in
         break;
       }
       case K_RESHAPE: {
-        nin(1);
-        n->l0 = parse_int_list(find_attr(attrs, "shape", op), op);
+        if (spec.sub == 1) {
+          // setDimensionSize (src/rew/ops/shape.nim:325-355): shapes are
+          // static here, so the result is the operand
+          nin(2);
+          const int64_t dim = parse_int(find_attr(attrs, "dimension", op), op);
+          if (dim < 0 || dim >= ins[0]->shape.rank)
+            invalid("eager 'setDimensionSize': dimension out of range");
+          if (!dt_is_int(ins[1]->dt) || ins[1]->shape.rank != 0)
+            invalid("eager 'setDimensionSize': size must be an integer scalar");
+          n->kind = K_RESHAPE;
+          n->sub = 0;
+          n->n_in_keep = 1;
+          n->l0 = ins[0]->shape.vec();
+          outs.push_back({ins[0]->dt, ins[0]->shape});
+          break;
+        }
+        if (spec.sub == 2) {
+          // dynamicReshape (src/rew/ops/shape.nim:360-393) to its static
+          // result_shape; operand 1 (the shape vector) is not read
+          nin(2);
+          n->l0 = parse_int_list(find_attr(attrs, "result_shape", op), op);
+          if (!dt_is_int(ins[1]->dt) || ins[1]->shape.rank != 1 ||
+              ins[1]->shape.d[0] != (int64_t)n->l0.size())
+            invalid("eager 'dynamicReshape': output_shape must be an integer vector of length " +
+                    std::to_string(n->l0.size()));
+          n->sub = 0;
+          n->n_in_keep = 1;
+        } else {
+          nin(1);
+          n->l0 = parse_int_list(find_attr(attrs, "shape", op), op);
+        }
         Shape s(n->l0);
         for (auto d : n->l0)
           if (d < 0) invalid("eager 'reshape': negative dim");
@@ -455,9 +488,22 @@ Node* prepare_node(Ctx* c, const std::string& op, const std::vector<Tensor*>& in
         break;
       }
       case K_IOTA: {
-        nin(0);
+        if (spec.sub == 1) {
+          // dynamicIota (src/rew/ops/shape.nim:442-475) over its static
+          // result_shape; operand 0 (the shape vector) is not read
+          nin(1);
+          n->l0 = parse_int_list(find_attr(attrs, "result_shape", op), op);
+          if (!dt_is_int(ins[0]->dt) || ins[0]->shape.rank != 1 ||
+              ins[0]->shape.d[0] != (int64_t)n->l0.size())
+            invalid("eager 'dynamicIota': output_shape must be an integer vector of length " +
+                    std::to_string(n->l0.size()));
+          n->sub = 0;
+          n->n_in_keep = 0;
+        } else {
+          nin(0);
+          n->l0 = parse_int_list(find_attr(attrs, "shape", op), op);
+        }
         n->dt_attr = parse_dtype_attr(find_attr(attrs, "dtype", op), op);
-        n->l0 = parse_int_list(find_attr(attrs, "shape", op), op);
         n->i0 = parse_int(find_attr(attrs, "dimension", op), op);
         for (auto& kv : attrs)
           if (kv.first == "device") {
@@ -741,6 +787,116 @@ Node* prepare_node(Ctx* c, const std::string& op, const std::vector<Tensor*>& in
         outs.push_back({x->dt, xs});
         break;
       }
+      case K_CONST: {
+        if (spec.sub == 0) {
+          // getDimensionSize (src/rew/ops/shape.nim:108-128): int32 scalar
+          nin(1);
+          n->i0 = parse_int(find_attr(attrs, "dimension", op), op);
+          if (n->i0 < 0 || n->i0 >= ins[0]->shape.rank)
+            invalid("eager 'getDimensionSize': dimension out of range");
+          n->i0 = ins[0]->shape.d[n->i0];
+          if (n->i0 > INT32_MAX)
+            fail(REW_MI355X_ERR_UNSUPPORTED, "eager 'getDimensionSize': size above INT32_MAX");
+          n->n_in_keep = 0;
+          outs.push_back({kI32, Shape()});
+        } else {
+          // replicaId / partitionId (src/rew/ops/distributed.nim:11-35): one
+          // replica of one partition, so uint32 0
+          nin(0);
+          n->i0 = 0;
+          outs.push_back({kU32, Shape()});
+        }
+        break;
+      }
+      case K_WINDOW: {
+        Tensor* x = ins.empty() ? nullptr : ins[0];
+        const int sz = x ? dt_size(x->dt) : 0;
+        if (x && (x->dt == kI4 || x->dt == kU4 || x->dt == kNF4 ||
+                  (sz != 1 && sz != 2 && sz != 4 && sz != 8)))
+          fail(REW_MI355X_ERR_UNSUPPORTED,
+               std::string("eager '") + op + "': dtype " + dt_enum_name(x->dt) + " not supported");
+        auto starts = [&](size_t first) {
+          if (ins.size() != first + (size_t)x->shape.rank)
+            invalid("eager '" + op + "': start index count " +
+                    std::to_string((int64_t)ins.size() - (int64_t)first) +
+                    " must match operand rank " + std::to_string(x->shape.rank));
+          for (size_t i = first; i < ins.size(); ++i)
+            if (!dt_is_int(ins[i]->dt) || ins[i]->shape.rank != 0)
+              invalid("eager '" + op + "': start index #" + std::to_string(i - first) +
+                      " must be an integer scalar");
+        };
+        if (spec.sub == kWinPad) {
+          // stablehlo.pad (src/rew/ops/shape.nim:139-172, padOutputShape
+          // src/rew/stablehlo/ops.nim:807-824)
+          nin(2);
+          if (ins[1]->dt != x->dt || ins[1]->shape.rank != 0)
+            invalid("eager pad: paddingValue must be a scalar of the operand dtype");
+          n->l0 = parse_int_list(find_attr(attrs, "edge_padding_low", op), op);
+          n->l1 = parse_int_list(find_attr(attrs, "edge_padding_high", op), op);
+          n->l2 = parse_int_list(find_attr(attrs, "interior_padding", op), op);
+          const Shape& xs = x->shape;
+          if ((int)n->l0.size() != xs.rank || (int)n->l1.size() != xs.rank ||
+              (int)n->l2.size() != xs.rank)
+            invalid("eager pad: pad: padding arrays must match operand rank " +
+                    std::to_string(xs.rank));
+          Shape s;
+          s.rank = xs.rank;
+          for (int i = 0; i < xs.rank; ++i) {
+            if (n->l2[i] < 0)
+              invalid("eager pad: pad: interior padding at dim " + std::to_string(i) +
+                      " must be non-negative");
+            s.d[i] = xs.d[i] + n->l0[i] + n->l1[i] + std::max<int64_t>(xs.d[i] - 1, 0) * n->l2[i];
+            if (s.d[i] < 0)
+              invalid("eager pad: pad: result dimension " + std::to_string(i) + " is negative");
+          }
+          outs.push_back({x->dt, s});
+        } else if (spec.sub == kWinSlice) {
+          // stablehlo.dynamic_slice (src/rew/ops/shape.nim:213-250)
+          if (!x) invalid("eager 'dynamicSlice': expected an operand");
+          starts(1);
+          n->l0 = parse_int_list(find_attr(attrs, "slice_sizes", op), op);
+          if ((int)n->l0.size() != x->shape.rank)
+            invalid("eager 'dynamicSlice': slice_sizes length must match operand rank");
+          for (int i = 0; i < x->shape.rank; ++i)
+            if (n->l0[i] < 0 || n->l0[i] > x->shape.d[i])
+              invalid("eager 'dynamicSlice': slice size " + std::to_string(n->l0[i]) +
+                      " out of range for dim " + std::to_string(i));
+          outs.push_back({x->dt, Shape(n->l0)});
+        } else {
+          // stablehlo.dynamic_update_slice (src/rew/ops/shape.nim:251-290)
+          if (ins.size() < 2) invalid("eager 'dynamicUpdateSlice': expected operand and update");
+          Tensor* up = ins[1];
+          if (up->dt != x->dt) invalid("eager 'dynamicUpdateSlice': update dtype differs");
+          if (up->shape.rank != x->shape.rank)
+            invalid("eager 'dynamicUpdateSlice': update rank must match operand rank");
+          for (int i = 0; i < x->shape.rank; ++i)
+            if (up->shape.d[i] > x->shape.d[i])
+              invalid("eager 'dynamicUpdateSlice': update larger than the operand at dim " +
+                      std::to_string(i));
+          starts(2);
+          outs.push_back({x->dt, x->shape});
+        }
+        break;
+      }
+      case K_CHOLESKY: {
+        // stablehlo.cholesky (src/rew/ops/linalg.nim:177-202)
+        nin(1);
+        Tensor* x = ins[0];
+        if (!dt_is_float(x->dt)) invalid("eager 'cholesky': operand must be floating point");
+        if (x->shape.rank < 2 || x->shape.d[x->shape.rank - 1] != x->shape.d[x->shape.rank - 2])
+          invalid("eager 'cholesky': innermost matrix dimensions must be square");
+        if (x->dt != kF32 && x->dt != kF64)
+          fail(REW_MI355X_ERR_UNSUPPORTED, "eager 'cholesky': only float32 / float64");
+        if (x->shape.d[x->shape.rank - 1] > kCholMaxN)
+          fail(REW_MI355X_ERR_UNSUPPORTED, "eager 'cholesky': matrices above " +
+                                               std::to_string(kCholMaxN) + " x " +
+                                               std::to_string(kCholMaxN));
+        const std::string lw = strip(find_attr(attrs, "lower", op));
+        if (lw != "true" && lw != "false") invalid("eager 'cholesky': lower must be true or false");
+        n->i0 = lw == "true";
+        outs.push_back({x->dt, x->shape});
+        break;
+      }
       case K_DOT:
       case K_DOT_GENERAL: {
         nin(2);
@@ -836,6 +992,7 @@ Node* prepare_node(Ctx* c, const std::string& op, const std::vector<Tensor*>& in
 std::vector<Tensor*> commit_node(Ctx* c, Node* n, const std::vector<Tensor*>& ins,
                                  const std::vector<std::pair<int, Shape>>& outs) {
   n->in = ins;
+  if (n->n_in_keep >= 0 && (size_t)n->n_in_keep < ins.size()) n->in.resize(n->n_in_keep);
   std::vector<Tensor*> result;
   for (size_t i = 0; i < outs.size(); ++i) {
     Tensor* t = new_tensor(c, outs[i].first, outs[i].second);
@@ -845,7 +1002,7 @@ std::vector<Tensor*> commit_node(Ctx* c, Node* n, const std::vector<Tensor*>& in
     n->out.push_back(t);
     result.push_back(t);
   }
-  for (auto* t : ins) t->uses++;
+  for (auto* t : n->in) t->uses++;
   n->order = c->order_counter++;
   c->pending.push_back(n);
   c->stats.ops_recorded++;

@@ -121,6 +121,16 @@ struct PtrVisit {
     field(f, l.dst);
     field(f, l.src);
   }
+  void operator()(WindowArgs& a) {
+    field(f, a.x);
+    field(f, a.y);
+    field(f, a.out);
+    for (int d = 0; d < a.rank; ++d) field(f, a.start[d]);
+  }
+  void operator()(CholeskyArgs& a) {
+    field(f, a.x);
+    field(f, a.out);
+  }
 };
 
 template <class F>
@@ -153,6 +163,8 @@ struct Exec {
     for (int j = 0; j < 6; ++j) l.a.ptr[j] = l.tab.data() + (size_t)j * l.a.n;
     run_routed_ffn(c, l.a, l.scratch);
   }
+  void operator()(WindowArgs& a) { launch_window(a, c->stream); }
+  void operator()(CholeskyArgs& a) { launch_cholesky(a, c->stream); }
   void operator()(FillL& l) {
     if (l.bytes == 0) return;
     if (l.src)

@@ -54,7 +54,7 @@ struct FillL {
 
 using LaunchArgs = std::variant<EwL, ReduceL, GemmL, FlashArgs, RowNormArgs, SoftmaxArgs,
                                 RopeArgs, GatherArgs, ArgmaxArgs, TopkArgs, SortArgs,
-                                IndexMapL, MoeL, FillL>;
+                                IndexMapL, MoeL, FillL, WindowArgs, CholeskyArgs>;
 
 struct Launch {
   LaunchArgs args;

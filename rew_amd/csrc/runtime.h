@@ -59,6 +59,9 @@ enum Kind : int {
   K_TRANSPOSE, K_REVERSE, K_BROADCAST_TO, K_BROADCAST, K_SLICE, K_CONCAT,
   K_IOTA, K_COMPARE, K_SELECT, K_CLAMP, K_REDUCE, K_DOT_GENERAL, K_DOT,
   K_INDEX_SELECT, K_ARGMAX, K_TOPK, K_REDUCE_PRECISION, K_PAD, K_SORT, K_GATHER, K_SCATTER,
+  K_CONST,     // a scalar whose value the op fixes (getDimensionSize, replicaId, partitionId)
+  K_WINDOW,    // pad / dynamicSlice / dynamicUpdateSlice (sub: kWin*)
+  K_CHOLESKY,
   // composite kernels created by the planner (never recorded directly)
   K_COUNT
 };
@@ -74,6 +77,8 @@ struct Node {
   int64_t i0 = 0, i1 = 0, i2 = 0;
   int dt_attr = -1;
   int cmp = 0;
+  int n_in_keep = -1;       // >= 0: only the first n_in_keep operands are read
+                            // (the rest only fix static shapes)
   // planner scratch
   bool dead = false;
   bool done = false;

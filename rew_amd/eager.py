@@ -292,16 +292,17 @@ def fromHost(data, dtype: DType | None = None, shape: Sequence[int] | None = Non
                  np.dtype(np.float16): DType.FLOAT16, np.dtype(np.int8): DType.INT8,
                  np.dtype(np.uint8): DType.UINT8, np.dtype(np.int16): DType.INT16,
                  np.dtype(np.uint16): DType.UINT16, np.dtype(np.int64): DType.INT64,
-                 np.dtype(np.float64): DType.FLOAT64}.get(arr.dtype)
+                 np.dtype(np.float64): DType.FLOAT64,
+                 np.dtype(np.uint64): DType.UINT64}.get(arr.dtype)
         if dtype is None:
             raise TensorError(f"fromHost: unsupported host dtype {arr.dtype}")
     dtype = DType(dtype)
+    shp = tuple(arr.shape) if shape is None else tuple(shape)  # (0-d stays 0-d below)
     if dtype == DType.BFLOAT16 and arr.dtype != np.uint16:
         arr = f32_to_bf16_bits(arr.astype(np.float32))
     else:
         arr = arr.astype(_NP[dtype], copy=False)
     arr = np.ascontiguousarray(arr)
-    shp = tuple(arr.shape) if shape is None else tuple(shape)
     n = 1
     for s in shp:
         n *= s

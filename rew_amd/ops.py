@@ -472,3 +472,122 @@ def torchIndexSelect(operand: Tensor, index: Tensor, dim: int, batchDims: int) -
         raise TensorError("torchIndexSelect: index must be an integer tensor")
     return _one("torchIndexSelect", [operand, index], [("dim", str(dim)),
                                                         ("batch_dims", str(batchDims))])
+
+
+# ---- shape, dynamic and linear-algebra ops outside the configs -------------------------
+# src/rew/ops/shape.nim:108-475, ops/distributed.nim:11-35, ops/linalg.nim:177-202
+
+_INT_DTYPES = {DType.INT4, DType.INT8, DType.INT16, DType.INT32, DType.INT64, DType.UINT4,
+               DType.UINT8, DType.UINT16, DType.UINT32, DType.UINT64}
+
+
+def getDimensionSize(a: Tensor, dimension: int) -> Tensor:
+    if dimension < 0 or dimension >= len(a.shape):
+        raise TensorError(f"getDimensionSize: dimension {dimension} out of range for rank "
+                          f"{len(a.shape)}")
+    return _one("getDimensionSize", [a], [("dimension", str(dimension))])
+
+
+def pad(a: Tensor, paddingValue: Tensor, edgePaddingLow: Sequence[int],
+        edgePaddingHigh: Sequence[int], interiorPadding: Sequence[int]) -> Tensor:
+    if paddingValue.dtype != a.dtype or len(paddingValue.shape) != 0:
+        raise TensorError(f"pad: paddingValue must be scalar with dtype {a.dtype.rew_name}")
+    rank = len(a.shape)
+    if not (len(edgePaddingLow) == len(edgePaddingHigh) == len(interiorPadding) == rank):
+        raise TensorError(f"pad: padding arrays must match operand rank {rank}")
+    for i, d in enumerate(a.shape):
+        if interiorPadding[i] < 0:
+            raise TensorError(f"pad: interior padding at dim {i} must be non-negative")
+        if d + edgePaddingLow[i] + edgePaddingHigh[i] + max(d - 1, 0) * interiorPadding[i] < 0:
+            raise TensorError(f"pad: result dimension {i} is negative")
+    return _one("pad", [a, paddingValue], [("edge_padding_low", _nimseq(edgePaddingLow)),
+                                           ("edge_padding_high", _nimseq(edgePaddingHigh)),
+                                           ("interior_padding", _nimseq(interiorPadding))])
+
+
+def _start_indices(a: Tensor, startIndices: Sequence[Tensor], op: str):
+    if len(startIndices) != len(a.shape):
+        raise TensorError(f"{op}: start index count {len(startIndices)} must match operand "
+                          f"rank {len(a.shape)}")
+    for i, idx in enumerate(startIndices):
+        if idx.device != a.device:
+            raise TensorError(f"{op}: device mismatch")
+        if idx.dtype not in _INT_DTYPES or len(idx.shape) != 0:
+            raise TensorError(f"{op}: start index #{i} must be an integer scalar")
+
+
+def dynamicSlice(a: Tensor, startIndices: Sequence[Tensor], sliceSizes: Sequence[int]) -> Tensor:
+    _start_indices(a, startIndices, "dynamicSlice")
+    if len(sliceSizes) != len(a.shape):
+        raise TensorError(f"dynamicSlice: sliceSizes length {len(sliceSizes)} must match "
+                          f"operand rank {len(a.shape)}")
+    for i, s in enumerate(sliceSizes):
+        if s < 0 or s > a.shape[i]:
+            raise TensorError(f"dynamicSlice: slice size {s} out of range for dim {i}")
+    return _one("dynamicSlice", [a, *startIndices], [("slice_sizes", _nimseq(sliceSizes))])
+
+
+def dynamicUpdateSlice(a: Tensor, update: Tensor, startIndices: Sequence[Tensor]) -> Tensor:
+    if update.dtype != a.dtype:
+        raise TensorError("dynamicUpdateSlice: update dtype must match operand dtype")
+    if len(update.shape) != len(a.shape):
+        raise TensorError("dynamicUpdateSlice: update rank must match operand rank")
+    for i, (u, d) in enumerate(zip(update.shape, a.shape)):
+        if u > d:
+            raise TensorError(f"dynamicUpdateSlice: update dim {i} exceeds operand dim")
+    _start_indices(a, startIndices, "dynamicUpdateSlice")
+    return _one("dynamicUpdateSlice", [a, update, *startIndices])
+
+
+def replicaId(device: Device | None = None) -> Tensor:
+    return _one("replicaId", [], [("device", str(device or defaultDevice()))])
+
+
+def partitionId(device: Device | None = None) -> Tensor:
+    return _one("partitionId", [], [("device", str(device or defaultDevice()))])
+
+
+def setDimensionSize(a: Tensor, size: Tensor, dimension: int) -> Tensor:
+    if dimension < 0 or dimension >= len(a.shape):
+        raise TensorError(f"setDimensionSize: dimension {dimension} out of range for rank "
+                          f"{len(a.shape)}")
+    if size.dtype not in _INT_DTYPES or len(size.shape) != 0:
+        raise TensorError("setDimensionSize: size must be an integer scalar")
+    return _one("setDimensionSize", [a, size], [("dimension", str(dimension))])
+
+
+def dynamicReshape(a: Tensor, outputShape: Tensor, resultShape: Sequence[int]) -> Tensor:
+    if outputShape.dtype not in _INT_DTYPES or tuple(outputShape.shape) != (len(resultShape),):
+        raise TensorError(f"dynamicReshape: outputShape must be an integer vector of length "
+                          f"{len(resultShape)}")
+    if any(d < 0 for d in resultShape):
+        raise TensorError("dynamicReshape: result shape contains negative dim")
+    if int(np.prod(resultShape, dtype=np.int64)) != int(np.prod(a.shape, dtype=np.int64)):
+        raise TensorError("dynamicReshape: result element count does not match operand")
+    return _one("dynamicReshape", [a, outputShape], [("result_shape", _nimseq(resultShape))])
+
+
+def dynamicIota(dtype: DType, outputShape: Tensor, resultShape: Sequence[int],
+                dimension: int) -> Tensor:
+    if dtype == DType.BOOL:
+        raise TensorError("dynamicIota: bool dtype is not supported")
+    if outputShape.dtype not in _INT_DTYPES or tuple(outputShape.shape) != (len(resultShape),):
+        raise TensorError(f"dynamicIota: outputShape must be an integer vector of length "
+                          f"{len(resultShape)}")
+    if dimension < 0 or dimension >= len(resultShape):
+        raise TensorError(f"dynamicIota: dimension {dimension} out of range for rank "
+                          f"{len(resultShape)}")
+    return _one("dynamicIota", [outputShape], [("dtype", DType(dtype).enum_name),
+                                                ("result_shape", _nimseq(resultShape)),
+                                                ("dimension", str(dimension))])
+
+
+def cholesky(a: Tensor, lower: bool = True) -> Tensor:
+    if a.dtype not in (DType.FLOAT16, DType.BFLOAT16, DType.FLOAT32, DType.FLOAT64):
+        raise TensorError(f"cholesky: operand must be floating point, got {a.dtype.rew_name}")
+    if len(a.shape) < 2:
+        raise TensorError(f"cholesky: operand rank must be at least 2, got {len(a.shape)}")
+    if a.shape[-1] != a.shape[-2]:
+        raise TensorError(f"cholesky: innermost matrix dimensions must be square, got "
+                          f"{list(a.shape)}")
+    return _one("cholesky", [a], [("lower", "true" if lower else "false")])

@@ -76,3 +76,64 @@ def test_sort_order_is_stable_nan_last(oracle):
                for v in x]
         want = sorted(range(len(x)), key=lambda i: key[i])
         assert list(got) == want
+
+
+# ---- pad / dynamicSlice / dynamicUpdateSlice / cholesky --------------------------------
+
+def test_pad_known_answer(oracle):
+    """tests/teager_dispatch.nim:477-483: a 2x2 padded by one on every edge."""
+    x = np.array([[4, 2], [2, 3]], np.float32)
+    got = oracle.pad(x, 0.0, [1, 1], [1, 1], [0, 0])
+    np.testing.assert_array_equal(got.ravel(), [0, 0, 0, 0, 0, 4, 2, 0, 0, 2, 3, 0, 0, 0, 0, 0])
+
+
+def test_pad_against_numpy(oracle):
+    """Non-negative edges without interior padding are np.pad with a constant;
+    interior padding is the zero-stuffed array (x placed at every
+    (interior + 1)-th position) padded the same way; negative edges crop the
+    padded array."""
+    rs = np.random.default_rng(5)
+    x = rs.integers(-50, 50, (3, 4, 2)).astype(np.int32)
+    lo, hi = [1, 0, 2], [0, 3, 1]
+    np.testing.assert_array_equal(oracle.pad(x, -7, lo, hi, [0, 0, 0]),
+                                  np.pad(x, list(zip(lo, hi)), constant_values=-7))
+    it = [2, 0, 1]
+    stuffed = np.full([d + (d - 1) * i for d, i in zip(x.shape, it)], -7, np.int32)
+    stuffed[::3, :, ::2] = x
+    np.testing.assert_array_equal(oracle.pad(x, -7, lo, hi, it),
+                                  np.pad(stuffed, list(zip(lo, hi)), constant_values=-7))
+    full = oracle.pad(x, -7, [2, 2, 2], [2, 2, 2], it)
+    np.testing.assert_array_equal(oracle.pad(x, -7, [-1, 2, 0], [2, -2, -1], it),
+                                  full[3:, :-4, 2:-3])
+
+
+def test_dynamic_slice_and_update_known_answers(oracle):
+    """tests/teager_dispatch.nim:496-503, and the StableHLO spec examples of
+    clamped starts (start (-1, 3) on a 4x4 operand)."""
+    a = np.array([[1, 2], [3, 4]], np.float32)
+    np.testing.assert_array_equal(oracle.dynamic_slice(a, [0, 1], [2, 1]).ravel(), [2, 4])
+    np.testing.assert_array_equal(
+        oracle.dynamic_update_slice(a, np.array([[9]], np.float32), [0, 1]).ravel(), [1, 9, 3, 4])
+    op = np.array([[0, 0, 1, 1], [0, 0, 1, 1], [0, 0, 0, 0], [0, 0, 0, 0]], np.int64)
+    np.testing.assert_array_equal(oracle.dynamic_slice(op, [-1, 3], [2, 2]), [[1, 1], [1, 1]])
+    op2 = np.array([[1, 1, 0, 0], [1, 1, 0, 0], [1, 1, 1, 1], [1, 1, 1, 1]], np.int64)
+    np.testing.assert_array_equal(
+        oracle.dynamic_update_slice(op2, np.ones((2, 2), np.int64), [-1, 3]), np.ones((4, 4)))
+
+
+def test_cholesky_pins(oracle):
+    """tests/teager_dispatch.nim:466-470 ([[4,2],[2,3]] -> [2,0,1,sqrt 2]),
+    np.linalg.cholesky on random SPD batches, the upper form as the
+    transpose, and L L^T == A."""
+    got = oracle.cholesky(np.array([[4, 2], [2, 3]], np.float32))
+    np.testing.assert_allclose(got.ravel(), [2, 0, 1, np.sqrt(2)], rtol=1e-15)
+    rs = np.random.default_rng(9)
+    m = rs.standard_normal((3, 7, 7))
+    spd = m @ m.transpose(0, 2, 1) + 7 * np.eye(7)
+    L = oracle.cholesky(spd, True)
+    np.testing.assert_allclose(L, np.linalg.cholesky(spd), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(L @ L.transpose(0, 2, 1), spd, rtol=1e-12)
+    np.testing.assert_allclose(oracle.cholesky(spd, False), L.transpose(0, 2, 1), rtol=1e-12)
+    # only the referenced triangle is read
+    junk = spd + np.triu(np.full((7, 7), 1e3), 1)
+    np.testing.assert_allclose(oracle.cholesky(junk, True), L, rtol=1e-12)
