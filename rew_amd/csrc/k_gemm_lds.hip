@@ -62,6 +62,21 @@
 
 namespace rew {
 
+// 16-byte store of an epilogue's output (REW_GEMM_NT_STORE: nontemporal).
+#ifndef REW_GEMM_NT_STORE
+#define REW_GEMM_NT_STORE 0
+#endif
+__device__ __forceinline__ void st_c16(void* p, const uint4& v) {
+  if constexpr (REW_GEMM_NT_STORE) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, (u32x4*)p);
+  } else {
+    *(uint4*)p = v;
+  }
+}
+
+
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -690,7 +705,7 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
         for (int x = 0; x < 8; x += 2)
           out[x >> 1] = vm::bf16x2_bits(act[u][x] * vm::as_f(up[u][x >> 1] << 16),
                                         act[u][x + 1] * vm::as_f(up[u][x >> 1] & 0xffff0000u));
-        if (row_ok(row)) *(uint4*)(C + (row0 + row) * c_sm + n) = *(const uint4*)out;
+        if (row_ok(row)) st_c16(C + (row0 + row) * c_sm + n, *(const uint4*)out);
       }
     }
   } else if (epi == EPI_NONE || epi == EPI_BIAS) {
@@ -707,7 +722,7 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
 #pragma unroll
           for (int x = 0; x < 8; ++x) dh[x] = vm::bf16_bits(bf(dh[x]) + bf(bh[x]));
         }
-        if (row_ok(row)) *(uint4*)(C + (row0 + row) * c_sm + n) = dv;
+        if (row_ok(row)) st_c16(C + (row0 + row) * c_sm + n, dv);
       }
     }
   } else if (epi == EPI_BIAS_RES) {
@@ -734,7 +749,7 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
           const float y = vm::round_bf16(bf(dh[x]) + bf(bh[x]));
           out[x] = vm::bf16_bits(bf(rh[x]) + y);
         }
-        if (row_ok(row)) *(uint4*)(C + (row0 + row) * c_sm + n) = *(const uint4*)out;
+        if (row_ok(row)) st_c16(C + (row0 + row) * c_sm + n, *(const uint4*)out);
       }
     };
     fetch(0, ra);
@@ -820,7 +835,7 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
             out[2 * x] = vm::bf16_bits(t1 - t2);
             out[2 * x + 1] = vm::bf16_bits(t3 + t4);
           }
-          if (row_ok(row)) *(uint4*)(C + bq * ob + sq * os + oh) = *(const uint4*)out;
+          if (row_ok(row)) st_c16(C + bq * ob + sq * os + oh, *(const uint4*)out);
         }
       };
       fetch(0, ta);

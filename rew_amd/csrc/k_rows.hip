@@ -243,56 +243,77 @@ __device__ __forceinline__ float wg_row_sum(float v, float (&part)[2][4]) {
   return (part[SLOT][0] + part[SLOT][1]) + (part[SLOT][2] + part[SLOT][3]);
 }
 
-template <int XB, int YB, int CPL>
+template <int XB, int YB, int CPL, int R>  // R rows per workgroup (bytes in flight per CU)
 __global__ void __launch_bounds__(256) rmsnorm_wg_kernel(RowNormArgs a) {
   constexpr int EPC = 16 / XB;
-  __shared__ float part[2][4];
-  const int64_t row = blockIdx.x;
+  __shared__ float part[R][4];
   const int t = threadIdx.x;
-  const char* x = (const char*)a.x + row * a.x_rs * XB;
-  uint4 raw[CPL];
+  const int64_t row0 = (int64_t)blockIdx.x * R;
+  uint4 raw[R][CPL];
 #pragma unroll
-  for (int k = 0; k < CPL; ++k) raw[k] = *(const uint4*)(x + ((int64_t)k * 256 + t) * 16);
-  auto elem = [&](int k, int e) {
-    const uint32_t* w = (const uint32_t*)&raw[k];
+  for (int q = 0; q < R; ++q) {
+    // past the last row (rows % R != 0) the last row is read again, its
+    // results not stored
+    const int64_t row = row0 + q < a.rows ? row0 + q : a.rows - 1;
+    const char* x = (const char*)a.x + src_row(a, row) * a.x_rs * XB;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) raw[q][k] = *(const uint4*)(x + ((int64_t)k * 256 + t) * 16);
+  }
+  auto elem = [&](int q, int k, int e) {
+    const uint32_t* w = (const uint32_t*)&raw[q][k];
     return XB == 2 ? as_f((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16)) : as_f(w[e]);
   };
-  float ss = 0.0f;
+  float ss[R];
 #pragma unroll
-  for (int k = 0; k < CPL; ++k)
+  for (int q = 0; q < R; ++q) {
+    ss[q] = 0.0f;
 #pragma unroll
-    for (int e = 0; e < EPC; ++e) {
-      const float v = elem(k, e);
-      const float sq = v * v;
-      ss += sq;
-    }
-  ss = wg_row_sum<0>(ss, part);
-  const float mean = ss / a.divisor;
-  const float r = sqrtf(mean + a.eps);
-  const float rinv = 1.0f / r;  // x / r as x * (1 / r), as in rms_row
-  char* y = (char*)a.y + row * a.n * YB;
+    for (int k = 0; k < CPL; ++k)
 #pragma unroll
-  for (int k = 0; k < CPL; ++k) {
-    const int64_t j = ((int64_t)k * 256 + t) * EPC;
-    float out[EPC];
+      for (int e = 0; e < EPC; ++e) {
+        const float v = elem(q, k, e);
+        const float sq = v * v;
+        ss[q] += sq;
+      }
 #pragma unroll
-    for (int e = 0; e < EPC; e += 4) {
-      const float4 g = *(const float4*)(a.gamma + j + e);
-      out[e] = g.x * (elem(k, e) * rinv);
-      out[e + 1] = g.y * (elem(k, e + 1) * rinv);
-      out[e + 2] = g.z * (elem(k, e + 2) * rinv);
-      out[e + 3] = g.w * (elem(k, e + 3) * rinv);
-    }
-    if (YB == 2) {
-      uint32_t o[EPC / 2];
+    for (int m = 32; m >= 1; m >>= 1) ss[q] += __shfl_xor(ss[q], m, 64);
+    if ((t & 63) == 0) part[q][t >> 6] = ss[q];
+  }
+  __syncthreads();
 #pragma unroll
-      for (int e = 0; e < EPC; e += 2) o[e / 2] = bf16x2_bits(out[e], out[e + 1]);
-      if (EPC == 8) *(uint4*)(y + j * 2) = *(const uint4*)o;
-      else *(uint2*)(y + j * 2) = *(const uint2*)o;
-    } else {
+  for (int q = 0; q < R; ++q) {
+    const int64_t row = row0 + q;
+    if (row >= a.rows) break;
+    const float tot = (part[q][0] + part[q][1]) + (part[q][2] + part[q][3]);
+    const float mean = tot / a.divisor;
+    const float r = sqrtf(mean + a.eps);
+    const float rinv = 1.0f / r;  // x / r as x * (1 / r), as in rms_row
+    char* y = (char*)a.y + row * a.n * YB;
+    char* xo = a.xout ? (char*)a.xout + row * a.n * XB : nullptr;
 #pragma unroll
-      for (int e = 0; e < EPC; e += 4)
-        *(float4*)(y + (j + e) * 4) = make_float4(out[e], out[e + 1], out[e + 2], out[e + 3]);
+    for (int k = 0; k < CPL; ++k) {
+      const int64_t j = ((int64_t)k * 256 + t) * EPC;
+      if (xo) *(uint4*)(xo + j * XB) = raw[q][k];  // gather form: the gathered row itself
+      float out[EPC];
+#pragma unroll
+      for (int e = 0; e < EPC; e += 4) {
+        const float4 g = *(const float4*)(a.gamma + j + e);
+        out[e] = g.x * (elem(q, k, e) * rinv);
+        out[e + 1] = g.y * (elem(q, k, e + 1) * rinv);
+        out[e + 2] = g.z * (elem(q, k, e + 2) * rinv);
+        out[e + 3] = g.w * (elem(q, k, e + 3) * rinv);
+      }
+      if (YB == 2) {
+        uint32_t o[EPC / 2];
+#pragma unroll
+        for (int e = 0; e < EPC; e += 2) o[e / 2] = bf16x2_bits(out[e], out[e + 1]);
+        if (EPC == 8) *(uint4*)(y + j * 2) = *(const uint4*)o;
+        else *(uint2*)(y + j * 2) = *(const uint2*)o;
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPC; e += 4)
+          *(float4*)(y + (j + e) * 4) = make_float4(out[e], out[e + 1], out[e + 2], out[e + 3]);
+      }
     }
   }
 }
@@ -326,16 +347,20 @@ void launch_rmsnorm_rows(const RowNormArgs& a, hipStream_t stream) {
   const int64_t chunks = (a.n + epc - 1) / epc;  // 16-byte chunks per row
   const bool vec = a.n % epc == 0 && (a.x_rs * xb) % 16 == 0 && ((uintptr_t)a.x & 15) == 0 &&
                    ((uintptr_t)a.y & 15) == 0 && (a.n * yb) % 16 == 0 && chunks <= 64 * 16;
-  // fp32 rows of 1024, 2048 or 4096: a workgroup per row (43 us against 59 us
-  // for the wave kernel on [8192, 4096]); bf16 rows keep the pipelined waves
-  // (the same time on [8192, 4096])
-  if (vec && !a.ids && xb == 4 && rows_wg() && ((uintptr_t)a.gamma & 15) == 0 &&
-      a.rows < (1 << 30) && (chunks == 256 || chunks == 512 || chunks == 1024)) {
+  if (vec && rows_wg() && ((uintptr_t)a.gamma & 15) == 0 && a.rows < (1 << 30) &&
+      (chunks == 256 || chunks == 512 || chunks == 1024) &&
+      !(a.ids && !rmsnorm_gather_ok(a))) {
+    // one row per workgroup: two or four rows per workgroup measured 1-8 %
+    // slower on [8192, 4096] bf16 and f32
     const dim3 grid((unsigned)a.rows), block(256);
-#define REW_RMS(XB, YB, CPL) hipLaunchKernelGGL((rmsnorm_wg_kernel<XB, YB, CPL>), grid, block, 0, stream, a)
+#define REW_RMS(XB, YB, CPL) \
+    hipLaunchKernelGGL((rmsnorm_wg_kernel<XB, YB, CPL, 1>), grid, block, 0, stream, a)
 #define REW_RMS_CPL(XB, YB) \
-    if (chunks == 256) REW_RMS(XB, YB, 1); else if (chunks == 512) REW_RMS(XB, YB, 2); else REW_RMS(XB, YB, 4)
-    if (yb == 2) { REW_RMS_CPL(4, 2); }
+    if (chunks == 256) { REW_RMS(XB, YB, 1); } else if (chunks == 512) { REW_RMS(XB, YB, 2); } \
+    else { REW_RMS(XB, YB, 4); }
+    if (xb == 2 && yb == 2) { REW_RMS_CPL(2, 2); }
+    else if (xb == 2) { REW_RMS_CPL(2, 4); }
+    else if (yb == 2) { REW_RMS_CPL(4, 2); }
     else { REW_RMS_CPL(4, 4); }
 #undef REW_RMS_CPL
 #undef REW_RMS
