@@ -1332,6 +1332,27 @@ class Translator {
       reduce(o);
     } else if (n == "stablehlo.sort") {
       sort(o, index);
+    } else if (n == "stablehlo.pad") {
+      // rew's generic form (src/rew/stablehlo/text.nim:589-622)
+      need_args(o, 2);
+      const std::string* lo = attr_raw(o, "edge_padding_low");
+      const std::string* hi = attr_raw(o, "edge_padding_high");
+      const std::string* in = attr_raw(o, "interior_padding");
+      if (!lo || !hi || !in) fail_at(o, "missing padding attributes");
+      one(o, "pad", o.arg,
+          {{"edge_padding_low", ints(i64_array(*lo, who_))},
+           {"edge_padding_high", ints(i64_array(*hi, who_))},
+           {"interior_padding", ints(i64_array(*in, who_))}});
+    } else if (n == "stablehlo.dynamic_slice") {
+      // (src/rew/stablehlo/text.nim:645-669)
+      if (o.arg.size() < 2 || o.res_ty.size() != 1) fail_at(o, "malformed dynamic_slice");
+      const std::string* ss = attr_raw(o, "slice_sizes");
+      if (!ss) fail_at(o, "missing slice_sizes");
+      one(o, "dynamicSlice", o.arg, {{"slice_sizes", ints(i64_array(*ss, who_))}});
+    } else if (n == "stablehlo.dynamic_update_slice") {
+      // (src/rew/stablehlo/text.nim:671-690)
+      if (o.arg.size() < 3 || o.res_ty.size() != 1) fail_at(o, "malformed dynamic_update_slice");
+      one(o, "dynamicUpdateSlice", o.arg, {});
     } else if (n == "stablehlo.gather") {
       gather(o);
     } else if (n == "stablehlo.scatter") {

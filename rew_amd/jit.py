@@ -319,6 +319,26 @@ def traceOp(op: str, operands: Sequence[Tensor], attrs: Sequence[tuple]) -> list
         ctx.lines.append(f"    %v{r.traceId} = stablehlo.slice %v{x.traceId} [{rng}] : "
                          f"({_ty(x.dtype, x.shape)}) -> {_ty(x.dtype, shape)}")
         return [r]
+    if op in ("pad", "dynamicSlice", "dynamicUpdateSlice"):
+        # rew's generic forms (src/rew/stablehlo/text.nim:589-690)
+        arr = lambda xs: "array<i64: " + ", ".join(str(int(v)) for v in xs) + ">"
+        args = ", ".join(f"%v{t.traceId}" for t in operands)
+        if op == "pad":
+            lo, hi, it = (_ints(a[k]) for k in ("edge_padding_low", "edge_padding_high",
+                                                "interior_padding"))
+            shape = [d + l + h + max(d - 1, 0) * i for d, l, h, i in zip(x.shape, lo, hi, it)]
+            attrs_s = (f" {{edge_padding_low = {arr(lo)}, edge_padding_high = {arr(hi)}, "
+                       f"interior_padding = {arr(it)}}}")
+            mn = "pad"
+        elif op == "dynamicSlice":
+            shape = _ints(a["slice_sizes"])
+            attrs_s, mn = f" {{slice_sizes = {arr(shape)}}}", "dynamic_slice"
+        else:
+            shape, attrs_s, mn = list(x.shape), "", "dynamic_update_slice"
+        r = ctx.value(x.dtype, shape)
+        ctx.lines.append(f"    %v{r.traceId} = \"stablehlo.{mn}\"({args}){attrs_s} : "
+                         f"{_sig(list(operands), _ty(x.dtype, shape))}")
+        return [r]
     if op == "concat":
         d = int(a["dimension"])
         shape = list(x.shape)

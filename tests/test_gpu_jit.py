@@ -288,3 +288,29 @@ def test_scatter_eager_and_jit_against_oracle(gpu, oracle, op, dt):
     (jitted,) = J.jit(lambda a: O.scatter([a[0]], a[1], [a[2]], dims, op),
                       f"scatter_{op}_{int(dt)}").call([xt, it, ut])
     np.testing.assert_array_equal(rd(jitted), want)
+
+
+def test_pad_and_dynamic_slices_eager_and_jit(gpu, oracle):
+    """stablehlo.pad / dynamic_slice / dynamic_update_slice in rew's generic
+    text form (src/rew/stablehlo/text.nim:589-690) equal the eager ops and
+    the oracle bit for bit, the start indices passed as module inputs."""
+    rs = np.random.default_rng(31)
+    x = rs.standard_normal((6, 9)).astype(np.float32)
+    u = rs.standard_normal((2, 4)).astype(np.float32)
+    xt, ut, vt = E.fromHost(x), E.fromHost(u), E.fromHost(np.float32(-2.0))
+    s0, s1 = E.fromHost(np.int32(5)), E.fromHost(np.int32(-3))   # both clamp
+
+    def fn(a):
+        p = O.pad(a[0], a[2], [1, -1], [2, 0], [1, 2])
+        d = O.dynamicSlice(a[0], [a[3], a[4]], [3, 4])
+        w = O.dynamicUpdateSlice(a[0], a[1], [a[3], a[4]])
+        return [p, d, w]
+
+    eager = [E.toHost(t) for t in fn([xt, ut, vt, s0, s1])]
+    jitted = [E.toHost(t) for t in J.jit(fn, "pad_dslice").call([xt, ut, vt, s0, s1])]
+    want = [oracle.pad(x, np.float32(-2.0), [1, -1], [2, 0], [1, 2]),
+            oracle.dynamic_slice(x, [5, -3], [3, 4]),
+            oracle.dynamic_update_slice(x, u, [5, -3])]
+    for e, j, w in zip(eager, jitted, want):
+        np.testing.assert_array_equal(e, w)
+        np.testing.assert_array_equal(j, w)

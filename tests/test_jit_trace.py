@@ -239,3 +239,21 @@ def test_moe_traces_with_parameters_as_arguments():
     assert t.count('"stablehlo.sort"') == 2
     assert t.count("stablehlo.dot_general") == 1 + 3 * (S + E_)
     assert t.rstrip().endswith("}")
+
+
+def test_emit_pad_and_dynamic_slices():
+    """The generic forms of rew's emitter (src/rew/stablehlo/text.nim:589-690,
+    arrays rendered by renderI64Array, text.nim:123-130)."""
+    def fn(a):
+        return [O.pad(a[0], a[1], [1, 0], [0, 2], [1, 0]),
+                O.dynamicSlice(a[0], [a[2], a[2]], [1, 2]),
+                O.dynamicUpdateSlice(a[0], a[3], [a[2], a[2]])]
+    text = traced(fn, [ph(DType.FLOAT32, [2, 3]), ph(DType.FLOAT32, []),
+                       ph(DType.INT32, []), ph(DType.FLOAT32, [1, 1])])
+    assert ('"stablehlo.pad"(%v1, %v2) {edge_padding_low = array<i64: 1, 0>, '
+            'edge_padding_high = array<i64: 0, 2>, interior_padding = array<i64: 1, 0>} : '
+            '(tensor<2x3xf32>, tensor<f32>) -> tensor<4x5xf32>') in text
+    assert ('"stablehlo.dynamic_slice"(%v1, %v3, %v3) {slice_sizes = array<i64: 1, 2>} : '
+            '(tensor<2x3xf32>, tensor<i32>, tensor<i32>) -> tensor<1x2xf32>') in text
+    assert ('"stablehlo.dynamic_update_slice"(%v1, %v4, %v3, %v3) : (tensor<2x3xf32>, '
+            'tensor<1x1xf32>, tensor<i32>, tensor<i32>) -> tensor<2x3xf32>') in text
