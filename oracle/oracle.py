@@ -328,6 +328,43 @@ def cholesky(a: np.ndarray, lower: bool = True) -> np.ndarray:
     return out
 
 
+def _bn_view(x, fi):
+    # [outer, C, inner] view with the feature dim in the middle
+    x = np.asarray(x, np.float64)
+    return x.reshape(int(np.prod(x.shape[:fi], dtype=np.int64)), x.shape[fi], -1)
+
+
+def batch_norm_inference(x, scale, offset, mean, var, eps, fi):
+    """stablehlo.batch_norm_inference (src/rew/ops/normalization.nim:87-118), float64:
+    scale (x - mean) / sqrt(var + eps) + offset along feature dim fi."""
+    v = _bn_view(x, fi)
+    b = lambda t: np.asarray(t, np.float64)[None, :, None]
+    return (b(scale) * ((v - b(mean)) / np.sqrt(b(var) + eps)) + b(offset)).reshape(np.shape(x))
+
+
+def batch_norm_training(x, scale, offset, eps, fi):
+    """stablehlo.batch_norm_training (normalization.nim:120-162): the batch mean and
+    the (biased) batch variance per feature, then the inference formula."""
+    v = _bn_view(x, fi)
+    mean = v.mean(axis=(0, 2))
+    var = ((v - mean[None, :, None]) ** 2).mean(axis=(0, 2))
+    return batch_norm_inference(x, scale, offset, mean, var, eps, fi), mean, var
+
+
+def batch_norm_grad(x, scale, mean, var, dy, eps, fi):
+    """stablehlo.batch_norm_grad (normalization.nim:164-205): the gradient of
+    sum(dy * batch_norm_training(x)) with mean and var the batch statistics."""
+    v, g = _bn_view(x, fi), _bn_view(dy, fi)
+    n = v.shape[0] * v.shape[2]
+    b = lambda t: np.asarray(t, np.float64)[None, :, None]
+    std = np.sqrt(b(var) + eps)
+    xn = (v - b(mean)) / std
+    d_off = g.sum(axis=(0, 2))
+    d_sc = (g * xn).sum(axis=(0, 2))
+    dx = b(scale) / std * (g - b(d_off) / n - xn * b(d_sc) / n)
+    return dx.reshape(np.shape(x)), d_sc, d_off
+
+
 # ---- composites ------------------------------------------------------------------------
 
 def softmax_rows(x: np.ndarray) -> np.ndarray:

@@ -346,4 +346,102 @@ void launch_cholesky(const CholeskyArgs& a, hipStream_t stream) {
   REW_HIP(hipGetLastError());
 }
 
+// ---- batch norm ----------------------------------------------------------------------
+
+namespace {
+
+template <typename T>
+__device__ __forceinline__ T bn_norm(T x, T m, T v, double eps) {
+  return (x - m) / sqrt(v + (T)eps);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) bn_inference_kernel(BatchNormArgs a) {
+  const T *x = (const T*)a.x, *sc = (const T*)a.scale, *of = (const T*)a.offset;
+  const T *mu = (const T*)a.mean, *va = (const T*)a.var;
+  T* y = (T*)a.out0;
+  const int64_t total = a.outer * a.C * a.inner;
+  const int64_t step = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += step) {
+    const int64_t c = (t / a.inner) % a.C;
+    y[t] = sc[c] * bn_norm<T>(x[t], mu[c], va[c], a.eps) + of[c];
+  }
+}
+
+// Workgroup sum of v (fixed tree: wave butterfly, then the four wave sums).
+template <typename T>
+__device__ __forceinline__ T bn_block_sum(T v, T* part) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  __syncthreads();  // part may still be read from the previous sum
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (part[0] + part[1]) + (part[2] + part[3]);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) bn_feature_kernel(BatchNormArgs a) {
+  __shared__ T part[4];
+  const int64_t c = blockIdx.x;
+  const int64_t n = a.outer * a.inner;
+  const T *x = (const T*)a.x, *sc = (const T*)a.scale;
+  auto at = [&](int64_t i) { return (i / a.inner) * a.C * a.inner + c * a.inner + i % a.inner; };
+  if (a.mode == kBnTraining) {
+    const T* of = (const T*)a.offset;
+    T s = 0;
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) s += x[at(i)];
+    const T mean = bn_block_sum<T>(s, part) / (T)n;
+    T q = 0;
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+      const T d = x[at(i)] - mean;
+      q += d * d;
+    }
+    const T var = bn_block_sum<T>(q, part) / (T)n;
+    if (threadIdx.x == 0) {
+      ((T*)a.out1)[c] = mean;
+      ((T*)a.out2)[c] = var;
+    }
+    T* y = (T*)a.out0;
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x)
+      y[at(i)] = sc[c] * bn_norm<T>(x[at(i)], mean, var, a.eps) + of[c];
+  } else {
+    const T *dy = (const T*)a.dy, mean = ((const T*)a.mean)[c], var = ((const T*)a.var)[c];
+    T sg = 0, sgx = 0;
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+      const T g = dy[at(i)];
+      sg += g;
+      sgx += g * bn_norm<T>(x[at(i)], mean, var, a.eps);
+    }
+    const T d_off = bn_block_sum<T>(sg, part);
+    const T d_sc = bn_block_sum<T>(sgx, part);
+    if (threadIdx.x == 0) {
+      ((T*)a.out1)[c] = d_sc;
+      ((T*)a.out2)[c] = d_off;
+    }
+    const T stddev = sqrt(var + (T)a.eps);
+    T* dx = (T*)a.out0;
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+      const T xn = bn_norm<T>(x[at(i)], mean, var, a.eps);
+      dx[at(i)] = sc[c] / stddev * (dy[at(i)] - d_off / (T)n - xn * d_sc / (T)n);
+    }
+  }
+}
+
+}  // namespace
+
+void launch_batchnorm(const BatchNormArgs& a, hipStream_t stream) {
+  const int64_t total = a.outer * a.C * a.inner;
+  if (total == 0) return;
+  if (a.mode == kBnInference) {
+    const unsigned grid = index_map_grid(total);
+    if (a.f64) hipLaunchKernelGGL(bn_inference_kernel<double>, dim3(grid), dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL(bn_inference_kernel<float>, dim3(grid), dim3(256), 0, stream, a);
+  } else {
+    if (a.C > 0x7fffffff) fail(REW_MI355X_ERR_INVALID, "internal: batch norm launch outside its limits");
+    if (a.f64) hipLaunchKernelGGL(bn_feature_kernel<double>, dim3((unsigned)a.C), dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL(bn_feature_kernel<float>, dim3((unsigned)a.C), dim3(256), 0, stream, a);
+  }
+  REW_HIP(hipGetLastError());
+}
+
 }  // namespace rew

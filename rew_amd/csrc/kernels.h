@@ -243,6 +243,26 @@ struct CholeskyArgs {
   int f64, lower;
 };
 void launch_cholesky(const CholeskyArgs& a, hipStream_t stream);
+
+// ---- batch norm (k_gather.hip) -------------------------------------------------------
+// stablehlo.batch_norm_{inference,training,grad} over x viewed as dense
+// [outer, C, inner] (C at feature_index), f32 or f64, N = outer inner:
+//   inference: y = scale (x - mean) / sqrt(var + eps) + offset   (out0)
+//   training:  mean = sum x / N, var = sum (x - mean)^2 / N (out1, out2),
+//              then y as inference                                (out0)
+//   grad:      xn = (x - mean) / sqrt(var + eps); d_offset = sum dy (out2),
+//              d_scale = sum dy xn (out1), dx = scale / sqrt(var + eps)
+//              (dy - d_offset / N - xn d_scale / N)               (out0)
+// Inference runs a thread per element, the others a workgroup per feature.
+enum { kBnInference = 0, kBnTraining = 1, kBnGrad = 2 };
+struct BatchNormArgs {
+  int mode, f64;
+  const void *x, *scale, *offset, *mean, *var, *dy;
+  void *out0, *out1, *out2;
+  int64_t outer, C, inner;
+  double eps;
+};
+void launch_batchnorm(const BatchNormArgs& a, hipStream_t stream);
 void launch_scatter(const IndexMapArgs& g, hipStream_t stream);
 
 // ---- argmax / topK (k_select.hip) ----------------------------------------------

@@ -344,6 +344,7 @@ struct Lower {
   void emit_index_map(Node* n);
   void emit_window(Node* n);
   void emit_cholesky(Node* n);
+  void emit_batchnorm(Node* n);
   // Materialize `t` (any kind) into a fresh dense tensor whose shape is the
   // permutation `perm` of t's shape.
   Tensor* emit_permuted_copy(Tensor* t, const std::vector<int>& perm);
@@ -1043,6 +1044,7 @@ void Lower::emit_anchor(Node* n) {
     case K_SCATTER: emit_index_map(n); break;
     case K_WINDOW: emit_window(n); break;
     case K_CHOLESKY: emit_cholesky(n); break;
+    case K_BATCHNORM: emit_batchnorm(n); break;
     case K_BITCAST: {
       Tensor* x = n->in[0];
       ensure_mat(x);
@@ -2869,6 +2871,47 @@ void Lower::emit_cholesky(Node* n) {
   Launch L{a};
   if (c->profiling)
     L.name = "cholesky{" + std::to_string(a.batch) + "x" + std::to_string(a.n) + "}";
+  run_launch(c, std::move(L));
+}
+
+// batch norm: operands in rew's order (inference: x, scale, offset, mean,
+// var; training: x, scale, offset; grad: x, scale, mean, var, dy).
+void Lower::emit_batchnorm(Node* n) {
+  for (Tensor* t : n->in) ensure_mat(t);
+  for (Tensor* t : n->out) tensor_alloc(t);
+  BatchNormArgs a;
+  std::memset(&a, 0, sizeof a);
+  Tensor* x = n->in[0];
+  a.mode = n->sub;
+  a.f64 = x->dt == kF64;
+  std::memcpy(&a.eps, &n->i1, sizeof a.eps);
+  const int fi = (int)n->i0;
+  a.outer = 1;
+  a.inner = 1;
+  for (int d = 0; d < fi; ++d) a.outer *= x->shape.d[d];
+  for (int d = fi + 1; d < x->shape.rank; ++d) a.inner *= x->shape.d[d];
+  a.C = x->shape.d[fi];
+  a.x = x->data();
+  a.scale = n->in[1]->data();
+  if (a.mode == kBnInference) {
+    a.offset = n->in[2]->data();
+    a.mean = n->in[3]->data();
+    a.var = n->in[4]->data();
+  } else if (a.mode == kBnTraining) {
+    a.offset = n->in[2]->data();
+  } else {
+    a.mean = n->in[2]->data();
+    a.var = n->in[3]->data();
+    a.dy = n->in[4]->data();
+  }
+  a.out0 = n->out[0]->data();
+  if (n->out.size() == 3) {
+    a.out1 = n->out[1]->data();
+    a.out2 = n->out[2]->data();
+  }
+  Launch L{a};
+  if (c->profiling) L.name = n->name + "{" + std::to_string(a.outer) + "x" + std::to_string(a.C) +
+                             "x" + std::to_string(a.inner) + "}";
   run_launch(c, std::move(L));
 }
 

@@ -105,6 +105,9 @@ static const std::unordered_map<std::string, OpSpec>& op_table() {
       {"getDimensionSize", {K_CONST, 0}}, {"replicaId", {K_CONST, 1}},
       {"partitionId", {K_CONST, 1}}, {"setDimensionSize", {K_RESHAPE, 1}},
       {"dynamicReshape", {K_RESHAPE, 2}}, {"dynamicIota", {K_IOTA, 1}},
+      {"batchNormInference", {K_BATCHNORM, kBnInference}},
+      {"batchNormTraining", {K_BATCHNORM, kBnTraining}},
+      {"batchNormGrad", {K_BATCHNORM, kBnGrad}},
   };
   return t;
 }
@@ -113,8 +116,7 @@ static const std::unordered_map<std::string, OpSpec>& op_table() {
 // does not implement natively.
 static bool known_but_unimplemented(const std::string& n) {
   static const char* names[] = {
-      "complex", "real", "imag", "conv2d", "maxPool2d", "batchNormInference",
-      "batchNormTraining", "batchNormGrad", "dynamicPad",
+      "complex", "real", "imag", "conv2d", "maxPool2d", "dynamicPad",
       "realDynamicSlice", "dynamicBroadcastInDim", "fft", "triangularSolve",
       "einsum", "unaryEinsum"};
   for (auto* s : names)
@@ -875,6 +877,42 @@ Node* prepare_node(Ctx* c, const std::string& op, const std::vector<Tensor*>& in
                       std::to_string(i));
           starts(2);
           outs.push_back({x->dt, x->shape});
+        }
+        break;
+      }
+      case K_BATCHNORM: {
+        // stablehlo.batch_norm_* (src/rew/ops/normalization.nim:40-205; output
+        // shapes and dtypes src/rew/eager.nim:1262-1285)
+        nin(spec.sub == kBnTraining ? 3 : 5);
+        Tensor* x = ins[0];
+        if (!dt_is_float(x->dt)) invalid("eager '" + op + "': operand must be floating point");
+        if (x->dt != kF32 && x->dt != kF64)
+          fail(REW_MI355X_ERR_UNSUPPORTED, "eager '" + op + "': only float32 / float64");
+        n->i0 = parse_int(find_attr(attrs, "feature_index", op), op);
+        if (n->i0 < 0 || n->i0 >= x->shape.rank)
+          invalid("eager '" + op + "': feature_index " + std::to_string(n->i0) +
+                  " out of range for rank " + std::to_string(x->shape.rank));
+        const std::string es = strip(find_attr(attrs, "epsilon", op));
+        char* end = nullptr;
+        const double e = std::strtod(es.c_str(), &end);
+        if (es.empty() || !end || *end) invalid("eager '" + op + "': malformed epsilon '" + es + "'");
+        const double eps = (double)(float)e;  // an f32 attribute
+        std::memcpy(&n->i1, &eps, sizeof eps);
+        const int64_t C = x->shape.d[n->i0];
+        const size_t dy = spec.sub == kBnGrad ? 4 : 0;
+        for (size_t i = 1; i < ins.size(); ++i) {
+          if (ins[i]->dt != x->dt) invalid("eager '" + op + "': operand dtypes differ");
+          if (i == dy) {
+            if (!(ins[i]->shape == x->shape)) invalid("eager '" + op + "': gradOutput shape differs");
+          } else if (ins[i]->shape.rank != 1 || ins[i]->shape.d[0] != C) {
+            invalid("eager '" + op + "': feature operand " + std::to_string(i) +
+                    " must have shape [" + std::to_string(C) + "]");
+          }
+        }
+        outs.push_back({x->dt, x->shape});
+        if (spec.sub != kBnInference) {
+          outs.push_back({x->dt, Shape(std::vector<int64_t>{C})});
+          outs.push_back({x->dt, Shape(std::vector<int64_t>{C})});
         }
         break;
       }

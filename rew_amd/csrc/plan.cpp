@@ -131,6 +131,10 @@ struct PtrVisit {
     field(f, a.x);
     field(f, a.out);
   }
+  void operator()(BatchNormArgs& a) {
+    for (const void** p : {&a.x, &a.scale, &a.offset, &a.mean, &a.var, &a.dy}) field(f, *p);
+    for (void** p : {&a.out0, &a.out1, &a.out2}) field(f, *p);
+  }
 };
 
 template <class F>
@@ -165,6 +169,7 @@ struct Exec {
   }
   void operator()(WindowArgs& a) { launch_window(a, c->stream); }
   void operator()(CholeskyArgs& a) { launch_cholesky(a, c->stream); }
+  void operator()(BatchNormArgs& a) { launch_batchnorm(a, c->stream); }
   void operator()(FillL& l) {
     if (l.bytes == 0) return;
     if (l.src)

@@ -54,7 +54,8 @@ struct FillL {
 
 using LaunchArgs = std::variant<EwL, ReduceL, GemmL, FlashArgs, RowNormArgs, SoftmaxArgs,
                                 RopeArgs, GatherArgs, ArgmaxArgs, TopkArgs, SortArgs,
-                                IndexMapL, MoeL, FillL, WindowArgs, CholeskyArgs>;
+                                IndexMapL, MoeL, FillL, WindowArgs, CholeskyArgs,
+                                BatchNormArgs>;
 
 struct Launch {
   LaunchArgs args;

@@ -591,3 +591,63 @@ def cholesky(a: Tensor, lower: bool = True) -> Tensor:
         raise TensorError(f"cholesky: innermost matrix dimensions must be square, got "
                           f"{list(a.shape)}")
     return _one("cholesky", [a], [("lower", "true" if lower else "false")])
+
+
+# ---- batch norm (src/rew/ops/normalization.nim:40-205) ----------------------------------
+
+def _bn_feature_index(operand: Tensor, featureIndex: int, op: str) -> list:
+    if operand.dtype not in (DType.FLOAT16, DType.BFLOAT16, DType.FLOAT32, DType.FLOAT64):
+        raise TensorError(f"{op}: operand must be floating point, got {operand.dtype.rew_name}")
+    if featureIndex < 0 or featureIndex >= len(operand.shape):
+        raise TensorError(f"{op}: featureIndex {featureIndex} out of range for rank "
+                          f"{len(operand.shape)}")
+    return [operand.shape[featureIndex]]
+
+
+def _bn_feature(operand: Tensor, t: Tensor, name: str, fshape, op: str):
+    if t.device != operand.device:
+        raise TensorError(f"{op}: device mismatch")
+    if t.dtype != operand.dtype:
+        raise TensorError(f"{op}: {name} dtype {t.dtype.rew_name} differs from operand dtype "
+                          f"{operand.dtype.rew_name}")
+    if list(t.shape) != list(fshape):
+        raise TensorError(f"{op}: {name} shape {list(t.shape)} must be {list(fshape)}")
+
+
+def _bn_attrs(epsilon: float, featureIndex: int):
+    return [("epsilon", repr(float(np.float32(epsilon)))), ("feature_index", str(featureIndex))]
+
+
+def batchNormInference(operand: Tensor, scale: Tensor, offset: Tensor, mean: Tensor,
+                       variance: Tensor, epsilon: float, featureIndex: int) -> Tensor:
+    fs = _bn_feature_index(operand, featureIndex, "batchNormInference")
+    for t, nm in ((scale, "scale"), (offset, "offset"), (mean, "mean"), (variance, "variance")):
+        _bn_feature(operand, t, nm, fs, "batchNormInference")
+    return _one("batchNormInference", [operand, scale, offset, mean, variance],
+                _bn_attrs(epsilon, featureIndex))
+
+
+def batchNormTraining(operand: Tensor, scale: Tensor, offset: Tensor, epsilon: float,
+                      featureIndex: int):
+    """(output, batchMean, batchVar)."""
+    fs = _bn_feature_index(operand, featureIndex, "batchNormTraining")
+    for t, nm in ((scale, "scale"), (offset, "offset")):
+        _bn_feature(operand, t, nm, fs, "batchNormTraining")
+    outs = dispatchEager("batchNormTraining", [operand, scale, offset],
+                         _bn_attrs(epsilon, featureIndex))
+    assert len(outs) == 3, "batchNormTraining: eager backend returned wrong arity"
+    return tuple(outs)
+
+
+def batchNormGrad(operand: Tensor, scale: Tensor, mean: Tensor, variance: Tensor,
+                  gradOutput: Tensor, epsilon: float, featureIndex: int):
+    """(gradOperand, gradScale, gradOffset)."""
+    fs = _bn_feature_index(operand, featureIndex, "batchNormGrad")
+    if gradOutput.dtype != operand.dtype or list(gradOutput.shape) != list(operand.shape):
+        raise TensorError("batchNormGrad: gradOutput type must match operand type")
+    for t, nm in ((scale, "scale"), (mean, "mean"), (variance, "variance")):
+        _bn_feature(operand, t, nm, fs, "batchNormGrad")
+    outs = dispatchEager("batchNormGrad", [operand, scale, mean, variance, gradOutput],
+                         _bn_attrs(epsilon, featureIndex))
+    assert len(outs) == 3, "batchNormGrad: eager backend returned wrong arity"
+    return tuple(outs)

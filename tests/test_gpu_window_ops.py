@@ -178,3 +178,52 @@ def test_validation_errors(gpu):
                          ("interior_padding", "[-1,0]")])
     with pytest.raises(E.EagerError, match="not implemented natively"):
         E.dispatchEager("fft", [x], [])
+
+
+def test_batch_norm_known_answers(mode):
+    """tests/teager_dispatch.nim:426-463."""
+    a = dev(np.array([1, 2, 3, 4], np.float32))
+    one, zero = dev(np.ones(4, np.float32)), dev(np.zeros(4, np.float32))
+    r = O.batchNormInference(a, one, zero, one, one, 0.0, 0)
+    assert r.dtype == DType.FLOAT32
+    np.testing.assert_array_equal(host(r), [0, 1, 2, 3])
+    x = dev(np.array([[1, 2], [3, 4]], np.float32))
+    o2, z2 = dev(np.ones(2, np.float32)), dev(np.zeros(2, np.float32))
+    y, m, v = O.batchNormTraining(x, o2, z2, 0.0, 1)
+    assert tuple(y.shape) == (2, 2) and tuple(m.shape) == (2,) and tuple(v.shape) == (2,)
+    np.testing.assert_allclose(host(y).ravel(), [-1, -1, 1, 1], rtol=1e-6)
+    np.testing.assert_array_equal(host(m), [2, 3])
+    np.testing.assert_array_equal(host(v), [1, 1])
+    g = dev(np.full((2, 2), 0.1, np.float32))
+    dx, ds, do = O.batchNormGrad(x, o2, dev(np.array([2, 3], np.float32)), o2, g, 0.0, 1)
+    np.testing.assert_allclose(host(dx).ravel(), 0, atol=1e-7)
+    np.testing.assert_allclose(host(ds), 0, atol=1e-7)
+    np.testing.assert_allclose(host(do), [0.2, 0.2], rtol=1e-6)
+
+
+@pytest.mark.parametrize("dt,shape,fi", [(np.float32, (8, 16, 33), 1), (np.float64, (5, 7), 0),
+                                         (np.float32, (4, 3, 2, 64), 3)])
+def test_batch_norm_against_oracle(mode, oracle, dt, shape, fi):
+    """All three forms against the float64 oracle: within 1e-5 (f32) or
+    1e-12 (f64) relative, normwise per output."""
+    rs = np.random.default_rng(22 + fi)
+    C = shape[fi]
+    x = (rs.standard_normal(shape) * 3 + 1).astype(dt)
+    sc, of = rs.standard_normal(C).astype(dt), rs.standard_normal(C).astype(dt)
+    mu, va = rs.standard_normal(C).astype(dt), (rs.random(C) + 0.5).astype(dt)
+    dy = rs.standard_normal(shape).astype(dt)
+    eps = 1e-3
+    tol = 1e-5 if dt == np.float32 else 1e-12
+
+    def check(got, want):
+        got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+        assert np.abs(got - want).max() <= tol * max(np.abs(want).max(), 1.0)
+
+    check(host(O.batchNormInference(dev(x), dev(sc), dev(of), dev(mu), dev(va), eps, fi)),
+          oracle.batch_norm_inference(x, sc, of, mu, va, np.float32(eps), fi))
+    got = O.batchNormTraining(dev(x), dev(sc), dev(of), eps, fi)
+    for g, w in zip(got, oracle.batch_norm_training(x, sc, of, np.float32(eps), fi)):
+        check(host(g), w)
+    got = O.batchNormGrad(dev(x), dev(sc), dev(mu), dev(va), dev(dy), eps, fi)
+    for g, w in zip(got, oracle.batch_norm_grad(x, sc, mu, va, dy, np.float32(eps), fi)):
+        check(host(g), w)

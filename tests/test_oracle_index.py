@@ -137,3 +137,42 @@ def test_cholesky_pins(oracle):
     # only the referenced triangle is read
     junk = spd + np.triu(np.full((7, 7), 1e3), 1)
     np.testing.assert_allclose(oracle.cholesky(junk, True), L, rtol=1e-12)
+
+
+def test_batch_norm_pins(oracle):
+    """tests/teager_dispatch.nim:426-463 known answers; training output with unit
+    scale and zero offset has per-feature mean 0 and variance var / (var + eps);
+    the grad equals central finite differences of sum(dy * training output)
+    (mean and variance recomputed from the perturbed input)."""
+    a = np.array([1, 2, 3, 4], np.float64)
+    one, zero = np.ones(4), np.zeros(4)
+    np.testing.assert_array_equal(oracle.batch_norm_inference(a, one, zero, one, one, 0.0, 0),
+                                  [0, 1, 2, 3])
+    y, m, v = oracle.batch_norm_training(a.reshape(2, 2), np.ones(2), np.zeros(2), 0.0, 1)
+    np.testing.assert_allclose(y.ravel(), [-1, -1, 1, 1])
+    np.testing.assert_array_equal(m, [2, 3])
+    np.testing.assert_array_equal(v, [1, 1])
+    dx, ds, do = oracle.batch_norm_grad(a.reshape(2, 2), np.ones(2), np.array([2., 3.]),
+                                        np.ones(2), np.full((2, 2), 0.1), 0.0, 1)
+    np.testing.assert_allclose(dx.ravel(), 0, atol=1e-15)
+    np.testing.assert_allclose(ds, 0, atol=1e-15)
+    np.testing.assert_allclose(do, [0.2, 0.2])
+    rs = np.random.default_rng(21)
+    x = rs.standard_normal((3, 4, 5))
+    eps = 1e-3
+    y, m, v = oracle.batch_norm_training(x, np.ones(4), np.zeros(4), eps, 1)
+    np.testing.assert_allclose(y.mean(axis=(0, 2)), 0, atol=1e-12)
+    np.testing.assert_allclose(y.var(axis=(0, 2)), v / (v + eps), rtol=1e-12)
+    sc, of, dy = rs.standard_normal(4), rs.standard_normal(4), rs.standard_normal(x.shape)
+    _, m, v = oracle.batch_norm_training(x, sc, of, eps, 1)
+    dx, dsc, doff = oracle.batch_norm_grad(x, sc, m, v, dy, eps, 1)
+    loss = lambda z: float((dy * oracle.batch_norm_training(z, sc, of, eps, 1)[0]).sum())
+    h, num = 1e-6, np.zeros_like(x)
+    for i in np.ndindex(*x.shape):
+        e = np.zeros_like(x)
+        e[i] = h
+        num[i] = (loss(x + e) - loss(x - e)) / (2 * h)
+    np.testing.assert_allclose(dx, num, rtol=1e-5, atol=1e-7)
+    xn = (x - m[None, :, None]) / np.sqrt(v[None, :, None] + eps)
+    np.testing.assert_allclose(dsc, (dy * xn).sum(axis=(0, 2)), rtol=1e-12)
+    np.testing.assert_allclose(doff, dy.sum(axis=(0, 2)), rtol=1e-12)
