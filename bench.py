@@ -19,8 +19,13 @@ known size, the calibration for the HBM byte counters).
 Prints ONE JSON line with the metric (from a timed pass of K steps), a
 roofline object for the dominant kernel (its launches timed by HIP events on
 the backend's own stream over a second, profiled pass of the same K steps),
-and a cpu_baseline: the CPU restatement in oracle/ timed on this host's
-cores on a bounded sample.
+a cpu_baseline (the CPU restatement in oracle/ timed on this host's cores on
+a bounded sample) and a parity object: after the timed passes, one more step
+of the same workload is read back and compared with that cpu_baseline's own
+oracle output on the sample (bit-exact for index and byte results, within
+the stated tolerance for floating point).  The default llama run also
+measures the other configurations (MNIST, the chain, the SwiGLU FFN, the
+MoE layer) the same way and carries their records under "configs".
 """
 from __future__ import annotations
 
@@ -222,15 +227,45 @@ def breakdown(syms, steps):
                    for k, v in syms.items()), key=lambda r: -r[1])
 
 
-def emit(args, metric, value, unit, ms_per_step, dtype, config, roof, cpu, extra, hib=True):
-    line = {"metric": metric, "value": round(value, 3 if value < 1000 else 1), "unit": unit,
-            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-            "ms_per_step": round(ms_per_step, 4), "higher_is_better": hib, "scaling": "weak",
-            "vs_baseline": None, "dtype": dtype,
-            "data": "synthetic (rew Threefry normalF32/uniformF32 inputs, random-init weights)",
-            "config": config, "roofline": roof, "cpu_baseline": cpu}
-    line.update(extra)
-    print(json.dumps(line), flush=True)
+def record(args, metric, value, unit, ms_per_step, dtype, config, roof, cpu, parity, extra,
+           hib=True, steps=None, warmup=None):
+    """One workload's result: the contract's fields plus `parity` (the same
+    run's outputs compared with the oracle on a sample) and `extra`."""
+    rec = {"metric": metric, "value": round(value, 3 if value < 1000 else 1), "unit": unit,
+           "n_gpus": 1, "steps": args.steps if steps is None else steps,
+           "warmup": args.warmup if warmup is None else warmup,
+           "ms_per_step": round(ms_per_step, 4), "higher_is_better": hib, "scaling": "weak",
+           "vs_baseline": None, "dtype": dtype,
+           "data": "synthetic (rew Threefry normalF32/uniformF32 inputs, random-init weights)",
+           "config": config, "roofline": roof, "cpu_baseline": cpu, "parity": parity}
+    rec.update(extra)
+    return rec
+
+
+def normwise(got, want) -> float:
+    got = np.asarray(got, np.float64).ravel()
+    want = np.asarray(want, np.float64).ravel()
+    return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-300))
+
+
+def max_rel(got, want) -> float:
+    """Largest elementwise |got - want| / |want| (pairs where both are 0 count as 0)."""
+    got = np.asarray(got, np.float64).ravel()
+    want = np.asarray(want, np.float64).ravel()
+    den = np.abs(want)
+    diff = np.abs(got - want)
+    rel = np.where(den > 0, diff / np.where(den > 0, den, 1.0), np.where(diff > 0, np.inf, 0.0))
+    return float(rel.max()) if rel.size else 0.0
+
+
+def parity_obj(checks, sample):
+    """`checks`: name -> (error, tolerance, kind).  ok = every error within its
+    tolerance; a tolerance of None marks a figure that is reported only."""
+    out = {"ok": all(e <= t for e, t, _ in checks.values() if t is not None), "sample": sample}
+    for name, (e, t, kind) in checks.items():
+        out[name] = {"err": e if isinstance(e, int) else float(f"{e:.3e}"), "tol": t,
+                     "kind": kind}
+    return out
 
 
 def oracle_mod():
@@ -270,9 +305,11 @@ def entry_flops(entry_name: str) -> int | None:
     return (4 if "swiglu" in entry_name else 2) * b * m * n * k
 
 
-def build_llama(cfg, seed=0x5EED0004):
+def build_llama(cfg, seed=0x5EED0004, norm="rms"):
     """Weights ~N(0, 0.02) bf16, zero biases, gammas ~N(1, 0.1) f32, keyed per
-    tensor in declaration order from initKey(seed)."""
+    tensor in declaration order from initKey(seed).  norm "rms" gives the
+    config's RMSNorm; "layer" gives rew's own LayerNorm (llama.nim:32-33) with
+    those gammas and zero betas."""
     H, nh, nkv, hd, I = (cfg["hidden"], cfg["heads"], cfg["kv_heads"], cfg["head_dim"],
                          cfg["intermediate"])
     V = cfg["vocab"]
@@ -298,18 +335,24 @@ def build_llama(cfg, seed=0x5EED0004):
     S = cfg["seq_len"]
     ids = rng.tokenIds(keys[10], cfg["batch"] * S, V)
     rope = nn.RotaryPositionEncoding.init(hd, S, cfg["rope_theta"])
+    if norm == "rms":
+        n1 = nn.RMSNorm(E.fromHost(host["g1"]), cfg["eps"])
+        n2 = nn.RMSNorm(E.fromHost(host["g2"]), cfg["eps"])
+    else:
+        zero = np.zeros(H, np.float32)
+        n1 = nn.LayerNorm(E.fromHost(host["g1"]), E.fromHost(zero), [H], cfg["eps"])
+        n2 = nn.LayerNorm(E.fromHost(host["g2"]), E.fromHost(zero), [H], cfg["eps"])
     layer = nn.LlamaDecoderLayer(
         nn.GroupedQueryAttention(m["q"], m["k"], m["v"], m["o"], nh, nkv, hd, rope),
-        nn.GatedFeedForward(m["g"], m["u"], m["d"]),
-        nn.RMSNorm(E.fromHost(host["g1"]), cfg["eps"]),
-        nn.RMSNorm(E.fromHost(host["g2"]), cfg["eps"]))
+        nn.GatedFeedForward(m["g"], m["u"], m["d"]), n1, n2)
     emb = nn.Embedding(E.fromHost(table, DType.BFLOAT16))
     return layer, emb, E.fromHost(ids), host, table, ids
 
 
-def cpu_baseline_llama(cfg, host, table, ids, seqs):
+def cpu_baseline_llama(cfg, host, table, ids, seqs, norm):
     """The oracle's restatement of the same layer on a bounded sample: the
-    first `seqs` of the batch's sequences, each a full S-token causal prefill."""
+    first `seqs` of the batch's sequences, each a full S-token causal prefill.
+    Returns (cpu_baseline, the oracle's output [seqs, S, H])."""
     orc = oracle_mod()
     nh, nkv, hd, S = cfg["heads"], cfg["kv_heads"], cfg["head_dim"], cfg["seq_len"]
     p = {}
@@ -320,20 +363,20 @@ def cpu_baseline_llama(cfg, host, table, ids, seqs):
     c, s = nn.rope_tables(hd, S, cfg["rope_theta"])
     x = orc.from_bf16(table[ids[:seqs * S]]).reshape(seqs, S, cfg["hidden"])
     t0 = time.perf_counter()
-    orc.llama_layer(x, p, nh, nkv, c, s, cfg["eps"], True, True, "rms")
+    want = orc.llama_layer(x, p, nh, nkv, c, s, cfg["eps"], True, True, norm)
     dt = time.perf_counter() - t0
-    return {"value": round(seqs * S / dt, 2), "unit": "tokens/s",
-            "cores": int(orc.lib().orc_num_threads()), "kind": "port",
-            "sample": f"{seqs} of the {cfg['batch']} sequences ({seqs * S} tokens, full "
-                      f"hidden/FFN/head dims, causal), oracle/ C restatement with OpenMP, "
-                      f"{dt:.1f} s"}
+    return ({"value": round(seqs * S / dt, 2), "unit": "tokens/s",
+             "cores": int(orc.lib().orc_num_threads()), "kind": "port",
+             "sample": f"{seqs} of the {cfg['batch']} sequences ({seqs * S} tokens, full "
+                       f"hidden/FFN/head dims, causal), oracle/ C restatement with OpenMP, "
+                       f"{dt:.1f} s"}, want)
 
 
 def run_llama(args):
     cfg = dict(C4)
     B, S, H = cfg["batch"], cfg["seq_len"], cfg["hidden"]
     t0 = time.perf_counter()
-    layer, emb, ids_t, host, table, ids = build_llama(cfg)
+    layer, emb, ids_t, host, table, ids = build_llama(cfg, norm=args.norm)
     E.sync()
     print(f"# inputs ready in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
 
@@ -348,14 +391,32 @@ def run_llama(args):
     flops = llama_layer_flops(B, S, H, cfg["heads"], cfg["kv_heads"], cfg["head_dim"],
                               cfg["intermediate"])
     syms = by_symbol(prof, entry_flops)
-    roof = roofline("llama", syms, "mfma")
+    roof = roofline("llama" if args.norm == "rms" else "llama_layernorm", syms, "mfma")
     kernel_ms = sum(v["ms"] for v in syms.values()) / args.steps
-    cpu = None if args.no_cpu_baseline else cpu_baseline_llama(cfg, host, table, ids,
-                                                               args.cpu_seqs)
+    # parity, outside the timed region: one more step of the same workload
+    # with the gathered embedding held, so both come back to the host
+    x_t = O.reshape(emb.lookup(ids_t), [B, S, H])
+    y_t = layer.forward(x_t, causal=True)
+    x_dev = E.toHost(x_t).reshape(B * S, H)
+    y_dev = E.toHostF32(y_t)
+    del x_t, y_t
+    emb_mismatch = int(np.count_nonzero(np.any(x_dev != table[ids], axis=1)))
+    checks = {"embedding_rows": (emb_mismatch, 0, "rows of the gathered [8192,4096] bf16 "
+                                 "embedding not bit-equal to table[ids]")}
+    cpu = None
+    sample = f"embedding: all {B * S} rows"
+    if not args.no_cpu_baseline:
+        cpu, want = cpu_baseline_llama(cfg, host, table, ids, args.cpu_seqs, args.norm)
+        checks["layer_out"] = (normwise(y_dev[:args.cpu_seqs], want), 2e-2,
+                               "normwise relative, bf16 layer output vs oracle")
+        sample += (f"; layer output: sequences 0..{args.cpu_seqs - 1} ({args.cpu_seqs * S} "
+                   f"tokens), the cpu_baseline's own oracle run")
+    parity = parity_obj(checks, sample)
     config = {"workload": "llama_decoder_layer_prefill_bf16", "batch": B, "seq_len": S,
               "hidden": H, "heads": cfg["heads"], "kv_heads": cfg["kv_heads"],
               "head_dim": cfg["head_dim"], "intermediate": cfg["intermediate"],
               "vocab": cfg["vocab"], "rope_theta": cfg["rope_theta"], "causal": True,
+              "norm": "rmsnorm" if args.norm == "rms" else "layernorm",
               "parallelism": "single-gpu"}
     extra = {"layer": {"algorithmic_tflop": round(flops / 1e12, 4),
                        "achieved_tflops": round(flops / (ms_per_step * 1e-3) / 1e12, 1),
@@ -366,13 +427,17 @@ def run_llama(args):
                        "first_call_ms": round(first_ms, 1),
                        "host": hostc,
                        "kernels": breakdown(syms, args.steps)[:12]}}
-    emit(args, "llama_layer_prefill_tokens_per_s", B * S * args.steps / wall, "tokens/s",
-         ms_per_step, "bf16", config, roof, cpu, extra)
+    metric = ("llama_layer_prefill_tokens_per_s" if args.norm == "rms"
+              else "llama_layer_layernorm_prefill_tokens_per_s")
+    return record(args, metric, B * S * args.steps / wall, "tokens/s", ms_per_step, "bf16",
+                  config, roof, cpu, parity, extra)
 
 
 # ---- C3: SwiGLU gated FFN ------------------------------------------------------------------
 
-def run_swiglu(args):
+def run_swiglu(args, steps=None, warmup=None):
+    steps = args.steps if steps is None else steps
+    warmup = args.warmup if warmup is None else warmup
     T, H, I = 4096, 4096, 14336
     keys = rng.split(rng.initKey(0x5EED0003), 4)
     x = E.f32_to_bf16_bits(rng.normalF32(keys[0], T * H)).reshape(1, T, H)
@@ -389,34 +454,44 @@ def run_swiglu(args):
         E.flush()
         return y
 
-    wall, dev_ms, first_ms, prof, hostc = timed_run(step, args.steps, args.warmup)
-    ms = wall * 1e3 / args.steps
+    wall, dev_ms, first_ms, prof, hostc = timed_run(step, steps, warmup)
+    ms = wall * 1e3 / steps
     flops = 2 * T * H * I * 3
     syms = by_symbol(prof, entry_flops)
     roof = roofline("swiglu", syms, "mfma")
-    cpu = None
+    y_dev = E.toHostF32(step()).reshape(T, H)
+    cpu, parity = None, None
     if not args.no_cpu_baseline:
         orc = oracle_mod()
-        rows = 256
-        xf = orc.from_bf16(x.reshape(T, H)[:rows])
+        rows = np.arange(0, T, 16)           # 256 token rows spread over the batch
+        xf = orc.from_bf16(x.reshape(T, H)[rows])
         wf = [orc.from_bf16(w) for w in ws]
         z = np.zeros(I, np.float32)
         t0 = time.perf_counter()
-        orc.gated_ffn(xf, wf[0], z, wf[1], z, wf[2], np.zeros(H, np.float32), True)
+        want = orc.gated_ffn(xf, wf[0], z, wf[1], z, wf[2], np.zeros(H, np.float32), True)
         dt = time.perf_counter() - t0
-        cpu = {"value": round(2 * rows * H * I * 3 / dt / 1e12, 4), "unit": "TFLOP/s",
+        cpu = {"value": round(2 * len(rows) * H * I * 3 / dt / 1e12, 4), "unit": "TFLOP/s",
                "cores": int(orc.lib().orc_num_threads()), "kind": "port",
-               "sample": f"{rows} of the {T} token rows through the same FFN, oracle/ C "
-                         f"restatement with OpenMP, {dt:.1f} s"}
-    emit(args, "swiglu_ffn_tflops", flops / (ms * 1e-3) / 1e12, "TFLOP/s", ms, "bf16",
-         {"workload": "swiglu_gated_ffn_bf16", "tokens": T, "hidden": H, "intermediate": I},
-         roof, cpu, {"kernels": breakdown(syms, args.steps), "first_call_ms": round(first_ms, 1),
-                     "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)})
+               "sample": f"{len(rows)} of the {T} token rows (every 16th) through the same "
+                         f"FFN, oracle/ C restatement with OpenMP, {dt:.1f} s"}
+        parity = parity_obj({"ffn_out": (normwise(y_dev[rows], want), 2e-2,
+                                         "normwise relative, bf16 FFN output vs oracle")},
+                            f"{len(rows)} token rows (every 16th of {T}), the cpu_baseline's "
+                            f"own oracle run")
+    return record(args, "swiglu_ffn_tflops", flops / (ms * 1e-3) / 1e12, "TFLOP/s", ms, "bf16",
+                  {"workload": "swiglu_gated_ffn_bf16", "tokens": T, "hidden": H,
+                   "intermediate": I},
+                  roof, cpu, parity,
+                  {"kernels": breakdown(syms, steps), "first_call_ms": round(first_ms, 1),
+                   "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)},
+                  steps=steps, warmup=warmup)
 
 
 # ---- C2: elementwise + reduction chain (HBM-bound) ----------------------------------------
 
-def run_chain(args):
+def run_chain(args, steps=None, warmup=None):
+    steps = args.steps if steps is None else steps
+    warmup = args.warmup if warmup is None else warmup
     R, Cn = 8192, 4096
     keys = rng.split(rng.initKey(0x5EED0002), 2)
     x = rng.normalF32(keys[0], R * Cn).reshape(R, Cn)
@@ -436,8 +511,8 @@ def run_chain(args):
         E.flush()
         return outs
 
-    wall, dev_ms, first_ms, prof, hostc = timed_run(step, args.steps, args.warmup)
-    ms = wall * 1e3 / args.steps
+    wall, dev_ms, first_ms, prof, hostc = timed_run(step, steps, warmup)
+    ms = wall * 1e3 / steps
 
     def bytes_of(name):
         if name.startswith("rmsnorm_rows"):
@@ -452,29 +527,46 @@ def run_chain(args):
 
     syms = by_symbol(prof, bytes_of)
     roof = roofline("chain", by_symbol(prof, bytes_of, by_shape=True), "hbm")
-    cpu = None
+    outs = [E.toHost(t) for t in step()]
+    cpu, parity = None, None
     if not args.no_cpu_baseline:
         orc = oracle_mod()
-        rows = 2048
-        xs, t0 = x[:rows], time.perf_counter()
+        rows = np.arange(0, R, 4)            # 2048 rows spread over the batch
+        xs, t0 = np.ascontiguousarray(x[rows]), time.perf_counter()
         reps = 0
-        while time.perf_counter() - t0 < 10.0:
+        while True:
             y = orc.binary(orc.MAX, orc.binary(orc.ADD, xs, xs), np.zeros_like(xs))
-            orc.reduce(orc.RSUM, y, [1])
-            orc.reduce(orc.RSUM, y, [1])
-            orc.reduce(orc.RMAX, y, [1])
-            orc.softmax_rows(xs)
-            orc.rmsnorm_rows(xs, g, 1e-5)
+            s_ = orc.reduce(orc.RSUM, y, [1])
+            m_ = orc.binary(orc.DIV, orc.reduce(orc.RSUM, y, [1]),
+                            np.full(len(rows), Cn, np.float32))
+            mx = orc.reduce(orc.RMAX, y, [1])
+            sm = orc.softmax_rows(xs)
+            rn = orc.rmsnorm_rows(xs, g, 1e-5)
             reps += 1
+            if time.perf_counter() - t0 >= 10.0:
+                break
         dt = time.perf_counter() - t0
-        cpu = {"value": round(total * rows / R * reps / dt / 1e9, 2), "unit": "GB/s",
+        cpu = {"value": round(total * len(rows) / R * reps / dt / 1e9, 2), "unit": "GB/s",
                "cores": int(orc.lib().orc_num_threads()), "kind": "port",
-               "sample": f"{reps} passes of the chain over {rows} of the {R} rows, oracle/ C "
-                         f"restatement, {dt:.1f} s"}
-    emit(args, "eager_chain_hbm_gbs", total / (ms * 1e-3) / 1e9, "GB/s", ms, "f32",
-         {"workload": "eager_elementwise_reduction_chain_f32", "rows": R, "cols": Cn},
-         roof, cpu, {"kernels": breakdown(syms, args.steps), "algorithmic_bytes_per_step": total,
-                     "hbm_frac": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+               "sample": f"{reps} passes of the chain over {len(rows)} of the {R} rows (every "
+                         f"4th), oracle/ C restatement, {dt:.1f} s"}
+        ry, rs, rm, rmx, rsm, rrn = (o[rows] for o in outs)
+        parity = parity_obj(
+            {"relu": (int(np.count_nonzero(ry.view(np.uint32) != y.view(np.uint32))), 0,
+                      "elements of relu(x + x) not bit-equal"),
+             "reduceSum": (max_rel(rs, s_), 1e-5, "max elementwise relative"),
+             "reduceMean": (max_rel(rm, m_), 1e-5, "max elementwise relative"),
+             "reduceMax": (int(np.count_nonzero(rmx.view(np.uint32) != mx.view(np.uint32))), 0,
+                           "rows not bit-equal"),
+             "softmax": (max_rel(rsm, sm), 1e-5, "max elementwise relative"),
+             "rmsNorm": (max_rel(rrn, rn), 1e-5, "max elementwise relative")},
+            f"{len(rows)} of the {R} rows (every 4th), the cpu_baseline's own oracle run")
+    return record(args, "eager_chain_hbm_gbs", total / (ms * 1e-3) / 1e9, "GB/s", ms, "f32",
+                  {"workload": "eager_elementwise_reduction_chain_f32", "rows": R, "cols": Cn},
+                  roof, cpu, parity,
+                  {"kernels": breakdown(syms, steps), "algorithmic_bytes_per_step": total,
+                   "hbm_frac": round(total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+                  steps=steps, warmup=warmup)
 
 
 # ---- copy: the streaming kernel the HBM byte counters are calibrated on --------------------
@@ -493,9 +585,12 @@ def run_copy(args):
     ms = wall * 1e3 / args.steps
     syms = by_symbol(prof, lambda name: 2 * n * 4)
     roof = roofline("copy", syms, "hbm")
-    emit(args, "stream_copy_gbs", 2 * n * 4 / (ms * 1e-3) / 1e9, "GB/s", ms, "f32",
-         {"workload": "stream_neg_f32", "elements": n}, roof, None,
-         {"bytes_per_launch": 2 * n * 4})
+    y = E.toHost(step())
+    parity = parity_obj({"neg": (int(np.count_nonzero(y != -1.0)), 0,
+                                 "elements of neg(1) not equal to -1")}, f"all {n} elements")
+    return record(args, "stream_copy_gbs", 2 * n * 4 / (ms * 1e-3) / 1e9, "GB/s", ms, "f32",
+                  {"workload": "stream_neg_f32", "elements": n}, roof, None, parity,
+                  {"bytes_per_launch": 2 * n * 4})
 
 
 # ---- C5: DeepSeek-style routed MoE layer ---------------------------------------------------
@@ -533,7 +628,9 @@ def build_moe(cfg, seed=0x5EED0005):
     return moe, E.fromHost(x, DType.BFLOAT16), host
 
 
-def run_moe(args):
+def run_moe(args, steps=None, warmup=None):
+    steps = args.steps if steps is None else steps
+    warmup = args.warmup if warmup is None else warmup
     cfg = dict(C5)
     T, H, I, E_, S, k = (cfg["tokens"], cfg["hidden"], cfg["intermediate"], cfg["routed"],
                          cfg["shared"], cfg["top_k"])
@@ -562,40 +659,90 @@ def run_moe(args):
             E.flush()
             return y
 
-    wall, dev_ms, first_ms, prof, hostc = timed_run(step, args.steps, args.warmup)
-    ms = wall * 1e3 / args.steps
+    wall, dev_ms, first_ms, prof, hostc = timed_run(step, steps, warmup)
+    ms = wall * 1e3 / steps
     flops = moe_flops(T, H, I, E_, S, k)
     syms = by_symbol(prof, entry_flops)
     roof = roofline("moe", syms, "mfma")
-    cpu = None
+    y_dev = E.toHostF32(step())
+    cpu, parity = None, None
     if not args.no_cpu_baseline:
         orc = oracle_mod()
-        rows = 256
-        xs = orc.from_bf16(host["x"][:rows])
+        rows = np.arange(0, T, T // 256)     # 256 tokens, one in every 32
+        xs = orc.from_bf16(host["x"][rows])
         z = lambda n: np.zeros(n, np.float32)
         exps = [(orc.from_bf16(a), z(I), orc.from_bf16(b), z(I), orc.from_bf16(c), z(H))
                 for a, b, c in host["experts"]]
         t0 = time.perf_counter()
-        orc.deepseek_moe(xs, exps[:S], exps[S:], host["wr"], z(E_), k)
+        want, _, _ = orc.deepseek_moe(xs, exps[:S], exps[S:], host["wr"], z(E_), k)
         dt = time.perf_counter() - t0
-        cpu = {"value": round(rows / dt, 2), "unit": "tokens/s",
+        cpu = {"value": round(len(rows) / dt, 2), "unit": "tokens/s",
                "cores": int(orc.lib().orc_num_threads()), "kind": "port",
-               "sample": f"{rows} of the {T} tokens through the reference's dense "
-                         f"formulation (every routed expert on every token, "
-                         f"deepseek.nim:122-145), oracle/ C restatement, {dt:.1f} s"}
-    emit(args, "moe_layer_tokens_per_s", T * args.steps / wall, "tokens/s", ms, "bf16",
-         {"workload": "deepseek_moe_layer_bf16", "tokens": T, "hidden": H, "intermediate": I,
-          "routed_experts": E_, "shared_experts": S, "top_k": k, "path": args.moe_path},
-         roof, cpu, {"kernels": breakdown(syms, args.steps), "first_call_ms": round(first_ms, 1),
-                     "host": hostc,
-                     "algorithmic_tflop": round(flops / 1e12, 4),
-                     "achieved_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
-                     "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)})
+               "sample": f"{len(rows)} of the {T} tokens (every {T // len(rows)}th) through "
+                         f"the reference's dense formulation (every routed expert on every "
+                         f"token, deepseek.nim:122-145), oracle/ C restatement, {dt:.1f} s"}
+        # router and expert ids of all T tokens.  The logits are an fp32
+        # GEMM over K = H whose accumulation order rew leaves to the plugin,
+        # so they are held to the bound every summation order meets:
+        # |got - exact| <= K * 2^-24 * sum_k |x_k| |w_k| (first order).  The
+        # ids must be the oracle's top-k of the device's own probabilities
+        # exactly, and a row whose ids differ from the oracle's top-k of the
+        # oracle's probabilities must be a near-tie (two candidates closer
+        # than twice that row's probability error)
+        xf = orc.from_bf16(host["x"])
+        logits_dev = E.toHost(moe.gate.forward(O.astype(xt, DType.FLOAT32)))
+        probs_dev = E.toHost(nn.softmax(moe.gate.forward(O.astype(xt, DType.FLOAT32)), 1))
+        ids_dev = E.toHost(moe.route(xt)[1])
+        logits = orc.linear(xf, host["wr"], z(E_), False)
+        absdot = np.abs(xf).astype(np.float64) @ np.abs(host["wr"]).astype(np.float64)
+        logit_ratio = float(np.max(np.abs(logits_dev.astype(np.float64) - logits) /
+                                   (H * 2.0 ** -24 * np.maximum(absdot, 1e-300))))
+        probs = orc.softmax_rows(logits)
+        _, ids_want = orc.topk_rows(probs, k)
+        _, ids_same = orc.topk_rows(probs_dev, k)
+        diff = np.where(np.any(ids_dev != ids_want, axis=1))[0]
+        not_tie = 0
+        for r in diff:
+            row_err = np.max(np.abs(probs_dev[r] - probs[r]))
+            srt = np.sort(probs[r])[::-1]
+            if np.min(srt[:k] - srt[1:k + 1]) > 2 * row_err:
+                not_tie += 1
+        parity = parity_obj(
+            {"moe_out": (normwise(y_dev[rows], want), 2e-2,
+                         "normwise relative, bf16 layer output vs the oracle's dense layer"),
+             "router_logits": (logit_ratio, 1.0,
+                               "max |got - oracle| / (K 2^-24 sum|x||w|), fp32 router GEMM, "
+                               "all tokens"),
+             "router_probs": (normwise(probs_dev, probs), None,
+                              "normwise relative, fp32 router softmax, all tokens "
+                              "(reported; bounded through the logits)"),
+             "expert_ids_given_probs": (int(np.count_nonzero(np.any(ids_dev != ids_same,
+                                                                     axis=1))), 0,
+                                        "rows whose device top-k ids differ from the "
+                                        "oracle's top-k of the same probabilities"),
+             "expert_ids_off_near_ties": (not_tie, 0,
+                                          f"rows whose ids differ from the oracle's and are "
+                                          f"not a near-tie ({len(diff)} rows differ in all)")},
+            f"ids and router: all {T} tokens; layer output: {len(rows)} tokens (every "
+            f"{T // len(rows)}th), the cpu_baseline's own oracle run")
+    return record(args, "moe_layer_tokens_per_s", T * steps / wall, "tokens/s", ms, "bf16",
+                  {"workload": "deepseek_moe_layer_bf16", "tokens": T, "hidden": H,
+                   "intermediate": I, "routed_experts": E_, "shared_experts": S, "top_k": k,
+                   "path": args.moe_path},
+                  roof, cpu, parity,
+                  {"kernels": breakdown(syms, steps), "first_call_ms": round(first_ms, 1),
+                   "host": hostc,
+                   "algorithmic_tflop": round(flops / 1e12, 4),
+                   "achieved_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+                   "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)},
+                  steps=steps, warmup=warmup)
 
 
 # ---- C1: MNIST-shaped MLP inference (latency-bound) ----------------------------------------
 
-def run_mnist(args):
+def run_mnist(args, steps=None, warmup=None):
+    steps = args.steps if steps is None else steps
+    warmup = args.warmup if warmup is None else warmup
     B, D, Hd, C = 128, 784, 128, 10
     keys = rng.split(rng.initKey(0x5EED0001), 3)
     x = rng.uniformF32(keys[0], B * D, 0.0, 1.0).reshape(B, D)
@@ -626,8 +773,8 @@ def run_mnist(args):
             E.flush()
             return ids
 
-    wall, dev_ms, first_ms, prof, hostc = timed_run(step, args.steps, args.warmup)
-    ms = wall * 1e3 / args.steps
+    wall, dev_ms, first_ms, prof, hostc = timed_run(step, steps, warmup)
+    ms = wall * 1e3 / steps
     flops = 2 * B * D * Hd + 2 * B * Hd * C
 
     def gemm_flops(name):
@@ -643,31 +790,52 @@ def run_mnist(args):
         ach = d["work"] / d["launches"] / (d["ms"] / d["launches"] * 1e-3) / 1e12
         roof["achieved"] = round(ach, 3)
         roof["frac"] = round(ach / FP32_PEAK_TFLOPS, 5)
-    cpu = None
+    ids_dev = E.toHost(step())
+    cpu, parity = None, None
     if not args.no_cpu_baseline:
         orc = oracle_mod()
         t0, reps = time.perf_counter(), 0
         z1, z2 = np.zeros(Hd, np.float32), np.zeros(C, np.float32)
-        while time.perf_counter() - t0 < 10.0:
+        while True:
             h = np.maximum(orc.linear(x, w1, z1, False), 0)
-            orc.argmax_rows(orc.softmax_rows(orc.linear(h, w2, z2, False)))
+            want = orc.argmax_rows(orc.softmax_rows(orc.linear(h, w2, z2, False)))
             reps += 1
+            if time.perf_counter() - t0 >= 10.0:
+                break
         dt = time.perf_counter() - t0
         cpu = {"value": round(B * reps / dt, 1), "unit": "rows/s",
                "cores": int(orc.lib().orc_num_threads()), "kind": "port",
                "sample": f"{reps} forwards of the full [128,784] batch, oracle/ C restatement, "
                          f"{dt:.1f} s"}
-    emit(args, "mnist_mlp_rows_per_s", B * args.steps / wall, "rows/s", ms, "f32",
-         {"workload": "mnist_mlp_inference_f32", "batch": B, "layers": [D, Hd, C],
-          "path": args.mnist_path},
-         roof, cpu, {"kernels": breakdown(syms, args.steps), "first_call_ms": round(first_ms, 2),
-                     "host": hostc,
-                     "us_per_forward": round(ms * 1e3, 1), "algorithmic_flops": flops,
-                     "device_us_per_forward": round(dev_ms * 1e3 / args.steps, 1)})
+        parity = parity_obj({"argmax": (int(np.count_nonzero(ids_dev != want)), 0,
+                                        "rows whose argmax differs (bit-exact)")},
+                            f"the full batch of {B} rows, the cpu_baseline's own oracle run")
+    return record(args, "mnist_mlp_rows_per_s", B * steps / wall, "rows/s", ms, "f32",
+                  {"workload": "mnist_mlp_inference_f32", "batch": B, "layers": [D, Hd, C],
+                   "path": args.mnist_path},
+                  roof, cpu, parity,
+                  {"kernels": breakdown(syms, steps), "first_call_ms": round(first_ms, 2),
+                   "host": hostc,
+                   "us_per_forward": round(ms * 1e3, 1), "algorithmic_flops": flops,
+                   "device_us_per_forward": round(dev_ms * 1e3 / steps, 1)},
+                  steps=steps, warmup=warmup)
+
+
+def compact(rec):
+    """The other configurations' records as carried on the headline line."""
+    keep = ("metric", "value", "unit", "ms_per_step", "steps", "warmup", "dtype", "config",
+            "roofline", "cpu_baseline", "parity", "kernels", "mfma_frac", "hbm_frac",
+            "us_per_forward", "device_us_per_forward")
+    return {k: rec[k] for k in keep if k in rec}
 
 
 WORKLOADS = {"llama": run_llama, "swiglu": run_swiglu, "chain": run_chain, "copy": run_copy,
              "moe": run_moe, "mnist": run_mnist}
+
+# the other configurations, run after the headline by default: (key, runner,
+# steps, warmup) -- MNIST forwards are ~30 us, so it takes more steps
+EXTRAS = [("C1_mnist_mlp", run_mnist, 200, 20), ("C2_eager_chain", run_chain, None, None),
+          ("C3_swiglu_ffn", run_swiglu, None, None), ("C5_deepseek_moe", run_moe, None, None)]
 
 
 def main():
@@ -676,6 +844,11 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="llama", choices=sorted(WORKLOADS))
+    ap.add_argument("--norm", default="rms", choices=["rms", "layer"],
+                    help="llama workload: the config's RMSNorm, or rew's own LayerNorm "
+                         "(src/rew/models/llama.nim:32-33)")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="llama workload: skip the other configurations' records")
     ap.add_argument("--cpu-seqs", type=int, default=2,
                     help="sequences of the llama batch in the cpu_baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -694,7 +867,15 @@ def main():
         print("bench.py: no HIP device visible", file=sys.stderr)
         sys.exit(1)
     E.installEagerBackend(E.mi355x(0))
-    WORKLOADS[args.workload](args)
+    rec = WORKLOADS[args.workload](args)
+    if args.workload == "llama" and not args.no_extras:
+        extras = {}
+        for key, fn, st, wu in EXTRAS:
+            print(f"# {key}", file=sys.stderr, flush=True)
+            extras[key] = compact(fn(args, st, wu))
+            E.sync()
+        rec["configs"] = extras
+    print(json.dumps(rec), flush=True)
 
 
 if __name__ == "__main__":
