@@ -36,57 +36,6 @@ __device__ __forceinline__ void st_f(void* p, int dt, int64_t i, float v) {
 
 constexpr int kRowRegs = 32;  // elements per thread kept in registers
 
-__global__ void __launch_bounds__(256) rmsnorm_rows_kernel(RowNormArgs a) {
-  __shared__ float part[4];
-  const int tid = threadIdx.x;
-  for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x) {
-    const char* x = (const char*)a.x + row * a.x_rs * dt_bytes(a.x_dt);
-    float v[kRowRegs];
-    float ss = 0.0f;
-#pragma unroll
-    for (int k = 0; k < kRowRegs; ++k) {
-      const int64_t j = tid + (int64_t)k * 256;
-      v[k] = j < a.n ? ld_f(x, a.x_dt, j) : 0.0f;
-      const float sq = v[k] * v[k];
-      ss += sq;
-    }
-    for (int64_t j = tid + (int64_t)kRowRegs * 256; j < a.n; j += 256) {
-      const float xv = ld_f(x, a.x_dt, j);
-      const float sq = xv * xv;
-      ss += sq;
-    }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
-    if ((tid & 63) == 0) part[tid >> 6] = ss;
-    __syncthreads();
-    const float sum = (part[0] + part[1]) + (part[2] + part[3]);
-    __syncthreads();
-    const float mean = sum / a.divisor;
-    const float r = sqrtf(mean + a.eps);
-    char* y = (char*)a.y + row * a.n * dt_bytes(a.y_dt);
-#pragma unroll
-    for (int k = 0; k < kRowRegs; ++k) {
-      const int64_t j = tid + (int64_t)k * 256;
-      if (j < a.n) {
-        const float nv = v[k] / r;
-        st_f(y, a.y_dt, j, a.gamma[j] * nv);
-      }
-    }
-    for (int64_t j = tid + (int64_t)kRowRegs * 256; j < a.n; j += 256) {
-      const float nv = ld_f(x, a.x_dt, j) / r;
-      st_f(y, a.y_dt, j, a.gamma[j] * nv);
-    }
-  }
-}
-
-// Fast path: one wave per row, the row held in registers as 16-byte chunks
-// (8 bf16 or 4 f32 per load), CH chunks per lane; a wave-only reduction; the
-// same op order as rmsnorm_rows_kernel (square, sum, / n, + eps, sqrt,
-// x / r, gamma * .).
-//
-// rms_row: that arithmetic for one row whose chunks are in raw (chunk k of
-// lane l holds elements (64 k + l) EPC_X ..); gam(k, e) is gamma of element
-// e of chunk k.  FULL: every chunk is in range (n == 64 CH EPC_X).
 // row of x that feeds output row r (the gather form reads it from ids)
 __device__ __forceinline__ int64_t src_row(const RowNormArgs& a, int64_t r) {
   if (!a.ids) return r;
@@ -100,6 +49,117 @@ __device__ __forceinline__ int64_t src_row(const RowNormArgs& a, int64_t r) {
   return i < 0 ? 0 : (i >= a.x_rows ? a.x_rows - 1 : i);
 }
 
+// Sum of v over the 256 threads of the workgroup: the wave butterfly, then
+// the four wave sums as (w0 + w1) + (w2 + w3).  `part` is free again when
+// this returns.
+__device__ __forceinline__ float block_sum(float v, float (&part)[4]) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const float sum = (part[0] + part[1]) + (part[2] + part[3]);
+  __syncthreads();
+  return sum;
+}
+
+// Any row length, stride, alignment and dtype pair: one workgroup per row,
+// kRowRegs elements per thread kept in registers, the rest re-read.  Both
+// norms; the gather form too (rows by id, the raw row stored to xout).
+__global__ void __launch_bounds__(256) rmsnorm_rows_kernel(RowNormArgs a) {
+  __shared__ float part[4];
+  const int tid = threadIdx.x;
+  const int xb = dt_bytes(a.x_dt);
+  for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x) {
+    const char* x = (const char*)a.x + src_row(a, row) * a.x_rs * xb;
+    char* xo = a.xout ? (char*)a.xout + row * a.n * xb : nullptr;
+    float v[kRowRegs];
+    // pass 1: sum of squares (rmsNorm) or sum (LayerNorm)
+    float s1 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kRowRegs; ++k) {
+      const int64_t j = tid + (int64_t)k * 256;
+      v[k] = j < a.n ? ld_f(x, a.x_dt, j) : 0.0f;
+      if (xo && j < a.n) st_f(xo, a.x_dt, j, v[k]);
+      if (a.layer) {
+        s1 += v[k];
+      } else {
+        const float sq = v[k] * v[k];
+        s1 += sq;
+      }
+    }
+    for (int64_t j = tid + (int64_t)kRowRegs * 256; j < a.n; j += 256) {
+      const float xv = ld_f(x, a.x_dt, j);
+      if (xo) st_f(xo, a.x_dt, j, xv);
+      if (a.layer) {
+        s1 += xv;
+      } else {
+        const float sq = xv * xv;
+        s1 += sq;
+      }
+    }
+    const float sum = block_sum(s1, part);
+    char* y = (char*)a.y + row * a.n * dt_bytes(a.y_dt);
+    if (!a.layer) {
+      const float mean = sum / a.divisor;
+      const float r = sqrtf(mean + a.eps);
+#pragma unroll
+      for (int k = 0; k < kRowRegs; ++k) {
+        const int64_t j = tid + (int64_t)k * 256;
+        if (j < a.n) {
+          const float nv = v[k] / r;
+          st_f(y, a.y_dt, j, a.gamma[j] * nv);
+        }
+      }
+      for (int64_t j = tid + (int64_t)kRowRegs * 256; j < a.n; j += 256) {
+        const float nv = ld_f(x, a.x_dt, j) / r;
+        st_f(y, a.y_dt, j, a.gamma[j] * nv);
+      }
+      continue;
+    }
+    // LayerNorm pass 2: sum of the centred squares
+    const float m = sum / a.divisor;
+    float s2 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kRowRegs; ++k) {
+      const int64_t j = tid + (int64_t)k * 256;
+      if (j < a.n) {
+        const float c = v[k] - m;
+        const float sq = c * c;
+        s2 += sq;
+      }
+    }
+    for (int64_t j = tid + (int64_t)kRowRegs * 256; j < a.n; j += 256) {
+      const float c = ld_f(x, a.x_dt, j) - m;
+      const float sq = c * c;
+      s2 += sq;
+    }
+    const float var = block_sum(s2, part) / a.divisor2;
+    const float inv = 1.0f / sqrtf(var + a.eps);  // rsqrt as the elementwise op computes it
+#pragma unroll
+    for (int k = 0; k < kRowRegs; ++k) {
+      const int64_t j = tid + (int64_t)k * 256;
+      if (j < a.n) {
+        const float nv = (v[k] - m) * inv;
+        const float gv = a.gamma[j] * nv;
+        st_f(y, a.y_dt, j, gv + a.beta[j]);
+      }
+    }
+    for (int64_t j = tid + (int64_t)kRowRegs * 256; j < a.n; j += 256) {
+      const float nv = (ld_f(x, a.x_dt, j) - m) * inv;
+      const float gv = a.gamma[j] * nv;
+      st_f(y, a.y_dt, j, gv + a.beta[j]);
+    }
+  }
+}
+
+// Fast path: one wave per row, the row held in registers as 16-byte chunks
+// (8 bf16 or 4 f32 per load), CH chunks per lane; a wave-only reduction; the
+// same op order as rmsnorm_rows_kernel (square, sum, / n, + eps, sqrt,
+// x / r, gamma * .).
+//
+// rms_row: that arithmetic for one row whose chunks are in raw (chunk k of
+// lane l holds elements (64 k + l) EPC_X ..); gam(k, e) is gamma of element
+// e of chunk k.  FULL: every chunk is in range (n == 64 CH EPC_X).
 template <int XB, int YB, int CH, bool FULL, typename Gamma>
 __device__ __forceinline__ void rms_row(const RowNormArgs& a, int64_t row, int lane,
                                         const uint4 (&raw)[CH], Gamma gam) {
@@ -318,6 +378,77 @@ __global__ void __launch_bounds__(256) rmsnorm_wg_kernel(RowNormArgs a) {
   }
 }
 
+// LayerNorm, laid out like rmsnorm_wg_kernel (one row per workgroup, thread
+// t holding chunks k 256 + t): the row sum, the mean, then the sum of the
+// centred squares from the same registers -- one read and one write of the
+// row.  Each workgroup-wide sum has its own LDS slot, so the second needs no
+// barrier before its writes.
+template <int XB, int YB, int CPL>
+__global__ void __launch_bounds__(256) layernorm_wg_kernel(RowNormArgs a) {
+  constexpr int EPC = 16 / XB;
+  __shared__ float part[2][4];
+  const int t = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  uint4 raw[CPL];
+  {
+    const char* x = (const char*)a.x + src_row(a, row) * a.x_rs * XB;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) raw[k] = *(const uint4*)(x + ((int64_t)k * 256 + t) * 16);
+  }
+  auto elem = [&](int k, int e) {
+    const uint32_t* w = (const uint32_t*)&raw[k];
+    return XB == 2 ? as_f((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16)) : as_f(w[e]);
+  };
+  if (a.xout) {  // gather form: the gathered row itself
+    char* xo = (char*)a.xout + row * a.n * XB;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) *(uint4*)(xo + ((int64_t)k * 256 + t) * 16) = raw[k];
+  }
+  float s1 = 0.0f;
+#pragma unroll
+  for (int k = 0; k < CPL; ++k)
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) s1 += elem(k, e);
+  const float m = wg_row_sum<0>(s1, part) / a.divisor;
+  float s2 = 0.0f;
+#pragma unroll
+  for (int k = 0; k < CPL; ++k)
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      const float c = elem(k, e) - m;
+      const float sq = c * c;
+      s2 += sq;
+    }
+  const float var = wg_row_sum<1>(s2, part) / a.divisor2;
+  const float inv = 1.0f / sqrtf(var + a.eps);  // rsqrt as the elementwise op computes it
+  char* y = (char*)a.y + row * a.n * YB;
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) {
+    const int64_t j = ((int64_t)k * 256 + t) * EPC;
+    float out[EPC];
+#pragma unroll
+    for (int e = 0; e < EPC; e += 4) {
+      const float4 g = *(const float4*)(a.gamma + j + e);
+      const float4 b = *(const float4*)(a.beta + j + e);
+      out[e] = g.x * ((elem(k, e) - m) * inv) + b.x;
+      out[e + 1] = g.y * ((elem(k, e + 1) - m) * inv) + b.y;
+      out[e + 2] = g.z * ((elem(k, e + 2) - m) * inv) + b.z;
+      out[e + 3] = g.w * ((elem(k, e + 3) - m) * inv) + b.w;
+    }
+    if (YB == 2) {
+      uint32_t o[EPC / 2];
+#pragma unroll
+      for (int e = 0; e < EPC; e += 2) o[e / 2] = bf16x2_bits(out[e], out[e + 1]);
+      if (EPC == 8) *(uint4*)(y + j * 2) = *(const uint4*)o;
+      else *(uint2*)(y + j * 2) = *(const uint2*)o;
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPC; e += 4)
+        *(float4*)(y + (j + e) * 4) = make_float4(out[e], out[e + 1], out[e + 2], out[e + 3]);
+    }
+  }
+}
+
 // REW_MI355X_ROWS=wave keeps the wave-per-row kernels for whole rows.
 static bool rows_wg() {
   static const bool on = [] {
@@ -347,6 +478,30 @@ void launch_rmsnorm_rows(const RowNormArgs& a, hipStream_t stream) {
   const int64_t chunks = (a.n + epc - 1) / epc;  // 16-byte chunks per row
   const bool vec = a.n % epc == 0 && (a.x_rs * xb) % 16 == 0 && ((uintptr_t)a.x & 15) == 0 &&
                    ((uintptr_t)a.y & 15) == 0 && (a.n * yb) % 16 == 0 && chunks <= 64 * 16;
+  if (a.layer) {
+    // LayerNorm: a workgroup per row of 256, 512 or 1024 chunks, else the
+    // general kernel (any shape, the gather form included)
+    if (vec && ((uintptr_t)a.gamma & 15) == 0 && ((uintptr_t)a.beta & 15) == 0 &&
+        a.rows < (1 << 30) && (chunks == 256 || chunks == 512 || chunks == 1024)) {
+      const dim3 grid((unsigned)a.rows), block(256);
+#define REW_LN(XB, YB, CPL) \
+      hipLaunchKernelGGL((layernorm_wg_kernel<XB, YB, CPL>), grid, block, 0, stream, a)
+#define REW_LN_CPL(XB, YB) \
+      if (chunks == 256) { REW_LN(XB, YB, 1); } else if (chunks == 512) { REW_LN(XB, YB, 2); } \
+      else { REW_LN(XB, YB, 4); }
+      if (xb == 2 && yb == 2) { REW_LN_CPL(2, 2); }
+      else if (xb == 2) { REW_LN_CPL(2, 4); }
+      else if (yb == 2) { REW_LN_CPL(4, 2); }
+      else { REW_LN_CPL(4, 4); }
+#undef REW_LN_CPL
+#undef REW_LN
+    } else {
+      const unsigned grid = (unsigned)(a.rows < 65536 ? a.rows : 65536);
+      hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(grid), dim3(256), 0, stream, a);
+    }
+    REW_HIP(hipGetLastError());
+    return;
+  }
   if (vec && rows_wg() && ((uintptr_t)a.gamma & 15) == 0 && a.rows < (1 << 30) &&
       (chunks == 256 || chunks == 512 || chunks == 1024) &&
       !(a.ids && !rmsnorm_gather_ok(a))) {

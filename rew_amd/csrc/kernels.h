@@ -422,6 +422,12 @@ struct RowNormArgs {
   int ids_dt;
   int64_t x_rows;
   void* xout;
+  // layer != 0: rew's LayerNorm (src/rew/nn/norm.nim:41-84) instead, op by
+  // op in fp32:  m = sum_j x_j / divisor;  c_j = x_j - m;
+  // v = sum_j c_j * c_j / divisor2;  y_j = gamma_j * (c_j * rsqrt(v + eps)) + beta_j
+  int layer;
+  const float* beta;
+  float divisor2;
 };
 void launch_rmsnorm_rows(const RowNormArgs& a, hipStream_t stream);
 // Whether launch_rmsnorm_rows runs the gather form of `a` (16-byte rows).

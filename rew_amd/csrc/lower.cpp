@@ -234,11 +234,15 @@ struct GemmPlan {
   int group = -1;
 };
 
-// rmsNorm chain (src/rew/nn/norm.nim:204-224) lowered to one row kernel.
+// rmsNorm chain (src/rew/nn/norm.nim:204-224) or LayerNorm chain
+// (norm.nim:41-84, layer) lowered to one row kernel.
 struct NormPlan {
   Tensor* src = nullptr;  // bf16 source (astype folded) or the f32 input itself
   Tensor* gamma = nullptr;
   float eps = 0.0f, divisor = 1.0f;
+  bool layer = false;
+  Tensor* beta = nullptr;  // layer: the shift
+  float divisor2 = 1.0f;   // layer: the variance's reduceMean divisor
 };
 
 // softmax chain (src/rew/nn/activation.nim:64-77) over the last axis, lowered
@@ -316,6 +320,8 @@ struct Lower {
   bool match_flash(Node* pv);
   void match_gemm_epilogues();
   void match_rows();
+  bool plan_norm(NormPlan np, Tensor* x, int x_uses, Tensor* o, std::vector<Tensor*>& inner);
+  bool match_layernorm(Node* ao);
   bool emit_norm(Tensor* t, const NormPlan& p);
   bool emit_rope(Tensor* t, const RopePlan& p);
   bool emit_softmax(Tensor* t, const SoftmaxPlan& p);
@@ -2333,6 +2339,111 @@ static std::vector<int64_t> iota_dims(int n) {
   return v;
 }
 
+// Registers a matched norm chain: its source x (an astype from bf16 with
+// `x_uses` uses, all inside the chain, is folded into the kernel's load),
+// its result o (or o's astype to bf16, its only consumer), the chain's
+// intermediates (never materialized) and, when x is an embedding lookup
+// seen through reshapes, the gather form.  False: x is neither f32 nor such
+// an astype.
+bool Lower::plan_norm(NormPlan np, Tensor* x, int x_uses, Tensor* o,
+                      std::vector<Tensor*>& inner) {
+  np.src = x;
+  if (!x->st && x->prod && x->prod->kind == K_CONVERT && x->ext == 0 && x->uses == x_uses &&
+      x->prod->in[0]->dt == kBF16) {
+    np.src = x->prod->in[0];
+    inner.push_back(x);
+  } else if (x->dt != kF32) {
+    return false;
+  }
+  Tensor* out = o;
+  Node* cv = sole_consumer(*this, o);
+  if (cv && cv->kind == K_CONVERT && cv->out[0]->dt == kBF16) {
+    inner.push_back(o);
+    out = cv->out[0];
+  }
+  for (Tensor* t : inner) t->plan_mat = false;
+  out->plan_mat = true;
+  norm_out[out] = np;
+  Tensor* s = np.src;
+  while (s && !s->st && s->prod && s->prod->kind == K_RESHAPE) s = s->prod->in[0];
+  if (s && s != np.src && !s->st && s->prod && s->prod->kind == K_INDEX_SELECT)
+    gather_norm[s] = out;
+  return true;
+}
+
+// rew's LayerNorm.forward over the last axis (normalizedShape of rank 1),
+// ending in the add node `ao`:
+//   mean = divide(reduceSum(x, [r-1]), bcast(n));  c = sub(x, bcast(mean, [0..r-2]))
+//   var = divide(reduceSum(mul(c, c), [r-1]), bcast(n))
+//   inv = rsqrt(add(var, bcast(eps)));  y = add(mul(bcast(gamma), mul(c, bcast(inv))),
+//                                              bcast(beta))
+// Each broadcast and intermediate must be used only inside the chain.
+bool Lower::match_layernorm(Node* ao) {
+  Tensor* o = ao->out[0];
+  const int r = o->shape.rank;
+  const int64_t n = o->shape.d[r - 1];
+  // a [n] f32 vector broadcast along the last axis
+  auto vec_bcast = [&](Tensor* t) -> Tensor* {
+    if (!t || t->st || !t->prod || t->prod->kind != K_BROADCAST_TO || t->ext != 0 ||
+        t->uses != 1 || !dims_are(t->prod->l1, {r - 1}))
+      return nullptr;
+    Tensor* v = t->prod->in[0];
+    return v->shape.rank == 1 && v->shape.d[0] == n && v->dt == kF32 ? v : nullptr;
+  };
+  // divide(reduceSum(v, [r-1]), bcast(const)) -> v
+  auto mean_of = [&](Tensor* t, float* dv, std::vector<Tensor*>& inner) -> Tensor* {
+    Node* md = chain_node(t, K_BINARY, 1);
+    if (!md || md->sub != 3 || !const_bcast(md->in[1], dv)) return nullptr;
+    Node* rs = chain_node(md->in[0], K_REDUCE, 1);
+    if (!rs || rs->sub != RED_SUM || !dims_are(rs->l0, {r - 1})) return nullptr;
+    inner.push_back(md->in[0]);
+    return rs->in[0];
+  };
+  for (int ord = 0; ord < 2; ++ord) {
+    Tensor* beta = vec_bcast(ao->in[1 - ord]);
+    Node* gm = chain_node(ao->in[ord], K_BINARY, 1);
+    if (!beta || !gm || gm->sub != 2) continue;
+    for (int og = 0; og < 2; ++og) {
+      Tensor* gamma = vec_bcast(gm->in[og]);
+      Node* nm = chain_node(gm->in[1 - og], K_BINARY, 1);
+      if (!gamma || !nm || nm->sub != 2) continue;
+      Tensor *cen = nm->in[0], *invB = nm->in[1];
+      Node* ib = chain_node(invB, K_BROADCAST_TO, 1);
+      if (!ib || ib->l1 != iota_dims(r - 1)) continue;
+      Node* rq = chain_node(ib->in[0], K_UNARY, 1);
+      if (!rq || rq->sub != 22) continue;  // rsqrt
+      Node* ve = chain_node(rq->in[0], K_BINARY, 1);
+      float eps, dv2, dv1;
+      if (!ve || ve->sub != 0 || !const_bcast(ve->in[1], &eps)) continue;
+      std::vector<Tensor*> inner = {ao->in[ord], ao->in[1 - ord], gm->in[og], gm->in[1 - og],
+                                    invB, ib->in[0], rq->in[0], ve->in[0]};
+      Tensor* sq = mean_of(ve->in[0], &dv2, inner);
+      Node* sqn = sq ? chain_node(sq, K_BINARY, 1) : nullptr;
+      if (!sqn || sqn->sub != 2 || sqn->in[0] != cen || sqn->in[1] != cen) continue;
+      // c feeds c * c (twice) and the normalisation
+      if (cen->st || !cen->prod || cen->prod->kind != K_BINARY || cen->prod->sub != 1 ||
+          cen->ext != 0 || cen->uses != 3)
+        continue;
+      Tensor *x = cen->prod->in[0], *meanB = cen->prod->in[1];
+      Node* mb = chain_node(meanB, K_BROADCAST_TO, 1);
+      if (!mb || mb->l1 != iota_dims(r - 1)) continue;
+      Tensor* xs = mean_of(mb->in[0], &dv1, inner);
+      if (xs != x || x->shape != o->shape) continue;
+      inner.insert(inner.end(), {sq, cen, meanB, mb->in[0]});
+      NormPlan np;
+      np.gamma = gamma;
+      np.beta = beta;
+      np.eps = eps;
+      np.divisor = dv1;
+      np.divisor2 = dv2;
+      np.layer = true;
+      // x feeds the mean's sum and c
+      if (plan_norm(np, x, 2, o, inner)) return true;
+    }
+  }
+  return false;
+}
+
 void Lower::match_rows() {
   for (Node* mo : nodes) {
     // ---- rmsNorm: mul(bcast(gamma), divide(x, bcast(sqrt(sum(x*x)/n + eps))))
@@ -2370,32 +2481,15 @@ void Lower::match_rows() {
         np.divisor = dv;
         std::vector<Tensor*> inner = {normed, rmsB, rb->in[0], sq_->in[0], ad->in[0],
                                       md->in[0], rs->in[0]};
-        np.src = x;
-        if (!x->st && x->prod && x->prod->kind == K_CONVERT && x->ext == 0 && x->uses == 3 &&
-            x->prod->in[0]->dt == kBF16) {
-          np.src = x->prod->in[0];
-          inner.push_back(x);
-        } else if (x->dt != kF32) {
-          continue;
-        }
-        Tensor* out = o;
-        Node* cv = sole_consumer(*this, o);
-        if (cv && cv->kind == K_CONVERT && cv->out[0]->dt == kBF16) {
-          inner.push_back(o);
-          out = cv->out[0];
-        }
-        for (Tensor* t : inner) t->plan_mat = false;
-        out->plan_mat = true;
-        norm_out[out] = np;
-        {
-          Tensor* s = np.src;
-          while (s && !s->st && s->prod && s->prod->kind == K_RESHAPE) s = s->prod->in[0];
-          if (s && s != np.src && !s->st && s->prod && s->prod->kind == K_INDEX_SELECT)
-            gather_norm[s] = out;
-        }
-        break;
+        if (plan_norm(np, x, 3, o, inner)) break;
       }
     }
+    // ---- LayerNorm: add(mul(bcast(gamma), mul(c, bcast(rsqrt(mean(c*c) + eps)))), bcast(beta)),
+    // c = sub(x, bcast(mean(x))), mean(v) = divide(reduceSum(v), n) (norm.nim:41-84,
+    // reduce.nim:132-150)
+    if (mo->kind == K_BINARY && mo->sub == 0 && mo->out[0]->dt == kF32 &&
+        mo->out[0]->shape.rank >= 2 && !mo->out[0]->st)
+      match_layernorm(mo);
     // ---- softmax: divide(e, bcast(reduceSum(e))), e = exp(sub(x, bcast(reduceMax(x))))
     // (only where the probabilities are materialized anyway: inside a fused
     // attention they never are)
@@ -2547,11 +2641,19 @@ bool Lower::emit_norm(Tensor* t, const NormPlan& p) {
   a.gamma = (const float*)p.gamma->data();
   a.eps = p.eps;
   a.divisor = p.divisor;
+  if (p.layer) {
+    ensure_mat(p.beta);
+    a.layer = 1;
+    a.beta = (const float*)p.beta->data();
+    a.divisor2 = p.divisor2;
+  }
   tensor_alloc(t);
   a.y = t->data();
   a.y_dt = t->dt;
   Launch L{a};
-  if (c->profiling) L.name = "rmsnorm_rows{" + std::to_string(a.rows) + "x" + std::to_string(n) + "}";
+  if (c->profiling)
+    L.name = std::string(p.layer ? "layernorm_rows{" : "rmsnorm_rows{") +
+             std::to_string(a.rows) + "x" + std::to_string(n) + "}";
   L.fused = true;
   run_launch(c, std::move(L));
   return true;
@@ -2700,6 +2802,12 @@ bool Lower::emit_gather_norm(Node* n, Tensor* t, const NormPlan& p) {
   a.gamma = (const float*)p.gamma->data();
   a.eps = p.eps;
   a.divisor = p.divisor;
+  if (p.layer) {
+    ensure_mat(p.beta);
+    a.layer = 1;
+    a.beta = (const float*)p.beta->data();
+    a.divisor2 = p.divisor2;
+  }
   a.y_dt = t->dt;
   a.xout = a.y = reinterpret_cast<void*>(uintptr_t(256));  // allocator blocks are aligned
   if (!rmsnorm_gather_ok(a)) return false;
@@ -2709,7 +2817,8 @@ bool Lower::emit_gather_norm(Node* n, Tensor* t, const NormPlan& p) {
   a.y = t->data();
   Launch L{a};
   if (c->profiling)
-    L.name = "gather_rmsnorm{" + std::to_string(a.rows) + "x" + std::to_string(nn) + "}";
+    L.name = std::string(p.layer ? "gather_layernorm{" : "gather_rmsnorm{") +
+             std::to_string(a.rows) + "x" + std::to_string(nn) + "}";
   L.fused = true;
   run_launch(c, std::move(L));
   return true;

@@ -68,6 +68,7 @@ struct PtrVisit {
   void operator()(RowNormArgs& a) {
     field(f, a.x);
     field(f, a.gamma);
+    field(f, a.beta);
     field(f, a.y);
     field(f, a.ids);
     field(f, a.xout);

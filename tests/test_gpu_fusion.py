@@ -161,6 +161,92 @@ def test_rmsnorm_row_kernel(gpu, oracle, shape, bf16):
         np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
 
 
+LN_SHAPES = [((2, 100, 4096), True), ((37, 1000), False), ((3, 9000), True),
+             ((4100, 4096), True), ((2500, 1024), False), ((300, 4096), False),
+             ((65, 2048), False), ((9, 7), True)]
+
+
+@pytest.mark.parametrize("shape,bf16", LN_SHAPES)
+def test_layernorm_row_kernel(gpu, oracle, shape, bf16):
+    """rew's LayerNorm chain (src/rew/nn/norm.nim:41-84; reduceMean as
+    reduceSum / n, reduce.nim:132-150) runs as one row kernel: a workgroup per
+    row for rows of 256, 512 or 1024 16-byte chunks, the general kernel
+    otherwise.  Checked against the oracle componentwise, relative to the
+    magnitudes the op sequence rounds on the way: |gamma| (|x| + mean |x|)
+    rsqrt(var + eps) + |beta| (the centring x - mean carries the mean's
+    absolute error whatever the summation order, and the row sums run in
+    another order than the op sequence's reductions)."""
+    key = oracle.init_key(900 + shape[-1])
+    n = shape[-1]
+    x = oracle.normal_f32(oracle.fold_in(key, 0), int(np.prod(shape)), 0.5, 2.0).reshape(shape)
+    if bf16:
+        x = oracle.round_bf16(x)
+    g = oracle.normal_f32(oracle.fold_in(key, 1), n, 1.0, 0.1)
+    b = oracle.normal_f32(oracle.fold_in(key, 2), n, 0.0, 0.1)
+    ln = nn.LayerNorm(E.fromHost(g), E.fromHost(b), [n], 1e-5)
+
+    def fn():
+        xt = E.fromHost(x, DType.BFLOAT16 if bf16 else DType.FLOAT32)
+        y = ln.forward(nn._f32(xt))
+        return nn._to(y, DType.BFLOAT16) if bf16 else y
+
+    got, names = _run(fn)
+    assert sum(k.startswith("layernorm_rows") for k in names) == 1, names
+    assert not any(k.startswith("reduce") or k.startswith("ew_") for k in names), names
+    ref, names2 = _run(fn, op_by_op=True)
+    assert not any(k.startswith("layernorm_rows") for k in names2), names2
+    x2 = x.reshape(-1, n)
+    want = oracle.layernorm_rows(x2, g, b, 1e-5).reshape(shape)
+    xd = x2.astype(np.float64)
+    inv = 1.0 / np.sqrt(xd.var(-1, keepdims=True) + 1e-5)
+    scale = (np.abs(g) * (np.abs(xd) + np.abs(xd).mean(-1, keepdims=True)) * inv +
+             np.abs(b)).reshape(shape)
+    for out in (got, ref):
+        if bf16:
+            out = _bits_f32(out)
+            # within one bf16 rounding of the fp32 reference
+            assert np.all(np.abs(out - want) <= 2.0 ** -8 * np.abs(want) + 1e-5 * scale)
+        else:
+            assert np.all(np.abs(out - want) <= 1e-5 * scale), \
+                float(np.max(np.abs(out - want) / scale))
+
+
+@pytest.mark.parametrize("ids_dt", [np.int32, np.int64])
+def test_embedding_lookup_layernorm_one_pass(gpu, oracle, ids_dt):
+    """rew's own decoder layer normalises with LayerNorm (models/llama.nim:
+    32-33, 106-117): its first norm over Embedding.lookup's rows runs as one
+    launch that writes the gathered rows (the residual) and their norm.  The
+    rows equal table[ids] (ids clamped) bit for bit, and the norm equals the
+    row kernel's on the same rows already in memory bit for bit."""
+    V, H, T = 1000, 4096, 300
+    key = oracle.init_key(4343)
+    w = oracle.round_bf16(oracle.normal_f32(key, V * H).reshape(V, H))
+    g = oracle.normal_f32(oracle.fold_in(key, 1), H, 1.0, 0.1)
+    bt = oracle.normal_f32(oracle.fold_in(key, 2), H, 0.0, 0.1)
+    ids = (np.arange(T) * 7919 % V).astype(ids_dt)
+    ids[3], ids[7] = -5, V + 11
+    table = E.fromHost(w, DType.BFLOAT16)
+    ln = nn.LayerNorm(E.fromHost(g), E.fromHost(bt), [H], 1e-5)
+
+    def fwd():
+        x = O.reshape(nn.Embedding(table).lookup(E.fromHost(ids)), [1, T, H])
+        normed = nn._to(ln.forward(nn._f32(x)), DType.BFLOAT16)
+        return O.concat([normed, x], 0)   # x is needed again (the residual)
+
+    got, names = _run(fwd)
+    assert any(n.startswith("gather_layernorm") for n in names), names
+    assert not any(n.startswith("gather_rows") or n.startswith("layernorm_rows")
+                   for n in names), names
+    rows = w[np.clip(ids.astype(np.int64), 0, V - 1)]
+    xt = E.fromHost(rows.reshape(1, T, H), DType.BFLOAT16)
+    plain, pn = _run(lambda: nn._to(ln.forward(nn._f32(xt)), DType.BFLOAT16))
+    assert any(n.startswith("layernorm_rows") for n in pn), pn
+    np.testing.assert_array_equal(got[0], plain[0])
+    np.testing.assert_array_equal(E.bf16_bits_to_f32(got[1]).reshape(T, H), rows)
+    want = oracle.layernorm_rows(rows, g, bt, 1e-5)
+    bf16_close(E.bf16_bits_to_f32(got[0]).reshape(T, H), want, 1e-2)
+
+
 @pytest.mark.parametrize("B,H,S,D,bf16", [(2, 4, 64, 128, True), (1, 3, 50, 64, False),
                                           (1, 2, 7, 32, True)])
 def test_rope_pair_kernel(gpu, oracle, B, H, S, D, bf16):

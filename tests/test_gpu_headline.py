@@ -130,10 +130,13 @@ def _linear(oracle, key, fi, fo):
     return nn.Linear(E.fromHost(w, DType.BFLOAT16), E.fromHost(b, DType.BFLOAT16)), w, b
 
 
-def test_llama_layer_full_dims(gpu, oracle):
+@pytest.mark.parametrize("norm", ["rms", "layer"])
+def test_llama_layer_full_dims(gpu, oracle, norm):
     """One sequence of the C4 configuration through rew's LlamaDecoderLayer
     op stream: the same seven launches as the bench, compared with the
-    oracle's restatement of the mixed-precision op sequence."""
+    oracle's restatement of the mixed-precision op sequence.  norm "rms" is
+    the configuration's RMSNorm; "layer" is rew's own layer, which
+    normalises with LayerNorm (src/rew/models/llama.nim:32-33, 84-85)."""
     B, S, H, nh, nkv, I = 1, 2048, 4096, 32, 8, 14336
     hd = H // nh
     key = oracle.init_key(0x5EED0004)
@@ -145,24 +148,31 @@ def test_llama_layer_full_dims(gpu, oracle):
     p["g1"] = oracle.normal_f32(ks[7], H, 1.0, 0.1)
     p["g2"] = oracle.normal_f32(ks[8], H, 1.0, 0.1)
     rope = nn.RotaryPositionEncoding.init(hd, S, 500000.0)
+    if norm == "rms":
+        n1, n2 = nn.RMSNorm(E.fromHost(p["g1"]), 1e-5), nn.RMSNorm(E.fromHost(p["g2"]), 1e-5)
+    else:
+        z = E.fromHost(np.zeros(H, np.float32))
+        n1 = nn.LayerNorm(E.fromHost(p["g1"]), z, [H], 1e-5)
+        n2 = nn.LayerNorm(E.fromHost(p["g2"]), z, [H], 1e-5)
     layer = nn.LlamaDecoderLayer(
         nn.GroupedQueryAttention(m["q"], m["k"], m["v"], m["o"], nh, nkv, hd, rope),
-        nn.GatedFeedForward(m["g"], m["u"], m["d"]),
-        nn.RMSNorm(E.fromHost(p["g1"]), 1e-5), nn.RMSNorm(E.fromHost(p["g2"]), 1e-5))
+        nn.GatedFeedForward(m["g"], m["u"], m["d"]), n1, n2)
     x = oracle.round_bf16(oracle.normal_f32(ks[9], B * S * H).reshape(B, S, H))
     E.profileBegin()
     got = E.toHostF32(layer.forward(E.fromHost(x, DType.BFLOAT16), causal=True))
     prof = E.profileEnd()
     names = [n for n, _, _ in prof]
     assert sum(c for _, c, _ in prof) == 7, names
+    kname = "rmsnorm_rows" if norm == "rms" else "layernorm_rows"
+    assert sum(c for n, c, _ in prof if n.startswith(kname)) == 2, names
     assert any(n.startswith("gemm_lds_swiglu") for n in names), names
     assert sum(n.startswith("gemm_lds_nn+bias+res") for n in names) == 2, names
     assert any(n.startswith("gemm_lds_nn{") and n.count("+rope") == 2 for n in names), names
     assert any(n.startswith("flash_attn_pp[1,32,8,2048,2048,128") for n in names), names
     c, s = nn.rope_tables(hd, S, 500000.0)
-    want = oracle.llama_layer(x, p, nh, nkv, c, s, 1e-5, True, True, "rms")
+    want = oracle.llama_layer(x, p, nh, nkv, c, s, 1e-5, True, True, norm)
     err = bf16_err(got, want)
-    print(f"llama layer [1,2048,4096] normwise relative error {err:.3e}")
+    print(f"llama layer [1,2048,4096] ({norm}) normwise relative error {err:.3e}")
     assert err <= 2e-2
 
 

@@ -180,6 +180,26 @@ def test_layernorm_moments(oracle):
     np.testing.assert_allclose(out.var(-1), 1.0, rtol=1e-4)
 
 
+def test_layernorm_affine_float64(oracle):
+    """LayerNorm with a non-trivial scale and shift (norm.nim:41-84:
+    gamma * ((x - mean) * rsqrt(var + eps)) + beta) against a float64
+    statement; a swapped gamma / beta, a dropped eps or the variance taken
+    around 0 instead of the mean all fail it."""
+    rng = np.random.default_rng(11)
+    x = rng.normal(1.5, 2.0, size=(64, 300)).astype(np.float32)
+    g = rng.normal(1.0, 0.3, size=300).astype(np.float32)
+    b = rng.normal(0.0, 0.5, size=300).astype(np.float32)
+    eps = 0.25  # large, so that dropping it shows
+    out = oracle.layernorm_rows(x, g, b, eps)
+    xd = x.astype(np.float64)
+    m = xd.mean(-1, keepdims=True)
+    v = ((xd - m) ** 2).mean(-1, keepdims=True)
+    want = g * ((xd - m) / np.sqrt(v + eps)) + b
+    np.testing.assert_allclose(out, want, rtol=1e-5, atol=1e-5)
+    assert not np.allclose(oracle.layernorm_rows(x, b, g, eps), want, atol=1e-3)
+    assert not np.allclose(oracle.layernorm_rows(x, g, b, 0.0), want, atol=1e-3)
+
+
 def test_rope_properties(oracle):
     c, s = oracle.rope_tables(8, 16, 10000.0)
     np.testing.assert_allclose(c * c + s * s, 1.0, rtol=1e-6)
