@@ -431,7 +431,10 @@ __global__ void __launch_bounds__(256) bn_feature_kernel(BatchNormArgs a) {
 
 void launch_batchnorm(const BatchNormArgs& a, hipStream_t stream) {
   const int64_t total = a.outer * a.C * a.inner;
-  if (total == 0) return;
+  // an empty batch (outer * inner == 0, C > 0) still writes the [C] outputs
+  // of training and grad: 0 / 0 = NaN statistics and zero gradient sums, as
+  // the feature kernel's empty loops give
+  if (a.C == 0 || (total == 0 && a.mode == kBnInference)) return;
   if (a.mode == kBnInference) {
     const unsigned grid = index_map_grid(total);
     if (a.f64) hipLaunchKernelGGL(bn_inference_kernel<double>, dim3(grid), dim3(256), 0, stream, a);

@@ -3166,7 +3166,7 @@ static void lower_graph(Ctx* c, Lower& L, const std::string* sig,
     L.cons = consumers;
     L.match_flash_out();
     L.match_gemm_epilogues();
-    L.match_moe();
+    if (!c->dense_moe) L.match_moe();
     L.match_rows();
     L.match_gemm_groups();
   }

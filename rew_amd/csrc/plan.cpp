@@ -325,7 +325,7 @@ std::string flush_signature(Ctx* c, const std::vector<Node*>& nodes,
     put(sh.d, (size_t)sh.rank * 8);
   };
   i32(c->mode);
-  i32((c->no_fusion_patterns ? 1 : 0) | (c->profiling ? 2 : 0));
+  i32((c->no_fusion_patterns ? 1 : 0) | (c->profiling ? 2 : 0) | (c->dense_moe ? 4 : 0));
   std::unordered_map<const Tensor*, std::pair<int32_t, int32_t>> where;
   std::unordered_map<const Tensor*, int32_t> leaf_of;
   std::unordered_map<const Storage*, int32_t> slot_of;

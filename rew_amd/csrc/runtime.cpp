@@ -59,6 +59,15 @@ void* Allocator::get(size_t bytes, size_t* rounded) {
     in_use += *rounded;
     return p;
   }
+  if (cap && in_use + cached + r > cap) {
+    trim();
+    if (in_use + r > cap)
+      fail(REW_MI355X_ERR_OOM, "device allocation of " + std::to_string(r) +
+                                   " bytes failed on mi355x:" + std::to_string(ordinal) +
+                                   " (limit REW_MI355X_MAX_DEVICE_BYTES = " +
+                                   std::to_string(cap) + ", " + std::to_string(in_use) +
+                                   " bytes in use)");
+  }
   void* p = nullptr;
   hipError_t e = hipMalloc(&p, r);
   if (e != hipSuccess) {
@@ -338,6 +347,10 @@ int rew_mi355x_init(int ordinal, rew_mi355x_ctx** out) {
         if (s[0] == '1') c->no_fusion_patterns = true;
       if (const char* s = std::getenv("REW_MI355X_PLAN_CACHE"))
         if (s[0] == '0') c->plan_cache = false;
+      if (const char* s = std::getenv("REW_MI355X_DENSE_MOE"))
+        if (s[0] == '1') c->dense_moe = true;
+      if (const char* s = std::getenv("REW_MI355X_MAX_DEVICE_BYTES"))
+        c->alloc.cap = (size_t)std::strtoull(s, nullptr, 10);
       g_ctx[ordinal] = c;
     }
     *out = reinterpret_cast<rew_mi355x_ctx*>(g_ctx[ordinal]);

@@ -93,6 +93,9 @@ struct Allocator {
   std::multimap<size_t, void*> free_blocks;
   size_t cached = 0;   // bytes in free_blocks
   size_t in_use = 0;   // bytes handed out
+  // most device bytes the allocator may hold (handed out + cached); 0: no
+  // limit but the device's (REW_MI355X_MAX_DEVICE_BYTES)
+  size_t cap = 0;
   int ordinal = 0;
   void* get(size_t bytes, size_t* rounded);
   void put(void* p, size_t rounded);
@@ -114,6 +117,10 @@ struct Ctx {
   int mode = REW_MI355X_MODE_DEFERRED;
   int flush_threshold = 4096;
   bool no_fusion_patterns = false;  // REW_MI355X_NO_PATTERNS=1: per-op kernels only
+  // REW_MI355X_DENSE_MOE=1: DeepSeekMoE's dense expert loop runs as written
+  // (every routed expert on every token), not as the routed rewrite, whose
+  // results equal the dense chain's only while every expert output is finite
+  bool dense_moe = false;
   rew_mi355x_stats stats{};
   int64_t jit_hits_base = 0;  // jit_cache_hits() when the stats were last reset
   int64_t compiled_base = 0, loaded_base = 0;  // program counters at the last reset

@@ -25,6 +25,7 @@
 // through the same fused kernels (flash attention, GEMM epilogues, routed
 // MoE) as the eager op stream and is launched at the next flush.
 #include <cmath>
+#include <cerrno>
 #include <cstring>
 #include <deque>
 #include <memory>
@@ -61,7 +62,7 @@ struct Op {
   std::string word;             // compare direction
   std::string bytes;            // constant raw bytes
   bool splat = false;           // constant dense<number>
-  double splat_v = 0.0;
+  std::string splat_text;       // the number as written ("1", "-2.5e-3", "0xFF800000")
   Attrs attrs;                  // generic attribute dictionary (raw values)
   std::vector<std::vector<int>> region_args;
   std::vector<std::vector<Op>> regions;
@@ -574,19 +575,34 @@ class Parser {
         expect("\"");
       } else if (eat_word("true")) {
         op->splat = true;
-        op->splat_v = 1.0;
+        op->splat_text = "1";
       } else if (eat_word("false")) {
         op->splat = true;
-        op->splat_v = 0.0;
+        op->splat_text = "0";
       } else {
-        const char* b = s_ + p_;
-        char* e = nullptr;
-        op->splat_v = std::strtod(b, &e);
-        if (e == b)
+        // a decimal number, or an unquoted hex literal (MLIR's form of a
+        // float's bit pattern, e.g. dense<0xFF800000> for -inf)
+        size_t len = 0;
+        while (p_ + len < n_ && (std::isalnum((unsigned char)s_[p_ + len]) ||
+                                 s_[p_ + len] == '.' || s_[p_ + len] == '+' ||
+                                 s_[p_ + len] == '-'))
+          ++len;
+        const std::string tok(s_ + p_, len);
+        bool ok = len > 0;
+        if (ok && (tok.rfind("0x", 0) == 0 || tok.rfind("0X", 0) == 0)) {
+          ok = tok.size() > 2 && tok.size() <= 18 &&
+               tok.find_first_not_of("0123456789abcdefABCDEF", 2) == std::string::npos;
+        } else if (ok) {
+          char* e = nullptr;
+          (void)std::strtod(tok.c_str(), &e);
+          ok = e == tok.c_str() + tok.size();
+        }
+        if (!ok)
           unsupported(who_ + ": StableHLO text line " + std::to_string(line_at(p_)) +
                       ": only hex and splat dense constants are supported");
-        p_ += (size_t)(e - b);
+        p_ += len;
         op->splat = true;
+        op->splat_text = tok;
       }
       expect(">");
       op->res_ty = signature(&op->bare_sig);
@@ -975,6 +991,63 @@ class Translator {
     if (o.res_ty.size() != 1) fail_at(o, "expected one result");
   }
 
+  // One element of a splat constant of type t, little-endian, into `one`.
+  // An unquoted hex literal is the element's bit pattern and must fit it.
+  // Integer types take integers only, parsed exactly (no detour through
+  // double) and range-checked; float types round the decimal value.
+  void splat_element(const Op& o, const Ty& t, uint8_t* one) {
+    const std::string& tok = o.splat_text;
+    const int size = dt_size(t.dt);
+    if (tok.rfind("0x", 0) == 0 || tok.rfind("0X", 0) == 0) {
+      if ((int)tok.size() - 2 > 2 * size)
+        fail_at(o, "hex constant " + tok + " is wider than " + t.text,
+                REW_MI355X_ERR_UNSUPPORTED);
+      const uint64_t bits = std::strtoull(tok.c_str() + 2, nullptr, 16);
+      std::memcpy(one, &bits, (size_t)size);
+      return;
+    }
+    if (dt_is_int(t.dt)) {
+      if (tok.find_first_not_of("0123456789", tok[0] == '-' || tok[0] == '+' ? 1 : 0) !=
+              std::string::npos || tok.size() < (tok[0] == '-' || tok[0] == '+' ? 2u : 1u))
+        fail_at(o, "integer constant " + tok + " of type " + t.text + " is not an integer",
+                REW_MI355X_ERR_UNSUPPORTED);
+      const bool neg = tok[0] == '-';
+      errno = 0;
+      const uint64_t mag = std::strtoull(tok.c_str() + (neg || tok[0] == '+' ? 1 : 0), nullptr, 10);
+      const int bits = 8 * size;
+      const bool sgn = dt_is_signed(t.dt);
+      const uint64_t max_pos = sgn ? (bits == 64 ? (uint64_t)INT64_MAX : (1ull << (bits - 1)) - 1)
+                                   : (bits == 64 ? UINT64_MAX : (1ull << bits) - 1);
+      const uint64_t max_neg = sgn ? (bits == 64 ? (uint64_t)INT64_MAX + 1 : 1ull << (bits - 1))
+                                   : 0;
+      if (errno == ERANGE || (neg ? mag > max_neg : mag > max_pos))
+        fail_at(o, "integer constant " + tok + " is out of range for " + t.text,
+                REW_MI355X_ERR_INVALID);
+      const uint64_t u = neg ? (uint64_t)0 - mag : mag;  // two's complement
+      std::memcpy(one, &u, (size_t)size);
+      return;
+    }
+    const double v = std::strtod(tok.c_str(), nullptr);
+    switch (t.dt) {
+      case kF32: { float f = (float)v; std::memcpy(one, &f, 4); break; }
+      case kF64: std::memcpy(one, &v, 8); break;
+      case kBF16: {
+        float f = (float)v;
+        uint32_t u;
+        std::memcpy(&u, &f, 4);
+        const uint16_t h = std::isnan(f) ? (uint16_t)((u >> 16) | 0x40u)
+                                         : (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+        std::memcpy(one, &h, 2);
+        break;
+      }
+      case kF16: { _Float16 h = (_Float16)v; std::memcpy(one, &h, 2); break; }
+      case kBool: one[0] = v != 0.0; break;
+      default:
+        fail_at(o, "decimal constant of type " + t.text + " not supported (write its bits "
+                   "as hex)", REW_MI355X_ERR_UNSUPPORTED);
+    }
+  }
+
   void constant(const Op& o) {
     const Ty& t = o.res_ty.at(0);
     const Shape s(t.d);
@@ -985,26 +1058,7 @@ class Translator {
     if (o.splat) {
       host.resize((size_t)bytes);
       std::vector<uint8_t> one(dt_size(t.dt));
-      const double v = o.splat_v;
-      switch (t.dt) {
-        case kF32: { float f = (float)v; std::memcpy(one.data(), &f, 4); break; }
-        case kF64: std::memcpy(one.data(), &v, 8); break;
-        case kBF16: {
-          float f = (float)v;
-          uint32_t u;
-          std::memcpy(&u, &f, 4);
-          const uint16_t h = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
-          std::memcpy(one.data(), &h, 2);
-          break;
-        }
-        case kF16: { _Float16 h = (_Float16)v; std::memcpy(one.data(), &h, 2); break; }
-        case kBool: one[0] = v != 0.0; break;
-        default: {
-          const int64_t iv = (int64_t)v;
-          std::memcpy(one.data(), &iv, one.size());  // little-endian truncation
-          break;
-        }
-      }
+      splat_element(o, t, one.data());
       for (int64_t i = 0; i < s.numel(); ++i)
         std::memcpy(&host[(size_t)(i * one.size())], one.data(), one.size());
     } else {

@@ -207,6 +207,43 @@ def test_reduce_with_a_non_identity_init(gpu):
     np.testing.assert_array_equal(E.toHost(r), x.sum(1) + 10.0)
 
 
+def test_splat_constants_exact(gpu):
+    """Splat constants as MLIR prints them: integers beyond 2^53 and at the
+    ends of their type's range are taken exactly, and an unquoted hex splat is
+    the element's bit pattern (dense<0xFF800000> is -inf in f32).  An integer
+    splat out of its type's range is an error, not a wrapped value."""
+    text = """module @m {
+  func.func @main(%v1: tensor<2xf32>) -> (tensor<3xi64>, tensor<3xi64>, tensor<2xui64>, tensor<2xf32>) {
+    %v2 = stablehlo.constant dense<9007199254740993> : tensor<3xi64>
+    %v3 = stablehlo.constant dense<-9223372036854775808> : tensor<3xi64>
+    %v4 = stablehlo.constant dense<18446744073709551615> : tensor<2xui64>
+    %v5 = stablehlo.constant dense<0xFF800000> : tensor<2xf32>
+    %v6 = stablehlo.add %v1, %v5 : tensor<2xf32>
+    func.return %v2, %v3, %v4, %v6 : tensor<3xi64>, tensor<3xi64>, tensor<2xui64>, tensor<2xf32>
+  }
+}
+"""
+    outs = J.executeJit("splats", "k", text, [E.fromHost(np.ones(2, np.float32))],
+                        [DType.INT64, DType.INT64, DType.UINT64, DType.FLOAT32],
+                        [[3], [3], [2], [2]])
+    r5, r7, r9, r11 = (E.toHost(t) for t in outs)
+    np.testing.assert_array_equal(r5, [9007199254740993] * 3)
+    np.testing.assert_array_equal(r7, [np.iinfo(np.int64).min] * 3)
+    np.testing.assert_array_equal(r9, [np.iinfo(np.uint64).max] * 2)
+    assert np.all(np.isneginf(r11))
+    bad = """module @m {
+  func.func @main(%v1: tensor<2xui8>) -> tensor<2xui8> {
+    %v2 = stablehlo.constant dense<300> : tensor<2xui8>
+    %v3 = stablehlo.add %v1, %v2 : tensor<2xui8>
+    func.return %v3 : tensor<2xui8>
+  }
+}
+"""
+    with pytest.raises(E.EagerError, match="integer constant 300 is out of range"):
+        J.executeJit("badsplat", "k", bad, [E.fromHost(np.zeros(2, np.uint8))],
+                     [DType.UINT8], [[2]])
+
+
 def test_donated_input_is_rejected_afterwards(gpu):
     j = J.jit(lambda a: [O.add(a[0], a[0])], "donate", donateArgs=[0])
     x = f32([1, 2])

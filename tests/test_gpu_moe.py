@@ -228,3 +228,66 @@ def test_direct_routed_ffn_rejects_bad_arguments(gpu, oracle):
         E.moeRoutedFfn(xt, start, topW, topI, moe.routedExperts[:2], [1, 1], 8)
     with pytest.raises(E.EagerError, match="outside"):
         E.moeRoutedFfn(xt, start, topW, topI, moe.routedExperts[:1], [8], 8)
+
+
+DENSE_CHILD = r"""
+import json, os, sys
+import numpy as np
+root = sys.argv[1]
+for p in (root, root + "/tests", root + "/oracle"):
+    sys.path.insert(0, p)
+import oracle as orc
+from test_gpu_moe import build_moe, inf_expert
+from rew_amd import eager as E
+from rew_amd.eager import DType
+E.installEagerBackend(E.mi355x(0))
+moe, host = build_moe(orc, 64, 128, 64, 8, 2, 1, 0x5EED0606)
+inf_expert(moe, 3)
+xt = E.fromHost(host["x"], DType.BFLOAT16)
+E.profileBegin()
+got = E.toHostF32(moe.forward(xt))
+names = [n for n, _, _ in E.profileEnd()]
+E.setMode(E.MODE_OP_BY_OP)
+ref = E.toHostF32(moe.forward(xt))
+E.setMode(E.MODE_DEFERRED)
+print(json.dumps({"names": names, "equal": bool(np.array_equal(got, ref, equal_nan=True)),
+                  "finite_rows": int(np.all(np.isfinite(got), axis=1).sum())}))
+"""
+
+
+def inf_expert(moe, e):
+    """Routed expert e's down projection gets a bias of +inf (bf16 0x7F80), so
+    its output is inf on every token."""
+    d = moe.routedExperts[e].downProj
+    H = d.weight.shape[1]
+    d.bias = E.fromHost(np.full(H, 0x7F80, np.uint16), DType.BFLOAT16)
+
+
+def test_dense_moe_switch_keeps_rews_nonfinite_semantics(gpu, oracle):
+    """REW_MI355X_DENSE_MOE=1 runs DeepSeekMoE's expert loop as written: with
+    one routed expert overflowing, every token's dense sum picks up
+    bf16(inf * 0) = NaN from it, exactly as the op-by-op chain does.  By
+    default the routed rewrite evaluates that expert only on its own tokens,
+    so the other tokens stay finite (the documented difference)."""
+    import json
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = Path(__file__).resolve().parents[1]
+    env = dict(os.environ, REW_MI355X_DENSE_MOE="1")
+    r = subprocess.run([sys.executable, "-c", DENSE_CHILD, str(root)], env=env,
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-3000:]
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    assert not any(n.startswith("moe_") for n in res["names"]), res["names"]
+    assert res["equal"] and res["finite_rows"] == 0, res
+    moe, host = build_moe(oracle, 64, 128, 64, 8, 2, 1, 0x5EED0606)
+    inf_expert(moe, 3)
+    E.profileBegin()
+    got = E.toHostF32(moe.forward(E.fromHost(host["x"], DType.BFLOAT16)))
+    names = [n for n, _, _ in E.profileEnd()]
+    assert any(n.startswith("moe_gemm_swiglu") for n in names), names
+    _, ids = moe.route(E.fromHost(host["x"], DType.BFLOAT16))
+    off = ~np.any(E.toHost(ids) == 3, axis=1)
+    assert off.any() and np.all(np.isfinite(got[off])), int(off.sum())

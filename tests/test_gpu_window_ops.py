@@ -201,6 +201,24 @@ def test_batch_norm_known_answers(mode):
     np.testing.assert_allclose(host(do), [0.2, 0.2], rtol=1e-6)
 
 
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_batch_norm_empty_batch(mode, dt):
+    """An empty batch ([0, C], feature dim 1) still gives the [C] outputs:
+    batchNormTraining's mean and variance are 0 / 0 = NaN, batchNormGrad's
+    gradient sums over no elements are 0, and the [0, C] results are empty."""
+    C = 5
+    x = np.zeros((0, C), dt)
+    sc, of = np.ones(C, dt), np.zeros(C, dt)
+    y, m, v = O.batchNormTraining(dev(x), dev(sc), dev(of), 1e-3, 1)
+    assert host(y).shape == (0, C)
+    assert np.all(np.isnan(host(m))) and np.all(np.isnan(host(v)))
+    dx, ds, do = O.batchNormGrad(dev(x), dev(sc), dev(np.zeros(C, dt)), dev(np.ones(C, dt)),
+                                 dev(x), 1e-3, 1)
+    assert host(dx).shape == (0, C)
+    np.testing.assert_array_equal(host(ds), 0)
+    np.testing.assert_array_equal(host(do), 0)
+
+
 @pytest.mark.parametrize("dt,shape,fi", [(np.float32, (8, 16, 33), 1), (np.float64, (5, 7), 0),
                                          (np.float32, (4, 3, 2, 64), 3)])
 def test_batch_norm_against_oracle(mode, oracle, dt, shape, fi):
