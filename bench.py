@@ -522,7 +522,9 @@ def run_chain(args, steps=None, warmup=None):
         if name.startswith("ew_"):  # the relu chain, or the [8192] divide of reduceMean
             return groups["relu_chain"] if name.startswith(f"ew_fused{{{R * Cn}x") else 3 * R * 4
         if name.startswith("reduce"):
-            return nbytes + R * 4
+            # one read of x; one [R] output per op, plus reduceMean's quotient
+            ops = int(name.split("ops")[0].rsplit(",", 1)[1]) if "ops" in name else 1
+            return nbytes + R * 4 * (ops + (1 if ",mean" in name else 0))
         return None
 
     syms = by_symbol(prof, bytes_of)

@@ -96,10 +96,30 @@ __global__ void __launch_bounds__(256) reduce_small_kernel(Program P, Space S,
   }
 }
 
+// reduceMean's divide after an interpreted reduction: y = x / d (f32)
+__global__ void __launch_bounds__(256) div_scalar_kernel(const float* x, float* y, uint32_t n,
+                                                         float d) {
+  for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) y[i] = x[i] / d;
+}
+
 void launch_reduce(const vm::Program& P, const vm::Space& S,
                    const ReduceArgs& A, bool vec, hipStream_t stream) {
   if (A.n_out == 0) return;
   if (jit_launch_reduce(P, S, A, vec, stream)) return;
+  if (A.n_mean > 0) {
+    // the interpreter stores the sums, then divides them
+    ReduceArgs plain = A;
+    plain.n_mean = 0;
+    launch_reduce(P, S, plain, vec, stream);
+    const unsigned blocks = (A.n_out + 255) / 256 < 65536 ? (A.n_out + 255) / 256 : 65536;
+    for (int x = 0; x < A.n_mean; ++x) {
+      const void* src = A.mean_src[x] ? A.extra_out[A.mean_src[x] - 1] : A.out;
+      hipLaunchKernelGGL(div_scalar_kernel, dim3(blocks), dim3(256), 0, stream,
+                         (const float*)src, (float*)A.mean_out[x], A.n_out, A.mean_div[x]);
+    }
+    REW_HIP(hipGetLastError());
+    return;
+  }
   if (A.n_extra > 0) {
     // the interpreter reduces one op per pass
     for (int x = -1; x < A.n_extra; ++x) {

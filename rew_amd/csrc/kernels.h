@@ -44,6 +44,14 @@ struct ReduceArgs {
   int n_extra = 0;
   int extra_op[3] = {0, 0, 0};
   void* extra_out[3] = {nullptr, nullptr, nullptr};
+  // reduceMean's divide (src/rew/ops/reduce.nim:132-150) at the store: f32
+  // output mean_out[i] = acc / mean_div[i] (IEEE fp32 division) of
+  // accumulator mean_src[i] (0: the main op, x: extra op x - 1), a RED_SUM
+  // with out_dtype f32
+  int n_mean = 0;
+  int mean_src[2] = {0, 0};
+  float mean_div[2] = {1.0f, 1.0f};
+  void* mean_out[2] = {nullptr, nullptr};
 };
 // Space = [kept..., reduced...]; program output 0 names the value register.
 void launch_reduce(const vm::Program& P, const vm::Space& S,

@@ -50,6 +50,9 @@ static bool is_ew(int k) {
 // Consumers that read an operand through a fused prologue.
 static bool takes_expression(int k) { return is_ew(k) || is_view(k) || k == K_REDUCE; }
 
+// Value of broadcastTo(scalar f32 constant, shape, []) (defined with the matchers).
+static bool const_bcast(Tensor* t, float* val);
+
 // ---------------------------------------------------------------------------
 // affine index maps: kernel coordinates -> tensor coordinates
 // ---------------------------------------------------------------------------
@@ -1127,6 +1130,33 @@ void Lower::emit_reduce(Node* n) {
         A.extra_op[A.n_extra] = m->sub;
         A.extra_out[A.n_extra++] = m->out[0]->data();
       }
+      // reduceMean (reduce.nim:132-150): divide(sum, broadcastTo(n)) of this
+      // sum or of a repeat of it in this flush, stored by the same pass
+      if (out->dt == kF32 && !cons.empty()) {
+        for (int src = 0; src <= (int)sib.size() && A.n_mean < 2; ++src) {
+          Node* rn = src ? sib[src - 1] : n;
+          if (rn->sub != RED_SUM) continue;
+          for (Node* q : nodes) {
+            if (q->kind != K_REDUCE || q->in[0] != x || q->l0 != rn->l0 || q->sub != RED_SUM ||
+                q->out[0]->dt != kF32)
+              continue;
+            auto ci = cons.find(q->out[0]);
+            if (ci == cons.end()) continue;
+            for (Node* d : ci->second) {
+              float dv;
+              Tensor* dt_ = d->out[0];
+              if (A.n_mean == 2 || d->kind != K_BINARY || d->sub != 3 ||
+                  d->in[0] != q->out[0] || !const_bcast(d->in[1], &dv) || dt_->dt != kF32 ||
+                  dt_->shape != out->shape || dt_->st || !dt_->plan_mat)
+                continue;
+              tensor_alloc(dt_);
+              A.mean_src[A.n_mean] = src;
+              A.mean_div[A.n_mean] = dv;
+              A.mean_out[A.n_mean++] = dt_->data();
+            }
+          }
+        }
+      }
       const bool vec = n_red > 0 && (dims.back() % kVec) == 0 &&
                        (n_red % kVec) == 0 && space.d[X.rank - 1] != 1;
       set_leaf_modes(g.P, S, vec);
@@ -1134,7 +1164,8 @@ void Lower::emit_reduce(Node* n) {
       if (c->profiling)
         L.name = "reduce{" + std::to_string(n_out) + "x" + std::to_string(n_red) + "x" +
                  std::to_string(g.P.n_ins) +
-                 (sib.empty() ? "" : "," + std::to_string(1 + sib.size()) + "ops") + "}";
+                 (sib.empty() ? "" : "," + std::to_string(1 + sib.size()) + "ops") +
+                 (A.n_mean ? ",mean" : "") + "}";
       L.fused = g.P.n_ins > 1 || !sib.empty();
       run_launch(c, std::move(L));
       reduce_done[key] = out;

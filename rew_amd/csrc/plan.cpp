@@ -45,6 +45,7 @@ struct PtrVisit {
     program_ptrs(l.P, f);
     field(f, l.A.out);
     for (int i = 0; i < l.A.n_extra; ++i) field(f, l.A.extra_out[i]);
+    for (int i = 0; i < l.A.n_mean; ++i) field(f, l.A.mean_out[i]);
   }
   void operator()(GemmL& l) {
     for (GemmArgs& g : l.g) {

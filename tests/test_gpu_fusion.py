@@ -476,6 +476,68 @@ def test_repeated_reduction_runs_once(gpu, oracle):
     np.testing.assert_allclose(got, (s + s / 1024).astype(np.float32), rtol=1e-5)
 
 
+MEAN_CHILD = r"""
+import json, sys
+import numpy as np
+sys.path.insert(0, sys.argv[1])
+from rew_amd import eager as E, nn, ops as O
+E.installEagerBackend(E.mi355x(0))
+shape, axes = json.loads(sys.argv[2])
+x = np.load(sys.argv[3])
+y = nn.relu(O.add(E.fromHost(x), E.fromHost(x)))
+outs = [O.reduceSum(y, axes), O.reduceMean(y, axes), O.reduceMax(y, axes)]
+np.save(sys.argv[4], np.stack([E.toHost(t) for t in outs]))
+"""
+
+
+@pytest.mark.parametrize("shape,axes", [((128, 1024), [1]), ((64, 100), [1]), ((8, 16, 300), [2])])
+def test_reduce_mean_divide_in_the_reduction(gpu, oracle, shape, axes, tmp_path):
+    """reduceMean is reduceSum then divide by the broadcast count
+    (src/rew/ops/reduce.nim:132-150).  Next to a reduceSum and a reduceMax of
+    the same tensor (the C2 chain), the divide is stored by the reduction's
+    own pass: one launch for the three results, equal to op-by-op bit for
+    bit (the same sum divided by the same fp32 constant).  The interpreter
+    (REW_MI355X_JIT=0) stores the sums and divides them afterwards: its mean
+    is its own sum / n exactly."""
+    import json
+    import subprocess
+    import sys
+    from pathlib import Path
+    x = oracle.normal_f32(oracle.init_key(970 + shape[-1]), int(np.prod(shape))).reshape(shape)
+
+    def fn():
+        y = nn.relu(O.add(E.fromHost(x), E.fromHost(x)))
+        return [O.reduceSum(y, axes), O.reduceMean(y, axes), O.reduceMax(y, axes)]
+
+    E.profileBegin()
+    got = [E.toHost(t) for t in fn()]
+    prof = E.profileEnd()
+    assert [n for n, _, _ in prof if n.startswith("reduce")] and \
+        sum(c for n, c, _ in prof if n.startswith("reduce") and ",mean" in n) == 1, prof
+    assert not any(n.startswith("ew_") for n, _, _ in prof), prof
+    E.setMode(E.MODE_OP_BY_OP)
+    try:
+        ref = [E.toHost(t) for t in fn()]
+    finally:
+        E.setMode(E.MODE_DEFERRED)
+    for g_, r_ in zip(got, ref):
+        np.testing.assert_array_equal(g_, r_)
+    n = int(np.prod([shape[a] for a in axes]))
+    np.testing.assert_array_equal(got[1], got[0] / np.float32(n))
+    np.save(tmp_path / "x.npy", x)
+    root = Path(__file__).resolve().parents[1]
+    env = dict(__import__("os").environ, REW_MI355X_JIT="0")
+    r = subprocess.run([sys.executable, "-c", MEAN_CHILD, str(root), json.dumps([shape, axes]),
+                        str(tmp_path / "x.npy"), str(tmp_path / "out.npy")], env=env,
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-3000:]
+    interp = np.load(tmp_path / "out.npy")
+    # the interpreter sums in its own order: its mean is its sum / n exactly
+    np.testing.assert_array_equal(interp[1], interp[0] / np.float32(n))
+    np.testing.assert_allclose(interp[0], got[0], rtol=1e-5)
+    np.testing.assert_array_equal(interp[2], got[2])
+
+
 @pytest.mark.parametrize("shape,axes", [((128, 1024), [1]), ((64, 100), [1]), ((8, 16, 300), [2])])
 def test_sibling_reductions_one_pass(gpu, oracle, shape, axes):
     """reduceSum, reduceMax and reduceMin of one tensor over the same axes
