@@ -780,6 +780,9 @@ def run_mnist(args, steps=None, warmup=None):
     flops = 2 * B * D * Hd + 2 * B * Hd * C
 
     def gemm_flops(name):
+        if name.startswith("class_head{"):  # the last Linear, softmax and argmax
+            m, k, n = (int(v) for v in name[11:name.index("}")].split("x"))
+            return 2 * m * k * n
         f = entry_flops(name)
         return f if f is not None and name.startswith("gemm") else None
 

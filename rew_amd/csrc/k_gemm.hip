@@ -126,24 +126,29 @@ __global__ void __launch_bounds__(256) gemm_generic_kernel(GemmArgs g) {
 // MLP's 128 x 784 x 128): the time is one output's k-chain plus the memory
 // latency in front of it, so every thread owns one output of a 16 x 16 tile
 // (sixteen times the generic kernel's workgroups).  WHOLE: the tile's whole
-// A (16 x K) and B (K x 16) slabs are loaded into LDS at once, one round of
-// loads in flight together, then the chains run; otherwise 64-deep chunks,
-// the next one loaded into registers while the current one is multiplied.
+// A (16 x K) and B (K x 16) slabs are loaded into LDS, both k-contiguous
+// (A's rows, B's columns, at a pitch of an odd number of 16-byte chunks so
+// that the 16 columns' 16-byte reads hit distinct banks), then each chain
+// reads four k-steps of both operands per pair of 16-byte LDS reads;
+// otherwise 64-deep chunks, the next one loaded into registers while the
+// current one is multiplied.
 // Each output is the same sequential fmaf chain over k = 0, 1, ... with zero
 // terms past K (to a multiple of 16) as gemm_generic_kernel's, so the
 // kernels give the same bits.
-constexpr int kSmallWholeK = 1024;  // WHOLE mode: 16-padded K up to this (136 KiB of LDS)
+constexpr int kSmallWholeK = 1024;  // WHOLE mode: 16-padded K up to this (129 KiB of LDS)
 
 template <bool WHOLE>
 __global__ void __launch_bounds__(256) gemm_f32_small_kernel(GemmArgs g) {
-  extern __shared__ float sm[];  // As [KC][17] then Bs [KC][17], KC = 64 or padded K
+  // WHOLE: As [16][KP] then Bs [16][KP] (k-contiguous, KP = padded K + 4);
+  // chunked: As [64][17] then Bs [64][17]
+  extern __shared__ float sm[];
   const int tid = threadIdx.x;
   const int r = tid >> 4, cc = tid & 15;
   const int64_t m0 = (int64_t)blockIdx.y * 16, n0 = (int64_t)blockIdx.x * 16;
   const int K16 = (int)((g.K + 15) & ~15);
-  const int KC = WHOLE ? K16 : 64;
+  const int KP = K16 + 4;
   float* As = sm;
-  float* Bs = sm + KC * 17;
+  float* Bs = sm + (WHOLE ? 16 * KP : 64 * 17);
   for (int64_t b = blockIdx.z; b < g.batch; b += gridDim.z) {
     if constexpr (WHOLE) {
       // A slab 16 x K16: 16 threads per row; B slab K16 x 16: 4 threads per
@@ -156,43 +161,61 @@ __global__ void __launch_bounds__(256) gemm_f32_small_kernel(GemmArgs g) {
                        g.a_sb % 4 == 0 && g.b_sb % 4 == 0 && ((uintptr_t)g.a & 15) == 0 &&
                        ((uintptr_t)g.b & 15) == 0;
       if (vec) {
+        // the slabs move in batches of kB 16-byte loads per operand, each
+        // batch's loads issued before its LDS stores (one memory latency per
+        // batch rather than per k-step): unconditional loads from clamped
+        // addresses, out-of-range values replaced by zeros after
+        constexpr int kB = 4;
         const float* ap = (const float*)g.a + b * g.a_sb + (ma < g.M ? ma : 0) * g.a_sm;
-        for (int k = la * 4; k < K16; k += 64) {
-          float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-          if (ma < g.M && k < g.K) v = *(const float4*)(ap + k);
-          As[k * 17 + ra] = v.x;
-          As[(k + 1) * 17 + ra] = v.y;
-          As[(k + 2) * 17 + ra] = v.z;
-          As[(k + 3) * 17 + ra] = v.w;
-        }
         const int64_t nb = n0 + nq;
         const float* bp = (const float*)g.b + b * g.b_sb + (nb < g.N ? nb : 0);
-        for (int k = kq; k < K16; k += 64) {
-          float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-          if (k < g.K && nb < g.N) v = *(const float4*)(bp + (int64_t)k * g.b_sk);
-          Bs[k * 17 + nq] = v.x;
-          Bs[k * 17 + nq + 1] = v.y;
-          Bs[k * 17 + nq + 2] = v.z;
-          Bs[k * 17 + nq + 3] = v.w;
+        const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 1
+        for (int i0 = 0; 64 * i0 < K16; i0 += kB) {
+          float4 va[kB], vb[kB];
+#pragma unroll
+          for (int i = 0; i < kB; ++i) {
+            const int ka = la * 4 + 64 * (i0 + i), kb = kq + 64 * (i0 + i);
+            va[i] = *(const float4*)(ap + (ka < g.K ? ka : 0));
+            vb[i] = *(const float4*)(bp + (int64_t)(kb < g.K ? kb : 0) * g.b_sk);
+          }
+#pragma unroll
+          for (int i = 0; i < kB; ++i) {
+            const int ka = la * 4 + 64 * (i0 + i), kb = kq + 64 * (i0 + i);
+            if (ka < K16)
+              *(float4*)&As[ra * KP + ka] = (ma < g.M && ka < g.K) ? va[i] : z;
+            if (kb < K16) {
+              const float4 v = (kb < g.K && nb < g.N) ? vb[i] : z;
+              Bs[nq * KP + kb] = v.x;
+              Bs[(nq + 1) * KP + kb] = v.y;
+              Bs[(nq + 2) * KP + kb] = v.z;
+              Bs[(nq + 3) * KP + kb] = v.w;
+            }
+          }
         }
       } else {
         for (int k = la; k < K16; k += 16)
-          As[k * 17 + ra] = (ma < g.M && k < g.K)
+          As[ra * KP + k] = (ma < g.M && k < g.K)
                                 ? load_as_float(g.a, g.dtype, b * g.a_sb + ma * g.a_sm + k * g.a_sk)
                                 : 0.0f;
         const int nc = tid & 15;
         const int64_t n = n0 + nc;
         for (int k = tid >> 4; k < K16; k += 16)
-          Bs[k * 17 + nc] = (k < g.K && n < g.N)
+          Bs[nc * KP + k] = (k < g.K && n < g.N)
                                 ? load_as_float(g.b, g.dtype, b * g.b_sb + k * g.b_sk + n * g.b_sn)
                                 : 0.0f;
       }
       __syncthreads();
       float acc = 0.0f;
-      for (int k = 0; k < K16; k += 16) {
-#pragma unroll
-        for (int kk = 0; kk < 16; ++kk)
-          acc = fmaf(As[(k + kk) * 17 + r], Bs[(k + kk) * 17 + cc], acc);
+      const float* ar = As + r * KP;
+      const float* br = Bs + cc * KP;
+#pragma unroll 4
+      for (int k = 0; k < K16; k += 4) {
+        const float4 av = *(const float4*)(ar + k), bv = *(const float4*)(br + k);
+        acc = fmaf(av.x, bv.x, acc);
+        acc = fmaf(av.y, bv.y, acc);
+        acc = fmaf(av.z, bv.z, acc);
+        acc = fmaf(av.w, bv.w, acc);
       }
       __syncthreads();
       const int64_t m = m0 + r, n = n0 + cc;
@@ -251,11 +274,11 @@ static void launch_gemm_small(const GemmArgs& g, hipStream_t stream) {
             (unsigned)(g.batch < 65535 ? g.batch : 65535));
   const int64_t k16 = (g.K + 15) & ~(int64_t)15;
   if (k16 <= kSmallWholeK) {
-    const size_t lds = (size_t)k16 * 17 * 4 * 2;
+    const size_t lds = (size_t)16 * (k16 + 4) * 4 * 2;
     static bool attr = [] {
       return hipFuncSetAttribute((const void*)gemm_f32_small_kernel<true>,
                                  hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 kSmallWholeK * 17 * 4 * 2) == hipSuccess;
+                                 16 * (kSmallWholeK + 4) * 4 * 2) == hipSuccess;
     }();
     if (attr || lds <= 65536) {
       hipLaunchKernelGGL(gemm_f32_small_kernel<true>, grid, dim3(256), lds, stream, g);

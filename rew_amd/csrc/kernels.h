@@ -283,6 +283,24 @@ struct ArgmaxArgs {
 };
 void launch_argmax(const ArgmaxArgs& g, hipStream_t stream);
 
+// ---- classifier head (k_head.hip) -----------------------------------------------
+// ids[r] = argmax_j softmax(x[r] W + b)[j] over fp32 rows in one launch,
+// each value with the unfused kernels' ops and order; the probabilities are
+// also stored when `probs` is set.  x rows of K at row stride x_rs, W dense
+// [K, N].
+struct HeadArgs {
+  const float* x;
+  int64_t x_rs;
+  const float *w, *b;
+  int64_t M, K, N;
+  float* probs;
+  int32_t* ids;
+};
+// K % 4 == 0, K rounded up to 16 <= 1024, N <= 64, (K rounded up to 16) N
+// <= 8192, 16-byte aligned x rows
+bool class_head_ok(const HeadArgs& a);
+void launch_class_head(const HeadArgs& a, hipStream_t stream);
+
 // topK over the last dim of dense f32 [rows, cols]: vals / idx [rows, k],
 // ranked larger-first (smaller-first when !largest), NaN last, ties to the
 // lower column.  1 <= k <= 64, k <= cols <= kTopkMaxCols.

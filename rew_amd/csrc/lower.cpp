@@ -286,6 +286,13 @@ struct MoePlan {
   std::vector<Tensor*> inner, mids;
 };
 
+// A classifier head, argmax(softmax(Linear(x))) over f32 rows (the end of
+// rew's MLP forward, nn/linear.nim:43-49 and nn/activation.nim:64-77), whose
+// logits and probabilities nobody else reads: one launch at the argmax.
+struct HeadPlan {
+  Tensor *x = nullptr, *w = nullptr, *b = nullptr;
+};
+
 struct Lower {
   Ctx* c;
   std::vector<Node*> nodes;  // live pending nodes in creation order
@@ -301,6 +308,7 @@ struct Lower {
   std::unordered_map<Tensor*, SoftmaxPlan> softmax_out;
   std::unordered_map<Tensor*, MoePlan> moe_out;
   std::unordered_map<Tensor*, Node*> flash_out;  // transposed flash output -> PV node
+  std::unordered_map<Tensor*, HeadPlan> head_out;  // argmax output -> fused head
   std::vector<std::vector<Tensor*>> gemm_groups;  // outputs of sibling projections
   // reductions emitted in this flush, by (input, op, dims, dtype): a repeat
   // (reduceMean's reduceSum next to a reduceSum of the same tensor) aliases
@@ -325,6 +333,8 @@ struct Lower {
   void match_rows();
   bool plan_norm(NormPlan np, Tensor* x, int x_uses, Tensor* o, std::vector<Tensor*>& inner);
   bool match_layernorm(Node* ao);
+  void match_class_head();
+  bool emit_class_head(Node* n, const HeadPlan& p);
   bool emit_norm(Tensor* t, const NormPlan& p);
   bool emit_rope(Tensor* t, const RopePlan& p);
   bool emit_softmax(Tensor* t, const SoftmaxPlan& p);
@@ -2894,6 +2904,13 @@ void Lower::emit_gather(Node* n) {
 // f32 operand.
 void Lower::emit_argmax(Node* n) {
   Tensor *x = n->in[0], *out = n->out[0];
+  auto hit = head_out.find(out);
+  if (hit != head_out.end()) {
+    const HeadPlan hp = hit->second;
+    head_out.erase(hit);
+    if (emit_class_head(n, hp)) return;
+    // outside the fused kernel's limits: the head runs as its own kernels
+  }
   ensure_mat(x);
   tensor_alloc(out);
   ArgmaxArgs g;
@@ -2911,6 +2928,71 @@ void Lower::emit_argmax(Node* n) {
     L.name = "argmax{" + std::to_string(g.outer) + "x" + std::to_string(g.n) + "x" +
              std::to_string(g.inner) + "}";
   run_launch(c, std::move(L));
+}
+
+// The classifier head: an argmax over dim 1 of a planned softmax of a
+// planned Linear (bias epilogue) whose logits and probabilities have no
+// other reader.  The plans stay registered, so a head the fused kernel
+// cannot take is emitted by them instead.
+void Lower::match_class_head() {
+  for (Node* n : nodes) {
+    if (n->kind != K_ARGMAX || n->i0 != 1) continue;
+    Tensor* p = n->in[0];
+    if (p->dt != kF32 || p->shape.rank != 2 || p->st || p->ext != 0 || p->uses != 1) continue;
+    auto sit = softmax_out.find(p);
+    if (sit == softmax_out.end()) continue;
+    Tensor* lg = sit->second.x;
+    auto lit = gemm_out.find(lg);
+    if (lit == gemm_out.end() || lg->st || lg->ext != 0 || lg->uses != 2) continue;
+    const GemmPlan& lp = lit->second;
+    if (lp.epi != EPI_BIAS || lp.dot2 || lp.group >= 0 || lg->shape != p->shape) continue;
+    Tensor *x = lp.dot->in[0], *w = lp.dot->in[1];
+    if (x->dt != kF32 || w->dt != kF32 || lg->dt != kF32 || lp.bias->dt != kF32) continue;
+    HeadPlan hp;
+    hp.x = x;
+    hp.w = w;
+    hp.b = lp.bias;
+    head_out[n->out[0]] = hp;
+    lg->plan_mat = false;
+    p->plan_mat = false;
+  }
+}
+
+bool Lower::emit_class_head(Node* n, const HeadPlan& p) {
+  Tensor* out = n->out[0];
+  const int64_t M = p.x->shape.d[0], K = p.x->shape.d[1], N = p.w->shape.d[1];
+  if (p.w->shape.d[0] != K || out->numel() != M) return false;
+  // a dense [rows, cols] (or [cols]) f32 operand's address, or null
+  auto dense = [&](Tensor* t, int64_t cols) -> const float* {
+    Tensor* base;
+    int64_t off, st[kMaxRank];
+    operand_strides(t, &base, &off, st);
+    if (st[t->shape.rank - 1] != 1 || (t->shape.rank == 2 && st[0] != cols)) return nullptr;
+    return (const float*)base->data() + off;
+  };
+  HeadArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.M = M;
+  a.K = K;
+  a.N = N;
+  a.x_rs = K;
+  a.x = reinterpret_cast<const float*>(uintptr_t(256));  // allocator blocks are aligned
+  if (!class_head_ok(a)) return false;
+  const void* xp;
+  rows_view(p.x, K, &xp, &a.x_rs);
+  a.x = (const float*)xp;
+  a.w = dense(p.w, N);
+  a.b = dense(p.b, N);
+  if (!a.w || !a.b || !class_head_ok(a)) return false;
+  tensor_alloc(out);
+  a.ids = (int32_t*)out->data();
+  Launch L{a};
+  if (c->profiling)
+    L.name = "class_head{" + std::to_string(M) + "x" + std::to_string(K) + "x" +
+             std::to_string(N) + "}";
+  L.fused = true;
+  run_launch(c, std::move(L));
+  return true;
 }
 
 // topK over the last dim (src/rew/ops/sort.nim:36-90 semantics).
@@ -3199,6 +3281,7 @@ static void lower_graph(Ctx* c, Lower& L, const std::string* sig,
     L.match_gemm_epilogues();
     if (!c->dense_moe) L.match_moe();
     L.match_rows();
+    L.match_class_head();
     L.match_gemm_groups();
   }
 

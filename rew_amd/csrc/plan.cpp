@@ -137,6 +137,13 @@ struct PtrVisit {
     for (const void** p : {&a.x, &a.scale, &a.offset, &a.mean, &a.var, &a.dy}) field(f, *p);
     for (void** p : {&a.out0, &a.out1, &a.out2}) field(f, *p);
   }
+  void operator()(HeadArgs& a) {
+    field(f, a.x);
+    field(f, a.w);
+    field(f, a.b);
+    field(f, a.probs);
+    field(f, a.ids);
+  }
 };
 
 template <class F>
@@ -172,6 +179,7 @@ struct Exec {
   void operator()(WindowArgs& a) { launch_window(a, c->stream); }
   void operator()(CholeskyArgs& a) { launch_cholesky(a, c->stream); }
   void operator()(BatchNormArgs& a) { launch_batchnorm(a, c->stream); }
+  void operator()(HeadArgs& a) { launch_class_head(a, c->stream); }
   void operator()(FillL& l) {
     if (l.bytes == 0) return;
     if (l.src)

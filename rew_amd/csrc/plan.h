@@ -55,7 +55,7 @@ struct FillL {
 using LaunchArgs = std::variant<EwL, ReduceL, GemmL, FlashArgs, RowNormArgs, SoftmaxArgs,
                                 RopeArgs, GatherArgs, ArgmaxArgs, TopkArgs, SortArgs,
                                 IndexMapL, MoeL, FillL, WindowArgs, CholeskyArgs,
-                                BatchNormArgs>;
+                                BatchNormArgs, HeadArgs>;
 
 struct Launch {
   LaunchArgs args;

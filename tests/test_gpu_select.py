@@ -76,6 +76,57 @@ def test_topk_rejects_out_of_range(gpu):
         O.topK(dev(np.zeros((2, 8), np.float32)), 9, -1, True)
 
 
+@pytest.mark.parametrize("M,K,N1,N2,fused", [(128, 784, 128, 10, True), (130, 100, 64, 7, True),
+                                             (33, 100, 128, 70, False)])
+def test_mlp_forward_two_launches(gpu, oracle, M, K, N1, N2, fused):
+    """rew's MLP forward -- Linear, relu, Linear, softmax, argmax
+    (nn/linear.nim:43-49, nn/activation.nim:21-77, ops/reduce.nim:202-225) --
+    with nothing but the ids read back runs as two launches, eager and under
+    lazy: the first Linear with the relu in its epilogue, then the last
+    Linear, the softmax and the argmax in one kernel (within its limits:
+    hidden <= 1024, classes <= 64).  The ids equal the unfused kernels' (the
+    same fma chains, softmax and argmax order) bit for bit, a row holding NaN
+    gives INT32_MAX, and outside the limits the head falls back to the
+    unfused kernels."""
+    from rew_amd import jit as J
+    rs = np.random.default_rng(M + K)
+    x = rs.random((M, K), dtype=np.float32)
+    x[5, 3] = np.nan
+    w1 = rng.xavierUniformF32(rng.initKey(K), K, N1).reshape(K, N1)
+    w2 = rng.xavierUniformF32(rng.initKey(N1), N1, N2).reshape(N1, N2)
+    b1 = rs.normal(0, 0.1, N1).astype(np.float32)
+    b2 = rs.normal(0, 0.1, N2).astype(np.float32)
+    xt, l1, l2 = dev(x), nn.Linear(dev(w1), dev(b1)), nn.Linear(dev(w2), dev(b2))
+
+    def head():
+        return O.argmax(nn.softmax(l2.forward(nn.relu(l1.forward(xt))), 1), 1)
+
+    E.profileBegin()
+    ids = E.toHost(head())
+    names = [n for n, _, _ in E.profileEnd()]
+    lz = J.lazy(lambda a: [nn.softmax(nn.Linear(a[3], a[4]).forward(
+        nn.relu(nn.Linear(a[1], a[2]).forward(a[0]))), 1)], "mlpHead")
+    E.profileBegin()
+    ids_lazy = E.toHost(O.argmax(lz.call([xt, l1.weight, l1.bias, l2.weight, l2.bias])[0], 1))
+    names_lazy = [n for n, _, _ in E.profileEnd()]
+    if fused:
+        assert names == [f"gemm_f32_small+bias+relu[1,{M},{N1},{K}]",
+                         f"class_head{{{M}x{N1}x{N2}}}"], names
+        assert names_lazy == names, names_lazy
+    else:
+        assert not any(n.startswith("class_head") for n in names + names_lazy), names
+    # the unfused kernels: every intermediate held, so each is materialized
+    h_t = nn.relu(l1.forward(xt))
+    z_t = l2.forward(h_t)
+    p_t = nn.softmax(z_t, 1)
+    ref = E.toHost(O.argmax(p_t, 1))
+    np.testing.assert_array_equal(ids, ref)
+    np.testing.assert_array_equal(ids_lazy, ref)
+    assert ids[5] == np.iinfo(np.int32).max
+    want = oracle.argmax_rows(E.toHost(p_t))
+    np.testing.assert_array_equal(ids, want)
+
+
 def test_mnist_mlp_inference(gpu, oracle):
     """Config C1: x [128,784] ~ U[0,1); Linear 784->128 + relu, Linear 128->10,
     softmax, argmax; Glorot-uniform weights (nn/init.nim:93-97), zero biases."""
