@@ -3345,6 +3345,21 @@ static void flush_graph(Ctx* c, std::vector<Node*>& all) {
     sig = flush_signature(c, L.nodes, &leaves, &leaf_slot);
     plan = plan_find(c, sig);
   }
+  if (c->capture && !sig.empty()) {
+    // a jit call recording its module's direct plan: what it needs of this graph
+    FlushCapture* cap = c->capture;
+    cap->done = true;
+    cap->sig = sig;
+    cap->leaves = leaves;
+    cap->node_meta.resize(L.nodes.size());
+    for (size_t i = 0; i < L.nodes.size(); ++i) {
+      const Node* n = L.nodes[i];
+      for (size_t o = 0; o < n->out.size(); ++o) {
+        cap->node_meta[i].emplace_back(n->out[o]->dt, n->out[o]->shape);
+        cap->out_ref.emplace(n->out[o], std::make_pair((int32_t)i, (int32_t)o));
+      }
+    }
+  }
   std::exception_ptr err;
   if (plan && plan->ok) {
     c->stats.flush_plan_hits++;

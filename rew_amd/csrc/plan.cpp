@@ -470,8 +470,13 @@ void plan_cache_clear(Ctx* c) {
 }
 
 // ---- replay -----------------------------------------------------------------------------
-void plan_replay(Ctx* c, const FlushPlan& p, const std::vector<Node*>& nodes,
-                 const std::vector<Tensor*>& leaves) {
+namespace {
+
+// The events of p over this flush's leaves; node(idx, out) names a node
+// output of the recorded graph.
+template <class NodeOut>
+void replay_events(Ctx* c, const FlushPlan& p, const std::vector<Tensor*>& leaves,
+                   NodeOut node) {
   std::vector<uintptr_t> slot((size_t)p.n_slots, 0);
   for (size_t s = 0; s < p.leaf_slot_first.size(); ++s)
     slot[s] = (uintptr_t)leaves[p.leaf_slot_first[s]]->data();
@@ -479,7 +484,7 @@ void plan_replay(Ctx* c, const FlushPlan& p, const std::vector<Node*>& nodes,
   auto get = [&](const PlanRef& r) -> Tensor* {
     switch (r.kind) {
       case PlanRef::LEAF: return leaves[r.idx];
-      case PlanRef::NODE: return nodes[r.idx]->out[r.out];
+      case PlanRef::NODE: return node(r.idx, r.out);
       default:
         if (!temps[r.idx]) temps[r.idx] = new_tensor(c, p.temps[r.idx].first, p.temps[r.idx].second);
         return temps[r.idx];
@@ -531,6 +536,48 @@ void plan_replay(Ctx* c, const FlushPlan& p, const std::vector<Node*>& nodes,
     throw;
   }
   release_temps();
+}
+
+}  // namespace
+
+void plan_replay(Ctx* c, const FlushPlan& p, const std::vector<Node*>& nodes,
+                 const std::vector<Tensor*>& leaves) {
+  replay_events(c, p, leaves, [&](int32_t i, int32_t o) { return nodes[i]->out[o]; });
+}
+
+std::vector<Tensor*> plan_replay_direct(Ctx* c, const DirectPlan& d,
+                                        const std::vector<Tensor*>& leaves) {
+  // node outputs exist as plain tensors, made when the plan first names them
+  std::vector<std::vector<Tensor*>> made(d.node_meta.size());
+  auto node = [&](int32_t i, int32_t o) -> Tensor* {
+    std::vector<Tensor*>& v = made[i];
+    if (v.empty()) v.assign(d.node_meta[i].size(), nullptr);
+    if (!v[o]) v[o] = new_tensor(c, d.node_meta[i][o].first, d.node_meta[i][o].second);
+    return v[o];
+  };
+  auto drop_all = [&] {
+    for (auto& v : made)
+      for (Tensor*& t : v)
+        if (t) {
+          maybe_destroy(t);
+          t = nullptr;
+        }
+  };
+  std::vector<Tensor*> res;
+  try {
+    replay_events(c, d.plan, leaves, node);
+    for (const auto& r : d.results) {
+      Tensor* t = node(r.first, r.second);
+      if (!t->st) throw Error(REW_MI355X_ERR_INVALID, "internal: direct plan left a result empty");
+      res.push_back(t);
+    }
+  } catch (...) {
+    drop_all();
+    throw;
+  }
+  for (Tensor* t : res) t->ext++;
+  drop_all();  // the results keep their owner references
+  return res;
 }
 
 }  // namespace rew

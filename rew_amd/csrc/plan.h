@@ -5,6 +5,7 @@
 #pragma once
 
 #include <string>
+#include <unordered_map>
 #include <variant>
 #include <vector>
 
@@ -117,6 +118,35 @@ void plan_record_end(Ctx* c, const std::string& sig, bool keep);
 // Enqueues plan p's allocations and launches over this flush's tensors.
 void plan_replay(Ctx* c, const FlushPlan& p, const std::vector<Node*>& nodes,
                  const std::vector<Tensor*>& leaves);
+
+// What a flush reports to a jit call that records its module's direct plan
+// (Ctx::capture): the flush's leaves in signature order, each live node's
+// outputs (dtype, shape), where each node output sits as (node, output),
+// and the signature under which the flush's plan is stored.
+struct FlushCapture {
+  bool done = false;
+  std::string sig;
+  std::vector<Tensor*> leaves;
+  std::vector<std::vector<std::pair<int, Shape>>> node_meta;
+  std::unordered_map<const Tensor*, std::pair<int32_t, int32_t>> out_ref;
+};
+
+// A jit module's lowering replayed without building its graph: the plan of
+// the flush that ran the module alone, with each leaf named as a module
+// input (>= 0) or constant (-1 - index), each node output's dtype and
+// shape, and the module results as (node, output).
+struct DirectPlan {
+  bool ok = false;  // false: not replayable directly (the graph path runs)
+  uint64_t epoch = 0;
+  FlushPlan plan;
+  std::vector<int32_t> leaf_src;
+  std::vector<std::vector<std::pair<int, Shape>>> node_meta;
+  std::vector<std::pair<int32_t, int32_t>> results;
+};
+// Enqueues d's plan over `leaves` (resolved from leaf_src) and returns the
+// module results, each holding one owner reference.
+std::vector<Tensor*> plan_replay_direct(Ctx* c, const DirectPlan& d,
+                                        const std::vector<Tensor*>& leaves);
 // Drops every stored plan of the context.
 void plan_cache_clear(Ctx* c);
 

@@ -648,6 +648,7 @@ int rew_mi355x_clear_cache(rew_mi355x_ctx* ctx) {
     // allocator once no tensor uses it), and so are the recorded flush plans.
     const_cache_clear(c);
     plan_cache_clear(c);
+    c->plan_epoch++;  // and the jit modules' direct plans
   });
 }
 

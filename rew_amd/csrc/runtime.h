@@ -20,6 +20,7 @@ struct RoutedFfn;
 struct JitModule;
 struct FlushPlan;
 struct PlanRecorder;
+struct FlushCapture;
 
 // A device allocation shared by every tensor that aliases it (a reshape of
 // a materialized tensor aliases its source).
@@ -153,6 +154,12 @@ struct Ctx {
   std::unordered_map<std::string, FlushPlan*> flush_plans;
   std::deque<std::string> plan_order;
   PlanRecorder* rec = nullptr;
+  // set by a jit call that records its module's direct plan: the next flush
+  // reports its leaves, nodes and signature here
+  FlushCapture* capture = nullptr;
+  // bumped by rew_mi355x_clear_cache: direct plans of jit modules recorded
+  // before the last clear are dropped on their next use
+  uint64_t plan_epoch = 0;
 };
 
 // ---- runtime services (runtime.cpp) -----------------------------------------

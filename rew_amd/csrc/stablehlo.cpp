@@ -24,6 +24,7 @@
 // Nodes join the deferred graph like eager ops, so a lazy batch lowers
 // through the same fused kernels (flash attention, GEMM epilogues, routed
 // MoE) as the eager op stream and is launched at the next flush.
+#include <chrono>
 #include <cmath>
 #include <cerrno>
 #include <cstring>
@@ -34,6 +35,7 @@
 #include <vector>
 
 #include "kernels.h"
+#include "plan.h"
 #include "runtime.h"
 
 namespace rew {
@@ -716,6 +718,9 @@ struct JitModule {
   std::vector<Step> steps;
   std::vector<int> ret;
   int64_t calls = 0;
+  // direct plans (plan.h) by input key, for modules of at least
+  // kDirectMinSteps steps called with nothing else pending
+  std::unordered_map<std::string, DirectPlan> direct;
 };
 
 namespace {
@@ -1503,31 +1508,41 @@ JitModule* compile_module(Ctx* c, const std::string& who, const char* text, size
 
 }  // namespace
 
-std::vector<Tensor*> jit_module_run(Ctx* c, const std::string& name, const std::string& cache_key,
-                             const char* text, size_t len, const std::vector<Tensor*>& ins) {
-  const std::string who = "jit '" + name + "'";
-  std::string key = std::to_string(c->ordinal) + "::" + name + "::" + cache_key + "::";
-  char hx[17];
-  std::snprintf(hx, sizeof hx, "%016llx", (unsigned long long)text_hash(text, len));
-  key += hx;
-  auto it = c->jit_modules.find(key);
-  JitModule* m;
-  if (it != c->jit_modules.end()) {
-    m = it->second;
-    c->stats.jit_module_hits++;
-  } else {
-    m = compile_module(c, who, text, len);
-    c->jit_modules.emplace(key, m);
-    c->stats.jit_module_compiles++;
+namespace {
+
+// Modules this large run directly once their plan is recorded: their host
+// cost is the graph they would otherwise build and flush on every call.
+constexpr size_t kDirectMinSteps = 64;
+constexpr size_t kDirectMaxPlans = 8;  // per module, all dropped when exceeded
+
+// What a flush of the module alone may depend on beyond the module itself:
+// the context's lowering flags and, per input, which earlier input is the
+// same tensor or shares its storage, the address bits alignment checks read
+// and the host bytes of small constants (the flush signature's leaf terms).
+std::string direct_key(Ctx* c, const std::vector<Tensor*>& ins) {
+  std::string k;
+  k.reserve(ins.size() * 12 + 4);
+  k.push_back((char)((c->no_fusion_patterns ? 1 : 0) | (c->profiling ? 2 : 0) |
+                     (c->dense_moe ? 4 : 0)));
+  std::unordered_map<const Tensor*, int32_t> first_t;
+  std::unordered_map<const Storage*, int32_t> first_s;
+  for (size_t i = 0; i < ins.size(); ++i) {
+    const Tensor* t = ins[i];
+    const int32_t ti = first_t.emplace(t, (int32_t)i).first->second;
+    const int32_t si = first_s.emplace(t->st, (int32_t)i).first->second;
+    const uint8_t lo = (uint8_t)((uintptr_t)t->st->ptr & 255);
+    k.append((const char*)&ti, 4);
+    k.append((const char*)&si, 4);
+    k.push_back((char)lo);
+    k.push_back(t->has_host ? 1 : 0);
+    if (t->has_host) k.append((const char*)t->host, sizeof t->host);
   }
-  if (ins.size() != m->arg_slot.size())
-    invalid(who + ": module takes " + std::to_string(m->arg_slot.size()) + " input(s), got " +
-            std::to_string(ins.size()));
-  for (size_t i = 0; i < ins.size(); ++i)
-    if (ins[i]->dt != m->arg_ty[i].first || ins[i]->shape != m->arg_ty[i].second)
-      invalid(who + ": input " + std::to_string(i) + " is " + type_text(ins[i]->dt, ins[i]->shape) +
-              ", the module expects " + type_text(m->arg_ty[i].first, m->arg_ty[i].second));
-  m->calls++;
+  return k;
+}
+
+// The module's nodes committed to the pending graph; its results, each
+// with one owner reference.
+std::vector<Tensor*> instantiate(Ctx* c, JitModule* m, const std::vector<Tensor*>& ins) {
   std::vector<Tensor*> v(m->n_slots, nullptr);
   for (size_t i = 0; i < ins.size(); ++i) v[m->arg_slot[i]] = ins[i];
   for (auto& kc : m->consts) v[kc.first] = kc.second;
@@ -1562,6 +1577,109 @@ std::vector<Tensor*> jit_module_run(Ctx* c, const std::string& name, const std::
     t->ext--;
     maybe_destroy(t);
   }
+  return res;
+}
+
+// The direct plan of a flush that ran module m alone (`cap`), or a plan
+// marked not replayable.
+DirectPlan make_direct(Ctx* c, JitModule* m, const std::vector<Tensor*>& ins,
+                       const std::vector<Tensor*>& res, const FlushCapture& cap) {
+  DirectPlan d;
+  d.epoch = c->plan_epoch;
+  if (!cap.done) return d;
+  auto pit = c->flush_plans.find(cap.sig);
+  if (pit == c->flush_plans.end() || !pit->second->ok) return d;
+  std::unordered_map<const Tensor*, int32_t> src;
+  for (size_t i = 0; i < ins.size(); ++i) src.emplace(ins[i], (int32_t)i);
+  for (size_t k = 0; k < m->consts.size(); ++k)
+    src.emplace(m->consts[k].second, -1 - (int32_t)k);
+  for (Tensor* t : cap.leaves) {
+    auto it = src.find(t);
+    if (it == src.end()) return d;
+    d.leaf_src.push_back(it->second);
+  }
+  for (Tensor* t : res) {
+    auto it = cap.out_ref.find(t);
+    if (it == cap.out_ref.end()) return d;  // a result that is an input or a constant
+    d.results.push_back(it->second);
+  }
+  d.plan = *pit->second;
+  d.node_meta = cap.node_meta;
+  d.ok = true;
+  return d;
+}
+
+}  // namespace
+
+std::vector<Tensor*> jit_module_run(Ctx* c, const std::string& name, const std::string& cache_key,
+                             const char* text, size_t len, const std::vector<Tensor*>& ins) {
+  const std::string who = "jit '" + name + "'";
+  std::string key = std::to_string(c->ordinal) + "::" + name + "::" + cache_key + "::";
+  char hx[17];
+  std::snprintf(hx, sizeof hx, "%016llx", (unsigned long long)text_hash(text, len));
+  key += hx;
+  auto it = c->jit_modules.find(key);
+  JitModule* m;
+  if (it != c->jit_modules.end()) {
+    m = it->second;
+    c->stats.jit_module_hits++;
+  } else {
+    m = compile_module(c, who, text, len);
+    c->jit_modules.emplace(key, m);
+    c->stats.jit_module_compiles++;
+  }
+  if (ins.size() != m->arg_slot.size())
+    invalid(who + ": module takes " + std::to_string(m->arg_slot.size()) + " input(s), got " +
+            std::to_string(ins.size()));
+  bool direct = c->mode == REW_MI355X_MODE_DEFERRED && c->plan_cache && c->pending.empty() &&
+                m->steps.size() >= kDirectMinSteps;
+  for (size_t i = 0; i < ins.size(); ++i) {
+    if (ins[i]->dt != m->arg_ty[i].first || ins[i]->shape != m->arg_ty[i].second)
+      invalid(who + ": input " + std::to_string(i) + " is " + type_text(ins[i]->dt, ins[i]->shape) +
+              ", the module expects " + type_text(m->arg_ty[i].first, m->arg_ty[i].second));
+    direct = direct && ins[i]->st;
+  }
+  m->calls++;
+  if (!direct) return instantiate(c, m, ins);
+  // rew's executeJit runs the module at once (eager.nim:1782-1847): with
+  // nothing else pending, the module's graph is flushed here, and later
+  // calls with the same input key replay that flush's plan directly
+  const std::string dk = direct_key(c, ins);
+  auto dit = m->direct.find(dk);
+  if (dit != m->direct.end() && dit->second.epoch != c->plan_epoch) {
+    m->direct.erase(dit);
+    dit = m->direct.end();
+  }
+  if (dit != m->direct.end()) {
+    if (!dit->second.ok) return instantiate(c, m, ins);
+    const auto t0 = std::chrono::steady_clock::now();
+    std::vector<Tensor*> leaves;
+    leaves.reserve(dit->second.leaf_src.size());
+    for (int32_t s : dit->second.leaf_src)
+      leaves.push_back(s >= 0 ? ins[s] : m->consts[-1 - s].second);
+    std::vector<Tensor*> res = plan_replay_direct(c, dit->second, leaves);
+    c->stats.flushes++;
+    c->stats.flush_plan_hits++;
+    c->stats.flush_host_ns += std::chrono::duration_cast<std::chrono::nanoseconds>(
+                                  std::chrono::steady_clock::now() - t0).count();
+    return res;
+  }
+  std::vector<Tensor*> res = instantiate(c, m, ins);
+  FlushCapture cap;
+  c->capture = &cap;
+  try {
+    flush(c);
+  } catch (...) {
+    c->capture = nullptr;
+    for (Tensor* t : res) {
+      t->ext--;
+      maybe_destroy(t);
+    }
+    throw;
+  }
+  c->capture = nullptr;
+  if (m->direct.size() >= kDirectMaxPlans) m->direct.clear();
+  m->direct.emplace(dk, make_direct(c, m, ins, res, cap));
   return res;
 }
 

@@ -138,20 +138,21 @@ def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
 class Device:
     """(target, ordinal); ``str(d)`` is rew's "target:ordinal" form."""
 
-    __slots__ = ("target", "ordinal")
+    __slots__ = ("target", "ordinal", "_hash")
 
     def __init__(self, target: str = "mi355x", ordinal: int = 0):
         if ordinal < 0:
             raise ValueError(f"initDevice: ordinal must be non-negative, got {ordinal}")
         self.target = target
         self.ordinal = ordinal
+        self._hash = hash((target, ordinal))
 
     def __eq__(self, other):
-        return isinstance(other, Device) and (self.target, self.ordinal) == (
-            other.target, other.ordinal)
+        return self is other or (isinstance(other, Device) and (self.target, self.ordinal) == (
+            other.target, other.ordinal))
 
     def __hash__(self):
-        return hash((self.target, self.ordinal))
+        return self._hash
 
     def __str__(self):
         return f"{self.target}:{self.ordinal}"

@@ -23,6 +23,7 @@ Mirror of rew's runtime tracing and its jit execution path:
 from __future__ import annotations
 
 import ctypes as C
+import operator
 import struct
 import threading
 from contextlib import contextmanager
@@ -519,6 +520,11 @@ def signatureOf(args: Sequence[Tensor]) -> str:
                     "#replicated" for a in args)
 
 
+# (dtype, shape, device) of a jit argument, and its native handle
+_arg_sig = operator.attrgetter("dtype", "shape", "device")
+_handle_of = operator.attrgetter("handle")
+
+
 class JitCacheEntry:
     """Lowering of one input signature (src/rew/transform/jit.nim:51-63)."""
 
@@ -552,6 +558,11 @@ class JitFunction:
         self.donateArgs = [int(i) for i in donateArgs]
         self.cache: dict[str, JitCacheEntry] = {}
         self._fast: dict[tuple, JitCacheEntry] = {}
+        # the last call's arguments and entry: the same tensor objects have
+        # the same signature (dtype, shape and device never change), so a
+        # call repeating them skips building the key.  Holds the last call's
+        # inputs until the next call.
+        self._last: tuple = ((), None)
 
     def _validate_donation(self, argCount: int) -> None:
         for idx in self.donateArgs:
@@ -579,9 +590,13 @@ class JitFunction:
 
     def compileFor(self, args: Sequence[Tensor]) -> JitCacheEntry:
         """The cache entry of this input signature, tracing on a miss."""
-        fk = tuple((a.dtype, a.shape, a.device) for a in args)
+        prev, pe = self._last
+        if pe is not None and len(prev) == len(args) and all(map(operator.is_, prev, args)):
+            return pe
+        fk = tuple(map(_arg_sig, args))
         e = self._fast.get(fk)
         if e is not None:
+            self._last = (tuple(args), e)
             return e
         sig = signatureOf(args)
         e = self.cache.get(sig)
@@ -589,6 +604,7 @@ class JitFunction:
             e = self._trace_once(args, sig)
             self.cache[sig] = e
         self._fast[fk] = e
+        self._last = (tuple(args), e)
         return e
 
     def lower(self, args: Sequence[Tensor]) -> TraceContext:
@@ -617,6 +633,7 @@ class JitFunction:
     def clearCache(self) -> None:
         self.cache.clear()
         self._fast.clear()
+        self._last = ((), None)
 
     def call(self, args: Sequence[Tensor]) -> list:
         """Trace on a miss, then execute through the backend
@@ -681,13 +698,13 @@ def _execute(jitName: str, cacheKey: str, text: bytes, inputs: Sequence[Tensor],
         raise EagerError("executeJit: outDtypes / outShapes length mismatch")
     d = inputs[0].device
     n = len(inputs)
-    hs = (C.c_void_p * n)()
-    for i, t in enumerate(inputs):
-        if t.device != d:
+    for t in inputs:
+        if t.device is not d and t.device != d:
             raise EagerError(f"jit '{jitName}': cross-device inputs forbidden")
-        if t.handle is None:
-            _raise_released(t, f"jit '{jitName}'")
-        hs[i] = t.handle
+    handles = list(map(_handle_of, inputs))
+    if None in handles:
+        _raise_released(inputs[handles.index(None)], f"jit '{jitName}'")
+    hs = (C.c_void_p * n)(*handles)
     for idx in donateIdx:
         if idx < 0 or idx >= n:
             raise EagerError(f"jit '{jitName}': donation index {idx} out of range")
