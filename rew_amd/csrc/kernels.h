@@ -283,6 +283,28 @@ struct ArgmaxArgs {
 };
 void launch_argmax(const ArgmaxArgs& g, hipStream_t stream);
 
+// ---- mixture-of-experts router (k_router.hip) -----------------------------------
+// ids / vals = topK(softmax(x W + b), k) per token row (largest first, NaN
+// last, lower column on ties) and weights = vals / (sum of the row's vals in
+// rank order), each value with the unfused kernels' ops and order; vals and
+// weights are stored when set.  x [T, H] f32 or bf16 at row stride x_rs
+// (elements), W dense f32 [H, E], b f32 [E].
+constexpr int kRouterMaxE = 64, kRouterMaxK = 16;
+struct RouterArgs {
+  const void* x;
+  int x_bf16;
+  int64_t x_rs;
+  const float *w, *b;
+  int64_t T, H;
+  int E, k;
+  int32_t* ids;
+  float *vals, *weights;
+};
+// H % 64 == 0, 4 <= E <= 64, E % 4 == 0, 1 <= k <= min(E, 16), 16-byte
+// aligned x rows and W
+bool moe_router_ok(const RouterArgs& a);
+void launch_moe_router(const RouterArgs& a, hipStream_t stream);
+
 // ---- classifier head (k_head.hip) -----------------------------------------------
 // ids[r] = argmax_j softmax(x[r] W + b)[j] over fp32 rows in one launch,
 // each value with the unfused kernels' ops and order; the probabilities are

@@ -293,6 +293,17 @@ struct HeadPlan {
   Tensor *x = nullptr, *w = nullptr, *b = nullptr;
 };
 
+// DeepSeekMoE.route (src/rew/models/deepseek.nim:132-137): topK of the
+// softmax of an f32 Linear of x (or of astype(x, f32) from bf16), and the
+// renormalised weights when the chain goes on to them; logits,
+// probabilities and (with the renormalisation) the raw values have no
+// other reader.  One launch makes the ids and the weights (or values).
+struct RouterPlan {
+  Tensor *x = nullptr, *w = nullptr, *b = nullptr;
+  Tensor *ids = nullptr, *vals = nullptr, *wts = nullptr;
+  int k = 0;
+};
+
 struct Lower {
   Ctx* c;
   std::vector<Node*> nodes;  // live pending nodes in creation order
@@ -309,6 +320,7 @@ struct Lower {
   std::unordered_map<Tensor*, MoePlan> moe_out;
   std::unordered_map<Tensor*, Node*> flash_out;  // transposed flash output -> PV node
   std::unordered_map<Tensor*, HeadPlan> head_out;  // argmax output -> fused head
+  std::unordered_map<Tensor*, RouterPlan> router_out;  // its ids / weights / values -> router
   std::vector<std::vector<Tensor*>> gemm_groups;  // outputs of sibling projections
   // reductions emitted in this flush, by (input, op, dims, dtype): a repeat
   // (reduceMean's reduceSum next to a reduceSum of the same tensor) aliases
@@ -335,6 +347,8 @@ struct Lower {
   bool match_layernorm(Node* ao);
   void match_class_head();
   bool emit_class_head(Node* n, const HeadPlan& p);
+  void match_router();
+  bool emit_router(const RouterPlan& p);
   bool emit_norm(Tensor* t, const NormPlan& p);
   bool emit_rope(Tensor* t, const RopePlan& p);
   bool emit_softmax(Tensor* t, const SoftmaxPlan& p);
@@ -908,6 +922,14 @@ static void alloc_regs(Program& P, const std::vector<int>& live_out,
 
 void Lower::ensure_mat(Tensor* t) {
   if (t->st) return;
+  auto rtt = router_out.find(t);
+  if (rtt != router_out.end()) {
+    const RouterPlan rp = rtt->second;
+    for (Tensor* o : {rp.ids, rp.vals, rp.wts})
+      if (o) router_out.erase(o);
+    if (emit_router(rp) && t->st) return;
+    // outside the fused kernel's limits: the chain's own plans run
+  }
   auto git = gemm_out.find(t);
   if (git != gemm_out.end()) {
     GemmPlan gp = git->second;
@@ -1812,6 +1834,23 @@ void Lower::match_gemm_epilogues() {
     }
   }
   // 2. bias (+ residual) epilogues of the remaining matmuls
+  std::unordered_map<const Node*, size_t> order;
+  for (size_t i = 0; i < nodes.size(); ++i) order.emplace(nodes[i], i);
+  // y = add(matmul D', bias) of a later matmul D': the sum add(.., y) is
+  // left to D''s epilogue, which reads this GEMM's output as its residual
+  // (DeepSeekMoE's shared experts, out = E_0(x) + E_1(x))
+  auto later_biased_matmul = [&](Tensor* y, size_t here) -> bool {
+    if (!y || y->st || !y->prod || y->prod->kind != K_BINARY || y->prod->sub != 0) return false;
+    for (Tensor* d : y->prod->in) {
+      Tensor* bias;
+      if (d->prod && !d->st && d->ext == 0 && d->uses == 1 && plain_matmul(d->prod) &&
+          bias_of(y->prod->in[0] == d ? y->prod->in[1] : y->prod->in[0], d->shape, &bias)) {
+        auto it = order.find(d->prod);
+        return it != order.end() && it->second > here;
+      }
+    }
+    return false;
+  };
   for (Node* n : nodes) {
     if (!plain_matmul(n)) continue;
     Tensor* D = n->out[0];
@@ -1835,7 +1874,8 @@ void Lower::match_gemm_epilogues() {
     }
     if (c1 && c1->kind == K_BINARY && c1->sub == 0 && c1->in[0] != c1->in[1]) {
       Tensor* R = c1->in[0] == r ? c1->in[1] : c1->in[0];
-      if (R->dt == D->dt && R->shape == r->shape && R->shape.numel() == D->numel()) {
+      if (R->dt == D->dt && R->shape == r->shape && R->shape.numel() == D->numel() &&
+          !later_biased_matmul(R, order[n])) {
         gp.epi = EPI_BIAS_RES;
         gp.res = R;
         inner.push_back(y);
@@ -2995,6 +3035,116 @@ bool Lower::emit_class_head(Node* n, const HeadPlan& p) {
   return true;
 }
 
+void Lower::match_router() {
+  for (Node* n : nodes) {
+    if (n->kind != K_TOPK || n->i2 != 1 || n->out.size() != 2) continue;  // largest first
+    Tensor* p = n->in[0];
+    if (p->dt != kF32 || p->shape.rank != 2 || p->st || p->ext != 0 || p->uses != 1) continue;
+    auto sit = softmax_out.find(p);
+    if (sit == softmax_out.end()) continue;
+    Tensor* lg = sit->second.x;
+    auto lit = gemm_out.find(lg);
+    if (lit == gemm_out.end() || lg->st || lg->ext != 0 || lg->uses != 2) continue;
+    const GemmPlan& lp = lit->second;
+    if (lp.epi != EPI_BIAS || lp.dot2 || lp.group >= 0 || lg->shape != p->shape) continue;
+    Tensor *xf = lp.dot->in[0], *w = lp.dot->in[1];
+    if (xf->dt != kF32 || w->dt != kF32 || lg->dt != kF32 || lp.bias->dt != kF32 ||
+        xf->shape.rank != 2)
+      continue;
+    RouterPlan rp;
+    rp.x = xf;
+    bool conv = false;
+    if (!xf->st && xf->prod && xf->prod->kind == K_CONVERT && xf->ext == 0 && xf->uses == 1 &&
+        xf->prod->in[0]->dt == kBF16) {
+      rp.x = xf->prod->in[0];
+      conv = true;
+    }
+    rp.w = w;
+    rp.b = lp.bias;
+    rp.k = (int)n->i0;
+    rp.ids = n->out[1];
+    rp.vals = n->out[0];
+    // divide(vals, broadcastTo(reduceSum(vals, [1]), vals.shape, [0]))
+    Tensor* tv = n->out[0];
+    Tensor *denom = nullptr, *dB = nullptr, *tw = nullptr;
+    auto ci = cons.find(tv);
+    if (!tv->st && tv->ext == 0 && tv->uses == 2 && ci != cons.end() && ci->second.size() == 2) {
+      Node *rs = nullptr, *dv = nullptr;
+      for (Node* q : ci->second) {
+        if (q->kind == K_REDUCE && q->sub == RED_SUM && dims_are(q->l0, {1})) rs = q;
+        else if (q->kind == K_BINARY && q->sub == 3 && q->in[0] == tv) dv = q;
+      }
+      Node* bc = rs ? sole_consumer(*this, rs->out[0]) : nullptr;
+      if (bc && dv && bc->kind == K_BROADCAST_TO && dims_are(bc->l1, {0}) &&
+          dv->in[1] == bc->out[0] &&
+          bc->out[0]->ext == 0 && bc->out[0]->uses == 1 && dv->out[0]->shape == tv->shape) {
+        denom = rs->out[0];
+        dB = bc->out[0];
+        tw = dv->out[0];
+      }
+    }
+    lg->plan_mat = false;
+    p->plan_mat = false;
+    if (conv) xf->plan_mat = false;
+    if (tw) {
+      rp.wts = tw;
+      rp.vals = nullptr;
+      tv->plan_mat = false;
+      denom->plan_mat = false;
+      dB->plan_mat = false;
+      tw->plan_mat = true;
+      router_out[tw] = rp;
+    } else {
+      router_out[tv] = rp;
+    }
+    router_out[rp.ids] = rp;
+  }
+}
+
+bool Lower::emit_router(const RouterPlan& p) {
+  const int64_t T = p.x->shape.d[0], H = p.x->shape.d[1];
+  const int64_t E = p.w->shape.d[1];
+  if (p.w->shape.d[0] != H || E > kRouterMaxE) return false;
+  auto dense = [&](Tensor* t, int64_t cols) -> const float* {
+    Tensor* base;
+    int64_t off, st[kMaxRank];
+    operand_strides(t, &base, &off, st);
+    if (st[t->shape.rank - 1] != 1 || (t->shape.rank == 2 && st[0] != cols)) return nullptr;
+    return (const float*)base->data() + off;
+  };
+  RouterArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.x_bf16 = p.x->dt == kBF16 ? 1 : 0;
+  a.T = T;
+  a.H = H;
+  a.E = (int)E;
+  a.k = p.k;
+  a.x_rs = H;
+  a.x = a.w = reinterpret_cast<const float*>(uintptr_t(256));  // allocator blocks are aligned
+  if (!moe_router_ok(a)) return false;
+  rows_view(p.x, H, &a.x, &a.x_rs);
+  a.w = dense(p.w, E);
+  a.b = dense(p.b, E);
+  if (!a.w || !a.b || !moe_router_ok(a)) return false;
+  tensor_alloc(p.ids);
+  a.ids = (int32_t*)p.ids->data();
+  if (p.wts) {
+    tensor_alloc(p.wts);
+    a.weights = (float*)p.wts->data();
+  }
+  if (p.vals) {
+    tensor_alloc(p.vals);
+    a.vals = (float*)p.vals->data();
+  }
+  Launch L{a};
+  if (c->profiling)
+    L.name = "moe_router{" + std::to_string(T) + "x" + std::to_string(H) + "x" +
+             std::to_string(E) + ",k" + std::to_string(p.k) + (p.wts ? ",norm" : "") + "}";
+  L.fused = true;
+  run_launch(c, std::move(L));
+  return true;
+}
+
 // topK over the last dim (src/rew/ops/sort.nim:36-90 semantics).
 void Lower::emit_topk(Node* n) {
   Tensor *x = n->in[0], *vals = n->out[0], *idx = n->out[1];
@@ -3282,6 +3432,7 @@ static void lower_graph(Ctx* c, Lower& L, const std::string* sig,
     if (!c->dense_moe) L.match_moe();
     L.match_rows();
     L.match_class_head();
+    L.match_router();
     L.match_gemm_groups();
   }
 

@@ -144,6 +144,14 @@ struct PtrVisit {
     field(f, a.probs);
     field(f, a.ids);
   }
+  void operator()(RouterArgs& a) {
+    field(f, a.x);
+    field(f, a.w);
+    field(f, a.b);
+    field(f, a.ids);
+    field(f, a.vals);
+    field(f, a.weights);
+  }
 };
 
 template <class F>
@@ -180,6 +188,7 @@ struct Exec {
   void operator()(CholeskyArgs& a) { launch_cholesky(a, c->stream); }
   void operator()(BatchNormArgs& a) { launch_batchnorm(a, c->stream); }
   void operator()(HeadArgs& a) { launch_class_head(a, c->stream); }
+  void operator()(RouterArgs& a) { launch_moe_router(a, c->stream); }
   void operator()(FillL& l) {
     if (l.bytes == 0) return;
     if (l.src)

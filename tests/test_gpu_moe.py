@@ -280,7 +280,8 @@ def test_dense_moe_switch_keeps_rews_nonfinite_semantics(gpu, oracle):
                        capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stderr[-3000:]
     res = json.loads(r.stdout.strip().splitlines()[-1])
-    assert not any(n.startswith("moe_") for n in res["names"]), res["names"]
+    assert not any(n.startswith("moe_gemm") or n.startswith("moe_combine")
+                   for n in res["names"]), res["names"]
     assert res["equal"] and res["finite_rows"] == 0, res
     moe, host = build_moe(oracle, 64, 128, 64, 8, 2, 1, 0x5EED0606)
     inf_expert(moe, 3)
@@ -291,3 +292,46 @@ def test_dense_moe_switch_keeps_rews_nonfinite_semantics(gpu, oracle):
     _, ids = moe.route(E.fromHost(host["x"], DType.BFLOAT16))
     off = ~np.any(E.toHost(ids) == 3, axis=1)
     assert off.any() and np.all(np.isfinite(got[off])), int(off.sum())
+
+
+@pytest.mark.parametrize("T,H,E_,k,bf16", [(8192, 2048, 64, 6, True), (200, 128, 16, 4, True),
+                                           (77, 256, 60, 3, False)])
+def test_router_one_launch(gpu, T, H, E_, k, bf16):
+    """DeepSeekMoE.route (deepseek.nim:132-137): the router Linear on
+    astype(x, f32), softmax, topK and the renormalisation run as one launch
+    (and topK of the softmax alone, without the renormalisation, too), equal
+    to the op-by-op kernels bit for bit: the same fmaf chain per logit, the
+    softmax and the ranking in the same order, the renormalising sum in rank
+    order.  A row of x holding NaN ranks its NaN probabilities last."""
+    rs = np.random.default_rng(T + E_)
+    x = rs.standard_normal((T, H)).astype(np.float32)
+    x[3, 5] = np.nan
+    wr = (rs.standard_normal((H, E_)) * 0.05).astype(np.float32)
+    br = (rs.standard_normal(E_) * 0.1).astype(np.float32)
+    if bf16:
+        xt = E.fromHost(E.f32_to_bf16_bits(x), DType.BFLOAT16)
+    else:
+        xt = E.fromHost(x)
+    m = nn.DeepSeekMoE(nn.Linear(E.fromHost(wr), E.fromHost(br)), [], [], k)
+
+    def route():
+        tw, ti = m.route(xt)
+        return E.toHost(tw), E.toHost(ti)
+
+    def raw():
+        tv, ti = O.topK(nn.softmax(m.gate.forward(nn._f32(xt)), 1), k, 1, True)
+        return E.toHost(tv), E.toHost(ti)
+
+    for fn, tag in ((route, ",norm}"), (raw, "}")):
+        E.profileBegin()
+        got = fn()
+        names = [n for n, _, _ in E.profileEnd()]
+        assert names == [f"moe_router{{{T}x{H}x{E_},k{k}{tag}"], names
+        E.setMode(E.MODE_OP_BY_OP)
+        try:
+            ref = fn()
+        finally:
+            E.setMode(E.MODE_DEFERRED)
+        np.testing.assert_array_equal(got[1], ref[1])
+        np.testing.assert_array_equal(got[0].view(np.uint32), ref[0].view(np.uint32))
+        assert np.all(np.isnan(got[0][3]))
