@@ -358,9 +358,11 @@ void launch_sort(const SortArgs& g, hipStream_t stream);
 
 // ---- routed MoE (k_moe.hip) ------------------------------------------------------
 constexpr int kMoeMaxK = 16;  // experts per token the combine handles
+constexpr int kMoeMaxMembers = 1536;  // routed experts per call (placement LDS: 36 n bytes)
 // Token placement for one group of routed experts ("members").
 struct MoeRouteArgs {
   const int32_t* topi;       // [T, k] expert ids
+  const float* topw;         // [T, k] gate weights
   int64_t T;
   int k;
   int E;                     // router width: ids are in [0, E)
@@ -371,11 +373,12 @@ struct MoeRouteArgs {
   int32_t* off;              // [n_members + 1] packed row offsets (out)
   int32_t* mt_start;         // [n_members + 1] tile starts (out)
   int32_t* perm;             // [T * k] packed row -> token (out)
-  int32_t* slot_of;          // [T * k] (token, k-slot) -> packed row (out)
+  int32_t* ord_slot;         // [T, k] the token's packed rows in chain order, then -1 (out)
+  float* ord_w;              // [T, k] their gate weights (out)
   int32_t* blk_cnt;          // [ceil(T / kMoeRouteBlock) * n_members] working counts
 };
 constexpr int kMoeRouteBlock = 256;  // tokens per routing workgroup
-void launch_moe_route(const MoeRouteArgs& a, hipStream_t stream);
+int launch_moe_route(const MoeRouteArgs& a, hipStream_t stream);  // returns the launches
 
 // out[t, :] = prev[t, :] then, for token t's routed members in chain order,
 // out = bf16(out + bf16(f32(y[slot, :]) * w)); bf16 rows, H % 8 == 0.
@@ -383,12 +386,10 @@ struct MoeCombineArgs {
   const uint16_t* prev;
   int64_t prev_rs;           // row stride of prev (elements)
   const uint16_t* y;         // [T * k, H] packed expert outputs
-  const float* topw;         // [T, k]
-  const int32_t* topi;       // [T, k]
-  const int32_t* slot_of;    // [T, k]
-  const int32_t* member_of;  // [E]
+  const int32_t* ord_slot;   // [T, k] from the placement
+  const float* ord_w;        // [T, k]
   int64_t T, H;
-  int k, E;
+  int k;
   uint16_t* out;             // dense [T, H]
 };
 void launch_moe_combine(const MoeCombineArgs& a, hipStream_t stream);

@@ -2282,6 +2282,7 @@ static bool reads_dense(Tensor* w) {
 // the running sum densely when their views are not).
 bool Lower::moe_lowerable(const MoePlan& p) {
   if (p.mem.empty() || p.x->shape.rank != 2 || p.topi->shape.rank != 2) return false;
+  if ((int64_t)p.mem.size() > kMoeMaxMembers) return false;
   const int64_t T = p.x->shape.d[0], H = p.x->shape.d[1];
   const int64_t k = p.topi->shape.d[1];
   if (k < 1 || k > kMoeMaxK || H % 8 || p.start->dt != kBF16 || p.start->numel() != T * H)

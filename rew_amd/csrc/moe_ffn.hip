@@ -7,9 +7,10 @@
 //   member_of [E] int32    expert id -> chain index, -1 off the chain
 //   members   [n] int32    chain index -> expert id
 //   tables    [6 n] ptr    per-expert weight / bias device pointers
-//   route     [2 (n + 1) + 2 R + nb n] int32   offsets, tile starts,
-//                                       packed row -> token, (token, slot) ->
-//                                       packed row, per-block counts (nb =
+//   route     [2 (n + 1) + 3 R + nb n] int32   offsets, tile starts,
+//                                       packed row -> token, each token's
+//                                       packed rows and weights (f32) in
+//                                       chain order, per-block counts (nb =
 //                                       ceil(T / 256) token blocks)
 //   hbuf      [R, I] bf16  SwiGLU outputs of the routed rows
 //   ybuf      [R, H] bf16  down-projection outputs of the routed rows
@@ -27,8 +28,9 @@
 namespace rew {
 
 // Experts whose table entries one metadata launch writes (from its
-// kernel arguments, so no host staging buffer is involved).
-constexpr int kMetaChunk = 32;
+// kernel arguments, so no host staging buffer is involved).  The first
+// launch also sets member_of to -1 before the chunks enter their members.
+constexpr int kMetaChunk = 64;
 
 struct MoeMetaChunk {
   int first, count, n;
@@ -36,26 +38,18 @@ struct MoeMetaChunk {
   const void* p[6][kMetaChunk];
 };
 
-__global__ void __launch_bounds__(64) moe_meta_kernel(MoeMetaChunk ch, int32_t* members,
-                                                      const void** tables) {
+__global__ void __launch_bounds__(256) moe_meta_kernel(MoeMetaChunk ch, int E, int32_t* members,
+                                                       int32_t* member_of, const void** tables) {
   const int i = threadIdx.x;
+  if (ch.first == 0) {
+    for (int e = i; e < E; e += 256) member_of[e] = -1;
+    __syncthreads();
+  }
   if (i >= ch.count) return;
   members[ch.first + i] = ch.ids[i];
+  member_of[ch.ids[i]] = ch.first + i;  // the ids are distinct
 #pragma unroll
   for (int j = 0; j < 6; ++j) tables[(size_t)j * ch.n + ch.first + i] = ch.p[j][i];
-}
-
-__global__ void __launch_bounds__(256) moe_member_of_kernel(const int32_t* members, int n,
-                                                            int E, int32_t* member_of) {
-  for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < E; e += gridDim.x * blockDim.x) {
-    int m = -1;
-    for (int i = 0; i < n; ++i)
-      if (members[i] == e) {
-        m = i;
-        break;
-      }
-    member_of[e] = m;
-  }
 }
 
 namespace {
@@ -77,7 +71,7 @@ Layout layout_of(const RoutedFfn& a) {
   o += up((size_t)a.n * 6 * sizeof(void*));
   L.route = o;
   const size_t nb = ((size_t)a.T + kMoeRouteBlock - 1) / kMoeRouteBlock;
-  o += up((2 * ((size_t)a.n + 1) + 2 * R + nb * (size_t)a.n) * 4);
+  o += up((2 * ((size_t)a.n + 1) + 3 * R + nb * (size_t)a.n) * 4);
   L.hbuf = o;
   o += up(R * (size_t)a.I * 2);
   L.ybuf = o;
@@ -128,7 +122,7 @@ void routed_ffn_check(const RoutedFfn& a) {
   if (a.k < 1 || a.k > kMoeMaxK) bad("k must be in 1.." + std::to_string(kMoeMaxK));
   if (a.E < 1) bad("router_width must be positive");
   if (a.n < 1 || a.n > a.E) bad("n_experts must be in 1..router_width");
-  if (a.n > 3200) bad("at most 3200 experts per call");
+  if (a.n > kMoeMaxMembers) bad("at most " + std::to_string(kMoeMaxMembers) + " experts per call");
   if (a.T * (int64_t)a.k >= ((int64_t)1 << 31)) bad("tokens * k must be below 2^31");
   if (!a.expert) bad("null expert_ids");
   for (int i = 0; i < a.n; ++i) {
@@ -184,16 +178,15 @@ void run_routed_ffn(Ctx* c, const RoutedFfn& a, void* scratch) {
       ch.ids[i] = a.expert[first + i];
       for (int j = 0; j < 6; ++j) ch.p[j][i] = a.ptr[j][first + i];
     }
-    hipLaunchKernelGGL(moe_meta_kernel, dim3(1), dim3(64), 0, c->stream, ch, members, tables);
+    hipLaunchKernelGGL(moe_meta_kernel, dim3(1), dim3(256), 0, c->stream, ch, (int)a.E, members,
+                       member_of, tables);
     REW_HIP(hipGetLastError());
   }
-  hipLaunchKernelGGL(moe_member_of_kernel, dim3((unsigned)((a.E + 255) / 256)), dim3(256), 0,
-                     c->stream, (const int32_t*)members, n, a.E, member_of);
-  REW_HIP(hipGetLastError());
   prof_end(c);
 
   MoeRouteArgs ra;
   ra.topi = a.topi;
+  ra.topw = a.topw;
   ra.T = a.T;
   ra.k = a.k;
   ra.E = a.E;
@@ -204,12 +197,13 @@ void run_routed_ffn(Ctx* c, const RoutedFfn& a, void* scratch) {
   ra.off = route;
   ra.mt_start = route + (n + 1);
   ra.perm = route + 2 * (n + 1);
-  ra.slot_of = route + 2 * (n + 1) + R;
-  ra.blk_cnt = route + 2 * (n + 1) + 2 * R;
+  ra.ord_slot = route + 2 * (n + 1) + R;
+  ra.ord_w = reinterpret_cast<float*>(route + 2 * (n + 1) + 2 * R);
+  ra.blk_cnt = route + 2 * (n + 1) + 3 * R;
   if (c->profiling)
     prof_begin(c, "moe_route{" + std::to_string(a.T) + "x" + std::to_string(a.k) + ",E" +
                       std::to_string(n) + "}");
-  launch_moe_route(ra, c->stream);
+  const int route_launches = launch_moe_route(ra, c->stream);
   prof_end(c);
 
   GemmArgs gs, gd;
@@ -258,20 +252,17 @@ void run_routed_ffn(Ctx* c, const RoutedFfn& a, void* scratch) {
   ca.prev = (const uint16_t*)a.start;
   ca.prev_rs = a.start_rs;
   ca.y = (const uint16_t*)gd.c;
-  ca.topw = a.topw;
-  ca.topi = a.topi;
-  ca.slot_of = ra.slot_of;
-  ca.member_of = member_of;
+  ca.ord_slot = ra.ord_slot;
+  ca.ord_w = ra.ord_w;
   ca.T = a.T;
   ca.H = a.H;
   ca.k = a.k;
-  ca.E = a.E;
   ca.out = (uint16_t*)a.out;
   if (c->profiling)
     prof_begin(c, "moe_combine{" + std::to_string(a.T) + "x" + std::to_string(a.H) + "}");
   launch_moe_combine(ca, c->stream);
   prof_end(c);
-  c->stats.kernels_launched += 5 + (n + kMetaChunk - 1) / kMetaChunk;
+  c->stats.kernels_launched += route_launches + 3 + (n + kMetaChunk - 1) / kMetaChunk;
   c->stats.fused_groups += 4;
 }
 

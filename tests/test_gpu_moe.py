@@ -219,6 +219,48 @@ def test_direct_routed_ffn_equals_graph_lowering(gpu, oracle, T):
     assert err <= 2e-2
 
 
+@pytest.mark.parametrize("T,E_,chain", [
+    (37, 16, [0, 2, 3, 5, 8, 9, 13, 15]),
+    (300, 16, [0, 2, 3, 5, 8, 9, 13, 15]),
+    # 1094 blocks of 256 tokens x 60 members: past the placement's fused
+    # count-table limit (65536 entries), so the block prefixes run as their
+    # own launch
+    (280000, 64, [e for e in range(64) if e % 16 != 7]),
+])
+def test_direct_routed_ffn_repeated_and_off_chain_ids(gpu, oracle, T, E_, chain):
+    """Top-k tables a router never produces, through the C-ABI entry point:
+    a repeated id (its rows computed once and weighted by the sum of its
+    slots' weights, as routedWeightForExpert sums topWeights * (ids == e)),
+    ids outside [0, width) and ids of experts off the chain (no
+    contribution).  Equal bit for bit to rew's dense chain over the same
+    tables, evaluated op by op."""
+    moe, host = build_moe(oracle, T, 256, 128, E_, 4, 1, 0x5EED0705 + T)
+    xt = E.fromHost(host["x"], DType.BFLOAT16)
+    start = moe.sharedExperts[0].forward(xt)
+    g = np.random.default_rng(T)
+    ti = np.argsort(g.random((T, E_)), axis=1)[:, :4].astype(np.int32)  # distinct
+    ti[::5, 1] = ti[::5, 0]          # one repeated pair (at most two equal ids)
+    ti[::7, 2] = -1                  # outside the router width
+    ti[::11, 3] = E_ + 3
+    tw = (g.random((T, 4), dtype=np.float32) + np.float32(0.05)).astype(np.float32)
+    topW, topI = E.fromHost(tw), E.fromHost(ti)
+    experts = [moe.routedExperts[e] for e in chain]
+    direct = E.toHost(E.moeRoutedFfn(xt, start, topW, topI, experts, chain, E_))
+    E.setMode(1)
+    try:
+        out = start
+        for e in chain:
+            w = nn.routedWeightForExpert(topW, topI, e)
+            wB = O.broadcastTo(O.unsqueeze(w, 1), list(xt.shape), [0, 1])
+            y = O.astype(moe.routedExperts[e].forward(xt), DType.FLOAT32)
+            out = O.add(out, O.astype(O.mul(y, wB), DType.BFLOAT16))
+        dense = E.toHost(out)
+    finally:
+        E.setMode(0)
+    assert np.isfinite(E.toHostF32(out)).all()
+    np.testing.assert_array_equal(direct, dense)
+
+
 def test_direct_routed_ffn_rejects_bad_arguments(gpu, oracle):
     moe, host = build_moe(oracle, 16, 128, 64, 8, 2, 0, 0x5EED0505)
     xt = E.fromHost(host["x"], DType.BFLOAT16)
