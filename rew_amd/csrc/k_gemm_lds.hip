@@ -173,7 +173,12 @@ __device__ __forceinline__ void tile_order(int64_t bid, int64_t tiles_m, int64_t
 
 // BUF: K % BK == 0 and every operand byte offset below 2^31 from its
 // descriptor base (checked at launch); the K-tail path then never runs.
-template <bool B_KC, bool DUAL, bool GROUP, bool BUF>
+// FAR (DUAL only): the gate and up matrices lie too far apart for one
+// descriptor (allocations need not be near each other), so B moves by
+// global_load_lds from per-lane 64-bit addresses (A still through its
+// descriptor): a few VALU instructions per B DMA more than one descriptor,
+// far fewer than the K-tail path.
+template <bool B_KC, bool DUAL, bool GROUP, bool BUF, bool FAR = false>
 __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs ga) {
   // LDS, 128 KiB.  K-tail path: four 32 KiB stages, each the A and B halves
   // of one k-tile.  BUF path: two 32 KiB A stages, each a k-tile pair (256
@@ -241,6 +246,7 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
   const uint16_t* B2 = nullptr;
   if constexpr (DUAL)
     B2 = GROUP ? (const uint16_t*)ga.b2[grp] : (const uint16_t*)g.b2 + b * g.b_sb;
+  static_assert(!FAR || (DUAL && BUF), "FAR is a DUAL BUF mode");
   // BUF descriptors: A from its (batch) base; B from the lower of B1 / B2
   const uint16_t* Bbase = (DUAL && B2 < B1) ? B2 : B1;
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, 0x7fffffffu);
@@ -293,8 +299,9 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
       if (col > g.N - 8) col = g.N - 8;
       pb[q] = src + (int64_t)kr * g.b_sk + col;
       b_sel[q] = kr;
-      vb[q] = (uint32_t)((const uint8_t*)src - (const uint8_t*)Bbase) +
-              (uint32_t)(((int64_t)kr * g.b_sk + col) * 2);
+      vb[q] = FAR ? 0u
+                  : (uint32_t)((const uint8_t*)src - (const uint8_t*)Bbase) +
+                        (uint32_t)(((int64_t)kr * g.b_sk + col) * 2);
     }
   }
 
@@ -325,11 +332,18 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
   // k-step and waited on that scalar load right after the barrier)
   const uint32_t b_kbytes = __builtin_amdgcn_readfirstlane((uint32_t)(B_KC ? 2 : g.b_sk * 2));
   // BUF: the B half of k-tile k0 / BK into B stage bst
+  // B DMA instruction q, sob bytes along k (FAR: from the lane's pointer)
+  auto dma_b = [&](int q, uint32_t sob, uint8_t* dst) {
+    if constexpr (FAR)
+      to_lds16((const uint8_t*)pb[q] + sob, dst);
+    else
+      buf_to_lds16(rb, vb[q], sob, dst);
+  };
   auto issue_b = [&](uint8_t* bst, int k0) {
     uint8_t* sb = bst + wave * 4096;
     const uint32_t sob = (uint32_t)k0 * b_kbytes;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) buf_to_lds16(rb, vb[q], sob, sb + q * 1024);
+    for (int q = 0; q < 4; ++q) dma_b(q, sob, sb + q * 1024);
   };
   // BUF: half `half` (rows 128 half .. + 127) of A of the k-tile pair
   // starting at k0, into A stage ast
@@ -353,7 +367,7 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
 #pragma unroll
       for (int q = 0; q < 4; ++q) buf_to_lds16(ra, va[q], soa, sa + q * 1024);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) buf_to_lds16(rb, vb[q], sob, sb + q * 1024);
+      for (int q = 0; q < 4; ++q) dma_b(q, sob, sb + q * 1024);
     } else {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -878,23 +892,26 @@ bool gemm_lds_ok(const GemmArgs& g, bool* b_kc) {
 
 // Whether the buffer-descriptor DMA path can run g: K a multiple of 2 BK
 // (A moves in k-tile pairs) and every byte offset the kernel forms (row
-// offset + k advance) below 2^31.
-static bool buf_ok(const GemmArgs& g, const GroupArgs* ga, bool bkc, bool dual) {
+// offset + k advance) below 2^31.  0: no; 1: yes; 2: yes with a descriptor
+// per SwiGLU matrix (their distance apart is past the limit, each matrix's
+// own extent is not).
+static int buf_mode(const GemmArgs& g, const GroupArgs* ga, bool bkc, bool dual) {
   constexpr int64_t kLim = (int64_t)1 << 31;
-  if (g.K % (2 * BK)) return false;
+  if (g.K % (2 * BK)) return 0;
   const int64_t a_span = ((g.M - 1) * g.a_sm + g.K) * 2;
-  int64_t b_span = bkc ? ((g.N - 1) * g.b_sn + g.K) * 2 : ((g.K - 1) * g.b_sk + g.N) * 2;
+  const int64_t b_span = bkc ? ((g.N - 1) * g.b_sn + g.K) * 2 : ((g.K - 1) * g.b_sk + g.N) * 2;
+  if (a_span >= kLim || b_span >= kLim) return 0;
   if (dual) {
     int64_t d = -1;
     if (ga) d = ga->dual_span;
     else d = (int64_t)((uintptr_t)g.b2 - (uintptr_t)g.b);
-    if (ga && d < 0) return false;
-    b_span += d < 0 ? -d : d;
+    if (ga && d < 0) return 0;
+    if (b_span + (d < 0 ? -d : d) >= kLim) return bkc ? 0 : 2;
   }
-  return a_span < kLim && b_span < kLim;
+  return 1;
 }
 
-static void launch_segs(const GemmSegs& gs, const GroupArgs* ga, bool bkc, bool buf,
+static void launch_segs(const GemmSegs& gs, const GroupArgs* ga, bool bkc, int buf,
                         hipStream_t stream) {
   const GemmArgs& g = gs.g[0];
   const bool dual = g.epi == EPI_SWIGLU;
@@ -905,11 +922,14 @@ static void launch_segs(const GemmSegs& gs, const GroupArgs* ga, bool bkc, bool 
   const GroupArgs none{};
   const GroupArgs& G = ga ? *ga : none;
   const dim3 grid((unsigned)tiles), block(256);
-#define REW_LDS_LAUNCH(BKC, DU, GR)                                                           \
-  do {                                                                                       \
-    if (buf)                                                                                 \
+#define REW_LDS_LAUNCH(BKC, DU, GR)                                                          \
+  do {                                                                                      \
+    if (DU && buf == 2)                                                                     \
+      hipLaunchKernelGGL((gemm_lds_kernel<BKC, DU, GR, true, DU>), grid, block, 0, stream, gs, \
+                         G);                                                                \
+    else if (buf)                                                                           \
       hipLaunchKernelGGL((gemm_lds_kernel<BKC, DU, GR, true>), grid, block, 0, stream, gs, G); \
-    else                                                                                     \
+    else                                                                                    \
       hipLaunchKernelGGL((gemm_lds_kernel<BKC, DU, GR, false>), grid, block, 0, stream, gs, G); \
   } while (0)
   if (ga) {
@@ -939,16 +959,18 @@ void launch_gemm_lds(const GemmArgs& g, const GroupArgs* ga, hipStream_t stream)
   gs.n = 1;
   gs.g[0] = g;
   gs.tn0[1] = (g.N + (dual ? 127 : 255)) / (dual ? 128 : 256);
-  launch_segs(gs, ga, bkc, buf_ok(g, ga, bkc, dual), stream);
+  launch_segs(gs, ga, bkc, buf_mode(g, ga, bkc, dual), stream);
 }
 
 bool gemm_multi_ok(const GemmArgs* segs, int n) {
   if (n < 1 || n > kMaxSegs) return false;
   bool bkc0 = false;
+  // SwiGLU segments (the dual kernel) go only with SwiGLU segments
+  const bool dual = segs[0].epi == EPI_SWIGLU;
   for (int i = 0; i < n; ++i) {
     const GemmArgs& g = segs[i];
     bool bkc;
-    if (!gemm_lds_ok(g, &bkc) || g.epi == EPI_SWIGLU) return false;
+    if (!gemm_lds_ok(g, &bkc) || (g.epi == EPI_SWIGLU) != dual) return false;
     if (i == 0) {
       bkc0 = bkc;
       continue;
@@ -966,12 +988,16 @@ void launch_gemm_multi(const GemmArgs* segs, int n, hipStream_t stream) {
   GemmSegs gs;
   std::memset(&gs, 0, sizeof gs);
   gs.n = n;
-  bool bkc = false, buf = true;
+  bool bkc = false;
+  int buf = 1;  // the lowest segment's mode, FAR over plain
+  const bool dual = segs[0].epi == EPI_SWIGLU;
+  const int tn = dual ? 128 : 256;  // output columns per tile
   for (int i = 0; i < n; ++i) {
     gemm_lds_ok(segs[i], &bkc);
-    buf = buf && buf_ok(segs[i], nullptr, bkc, false);
+    const int m = buf_mode(segs[i], nullptr, bkc, dual);
+    buf = (buf == 0 || m == 0) ? 0 : (buf == 2 || m == 2 ? 2 : 1);
     gs.g[i] = segs[i];
-    gs.tn0[i + 1] = gs.tn0[i] + (segs[i].N + 255) / 256;
+    gs.tn0[i + 1] = gs.tn0[i] + (segs[i].N + tn - 1) / tn;
   }
   launch_segs(gs, nullptr, bkc, buf, stream);
 }

@@ -39,6 +39,85 @@ __device__ __forceinline__ bool rank_first(float av, int ai, float bv, int bi) {
   return ai < bi;
 }
 
+// The rest of the router for one row whose logits (without the bias) 16
+// lanes hold, four columns each (lanes 16 q .. 16 q + 15 of a wave; lane
+// l16 columns c4 .. c4 + 3): softmax_tile_kernel's steps (the max, expf, the
+// running sum in column order on the row's first lane, the quotients),
+// topk_rows_kernel's ranking and the renormalisation in rank order.  Every
+// thread of the workgroup calls it (it holds barriers); row t >= T stores
+// nothing.  lg: the row's LDS scratch of kRouterMaxE + 1 floats.
+__device__ __forceinline__ void router_tail(const RouterArgs& a, float (&y)[4], int c4,
+                                            int64_t t, float* lg) {
+  const int E = a.E;
+  const int l16 = threadIdx.x & 15;
+  const bool row_ok = t < a.T;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (c4 + j >= E) y[j] = 0.0f;
+  // softmax: the max (order-free) over the 16 lanes, the exps in place, the
+  // sum in column order on the row's first lane (the reduction's order),
+  // then the quotients
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (c4 + j < E) m = vm::fmax_prop(m, y[j]);
+#pragma unroll
+  for (int off = 8; off >= 1; off >>= 1) m = vm::fmax_prop(m, __shfl_xor(m, off, 16));
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (c4 + j < E) {
+      y[j] = expf(y[j] - m);
+      lg[c4 + j] = y[j];
+    }
+  __syncthreads();
+  if (l16 == 0) {
+    float sum = 0.0f;
+    for (int j = 0; j < E; ++j) sum = sum + lg[j];
+    lg[kRouterMaxE] = sum;
+  }
+  __syncthreads();
+  const float sum = lg[kRouterMaxE];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) y[j] = y[j] / sum;
+  // top-k: each round the best untaken column of each lane, then the best of
+  // the 16 (a total order, so every lane agrees on the winner); the row's
+  // first lane keeps the values for the renormalisation in rank order
+  // (the values wait in lg[0 .. k), which only the row's first lane touches
+  // from here on: the exps there are spent)
+  uint32_t taken = 0;
+  float denom = 0.0f;
+  for (int s = 0; s < a.k; ++s) {
+    float bv = 0.0f;
+    int bi = kNoCol;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (c4 + j < E && !((taken >> j) & 1) && rank_first(y[j], c4 + j, bv, bi)) {
+        bv = y[j];
+        bi = c4 + j;
+      }
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 16);
+      const int oi = __shfl_xor(bi, off, 16);
+      if (rank_first(ov, oi, bv, bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if (bi >= c4 && bi < c4 + 4) taken |= 1u << (bi - c4);
+    if (l16 == 0) {
+      lg[s] = bv;
+      denom = denom + bv;
+      if (row_ok) {
+        a.ids[t * a.k + s] = bi;
+        if (a.vals) a.vals[t * a.k + s] = bv;
+      }
+    }
+  }
+  if (l16 == 0 && row_ok && a.weights)
+    for (int s = 0; s < a.k; ++s) a.weights[t * a.k + s] = lg[s] / denom;
+}
+
 template <bool XBF16>
 __global__ void __launch_bounds__(256) moe_router_kernel(RouterArgs a) {
   __shared__ __attribute__((aligned(16))) float As[32][17];  // [k][row]
@@ -127,75 +206,171 @@ __global__ void __launch_bounds__(256) moe_router_kernel(RouterArgs a) {
   }
   // the row's 16 lanes (one wave holds four rows) hold its logits, four
   // columns each; columns past E take no part
-  const int l16 = tid & 15;
-  const bool row_ok = m0 + r < a.T;
-  float y[4];
   const float accs[4] = {acc0, acc1, acc2, acc3};
+  float y[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) y[j] = c4 + j < E ? accs[j] + bias[j] : 0.0f;
-  // softmax: the max (order-free) over the 16 lanes, the exps in place, the
-  // sum in column order on the row's first lane (the reduction's order),
-  // then the quotients
-  float m = -INFINITY;
+  for (int j = 0; j < 4; ++j) y[j] = accs[j] + bias[j];
+  router_tail(a, y, c4, m0 + r, lg[r]);
+}
+
+// The DPP form, for H % 128 == 0: thread (wave w, lane l) owns rows
+// 8 w + 2 (l / 16) and the next of the workgroup's 32, and columns
+// 4 (l % 16) .. + 3.  x never passes through LDS: for each 128-deep k-chunk,
+// lane l holds x[row][k0 + 8 (l % 16) .. + 7] of its two rows in registers,
+// and the value at k is broadcast from lane (k - k0) / 8 of each 16-lane row
+// by DPP row_newbcast.  W's chunk ([128, 64] f32, 32 KiB) is staged through
+// LDS, two stages: W rows loaded into registers during chunk c are written
+// to LDS at the start of chunk c + 1 (for chunk c + 2), so a whole chunk of
+// arithmetic covers each load.  Each logit is
+// the same fmaf chain over k from 0 as the narrow kernel's, so the bits
+// agree.  Per k a thread issues 2 broadcasts, 8 fmas and one 16-byte LDS
+// read, against 4 fmas, a 16-byte and a 4-byte LDS read in the narrow form:
+// the LDS traffic per fma halves and the broadcasts need no LDS.
+template <int J>
+__device__ __forceinline__ float row_bcast(float v) {
+  return __int_as_float(
+      __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + J, 0xf, 0xf, true));
+}
+
+// k-steps 8 J .. 8 J + 7 of a chunk; bc holds their W rows, read one group ahead
+template <int J>
+__device__ __forceinline__ void router_chunk(const float (*bs)[64], int c4, const float (&f0)[8],
+                                             const float (&f1)[8], const float4 (&bc)[8],
+                                             float (&acc0)[4], float (&acc1)[4]) {
+  float4 bn[8];
+  if constexpr (J + 1 < 16) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    if (c4 + j < E) m = vm::fmax_prop(m, y[j]);
-#pragma unroll
-  for (int off = 8; off >= 1; off >>= 1) m = vm::fmax_prop(m, __shfl_xor(m, off, 16));
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    if (c4 + j < E) {
-      y[j] = expf(y[j] - m);
-      lg[r][c4 + j] = y[j];
-    }
-  __syncthreads();
-  if (l16 == 0) {
-    float sum = 0.0f;
-    for (int j = 0; j < E; ++j) sum = sum + lg[r][j];
-    lg[r][kRouterMaxE] = sum;
+    for (int e = 0; e < 8; ++e) bn[e] = *(const float4*)&bs[8 * (J + 1) + e][c4];
   }
-  __syncthreads();
-  const float sum = lg[r][kRouterMaxE];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) y[j] = y[j] / sum;
-  // top-k: each round the best untaken column of each lane, then the best of
-  // the 16 (a total order, so every lane agrees on the winner); the row's
-  // first lane keeps the values for the renormalisation in rank order
-  uint32_t taken = 0;
-  float vals[kRouterMaxK];
-  float denom = 0.0f;
-  for (int s = 0; s < a.k; ++s) {
-    float bv = 0.0f;
-    int bi = kNoCol;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (c4 + j < E && !((taken >> j) & 1) && rank_first(y[j], c4 + j, bv, bi)) {
-        bv = y[j];
-        bi = c4 + j;
-      }
-#pragma unroll
-    for (int off = 8; off >= 1; off >>= 1) {
-      const float ov = __shfl_xor(bv, off, 16);
-      const int oi = __shfl_xor(bi, off, 16);
-      if (rank_first(ov, oi, bv, bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    if (bi >= c4 && bi < c4 + 4) taken |= 1u << (bi - c4);
-    if (l16 == 0) {
-      vals[s] = bv;
-      denom = denom + bv;
-      if (row_ok) {
-        const int64_t t = m0 + r;
-        a.ids[t * a.k + s] = bi;
-        if (a.vals) a.vals[t * a.k + s] = bv;
-      }
-    }
+  for (int e = 0; e < 8; ++e) {
+    const float a0 = row_bcast<J>(f0[e]), a1 = row_bcast<J>(f1[e]);
+    acc0[0] = fmaf(a0, bc[e].x, acc0[0]);
+    acc0[1] = fmaf(a0, bc[e].y, acc0[1]);
+    acc0[2] = fmaf(a0, bc[e].z, acc0[2]);
+    acc0[3] = fmaf(a0, bc[e].w, acc0[3]);
+    acc1[0] = fmaf(a1, bc[e].x, acc1[0]);
+    acc1[1] = fmaf(a1, bc[e].y, acc1[1]);
+    acc1[2] = fmaf(a1, bc[e].z, acc1[2]);
+    acc1[3] = fmaf(a1, bc[e].w, acc1[3]);
   }
-  if (l16 == 0 && row_ok && a.weights) {
-    const int64_t t = m0 + r;
-    for (int s = 0; s < a.k; ++s) a.weights[t * a.k + s] = vals[s] / denom;
+  if constexpr (J + 1 < 16) router_chunk<J + 1>(bs, c4, f0, f1, bn, acc0, acc1);
+}
+
+template <bool XBF16>
+__global__ void __launch_bounds__(256) moe_router_dpp_kernel(RouterArgs a) {
+  __shared__ __attribute__((aligned(16))) float Bs[2][128][64];  // 64 KiB
+  __shared__ float lg[32][kRouterMaxE + 1];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, c4 = l16 * 4;
+  const int rp = wave * 8 + (lane >> 4) * 2;  // the thread's first row in the workgroup
+  const int64_t m0 = (int64_t)blockIdx.x * 32;
+  const int E = a.E;
+  constexpr int xe = XBF16 ? 2 : 4;
+  constexpr int NV = XBF16 ? 1 : 2;  // 16-byte x vectors per row per chunk
+  const int64_t r0 = m0 + rp < a.T ? m0 + rp : a.T - 1;
+  const int64_t r1 = m0 + rp + 1 < a.T ? m0 + rp + 1 : a.T - 1;
+  const char* x0 = (const char*)a.x + (r0 * a.x_rs + l16 * 8) * xe;
+  const char* x1 = (const char*)a.x + (r1 * a.x_rs + l16 * 8) * xe;
+  // W chunk loader: 2048 16-byte vectors, thread tid takes k-rows
+  // tid / 16 + 16 i and columns 4 (tid % 16) .. + 3 (clamped past E)
+  const int bk = tid >> 4, bc4 = (tid & 15) * 4;
+  const float* wp = a.w + (int64_t)bk * E + (bc4 < E ? bc4 : E - 4);
+  float bias[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) bias[j] = a.b[c4 + j < E ? c4 + j : 0];
+  float acc0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, acc1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int nch = (int)(a.H / 128);
+  // the next chunk's x (as loaded) and W rows, in registers
+  uint4 n0[NV], n1[NV];
+  // (eight named registers: as an array the compiler kept them in scratch
+  // memory across the chunk loop)
+  float4 nb0, nb1, nb2, nb3, nb4, nb5, nb6, nb7;
+#define REW_NB_LOAD(K0)                                       \
+  do {                                                        \
+    const float* q_ = wp + (int64_t)(K0) * E;                 \
+    nb0 = *(const float4*)(q_);                               \
+    nb1 = *(const float4*)(q_ + 16 * (int64_t)E);             \
+    nb2 = *(const float4*)(q_ + 32 * (int64_t)E);             \
+    nb3 = *(const float4*)(q_ + 48 * (int64_t)E);             \
+    nb4 = *(const float4*)(q_ + 64 * (int64_t)E);             \
+    nb5 = *(const float4*)(q_ + 80 * (int64_t)E);             \
+    nb6 = *(const float4*)(q_ + 96 * (int64_t)E);             \
+    nb7 = *(const float4*)(q_ + 112 * (int64_t)E);            \
+  } while (0)
+#define REW_NB_STORE(ST)                                      \
+  do {                                                        \
+    float (*bw_)[64] = Bs[ST];                                \
+    *(float4*)&bw_[bk][bc4] = nb0;                            \
+    *(float4*)&bw_[bk + 16][bc4] = nb1;                       \
+    *(float4*)&bw_[bk + 32][bc4] = nb2;                       \
+    *(float4*)&bw_[bk + 48][bc4] = nb3;                       \
+    *(float4*)&bw_[bk + 64][bc4] = nb4;                       \
+    *(float4*)&bw_[bk + 80][bc4] = nb5;                       \
+    *(float4*)&bw_[bk + 96][bc4] = nb6;                       \
+    *(float4*)&bw_[bk + 112][bc4] = nb7;                      \
+  } while (0)
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    n0[i] = *(const uint4*)(x0 + 16 * i);
+    n1[i] = *(const uint4*)(x1 + 16 * i);
+  }
+  REW_NB_LOAD(0);
+  REW_NB_STORE(0);
+  REW_NB_LOAD(nch > 1 ? 128 : 0);
+  __syncthreads();
+  for (int c = 0; c < nch; ++c) {
+    // chunk c + 1's W rows into the other stage (last read in chunk c - 1,
+    // before the barrier that ended it), then chunk c + 2's loads; all
+    // chunk indices are clamped, so no branch separates a load from its use
+    REW_NB_STORE((c + 1) & 1);
+    REW_NB_LOAD((int64_t)(c + 2 < nch ? c + 2 : nch - 1) * 128);
+    float f0[8], f1[8];
+    if constexpr (XBF16) {
+      const uint32_t w0[4] = {n0[0].x, n0[0].y, n0[0].z, n0[0].w};
+      const uint32_t w1[4] = {n1[0].x, n1[0].y, n1[0].z, n1[0].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f0[2 * i] = vm::as_f(w0[i] << 16);
+        f0[2 * i + 1] = vm::as_f(w0[i] & 0xffff0000u);
+        f1[2 * i] = vm::as_f(w1[i] << 16);
+        f1[2 * i + 1] = vm::as_f(w1[i] & 0xffff0000u);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        f0[4 * i] = vm::as_f(n0[i].x);
+        f0[4 * i + 1] = vm::as_f(n0[i].y);
+        f0[4 * i + 2] = vm::as_f(n0[i].z);
+        f0[4 * i + 3] = vm::as_f(n0[i].w);
+        f1[4 * i] = vm::as_f(n1[i].x);
+        f1[4 * i + 1] = vm::as_f(n1[i].y);
+        f1[4 * i + 2] = vm::as_f(n1[i].z);
+        f1[4 * i + 3] = vm::as_f(n1[i].w);
+      }
+    }
+    // the next chunk's x
+    const int64_t kn = (int64_t)(c + 1 < nch ? c + 1 : c) * 128;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      n0[i] = *(const uint4*)(x0 + kn * xe + 16 * i);
+      n1[i] = *(const uint4*)(x1 + kn * xe + 16 * i);
+    }
+    const float (*bs)[64] = Bs[c & 1];
+    float4 b0[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) b0[e] = *(const float4*)&bs[e][c4];
+    router_chunk<0>(bs, c4, f0, f1, b0, acc0, acc1);
+    __syncthreads();
+  }
+#undef REW_NB_LOAD
+#undef REW_NB_STORE
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    float y[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) y[j] = (rr ? acc1[j] : acc0[j]) + bias[j];
+    router_tail(a, y, c4, m0 + rp + rr, lg[rp + rr]);
   }
 }
 
@@ -211,6 +386,15 @@ bool moe_router_ok(const RouterArgs& a) {
 
 void launch_moe_router(const RouterArgs& a, hipStream_t stream) {
   if (!moe_router_ok(a)) fail(REW_MI355X_ERR_INVALID, "internal: router launch outside its limits");
+  if (a.H % 128 == 0) {
+    const unsigned blocks = (unsigned)((a.T + 31) / 32);
+    if (a.x_bf16)
+      hipLaunchKernelGGL(moe_router_dpp_kernel<true>, dim3(blocks), dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL(moe_router_dpp_kernel<false>, dim3(blocks), dim3(256), 0, stream, a);
+    REW_HIP(hipGetLastError());
+    return;
+  }
   const unsigned blocks = (unsigned)((a.T + 15) / 16);
   if (a.x_bf16)
     hipLaunchKernelGGL(moe_router_kernel<true>, dim3(blocks), dim3(256), 0, stream, a);

@@ -1994,7 +1994,8 @@ static const char* epi_suffix(int epi) {
 
 bool Lower::emit_gemm_fused(Tensor* t, const GemmPlan& p) {
   if (p.group >= 0) {
-    // the planned siblings (q / k / v of one input) in one launch
+    // the planned siblings (q / k / v of one input, or the SwiGLU pairs of
+    // DeepSeekMoE's shared experts) in one launch
     std::vector<Tensor*> outs = {t};
     std::vector<GemmPlan> plans = {p};
     for (Tensor* u : gemm_groups[p.group]) {
@@ -2021,7 +2022,8 @@ bool Lower::emit_gemm_fused(Tensor* t, const GemmPlan& p) {
       Launch L{GemmL{args, true}};
       if (c->profiling) {
         char nm[200];
-        std::snprintf(nm, sizeof nm, "gemm_lds_nn{%s}[1,%lld,%lld,%lld]", parts.c_str(),
+        std::snprintf(nm, sizeof nm, "%s{%s}[1,%lld,%lld,%lld]",
+                      p.epi == EPI_SWIGLU ? "gemm_lds_swiglu" : "gemm_lds_nn", parts.c_str(),
                       (long long)args[0].M, (long long)n_all, (long long)args[0].K);
         L.name = nm;
       }
@@ -2057,23 +2059,28 @@ bool Lower::emit_gemm_fused(Tensor* t, const GemmPlan& p) {
 // v projections of GroupedQueryAttention.forward, groupedqueryattention.nim)
 // become one multi-segment launch.
 void Lower::match_gemm_groups() {
-  std::unordered_map<Tensor*, std::vector<Tensor*>> by_a;
-  std::vector<Tensor*> order;
+  // key: the input seen through reshapes (q, k and v each reshape the same
+  // normed tensor), and whether the plan is a SwiGLU pair (DeepSeekMoE's
+  // shared experts all read x; the dual kernel takes only SwiGLU segments)
+  using Key = std::pair<Tensor*, bool>;
+  std::map<Key, std::vector<Tensor*>> by_a;
+  std::vector<Key> order;
   for (Node* n : nodes)
     for (Tensor* t : n->out) {
       auto it = gemm_out.find(t);
       if (it == gemm_out.end()) continue;
       const GemmPlan& gp = it->second;
-      if (gp.epi != EPI_BIAS && gp.epi != EPI_BIAS_ROPE && gp.epi != EPI_BIAS_RES) continue;
-      // key: the input seen through reshapes (q, k and v each reshape the
-      // same normed tensor) plus its shape as a matrix
+      const bool dual = gp.epi == EPI_SWIGLU;
+      if (gp.epi != EPI_BIAS && gp.epi != EPI_BIAS_ROPE && gp.epi != EPI_BIAS_RES && !dual)
+        continue;
       Tensor* a = gp.dot->in[0];
       while (a->prod && a->prod->kind == K_RESHAPE && !a->st) a = a->prod->in[0];
       if (gp.dot->in[0]->shape.rank != 2) continue;
-      if (!by_a.count(a)) order.push_back(a);
-      by_a[a].push_back(t);
+      const Key key{a, dual};
+      if (!by_a.count(key)) order.push_back(key);
+      by_a[key].push_back(t);
     }
-  for (Tensor* a : order) {
+  for (const Key& a : order) {
     std::vector<Tensor*>& v = by_a[a];
     for (size_t i = 0; i + 1 < v.size(); i += kMaxSegs) {
       const size_t n = std::min(v.size() - i, (size_t)kMaxSegs);

@@ -86,6 +86,49 @@ def test_residual_epilogue(gpu, oracle, B, S, H):
     bf16_close(_bits_f32(got), want)
 
 
+def far_apart(mats):
+    """bf16 matrices of one shape placed more than 2 GiB apart inside one
+    allocation: matrix i is rows R i .. R i + r of `big` [R k + r, c].
+    Returns (big, R, view) with view(i) that matrix as a slice; a slice
+    stays a view only while the caller does not hold it at the flush, so
+    make it inside the function that is flushed."""
+    r, c = mats[0].shape
+    R = (1 << 31) // (c * 2) + 64
+    big = O.zeros([R * (len(mats) - 1) + r, c], DType.BFLOAT16)
+    for i, m in enumerate(mats):
+        big = O.dynamicUpdateSlice(big, E.fromHost(m, DType.BFLOAT16),
+                                   [O.scalarI32(R * i), O.scalarI32(0)])
+    E.flush()
+    return big, R, lambda i: O.slice_(big, [R * i, 0], [R * i + r, c])
+
+
+def test_swiglu_gate_and_up_far_apart(gpu, oracle):
+    """The dual SwiGLU kernel addresses both weight matrices through one
+    buffer descriptor when they lie within 2 GiB of each other; allocations
+    need not, and with the up weight 2 GiB past the gate weight it takes a
+    descriptor per matrix.  Same bits as op by op."""
+    T, E_, I = 2048, 512, 1536  # 8 x 12 dual tiles: the LDS kernel
+    key = oracle.init_key(777)
+    wg, bg = _lin(oracle, oracle.fold_in(key, 0), E_, I, 0.3)
+    wu, bu = _lin(oracle, oracle.fold_in(key, 1), E_, I, 0.3)
+    wd, bd = _lin(oracle, oracle.fold_in(key, 2), I, E_, 0.3)
+    x = oracle.round_bf16(oracle.normal_f32(oracle.fold_in(key, 3), T * E_).reshape(1, T, E_))
+    _, _, view = far_apart([wg, wu])
+
+    def fn():
+        mk = lambda w, b: nn.Linear(w, E.fromHost(b, DType.BFLOAT16))
+        ffn = nn.GatedFeedForward(mk(view(0), bg), mk(view(1), bu),
+                                  mk(E.fromHost(wd, DType.BFLOAT16), bd))
+        return ffn.forward(E.fromHost(x, DType.BFLOAT16))
+
+    got, names = _run(fn)
+    assert any(n.startswith("gemm_lds_swiglu") for n in names), names
+    ref, _ = _run(fn, op_by_op=True)
+    np.testing.assert_array_equal(got, ref)
+    want = oracle.gated_ffn(x.reshape(T, E_), wg, bg, wu, bu, wd, bd, True).reshape(1, T, E_)
+    bf16_close(_bits_f32(got), want)
+
+
 @pytest.mark.parametrize("T,E_,I", [(256, 256, 512), (300, 128, 264), (1024, 512, 1408)])
 def test_swiglu_dual_gemm(gpu, oracle, T, E_, I):
     key = oracle.init_key(300 + I)

@@ -22,6 +22,9 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
+import ctypes as C
+
+from rew_amd import _lib
 from rew_amd import eager as E
 from rew_amd import nn, rng
 from rew_amd import ops as O
@@ -106,6 +109,13 @@ def test_moe_matches_oracle(gpu, oracle, T, H, I, E_, k, n_shared):
     prof = [name for name, _, _ in E.profileEnd()]
     assert any(n.startswith("moe_gemm_swiglu") for n in prof), prof
     assert any(n.startswith("moe_combine") for n in prof), prof
+    # the shared experts' SwiGLU GEMMs read the same x: one launch of
+    # n_shared segments
+    shared = [n for n in prof if n.startswith("gemm_lds_swiglu{")]
+    if n_shared == 2:
+        assert shared == [f"gemm_lds_swiglu{{{I},{I}}}[1,{T},{2 * I},{H}]"], prof
+    else:
+        assert shared == [], prof
     want, ti, tw = oracle.deepseek_moe(host["x"], host["shared"], host["routed"], host["wr"],
                                        host["br"], k)
     err = np.linalg.norm(out - want) / np.linalg.norm(want)
@@ -124,6 +134,54 @@ def test_moe_sparse_equals_dense_op_by_op(gpu, oracle):
         E.setMode(0)
     # equal values (an exact zero's sign may differ: dense adds +-0 terms)
     np.testing.assert_array_equal(sparse, dense)
+
+
+def test_moe_expert_matrices_far_apart(gpu, oracle):
+    """Expert gate and up weights more than 2 GiB apart (allocations need
+    not be near each other).  Shared expert 1's: the two shared SwiGLU GEMMs
+    still run as one launch, with a descriptor per matrix; routed expert 5's
+    through the C-ABI entry point: the grouped GEMM does the same for every
+    expert.  Same bits as with the weights near each other."""
+    from test_gpu_fusion import far_apart
+    moe, host = build_moe(oracle, 512, 256, 128, 16, 4, 2, 0x5EED0905)
+    xt = E.fromHost(host["x"], DType.BFLOAT16)
+    near = E.toHost(moe.forward(xt))
+    sh = host["shared"][1]
+    _, _, view = far_apart([sh[0], sh[2]])
+    ex1 = moe.sharedExperts[1]
+    saved = (ex1.gateProj, ex1.upProj)
+
+    def forward_far():
+        # the views are dropped again before the flush, so they stay views
+        ex1.gateProj = nn.Linear(view(0), saved[0].bias)
+        ex1.upProj = nn.Linear(view(1), saved[1].bias)
+        y = moe.forward(xt)
+        ex1.gateProj, ex1.upProj = saved
+        return y
+
+    E.profileBegin()
+    far = E.toHost(forward_far())
+    prof = [n for n, _, _ in E.profileEnd()]
+    assert any(n.startswith("gemm_lds_swiglu{128,128}") for n in prof), prof
+    np.testing.assert_array_equal(far, near)
+
+    # the routed grouped GEMM: expert 5's up weight read 2 GiB past a copy
+    # of its gate weight
+    rt = host["routed"][5]
+    big, R, _ = far_apart([rt[0], rt[2]])
+    start = moe.sharedExperts[0].forward(xt)
+    topW, topI = moe.route(xt)
+    ref = E.toHost(E.moeRoutedFfn(xt, start, topW, topI, moe.routedExperts,
+                                  list(range(16)), 16))
+    lib = _lib.load()
+    out = E.empty(DType.BFLOAT16, xt.shape)
+    a, keep = E._moe_args(xt, start, topW, topI, moe.routedExperts, list(range(16)), 16, out)
+    gp = E.devicePtr(big)
+    up = gp + R * rt[0].shape[1] * 2
+    C.cast(a.gate_w, C.POINTER(C.c_void_p))[5] = gp
+    C.cast(a.up_w, C.POINTER(C.c_void_p))[5] = up
+    assert lib.rew_mi355x_moe_routed_ffn(E.context(), C.byref(a)) == 0, lib.rew_mi355x_last_error()
+    np.testing.assert_array_equal(E.toHost(out), ref)
 
 
 def test_moe_routing_weights(gpu, oracle):
@@ -337,7 +395,9 @@ def test_dense_moe_switch_keeps_rews_nonfinite_semantics(gpu, oracle):
 
 
 @pytest.mark.parametrize("T,H,E_,k,bf16", [(8192, 2048, 64, 6, True), (200, 128, 16, 4, True),
-                                           (77, 256, 60, 3, False)])
+                                           (77, 256, 60, 3, False), (300, 1024, 64, 8, False),
+                                           # H % 128 != 0: the 16-row narrow form
+                                           (50, 192, 32, 2, True)])
 def test_router_one_launch(gpu, T, H, E_, k, bf16):
     """DeepSeekMoE.route (deepseek.nim:132-137): the router Linear on
     astype(x, f32), softmax, topK and the renormalisation run as one launch
