@@ -102,6 +102,10 @@ __global__ void __launch_bounds__(1024) moe_scan_kernel(MoeRouteArgs a, int nblk
     }
     a.off[a.n_members] = off;
     a.mt_start[a.n_members] = mt;
+    for (int sh = 1; sh <= a.n_shared; ++sh) {
+      a.off[a.n_members + sh] = off + sh * (int)a.T;
+      a.mt_start[a.n_members + sh] = mt + sh * (int)((a.T + a.tile_m - 1) / a.tile_m);
+    }
   }
 }
 
@@ -181,6 +185,10 @@ __global__ void __launch_bounds__(256) moe_place_kernel(MoeRouteArgs a, int nblk
       if (blk == 0 && lane == 63) {
         a.off[n] = i1;
         a.mt_start[n] = i2;
+        for (int sh = 1; sh <= a.n_shared; ++sh) {  // groups of all T tokens
+          a.off[n + sh] = i1 + sh * (int)a.T;
+          a.mt_start[n + sh] = i2 + sh * (int)((a.T + a.tile_m - 1) / a.tile_m);
+        }
       }
     }
     __syncthreads();
@@ -260,11 +268,13 @@ __global__ void __launch_bounds__(256) moe_place_kernel(MoeRouteArgs a, int nblk
     a.ord_slot[row + p] = slot;
     a.ord_w[row + p] = w;
   }
-  if (live)
+  if (live) {
     for (int i = nmem; i < a.k; ++i) {
       a.ord_slot[row + i] = -1;
       a.ord_w[row + i] = 0.0f;
     }
+    for (int sh = 0; sh < a.n_shared; ++sh) a.perm[a.T * a.k + sh * a.T + t] = (int32_t)t;
+  }
 }
 
 // One wave per token (four per workgroup).  Lanes q < k read the token's

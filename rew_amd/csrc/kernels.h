@@ -376,6 +376,9 @@ struct MoeRouteArgs {
   int32_t* ord_slot;         // [T, k] the token's packed rows in chain order, then -1 (out)
   float* ord_w;              // [T, k] their gate weights (out)
   int32_t* blk_cnt;          // [ceil(T / kMoeRouteBlock) * n_members] working counts
+  // groups of all T tokens after the members (shared experts): off and
+  // mt_start gain n_shared entries, perm rows T k + s T + t = t
+  int n_shared;
 };
 constexpr int kMoeRouteBlock = 256;  // tokens per routing workgroup
 int launch_moe_route(const MoeRouteArgs& a, hipStream_t stream);  // returns the launches
@@ -405,6 +408,13 @@ void launch_moe_combine(const MoeCombineArgs& a, hipStream_t stream);
 // down bias [H]; W dense row-major).  `expert` and the six tables are host
 // arrays of n entries.  Scratch: routed_ffn_scratch_bytes() of device
 // memory, 256-byte aligned, that no other work uses meanwhile.
+// With n_shared > 0 the shared experts come first and `start` is theirs:
+//   start = bf16(... bf16(S_0(x) + S_1(x)) ... + S_{n_shared-1}(x)),
+// S_s(x) = down_s(SwiGLU_s(x)) with the weights sptr[j][s] (same order as
+// ptr); their SwiGLU GEMMs run in the routed experts' grouped launch as
+// groups of all T rows, their down GEMMs as ordinary GEMMs with the bias
+// and (after the first) residual epilogues, exactly the separate launches'
+// arithmetic; `start` is then not read.
 struct RoutedFfn {
   const void* x = nullptr;       // [T, H] bf16, rows x_rs apart
   int64_t x_rs = 0;
@@ -416,6 +426,8 @@ struct RoutedFfn {
   int k = 0, E = 0, n = 0;
   const int32_t* expert = nullptr;
   const void* const* ptr[6] = {};
+  int n_shared = 0;
+  const void* const* sptr[6] = {};
   void* out = nullptr;           // [T, H] bf16, dense
 };
 // Throws Error(REW_MI355X_ERR_INVALID) naming the first argument the

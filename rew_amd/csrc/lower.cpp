@@ -284,6 +284,11 @@ struct MoePlan {
   // the members' intermediates (never materialized) and the running sums
   // between members
   std::vector<Tensor*> inner, mids;
+  // the shared experts whose sum is `start` (e = -1), when the group also
+  // owns them: their SwiGLU GEMMs join the members' grouped launch and
+  // `start` with their intermediates is never materialized
+  std::vector<MoeMember> shared;
+  std::vector<Tensor*> shared_inner;
 };
 
 // A classifier head, argmax(softmax(Linear(x))) over f32 rows (the end of
@@ -337,6 +342,7 @@ struct Lower {
 
   void match_moe();
   bool moe_lowerable(const MoePlan& p);
+  bool match_shared(MoePlan& g, Tensor* first_sum);
   bool emit_moe(Tensor* t, const MoePlan& p);
   void dense_rows(Tensor* x, int64_t n, const void** ptr, int64_t* rs);
 
@@ -2238,9 +2244,109 @@ void Lower::match_moe() {
       gemm_out.erase(t);
     }
     for (Tensor* t : g.mids) t->plan_mat = false;
+    if (match_shared(g, g.mids.empty() ? kv.first : g.mids.front())) {
+      for (Tensor* t : g.shared_inner) {
+        t->plan_mat = false;
+        gemm_out.erase(t);
+      }
+    }
     kv.first->plan_mat = true;
     moe_out[kv.first] = std::move(g);
   }
+}
+
+static bool reads_dense(Tensor* w);
+
+// DeepSeekMoE.forward's shared experts (deepseek.nim:123-126): out =
+// S_0(x), then out = out + S_i(x), which the GEMM epilogues planned as
+// start = down_{n-1}(SwiGLU_{n-1}(x)) + bias with the earlier sum as its
+// residual, ..., down_0 with the bias alone.  Every SwiGLU reads the
+// group's own x, and every link of the chain (start included) is read by
+// the next one only, so the group can compute them itself.  With one
+// shared expert the epilogue planning has already taken the first routed
+// add (first_sum = start + the first member's contribution) into that
+// expert's down GEMM as its residual; the group then takes that plan back
+// with the bias epilogue alone.
+bool Lower::match_shared(MoePlan& g, Tensor* first_sum) {
+  std::vector<MoeMember> sh;
+  std::vector<Tensor*> inner;
+  const int64_t T = g.x->shape.d[0], H = g.x->shape.d[1];
+  const int64_t I = g.mem[0].sw.dot->in[1]->shape.d[1];
+  auto weight = [&](Tensor* w, int64_t rows, int64_t cols) {
+    return w->dt == kBF16 && w->shape.rank == 2 && w->shape.d[0] == rows &&
+           w->shape.d[1] == cols && reads_dense(w);
+  };
+  auto vec = [&](Tensor* v, int64_t len) { return v && v->dt == kBF16 && v->numel() == len; };
+  Tensor* s = g.start;
+  Tensor* taken = nullptr;  // the first routed add's plan, taken back
+  for (;;) {
+    if (s->ext != 0 || s->uses != 1 || s->dt != kBF16 || s->shape != g.x->shape) return false;
+    GemmPlan dn;
+    auto dit = gemm_out.find(s);
+    if (dit != gemm_out.end()) {
+      dn = dit->second;
+    } else {
+      auto fit = sh.empty() ? gemm_out.find(first_sum) : gemm_out.end();
+      if (fit == gemm_out.end() || fit->second.epi != EPI_BIAS_RES || !fit->second.dot ||
+          !s->prod || s->prod->kind != K_BINARY ||
+          (s->prod->in[0] != fit->second.dot->out[0] && s->prod->in[1] != fit->second.dot->out[0]))
+        return false;
+      dn = fit->second;
+      dn.epi = EPI_BIAS;
+      dn.res = nullptr;
+      taken = first_sum;
+    }
+    if ((dn.epi != EPI_BIAS && dn.epi != EPI_BIAS_RES) || !dn.dot) return false;
+    Tensor* hb = dn.dot->in[0];
+    auto sit = gemm_out.find(hb);
+    if (sit == gemm_out.end() || sit->second.epi != EPI_SWIGLU || hb->ext != 0 || hb->uses != 1)
+      return false;
+    const GemmPlan& sw = sit->second;
+    if (!sw.dot || !sw.dot2 || sw.dot->in[0] != g.x || sw.dot2->in[0] != g.x) return false;
+    if (!weight(sw.dot->in[1], H, I) || !weight(sw.dot2->in[1], H, I) ||
+        !weight(dn.dot->in[1], I, H) || !vec(sw.bias, I) || !vec(sw.bias2, I) ||
+        !vec(dn.bias, H))
+      return false;
+    MoeMember m;
+    m.e = -1;
+    m.sw = sw;
+    m.dn = dn;
+    sh.insert(sh.begin(), m);
+    inner.push_back(s);
+    inner.push_back(hb);
+    if (dn.epi == EPI_BIAS) break;
+    s = dn.res;
+    if (!s || (int64_t)sh.size() >= kMoeMaxMembers - (int64_t)g.mem.size()) return false;
+  }
+  // the down GEMMs run with their epilogues on dense rows (stand-in
+  // addresses: the real ones are aligned allocator blocks)
+  for (size_t i = 0; i < sh.size(); ++i) {
+    GemmArgs d{};
+    void* const al = reinterpret_cast<void*>(uintptr_t(4096));
+    d.dtype = d.c_dtype = kBF16;
+    d.batch = 1;
+    d.a = d.b = d.bias = al;
+    d.c = al;
+    d.M = T;
+    d.K = I;
+    d.N = H;
+    d.a_sm = I;
+    d.a_sk = 1;
+    d.b_sk = H;
+    d.b_sn = 1;
+    d.c_sm = H;
+    d.c_sb = T * H;
+    d.epi = i ? EPI_BIAS_RES : EPI_BIAS;
+    if (i) {
+      d.res = al;
+      d.res_sm = H;
+    }
+    if (!gemm_epilogue_ok(d)) return false;
+  }
+  if (taken) gemm_out.erase(taken);  // the group's combine makes that sum
+  g.shared = std::move(sh);
+  g.shared_inner = std::move(inner);
+  return true;
 }
 
 // Arguments of the two grouped expert GEMMs over dense [*, H] token rows
@@ -2332,8 +2438,8 @@ void Lower::dense_rows(Tensor* x, int64_t n, const void** ptr, int64_t* rs) {
 }
 
 bool Lower::emit_moe(Tensor* t, const MoePlan& p) {
-  const int n = (int)p.mem.size();
-  ensure_mat(p.start);
+  const int n = (int)p.mem.size(), ns = (int)p.shared.size();
+  if (!ns) ensure_mat(p.start);  // (else the group computes it)
   ensure_mat(p.x);
   ensure_mat(p.topi);
   ensure_mat(p.topw);
@@ -2342,9 +2448,9 @@ bool Lower::emit_moe(Tensor* t, const MoePlan& p) {
   const void* xp;
   int64_t x_rs;
   dense_rows(p.x, H, &xp, &x_rs);
-  const void* sp;
-  int64_t s_rs;
-  dense_rows(p.start, H, &sp, &s_rs);
+  const void* sp = nullptr;
+  int64_t s_rs = 0;
+  if (!ns) dense_rows(p.start, H, &sp, &s_rs);
   if (p.topi->st == nullptr || p.topw->st == nullptr) return false;
 
   // member weights: gate/up [H, I], down [I, H], dense row-major.  Only the
@@ -2365,17 +2471,20 @@ bool Lower::emit_moe(Tensor* t, const MoePlan& p) {
     return v->data();
   };
   const int64_t I = p.mem[0].sw.dot->in[1]->shape.d[1];
-  std::vector<const void*> ptrs(6 * (size_t)n);
+  // the members' six tables, then the shared experts' (table j of the
+  // shared experts at 6 n + j ns)
+  std::vector<const void*> ptrs(6 * (size_t)(n + ns));
   std::vector<int32_t> ids(n);
-  for (int i = 0; i < n; ++i) {
-    const MoeMember& m = p.mem[i];
-    ids[i] = m.e;
+  for (int i = 0; i < n + ns; ++i) {
+    const MoeMember& m = i < n ? p.mem[i] : p.shared[i - n];
+    if (i < n) ids[i] = m.e;
     const void* q[6] = {weight(m.sw.dot->in[1], H, I), weight(m.sw.dot2->in[1], H, I),
                         vec(m.sw.bias, I), vec(m.sw.bias2, I),
                         weight(m.dn.dot->in[1], I, H), vec(m.dn.bias, H)};
     for (int j = 0; j < 6; ++j) {
       if (!q[j] || ((uintptr_t)q[j] & 15)) return false;
-      ptrs[(size_t)j * n + i] = q[j];
+      if (i < n) ptrs[(size_t)j * n + i] = q[j];
+      else ptrs[6 * (size_t)n + (size_t)j * ns + (i - n)] = q[j];
     }
   }
   RoutedFfn a;
@@ -2393,6 +2502,8 @@ bool Lower::emit_moe(Tensor* t, const MoePlan& p) {
   a.n = n;
   a.expert = ids.data();
   for (int j = 0; j < 6; ++j) a.ptr[j] = ptrs.data() + (size_t)j * n;
+  a.n_shared = ns;
+  for (int j = 0; j < 6 && ns; ++j) a.sptr[j] = ptrs.data() + 6 * (size_t)n + (size_t)j * ns;
   tensor_alloc(t);
   a.out = t->data();
   try {

@@ -29,8 +29,9 @@ namespace rew {
 
 // Experts whose table entries one metadata launch writes (from its
 // kernel arguments, so no host staging buffer is involved).  The first
-// launch also sets member_of to -1 before the chunks enter their members.
-constexpr int kMetaChunk = 64;
+// launch also sets member_of to -1 before the chunks enter their members;
+// an entry with id -1 (a shared expert) only fills its table slots.
+constexpr int kMetaChunk = 72;
 
 struct MoeMetaChunk {
   int first, count, n;
@@ -46,8 +47,10 @@ __global__ void __launch_bounds__(256) moe_meta_kernel(MoeMetaChunk ch, int E, i
     __syncthreads();
   }
   if (i >= ch.count) return;
-  members[ch.first + i] = ch.ids[i];
-  member_of[ch.ids[i]] = ch.first + i;  // the ids are distinct
+  if (ch.ids[i] >= 0) {
+    members[ch.first + i] = ch.ids[i];
+    member_of[ch.ids[i]] = ch.first + i;  // the ids are distinct
+  }
 #pragma unroll
   for (int j = 0; j < 6; ++j) tables[(size_t)j * ch.n + ch.first + i] = ch.p[j][i];
 }
@@ -55,12 +58,16 @@ __global__ void __launch_bounds__(256) moe_meta_kernel(MoeMetaChunk ch, int E, i
 namespace {
 
 struct Layout {
-  size_t member_of, members, tables, route, hbuf, ybuf, total;
+  size_t member_of, members, tables, route, hbuf, ybuf, sbuf, total;
 };
 
+// (with shared experts: their table entries follow the members', their
+// hidden rows the routed rows in hbuf, and sbuf holds two [T, H] running
+// sums of their outputs)
 Layout layout_of(const RoutedFfn& a) {
   auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
-  const size_t R = (size_t)a.T * (size_t)a.k;
+  const size_t R = (size_t)a.T * (size_t)a.k, ns = (size_t)a.n_shared;
+  const size_t groups = (size_t)a.n + ns;
   Layout L;
   size_t o = 0;
   L.member_of = o;
@@ -68,14 +75,16 @@ Layout layout_of(const RoutedFfn& a) {
   L.members = o;
   o += up((size_t)a.n * 4);
   L.tables = o;
-  o += up((size_t)a.n * 6 * sizeof(void*));
+  o += up(groups * 6 * sizeof(void*));
   L.route = o;
   const size_t nb = ((size_t)a.T + kMoeRouteBlock - 1) / kMoeRouteBlock;
-  o += up((2 * ((size_t)a.n + 1) + 3 * R + nb * (size_t)a.n) * 4);
+  o += up((2 * (groups + 1) + 3 * R + ns * (size_t)a.T + nb * (size_t)a.n) * 4);
   L.hbuf = o;
-  o += up(R * (size_t)a.I * 2);
+  o += up((R + ns * (size_t)a.T) * (size_t)a.I * 2);
   L.ybuf = o;
   o += up(R * (size_t)a.H * 2);
+  L.sbuf = o;
+  if (ns) o += 2 * up((size_t)a.T * (size_t)a.H * 2);
   L.total = o;
   return L;
 }
@@ -111,6 +120,37 @@ void gemm_args(const RoutedFfn& a, GemmArgs* gs, GemmArgs* gd) {
 
 bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// Shared expert i's down projection: its SwiGLU rows (dense [T, I]) times
+// its down weight plus bias, plus the running sum of the earlier shared
+// experts (res) after the first -- the fused GEMM epilogues of the
+// separate launches.
+GemmArgs shared_down_args(const RoutedFfn& a, int i, const void* hrows, const void* res,
+                          void* out) {
+  GemmArgs g{};
+  g.dtype = REW_DT_BFLOAT16;
+  g.c_dtype = REW_DT_BFLOAT16;
+  g.batch = 1;
+  g.a = hrows;
+  g.a_sm = a.I;
+  g.a_sk = 1;
+  g.b = a.sptr[4][i];
+  g.b_sk = a.H;
+  g.b_sn = 1;
+  g.M = a.T;
+  g.K = a.I;
+  g.N = a.H;
+  g.c = out;
+  g.c_sm = a.H;
+  g.c_sb = a.T * a.H;
+  g.bias = a.sptr[5][i];
+  g.epi = i == 0 ? EPI_BIAS : EPI_BIAS_RES;
+  if (i > 0) {
+    g.res = res;
+    g.res_sm = a.H;
+  }
+  return g;
+}
+
 }  // namespace
 
 size_t routed_ffn_scratch_bytes(const RoutedFfn& a) { return layout_of(a).total; }
@@ -140,10 +180,24 @@ void routed_ffn_check(const RoutedFfn& a) {
         bad(std::string(kTable[j]) + "[" + std::to_string(i) +
             "] is null or not 16-byte aligned");
   }
+  if (a.n_shared < 0 || a.n + a.n_shared > kMoeMaxMembers)
+    bad("at most " + std::to_string(kMoeMaxMembers) + " experts per call");
+  for (int j = 0; j < 6 && a.n_shared > 0; ++j) {
+    if (!a.sptr[j]) bad(std::string("null shared ") + kTable[j] + " table");
+    for (int i = 0; i < a.n_shared; ++i)
+      if (!a.sptr[j][i] || !al16(a.sptr[j][i]))
+        bad(std::string("shared ") + kTable[j] + "[" + std::to_string(i) +
+            "] is null or not 16-byte aligned");
+  }
+  if (a.T * ((int64_t)a.k + a.n_shared) >= ((int64_t)1 << 31))
+    bad("tokens * (k + shared experts) must be below 2^31");
   if (a.T == 0) return;
-  if (!a.x || !a.start || !a.topi || !a.topw || !a.out) bad("null device pointer");
-  if (!al16(a.x) || !al16(a.start) || !al16(a.out)) bad("rows must be 16-byte aligned");
-  if (a.x_rs < a.H || a.x_rs % 8 || a.start_rs < a.H || a.start_rs % 8)
+  const bool own_start = a.n_shared > 0;
+  if (!a.x || (!own_start && !a.start) || !a.topi || !a.topw || !a.out)
+    bad("null device pointer");
+  if (!al16(a.x) || (!own_start && !al16(a.start)) || !al16(a.out))
+    bad("rows must be 16-byte aligned");
+  if (a.x_rs < a.H || a.x_rs % 8 || (!own_start && (a.start_rs < a.H || a.start_rs % 8)))
     bad("row strides must be >= hidden and multiples of 8 elements");
   GemmArgs gs, gd;
   gemm_args(a, &gs, &gd);
@@ -153,6 +207,10 @@ void routed_ffn_check(const RoutedFfn& a) {
   gd.c = rows;
   if (!gemm_grouped_ok(gs) || !gemm_grouped_ok(gd))
     bad("the expert GEMMs exceed the grouped kernel's 32-bit operand extents");
+  for (int i = 0; i < a.n_shared; ++i) {
+    GemmArgs g = shared_down_args(a, i, rows, rows, rows);
+    if (!gemm_epilogue_ok(g)) bad("the shared experts' down GEMMs cannot run with their epilogues");
+  }
 }
 
 void run_routed_ffn(Ctx* c, const RoutedFfn& a, void* scratch) {
@@ -162,21 +220,22 @@ void run_routed_ffn(Ctx* c, const RoutedFfn& a, void* scratch) {
   int32_t* members = reinterpret_cast<int32_t*>(s + L.members);
   const void** tables = reinterpret_cast<const void**>(s + L.tables);
   int32_t* route = reinterpret_cast<int32_t*>(s + L.route);
-  const int n = a.n;
+  const int n = a.n, ns = a.n_shared, groups = n + ns;
   const int64_t R = a.T * a.k;
 
   // (profile names are built only while profiling: the allocation-free
   // entry point runs this sequence without touching the host heap)
   if (c->profiling) prof_begin(c, "moe_tables{E" + std::to_string(n) + "}");
-  for (int first = 0; first < n; first += kMetaChunk) {
+  for (int first = 0; first < groups; first += kMetaChunk) {
     MoeMetaChunk ch;
     std::memset(&ch, 0, sizeof ch);
     ch.first = first;
-    ch.count = std::min(kMetaChunk, n - first);
-    ch.n = n;
+    ch.count = std::min(kMetaChunk, groups - first);
+    ch.n = groups;
     for (int i = 0; i < ch.count; ++i) {
-      ch.ids[i] = a.expert[first + i];
-      for (int j = 0; j < 6; ++j) ch.p[j][i] = a.ptr[j][first + i];
+      const int e = first + i;  // members, then the shared experts (id -1)
+      ch.ids[i] = e < n ? a.expert[e] : -1;
+      for (int j = 0; j < 6; ++j) ch.p[j][i] = e < n ? a.ptr[j][e] : a.sptr[j][e - n];
     }
     hipLaunchKernelGGL(moe_meta_kernel, dim3(1), dim3(256), 0, c->stream, ch, (int)a.E, members,
                        member_of, tables);
@@ -194,12 +253,14 @@ void run_routed_ffn(Ctx* c, const RoutedFfn& a, void* scratch) {
   ra.members = members;
   ra.n_members = n;
   ra.tile_m = 256;
+  ra.n_shared = ns;
+  const int64_t RS = R + (int64_t)ns * a.T;  // hidden rows: routed, then shared
   ra.off = route;
-  ra.mt_start = route + (n + 1);
-  ra.perm = route + 2 * (n + 1);
-  ra.ord_slot = route + 2 * (n + 1) + R;
-  ra.ord_w = reinterpret_cast<float*>(route + 2 * (n + 1) + 2 * R);
-  ra.blk_cnt = route + 2 * (n + 1) + 3 * R;
+  ra.mt_start = route + (groups + 1);
+  ra.perm = route + 2 * (groups + 1);
+  ra.ord_slot = route + 2 * (groups + 1) + RS;
+  ra.ord_w = reinterpret_cast<float*>(route + 2 * (groups + 1) + RS + R);
+  ra.blk_cnt = route + 2 * (groups + 1) + RS + 2 * R;
   if (c->profiling)
     prof_begin(c, "moe_route{" + std::to_string(a.T) + "x" + std::to_string(a.k) + ",E" +
                       std::to_string(n) + "}");
@@ -211,33 +272,57 @@ void run_routed_ffn(Ctx* c, const RoutedFfn& a, void* scratch) {
   gs.c = s + L.hbuf;
   gd.a = s + L.hbuf;
   gd.c = s + L.ybuf;
+  // the SwiGLU launch covers the members and the shared experts (groups of
+  // all T tokens); the down launch the members only
   GroupArgs ga;
   ga.off = ra.off;
   ga.mt_start = ra.mt_start;
-  ga.n_groups = n;
-  ga.max_mtiles = (R + 255) / 256 + n;
+  ga.n_groups = groups;
+  ga.max_mtiles = (R + 255) / 256 + n + (int64_t)ns * ((a.T + 255) / 256);
   ga.rows = ra.perm;
   ga.b = tables;
-  ga.b2 = tables + n;
-  ga.bias = tables + 2 * n;
-  ga.bias2 = tables + 3 * n;
+  ga.b2 = tables + groups;
+  ga.bias = tables + 2 * groups;
+  ga.bias2 = tables + 3 * groups;
   ga.dual_span = 0;
-  for (int i = 0; i < n; ++i) {
-    const int64_t d = (int64_t)((uintptr_t)a.ptr[1][i] - (uintptr_t)a.ptr[0][i]);
+  for (int i = 0; i < groups; ++i) {
+    const void* g0 = i < n ? a.ptr[0][i] : a.sptr[0][i - n];
+    const void* g1 = i < n ? a.ptr[1][i] : a.sptr[1][i - n];
+    const int64_t d = (int64_t)((uintptr_t)g1 - (uintptr_t)g0);
     ga.dual_span = std::max(ga.dual_span, d < 0 ? -d : d);
   }
   if (c->profiling) {
     char nm[160];
-    std::snprintf(nm, sizeof nm, "moe_gemm_swiglu[%d,%lld,%lld,%lld]", n, (long long)R,
+    std::snprintf(nm, sizeof nm, "moe_gemm_swiglu[%d,%lld,%lld,%lld]", groups, (long long)RS,
                   (long long)a.I, (long long)a.H);
     prof_begin(c, nm);
   }
   launch_gemm_grouped(gs, ga, c->stream);
   prof_end(c);
+  // the shared experts' running sum, [T, H] in sbuf (two buffers in turn)
+  const void* prev = a.start;
+  int64_t prev_rs = a.start_rs;
+  for (int i = 0; i < ns; ++i) {
+    void* dst = s + L.sbuf + (size_t)(i & 1) * ((((size_t)a.T * a.H * 2) + 255) & ~(size_t)255);
+    const GemmArgs g = shared_down_args(
+        a, i, s + L.hbuf + (size_t)(R + (int64_t)i * a.T) * a.I * 2, prev, dst);
+    if (c->profiling) {
+      char nm[160];
+      std::snprintf(nm, sizeof nm, "moe_shared_down%s[1,%lld,%lld,%lld]",
+                    i ? "+bias+res" : "+bias", (long long)a.T, (long long)a.H, (long long)a.I);
+      prof_begin(c, nm);
+    }
+    launch_gemm(g, c->stream);
+    prof_end(c);
+    prev = dst;
+    prev_rs = a.H;
+  }
+  ga.n_groups = n;
+  ga.max_mtiles = (R + 255) / 256 + n;
   ga.rows = nullptr;
-  ga.b = tables + 4 * n;
+  ga.b = tables + 4 * groups;
   ga.b2 = nullptr;
-  ga.bias = tables + 5 * n;
+  ga.bias = tables + 5 * groups;
   ga.bias2 = nullptr;
   if (c->profiling) {
     char nm[160];
@@ -249,8 +334,8 @@ void run_routed_ffn(Ctx* c, const RoutedFfn& a, void* scratch) {
   prof_end(c);
 
   MoeCombineArgs ca;
-  ca.prev = (const uint16_t*)a.start;
-  ca.prev_rs = a.start_rs;
+  ca.prev = (const uint16_t*)prev;
+  ca.prev_rs = prev_rs;
   ca.y = (const uint16_t*)gd.c;
   ca.ord_slot = ra.ord_slot;
   ca.ord_w = ra.ord_w;
@@ -262,7 +347,7 @@ void run_routed_ffn(Ctx* c, const RoutedFfn& a, void* scratch) {
     prof_begin(c, "moe_combine{" + std::to_string(a.T) + "x" + std::to_string(a.H) + "}");
   launch_moe_combine(ca, c->stream);
   prof_end(c);
-  c->stats.kernels_launched += route_launches + 3 + (n + kMetaChunk - 1) / kMetaChunk;
+  c->stats.kernels_launched += route_launches + 3 + ns + (groups + kMetaChunk - 1) / kMetaChunk;
   c->stats.fused_groups += 4;
 }
 

@@ -182,6 +182,8 @@ struct Exec {
   void operator()(MoeL& l) {
     l.a.expert = l.expert.data();
     for (int j = 0; j < 6; ++j) l.a.ptr[j] = l.tab.data() + (size_t)j * l.a.n;
+    for (int j = 0; j < 6 && l.a.n_shared; ++j)
+      l.a.sptr[j] = l.tab.data() + 6 * (size_t)l.a.n + (size_t)j * l.a.n_shared;
     run_routed_ffn(c, l.a, l.scratch);
   }
   void operator()(WindowArgs& a) { launch_window(a, c->stream); }

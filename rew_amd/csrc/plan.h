@@ -38,7 +38,8 @@ struct IndexMapL {
   bool scatter;
 };
 // The routed experts: RoutedFfn's host tables live here (expert ids, then
-// the six per-expert device pointer tables, table j at tab[j * n]).
+// the six per-expert device pointer tables, table j at tab[j * n], and the
+// shared experts' after them, table j at tab[6 n + j n_shared]).
 struct MoeL {
   RoutedFfn a;
   std::vector<int32_t> expert;

@@ -109,13 +109,11 @@ def test_moe_matches_oracle(gpu, oracle, T, H, I, E_, k, n_shared):
     prof = [name for name, _, _ in E.profileEnd()]
     assert any(n.startswith("moe_gemm_swiglu") for n in prof), prof
     assert any(n.startswith("moe_combine") for n in prof), prof
-    # the shared experts' SwiGLU GEMMs read the same x: one launch of
-    # n_shared segments
-    shared = [n for n in prof if n.startswith("gemm_lds_swiglu{")]
-    if n_shared == 2:
-        assert shared == [f"gemm_lds_swiglu{{{I},{I}}}[1,{T},{2 * I},{H}]"], prof
-    else:
-        assert shared == [], prof
+    # the shared experts belong to the group: their SwiGLU GEMMs are groups
+    # of all T rows in the members' grouped launch, their down GEMMs follow
+    sw = [n for n in prof if "swiglu" in n]
+    assert sw == [f"moe_gemm_swiglu[{E_ + n_shared},{T * k + n_shared * T},{I},{H}]"], prof
+    assert sum(n.startswith("moe_shared_down") for n in prof) == n_shared, prof
     want, ti, tw = oracle.deepseek_moe(host["x"], host["shared"], host["routed"], host["wr"],
                                        host["br"], k)
     err = np.linalg.norm(out - want) / np.linalg.norm(want)
@@ -139,9 +137,9 @@ def test_moe_sparse_equals_dense_op_by_op(gpu, oracle):
 def test_moe_expert_matrices_far_apart(gpu, oracle):
     """Expert gate and up weights more than 2 GiB apart (allocations need
     not be near each other).  Shared expert 1's: the two shared SwiGLU GEMMs
-    still run as one launch, with a descriptor per matrix; routed expert 5's
-    through the C-ABI entry point: the grouped GEMM does the same for every
-    expert.  Same bits as with the weights near each other."""
+    still run as one launch, reading B through per-lane addresses; routed
+    expert 5's through the C-ABI entry point: the grouped GEMM does the same
+    for every expert.  Same bits as with the weights near each other."""
     from test_gpu_fusion import far_apart
     moe, host = build_moe(oracle, 512, 256, 128, 16, 4, 2, 0x5EED0905)
     xt = E.fromHost(host["x"], DType.BFLOAT16)
@@ -162,6 +160,8 @@ def test_moe_expert_matrices_far_apart(gpu, oracle):
     E.profileBegin()
     far = E.toHost(forward_far())
     prof = [n for n, _, _ in E.profileEnd()]
+    # (weights seen through pending views stay out of the MoE group: the two
+    # shared SwiGLU GEMMs run as their own two-segment launch)
     assert any(n.startswith("gemm_lds_swiglu{128,128}") for n in prof), prof
     np.testing.assert_array_equal(far, near)
 
