@@ -161,29 +161,39 @@ __global__ void __launch_bounds__(256) gemm_f32_small_kernel(GemmArgs g) {
                        g.a_sb % 4 == 0 && g.b_sb % 4 == 0 && ((uintptr_t)g.a & 15) == 0 &&
                        ((uintptr_t)g.b & 15) == 0;
       if (vec) {
-        // the slabs move in batches of kB 16-byte loads per operand, each
-        // batch's loads issued before its LDS stores (one memory latency per
-        // batch rather than per k-step): unconditional loads from clamped
-        // addresses, out-of-range values replaced by zeros after
-        constexpr int kB = 4;
-        const float* ap = (const float*)g.a + b * g.a_sb + (ma < g.M ? ma : 0) * g.a_sm;
+        // A's slab moves HBM/L2 -> LDS by global_load_lds (16 bytes per lane,
+        // lane-contiguous 1 KiB per instruction over the padded rows, every
+        // instruction of a thread in flight at once and no VGPRs held); B's
+        // goes through registers (it is transposed to k-contiguous) in two
+        // batches of up to kB 16-byte loads per thread, each batch's loads
+        // issued before its LDS stores.  Unconditional loads from clamped
+        // addresses; the A pad [K, K16) and B's out-of-range values are
+        // zeroed after.
+        const int abytes = 16 * KP * 4;
+        const float* a0 = (const float*)g.a + b * g.a_sb;
+        for (int o = (tid >> 6) * 1024; o < abytes; o += 4096) {
+          const int lo = o + (tid & 63) * 16;  // this lane's LDS byte
+          const int r = lo / (KP * 4), k = (lo - r * KP * 4) >> 2;
+          const int64_t m = m0 + (r < 16 ? r : 15);
+          const float* src = a0 + (m < g.M ? m : g.M - 1) * g.a_sm + (k < g.K ? k : 0);
+          if (lo < abytes)
+            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)((char*)As + o), 16, 0, 0);
+        }
+        constexpr int kB = 7;
         const int64_t nb = n0 + nq;
         const float* bp = (const float*)g.b + b * g.b_sb + (nb < g.N ? nb : 0);
         const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll 1
         for (int i0 = 0; 64 * i0 < K16; i0 += kB) {
-          float4 va[kB], vb[kB];
+          float4 vb[kB];
 #pragma unroll
           for (int i = 0; i < kB; ++i) {
-            const int ka = la * 4 + 64 * (i0 + i), kb = kq + 64 * (i0 + i);
-            va[i] = *(const float4*)(ap + (ka < g.K ? ka : 0));
+            const int kb = kq + 64 * (i0 + i);
             vb[i] = *(const float4*)(bp + (int64_t)(kb < g.K ? kb : 0) * g.b_sk);
           }
 #pragma unroll
           for (int i = 0; i < kB; ++i) {
-            const int ka = la * 4 + 64 * (i0 + i), kb = kq + 64 * (i0 + i);
-            if (ka < K16)
-              *(float4*)&As[ra * KP + ka] = (ma < g.M && ka < g.K) ? va[i] : z;
+            const int kb = kq + 64 * (i0 + i);
             if (kb < K16) {
               const float4 v = (kb < g.K && nb < g.N) ? vb[i] : z;
               Bs[nq * KP + kb] = v.x;
@@ -193,6 +203,18 @@ __global__ void __launch_bounds__(256) gemm_f32_small_kernel(GemmArgs g) {
             }
           }
         }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        // zeros where the chain runs past K (K16 > K) and in the rows past M
+        for (int e = tid; e < 16 * (K16 - (int)g.K); e += 256) {
+          const int r = e / (K16 - (int)g.K);
+          As[r * KP + g.K + (e - r * (K16 - (int)g.K))] = 0.0f;
+        }
+        if (m0 + 16 > g.M)
+          for (int e = tid; e < 16 * K16; e += 256) {
+            const int r = e / K16;
+            if (m0 + r >= g.M) As[r * KP + (e - r * K16)] = 0.0f;
+          }
       } else {
         for (int k = la; k < K16; k += 16)
           As[ra * KP + k] = (ma < g.M && k < g.K)
