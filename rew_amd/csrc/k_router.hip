@@ -9,8 +9,10 @@
 // The product is gemm_f32_narrow_kernel's (16 rows per workgroup, thread t
 // owns row t / 16 and columns 4 (t % 16) .. + 3, 32-deep k-steps in two
 // register sets): every logit is the same sequential fmaf chain over k from
-// 0, then the bias add.  x may be bf16: its conversion to f32 is exact and
-// happens on the load.  Then the 16 lanes of each row take
+// 0, then the bias add.  For H % 128 == 0 the matrix-core form below runs
+// the same chains on f32 MFMAs, which round each step as fmaf does.  x may
+// be bf16: its conversion to f32 is exact and happens on the load.  Then
+// the 16 lanes of each row take
 // softmax_tile_kernel's steps (the max, expf, the running sum in column
 // order, the quotients), topk_rows_kernel's ranking (larger first, NaN last,
 // the lower column on ties) and the renormalisation in rank order, as the
@@ -39,38 +41,40 @@ __device__ __forceinline__ bool rank_first(float av, int ai, float bv, int bi) {
   return ai < bi;
 }
 
-// The rest of the router for one row whose logits (without the bias) 16
-// lanes hold, four columns each (lanes 16 q .. 16 q + 15 of a wave; lane
-// l16 columns c4 .. c4 + 3): softmax_tile_kernel's steps (the max, expf, the
-// running sum in column order on the row's first lane, the quotients),
+// The rest of the router for one row whose logits (with the bias) LANES
+// lanes of a wave hold, COLS columns each (lanes LANES q .. LANES q +
+// LANES - 1; the lane with l = lane % LANES holds columns c0 = COLS l ..
+// c0 + COLS - 1): softmax_tile_kernel's steps (the max, expf, the running
+// sum in column order on the row's first lane, the quotients),
 // topk_rows_kernel's ranking and the renormalisation in rank order.  Every
 // thread of the workgroup calls it (it holds barriers); row t >= T stores
 // nothing.  lg: the row's LDS scratch of kRouterMaxE + 1 floats.
-__device__ __forceinline__ void router_tail(const RouterArgs& a, float (&y)[4], int c4,
+template <int LANES, int COLS>
+__device__ __forceinline__ void router_tail(const RouterArgs& a, float (&y)[COLS], int c0,
                                             int64_t t, float* lg) {
   const int E = a.E;
-  const int l16 = threadIdx.x & 15;
+  const int l = threadIdx.x & (LANES - 1);
   const bool row_ok = t < a.T;
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    if (c4 + j >= E) y[j] = 0.0f;
-  // softmax: the max (order-free) over the 16 lanes, the exps in place, the
+  for (int j = 0; j < COLS; ++j)
+    if (c0 + j >= E) y[j] = 0.0f;
+  // softmax: the max (order-free) over the lanes, the exps in place, the
   // sum in column order on the row's first lane (the reduction's order),
   // then the quotients
   float m = -INFINITY;
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    if (c4 + j < E) m = vm::fmax_prop(m, y[j]);
+  for (int j = 0; j < COLS; ++j)
+    if (c0 + j < E) m = vm::fmax_prop(m, y[j]);
 #pragma unroll
-  for (int off = 8; off >= 1; off >>= 1) m = vm::fmax_prop(m, __shfl_xor(m, off, 16));
+  for (int off = LANES / 2; off >= 1; off >>= 1) m = vm::fmax_prop(m, __shfl_xor(m, off, LANES));
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    if (c4 + j < E) {
+  for (int j = 0; j < COLS; ++j)
+    if (c0 + j < E) {
       y[j] = expf(y[j] - m);
-      lg[c4 + j] = y[j];
+      lg[c0 + j] = y[j];
     }
   __syncthreads();
-  if (l16 == 0) {
+  if (l == 0) {
     float sum = 0.0f;
     for (int j = 0; j < E; ++j) sum = sum + lg[j];
     lg[kRouterMaxE] = sum;
@@ -78,10 +82,10 @@ __device__ __forceinline__ void router_tail(const RouterArgs& a, float (&y)[4], 
   __syncthreads();
   const float sum = lg[kRouterMaxE];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) y[j] = y[j] / sum;
+  for (int j = 0; j < COLS; ++j) y[j] = y[j] / sum;
   // top-k: each round the best untaken column of each lane, then the best of
-  // the 16 (a total order, so every lane agrees on the winner); the row's
-  // first lane keeps the values for the renormalisation in rank order
+  // the row's lanes (a total order, so every lane agrees on the winner); the
+  // row's first lane keeps the values for the renormalisation in rank order
   // (the values wait in lg[0 .. k), which only the row's first lane touches
   // from here on: the exps there are spent)
   uint32_t taken = 0;
@@ -90,22 +94,22 @@ __device__ __forceinline__ void router_tail(const RouterArgs& a, float (&y)[4], 
     float bv = 0.0f;
     int bi = kNoCol;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (c4 + j < E && !((taken >> j) & 1) && rank_first(y[j], c4 + j, bv, bi)) {
+    for (int j = 0; j < COLS; ++j)
+      if (c0 + j < E && !((taken >> j) & 1) && rank_first(y[j], c0 + j, bv, bi)) {
         bv = y[j];
-        bi = c4 + j;
+        bi = c0 + j;
       }
 #pragma unroll
-    for (int off = 8; off >= 1; off >>= 1) {
-      const float ov = __shfl_xor(bv, off, 16);
-      const int oi = __shfl_xor(bi, off, 16);
+    for (int off = LANES / 2; off >= 1; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, LANES);
+      const int oi = __shfl_xor(bi, off, LANES);
       if (rank_first(ov, oi, bv, bi)) {
         bv = ov;
         bi = oi;
       }
     }
-    if (bi >= c4 && bi < c4 + 4) taken |= 1u << (bi - c4);
-    if (l16 == 0) {
+    if (bi >= c0 && bi < c0 + COLS) taken |= 1u << (bi - c0);
+    if (l == 0) {
       lg[s] = bv;
       denom = denom + bv;
       if (row_ok) {
@@ -114,7 +118,7 @@ __device__ __forceinline__ void router_tail(const RouterArgs& a, float (&y)[4], 
       }
     }
   }
-  if (l16 == 0 && row_ok && a.weights)
+  if (l == 0 && row_ok && a.weights)
     for (int s = 0; s < a.k; ++s) a.weights[t * a.k + s] = lg[s] / denom;
 }
 
@@ -210,106 +214,103 @@ __global__ void __launch_bounds__(256) moe_router_kernel(RouterArgs a) {
   float y[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) y[j] = accs[j] + bias[j];
-  router_tail(a, y, c4, m0 + r, lg[r]);
+  router_tail<16, 4>(a, y, c4, m0 + r, lg[r]);
 }
 
-// The DPP form, for H % 128 == 0: thread (wave w, lane l) owns rows
-// 8 w + 2 (l / 16) and the next of the workgroup's 32, and columns
-// 4 (l % 16) .. + 3.  x never passes through LDS: for each 128-deep k-chunk,
-// lane l holds x[row][k0 + 8 (l % 16) .. + 7] of its two rows in registers,
-// and the value at k is broadcast from lane (k - k0) / 8 of each 16-lane row
-// by DPP row_newbcast.  W's chunk ([128, 64] f32, 32 KiB) is staged through
-// LDS, two stages: W rows loaded into registers during chunk c are written
-// to LDS at the start of chunk c + 1 (for chunk c + 2), so a whole chunk of
-// arithmetic covers each load.  Each logit is
-// the same fmaf chain over k from 0 as the narrow kernel's, so the bits
-// agree.  Per k a thread issues 2 broadcasts, 8 fmas and one 16-byte LDS
-// read, against 4 fmas, a 16-byte and a 4-byte LDS read in the narrow form:
-// the LDS traffic per fma halves and the broadcasts need no LDS.
-template <int J>
-__device__ __forceinline__ float row_bcast(float v) {
-  return __int_as_float(
-      __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + J, 0xf, 0xf, true));
-}
+// W chunk staging of the matrix-core form: a [128, 64] f32 chunk
+// of W's rows (columns past E clamped to E - 4 .. E - 1) is 2048 16-byte
+// vectors; thread tid loads k-rows bk + 16 i (bk = tid / 16) at columns
+// bc4 .. bc4 + 3 (bc4 = 4 (tid % 16)) from wp into eight named registers
+// (as an array the compiler kept them in scratch memory across the chunk
+// loop) and stores them to stage ST of Bs.
+#define REW_NB_LOAD(K0)                                       \
+do {                                                        \
+  const float* q_ = wp + (int64_t)(K0) * E;                 \
+  nb0 = *(const float4*)(q_);                               \
+  nb1 = *(const float4*)(q_ + 16 * (int64_t)E);             \
+  nb2 = *(const float4*)(q_ + 32 * (int64_t)E);             \
+  nb3 = *(const float4*)(q_ + 48 * (int64_t)E);             \
+  nb4 = *(const float4*)(q_ + 64 * (int64_t)E);             \
+  nb5 = *(const float4*)(q_ + 80 * (int64_t)E);             \
+  nb6 = *(const float4*)(q_ + 96 * (int64_t)E);             \
+  nb7 = *(const float4*)(q_ + 112 * (int64_t)E);            \
+} while (0)
+#define REW_NB_STORE(ST)                                      \
+do {                                                        \
+  float (*bw_)[64] = Bs[ST];                                \
+  *(float4*)&bw_[bk][bc4] = nb0;                            \
+  *(float4*)&bw_[bk + 16][bc4] = nb1;                       \
+  *(float4*)&bw_[bk + 32][bc4] = nb2;                       \
+  *(float4*)&bw_[bk + 48][bc4] = nb3;                       \
+  *(float4*)&bw_[bk + 64][bc4] = nb4;                       \
+  *(float4*)&bw_[bk + 80][bc4] = nb5;                       \
+  *(float4*)&bw_[bk + 96][bc4] = nb6;                       \
+  *(float4*)&bw_[bk + 112][bc4] = nb7;                      \
+} while (0)
 
-// k-steps 8 J .. 8 J + 7 of a chunk; bc holds their W rows, read one group ahead
+// The matrix-core form, for H % 128 == 0: wave w owns rows 8 w .. 8 w + 7 of
+// the workgroup's 32 as two quads, and each k-step of a quad is one
+// v_mfma_f32_4x4x1_16b_f32: sixteen 4 x 4 blocks, block b computing the
+// quad's 4 rows by columns 4 b .. 4 b + 3, so lane l accumulates column l of
+// the 4 rows.  An f32 MFMA with one k per block rounds each step exactly as
+// fmaf(x, w, acc) does (a single rounding of the exact product plus the
+// accumulator, denormals kept), so the chain over k from 0 gives every logit
+// the bits of the VALU chain, at twice the VALU's multiply-add rate.  x
+// reaches the matrix core by the MFMA's A broadcast: lane 4 j + i holds
+// x[row i][k0 + 8 j .. + 7] of a 128-deep chunk (one 16-byte load per quad
+// for bf16), and the step for k = k0 + 8 j + e takes A from value e of lane
+// group j (CBSZ 4, ABID j).  W's [128, 64] chunks are staged through LDS in
+// two stages: W rows loaded into registers during chunk c are written to LDS
+// at the start of chunk c + 1 (for chunk c + 2), so a whole chunk of
+// arithmetic covers each load; lane l reads W[k][l], one 4-byte read per k
+// shared by both quads.  A dependent 4x4x1 f32 MFMA waits about 40 cycles for
+// the previous step of its chain, and the T x E logits give each SIMD only
+// two chains (its wave's two quads), so the chains' latency, not the matrix
+// core's rate, sets the time: about 24 cycles per MFMA.
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+// k-steps 8 J .. 8 J + 7 of a chunk; bc and bn hold the W values of groups J
+// and J + 1, and group J + 2's are read here, two groups (32 MFMAs) ahead of
+// their use (the scheduling barrier keeps the compiler from sinking the
+// reads next to their MFMAs)
 template <int J>
-__device__ __forceinline__ void router_chunk(const float (*bs)[64], int c4, const float (&f0)[8],
-                                             const float (&f1)[8], const float4 (&bc)[8],
-                                             float (&acc0)[4], float (&acc1)[4]) {
-  float4 bn[8];
-  if constexpr (J + 1 < 16) {
+__device__ __forceinline__ void router_mchunk(const float (*bs)[64], int lane,
+                                              const float (&x0)[8], const float (&x1)[8],
+                                              const float (&bc)[8], const float (&bn)[8],
+                                              f4_t& acc0, f4_t& acc1) {
+  float bnn[8];
+  if constexpr (J + 2 < 16) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) bn[e] = *(const float4*)&bs[8 * (J + 1) + e][c4];
+    for (int e = 0; e < 8; ++e) bnn[e] = bs[8 * (J + 2) + e][lane];
   }
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float a0 = row_bcast<J>(f0[e]), a1 = row_bcast<J>(f1[e]);
-    acc0[0] = fmaf(a0, bc[e].x, acc0[0]);
-    acc0[1] = fmaf(a0, bc[e].y, acc0[1]);
-    acc0[2] = fmaf(a0, bc[e].z, acc0[2]);
-    acc0[3] = fmaf(a0, bc[e].w, acc0[3]);
-    acc1[0] = fmaf(a1, bc[e].x, acc1[0]);
-    acc1[1] = fmaf(a1, bc[e].y, acc1[1]);
-    acc1[2] = fmaf(a1, bc[e].z, acc1[2]);
-    acc1[3] = fmaf(a1, bc[e].w, acc1[3]);
+    acc0 = __builtin_amdgcn_mfma_f32_4x4x1f32(x0[e], bc[e], acc0, 4, J, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_4x4x1f32(x1[e], bc[e], acc1, 4, J, 0);
   }
-  if constexpr (J + 1 < 16) router_chunk<J + 1>(bs, c4, f0, f1, bn, acc0, acc1);
+  if constexpr (J + 1 < 16) router_mchunk<J + 1>(bs, lane, x0, x1, bn, bnn, acc0, acc1);
 }
 
 template <bool XBF16>
-__global__ void __launch_bounds__(256) moe_router_dpp_kernel(RouterArgs a) {
+__global__ void __launch_bounds__(256) moe_router_mfma_kernel(RouterArgs a) {
   __shared__ __attribute__((aligned(16))) float Bs[2][128][64];  // 64 KiB
   __shared__ float lg[32][kRouterMaxE + 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int l16 = lane & 15, c4 = l16 * 4;
-  const int rp = wave * 8 + (lane >> 4) * 2;  // the thread's first row in the workgroup
   const int64_t m0 = (int64_t)blockIdx.x * 32;
   const int E = a.E;
   constexpr int xe = XBF16 ? 2 : 4;
-  constexpr int NV = XBF16 ? 1 : 2;  // 16-byte x vectors per row per chunk
-  const int64_t r0 = m0 + rp < a.T ? m0 + rp : a.T - 1;
-  const int64_t r1 = m0 + rp + 1 < a.T ? m0 + rp + 1 : a.T - 1;
-  const char* x0 = (const char*)a.x + (r0 * a.x_rs + l16 * 8) * xe;
-  const char* x1 = (const char*)a.x + (r1 * a.x_rs + l16 * 8) * xe;
-  // W chunk loader: 2048 16-byte vectors, thread tid takes k-rows
-  // tid / 16 + 16 i and columns 4 (tid % 16) .. + 3 (clamped past E)
+  constexpr int NV = XBF16 ? 1 : 2;  // 16-byte x vectors per lane per quad per chunk
+  // lane 4 j + i: row i of each quad, k offset 8 j within a chunk
+  const int64_t q0 = m0 + 8 * wave + (lane & 3), q1 = q0 + 4;
+  const int64_t r0 = q0 < a.T ? q0 : a.T - 1, r1 = q1 < a.T ? q1 : a.T - 1;
+  const char* x0 = (const char*)a.x + (r0 * a.x_rs + 8 * (lane >> 2)) * xe;
+  const char* x1 = (const char*)a.x + (r1 * a.x_rs + 8 * (lane >> 2)) * xe;
   const int bk = tid >> 4, bc4 = (tid & 15) * 4;
   const float* wp = a.w + (int64_t)bk * E + (bc4 < E ? bc4 : E - 4);
-  float bias[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) bias[j] = a.b[c4 + j < E ? c4 + j : 0];
-  float acc0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, acc1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   const int nch = (int)(a.H / 128);
-  // the next chunk's x (as loaded) and W rows, in registers
   uint4 n0[NV], n1[NV];
-  // (eight named registers: as an array the compiler kept them in scratch
-  // memory across the chunk loop)
   float4 nb0, nb1, nb2, nb3, nb4, nb5, nb6, nb7;
-#define REW_NB_LOAD(K0)                                       \
-  do {                                                        \
-    const float* q_ = wp + (int64_t)(K0) * E;                 \
-    nb0 = *(const float4*)(q_);                               \
-    nb1 = *(const float4*)(q_ + 16 * (int64_t)E);             \
-    nb2 = *(const float4*)(q_ + 32 * (int64_t)E);             \
-    nb3 = *(const float4*)(q_ + 48 * (int64_t)E);             \
-    nb4 = *(const float4*)(q_ + 64 * (int64_t)E);             \
-    nb5 = *(const float4*)(q_ + 80 * (int64_t)E);             \
-    nb6 = *(const float4*)(q_ + 96 * (int64_t)E);             \
-    nb7 = *(const float4*)(q_ + 112 * (int64_t)E);            \
-  } while (0)
-#define REW_NB_STORE(ST)                                      \
-  do {                                                        \
-    float (*bw_)[64] = Bs[ST];                                \
-    *(float4*)&bw_[bk][bc4] = nb0;                            \
-    *(float4*)&bw_[bk + 16][bc4] = nb1;                       \
-    *(float4*)&bw_[bk + 32][bc4] = nb2;                       \
-    *(float4*)&bw_[bk + 48][bc4] = nb3;                       \
-    *(float4*)&bw_[bk + 64][bc4] = nb4;                       \
-    *(float4*)&bw_[bk + 80][bc4] = nb5;                       \
-    *(float4*)&bw_[bk + 96][bc4] = nb6;                       \
-    *(float4*)&bw_[bk + 112][bc4] = nb7;                      \
-  } while (0)
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     n0[i] = *(const uint4*)(x0 + 16 * i);
@@ -319,6 +320,7 @@ __global__ void __launch_bounds__(256) moe_router_dpp_kernel(RouterArgs a) {
   REW_NB_STORE(0);
   REW_NB_LOAD(nch > 1 ? 128 : 0);
   __syncthreads();
+  f4_t acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int c = 0; c < nch; ++c) {
     // chunk c + 1's W rows into the other stage (last read in chunk c - 1,
     // before the barrier that ended it), then chunk c + 2's loads; all
@@ -357,22 +359,37 @@ __global__ void __launch_bounds__(256) moe_router_dpp_kernel(RouterArgs a) {
       n1[i] = *(const uint4*)(x1 + kn * xe + 16 * i);
     }
     const float (*bs)[64] = Bs[c & 1];
-    float4 b0[8];
+    float b0[8], b1[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) b0[e] = *(const float4*)&bs[e][c4];
-    router_chunk<0>(bs, c4, f0, f1, b0, acc0, acc1);
+    for (int e = 0; e < 8; ++e) {
+      b0[e] = bs[e][lane];
+      b1[e] = bs[8 + e][lane];
+    }
+    router_mchunk<0>(bs, lane, f0, f1, b0, b1, acc0, acc1);
     __syncthreads();
   }
-#undef REW_NB_LOAD
-#undef REW_NB_STORE
+  // lane l holds column l of the wave's 8 rows: the logits (with the bias)
+  // go to the rows' LDS scratch, and each row's 16 lanes read their 4
+  // columns back for the tail
+  const float bias = a.b[lane < E ? lane : 0];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    lg[8 * wave + i][lane] = acc0[i] + bias;
+    lg[8 * wave + 4 + i][lane] = acc1[i] + bias;
+  }
+  __syncthreads();
+  const int c4 = (lane & 15) * 4;
 #pragma unroll
   for (int rr = 0; rr < 2; ++rr) {
+    const int row = 8 * wave + 4 * rr + (lane >> 4);
     float y[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) y[j] = (rr ? acc1[j] : acc0[j]) + bias[j];
-    router_tail(a, y, c4, m0 + rp + rr, lg[rp + rr]);
+    for (int j = 0; j < 4; ++j) y[j] = lg[row][c4 + j];
+    router_tail<16, 4>(a, y, c4, m0 + row, lg[row]);
   }
 }
+#undef REW_NB_LOAD
+#undef REW_NB_STORE
 
 }  // namespace
 
@@ -389,9 +406,9 @@ void launch_moe_router(const RouterArgs& a, hipStream_t stream) {
   if (a.H % 128 == 0) {
     const unsigned blocks = (unsigned)((a.T + 31) / 32);
     if (a.x_bf16)
-      hipLaunchKernelGGL(moe_router_dpp_kernel<true>, dim3(blocks), dim3(256), 0, stream, a);
+      hipLaunchKernelGGL(moe_router_mfma_kernel<true>, dim3(blocks), dim3(256), 0, stream, a);
     else
-      hipLaunchKernelGGL(moe_router_dpp_kernel<false>, dim3(blocks), dim3(256), 0, stream, a);
+      hipLaunchKernelGGL(moe_router_mfma_kernel<false>, dim3(blocks), dim3(256), 0, stream, a);
     REW_HIP(hipGetLastError());
     return;
   }
