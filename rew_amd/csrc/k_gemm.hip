@@ -291,9 +291,191 @@ __global__ void __launch_bounds__(256) gemm_f32_small_kernel(GemmArgs g) {
   }
 }
 
+// The smallest problems (fewer than 256 of the 16 x 16 tiles, f32 operands
+// with k-contiguous A rows and n-contiguous B rows): one wave per 8 x 8
+// tile, so four times the 16 x 16 kernel's workgroups, one output per lane.
+// With one wave per CU the time is the wave's own instruction stream: the
+// slabs' load latency, then per k-step one fma and three quarters of an LDS
+// read, each stall of which the wave sits out alone.  So the slabs move in
+// 256-deep k-blocks by global_load_lds (16 bytes per lane, all blocks in
+// flight at once, A's eight 1 KiB row pieces and B's eight 1 KiB pieces of
+// [k][8] rows per block, 16 instructions per block, clamped addresses), and
+// the chain starts as soon as the first block has landed: before it reads a
+// block it waits only for that block's instructions (vmcnt counts loads in
+// issue order; the compiler places these waits, as each block has its own
+// arrays).  Each block has its own pair of LDS arrays, A as [8][260]
+// (the eight rows' 16-byte reads land on distinct banks) and B as [256][8].
+// The chain reads 32 k-steps per group, the next group's reads issued before
+// the current group's fmas, in two register sets that trade roles.  Rows past M and columns past N load
+// clamped data whose outputs are never stored.  Each output is the same fmaf
+// chain over k = 0, 1, ... as gemm_f32_small_kernel's, its zero terms past K
+// (to a multiple of 16) applied in registers, so the bits agree.
+constexpr int kTinyK = 1024;      // K up to this
+constexpr int kTinyBlock = 256;   // k-steps per load block
+constexpr int kTinyPitch = 260;   // A row pitch in LDS (floats)
+
+typedef __attribute__((address_space(3))) float tiny_lds;
+typedef float tiny_f4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tiny_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  void* p = (void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(p, (short)0, (int)bytes, 0x00020000);
+}
+
+// block kb's DMA: A row rr's k = 256 kb + 4 lane .. + 3 into sa[rr][..], then
+// B's k-rows 256 kb + 32 j + lane / 2 at columns n0 + 4 (lane % 2) .. + 3
+// into sb[32 j + lane / 2][..]; addresses clamped into the operands
+__device__ __forceinline__ void tiny_dma(const GemmArgs& g, const float* a0, const float* b0,
+                                         int64_t m0, int64_t n0, int kb, tiny_lds* sa, tiny_lds* sb) {
+  const int lane = threadIdx.x, K = (int)g.K;
+  // byte offsets into buffer descriptors over this batch's A rows m0 ..
+  // m0 + 7 and B (the operands are small: tiny_ok bounds K, and M and N
+  // by the tile count)
+  const int64_t ml = m0 + 7 < g.M ? m0 + 7 : g.M - 1;
+  const __amdgpu_buffer_rsrc_t ra = tiny_rsrc(a0 + m0 * g.a_sm, (uint32_t)(((ml - m0) * g.a_sm + K) * 4));
+  const __amdgpu_buffer_rsrc_t rb = tiny_rsrc(b0, (uint32_t)(((int64_t)(K - 1) * g.b_sk + g.N) * 4));
+#pragma unroll
+  for (int rr = 0; rr < 8; ++rr) {
+    const int k = kb * kTinyBlock + 4 * lane;
+    const int64_t m = m0 + rr < g.M ? rr : ml - m0;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (__attribute__((address_space(3))) void*)(sa + rr * kTinyPitch), 16,
+                                             (uint32_t)((m * g.a_sm + (k < K ? k : 0)) * 4), 0, 0, 0);
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int k = kb * kTinyBlock + 32 * j + (lane >> 1);
+    const int64_t n = n0 + (lane & 1) * 4;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (__attribute__((address_space(3))) void*)(sb + 256 * j), 16,
+                                             (uint32_t)(((int64_t)(k < K ? k : 0) * g.b_sk + (n < g.N ? n : 0)) * 4), 0, 0, 0);
+  }
+}
+
+// 32 k-steps from k0 of one block: A's eight 16-byte reads, B's 32 values
+__device__ __forceinline__ void tiny_group_load(const tiny_lds* sa, const tiny_lds* sb, int r, int c,
+                                                int k0, tiny_f4 (&a)[8], float (&b)[32]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = *(const __attribute__((address_space(3))) tiny_f4*)(sa + r * kTinyPitch + k0 + 4 * i);
+#pragma unroll
+  for (int i = 0; i < 32; ++i) b[i] = sb[(k0 + i) * 8 + c];
+}
+__device__ __forceinline__ void tiny_group_fma(float& acc, const tiny_f4 (&a)[8],
+                                               const float (&b)[32]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    acc = fmaf(a[i].x, b[4 * i], acc);
+    acc = fmaf(a[i].y, b[4 * i + 1], acc);
+    acc = fmaf(a[i].z, b[4 * i + 2], acc);
+    acc = fmaf(a[i].w, b[4 * i + 3], acc);
+  }
+}
+
+// the chain over one block's ng (<= 8) 32-step groups, the next group's
+// reads issued before the current group's fmas in two register sets
+__device__ __forceinline__ void tiny_chain_block(const tiny_lds* sa, const tiny_lds* sb, int r, int c,
+                                                 int ng, float& acc) {
+  tiny_f4 a0[8], a1[8];
+  float b0[32], b1[32];
+  tiny_group_load(sa, sb, r, c, 0, a0, b0);
+#pragma unroll
+  for (int gi = 0; gi < 8; gi += 2) {
+    if (gi >= ng) break;
+    if (gi + 1 < ng) tiny_group_load(sa, sb, r, c, 32 * (gi + 1), a1, b1);
+    tiny_group_fma(acc, a0, b0);
+    if (gi + 1 >= ng) break;
+    if (gi + 2 < ng) tiny_group_load(sa, sb, r, c, 32 * (gi + 2), a0, b0);
+    tiny_group_fma(acc, a1, b1);
+  }
+}
+
+// the k-steps from k0 to K (fewer than 32, inside one block), four at a time
+__device__ __forceinline__ void tiny_chain_tail(const tiny_lds* sa, const tiny_lds* sb, int r, int c,
+                                                int k0, int k1, float& acc) {
+  for (int k = k0; k < k1; k += 4) {
+    const tiny_f4 av = *(const __attribute__((address_space(3))) tiny_f4*)(sa + r * kTinyPitch + k);
+    acc = fmaf(av.x, sb[k * 8 + c], acc);
+    acc = fmaf(av.y, sb[(k + 1) * 8 + c], acc);
+    acc = fmaf(av.z, sb[(k + 2) * 8 + c], acc);
+    acc = fmaf(av.w, sb[(k + 3) * 8 + c], acc);
+  }
+}
+
+__global__ void __launch_bounds__(64) gemm_f32_tiny_kernel(GemmArgs g) {
+  // one pair of arrays per k-block, so that the compiler's waits for an LDS
+  // read cover only the DMA of that read's block
+  __shared__ __attribute__((aligned(16))) float ta0[8 * kTinyPitch], ta1[8 * kTinyPitch],
+      ta2[8 * kTinyPitch], ta3[8 * kTinyPitch];
+  __shared__ __attribute__((aligned(16))) float tb0[kTinyBlock * 8], tb1[kTinyBlock * 8],
+      tb2[kTinyBlock * 8], tb3[kTinyBlock * 8];
+  // LDS-typed pointers (no generic-to-LDS conversions at each use)
+  tiny_lds *sa0 = (tiny_lds*)ta0, *sa1 = (tiny_lds*)ta1, *sa2 = (tiny_lds*)ta2, *sa3 = (tiny_lds*)ta3;
+  tiny_lds *sb0 = (tiny_lds*)tb0, *sb1 = (tiny_lds*)tb1, *sb2 = (tiny_lds*)tb2, *sb3 = (tiny_lds*)tb3;
+  const int lane = threadIdx.x;
+  const int r = lane >> 3, c = lane & 7;
+  const int K = (int)g.K;
+  const int K16 = (K + 15) & ~15, K32 = K & ~31;
+  const int nkb = (K + kTinyBlock - 1) / kTinyBlock;
+  const int64_t m0 = (int64_t)blockIdx.y * 8, n0 = (int64_t)blockIdx.x * 8;
+  auto ng = [&](int kb) {
+    const int n = (K32 - kb * kTinyBlock) / 32;
+    return n < 0 ? 0 : (n > 8 ? 8 : n);
+  };
+  for (int64_t b = blockIdx.z; b < g.batch; b += gridDim.z) {
+    const float* a0 = (const float*)g.a + b * g.a_sb;
+    const float* b0 = (const float*)g.b + b * g.b_sb;
+    // all four blocks are issued whatever K is (blocks past K load clamped
+    // addresses), in a fixed order with the chain: blocks 0 and 1, block 0's
+    // chain, block 2, block 1's chain, block 3, then the rest.  So the
+    // compiler's waits before each block's first read count exactly the DMA
+    // instructions issued after that block's, and the wave's issue of the
+    // later blocks (its outstanding loads are capped) overlaps the chain.
+    tiny_dma(g, a0, b0, m0, n0, 0, sa0, sb0);
+    tiny_dma(g, a0, b0, m0, n0, 1, sa1, sb1);
+    float acc = 0.0f;
+    tiny_chain_block(sa0, sb0, r, c, ng(0), acc);
+    tiny_dma(g, a0, b0, m0, n0, 2, sa2, sb2);
+    if (nkb > 1) tiny_chain_block(sa1, sb1, r, c, ng(1), acc);
+    tiny_dma(g, a0, b0, m0, n0, 3, sa3, sb3);
+    if (nkb > 2) tiny_chain_block(sa2, sb2, r, c, ng(2), acc);
+    if (nkb > 3) tiny_chain_block(sa3, sb3, r, c, ng(3), acc);
+    if (K32 < K) {
+      // the last k-steps lie in one block
+      const int kb = K32 / kTinyBlock, k0 = K32 - kb * kTinyBlock, k1 = K - kb * kTinyBlock;
+      if (kb == 0) tiny_chain_tail(sa0, sb0, r, c, k0, k1, acc);
+      else if (kb == 1) tiny_chain_tail(sa1, sb1, r, c, k0, k1, acc);
+      else if (kb == 2) tiny_chain_tail(sa2, sb2, r, c, k0, k1, acc);
+      else tiny_chain_tail(sa3, sb3, r, c, k0, k1, acc);
+    }
+    for (int k = K; k < K16; ++k) acc = fmaf(0.0f, 0.0f, acc);
+    // every DMA landed and every read done before the next batch's loads
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
+    __syncthreads();
+    const int64_t m = m0 + r, n = n0 + c;
+    if (m < g.M && n < g.N)
+      vm::store_scalar(g.c, g.c_dtype, b * g.c_sb + m * g.c_sm + n,
+                       vm::as_u(epi_value(g, b, m, n, acc)));
+  }
+}
+
+static bool tiny_ok(const GemmArgs& g) {
+  const int64_t tiles16 = ((g.M + 15) / 16) * ((g.N + 15) / 16) * g.batch;
+  return tiles16 < 256 && g.dtype == REW_DT_FLOAT32 && g.a_sk == 1 && g.b_sn == 1 &&
+         g.K >= 4 && g.K % 4 == 0 && g.K <= kTinyK && g.N % 4 == 0 && g.a_sm % 4 == 0 &&
+         g.b_sk % 4 == 0 && g.a_sb % 4 == 0 && g.b_sb % 4 == 0 &&
+         ((uintptr_t)g.a & 15) == 0 && ((uintptr_t)g.b & 15) == 0;
+}
+
 static void launch_gemm_small(const GemmArgs& g, hipStream_t stream) {
   dim3 grid((unsigned)((g.N + 15) / 16), (unsigned)((g.M + 15) / 16),
             (unsigned)(g.batch < 65535 ? g.batch : 65535));
+  if (tiny_ok(g)) {
+    dim3 tgrid((unsigned)((g.N + 7) / 8), (unsigned)((g.M + 7) / 8),
+               (unsigned)(g.batch < 65535 ? g.batch : 65535));
+    hipLaunchKernelGGL(gemm_f32_tiny_kernel, tgrid, dim3(64), 0, stream, g);
+    return;
+  }
   const int64_t k16 = (g.K + 15) & ~(int64_t)15;
   if (k16 <= kSmallWholeK) {
     const size_t lds = (size_t)16 * (k16 + 4) * 4 * 2;

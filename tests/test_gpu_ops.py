@@ -233,12 +233,18 @@ def test_matmul_f32_narrow(gpu, oracle, M, K, N):
     assert np.all(np.abs(got - want) <= bound + 1e-30)
 
 
-@pytest.mark.parametrize("M,K,N", [(128, 784, 128), (128, 128, 10), (37, 100, 70)])
+@pytest.mark.parametrize("M,K,N", [(128, 784, 128), (128, 128, 10), (37, 100, 70),
+                                   # the one-wave 8x8 form: ragged rows, K past the
+                                   # last 32-step group and short of 16, K < 32, K at
+                                   # its limit
+                                   (37, 100, 72), (130, 52, 20), (16, 12, 8),
+                                   (72, 1024, 68)])
 def test_matmul_f32_small_equals_generic(gpu, oracle, M, K, N):
     """Products with too few 64x64 tiles to fill the GPU (the MNIST MLP's)
-    take 16x16 tiles with the next k-chunk prefetched; each output keeps the
-    generic kernel's fmaf chain, so a batch of 128 of the same product (enough
-    tiles for the generic kernel) gives the same bits in every slice."""
+    take 16x16 tiles, or one wave per 8x8 tile when even the 16x16 tiles
+    would leave most CUs idle; each output keeps the generic kernel's fmaf
+    chain, so a batch of 128 of the same product (enough tiles for the
+    generic kernel) gives the same bits in every slice."""
     r = rng(M * 3 + K + N)
     a = r.uniform(-1, 1, (M, K)).astype(np.float32)
     b = r.uniform(-0.1, 0.1, (K, N)).astype(np.float32)
