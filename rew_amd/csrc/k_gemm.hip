@@ -763,8 +763,10 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_256_kernel(GemmArgs g, Group
       else hi = mid - 1;
     }
     grp = lo;
-    row0 = ga.off[grp] + (tm - ga.mt_start[grp]) * BM;
-    m_rows = min((int64_t)BM, (int64_t)ga.off[grp + 1] - row0);
+    // (a small group's tiles hold group_tile_rows rows, the rest unused)
+    const int tr = group_tile_rows(ga.off[grp + 1] - ga.off[grp]);
+    row0 = ga.off[grp] + (tm - ga.mt_start[grp]) * tr;
+    m_rows = min((int64_t)tr, (int64_t)ga.off[grp + 1] - row0);
   } else {
     const int64_t tiles_m = (g.M + BM - 1) / BM;
     tile_of(blockIdx.x, tiles_m, tiles_n, g.batch, &b, &tm, &tn);

@@ -50,7 +50,9 @@
 // Modes (template): B N-contiguous or K-contiguous; DUAL (SwiGLU: the tile's
 // 256 B columns are 128 gate + 128 up columns of two weight matrices, each
 // lane fetching from either); GROUP (routed experts: tile -> group from the
-// device tables, A rows gathered through a row list).  The MFMAs produce
+// device tables, A rows gathered through a row list; a group of at most 128
+// rows gets 64-row tiles, the four waves side by side on 64 x 64 outputs
+// each, with the same B stream and ring).  The MFMAs produce
 // C^T blocks, so each lane holds runs of four consecutive output columns:
 // the epilogue writes them to a C tile in LDS as 8-byte chunks, then stores
 // whole 512-byte row segments with the fused bias / residual / SwiGLU
@@ -205,12 +207,12 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
   };
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
   constexpr int TN = DUAL ? BN / 2 : BN;  // output columns per workgroup
 
   // ---- tile (and, over several GEMMs of one A, its segment) ---------------------------
   int64_t b = 0, tm = 0, tn = 0, m_rows, row0;
   int grp = 0, seg = 0;
+  bool small = false;  // a kSmallTileM-row tile of a small group
   if constexpr (GROUP) {
     // The grid covers the host's bound on the tiles (max_mtiles rows of
     // them); the routing fixes the real count, read here.  Workgroups past it
@@ -237,8 +239,10 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
       else hi = mid - 1;
     }
     grp = lo;
-    row0 = ga.off[grp] + (tm - ga.mt_start[grp]) * BM;
-    m_rows = min((int64_t)BM, (int64_t)ga.off[grp + 1] - row0);
+    const int tr = group_tile_rows(ga.off[grp + 1] - ga.off[grp]);
+    small = tr == kSmallTileM;
+    row0 = ga.off[grp] + (tm - ga.mt_start[grp]) * tr;
+    m_rows = min((int64_t)tr, (int64_t)ga.off[grp + 1] - row0);
   } else {
     tile_order(blockIdx.x, (gs.g[0].M + BM - 1) / BM, gs.tn0[gs.n], gs.g[0].batch, &b, &tm,
                &tn);
@@ -247,6 +251,21 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
     row0 = tm * BM;
     m_rows = min((int64_t)BM, gs.g[0].M - row0);
   }
+
+  // The rest of the kernel is one of two bodies (SM): the 256-row tile, its
+  // four waves 2 x 2 of 128 x 128 outputs, or a small group's 64-row tile
+  // (grouped, buffer path, N-contiguous B), its four waves side by side,
+  // each 64 rows x 64 of the 256 B columns: the same B stream and ring, a
+  // quarter of the MFMAs and of the A stream.  (Grouped launches in the
+  // other modes run a small group's tiles with the 256-row body.)
+  auto run = [&](auto SM) {
+  constexpr bool SMALL = decltype(SM)::value;
+  static_assert(!SMALL || (GROUP && BUF && !B_KC), "64-row tiles: grouped buffer path");
+  constexpr int MI = SMALL ? 2 : 4;    // 32-row blocks per wave
+  constexpr int NJ = SMALL ? 2 : 4;    // 32-column blocks per wave
+  constexpr int NAQ = SMALL ? 2 : 8;   // A pair DMA instructions per wave
+  const int wm = SMALL ? 0 : wave >> 1;                    // rows wm * 128 ..
+  const int cb0 = SMALL ? wave * 64 : (wave & 1) * 128;    // the wave's first B column
   const GemmArgs& g = gs.g[seg];
   const int64_t n0 = tn * TN;
   const int K = (int)g.K;
@@ -316,18 +335,19 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
     }
   }
 
-  // BUF: A moves a k-tile pair at a time, 8 instructions per wave; lane l of
-  // instruction q of wave w covers row r = 8 (8 w + q) + l / 8, physical
-  // 16-byte chunk l % 8, which holds logical chunk (l % 8) ^ ((r >> 1) & 7)
-  // (chunks 0-3 the first k-tile of the pair, 4-7 the second).  The 16 lanes
-  // a ds_read_b128 serves per cycle read one logical chunk of 16 rows;
-  // rows r and r + 1 fall in different halves of a 256-byte bank window and
-  // the XOR spreads the 8 even (odd) rows over 8 distinct chunks.
-  uint32_t vap[8];
+  // BUF: A moves a k-tile pair at a time, NAQ (8; 64-row tiles 2)
+  // instructions per wave; lane l of instruction q of wave w covers row
+  // r = 8 (NAQ w + q) + l / 8, physical 16-byte chunk l % 8, which holds
+  // logical chunk (l % 8) ^ ((r >> 1) & 7) (chunks 0-3 the first k-tile of
+  // the pair, 4-7 the second).  The 16 lanes a ds_read_b128 serves per cycle
+  // read one logical chunk of 16 rows; rows r and r + 1 fall in different
+  // halves of a 256-byte bank window and the XOR spreads the 8 even (odd)
+  // rows over 8 distinct chunks.
+  uint32_t vap[NAQ];
   if constexpr (BUF) {
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int r = 8 * (8 * wave + q) + (lane >> 3);
+    for (int q = 0; q < NAQ; ++q) {
+      const int r = 8 * (NAQ * wave + q) + (lane >> 3);
       const int c = (lane & 7) ^ ((r >> 1) & 7);
       const int rr = r < m_rows ? r : (int)m_rows - 1;
       int64_t arow;
@@ -356,12 +376,13 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
 #pragma unroll
     for (int q = 0; q < 4; ++q) dma_b(q, sob, sb + q * 1024);
   };
-  // BUF: half `half` (rows 128 half .. + 127) of A of the k-tile pair
+  // BUF: half `half` of this wave's instructions (its rows
+  // 8 (NAQ w + NAQ / 2 half) .. + 4 NAQ - 1) for the A of the k-tile pair
   // starting at k0, into A stage ast
   auto issue_a = [&](uint8_t* ast, int k0, int half) {
-    uint8_t* sa = ast + wave * 8192;
+    uint8_t* sa = ast + wave * NAQ * 1024;
 #pragma unroll
-    for (int q = 4 * half; q < 4 * half + 4; ++q)
+    for (int q = NAQ / 2 * half; q < NAQ / 2 * (half + 1); ++q)
       buf_to_lds16(ra, vap[q], (uint32_t)k0 * 2, sa + q * 1024);
   };
 
@@ -423,10 +444,10 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
     for (int h = 0; h < 2; ++h)
       ap_off[h][s] = a_row * 128 + (((4 * h + 2 * s + (lane >> 5)) ^ ((a_row >> 1) & 7)) * 16);
   }
-  int b_off[4];   // per fragment column block j (substep s adds s * 8192), from the B half
+  int b_off[NJ];  // per fragment column block j (substep s adds s * 8192), from the B half
   int bk_off[2];  // B_KC: per substep
   if constexpr (B_KC) {
-    const int b_row = wn * 128 + (lane & 31);
+    const int b_row = cb0 + (lane & 31);
 #pragma unroll
     for (int s = 0; s < 2; ++s)
       bk_off[s] = b_row * 64 + (((2 * s + (lane >> 5)) ^ ((b_row >> 2) & 3)) * 16);
@@ -434,34 +455,34 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
     const int grp16 = lane >> 4, s16 = lane & 15;
     const int kr = 8 * (grp16 >> 1) + (s16 >> 2);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int col = wn * 128 + j * 32 + 16 * (grp16 & 1) + 4 * (s16 & 3);
+    for (int j = 0; j < NJ; ++j) {
+      const int col = cb0 + j * 32 + 16 * (grp16 & 1) + 4 * (s16 & 3);
       b_off[j] = kr * 512 + ((((col >> 3) ^ (4 * (kr & 3)))) * 16) + (col & 7) * 2;
     }
   }
 
-  f32x16_t acc[4][4];
+  f32x16_t acc[MI][NJ];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  bf16x8_t fa[2][4], fb[2][4];
+  bf16x8_t fa[2][MI], fb[2][NJ];
   // fragments of one substep: A rows from abase (a row stride of `ast`
   // bytes per 32-row block), B from bbase (the B half of a stage)
   constexpr int AST = BUF ? 32 * 128 : 32 * 64;
   auto read_frags = [&](const uint8_t* abase, int aoff, const uint8_t* bbase, int s, int slot) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fa[slot][i] = *(const bf16x8_t*)(abase + aoff + i * AST);
+    for (int i = 0; i < MI; ++i) fa[slot][i] = *(const bf16x8_t*)(abase + aoff + i * AST);
     if constexpr (B_KC) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < NJ; ++j)
         fb[slot][j] = *(const bf16x8_t*)(bbase + bk_off[s] + j * 32 * 64);
     } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < NJ; ++j) {
         const uint8_t* p = bbase + b_off[j] + s * 16 * 512;
         const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)p);
         const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(p + 4 * 512));
@@ -478,9 +499,9 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
   // products and their k order per element are the same either way.
   auto mfmas = [&](int slot) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < NJ; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[slot][j], fa[slot][i], acc[i][j],
                                                             0, 0, 0);
   };
@@ -521,6 +542,17 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
       if (x < 12) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
       if (x % (16 / nvm) == 0) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM (DMA)
+    }
+  };
+  // 64-row tiles, either substep: 4 MFMAs with the 6 fragment reads and nvm
+  // (1 or 4) DMA instructions
+  auto pin_small = [&](int nvm) {
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      if (x < 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS reads
+      else __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (nvm == 4 || x == 0) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM
     }
   };
   // K-tail path: stage kt % NS holds A and B of tile kt; tile kt + NS goes
@@ -569,15 +601,20 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
       issue_b(BS((j + 2) & 3), (kt + 2 < nk ? kt + 2 : kt) * BK);
     }
     mfmas(0);
-    pin_reads4();
+    if constexpr (SMALL) pin_small(j & 1 ? 4 : NAQ / 2);
+    else pin_reads4();
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(waitcnt_imm(8, 0));
+    // (64-row tiles: a pair half is NAQ / 2 instructions, so the even
+    // steps' count is NAQ)
+    if (j & 1) __builtin_amdgcn_s_waitcnt(waitcnt_imm(8, 0));
+    else __builtin_amdgcn_s_waitcnt(waitcnt_imm(NAQ, 0));
     block_barrier();
     read_frags(anxt, ap_off[jn & 1][0], BS(jn), 0, 0);
     if (j & 1) issue_a(acur, (kt + 3 < nk ? kt + 3 : kt - 1) * BK, 0);
     else issue_b(BS(j), (kt + NS < nk ? kt + NS : kt) * BK);
     mfmas(1);
-    pin_last(4);
+    if constexpr (SMALL) pin_small(j & 1 ? NAQ / 2 : 4);
+    else pin_last(4);
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -591,7 +628,8 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
     issue_b(BS(2), (2 < nk ? 2 : 0) * BK);
     issue_b(BS(1), (1 < nk ? 1 : 0) * BK);
     issue_a(AS(1), (2 < nk ? 2 : 0) * BK, 0);
-    __builtin_amdgcn_s_waitcnt(waitcnt_imm(12, 15));
+    // (the last three requests, 8 + NAQ / 2 instructions, stay in flight)
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(8 + NAQ / 2, 15));
     block_barrier();
     read_frags(AS(0), ap_off[0][0], BS(0), 0, 0);
     // Whole turns of the ring, then the remaining steps (nk is even): no
@@ -636,14 +674,14 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
   };
   {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < MI; ++i) {
       uint8_t* cb = CB(wm * 4 + i);  // rows wm * 128 + 32 i + [0, 32)
       const int lr = lane & 31;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < NJ; ++j)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const int col = wn * 128 + j * 32 + q * 8 + (lane >> 5) * 4;
+          const int col = cb0 + j * 32 + q * 8 + (lane >> 5) * 4;
           float v[4];
 #pragma unroll
           for (int x = 0; x < 4; ++x) v[x] = acc[i][j][q * 4 + x];
@@ -660,7 +698,7 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
   constexpr int OC = DUAL ? 128 : 256;  // output columns per tile
   constexpr int CH = OC / 8;            // 16-byte chunks per output row
   constexpr int RPI = 256 / CH;         // rows per pass of the workgroup
-  constexpr int PASSES = BM / RPI;
+  constexpr int PASSES = (SMALL ? kSmallTileM : BM) / RPI;
   const int ch = tid % CH, r_in = tid / CH;
   const int64_t n = n0 + ch * 8;
   const bool col_ok = n < g.N;
@@ -689,7 +727,7 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
   auto row_of = [&](int p) { return p * RPI + r_in; };
   auto row_ok = [&](int row) { return row < m_rows && col_ok; };
   auto crow = [&](int row) { return row0 + (row < m_rows ? row : (int)m_rows - 1); };
-  constexpr int U = 8;
+  constexpr int U = SMALL ? 4 : 8;
   static_assert(PASSES % U == 0, "passes per operand batch");
 
   if (epi == EPI_SWIGLU) {
@@ -790,7 +828,8 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
     // on the four pairs of a chunk, scattered into the rotated tensor's
     // layout
     constexpr int UR = 4;
-    static_assert(PASSES % (2 * UR) == 0, "rotation operand batches");
+    // (DUAL kernels never take this branch: their epilogue is the SwiGLU)
+    static_assert(DUAL || PASSES % (2 * UR) == 0, "rotation operand batches");
     const uint32_t nn = (uint32_t)nc;
     const uint32_t hq = nn / (uint32_t)g.rope_D, dq = nn - hq * (uint32_t)g.rope_D;
     const uint32_t rS = (uint32_t)g.rope_S;
@@ -876,6 +915,15 @@ __global__ void __launch_bounds__(256, 1) gemm_lds_kernel(GemmSegs gs, GroupArgs
     else if (vmode == 1) rotate(IntK<1>{});
     else rotate(IntK<0>{});
   }
+  };  // run
+
+  if constexpr (GROUP && BUF && !B_KC) {
+    if (small) {  // (uniform)
+      run(IntK<1>{});
+      return;
+    }
+  }
+  run(IntK<0>{});
 }
 
 // Conditions of the gemm_lds kernels: bf16 in / out, K-contiguous A with

@@ -98,13 +98,13 @@ __global__ void __launch_bounds__(1024) moe_scan_kernel(MoeRouteArgs a, int nblk
       a.off[m] = off;
       a.mt_start[m] = mt;
       off += tot[m];
-      mt += (tot[m] + a.tile_m - 1) / a.tile_m;
+      mt += group_tiles(tot[m]);
     }
     a.off[a.n_members] = off;
     a.mt_start[a.n_members] = mt;
     for (int sh = 1; sh <= a.n_shared; ++sh) {
       a.off[a.n_members + sh] = off + sh * (int)a.T;
-      a.mt_start[a.n_members + sh] = mt + sh * (int)((a.T + a.tile_m - 1) / a.tile_m);
+      a.mt_start[a.n_members + sh] = mt + sh * group_tiles(a.T);
     }
   }
 }
@@ -152,7 +152,7 @@ __global__ void __launch_bounds__(256) moe_place_kernel(MoeRouteArgs a, int nblk
       const int all = part[4 * n + m] + part[5 * n + m] + part[6 * n + m] + part[7 * n + m];
       base[m] = part[m] + part[n + m] + part[2 * n + m] + part[3 * n + m];
       tot[m] = all;
-      til[m] = (all + a.tile_m - 1) / a.tile_m;
+      til[m] = group_tiles(all);
     }
     __syncthreads();
     if (wave == 0) {
@@ -187,7 +187,7 @@ __global__ void __launch_bounds__(256) moe_place_kernel(MoeRouteArgs a, int nblk
         a.mt_start[n] = i2;
         for (int sh = 1; sh <= a.n_shared; ++sh) {  // groups of all T tokens
           a.off[n + sh] = i1 + sh * (int)a.T;
-          a.mt_start[n + sh] = i2 + sh * (int)((a.T + a.tile_m - 1) / a.tile_m);
+          a.mt_start[n + sh] = i2 + sh * group_tiles(a.T);
         }
       }
     }
@@ -359,7 +359,7 @@ __global__ void __launch_bounds__(256) moe_combine_kernel(MoeCombineArgs a) {
 
 int launch_moe_route(const MoeRouteArgs& a, hipStream_t stream) {
   if (a.n_members <= 0) return 0;
-  if (a.k < 1 || a.k > kMoeMaxK || a.tile_m <= 0 || a.n_members > kMoeMaxMembers)
+  if (a.k < 1 || a.k > kMoeMaxK || a.n_members > kMoeMaxMembers)
     fail(REW_MI355X_ERR_INVALID, "internal: MoE routing launch outside its limits");
   const int nblk = (int)((a.T + kMoeRouteBlock - 1) / kMoeRouteBlock);
   const size_t n4 = (size_t)a.n_members * sizeof(int);

@@ -110,7 +110,7 @@ enum GemmEpi : int {
 void launch_gemm(const GemmArgs& g, hipStream_t stream);
 
 // Grouped GEMM over packed rows (the routed experts of a MoE layer).  Group
-// i owns packed rows [off[i], off[i+1]) and 256-row tiles
+// i owns packed rows [off[i], off[i+1]) and row tiles
 // [mt_start[i], mt_start[i+1]); its B / b2 / bias / bias2 come from the
 // device pointer tables.  Row r of the A operand is A row rows[r] when
 // `rows` is set (a gather from the token matrix), else packed row r.  C is
@@ -120,6 +120,18 @@ void launch_gemm(const GemmArgs& g, hipStream_t stream);
 // meaning except: a = the A matrix (token matrix when gathering) with M its
 // row count; b, b2, bias, bias2 ignored (taken from the tables); c = the
 // packed output with c_sm its row stride.
+//
+// A group of at most kSmallGroupRows rows is cut into kSmallTileM-row tiles
+// (the LDS kernel runs those with its four waves side by side on 64 rows, a
+// quarter of the MFMAs of a 256-row tile), any other group into 256-row
+// tiles: group_tiles gives the count the routing writes into mt_start, and
+// every grouped kernel reads a group's tile height back by group_tile_rows.
+constexpr int kSmallGroupRows = 128;
+constexpr int kSmallTileM = 64;
+constexpr int group_tile_rows(int64_t rows) { return rows <= kSmallGroupRows ? kSmallTileM : 256; }
+constexpr int group_tiles(int64_t rows) {
+  return (int)((rows + group_tile_rows(rows) - 1) / group_tile_rows(rows));
+}
 struct GroupArgs {
   const int32_t* off;       // n_groups + 1 (device)
   const int32_t* mt_start;  // n_groups + 1 (device)
@@ -369,9 +381,8 @@ struct MoeRouteArgs {
   const int32_t* member_of;  // [E] member index or -1 (device)
   const int32_t* members;    // [n_members] expert id (device)
   int n_members;
-  int tile_m;                // row tile of the grouped GEMMs
   int32_t* off;              // [n_members + 1] packed row offsets (out)
-  int32_t* mt_start;         // [n_members + 1] tile starts (out)
+  int32_t* mt_start;         // [n_members + 1] tile starts, group_tiles each (out)
   int32_t* perm;             // [T * k] packed row -> token (out)
   int32_t* ord_slot;         // [T, k] the token's packed rows in chain order, then -1 (out)
   float* ord_w;              // [T, k] their gate weights (out)

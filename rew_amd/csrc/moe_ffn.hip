@@ -252,7 +252,6 @@ void run_routed_ffn(Ctx* c, const RoutedFfn& a, void* scratch) {
   ra.member_of = member_of;
   ra.members = members;
   ra.n_members = n;
-  ra.tile_m = 256;
   ra.n_shared = ns;
   const int64_t RS = R + (int64_t)ns * a.T;  // hidden rows: routed, then shared
   ra.off = route;
@@ -278,7 +277,8 @@ void run_routed_ffn(Ctx* c, const RoutedFfn& a, void* scratch) {
   ga.off = ra.off;
   ga.mt_start = ra.mt_start;
   ga.n_groups = groups;
-  ga.max_mtiles = (R + 255) / 256 + n + (int64_t)ns * ((a.T + 255) / 256);
+  // (a group of r rows takes at most r / 256 + 2 tiles, group_tiles)
+  ga.max_mtiles = (R + 255) / 256 + 2 * n + (int64_t)ns * group_tiles(a.T);
   ga.rows = ra.perm;
   ga.b = tables;
   ga.b2 = tables + groups;
@@ -318,7 +318,7 @@ void run_routed_ffn(Ctx* c, const RoutedFfn& a, void* scratch) {
     prev_rs = a.H;
   }
   ga.n_groups = n;
-  ga.max_mtiles = (R + 255) / 256 + n;
+  ga.max_mtiles = (R + 255) / 256 + 2 * n;
   ga.rows = nullptr;
   ga.b = tables + 4 * groups;
   ga.b2 = nullptr;

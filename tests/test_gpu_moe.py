@@ -134,6 +134,79 @@ def test_moe_sparse_equals_dense_op_by_op(gpu, oracle):
     np.testing.assert_array_equal(sparse, dense)
 
 
+def small_and_large_groups(oracle):
+    """Groups of more than 128 rows (256-row tiles, ragged last ones), of
+    65-128 rows (two 64-row tiles) and of at most 64 rows (one) in the same
+    grouped launches (this seed's router, two experts biased: rows per
+    expert 215, 37, 500, 334, 4, 105, 22, 62, 1 and zeros).  Returns the
+    sparse and the dense op-by-op results and the oracle's."""
+    T, H, I, E_, k = 640, 256, 128, 16, 2
+    moe, host = build_moe(oracle, T, H, I, E_, k, 1, 0x5EED0205)
+    br = np.zeros(E_, np.float32)
+    br[1] = 0.33
+    br[9] = 0.165
+    moe.gate = nn.Linear(E.fromHost(host["wr"]), E.fromHost(br))
+    probs = oracle.softmax_rows(oracle.linear(host["x"], host["wr"], br, False))
+    _, ids = oracle.topk_rows(probs, k)
+    rows = np.bincount(ids.ravel(), minlength=E_)
+    assert (rows > 256).any() and (rows % 256 != 0)[rows > 256].any(), rows
+    assert ((rows > 64) & (rows <= 128)).any() and ((rows > 0) & (rows <= 64)).any(), rows
+    xt = E.fromHost(host["x"], DType.BFLOAT16)
+    sparse = E.toHostF32(moe.forward(xt))
+    E.setMode(E.MODE_OP_BY_OP)
+    try:
+        dense = E.toHostF32(moe.forward(xt))
+    finally:
+        E.setMode(E.MODE_DEFERRED)
+    want, _, _ = oracle.deepseek_moe(host["x"], host["shared"], host["routed"], host["wr"],
+                                     br, k)
+    return sparse, dense, want
+
+
+def test_moe_small_and_large_groups(gpu, oracle):
+    """The 64-row tiles of the small groups run the same MFMA sequence per
+    output as the 256-row tiles, so the sparse result equals the dense
+    op-by-op one and stays within the oracle's tolerance."""
+    sparse, dense, want = small_and_large_groups(oracle)
+    np.testing.assert_array_equal(sparse, dense)
+    err = np.linalg.norm(sparse - want) / np.linalg.norm(want)
+    assert err <= 2e-2, f"normwise relative error {err:.3e}"
+
+
+MIXED_CHILD = r"""
+import json, sys
+import numpy as np
+root = sys.argv[1]
+for p in (root, root + "/tests", root + "/oracle"):
+    sys.path.insert(0, p)
+import oracle as orc
+from test_gpu_moe import small_and_large_groups
+from rew_amd import eager as E
+E.installEagerBackend(E.mi355x(0))
+sparse, dense, want = small_and_large_groups(orc)
+print(json.dumps({"equal": bool(np.array_equal(sparse, dense)),
+                  "err": float(np.linalg.norm(sparse - want) / np.linalg.norm(want))}))
+"""
+
+
+def test_moe_small_groups_on_the_register_staged_kernel(gpu, oracle):
+    """REW_MI355X_GEMM_TILE=256 sends the grouped GEMMs to the register-staged
+    256 x 256 kernel, which reads the same 64-row tiles of the small groups
+    (as 256-row tiles with the rows past 64 unused)."""
+    import json
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = Path(__file__).resolve().parents[1]
+    env = dict(os.environ, REW_MI355X_GEMM_TILE="256")
+    r = subprocess.run([sys.executable, "-c", MIXED_CHILD, str(root)], env=env,
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-3000:]
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    assert res["equal"] and res["err"] <= 2e-2, res
+
+
 def test_moe_expert_matrices_far_apart(gpu, oracle):
     """Expert gate and up weights more than 2 GiB apart (allocations need
     not be near each other).  Shared expert 1's: the two shared SwiGLU GEMMs
