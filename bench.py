@@ -298,7 +298,7 @@ def entry_flops(entry_name: str) -> int | None:
         B, H, _, Sq, Sk, D, cmp, _ = dims
         return 4 * B * H * D * visible_pairs(Sq, Sk, cmp)
     if entry_name.startswith("moe_gemm"):
-        _, rows, n, k = dims  # [members, routed rows, N, K]
+        _, rows, n, k = dims  # [groups, rows (routed, then shared), N, K]
         return (4 if "swiglu" in entry_name else 2) * rows * n * k
     b, m, n, k = dims
     # the SwiGLU kernel runs the gate and up projections over the same A

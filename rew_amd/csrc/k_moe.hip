@@ -16,7 +16,9 @@
 //                     never depends on timing;
 //   (grouped SwiGLU and down-projection GEMMs over the packed rows, k_gemm.hip)
 //   moe_combine_kernel per token: start from the running sum before the
-//                     first routed expert, then for the token's routed
+//                     first routed expert (the caller's rows, or the shared
+//                     experts' outputs added in order with bf16 rounding
+//                     after each add), then for the token's routed
 //                     members in chain order add bf16(f32(y) * w) with bf16
 //                     rounding after every add -- the dense op sequence's
 //                     arithmetic on the only rows where it is non-zero.
@@ -315,6 +317,20 @@ __global__ void __launch_bounds__(256) moe_combine_kernel(MoeCombineArgs a) {
           acc1[x] = vm::as_f((uint32_t)x1[x] << 16);
         }
       }
+      // the later shared experts' rows: out = bf16(out + row), as the
+      // residual epilogue of rew's chain add
+#pragma unroll 1
+      for (int s = 1; s < a.n_prev; ++s) {
+        const uint4 q0 = *(const uint4*)(prow + s * a.prev_sb + h0);
+        const uint4 q1 = *(const uint4*)(prow + s * a.prev_sb + h1);
+        const uint16_t* x0 = (const uint16_t*)&q0;
+        const uint16_t* x1 = (const uint16_t*)&q1;
+#pragma unroll
+        for (int x = 0; x < 8; ++x) {
+          acc0[x] = vm::round_bf16(acc0[x] + vm::as_f((uint32_t)x0[x] << 16));
+          acc1[x] = vm::round_bf16(acc1[x] + vm::as_f((uint32_t)x1[x] << 16));
+        }
+      }
       auto add = [&](const uint4& y0, const uint4& y1, float wgt) {
         const uint16_t* a0 = (const uint16_t*)&y0;
         const uint16_t* a1 = (const uint16_t*)&y1;
@@ -401,8 +417,8 @@ int launch_moe_route(const MoeRouteArgs& a, hipStream_t stream) {
 
 void launch_moe_combine(const MoeCombineArgs& a, hipStream_t stream) {
   if (a.T == 0) return;
-  if (a.H % 8 || a.prev_rs % 8 || ((uintptr_t)a.prev & 15) || ((uintptr_t)a.y & 15) ||
-      ((uintptr_t)a.out & 15) || a.k < 1 || a.k > kMoeMaxK)
+  if (a.H % 8 || a.prev_rs % 8 || a.prev_sb % 8 || a.n_prev < 1 || ((uintptr_t)a.prev & 15) ||
+      ((uintptr_t)a.y & 15) || ((uintptr_t)a.out & 15) || a.k < 1 || a.k > kMoeMaxK)
     fail(REW_MI355X_ERR_INVALID, "internal: MoE combine launch outside its limits");
   const int64_t blocks = (a.T + 3) / 4;
   const dim3 grid((unsigned)(blocks < 65536 ? blocks : 65536));

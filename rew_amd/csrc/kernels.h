@@ -394,11 +394,15 @@ struct MoeRouteArgs {
 constexpr int kMoeRouteBlock = 256;  // tokens per routing workgroup
 int launch_moe_route(const MoeRouteArgs& a, hipStream_t stream);  // returns the launches
 
-// out[t, :] = prev[t, :] then, for token t's routed members in chain order,
-// out = bf16(out + bf16(f32(y[slot, :]) * w)); bf16 rows, H % 8 == 0.
+// out[t, :] = prev[t, :], then out = bf16(out + prev[s prev_sb + t, :]) for
+// s = 1 .. n_prev - 1 (the shared experts' running sum), then, for token
+// t's routed members in chain order, out = bf16(out + bf16(f32(y[slot, :]) *
+// w)); bf16 rows, H % 8 == 0.
 struct MoeCombineArgs {
   const uint16_t* prev;
   int64_t prev_rs;           // row stride of prev (elements)
+  int n_prev = 1;            // prev rows folded per token
+  int64_t prev_sb = 0;       // elements from one folded prev row set to the next
   const uint16_t* y;         // [T * k, H] packed expert outputs
   const int32_t* ord_slot;   // [T, k] from the placement
   const float* ord_w;        // [T, k]

@@ -14,7 +14,8 @@
 //                                       ceil(T / 256) token blocks)
 //   hbuf      [R, I] bf16  SwiGLU outputs of the routed rows
 //   ybuf      [R, H] bf16  down-projection outputs of the routed rows
-// with R = T k routed rows.  Every byte a kernel reads is written earlier
+// with R = T k routed rows (with shared experts both hold their T rows
+// each after the routed rows: R + n_shared T).  Every byte a kernel reads is written earlier
 // in the same sequence, so nothing has to start at zero.
 #include <hip/hip_runtime.h>
 
@@ -58,12 +59,11 @@ __global__ void __launch_bounds__(256) moe_meta_kernel(MoeMetaChunk ch, int E, i
 namespace {
 
 struct Layout {
-  size_t member_of, members, tables, route, hbuf, ybuf, sbuf, total;
+  size_t member_of, members, tables, route, hbuf, ybuf, total;
 };
 
 // (with shared experts: their table entries follow the members', their
-// hidden rows the routed rows in hbuf, and sbuf holds two [T, H] running
-// sums of their outputs)
+// hidden and output rows the routed rows in hbuf and ybuf)
 Layout layout_of(const RoutedFfn& a) {
   auto up = [](size_t b) { return (b + 255) & ~(size_t)255; };
   const size_t R = (size_t)a.T * (size_t)a.k, ns = (size_t)a.n_shared;
@@ -82,15 +82,15 @@ Layout layout_of(const RoutedFfn& a) {
   L.hbuf = o;
   o += up((R + ns * (size_t)a.T) * (size_t)a.I * 2);
   L.ybuf = o;
-  o += up(R * (size_t)a.H * 2);
-  L.sbuf = o;
-  if (ns) o += 2 * up((size_t)a.T * (size_t)a.H * 2);
+  o += up((R + ns * (size_t)a.T) * (size_t)a.H * 2);
   L.total = o;
   return L;
 }
 
 // The two grouped GEMMs: SwiGLU over x's routed rows, down projection over
-// the packed hidden rows (operand tables and outputs filled in by the caller).
+// the packed hidden rows, each with the shared experts' groups of all T
+// tokens after the members' (operand tables and outputs filled in by the
+// caller).
 void gemm_args(const RoutedFfn& a, GemmArgs* gs, GemmArgs* gd) {
   *gs = GemmArgs{};
   *gd = GemmArgs{};
@@ -109,7 +109,7 @@ void gemm_args(const RoutedFfn& a, GemmArgs* gs, GemmArgs* gd) {
   gs->b_sk = a.I;
   gs->c_sm = a.I;
   gs->epi = EPI_SWIGLU;
-  gd->M = a.T * a.k;
+  gd->M = a.T * ((int64_t)a.k + a.n_shared);
   gd->K = a.I;
   gd->N = a.H;
   gd->a_sm = a.I;
@@ -119,37 +119,6 @@ void gemm_args(const RoutedFfn& a, GemmArgs* gs, GemmArgs* gd) {
 }
 
 bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
-
-// Shared expert i's down projection: its SwiGLU rows (dense [T, I]) times
-// its down weight plus bias, plus the running sum of the earlier shared
-// experts (res) after the first -- the fused GEMM epilogues of the
-// separate launches.
-GemmArgs shared_down_args(const RoutedFfn& a, int i, const void* hrows, const void* res,
-                          void* out) {
-  GemmArgs g{};
-  g.dtype = REW_DT_BFLOAT16;
-  g.c_dtype = REW_DT_BFLOAT16;
-  g.batch = 1;
-  g.a = hrows;
-  g.a_sm = a.I;
-  g.a_sk = 1;
-  g.b = a.sptr[4][i];
-  g.b_sk = a.H;
-  g.b_sn = 1;
-  g.M = a.T;
-  g.K = a.I;
-  g.N = a.H;
-  g.c = out;
-  g.c_sm = a.H;
-  g.c_sb = a.T * a.H;
-  g.bias = a.sptr[5][i];
-  g.epi = i == 0 ? EPI_BIAS : EPI_BIAS_RES;
-  if (i > 0) {
-    g.res = res;
-    g.res_sm = a.H;
-  }
-  return g;
-}
 
 }  // namespace
 
@@ -207,10 +176,6 @@ void routed_ffn_check(const RoutedFfn& a) {
   gd.c = rows;
   if (!gemm_grouped_ok(gs) || !gemm_grouped_ok(gd))
     bad("the expert GEMMs exceed the grouped kernel's 32-bit operand extents");
-  for (int i = 0; i < a.n_shared; ++i) {
-    GemmArgs g = shared_down_args(a, i, rows, rows, rows);
-    if (!gemm_epilogue_ok(g)) bad("the shared experts' down GEMMs cannot run with their epilogues");
-  }
 }
 
 void run_routed_ffn(Ctx* c, const RoutedFfn& a, void* scratch) {
@@ -299,26 +264,8 @@ void run_routed_ffn(Ctx* c, const RoutedFfn& a, void* scratch) {
   }
   launch_gemm_grouped(gs, ga, c->stream);
   prof_end(c);
-  // the shared experts' running sum, [T, H] in sbuf (two buffers in turn)
-  const void* prev = a.start;
-  int64_t prev_rs = a.start_rs;
-  for (int i = 0; i < ns; ++i) {
-    void* dst = s + L.sbuf + (size_t)(i & 1) * ((((size_t)a.T * a.H * 2) + 255) & ~(size_t)255);
-    const GemmArgs g = shared_down_args(
-        a, i, s + L.hbuf + (size_t)(R + (int64_t)i * a.T) * a.I * 2, prev, dst);
-    if (c->profiling) {
-      char nm[160];
-      std::snprintf(nm, sizeof nm, "moe_shared_down%s[1,%lld,%lld,%lld]",
-                    i ? "+bias+res" : "+bias", (long long)a.T, (long long)a.H, (long long)a.I);
-      prof_begin(c, nm);
-    }
-    launch_gemm(g, c->stream);
-    prof_end(c);
-    prev = dst;
-    prev_rs = a.H;
-  }
-  ga.n_groups = n;
-  ga.max_mtiles = (R + 255) / 256 + 2 * n;
+  // the down launch: the members' and the shared experts' groups again,
+  // over the packed hidden rows, each output row a bias epilogue
   ga.rows = nullptr;
   ga.b = tables + 4 * groups;
   ga.b2 = nullptr;
@@ -326,16 +273,25 @@ void run_routed_ffn(Ctx* c, const RoutedFfn& a, void* scratch) {
   ga.bias2 = nullptr;
   if (c->profiling) {
     char nm[160];
-    std::snprintf(nm, sizeof nm, "moe_gemm_down[%d,%lld,%lld,%lld]", n, (long long)R,
+    std::snprintf(nm, sizeof nm, "moe_gemm_down[%d,%lld,%lld,%lld]", groups, (long long)RS,
                   (long long)a.H, (long long)a.I);
     prof_begin(c, nm);
   }
   launch_gemm_grouped(gd, ga, c->stream);
   prof_end(c);
 
+  // the combine starts from the shared experts' outputs (rew's running
+  // sum, each add rounded) or, without them, from the caller's start rows
   MoeCombineArgs ca;
-  ca.prev = (const uint16_t*)prev;
-  ca.prev_rs = prev_rs;
+  if (ns) {
+    ca.prev = (const uint16_t*)(s + L.ybuf) + (size_t)R * a.H;
+    ca.prev_rs = a.H;
+  } else {
+    ca.prev = (const uint16_t*)a.start;
+    ca.prev_rs = a.start_rs;
+  }
+  ca.n_prev = ns ? ns : 1;
+  ca.prev_sb = a.T * a.H;
   ca.y = (const uint16_t*)gd.c;
   ca.ord_slot = ra.ord_slot;
   ca.ord_w = ra.ord_w;
@@ -347,7 +303,7 @@ void run_routed_ffn(Ctx* c, const RoutedFfn& a, void* scratch) {
     prof_begin(c, "moe_combine{" + std::to_string(a.T) + "x" + std::to_string(a.H) + "}");
   launch_moe_combine(ca, c->stream);
   prof_end(c);
-  c->stats.kernels_launched += route_launches + 3 + ns + (groups + kMetaChunk - 1) / kMetaChunk;
+  c->stats.kernels_launched += route_launches + 3 + (groups + kMetaChunk - 1) / kMetaChunk;
   c->stats.fused_groups += 4;
 }
 

@@ -109,11 +109,13 @@ def test_moe_matches_oracle(gpu, oracle, T, H, I, E_, k, n_shared):
     prof = [name for name, _, _ in E.profileEnd()]
     assert any(n.startswith("moe_gemm_swiglu") for n in prof), prof
     assert any(n.startswith("moe_combine") for n in prof), prof
-    # the shared experts belong to the group: their SwiGLU GEMMs are groups
-    # of all T rows in the members' grouped launch, their down GEMMs follow
+    # the shared experts belong to the group: their SwiGLU and down GEMMs
+    # are groups of all T rows in the members' two grouped launches
     sw = [n for n in prof if "swiglu" in n]
     assert sw == [f"moe_gemm_swiglu[{E_ + n_shared},{T * k + n_shared * T},{I},{H}]"], prof
-    assert sum(n.startswith("moe_shared_down") for n in prof) == n_shared, prof
+    dn = [n for n in prof if n.startswith("moe_gemm_down")]
+    assert dn == [f"moe_gemm_down[{E_ + n_shared},{T * k + n_shared * T},{H},{I}]"], prof
+    assert not any(n.startswith("moe_shared_down") for n in prof), prof
     want, ti, tw = oracle.deepseek_moe(host["x"], host["shared"], host["routed"], host["wr"],
                                        host["br"], k)
     err = np.linalg.norm(out - want) / np.linalg.norm(want)
