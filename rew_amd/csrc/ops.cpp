@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <cctype>
 #include <cstdlib>
+#include <cstring>
 #include <unordered_map>
 
 #include "kernels.h"
@@ -116,9 +117,7 @@ static const std::unordered_map<std::string, OpSpec>& op_table() {
 // does not implement natively.
 static bool known_but_unimplemented(const std::string& n) {
   static const char* names[] = {
-      "complex", "real", "imag", "conv2d", "maxPool2d", "dynamicPad",
-      "realDynamicSlice", "dynamicBroadcastInDim", "fft", "triangularSolve",
-      "einsum", "unaryEinsum"};
+      "complex", "real", "imag", "conv2d", "maxPool2d", "fft", "triangularSolve"};
   for (auto* s : names)
     if (n == s) return true;
   return false;
@@ -1050,9 +1049,272 @@ std::vector<Tensor*> commit_node(Ctx* c, Node* n, const std::vector<Tensor*>& in
   return result;
 }
 
+std::vector<Tensor*> record_op(Ctx* c, const std::string& op, const std::vector<Tensor*>& ins,
+                               const Attrs& attrs);
+
+static std::string int_list_text(const std::vector<int64_t>& v) {
+  std::string s = "[";
+  for (size_t i = 0; i < v.size(); ++i) s += (i ? "," : "") + std::to_string(v[i]);
+  return s + "]";
+}
+
+// rew's einsum / unaryEinsum (src/rew/ops/linalg.nim:378-430; their eager
+// attrs einsum_config and output_shape, eager.nim:1495-1502) recorded as
+// primitive nodes.  TensorFlow's einsum grammar with an explicit "->",
+// letters as labels (no ellipsis, no label repeated within one operand):
+//   * labels of one operand that reach neither the other operand nor the
+//     output are summed out first (reduceSum);
+//   * one dotGeneral then batches the labels both operands and the output
+//     hold and contracts those only the operands share;
+//   * a transpose puts the dot's [batch, lhs-only, rhs-only] order (or a
+//     unary einsum's remaining order) into the output's.
+static std::vector<Tensor*> record_einsum(Ctx* c, const std::string& op,
+                                          const std::vector<Tensor*>& ins, const Attrs& attrs) {
+  const bool unary = op == "unaryEinsum";
+  const size_t nin = unary ? 1 : 2;
+  if (ins.size() != nin)
+    invalid("eager '" + op + "': expected " + std::to_string(nin) + " operand(s), got " +
+            std::to_string(ins.size()));
+  std::string cfg = find_attr(attrs, "einsum_config", op);
+  std::string sp;
+  for (char ch : cfg)
+    if (ch != ' ') sp.push_back(ch);
+  const size_t arrow = sp.find("->");
+  if (sp.empty() || arrow == std::string::npos)
+    fail(REW_MI355X_ERR_UNSUPPORTED, "eager '" + op + "': config '" + cfg +
+                                         "' needs an explicit '->' output");
+  if (sp.find("...") != std::string::npos)
+    fail(REW_MI355X_ERR_UNSUPPORTED, "eager '" + op + "': ellipsis labels are not supported");
+  std::vector<std::string> in_spec;
+  {
+    const std::string lhs = sp.substr(0, arrow);
+    size_t b = 0;
+    for (;;) {
+      const size_t e = lhs.find(',', b);
+      in_spec.push_back(lhs.substr(b, e == std::string::npos ? std::string::npos : e - b));
+      if (e == std::string::npos) break;
+      b = e + 1;
+    }
+  }
+  const std::string out_spec = sp.substr(arrow + 2);
+  if (in_spec.size() != nin)
+    invalid("eager '" + op + "': config '" + cfg + "' names " + std::to_string(in_spec.size()) +
+            " operand(s)");
+  auto check_spec = [&](const std::string& s, const char* what) {
+    for (size_t i = 0; i < s.size(); ++i) {
+      if (!std::isalpha((unsigned char)s[i]))
+        invalid("eager '" + op + "': bad label '" + std::string(1, s[i]) + "' in " + what);
+      if (s.find(s[i]) != i)
+        fail(REW_MI355X_ERR_UNSUPPORTED, "eager '" + op + "': label '" + std::string(1, s[i]) +
+                                             "' repeated in " + what);
+    }
+  };
+  for (size_t i = 0; i < nin; ++i) {
+    check_spec(in_spec[i], "an operand");
+    if ((int)in_spec[i].size() != ins[i]->shape.rank)
+      invalid("eager '" + op + "': operand " + std::to_string(i) + " has rank " +
+              std::to_string(ins[i]->shape.rank) + ", config '" + cfg + "' gives it " +
+              std::to_string(in_spec[i].size()) + " label(s)");
+  }
+  check_spec(out_spec, "the output");
+  if (!unary && ins[0]->dt != ins[1]->dt)
+    invalid(std::string("eager 'einsum': dtype mismatch (") + dt_enum_name(ins[0]->dt) + " vs " +
+            dt_enum_name(ins[1]->dt) + ")");
+  // label sizes agree across operands
+  int64_t size_of[128];
+  for (auto& v : size_of) v = -1;
+  for (size_t i = 0; i < nin; ++i)
+    for (size_t k = 0; k < in_spec[i].size(); ++k) {
+      const int ch = (unsigned char)in_spec[i][k];
+      const int64_t d = ins[i]->shape.d[k];
+      if (size_of[ch] >= 0 && size_of[ch] != d)
+        invalid("eager '" + op + "': label '" + std::string(1, (char)ch) + "' sizes " +
+                std::to_string(size_of[ch]) + " and " + std::to_string(d));
+      size_of[ch] = d;
+    }
+  for (char ch : out_spec)
+    if (size_of[(unsigned char)ch] < 0)
+      invalid("eager '" + op + "': output label '" + std::string(1, ch) + "' is in no operand");
+  const std::vector<int64_t> want = parse_int_list(find_attr(attrs, "output_shape", op), op);
+
+  std::vector<Tensor*> owned;  // intermediate results (one reference each)
+  auto release = [&]() {
+    for (Tensor* t : owned) {
+      t->ext--;
+      maybe_destroy(t);
+    }
+    owned.clear();
+  };
+  auto run1 = [&](const std::string& name, const std::vector<Tensor*>& xs,
+                  const Attrs& a) -> Tensor* {
+    std::vector<Tensor*> r = record_op(c, name, xs, a);
+    owned.push_back(r[0]);
+    return r[0];
+  };
+  try {
+    std::vector<Tensor*> x(ins.begin(), ins.end());
+    std::vector<std::string> lab(in_spec.begin(), in_spec.end());
+    for (size_t i = 0; i < nin; ++i) {
+      const std::string other = nin == 2 ? lab[1 - i] : std::string();
+      std::vector<int64_t> dims;
+      std::string keep;
+      for (size_t k = 0; k < lab[i].size(); ++k) {
+        const char ch = lab[i][k];
+        if (out_spec.find(ch) == std::string::npos && other.find(ch) == std::string::npos)
+          dims.push_back((int64_t)k);
+        else
+          keep.push_back(ch);
+      }
+      if (!dims.empty()) {
+        x[i] = run1("reduceSum", {x[i]}, {{"dims", int_list_text(dims)}});
+        lab[i] = keep;
+      }
+    }
+    std::string cur;  // labels of the running result, in order
+    Tensor* y;
+    if (unary) {
+      y = x[0];
+      cur = lab[0];
+    } else {
+      std::vector<int64_t> lb, rb, lc, rc;
+      std::string batch, lfree, rfree;
+      for (size_t k = 0; k < lab[0].size(); ++k) {
+        const char ch = lab[0][k];
+        const size_t j = lab[1].find(ch);
+        if (j == std::string::npos) {
+          lfree.push_back(ch);
+        } else if (out_spec.find(ch) != std::string::npos) {
+          lb.push_back((int64_t)k);
+          rb.push_back((int64_t)j);
+          batch.push_back(ch);
+        } else {
+          lc.push_back((int64_t)k);
+          rc.push_back((int64_t)j);
+        }
+      }
+      for (char ch : lab[1])
+        if (lab[0].find(ch) == std::string::npos) rfree.push_back(ch);
+      y = run1("dotGeneral", {x[0], x[1]},
+               {{"lhs_batching", int_list_text(lb)}, {"rhs_batching", int_list_text(rb)},
+                {"lhs_contracting", int_list_text(lc)}, {"rhs_contracting", int_list_text(rc)}});
+      cur = batch + lfree + rfree;
+    }
+    if (cur.size() != out_spec.size())
+      invalid("eager '" + op + "': config '" + cfg + "' leaves labels '" + cur +
+              "' for output '" + out_spec + "'");
+    std::vector<int64_t> perm;
+    bool ident = true;
+    for (size_t k = 0; k < out_spec.size(); ++k) {
+      const size_t j = cur.find(out_spec[k]);
+      perm.push_back((int64_t)j);
+      ident = ident && j == k;
+    }
+    if (!ident) y = run1("transpose", {y}, {{"permutation", int_list_text(perm)}});
+    if (y->shape.rank != (int)want.size())
+      invalid("eager '" + op + "': output_shape " + int_list_text(want) + " but the config gives " +
+              y->shape.str());
+    for (int k = 0; k < y->shape.rank; ++k)
+      if (y->shape.d[k] != want[k])
+        invalid("eager '" + op + "': output_shape " + int_list_text(want) +
+                " but the config gives " + y->shape.str());
+    y->ext++;  // (an identity unary einsum hands back the operand, one more reference)
+    release();
+    return {y};
+  } catch (...) {
+    release();
+    throw;
+  }
+}
+
+// The values of an integer vector operand of length n, read back from the
+// device (the pending graph is flushed first, as rew_mi355x_to_host does).
+static std::vector<int64_t> read_index_vector(Ctx* c, Tensor* t, const std::string& op,
+                                              const char* what, size_t n) {
+  if (!dt_is_int(t->dt) || t->shape.rank != 1 || t->shape.d[0] != (int64_t)n)
+    invalid("eager '" + op + "': " + what + " must be an integer vector of length " +
+            std::to_string(n));
+  if (t->prod) flush(c);
+  if (!t->st) invalid("eager '" + op + "': " + what + " has no data (an earlier flush failed)");
+  std::vector<uint8_t> raw((size_t)t->nbytes());
+  if (!raw.empty()) {
+    REW_HIP(hipMemcpyAsync(raw.data(), t->data(), raw.size(), hipMemcpyDeviceToHost, c->stream));
+    REW_HIP(hipStreamSynchronize(c->stream));
+  }
+  std::vector<int64_t> v(n);
+  const int w = dt_size(t->dt);
+  const bool sgn = t->dt == kI8 || t->dt == kI16 || t->dt == kI32 || t->dt == kI64;
+  for (size_t i = 0; i < n; ++i) {
+    uint64_t u = 0;
+    std::memcpy(&u, raw.data() + i * w, (size_t)w);
+    if (sgn && w < 8 && (u >> (8 * w - 1)) & 1) u |= ~0ull << (8 * w);
+    v[i] = (int64_t)u;
+  }
+  return v;
+}
+
+// The shape-operand ops rew dispatches with a static result_shape
+// (src/rew/ops/shape.nim:395-441 dynamicPad, 477-517 realDynamicSlice;
+// src/rew/ops/linalg.nim:288-326 dynamicBroadcastInDim) as their static
+// forms.  The broadcast's output-dimensions operand only restates the
+// result shape and is not read; the padding and slice bounds are read back
+// from the device (a synchronising read) and the static pad / slice runs.
+static std::vector<Tensor*> record_dynamic_shape_op(Ctx* c, const std::string& op,
+                                                    const std::vector<Tensor*>& ins,
+                                                    const Attrs& attrs) {
+  const std::vector<int64_t> rs = parse_int_list(find_attr(attrs, "result_shape", op), op);
+  auto need = [&](size_t n) {
+    if (ins.size() != n)
+      invalid("eager '" + op + "': expected " + std::to_string(n) + " operand(s), got " +
+              std::to_string(ins.size()));
+  };
+  std::vector<Tensor*> r;
+  if (op == "dynamicBroadcastInDim") {
+    need(2);
+    if (!dt_is_int(ins[1]->dt) || ins[1]->shape.rank != 1 ||
+        ins[1]->shape.d[0] != (int64_t)rs.size())
+      invalid("eager 'dynamicBroadcastInDim': outputDimensions must be an integer vector of "
+              "length " + std::to_string(rs.size()));
+    r = record_op(c, "broadcastTo", {ins[0]},
+                  {{"output_shape", int_list_text(rs)},
+                   {"broadcast_dimensions", find_attr(attrs, "broadcast_dimensions", op)}});
+  } else if (op == "dynamicPad") {
+    need(5);
+    const size_t rank = (size_t)ins[0]->shape.rank;
+    const auto lo = read_index_vector(c, ins[2], op, "edgePaddingLow", rank);
+    const auto hi = read_index_vector(c, ins[3], op, "edgePaddingHigh", rank);
+    const auto in = read_index_vector(c, ins[4], op, "interiorPadding", rank);
+    r = record_op(c, "pad", {ins[0], ins[1]},
+                  {{"edge_padding_low", int_list_text(lo)}, {"edge_padding_high", int_list_text(hi)},
+                   {"interior_padding", int_list_text(in)}});
+  } else {  // realDynamicSlice
+    need(4);
+    const size_t rank = (size_t)ins[0]->shape.rank;
+    const auto st = read_index_vector(c, ins[1], op, "startIndices", rank);
+    const auto li = read_index_vector(c, ins[2], op, "limitIndices", rank);
+    const auto sd = read_index_vector(c, ins[3], op, "strides", rank);
+    r = record_op(c, "slice", {ins[0]},
+                  {{"start_indices", int_list_text(st)}, {"limit_indices", int_list_text(li)},
+                   {"strides", int_list_text(sd)}});
+  }
+  const Shape& got = r[0]->shape;
+  bool ok = got.rank == (int)rs.size();
+  for (int k = 0; ok && k < got.rank; ++k) ok = got.d[k] == rs[k];
+  if (!ok) {
+    const std::string gs = got.str();
+    r[0]->ext--;
+    maybe_destroy(r[0]);
+    invalid("eager '" + op + "': result_shape " + int_list_text(rs) + " but the operands give " +
+            gs);
+  }
+  return r;
+}
+
 std::vector<Tensor*> record_op(Ctx* c, const std::string& op,
                                const std::vector<Tensor*>& ins,
                                const Attrs& attrs) {
+  if (op == "einsum" || op == "unaryEinsum") return record_einsum(c, op, ins, attrs);
+  if (op == "dynamicPad" || op == "realDynamicSlice" || op == "dynamicBroadcastInDim")
+    return record_dynamic_shape_op(c, op, ins, attrs);
   std::vector<std::pair<int, Shape>> outs;
   Node* n = prepare_node(c, op, ins, attrs, &outs);
   return commit_node(c, n, ins, outs);

@@ -32,6 +32,7 @@
 #include <memory>
 #include <string>
 #include <unordered_map>
+#include <unordered_set>
 #include <vector>
 
 #include "kernels.h"
@@ -128,6 +129,7 @@ class Parser {
   size_t p_ = 0;
   std::string who_;
   std::unordered_map<std::string, int> names_;
+  std::unordered_set<std::string> rew_alias_;  // names registered by rew_result_names
   int next_slot_ = 0;
 
   int line_at(size_t p) const {
@@ -214,10 +216,27 @@ class Parser {
     return it->second;
   }
   int define(const std::string& nm) {
-    if (names_.count(nm)) err("redefinition of %" + nm);
+    if (names_.count(nm) && !rew_alias_.count(nm)) err("redefinition of %" + nm);
+    rew_alias_.erase(nm);
     const int s = next_slot_++;
-    names_.emplace(nm, s);
+    names_[nm] = s;
     return s;
+  }
+  // rew's emitter prints a multi-result if / while as `%vN:K = ...` but then
+  // names result i by its own id, %v(N+i) (text.nim:995-1001, 1106-1111 with
+  // valueRef); those names are registered too, unless the text defines them
+  // itself later.
+  void rew_result_names(const std::string& base, const std::vector<int>& res) {
+    if (base.size() < 2 || base[0] != 'v') return;
+    for (size_t i = 1; i < base.size(); ++i)
+      if (!std::isdigit((unsigned char)base[i])) return;
+    const long long n0 = std::atoll(base.c_str() + 1);
+    for (size_t i = 0; i < res.size(); ++i) {
+      const std::string nm = "v" + std::to_string(n0 + (long long)i);
+      if (names_.count(nm)) continue;
+      names_.emplace(nm, res[i]);
+      rew_alias_.insert(nm);
+    }
   }
   int64_t integer() {
     ws();
@@ -486,10 +505,12 @@ class Parser {
     }
     // results
     std::vector<std::string> names;
+    std::vector<std::pair<std::string, size_t>> groups;  // %nm:K, first index
     for (;;) {
       std::string nm = value_name();
       if (eat(":")) {
         const int64_t k = integer();
+        groups.push_back({nm, names.size()});
         for (int64_t i = 0; i < k; ++i) names.push_back(nm + "#" + std::to_string(i));
       } else {
         names.push_back(nm);
@@ -505,6 +526,12 @@ class Parser {
           "lists " + std::to_string(op.res_ty.size()));
     // results are defined after the operands (and region values) were used
     for (auto& nm : names) op.res.push_back(define(nm));
+    for (auto& g : groups) {
+      std::vector<int> rs;
+      for (size_t i = g.second; i < names.size() && names[i].rfind(g.first + "#", 0) == 0; ++i)
+        rs.push_back(op.res[i]);
+      rew_result_names(g.first, rs);
+    }
     ops->push_back(std::move(op));
   }
 
@@ -701,10 +728,25 @@ class Parser {
 
 // ---- translated form ----------------------------------------------------------------
 
+struct Step;
+// A region of a control-flow op: its argument slots, its steps and the
+// slots its stablehlo.return hands back.
+struct Block {
+  std::vector<int> args;
+  std::vector<Step> steps;
+  std::vector<int> ret;
+};
+enum StepKind : int { kStepNode = 0, kStepWhile = 1, kStepIf = 2, kStepCase = 3 };
 struct Step {
   Node proto;  // prepared node: typed attributes set, no operands
   std::vector<int> in, out;
   std::vector<std::pair<int, Shape>> outs;
+  // control flow (kind != kStepNode): `in` holds the op's n_opnd operands
+  // (while: the initial carry; if / case: the predicate / branch index),
+  // then every slot the regions read from outside them (for liveness)
+  int kind = kStepNode;
+  int n_opnd = 0;
+  std::vector<Block> blocks;
 };
 
 }  // namespace
@@ -717,6 +759,7 @@ struct JitModule {
   std::vector<std::pair<int, Tensor*>> consts;  // slot, tensor (one reference each)
   std::vector<Step> steps;
   std::vector<int> ret;
+  bool has_control = false;  // while / if / case steps (run host-side per call)
   int64_t calls = 0;
   // direct plans (plan.h) by input key, for modules of at least
   // kDirectMinSteps steps called with nothing else pending
@@ -871,8 +914,10 @@ class Translator {
     for (size_t i = 0; i < f.ops.size(); ++i)
       for (int r : f.ops[i].res) def_op_[r] = (int)i;
     uses_.assign(n_parsed_slots, {});
-    for (size_t i = 0; i < f.ops.size(); ++i)
+    for (size_t i = 0; i < f.ops.size(); ++i) {
       for (int a : f.ops[i].arg) uses_[a].push_back((int)i);
+      for (const auto& r : f.ops[i].regions) region_uses(r);
+    }
     ret_use_.assign(n_parsed_slots, false);
     for (int r : f.ret) ret_use_[r] = true;
     redirect_.assign(f.ops.size(), -1);
@@ -907,6 +952,15 @@ class Translator {
   std::vector<bool> ret_use_;
   std::vector<Tensor*> phantoms_;
   std::unordered_map<std::string, std::pair<int, int>> topk_;  // (x, k, largest) -> slots
+
+  // uses inside regions count as -1 (no peephole looks into a region)
+  void region_uses(const std::vector<Op>& ops) {
+    for (const Op& o : ops) {
+      for (int a : o.arg)
+        if (a >= 0 && a < (int)uses_.size()) uses_[a].push_back(-1);
+      for (const auto& r : o.regions) region_uses(r);
+    }
+  }
 
   [[noreturn]] void fail_at(const Op& o, const std::string& m, int code = REW_MI355X_ERR_INVALID) {
     fail(code, who_ + ": line " + std::to_string(o.line) + ": " + o.name + ": " + m);
@@ -1191,6 +1245,7 @@ class Translator {
     for (size_t r = 0; r < o.res.size(); ++r) {
       if (ret_use_[o.res[r]]) return false;
       for (int u : uses_[o.res[r]]) {
+        if (u < 0) return false;  // read inside a region
         const int64_t kk = head_slice(u, dim, xs);
         if (kk <= 0 || (k >= 0 && kk != k)) return false;
         k = kk;
@@ -1311,7 +1366,7 @@ class Translator {
 
   void op(const Op& o, int index) {
     const std::string& n = o.name;
-    if (redirect_[index] >= 0) {  // a slice the topK peephole answers
+    if (index >= 0 && redirect_[index] >= 0) {  // a slice the topK peephole answers
       bind(o, 0, redirect_[index]);
       return;
     }
@@ -1412,6 +1467,8 @@ class Translator {
       // (src/rew/stablehlo/text.nim:671-690)
       if (o.arg.size() < 3 || o.res_ty.size() != 1) fail_at(o, "malformed dynamic_update_slice");
       one(o, "dynamicUpdateSlice", o.arg, {});
+    } else if (n == "stablehlo.while" || n == "stablehlo.if" || n == "stablehlo.case") {
+      control(o);
     } else if (n == "stablehlo.gather") {
       gather(o);
     } else if (n == "stablehlo.scatter") {
@@ -1419,6 +1476,138 @@ class Translator {
     } else {
       fail_at(o, "op not supported by the mi355x jit path", REW_MI355X_ERR_UNSUPPORTED);
     }
+  }
+
+  // ---- control flow (src/rew/transform/control.nim: cond / whileLoop / fori
+  // trace stablehlo.if and stablehlo.while; the text is text.nim's emitIf /
+  // emitWhile).  Each region is translated into a Block over the module's
+  // slots; the call runs the regions on the host side (instantiate), reading
+  // each predicate back from the device, as PJRT's executable does.
+
+  // The region's ops as a Block whose argument slots carry `types`.
+  Block block(const Op& o, size_t r, const std::vector<std::pair<int, Shape>>& types) {
+    const auto& args = o.region_args.at(r);
+    if (args.size() != types.size())
+      fail_at(o, "region " + std::to_string(r) + " takes " + std::to_string(args.size()) +
+                     " argument(s), expected " + std::to_string(types.size()));
+    Block b;
+    for (size_t i = 0; i < args.size(); ++i) {
+      set_slot(args[i], types[i].first, types[i].second);
+      b.args.push_back(args[i]);
+    }
+    std::vector<Step> saved;
+    saved.swap(m_->steps);
+    bool returned = false;
+    for (const Op& ro : o.regions[r]) {
+      if (returned) fail_at(ro, "op after the region's stablehlo.return");
+      if (ro.name == "stablehlo.return") {
+        for (int a : ro.arg) b.ret.push_back(resolve(a));
+        returned = true;
+        continue;
+      }
+      op(ro, -1);
+    }
+    b.steps.swap(m_->steps);
+    m_->steps.swap(saved);
+    if (!returned) fail_at(o, "region " + std::to_string(r) + " has no stablehlo.return");
+    return b;
+  }
+
+  // The region's results have the types `types`.
+  void check_ret(const Op& o, const Block& b, size_t r,
+                 const std::vector<std::pair<int, Shape>>& types) {
+    if (b.ret.size() != types.size())
+      fail_at(o, "region " + std::to_string(r) + " returns " + std::to_string(b.ret.size()) +
+                     " value(s), expected " + std::to_string(types.size()));
+    for (size_t i = 0; i < types.size(); ++i)
+      if (slot_dt_[b.ret[i]] != types[i].first || slot_shape_[b.ret[i]] != types[i].second)
+        fail_at(o, "region " + std::to_string(r) + " result " + std::to_string(i) + " is " +
+                       type_text(slot_dt_[b.ret[i]], slot_shape_[b.ret[i]]) + ", expected " +
+                       type_text(types[i].first, types[i].second));
+  }
+
+  // Slots a block reads that it does not define (outer values it captures).
+  static void captured(const Block& b, std::vector<int>* out) {
+    std::vector<int> defined(b.args.begin(), b.args.end());
+    auto is_def = [&](int s) {
+      for (int d : defined)
+        if (d == s) return true;
+      return false;
+    };
+    auto need = [&](int s) {
+      if (is_def(s)) return;
+      for (int x : *out)
+        if (x == s) return;
+      out->push_back(s);
+    };
+    for (const Step& st : b.steps) {
+      for (int s : st.in) need(s);
+      for (int s : st.out) defined.push_back(s);
+    }
+    for (int s : b.ret) need(s);
+  }
+
+  void control(const Op& o) {
+    const std::string& n = o.name;
+    Step st;
+    std::vector<std::pair<int, Shape>> res_types;
+    for (const Ty& t : o.res_ty) {
+      if (t.dt < 0) fail_at(o, "result type " + t.text + " not supported", REW_MI355X_ERR_UNSUPPORTED);
+      res_types.push_back({t.dt, Shape(t.d)});
+    }
+    if (o.res.size() != res_types.size()) fail_at(o, "result count mismatch");
+    auto scalar = [&](int s, int dt, const char* what) {
+      s = resolve(s);
+      if (slot_dt_[s] != dt || slot_shape_[s].rank != 0)
+        fail_at(o, std::string(what) + " must be a " + dt_enum_name(dt) + " scalar, got " +
+                       type_text(slot_dt_[s], slot_shape_[s]));
+    };
+    if (n == "stablehlo.while") {
+      // "stablehlo.while"(%init...) ({^cond(...): ... return(%pred)}, {^body(...): ...
+      // return(%next...)}) (text.nim:1091-1130)
+      if (o.arg.empty() || o.regions.size() != 2) fail_at(o, "expected a carry and two regions");
+      std::vector<std::pair<int, Shape>> carry;
+      for (int a : o.arg) {
+        const int s = resolve(a);
+        carry.push_back({slot_dt_[s], slot_shape_[s]});
+      }
+      if (res_types != carry) fail_at(o, "result types differ from the carry's");
+      st.kind = kStepWhile;
+      st.blocks.push_back(block(o, 0, carry));
+      check_ret(o, st.blocks[0], 0, {{kBool, Shape()}});
+      st.blocks.push_back(block(o, 1, carry));
+      check_ret(o, st.blocks[1], 1, carry);
+    } else if (n == "stablehlo.if") {
+      // "stablehlo.if"(%pred) ({then ...}, {else ...}) (text.nim:984-1020)
+      if (o.arg.size() != 1 || o.regions.size() != 2) fail_at(o, "expected a predicate and two regions");
+      scalar(o.arg[0], kBool, "the predicate");
+      st.kind = kStepIf;
+      for (size_t r = 0; r < 2; ++r) {
+        st.blocks.push_back(block(o, r, {}));
+        check_ret(o, st.blocks[r], r, res_types);
+      }
+    } else {
+      // "stablehlo.case"(%index) ({branch 0}, ..., {branch N-1})
+      if (o.arg.size() != 1 || o.regions.empty()) fail_at(o, "expected an index and regions");
+      scalar(o.arg[0], kI32, "the branch index");
+      st.kind = kStepCase;
+      for (size_t r = 0; r < o.regions.size(); ++r) {
+        st.blocks.push_back(block(o, r, {}));
+        check_ret(o, st.blocks[r], r, res_types);
+      }
+    }
+    for (int a : o.arg) st.in.push_back(resolve(a));
+    st.n_opnd = (int)st.in.size();
+    std::vector<int> cap;
+    for (const Block& b : st.blocks) captured(b, &cap);
+    for (int s : cap) st.in.push_back(s);
+    for (size_t i = 0; i < o.res.size(); ++i) {
+      set_slot(o.res[i], res_types[i].first, res_types[i].second);
+      st.out.push_back(o.res[i]);
+    }
+    st.outs = res_types;
+    m_->steps.push_back(std::move(st));
+    m_->has_control = true;
   }
 
   // Drops steps none of whose outputs reach a func.return.
@@ -1540,6 +1729,116 @@ std::string direct_key(Ctx* c, const std::vector<Tensor*>& ins) {
   return k;
 }
 
+void release_all(std::vector<Tensor*>* ts) {
+  for (Tensor* t : *ts) {
+    t->ext--;
+    maybe_destroy(t);
+  }
+  ts->clear();
+}
+
+// The value of a scalar (bool or i32) result, read back from the device:
+// the pending graph is flushed first, as rew_mi355x_to_host does.
+int64_t read_scalar(Ctx* c, Tensor* t) {
+  if (t->prod) flush(c);
+  if (!t->st) invalid("jit: control-flow predicate has no data (an earlier flush failed)");
+  int64_t v = 0;
+  const size_t n = (size_t)t->nbytes();
+  if (n > sizeof v) invalid("jit: control-flow predicate is not a scalar");
+  REW_HIP(hipMemcpyAsync(&v, t->data(), n, hipMemcpyDeviceToHost, c->stream));
+  REW_HIP(hipStreamSynchronize(c->stream));
+  if (t->dt == kBool) return (v & 0xff) != 0;
+  return (int64_t)(int32_t)(uint32_t)v;
+}
+
+void run_steps(Ctx* c, const std::vector<Step>& steps, std::vector<Tensor*>& v,
+               std::vector<Tensor*>& made);
+
+// Runs block b with arguments `args`; returns its results, each with one
+// owner reference.  Everything else the block made is released.
+std::vector<Tensor*> run_block(Ctx* c, const Block& b, const std::vector<Tensor*>& args,
+                               std::vector<Tensor*>& v) {
+  for (size_t i = 0; i < args.size(); ++i) v[b.args[i]] = args[i];
+  std::vector<Tensor*> made;
+  try {
+    run_steps(c, b.steps, v, made);
+  } catch (...) {
+    release_all(&made);
+    throw;
+  }
+  std::vector<Tensor*> res;
+  for (int r : b.ret) {
+    v[r]->ext++;
+    res.push_back(v[r]);
+  }
+  release_all(&made);
+  return res;
+}
+
+// A control step (src/rew/transform/control.nim): the chosen region of an
+// if / case, or the loop of a while, its predicate read back each turn.
+// Results go into v and `made` (one owner reference each).
+void run_control(Ctx* c, const Step& st, std::vector<Tensor*>& v, std::vector<Tensor*>& made) {
+  std::vector<Tensor*> res;
+  if (st.kind == kStepWhile) {
+    std::vector<Tensor*> carry;
+    for (int i = 0; i < st.n_opnd; ++i) {
+      v[st.in[i]]->ext++;
+      carry.push_back(v[st.in[i]]);
+    }
+    try {
+      for (;;) {
+        std::vector<Tensor*> p = run_block(c, st.blocks[0], carry, v);
+        bool go;
+        try {
+          go = read_scalar(c, p[0]) != 0;
+        } catch (...) {
+          release_all(&p);
+          throw;
+        }
+        release_all(&p);
+        if (!go) break;
+        std::vector<Tensor*> next = run_block(c, st.blocks[1], carry, v);
+        release_all(&carry);
+        carry.swap(next);
+      }
+    } catch (...) {
+      release_all(&carry);
+      throw;
+    }
+    res.swap(carry);
+  } else {
+    int64_t k = read_scalar(c, v[st.in[0]]);
+    const int nb = (int)st.blocks.size();
+    if (st.kind == kStepIf) k = k ? 0 : 1;  // then, else
+    else if (k < 0 || k >= nb) k = nb - 1;  // stablehlo.case: out of range -> last
+    res = run_block(c, st.blocks[(size_t)k], {}, v);
+  }
+  for (size_t j = 0; j < res.size(); ++j) {
+    v[st.out[j]] = res[j];
+    made.push_back(res[j]);
+  }
+}
+
+void run_steps(Ctx* c, const std::vector<Step>& steps, std::vector<Tensor*>& v,
+               std::vector<Tensor*>& made) {
+  std::vector<Tensor*> in;
+  for (const Step& st : steps) {
+    if (st.kind != kStepNode) {
+      run_control(c, st, v, made);
+      continue;
+    }
+    in.clear();
+    for (int s : st.in) in.push_back(v[s]);
+    Node* n = new Node(st.proto);
+    std::vector<Tensor*> outs = commit_node(c, n, in, st.outs);
+    for (size_t j = 0; j < outs.size(); ++j) {
+      v[st.out[j]] = outs[j];
+      made.push_back(outs[j]);
+    }
+  }
+}
+
 // The module's nodes committed to the pending graph; its results, each
 // with one owner reference.
 std::vector<Tensor*> instantiate(Ctx* c, JitModule* m, const std::vector<Tensor*>& ins) {
@@ -1548,23 +1847,10 @@ std::vector<Tensor*> instantiate(Ctx* c, JitModule* m, const std::vector<Tensor*
   for (auto& kc : m->consts) v[kc.first] = kc.second;
   std::vector<Tensor*> made;
   made.reserve(m->steps.size() * 2);
-  std::vector<Tensor*> in;
   try {
-    for (const Step& st : m->steps) {
-      in.clear();
-      for (int s : st.in) in.push_back(v[s]);
-      Node* n = new Node(st.proto);
-      std::vector<Tensor*> outs = commit_node(c, n, in, st.outs);
-      for (size_t j = 0; j < outs.size(); ++j) {
-        v[st.out[j]] = outs[j];
-        made.push_back(outs[j]);
-      }
-    }
+    run_steps(c, m->steps, v, made);
   } catch (...) {
-    for (Tensor* t : made) {
-      t->ext--;
-      maybe_destroy(t);
-    }
+    release_all(&made);
     throw;
   }
   std::vector<Tensor*> res;
@@ -1631,8 +1917,9 @@ std::vector<Tensor*> jit_module_run(Ctx* c, const std::string& name, const std::
   if (ins.size() != m->arg_slot.size())
     invalid(who + ": module takes " + std::to_string(m->arg_slot.size()) + " input(s), got " +
             std::to_string(ins.size()));
+  // (a module with control flow flushes inside the call, per predicate)
   bool direct = c->mode == REW_MI355X_MODE_DEFERRED && c->plan_cache && c->pending.empty() &&
-                m->steps.size() >= kDirectMinSteps;
+                m->steps.size() >= kDirectMinSteps && !m->has_control;
   for (size_t i = 0; i < ins.size(); ++i) {
     if (ins[i]->dt != m->arg_ty[i].first || ins[i]->shape != m->arg_ty[i].second)
       invalid(who + ": input " + std::to_string(i) + " is " + type_text(ins[i]->dt, ins[i]->shape) +

@@ -651,3 +651,73 @@ def batchNormGrad(operand: Tensor, scale: Tensor, mean: Tensor, variance: Tensor
                          _bn_attrs(epsilon, featureIndex))
     assert len(outs) == 3, "batchNormGrad: eager backend returned wrong arity"
     return tuple(outs)
+
+
+# ---- einsum and the shape-operand ops (src/rew/ops/linalg.nim, shape.nim) -----------
+
+def _join_ints(xs: Sequence[int]) -> str:
+    """joinInts (src/rew/ops/linalg.nim:21-29): "[a,b,c]"."""
+    return "[" + ",".join(str(int(x)) for x in xs) + "]"
+
+
+def einsum(a: Tensor, b: Tensor, config: str, outputShape: Sequence[int]) -> Tensor:
+    """src/rew/ops/linalg.nim:378-403 (TensorFlow einsum grammar, explicit result shape)."""
+    if a.device != b.device:
+        raise TensorError("einsum: device mismatch")
+    if a.dtype != b.dtype:
+        raise TensorError(f"einsum: dtype mismatch ({a.dtype.rew_name} vs {b.dtype.rew_name})")
+    if not config:
+        raise TensorError("einsum: config must not be empty")
+    return _one("einsum", [a, b], [("einsum_config", config),
+                                   ("output_shape", _join_ints(outputShape))])
+
+
+def unaryEinsum(a: Tensor, config: str, outputShape: Sequence[int]) -> Tensor:
+    """src/rew/ops/linalg.nim:405-430."""
+    if not config:
+        raise TensorError("unaryEinsum: config must not be empty")
+    return _one("unaryEinsum", [a], [("einsum_config", config),
+                                     ("output_shape", _join_ints(outputShape))])
+
+
+def dynamicBroadcastInDim(t: Tensor, outputDimensions: Tensor, resultShape: Sequence[int],
+                          broadcastDimensions: Sequence[int],
+                          knownExpandingDimensions: Sequence[int] = (),
+                          knownNonexpandingDimensions: Sequence[int] = ()) -> Tensor:
+    """src/rew/ops/linalg.nim:288-326."""
+    if outputDimensions.dtype not in _INT_DTYPES or \
+            tuple(outputDimensions.shape) != (len(resultShape),):
+        raise TensorError("dynamicBroadcastInDim: outputDimensions must be an integer vector "
+                          f"of length {len(resultShape)}")
+    return _one("dynamicBroadcastInDim", [t, outputDimensions],
+                [("result_shape", _join_ints(resultShape)),
+                 ("broadcast_dimensions", _join_ints(broadcastDimensions)),
+                 ("known_expanding_dimensions", _join_ints(knownExpandingDimensions)),
+                 ("known_nonexpanding_dimensions", _join_ints(knownNonexpandingDimensions))])
+
+
+def dynamicPad(a: Tensor, paddingValue: Tensor, edgePaddingLow: Tensor,
+               edgePaddingHigh: Tensor, interiorPadding: Tensor,
+               resultShape: Sequence[int]) -> Tensor:
+    """src/rew/ops/shape.nim:395-441."""
+    if paddingValue.dtype != a.dtype or len(paddingValue.shape) != 0:
+        raise TensorError(f"dynamicPad: paddingValue must be scalar with dtype {a.dtype.rew_name}")
+    for name, t in (("edgePaddingLow", edgePaddingLow), ("edgePaddingHigh", edgePaddingHigh),
+                    ("interiorPadding", interiorPadding)):
+        if t.dtype not in _INT_DTYPES or tuple(t.shape) != (len(a.shape),):
+            raise TensorError(f"dynamicPad: {name} must be an integer vector of length "
+                              f"{len(a.shape)}")
+    return _one("dynamicPad", [a, paddingValue, edgePaddingLow, edgePaddingHigh, interiorPadding],
+                [("result_shape", _nimseq(resultShape))])
+
+
+def realDynamicSlice(a: Tensor, startIndices: Tensor, limitIndices: Tensor, strides: Tensor,
+                     resultShape: Sequence[int]) -> Tensor:
+    """src/rew/ops/shape.nim:477-517."""
+    for name, t in (("startIndices", startIndices), ("limitIndices", limitIndices),
+                    ("strides", strides)):
+        if t.dtype not in _INT_DTYPES or tuple(t.shape) != (len(a.shape),):
+            raise TensorError(f"realDynamicSlice: {name} must be an integer vector of length "
+                              f"{len(a.shape)}")
+    return _one("realDynamicSlice", [a, startIndices, limitIndices, strides],
+                [("result_shape", _nimseq(resultShape))])

@@ -1,0 +1,82 @@
+"""GPU checks of einsum / unaryEinsum (src/rew/ops/linalg.nim:378-430) and the
+shape-operand ops dynamicPad, realDynamicSlice and dynamicBroadcastInDim
+(src/rew/ops/shape.nim:395-517, linalg.nim:288-326), which the library
+records as primitive nodes (reduceSum, dotGeneral, transpose; pad, slice,
+broadcastTo).  einsum is checked against numpy.einsum in float64 (fp32
+tolerance 1e-5 normwise); the index ops bit for bit against numpy."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+from rew_amd import eager as E
+from rew_amd import ops as O
+from rew_amd.eager import DType, EagerError
+
+
+def rnd(shape, seed):
+    return np.random.default_rng(seed).standard_normal(shape).astype(np.float32)
+
+
+CASES = [
+    ("ab,bc->ac", (5, 7), (7, 3)),
+    ("bij,bjk->bik", (2, 4, 6), (2, 6, 3)),
+    ("ab,bc->ca", (4, 5), (5, 6)),
+    ("a,b->ab", (3,), (4,)),
+    ("ab,ab->", (6, 5), (6, 5)),
+    ("abc,cd->ad", (3, 4, 5), (5, 2)),
+    ("ij,kj->ik", (8, 16), (3, 16)),
+    ("bhqd,bhkd->bhqk", (2, 3, 5, 8), (2, 3, 7, 8)),
+]
+
+
+@pytest.mark.parametrize("cfg,sa,sb", CASES)
+def test_einsum_against_numpy(gpu, cfg, sa, sb):
+    a, b = rnd(sa, 1), rnd(sb, 2)
+    want = np.einsum(cfg, a.astype(np.float64), b.astype(np.float64))
+    got = E.toHost(O.einsum(E.fromHost(a), E.fromHost(b), cfg, list(want.shape)))
+    assert got.shape == want.shape
+    err = np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30)
+    assert err <= 1e-5, (cfg, err)
+
+
+@pytest.mark.parametrize("cfg,sa", [("abc->cab", (2, 3, 4)), ("abc->b", (3, 4, 5)),
+                                    ("ab->", (4, 6)), ("ab->ab", (2, 3))])
+def test_unary_einsum_against_numpy(gpu, cfg, sa):
+    a = rnd(sa, 3)
+    want = np.einsum(cfg, a.astype(np.float64))
+    got = E.toHost(O.unaryEinsum(E.fromHost(a), cfg, list(want.shape)))
+    assert got.shape == want.shape
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
+
+
+def test_einsum_errors(gpu):
+    a, b = E.fromHost(rnd((3, 3), 4)), E.fromHost(rnd((3, 3), 5))
+    with pytest.raises(EagerError, match="repeated"):
+        O.einsum(a, b, "aa,ab->b", [3])       # a diagonal: not supported
+    with pytest.raises(EagerError, match="->"):
+        O.einsum(a, b, "ab,bc", [3, 3])
+    with pytest.raises(EagerError, match="output_shape"):
+        O.einsum(a, b, "ab,bc->ac", [3, 4])
+
+
+def test_dynamic_broadcast_pad_slice(gpu):
+    x = np.arange(12, dtype=np.float32).reshape(3, 4)
+    i32 = lambda v: E.fromHost(np.asarray(v, np.int32))
+    # dynamicBroadcastInDim: [3,4] -> [2,3,4] along dims (1, 2)
+    got = E.toHost(O.dynamicBroadcastInDim(E.fromHost(x), i32([2, 3, 4]), [2, 3, 4], [1, 2]))
+    assert got.tolist() == np.broadcast_to(x, (2, 3, 4)).tolist()
+    # dynamicPad with low (1, 0), high (0, 2), interior (1, 1)
+    pv = E.fromHost(np.float32(-1.0))
+    got = E.toHost(O.dynamicPad(E.fromHost(x), pv, i32([1, 0]), i32([0, 2]), i32([1, 1]),
+                                [6, 9]))
+    want = np.full((6, 9), -1.0, np.float32)
+    want[1::2, 0:7:2] = x
+    assert got.tolist() == want.tolist()
+    # realDynamicSlice rows 1..3 step 1, cols 0..4 step 2 (int64 bounds)
+    i64 = lambda v: E.fromHost(np.asarray(v, np.int64))
+    got = E.toHost(O.realDynamicSlice(E.fromHost(x), i64([1, 0]), i64([3, 4]), i64([1, 2]),
+                                      [2, 2]))
+    assert got.tolist() == x[1:3, 0:4:2].tolist()
+    with pytest.raises(EagerError, match="result_shape"):
+        O.realDynamicSlice(E.fromHost(x), i64([0, 0]), i64([3, 4]), i64([1, 1]), [2, 2])
