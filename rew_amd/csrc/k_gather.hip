@@ -327,7 +327,52 @@ __global__ void __launch_bounds__(256) cholesky_kernel(CholeskyArgs a) {
   }
 }
 
+// Triangular solve: T = op(a) restricted to the referenced triangle;
+// right-side systems x T = b are T^T x^T = b^T, solved per row of b.
+template <typename T>
+__global__ void __launch_bounds__(256) trisolve_kernel(TriSolveArgs p) {
+  __shared__ T A[kCholMaxN][kCholMaxN + 1];
+  const int n = (int)p.n;
+  const int64_t m = p.m;
+  const T* a = (const T*)p.a + (int64_t)blockIdx.x * n * n;
+  const T* b = (const T*)p.b + (int64_t)blockIdx.x * n * m;
+  T* x = (T*)p.out + (int64_t)blockIdx.x * n * m;
+  for (int e = threadIdx.x; e < n * n; e += blockDim.x) {
+    const int i = e / n, j = e % n;
+    const bool ref = p.lower ? i >= j : j >= i;
+    A[i][j] = ref ? a[e] : T(0);
+  }
+  __syncthreads();
+  // effective matrix of the column system: E = op(a) (left) or op(a)^T
+  // (right); E(i, k) = A[k][i] when exactly one of (trans, right) holds
+  const bool flip = (bool)p.trans != !p.left;
+  const bool low = (bool)p.lower != flip;  // E is lower triangular
+  for (int64_t r = threadIdx.x; r < m; r += blockDim.x) {
+    // element i of right-hand side r: b[i, r] (left) or b[r, i] (right)
+    const int64_t si = p.left ? m : 1, sr = p.left ? 1 : n;
+    for (int s = 0; s < n; ++s) {
+      const int i = low ? s : n - 1 - s;
+      T acc = b[i * si + r * sr];
+      if (low) {
+        for (int k = 0; k < i; ++k) acc -= (flip ? A[k][i] : A[i][k]) * x[k * si + r * sr];
+      } else {
+        for (int k = i + 1; k < n; ++k) acc -= (flip ? A[k][i] : A[i][k]) * x[k * si + r * sr];
+      }
+      x[i * si + r * sr] = p.unit ? acc : acc / A[i][i];
+    }
+  }
+}
+
 }  // namespace
+
+void launch_trisolve(const TriSolveArgs& a, hipStream_t stream) {
+  if (a.batch == 0 || a.n == 0 || a.m == 0) return;
+  if (a.n > kCholMaxN || a.batch > 0x7fffffff)
+    fail(REW_MI355X_ERR_INVALID, "internal: triangularSolve launch outside its limits");
+  if (a.f64) hipLaunchKernelGGL(trisolve_kernel<double>, dim3((unsigned)a.batch), dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL(trisolve_kernel<float>, dim3((unsigned)a.batch), dim3(256), 0, stream, a);
+  REW_HIP(hipGetLastError());
+}
 
 void launch_window(const WindowArgs& a, hipStream_t stream) {
   if (a.total == 0) return;

@@ -264,6 +264,22 @@ struct CholeskyArgs {
 };
 void launch_cholesky(const CholeskyArgs& a, hipStream_t stream);
 
+// ---- triangular solve (k_gather.hip) -------------------------------------------------
+// stablehlo.triangular_solve over [batch, n, n] a and b of [batch, n, m]
+// (left_side: op(a) x = b) or [batch, m, n] (x op(a) = b), f32 / f64, n <=
+// kCholMaxN: op(a) is a or its transpose (real adjoint = transpose), only the
+// `lower` (or upper) triangle of a is read, and unit_diagonal takes its
+// diagonal as ones.  One workgroup per matrix, a in LDS, one thread per
+// right-hand side by substitution with the sums in k order.
+struct TriSolveArgs {
+  const void* a;
+  const void* b;
+  void* out;
+  int64_t batch, n, m;
+  int f64, left, lower, unit, trans;
+};
+void launch_trisolve(const TriSolveArgs& a, hipStream_t stream);
+
 // ---- batch norm (k_gather.hip) -------------------------------------------------------
 // stablehlo.batch_norm_{inference,training,grad} over x viewed as dense
 // [outer, C, inner] (C at feature_index), f32 or f64, N = outer inner:

@@ -383,6 +383,7 @@ struct Lower {
   void emit_index_map(Node* n);
   void emit_window(Node* n);
   void emit_cholesky(Node* n);
+  void emit_trisolve(Node* n);
   void emit_batchnorm(Node* n);
   // Materialize `t` (any kind) into a fresh dense tensor whose shape is the
   // permutation `perm` of t's shape.
@@ -1091,6 +1092,7 @@ void Lower::emit_anchor(Node* n) {
     case K_SCATTER: emit_index_map(n); break;
     case K_WINDOW: emit_window(n); break;
     case K_CHOLESKY: emit_cholesky(n); break;
+    case K_TRISOLVE: emit_trisolve(n); break;
     case K_BATCHNORM: emit_batchnorm(n); break;
     case K_BITCAST: {
       Tensor* x = n->in[0];
@@ -3362,6 +3364,31 @@ void Lower::emit_cholesky(Node* n) {
   Launch L{a};
   if (c->profiling)
     L.name = "cholesky{" + std::to_string(a.batch) + "x" + std::to_string(a.n) + "}";
+  run_launch(c, std::move(L));
+}
+
+void Lower::emit_trisolve(Node* n) {
+  Tensor *a = n->in[0], *b = n->in[1];
+  ensure_mat(a);
+  ensure_mat(b);
+  tensor_alloc(n->out[0]);
+  TriSolveArgs p;
+  std::memset(&p, 0, sizeof p);
+  p.a = a->data();
+  p.b = b->data();
+  p.out = n->out[0]->data();
+  p.n = a->shape.d[a->shape.rank - 1];
+  p.batch = p.n ? a->numel() / (p.n * p.n) : 0;
+  p.m = p.n && p.batch ? b->numel() / (p.batch * p.n) : 0;
+  p.f64 = a->dt == kF64;
+  p.left = (int)(n->i0 & 1);
+  p.lower = (int)((n->i0 >> 1) & 1);
+  p.unit = (int)((n->i0 >> 2) & 1);
+  p.trans = (int)((n->i0 >> 3) & 1);
+  Launch L{p};
+  if (c->profiling)
+    L.name = "triangular_solve{" + std::to_string(p.batch) + "x" + std::to_string(p.n) + "x" +
+             std::to_string(p.m) + "}";
   run_launch(c, std::move(L));
 }
 

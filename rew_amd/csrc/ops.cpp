@@ -103,6 +103,7 @@ static const std::unordered_map<std::string, OpSpec>& op_table() {
       // eager ops of rew's table outside the configs (src/rew/eager.nim:838-850)
       {"pad", {K_WINDOW, kWinPad}}, {"dynamicSlice", {K_WINDOW, kWinSlice}},
       {"dynamicUpdateSlice", {K_WINDOW, kWinUpdate}}, {"cholesky", {K_CHOLESKY, 0}},
+      {"triangularSolve", {K_TRISOLVE, 0}},
       {"getDimensionSize", {K_CONST, 0}}, {"replicaId", {K_CONST, 1}},
       {"partitionId", {K_CONST, 1}}, {"setDimensionSize", {K_RESHAPE, 1}},
       {"dynamicReshape", {K_RESHAPE, 2}}, {"dynamicIota", {K_IOTA, 1}},
@@ -117,7 +118,7 @@ static const std::unordered_map<std::string, OpSpec>& op_table() {
 // does not implement natively.
 static bool known_but_unimplemented(const std::string& n) {
   static const char* names[] = {
-      "complex", "real", "imag", "conv2d", "maxPool2d", "fft", "triangularSolve"};
+      "complex", "real", "imag", "conv2d", "maxPool2d", "fft"};
   for (auto* s : names)
     if (n == s) return true;
   return false;
@@ -932,6 +933,46 @@ Node* prepare_node(Ctx* c, const std::string& op, const std::vector<Tensor*>& in
         if (lw != "true" && lw != "false") invalid("eager 'cholesky': lower must be true or false");
         n->i0 = lw == "true";
         outs.push_back({x->dt, x->shape});
+        break;
+      }
+      case K_TRISOLVE: {
+        // stablehlo.triangular_solve (src/rew/ops/linalg.nim:350-376; attrs
+        // left_side, lower, unit_diagonal, transpose_a)
+        nin(2);
+        Tensor *a = ins[0], *b = ins[1];
+        if (a->dt != b->dt) invalid("eager 'triangularSolve': dtype mismatch");
+        if (!dt_is_float(a->dt)) invalid("eager 'triangularSolve': operands must be floating point");
+        const int r = a->shape.rank;
+        if (r < 2 || a->shape.d[r - 1] != a->shape.d[r - 2])
+          invalid("eager 'triangularSolve': a's innermost matrix dimensions must be square");
+        auto flag = [&](const char* k) {
+          const std::string v = strip(find_attr(attrs, k, op));
+          if (v != "true" && v != "false")
+            invalid(std::string("eager 'triangularSolve': ") + k + " must be true or false");
+          return v == "true";
+        };
+        const bool left = flag("left_side"), lower = flag("lower"), unit = flag("unit_diagonal");
+        const std::string ta = strip(find_attr(attrs, "transpose_a", op));
+        bool trans;
+        if (ta == "NO_TRANSPOSE") trans = false;
+        else if (ta == "TRANSPOSE" || ta == "ADJOINT") trans = true;  // real operands
+        else invalid("eager 'triangularSolve': transpose_a must be NO_TRANSPOSE, TRANSPOSE or "
+                     "ADJOINT, got '" + ta + "'");
+        const int64_t nn = a->shape.d[r - 1];
+        bool ok = b->shape.rank == r;
+        for (int k = 0; ok && k < r - 2; ++k) ok = a->shape.d[k] == b->shape.d[k];
+        if (ok) ok = left ? b->shape.d[r - 2] == nn : b->shape.d[r - 1] == nn;
+        if (!ok)
+          invalid("eager 'triangularSolve': b " + b->shape.str() + " does not fit a " +
+                  a->shape.str() + (left ? " (left side)" : " (right side)"));
+        if (a->dt != kF32 && a->dt != kF64)
+          fail(REW_MI355X_ERR_UNSUPPORTED, "eager 'triangularSolve': only float32 / float64");
+        if (nn > kCholMaxN)
+          fail(REW_MI355X_ERR_UNSUPPORTED, "eager 'triangularSolve': matrices above " +
+                                               std::to_string(kCholMaxN) + " x " +
+                                               std::to_string(kCholMaxN));
+        n->i0 = (left ? 1 : 0) | (lower ? 2 : 0) | (unit ? 4 : 0) | (trans ? 8 : 0);
+        outs.push_back({b->dt, b->shape});
         break;
       }
       case K_DOT:

@@ -133,6 +133,11 @@ struct PtrVisit {
     field(f, a.x);
     field(f, a.out);
   }
+  void operator()(TriSolveArgs& a) {
+    field(f, a.a);
+    field(f, a.b);
+    field(f, a.out);
+  }
   void operator()(BatchNormArgs& a) {
     for (const void** p : {&a.x, &a.scale, &a.offset, &a.mean, &a.var, &a.dy}) field(f, *p);
     for (void** p : {&a.out0, &a.out1, &a.out2}) field(f, *p);
@@ -188,6 +193,7 @@ struct Exec {
   }
   void operator()(WindowArgs& a) { launch_window(a, c->stream); }
   void operator()(CholeskyArgs& a) { launch_cholesky(a, c->stream); }
+  void operator()(TriSolveArgs& a) { launch_trisolve(a, c->stream); }
   void operator()(BatchNormArgs& a) { launch_batchnorm(a, c->stream); }
   void operator()(HeadArgs& a) { launch_class_head(a, c->stream); }
   void operator()(RouterArgs& a) { launch_moe_router(a, c->stream); }

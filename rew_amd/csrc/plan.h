@@ -56,7 +56,7 @@ struct FillL {
 
 using LaunchArgs = std::variant<EwL, ReduceL, GemmL, FlashArgs, RowNormArgs, SoftmaxArgs,
                                 RopeArgs, GatherArgs, ArgmaxArgs, TopkArgs, SortArgs,
-                                IndexMapL, MoeL, FillL, WindowArgs, CholeskyArgs,
+                                IndexMapL, MoeL, FillL, WindowArgs, CholeskyArgs, TriSolveArgs,
                                 BatchNormArgs, HeadArgs, RouterArgs>;
 
 struct Launch {

@@ -63,6 +63,7 @@ enum Kind : int {
   K_CONST,     // a scalar whose value the op fixes (getDimensionSize, replicaId, partitionId)
   K_WINDOW,    // pad / dynamicSlice / dynamicUpdateSlice (sub: kWin*)
   K_CHOLESKY,
+  K_TRISOLVE,
   K_BATCHNORM, // batchNormInference / Training / Grad (sub: kBn*)
   // composite kernels created by the planner (never recorded directly)
   K_COUNT

@@ -721,3 +721,15 @@ def realDynamicSlice(a: Tensor, startIndices: Tensor, limitIndices: Tensor, stri
                               f"{len(a.shape)}")
     return _one("realDynamicSlice", [a, startIndices, limitIndices, strides],
                 [("result_shape", _nimseq(resultShape))])
+
+
+def triangularSolve(a: Tensor, b: Tensor, leftSide: bool = True, lower: bool = True,
+                    unitDiagonal: bool = False, transposeA: str = "NO_TRANSPOSE") -> Tensor:
+    """src/rew/ops/linalg.nim:350-376 (transposeA: NO_TRANSPOSE, TRANSPOSE or ADJOINT)."""
+    if a.device != b.device:
+        raise TensorError("triangularSolve: device mismatch")
+    return _one("triangularSolve", [a, b],
+                [("left_side", "true" if leftSide else "false"),
+                 ("lower", "true" if lower else "false"),
+                 ("unit_diagonal", "true" if unitDiagonal else "false"),
+                 ("transpose_a", transposeA)])

@@ -80,3 +80,38 @@ def test_dynamic_broadcast_pad_slice(gpu):
     assert got.tolist() == x[1:3, 0:4:2].tolist()
     with pytest.raises(EagerError, match="result_shape"):
         O.realDynamicSlice(E.fromHost(x), i64([0, 0]), i64([3, 4]), i64([1, 1]), [2, 2])
+
+
+@pytest.mark.parametrize("left", [True, False])
+@pytest.mark.parametrize("lower", [True, False])
+@pytest.mark.parametrize("trans", ["NO_TRANSPOSE", "TRANSPOSE", "ADJOINT"])
+@pytest.mark.parametrize("unit", [False, True])
+def test_triangular_solve_against_numpy(gpu, left, lower, trans, unit):
+    # stablehlo.triangular_solve (src/rew/ops/linalg.nim:350-376): the
+    # referenced triangle only (the other one holds junk), batched
+    rng = np.random.default_rng(7)
+    n, m, bt = 12, 5, 3
+    a = rng.standard_normal((bt, n, n)).astype(np.float32)
+    a[:, np.arange(n), np.arange(n)] += 4.0 * np.sign(a[:, np.arange(n), np.arange(n)]) + 0.5
+    b = rng.standard_normal((bt, n, m) if left else (bt, m, n)).astype(np.float32)
+    t = np.tril(a) if lower else np.triu(a)
+    if unit:
+        t = t.copy()
+        t[:, np.arange(n), np.arange(n)] = 1.0
+    op = t if trans == "NO_TRANSPOSE" else np.swapaxes(t, 1, 2)
+    op64 = op.astype(np.float64)
+    want = (np.linalg.solve(op64, b.astype(np.float64)) if left
+            else np.swapaxes(np.linalg.solve(np.swapaxes(op64, 1, 2),
+                                             np.swapaxes(b.astype(np.float64), 1, 2)), 1, 2))
+    got = E.toHost(O.triangularSolve(E.fromHost(a), E.fromHost(b), left, lower, unit, trans))
+    assert got.shape == b.shape
+    err = np.linalg.norm(got - want) / np.linalg.norm(want)
+    assert err <= 1e-5, err
+
+
+def test_triangular_solve_errors(gpu):
+    a = E.fromHost(np.eye(4, dtype=np.float32))
+    with pytest.raises(EagerError, match="does not fit"):
+        O.triangularSolve(a, E.fromHost(np.ones((3, 2), np.float32)))
+    with pytest.raises(EagerError, match="transpose_a"):
+        O.triangularSolve(a, E.fromHost(np.ones((4, 2), np.float32)), transposeA="CONJ")
