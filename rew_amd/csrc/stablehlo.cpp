@@ -736,7 +736,7 @@ struct Block {
   std::vector<Step> steps;
   std::vector<int> ret;
 };
-enum StepKind : int { kStepNode = 0, kStepWhile = 1, kStepIf = 2, kStepCase = 3 };
+enum StepKind : int { kStepNode = 0, kStepWhile = 1, kStepIf = 2, kStepCase = 3, kStepEager = 4 };
 struct Step {
   Node proto;  // prepared node: typed attributes set, no operands
   std::vector<int> in, out;
@@ -747,6 +747,10 @@ struct Step {
   int kind = kStepNode;
   int n_opnd = 0;
   std::vector<Block> blocks;
+  // kStepEager: the eager op recorded at call time (record_op), for ops the
+  // library composes from several nodes or that read operand values
+  std::string eager_op;
+  Attrs eager_attrs;
 };
 
 }  // namespace
@@ -826,12 +830,18 @@ std::unordered_map<std::string, std::vector<int64_t>> dim_numbers(const std::str
 }
 
 // "array<i64: 1, 3>" -> {1, 3}
+// "array<i64: 1, 2>" or rew's "[1, 2]" (text.nim renderI64Array)
 std::vector<int64_t> i64_array(const std::string& raw, const std::string& who) {
-  const size_t c = raw.find(':'), e = raw.rfind('>');
-  if (raw.compare(0, 6, "array<") != 0 || c == std::string::npos || e == std::string::npos)
-    invalid(who + ": malformed i64 array '" + raw + "'");
+  std::string body;
+  if (!raw.empty() && raw[0] == '[' && raw.back() == ']') {
+    body = raw.substr(1, raw.size() - 2);
+  } else {
+    const size_t c = raw.find(':'), e = raw.rfind('>');
+    if (raw.compare(0, 6, "array<") != 0 || c == std::string::npos || e == std::string::npos)
+      invalid(who + ": malformed i64 array '" + raw + "'");
+    body = raw.substr(c + 1, e - c - 1);
+  }
   std::vector<int64_t> v;
-  std::string body = raw.substr(c + 1, e - c - 1);
   size_t q = 0;
   while (q < body.size()) {
     while (q < body.size() && (body[q] == ' ' || body[q] == ',')) ++q;
@@ -1469,6 +1479,43 @@ class Translator {
       one(o, "dynamicUpdateSlice", o.arg, {});
     } else if (n == "stablehlo.while" || n == "stablehlo.if" || n == "stablehlo.case") {
       control(o);
+    } else if (n == "stablehlo.einsum" || n == "stablehlo.unary_einsum") {
+      // (text.nim:1696-1728)
+      const std::string* cfg = attr_raw(o, "einsum_config");
+      if (!cfg) fail_at(o, "missing einsum_config");
+      need_args(o, n == "stablehlo.einsum" ? 2 : 1);
+      eager_step(o, n == "stablehlo.einsum" ? "einsum" : "unaryEinsum",
+                 {{"einsum_config", unquote(*cfg)}, {"output_shape", shape_text(rt->d)}});
+    } else if (n == "stablehlo.triangular_solve") {
+      // (text.nim:1645-1695): transpose_a = #stablehlo<transpose KIND>
+      need_args(o, 2);
+      Attrs at;
+      for (const char* k : {"left_side", "lower", "unit_diagonal"}) {
+        const std::string* v = attr_raw(o, k);
+        if (!v) fail_at(o, std::string("missing ") + k);
+        at.push_back({k, *v});
+      }
+      const std::string* ta = attr_raw(o, "transpose_a");
+      if (!ta) fail_at(o, "missing transpose_a");
+      std::string kind = unquote(*ta);
+      const size_t sp = kind.find_last_of(' ');
+      if (sp != std::string::npos) kind = kind.substr(sp + 1);
+      while (!kind.empty() && kind.back() == '>') kind.pop_back();
+      at.push_back({"transpose_a", kind});
+      one(o, "triangularSolve", o.arg, at);
+    } else if (n == "stablehlo.dynamic_pad" || n == "stablehlo.real_dynamic_slice") {
+      // (text.nim:780-801): the index operands are read when the module runs
+      need_args(o, n == "stablehlo.dynamic_pad" ? 5 : 4);
+      eager_step(o, n == "stablehlo.dynamic_pad" ? "dynamicPad" : "realDynamicSlice",
+                 {{"result_shape", shape_text(rt->d)}});
+    } else if (n == "stablehlo.dynamic_broadcast_in_dim") {
+      // (text.nim:1575-1610): a broadcast to the static result type
+      need_args(o, 2);
+      const std::string* bd = attr_raw(o, "broadcast_dimensions");
+      if (!bd) fail_at(o, "missing broadcast_dimensions");
+      one(o, "broadcastTo", {o.arg[0]},
+          {{"output_shape", shape_text(rt->d)},
+           {"broadcast_dimensions", shape_text(i64_array(*bd, who_))}});
     } else if (n == "stablehlo.gather") {
       gather(o);
     } else if (n == "stablehlo.scatter") {
@@ -1476,6 +1523,30 @@ class Translator {
     } else {
       fail_at(o, "op not supported by the mi355x jit path", REW_MI355X_ERR_UNSUPPORTED);
     }
+  }
+
+  static std::string unquote(std::string v) {
+    while (!v.empty() && v.back() == ' ') v.pop_back();
+    if (v.size() >= 2 && v.front() == '"' && v.back() == '"') v = v.substr(1, v.size() - 2);
+    return v;
+  }
+
+  // An op the call records through the eager path (record_op), typed by the
+  // text's result type.
+  void eager_step(const Op& o, const std::string& name, const Attrs& attrs) {
+    const Ty& t = o.res_ty[0];
+    if (t.dt < 0) fail_at(o, "unsupported result type", REW_MI355X_ERR_UNSUPPORTED);
+    Step st;
+    st.kind = kStepEager;
+    st.eager_op = name;
+    st.eager_attrs = attrs;
+    for (int a : o.arg) st.in.push_back(resolve(a));
+    st.n_opnd = (int)st.in.size();
+    set_slot(o.res[0], t.dt, Shape(t.d));
+    st.out.push_back(o.res[0]);
+    st.outs.push_back({t.dt, Shape(t.d)});
+    m_->steps.push_back(std::move(st));
+    m_->has_control = true;  // (may read operands back: no direct plan)
   }
 
   // ---- control flow (src/rew/transform/control.nim: cond / whileLoop / fori
@@ -1824,6 +1895,18 @@ void run_steps(Ctx* c, const std::vector<Step>& steps, std::vector<Tensor*>& v,
                std::vector<Tensor*>& made) {
   std::vector<Tensor*> in;
   for (const Step& st : steps) {
+    if (st.kind == kStepEager) {
+      in.clear();
+      for (int s : st.in) in.push_back(v[s]);
+      std::vector<Tensor*> outs = record_op(c, st.eager_op, in, st.eager_attrs);
+      for (size_t j = 0; j < outs.size(); ++j) made.push_back(outs[j]);
+      if (outs.size() != st.out.size() || outs[0]->dt != st.outs[0].first ||
+          outs[0]->shape != st.outs[0].second)
+        invalid("jit: " + st.eager_op + " gives " + type_text(outs[0]->dt, outs[0]->shape) +
+                ", the module's type is " + type_text(st.outs[0].first, st.outs[0].second));
+      for (size_t j = 0; j < outs.size(); ++j) v[st.out[j]] = outs[j];
+      continue;
+    }
     if (st.kind != kStepNode) {
       run_control(c, st, v, made);
       continue;

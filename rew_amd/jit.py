@@ -340,6 +340,50 @@ def traceOp(op: str, operands: Sequence[Tensor], attrs: Sequence[tuple]) -> list
         ctx.lines.append(f"    %v{r.traceId} = \"stablehlo.{mn}\"({args}){attrs_s} : "
                          f"{_sig(list(operands), _ty(x.dtype, shape))}")
         return [r]
+    if op in ("einsum", "unaryEinsum"):
+        # emitEinsumAt (src/rew/stablehlo/text.nim:1696-1728)
+        shape = _ints(a["output_shape"])
+        r = ctx.value(x.dtype, shape)
+        mn = "einsum" if op == "einsum" else "unary_einsum"
+        ctx.lines.append(f"    %v{r.traceId} = \"stablehlo.{mn}\"("
+                         + ", ".join(f"%v{t.traceId}" for t in operands)
+                         + f") {{einsum_config = \"{a['einsum_config']}\"}} : "
+                         + _sig(list(operands), _ty(x.dtype, shape)))
+        return [r]
+    if op == "triangularSolve":
+        # emitTriangularSolveAt (text.nim:1645-1695)
+        b = operands[1]
+        r = ctx.value(b.dtype, b.shape)
+        ctx.lines.append(f"    %v{r.traceId} = \"stablehlo.triangular_solve\"(%v{x.traceId}, "
+                         f"%v{b.traceId}) {{left_side = {a['left_side']}, lower = {a['lower']}, "
+                         f"unit_diagonal = {a['unit_diagonal']}, transpose_a = "
+                         f"#stablehlo<transpose {a['transpose_a']}>}} : "
+                         + _sig(list(operands), _ty(b.dtype, b.shape)))
+        return [r]
+    if op in ("dynamicPad", "realDynamicSlice"):
+        # emitGenericVariadicAt (text.nim:780-801)
+        shape = _ints(a["result_shape"])
+        r = ctx.value(x.dtype, shape)
+        mn = "dynamic_pad" if op == "dynamicPad" else "real_dynamic_slice"
+        ctx.lines.append(f"    %v{r.traceId} = \"stablehlo.{mn}\"("
+                         + ", ".join(f"%v{t.traceId}" for t in operands) + ") : "
+                         + _sig(list(operands), _ty(x.dtype, shape)))
+        return [r]
+    if op == "dynamicBroadcastInDim":
+        # emitDynamicBroadcastInDimAt (text.nim:1575-1610)
+        shape = _ints(a["result_shape"])
+        r = ctx.value(x.dtype, shape)
+        arr = lambda xs: "[" + ", ".join(str(int(v)) for v in xs) + "]"
+        extra = ""
+        for k, name in (("known_expanding_dimensions", "known_expanding_dimensions"),
+                        ("known_nonexpanding_dimensions", "known_nonexpanding_dimensions")):
+            if _ints(a.get(k, "[]")):
+                extra += f", {name} = {arr(_ints(a[k]))}"
+        ctx.lines.append(f"    %v{r.traceId} = \"stablehlo.dynamic_broadcast_in_dim\"("
+                         f"%v{x.traceId}, %v{operands[1].traceId}) {{broadcast_dimensions = "
+                         f"{arr(_ints(a['broadcast_dimensions']))}{extra}}} : "
+                         + _sig(list(operands), _ty(x.dtype, shape)))
+        return [r]
     if op == "concat":
         d = int(a["dimension"])
         shape = list(x.shape)

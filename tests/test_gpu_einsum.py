@@ -115,3 +115,35 @@ def test_triangular_solve_errors(gpu):
         O.triangularSolve(a, E.fromHost(np.ones((3, 2), np.float32)))
     with pytest.raises(EagerError, match="transpose_a"):
         O.triangularSolve(a, E.fromHost(np.ones((4, 2), np.float32)), transposeA="CONJ")
+
+
+def test_ops_under_jit_equal_eager(gpu):
+    # the same ops traced by jit (stablehlo.einsum / unary_einsum /
+    # triangular_solve / dynamic_pad / real_dynamic_slice /
+    # dynamic_broadcast_in_dim in rew's text forms) give the eager results
+    from rew_amd import jit as J
+    rng = np.random.default_rng(11)
+    a = rng.standard_normal((4, 6)).astype(np.float32)
+    b = rng.standard_normal((6, 3)).astype(np.float32)
+    t = np.tril(rng.standard_normal((6, 6)).astype(np.float32)) + 4 * np.eye(6, dtype=np.float32)
+    i32 = lambda v: E.fromHost(np.asarray(v, np.int32))
+
+    def f(x):
+        e = O.einsum(x[0], x[1], "ab,bc->ca", [3, 4])
+        u = O.unaryEinsum(x[0], "ab->b", [6])
+        s = O.triangularSolve(x[2], x[1], True, True, False, "TRANSPOSE")
+        p = O.dynamicPad(x[0], x[3], x[4], x[4], x[5], [6, 11])
+        r = O.realDynamicSlice(x[0], x[5], x[6], x[7], [4, 3])
+        g = O.dynamicBroadcastInDim(x[1], x[8], [2, 6, 3], [1, 2])
+        return [e, u, s, p, r, g]
+    ins = [E.fromHost(a), E.fromHost(b), E.fromHost(t), E.fromHost(np.float32(0.5)),
+           i32([1, 0]), i32([0, 1]), i32([4, 6]), i32([1, 2]), i32([2, 6, 3])]
+    text = J.jit(f, "opsJit").text(ins)
+    for mn in ("stablehlo.einsum", "stablehlo.unary_einsum", "stablehlo.triangular_solve",
+               "stablehlo.dynamic_pad", "stablehlo.real_dynamic_slice",
+               "stablehlo.dynamic_broadcast_in_dim"):
+        assert mn in text, mn
+    got = [E.toHost(o) for o in J.jit(f, "opsJit").call(ins)]
+    want = [E.toHost(o) for o in f(ins)]
+    for g_, w_ in zip(got, want):
+        assert g_.shape == w_.shape and g_.tolist() == w_.tolist()
