@@ -363,7 +363,108 @@ __global__ void __launch_bounds__(256) trisolve_kernel(TriSolveArgs p) {
   }
 }
 
+__global__ void __launch_bounds__(256) complex_kernel(ComplexArgs a) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.n) return;
+  const int w = a.esize;
+  auto cp = [&](void* dst, const void* src) {
+    if (w == 8) *(uint64_t*)dst = *(const uint64_t*)src;
+    else if (w == 4) *(uint32_t*)dst = *(const uint32_t*)src;
+    else *(uint16_t*)dst = *(const uint16_t*)src;
+  };
+  uint8_t* o = (uint8_t*)a.out;
+  const uint8_t* x = (const uint8_t*)a.x;
+  switch (a.mode) {
+    case 0:
+      cp(o + 2 * i * w, x + i * w);
+      cp(o + (2 * i + 1) * w, (const uint8_t*)a.y + i * w);
+      break;
+    case 1: cp(o + i * w, x + 2 * i * w); break;
+    case 2: cp(o + i * w, x + (2 * i + 1) * w); break;
+    case 3: cp(o + i * w, x + i * w); break;
+    default: {
+      const uint64_t z = 0;
+      cp(o + i * w, &z);
+    }
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) fft1_kernel(Fft1Args a) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t total = a.outer * a.len_out * a.inner;
+  if (i >= total) return;
+  const int64_t in_ = i % a.inner, k = (i / a.inner) % a.len_out, o = i / (a.inner * a.len_out);
+  const int64_t n = a.n;
+  const int64_t base = o * a.len_in * a.inner + in_;  // element (o, 0, in_) of x
+  const T* x = (const T*)a.x;
+  T* out = (T*)a.out;
+  double re = 0.0, im = 0.0;
+  const double sgn = a.mode == 1 || a.mode == 3 ? 1.0 : -1.0;
+  auto tw = [&](int64_t j, double* c, double* s) {
+    const int64_t r = (k * j) % n;  // exp(sgn 2 pi i r / n)
+    double sp, cp;
+    sincospi(2.0 * (double)r / (double)n, &sp, &cp);
+    *c = cp;
+    *s = sgn * sp;
+  };
+  if (a.mode == 3) {
+    // real output: x[k] = (1/n)(Re X0 + 2 sum_{0<j<(n+1)/2} Re(X_j w^{jk}) + [n even] Re X_{n/2} (-1)^k)
+    const int64_t h = (n + 1) / 2;
+    for (int64_t j = 0; j < a.len_in && j <= n / 2; ++j) {
+      const T* z = x + 2 * (base + j * a.inner);
+      double c, s;
+      tw(j, &c, &s);
+      const double v = (double)z[0] * c - (double)z[1] * s;
+      if (j == 0) re += (double)z[0];
+      else if (j < h) re += 2.0 * v;
+      else re += (double)z[0] * c;  // j == n / 2, n even: (-1)^k Re X
+    }
+    out[i] = (T)(re / (double)n);
+    return;
+  }
+  for (int64_t j = 0; j < a.len_in; ++j) {
+    double xr, xi = 0.0;
+    if (a.mode == 2) {
+      xr = (double)x[base + j * a.inner];
+    } else {
+      const T* z = x + 2 * (base + j * a.inner);
+      xr = (double)z[0];
+      xi = (double)z[1];
+    }
+    double c, s;
+    tw(j, &c, &s);
+    re += xr * c - xi * s;
+    im += xr * s + xi * c;
+  }
+  if (a.mode == 1) {
+    re /= (double)n;
+    im /= (double)n;
+  }
+  out[2 * i] = (T)re;
+  out[2 * i + 1] = (T)im;
+}
+
 }  // namespace
+
+void launch_complex(const ComplexArgs& a, hipStream_t stream) {
+  if (a.n == 0) return;
+  if (a.esize != 2 && a.esize != 4 && a.esize != 8)
+    fail(REW_MI355X_ERR_INVALID, "internal: complex launch outside its limits");
+  hipLaunchKernelGGL(complex_kernel, dim3((unsigned)((a.n + 255) / 256)), dim3(256), 0, stream, a);
+  REW_HIP(hipGetLastError());
+}
+
+void launch_fft1(const Fft1Args& a, hipStream_t stream) {
+  const int64_t total = a.outer * a.len_out * a.inner;
+  if (total == 0) return;
+  if (a.n <= 0 || total > (int64_t)0x7fffffff * 256)
+    fail(REW_MI355X_ERR_INVALID, "internal: fft launch outside its limits");
+  const dim3 grid((unsigned)((total + 255) / 256));
+  if (a.f64) hipLaunchKernelGGL(fft1_kernel<double>, grid, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL(fft1_kernel<float>, grid, dim3(256), 0, stream, a);
+  REW_HIP(hipGetLastError());
+}
 
 void launch_trisolve(const TriSolveArgs& a, hipStream_t stream) {
   if (a.batch == 0 || a.n == 0 || a.m == 0) return;

@@ -280,6 +280,32 @@ struct TriSolveArgs {
 };
 void launch_trisolve(const TriSolveArgs& a, hipStream_t stream);
 
+// ---- complex parts and the discrete Fourier transform (k_gather.hip) -----------------
+// complex(re, im) interleaves two f32 / f64 tensors into c64 / c128; real / imag
+// take a component (or, of a real tensor, the tensor / zeros).  mode: 0 complex,
+// 1 real part, 2 imaginary part, 3 copy, 4 zeros; esize: component bytes.
+struct ComplexArgs {
+  const void* x;
+  const void* y;
+  void* out;
+  int64_t n;  // result elements
+  int esize, mode;
+};
+void launch_complex(const ComplexArgs& a, hipStream_t stream);
+// One-axis DFT of [outer, len_in, inner] into [outer, len_out, inner], a thread
+// per result element summing in double with twiddles exp(-+2 pi i k j / n) from
+// (k j mod n): mode 0 complex forward, 1 complex inverse (scaled 1/n), 2 real to
+// complex (len_out = n / 2 + 1), 3 complex to real (len_in = n / 2 + 1, the
+// spectrum taken as Hermitian: the imaginary parts of bins 0 and n / 2 are not
+// read).  f64: c128 / f64 data, else c64 / f32.
+struct Fft1Args {
+  const void* x;
+  void* out;
+  int64_t outer, inner, len_in, len_out, n;
+  int f64, mode;
+};
+void launch_fft1(const Fft1Args& a, hipStream_t stream);
+
 // ---- batch norm (k_gather.hip) -------------------------------------------------------
 // stablehlo.batch_norm_{inference,training,grad} over x viewed as dense
 // [outer, C, inner] (C at feature_index), f32 or f64, N = outer inner:

@@ -384,6 +384,8 @@ struct Lower {
   void emit_window(Node* n);
   void emit_cholesky(Node* n);
   void emit_trisolve(Node* n);
+  void emit_complex(Node* n);
+  void emit_fft1(Node* n);
   void emit_batchnorm(Node* n);
   // Materialize `t` (any kind) into a fresh dense tensor whose shape is the
   // permutation `perm` of t's shape.
@@ -1093,6 +1095,8 @@ void Lower::emit_anchor(Node* n) {
     case K_WINDOW: emit_window(n); break;
     case K_CHOLESKY: emit_cholesky(n); break;
     case K_TRISOLVE: emit_trisolve(n); break;
+    case K_COMPLEX: emit_complex(n); break;
+    case K_FFT1: emit_fft1(n); break;
     case K_BATCHNORM: emit_batchnorm(n); break;
     case K_BITCAST: {
       Tensor* x = n->in[0];
@@ -3389,6 +3393,47 @@ void Lower::emit_trisolve(Node* n) {
   if (c->profiling)
     L.name = "triangular_solve{" + std::to_string(p.batch) + "x" + std::to_string(p.n) + "x" +
              std::to_string(p.m) + "}";
+  run_launch(c, std::move(L));
+}
+
+void Lower::emit_complex(Node* n) {
+  for (Tensor* t : n->in) ensure_mat(t);
+  tensor_alloc(n->out[0]);
+  ComplexArgs p;
+  std::memset(&p, 0, sizeof p);
+  p.x = n->in[0]->data();
+  p.y = n->in.size() > 1 ? n->in[1]->data() : nullptr;
+  p.out = n->out[0]->data();
+  p.n = n->out[0]->numel();
+  p.mode = (int)n->i0;
+  p.esize = (int)n->i1;
+  Launch L{p};
+  if (c->profiling) L.name = std::string("complex{") + n->name + "}";
+  run_launch(c, std::move(L));
+}
+
+void Lower::emit_fft1(Node* n) {
+  Tensor* x = n->in[0];
+  ensure_mat(x);
+  tensor_alloc(n->out[0]);
+  Fft1Args p;
+  std::memset(&p, 0, sizeof p);
+  p.x = x->data();
+  p.out = n->out[0]->data();
+  const int ax = (int)n->i0;
+  p.outer = 1;
+  p.inner = 1;
+  for (int d = 0; d < ax; ++d) p.outer *= x->shape.d[d];
+  for (int d = ax + 1; d < x->shape.rank; ++d) p.inner *= x->shape.d[d];
+  p.len_in = x->shape.d[ax];
+  p.len_out = n->out[0]->shape.d[ax];
+  p.n = n->i2;
+  p.mode = (int)n->i1;
+  p.f64 = x->dt == kF64 || x->dt == kC128;
+  Launch L{p};
+  if (c->profiling)
+    L.name = "fft1{" + std::to_string(p.outer) + "x" + std::to_string(p.len_in) + "x" +
+             std::to_string(p.inner) + ",m" + std::to_string(p.mode) + "}";
   run_launch(c, std::move(L));
 }
 

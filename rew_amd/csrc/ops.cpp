@@ -104,6 +104,9 @@ static const std::unordered_map<std::string, OpSpec>& op_table() {
       {"pad", {K_WINDOW, kWinPad}}, {"dynamicSlice", {K_WINDOW, kWinSlice}},
       {"dynamicUpdateSlice", {K_WINDOW, kWinUpdate}}, {"cholesky", {K_CHOLESKY, 0}},
       {"triangularSolve", {K_TRISOLVE, 0}},
+      {"complex", {K_COMPLEX, 0}}, {"real", {K_COMPLEX, 1}}, {"imag", {K_COMPLEX, 2}},
+      // one axis of rew's fft (recorded by record_fft; not a rew op name)
+      {"fft1d", {K_FFT1, 0}},
       {"getDimensionSize", {K_CONST, 0}}, {"replicaId", {K_CONST, 1}},
       {"partitionId", {K_CONST, 1}}, {"setDimensionSize", {K_RESHAPE, 1}},
       {"dynamicReshape", {K_RESHAPE, 2}}, {"dynamicIota", {K_IOTA, 1}},
@@ -118,7 +121,7 @@ static const std::unordered_map<std::string, OpSpec>& op_table() {
 // does not implement natively.
 static bool known_but_unimplemented(const std::string& n) {
   static const char* names[] = {
-      "complex", "real", "imag", "conv2d", "maxPool2d", "fft"};
+      "conv2d", "maxPool2d"};
   for (auto* s : names)
     if (n == s) return true;
   return false;
@@ -935,6 +938,71 @@ Node* prepare_node(Ctx* c, const std::string& op, const std::vector<Tensor*>& in
         outs.push_back({x->dt, x->shape});
         break;
       }
+      case K_COMPLEX: {
+        // complex (src/rew/ops/arith.nim:86-106), real / imag (unary.nim:184-224)
+        if (spec.sub == 0) {
+          nin(2);
+          Tensor *re = ins[0], *im = ins[1];
+          if (re->dt != kF32 && re->dt != kF64)
+            invalid("eager 'complex': operands must be float32 or float64, got " +
+                    std::string(dt_enum_name(re->dt)));
+          if (im->dt != re->dt) invalid("eager 'complex': dtype mismatch");
+          if (im->shape != re->shape) invalid("eager 'complex': shape mismatch");
+          n->i0 = 0;
+          n->i1 = dt_size(re->dt);
+          outs.push_back({re->dt == kF32 ? (int)kC64 : (int)kC128, re->shape});
+        } else {
+          nin(1);
+          Tensor* x = ins[0];
+          const bool cx = x->dt == kC64 || x->dt == kC128;
+          if (!cx && !dt_is_float(x->dt))
+            invalid("eager '" + op + "': operand must be floating point or complex, got " +
+                    dt_enum_name(x->dt));
+          if (cx) {
+            n->i0 = spec.sub;  // 1 real part, 2 imaginary part
+            n->i1 = dt_size(x->dt) / 2;
+            outs.push_back({x->dt == kC64 ? (int)kF32 : (int)kF64, x->shape});
+          } else {
+            n->i0 = spec.sub == 1 ? 3 : 4;  // a real tensor's real part is itself, imag zeros
+            n->i1 = dt_size(x->dt);
+            outs.push_back({x->dt, x->shape});
+          }
+        }
+        break;
+      }
+      case K_FFT1: {
+        // attrs axis, mode (0 forward, 1 inverse, 2 real to complex, 3 complex to
+        // real), n (the transform length along axis)
+        nin(1);
+        Tensor* x = ins[0];
+        const int64_t ax = std::atoll(find_attr(attrs, "axis", op).c_str());
+        const int64_t mode = std::atoll(find_attr(attrs, "mode", op).c_str());
+        const int64_t len = std::atoll(find_attr(attrs, "n", op).c_str());
+        if (ax < 0 || ax >= x->shape.rank || mode < 0 || mode > 3 || len < 0)
+          invalid("eager 'fft1d': bad axis / mode / length");
+        const bool cx = x->dt == kC64 || x->dt == kC128;
+        Shape s = x->shape;
+        int odt = x->dt;
+        if (mode == 2) {
+          if (x->dt != kF32 && x->dt != kF64) invalid("eager 'fft': RFFT operand must be f32 or f64");
+          if (x->shape.d[ax] != len) invalid("eager 'fft': RFFT length mismatch");
+          s.d[ax] = len / 2 + 1;
+          odt = x->dt == kF32 ? (int)kC64 : (int)kC128;
+        } else if (mode == 3) {
+          if (!cx) invalid("eager 'fft': IRFFT operand must be complex");
+          if (x->shape.d[ax] != len / 2 + 1) invalid("eager 'fft': IRFFT length mismatch");
+          s.d[ax] = len;
+          odt = x->dt == kC64 ? (int)kF32 : (int)kF64;
+        } else {
+          if (!cx) invalid("eager 'fft': FFT / IFFT operand must be complex");
+          if (x->shape.d[ax] != len) invalid("eager 'fft': FFT length mismatch");
+        }
+        n->i0 = ax;
+        n->i1 = mode;
+        n->i2 = len;
+        outs.push_back({odt, s});
+        break;
+      }
       case K_TRISOLVE: {
         // stablehlo.triangular_solve (src/rew/ops/linalg.nim:350-376; attrs
         // left_side, lower, unit_diagonal, transpose_a)
@@ -1350,10 +1418,84 @@ static std::vector<Tensor*> record_dynamic_shape_op(Ctx* c, const std::string& o
   return r;
 }
 
+// rew's fft (src/rew/ops/linalg.nim:328-348; stablehlo.fft with fft_type
+// FFT / IFFT / RFFT / IRFFT over the trailing len(fft_length) dims, 1-3) as
+// one-axis DFTs: RFFT transforms the last axis real to complex, then the
+// others complex; IRFFT the leading ones complex (inverse), then the last one
+// complex to real; FFT / IFFT every axis.  Each axis is an exact-length DFT
+// summed in double.
+static std::vector<Tensor*> record_fft(Ctx* c, const std::vector<Tensor*>& ins,
+                                       const Attrs& attrs) {
+  if (ins.size() != 1) invalid("eager 'fft': expected 1 operand, got " + std::to_string(ins.size()));
+  const std::string ty = strip(find_attr(attrs, "fft_type", "fft"));
+  const std::vector<int64_t> len = parse_int_list(find_attr(attrs, "fft_length", "fft"), "fft");
+  Tensor* x = ins[0];
+  const int r = x->shape.rank;
+  if (len.empty() || len.size() > 3)
+    invalid("eager 'fft': fftLength must have length 1..3, got " + std::to_string(len.size()));
+  if ((int)len.size() > r) invalid("eager 'fft': fftLength rank exceeds operand rank");
+  for (int64_t d : len)
+    if (d < 0) invalid("eager 'fft': fftLength dimensions must be non-negative");
+  const int s0 = r - (int)len.size();
+  const bool cx = x->dt == kC64 || x->dt == kC128;
+  std::vector<std::pair<int, int>> passes;  // (axis, mode)
+  const int last = r - 1;
+  if (ty == "FFT" || ty == "IFFT") {
+    if (!cx) invalid("eager 'fft': FFT/IFFT operand must be complex, got " + std::string(dt_enum_name(x->dt)));
+    for (int a = last; a >= s0; --a) passes.push_back({a, ty == "FFT" ? 0 : 1});
+  } else if (ty == "RFFT") {
+    if (x->dt != kF32 && x->dt != kF64)
+      invalid("eager 'fft': RFFT operand must be float32 or float64, got " + std::string(dt_enum_name(x->dt)));
+    passes.push_back({last, 2});
+    for (int a = last - 1; a >= s0; --a) passes.push_back({a, 0});
+  } else if (ty == "IRFFT") {
+    if (!cx) invalid("eager 'fft': IRFFT operand must be complex, got " + std::string(dt_enum_name(x->dt)));
+    for (int a = s0; a < last; ++a) passes.push_back({a, 1});
+    passes.push_back({last, 3});
+  } else {
+    invalid("eager 'fft': fft_type must be FFT, IFFT, RFFT or IRFFT, got '" + ty + "'");
+  }
+  // operand extents: FFT / IFFT / RFFT need the trailing dims equal to
+  // fftLength; IRFFT the last one equal to fftLength[-1] / 2 + 1
+  for (size_t i = 0; i < len.size(); ++i) {
+    const int a = s0 + (int)i;
+    const int64_t want = (ty == "IRFFT" && a == last) ? len[i] / 2 + 1 : len[i];
+    if (x->shape.d[a] != want)
+      invalid("eager 'fft': operand dimension " + std::to_string(a) + " is " +
+              std::to_string(x->shape.d[a]) + ", fftLength needs " + std::to_string(want));
+  }
+  std::vector<Tensor*> owned;
+  Tensor* y = x;
+  try {
+    for (auto& ps : passes) {
+      const int64_t n = len[(size_t)(ps.first - s0)];
+      std::vector<Tensor*> o = record_op(c, "fft1d", {y},
+                                         {{"axis", std::to_string(ps.first)},
+                                          {"mode", std::to_string(ps.second)},
+                                          {"n", std::to_string(n)}});
+      owned.push_back(o[0]);
+      y = o[0];
+    }
+  } catch (...) {
+    for (Tensor* t : owned) {
+      t->ext--;
+      maybe_destroy(t);
+    }
+    throw;
+  }
+  y->ext++;
+  for (Tensor* t : owned) {
+    t->ext--;
+    maybe_destroy(t);
+  }
+  return {y};
+}
+
 std::vector<Tensor*> record_op(Ctx* c, const std::string& op,
                                const std::vector<Tensor*>& ins,
                                const Attrs& attrs) {
   if (op == "einsum" || op == "unaryEinsum") return record_einsum(c, op, ins, attrs);
+  if (op == "fft") return record_fft(c, ins, attrs);
   if (op == "dynamicPad" || op == "realDynamicSlice" || op == "dynamicBroadcastInDim")
     return record_dynamic_shape_op(c, op, ins, attrs);
   std::vector<std::pair<int, Shape>> outs;

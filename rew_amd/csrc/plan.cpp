@@ -133,6 +133,15 @@ struct PtrVisit {
     field(f, a.x);
     field(f, a.out);
   }
+  void operator()(ComplexArgs& a) {
+    field(f, a.x);
+    field(f, a.y);
+    field(f, a.out);
+  }
+  void operator()(Fft1Args& a) {
+    field(f, a.x);
+    field(f, a.out);
+  }
   void operator()(TriSolveArgs& a) {
     field(f, a.a);
     field(f, a.b);
@@ -194,6 +203,8 @@ struct Exec {
   void operator()(WindowArgs& a) { launch_window(a, c->stream); }
   void operator()(CholeskyArgs& a) { launch_cholesky(a, c->stream); }
   void operator()(TriSolveArgs& a) { launch_trisolve(a, c->stream); }
+  void operator()(ComplexArgs& a) { launch_complex(a, c->stream); }
+  void operator()(Fft1Args& a) { launch_fft1(a, c->stream); }
   void operator()(BatchNormArgs& a) { launch_batchnorm(a, c->stream); }
   void operator()(HeadArgs& a) { launch_class_head(a, c->stream); }
   void operator()(RouterArgs& a) { launch_moe_router(a, c->stream); }

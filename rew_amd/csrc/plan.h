@@ -56,7 +56,7 @@ struct FillL {
 
 using LaunchArgs = std::variant<EwL, ReduceL, GemmL, FlashArgs, RowNormArgs, SoftmaxArgs,
                                 RopeArgs, GatherArgs, ArgmaxArgs, TopkArgs, SortArgs,
-                                IndexMapL, MoeL, FillL, WindowArgs, CholeskyArgs, TriSolveArgs,
+                                IndexMapL, MoeL, FillL, WindowArgs, CholeskyArgs, TriSolveArgs, ComplexArgs, Fft1Args,
                                 BatchNormArgs, HeadArgs, RouterArgs>;
 
 struct Launch {

@@ -64,6 +64,8 @@ enum Kind : int {
   K_WINDOW,    // pad / dynamicSlice / dynamicUpdateSlice (sub: kWin*)
   K_CHOLESKY,
   K_TRISOLVE,
+  K_COMPLEX,
+  K_FFT1,
   K_BATCHNORM, // batchNormInference / Training / Grad (sub: kBn*)
   // composite kernels created by the planner (never recorded directly)
   K_COUNT

@@ -111,7 +111,8 @@ _NP = {DType.BOOL: np.bool_, DType.INT8: np.int8, DType.INT16: np.int16,
        DType.INT32: np.int32, DType.INT64: np.int64, DType.UINT8: np.uint8,
        DType.UINT16: np.uint16, DType.UINT32: np.uint32, DType.UINT64: np.uint64,
        DType.FLOAT16: np.float16, DType.BFLOAT16: np.uint16, DType.FLOAT32: np.float32,
-       DType.FLOAT64: np.float64}
+       DType.FLOAT64: np.float64, DType.COMPLEX64: np.complex64,
+       DType.COMPLEX128: np.complex128}
 
 float32 = DType.FLOAT32
 bfloat16 = DType.BFLOAT16
@@ -294,7 +295,9 @@ def fromHost(data, dtype: DType | None = None, shape: Sequence[int] | None = Non
                  np.dtype(np.uint8): DType.UINT8, np.dtype(np.int16): DType.INT16,
                  np.dtype(np.uint16): DType.UINT16, np.dtype(np.int64): DType.INT64,
                  np.dtype(np.float64): DType.FLOAT64,
-                 np.dtype(np.uint64): DType.UINT64}.get(arr.dtype)
+                 np.dtype(np.uint64): DType.UINT64,
+                 np.dtype(np.complex64): DType.COMPLEX64,
+                 np.dtype(np.complex128): DType.COMPLEX128}.get(arr.dtype)
         if dtype is None:
             raise TensorError(f"fromHost: unsupported host dtype {arr.dtype}")
     dtype = DType(dtype)

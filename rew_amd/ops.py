@@ -733,3 +733,27 @@ def triangularSolve(a: Tensor, b: Tensor, leftSide: bool = True, lower: bool = T
                  ("lower", "true" if lower else "false"),
                  ("unit_diagonal", "true" if unitDiagonal else "false"),
                  ("transpose_a", transposeA)])
+
+
+# ---- complex parts and the Fourier transform ----------------------------------------
+
+def complex(real: Tensor, imag: Tensor) -> Tensor:  # noqa: A001 (rew's name)
+    """src/rew/ops/arith.nim:86-106: float32 / float64 parts -> complex64 / complex128."""
+    if real.dtype not in (DType.FLOAT32, DType.FLOAT64):
+        raise TensorError(f"complex: operands must be float32 or float64, got {real.dtype.rew_name}")
+    return _one("complex", [real, imag])
+
+
+def real(a: Tensor) -> Tensor:
+    """src/rew/ops/unary.nim:184-202."""
+    return _one("real", [a])
+
+
+def imag(a: Tensor) -> Tensor:
+    """src/rew/ops/unary.nim:204-224."""
+    return _one("imag", [a])
+
+
+def fft(a: Tensor, fftType: str, fftLength: Sequence[int]) -> Tensor:
+    """src/rew/ops/linalg.nim:328-348 (fftType FFT, IFFT, RFFT or IRFFT)."""
+    return _one("fft", [a], [("fft_type", fftType), ("fft_length", _join_ints(fftLength))])
