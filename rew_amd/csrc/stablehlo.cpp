@@ -1503,6 +1503,23 @@ class Translator {
       while (!kind.empty() && kind.back() == '>') kind.pop_back();
       at.push_back({"transpose_a", kind});
       one(o, "triangularSolve", o.arg, at);
+    } else if (n == "stablehlo.complex") {
+      need_args(o, 2);
+      one(o, "complex", o.arg, {});
+    } else if (n == "stablehlo.real" || n == "stablehlo.imag") {
+      need_args(o, 1);
+      one(o, n == "stablehlo.real" ? "real" : "imag", o.arg, {});
+    } else if (n == "stablehlo.fft") {
+      // (text.nim emitFftAt): fft_type = #stablehlo<fft_type KIND>, fft_length = [..]
+      need_args(o, 1);
+      const std::string* ft = attr_raw(o, "fft_type");
+      const std::string* fl = attr_raw(o, "fft_length");
+      if (!ft || !fl) fail_at(o, "missing fft_type / fft_length");
+      std::string kind = unquote(*ft);
+      const size_t sp = kind.find_last_of(' ');
+      if (sp != std::string::npos) kind = kind.substr(sp + 1);
+      while (!kind.empty() && kind.back() == '>') kind.pop_back();
+      eager_step(o, "fft", {{"fft_type", kind}, {"fft_length", shape_text(i64_array(*fl, who_))}});
     } else if (n == "stablehlo.dynamic_pad" || n == "stablehlo.real_dynamic_slice") {
       // (text.nim:780-801): the index operands are read when the module runs
       need_args(o, n == "stablehlo.dynamic_pad" ? 5 : 4);

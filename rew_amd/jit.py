@@ -350,6 +350,36 @@ def traceOp(op: str, operands: Sequence[Tensor], attrs: Sequence[tuple]) -> list
                          + f") {{einsum_config = \"{a['einsum_config']}\"}} : "
                          + _sig(list(operands), _ty(x.dtype, shape)))
         return [r]
+    if op == "complex":
+        # emitComplexAt (text.nim:826-838)
+        dt = {DType.FLOAT32: DType.COMPLEX64, DType.FLOAT64: DType.COMPLEX128}[x.dtype]
+        r = ctx.value(dt, x.shape)
+        ctx.lines.append(f"    %v{r.traceId} = stablehlo.complex %v{x.traceId}, "
+                         f"%v{operands[1].traceId} : {_ty(dt, x.shape)}")
+        return [r]
+    if op in ("real", "imag"):
+        # emitTypeChangingUnaryAt (text.nim:390-406)
+        dt = {DType.COMPLEX64: DType.FLOAT32, DType.COMPLEX128: DType.FLOAT64}.get(x.dtype, x.dtype)
+        return [_typed(ctx, op, x, "", dt, x.shape, quoted=True)]
+    if op == "fft":
+        # emitFftAt (text.nim:1612-1638)
+        fl = _ints(a["fft_length"])
+        ty = a["fft_type"]
+        shape = list(x.shape)
+        cx = {DType.FLOAT32: DType.COMPLEX64, DType.FLOAT64: DType.COMPLEX128}
+        rl = {DType.COMPLEX64: DType.FLOAT32, DType.COMPLEX128: DType.FLOAT64}
+        dt = x.dtype
+        if ty == "RFFT":
+            shape[-1] = fl[-1] // 2 + 1
+            dt = cx.get(x.dtype, x.dtype)
+        elif ty == "IRFFT":
+            shape[-1] = fl[-1]
+            dt = rl.get(x.dtype, x.dtype)
+        r = ctx.value(dt, shape)
+        ctx.lines.append(f"    %v{r.traceId} = \"stablehlo.fft\"(%v{x.traceId}) {{fft_type = "
+                         f"#stablehlo<fft_type {ty}>, fft_length = [{', '.join(map(str, fl))}]}} : "
+                         + _sig([x], _ty(dt, shape)))
+        return [r]
     if op == "triangularSolve":
         # emitTriangularSolveAt (text.nim:1645-1695)
         b = operands[1]

@@ -58,6 +58,21 @@ def test_rfft_irfft(gpu, shape, k):
     close(back, x, 1e-5)
 
 
+def test_fft_under_jit_equals_eager(gpu):
+    from rew_amd import jit as J
+    x = np.random.default_rng(6).standard_normal((3, 8, 6)).astype(np.float32)
+
+    def f(a):
+        s = O.fft(a[0], "RFFT", [8, 6])
+        return [s, O.fft(s, "IRFFT", [8, 6]), O.real(s), O.imag(s)]
+    j = J.jit(f, "fftJit")
+    assert '"stablehlo.fft"' in j.text([E.fromHost(x)])
+    got = [E.toHost(o) for o in j.call([E.fromHost(x)])]
+    want = [E.toHost(o) for o in f([E.fromHost(x)])]
+    for g_, w_ in zip(got, want):
+        assert g_.shape == w_.shape and g_.tolist() == w_.tolist()
+
+
 def test_fft_f64_and_errors(gpu):
     x = crnd((5, 12), 4, np.complex128)
     close(E.toHost(O.fft(E.fromHost(x), "FFT", [12])), np.fft.fft(x), 1e-12)

@@ -262,13 +262,13 @@ def test_input_mismatch_and_unsupported_op(gpu):
         J.executeJit("neg", "k", text, [f32([1, 2, 3])], [DType.FLOAT32], [[3]])
     bad = """module @m {
   func.func @main(%v1: tensor<2xf32>) -> tensor<2xf32> {
-    %v2 = stablehlo.fft %v1 : tensor<2xf32>
+    %v2 = stablehlo.convolution %v1 : tensor<2xf32>
     func.return %v2 : tensor<2xf32>
   }
 }
 """
-    with pytest.raises(E.EagerError, match="line 3: stablehlo.fft: op not supported"):
-        J.executeJit("fft", "k", bad, [f32([1, 2])], [DType.FLOAT32], [[2]])
+    with pytest.raises(E.EagerError, match="line 3: stablehlo.convolution: op not supported"):
+        J.executeJit("conv", "k", bad, [f32([1, 2])], [DType.FLOAT32], [[2]])
 
 
 GATHER_CASES = [

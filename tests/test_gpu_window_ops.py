@@ -177,7 +177,7 @@ def test_validation_errors(gpu):
                         [("edge_padding_low", "[0,0]"), ("edge_padding_high", "[0,0]"),
                          ("interior_padding", "[-1,0]")])
     with pytest.raises(E.EagerError, match="not implemented natively"):
-        E.dispatchEager("fft", [x], [])
+        E.dispatchEager("conv2d", [x], [])
 
 
 def test_batch_norm_known_answers(mode):
