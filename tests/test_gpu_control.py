@@ -97,3 +97,21 @@ def test_cond_nested_in_loop_under_lazy(gpu):
     for _ in range(6):
         w = w * np.float32(0.5) if w.sum() > 10 else w * np.float32(3.0) + np.float32(1.0)
     assert int(E.toHost(n)) == 6 and E.toHost(v).tolist() == w.tolist()
+
+
+def test_edge_cases_zero_trip_single_branch_nested_loops(gpu):
+    # a loop whose predicate is false at once returns its initial carry;
+    # a one-branch case runs it whatever the index; loops nest
+    def f(a):
+        z = K.whileLoop([a[0]], lambda c: O.compare(O.reduceSum(c[0], [0]),
+                                                    O.scalarF32(-1e9), "LT"),
+                        lambda c: [O.neg(c[0])])
+        s = K.caseOp(O.scalarI32(5), [lambda: [O.add(a[0], a[0])]])
+        outer = K.fori(0, 3, [a[0]], lambda i, c: K.fori(0, 2, [c[0]],
+                                                         lambda j, d: [O.add(d[0], a[0])]))
+        return [z[0], s[0], outer[0]]
+    x = np.array([1.0, -2.0, 0.5], np.float32)
+    z, s, o = J.jit(f, "edgeLoops").call([f32(x)])
+    assert E.toHost(z).tolist() == x.tolist()
+    assert E.toHost(s).tolist() == (x + x).tolist()
+    assert E.toHost(o).tolist() == (x * 7).tolist()

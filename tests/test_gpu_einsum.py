@@ -147,3 +147,19 @@ def test_ops_under_jit_equal_eager(gpu):
     want = [E.toHost(o) for o in f(ins)]
     for g_, w_ in zip(got, want):
         assert g_.shape == w_.shape and g_.tolist() == w_.tolist()
+
+
+def test_largest_triangular_solve_and_edge_transforms(gpu):
+    # the 64 x 64 limit, a length-1 FFT, an einsum over an empty batch
+    rng = np.random.default_rng(9)
+    a = np.tril(rng.standard_normal((64, 64))).astype(np.float64) + 8 * np.eye(64)
+    b = rng.standard_normal((64, 3))
+    got = E.toHost(O.triangularSolve(E.fromHost(a), E.fromHost(b)))
+    np.testing.assert_allclose(got, np.linalg.solve(a, b), rtol=1e-10, atol=1e-12)
+    with pytest.raises(EagerError, match="above 64"):
+        O.triangularSolve(E.fromHost(np.eye(65)), E.fromHost(np.ones((65, 1))))
+    z = (rng.standard_normal((4, 1)) + 1j * rng.standard_normal((4, 1))).astype(np.complex64)
+    assert E.toHost(O.fft(E.fromHost(z), "FFT", [1])).tolist() == z.tolist()
+    e = E.toHost(O.einsum(E.fromHost(np.zeros((0, 2, 3), np.float32)),
+                          E.fromHost(np.zeros((0, 3, 4), np.float32)), "bij,bjk->bik", [0, 2, 4]))
+    assert e.shape == (0, 2, 4)
