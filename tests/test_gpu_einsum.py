@@ -27,6 +27,10 @@ CASES = [
     ("abc,cd->ad", (3, 4, 5), (5, 2)),
     ("ij,kj->ik", (8, 16), (3, 16)),
     ("bhqd,bhkd->bhqk", (2, 3, 5, 8), (2, 3, 7, 8)),
+    ("ab,ab->ab", (3, 4), (3, 4)),      # batch only: the elementwise product
+    ("ab,b->a", (5, 6), (6,)),          # matrix-vector
+    ("i,i->", (7,), (7,)),              # inner product
+    ("ab,c->cab", (2, 3), (4,)),        # outer product, reordered
 ]
 
 
