@@ -196,3 +196,67 @@ def caseOp(index: Tensor, branches: Sequence[Callable[[], Sequence[Tensor]]]) ->
     text[-1] += f") : (tensor<i32>) -> {out_ty}"
     ctx.lines += ["    " + text[0]] + text[1:]
     return res
+
+
+def scan(init: Sequence[Tensor], xs: Sequence[Tensor],
+         body: Callable[[Sequence[Tensor], Sequence[Tensor]], tuple]) -> tuple:
+    """Sequential scan over the leading axis of `xs` (control.nim:290-420):
+    the body is traced once on slice 0 for its output types (those ops stay
+    in the trace, unused), then a whileLoop carries (counter, carry...,
+    ys accumulators...), slicing x[counter] with dynamicSlice and writing
+    each y into its accumulator with dynamicUpdateSlice.  Returns
+    (carry, ys).  As in rew, the update's start list has one entry per
+    dimension of y (the counter, then zeros), which fits scalar ys."""
+    _require_trace_mode("scan")
+    if len(xs) == 0:
+        raise CondError("scan: at least one xs tensor required")
+    ctx = _jit.currentTrace()
+    n = xs[0].shape[0]
+    for x in xs:
+        _require_trace(ctx, x, "scan")
+        if x.shape[0] != n:
+            raise CondError("scan: all xs must have the same leading dim size")
+    for t in init:
+        _require_trace(ctx, t, "scan")
+    start_zeros = [_ops.scalarI32(0) for _ in xs[0].shape]
+    sizes = [1] + list(xs[0].shape[1:])
+
+    def squeeze0(t):
+        return _ops.reshape(t, list(t.shape[1:]))
+    x0 = [squeeze0(_ops.dynamicSlice(x, start_zeros, sizes)) for x in xs]
+    dummy_carry, dummy_y = body(list(init), x0)
+    if len(dummy_carry) != len(init):
+        raise CondError(f"scan: body returned {len(dummy_carry)} carry value(s), "
+                        f"expected {len(init)}")
+    counter0, n_val, one = _ops.scalarI32(0), _ops.scalarI32(n), _ops.scalarI32(1)
+    nc, ny = len(init), len(dummy_y)
+    full = [counter0] + list(init)
+    for t in dummy_y:
+        shp = [n] + list(t.shape)
+        if t.dtype == DType.FLOAT32:
+            full.append(_ops.broadcastTo(_ops.scalarF32(0.0), shp, []))
+        elif t.dtype == DType.INT32:
+            full.append(_ops.broadcastTo(_ops.scalarI32(0), shp, []))
+        else:
+            full.append(_ops.astype(_ops.broadcastTo(_ops.scalarF32(0.0), shp, []), t.dtype))
+
+    def body_fn(args):
+        counter = args[0]
+        carry = list(args[1:1 + nc])
+        xsl = []
+        for x in xs:
+            starts = [counter] + [_ops.scalarI32(0) for _ in range(1, len(x.shape))]
+            xsl.append(squeeze0(_ops.dynamicSlice(x, starts, sizes)))
+        new_carry, ys_out = body(carry, xsl)
+        if len(new_carry) != nc:
+            raise CondError(f"scan: body returned {len(new_carry)} carry value(s), expected {nc}")
+        if len(ys_out) != ny:
+            raise CondError(f"scan: body returned {len(ys_out)} y value(s), expected {ny}")
+        res = [_ops.add(counter, one)] + list(new_carry)
+        for yi, y in enumerate(ys_out):
+            starts = [counter] + [_ops.scalarI32(0) for _ in range(1, len(y.shape))]
+            res.append(_ops.dynamicUpdateSlice(args[1 + nc + yi], _ops.unsqueeze(y, 0), starts))
+        return res
+
+    outs = whileLoop(full, lambda a: _ops.compare(a[0], n_val, "LT"), body_fn)
+    return list(outs[1:1 + nc]), list(outs[1 + nc:])

@@ -115,3 +115,26 @@ def test_edge_cases_zero_trip_single_branch_nested_loops(gpu):
     assert E.toHost(z).tolist() == x.tolist()
     assert E.toHost(s).tolist() == (x + x).tolist()
     assert E.toHost(o).tolist() == (x * 7).tolist()
+
+
+def test_scan_running_sum(gpu):
+    # control.nim scan: carry the running sum of the rows of xs, emit each
+    # row's dot with w as a scalar y
+    def f(a):
+        def body(carry, x):
+            s = O.add(carry[0], x[0])
+            y = O.reduceSum(O.mul(x[0], a[1]), [0])
+            return [s], [y]
+        carry, ys = K.scan([a[2]], [a[0]], body)
+        return [carry[0], ys[0]]
+    xs = np.random.default_rng(3).standard_normal((5, 4)).astype(np.float32)
+    w = np.array([1.0, -1.0, 0.5, 2.0], np.float32)
+    c0 = np.zeros(4, np.float32)
+    carry, ys = J.jit(f, "scanSum").call([f32(xs), f32(w), f32(c0)])
+    want_c = c0.copy()
+    for r in xs:
+        want_c = want_c + r
+    assert E.toHost(carry).tolist() == want_c.tolist()
+    got = E.toHost(ys)
+    assert got.shape == (5,)
+    np.testing.assert_allclose(got, (xs * w).sum(1), rtol=1e-5, atol=1e-6)
